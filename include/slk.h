@@ -1,0 +1,202 @@
+/*
+ * slk.h -- C ABI of libslk, an MI355X (gfx950) implementation of the DROID-SLAM
+ * per-edge update path of vibekernels/slam-hands (cuda_slam, cuda_pipeline):
+ * all-pairs correlation + 4-level pyramid + radius-3 lookup, SE3 reprojection
+ * kernels, and Schur-complement bundle adjustment.
+ *
+ * Conventions (kept from the reference, cuda_slam/main.cu and ba.cuh):
+ *  - every tensor argument is a caller-owned DEVICE pointer unless its name
+ *    ends in `_host`; sizes are element counts;
+ *  - fmaps [nframes][C][h][w]; coords [B][2][h*w] (x plane, then y plane);
+ *    lookup output [B][levels*(2r+1)^2][h*w], channel l*49 + a*7 + b with a the
+ *    x offset and b the y offset; poses [N][7] = [tx,ty,tz,qx,qy,qz,qw]
+ *    (world->camera); disps [N][h*w]; intrinsics [4] = fx,fy,cx,cy at 1/8 res;
+ *    target/weight [M][2][h*w]; eta [N][h*w] indexed by absolute keyframe;
+ *  - every call is stream-ordered on `stream` (0 = legacy default stream) and
+ *    returns an slk_status; work already enqueued when an error is returned is
+ *    not rolled back. The reference instead exit(1)s on any CUDA error
+ *    (nn.cuh:17-41); the C++ adapters in slam-hands_amd/adapters keep that.
+ *
+ * Each entry point cites the reference interface it replaces.
+ */
+#ifndef SLK_H
+#define SLK_H
+
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct slk_ctx slk_ctx;
+
+typedef enum {
+    SLK_OK = 0,
+    SLK_E_ARG = 1,     /* invalid argument or unsupported shape */
+    SLK_E_HIP = 2,     /* HIP runtime error (message in slk_last_error) */
+    SLK_E_NOT_SPD = 3, /* BA system not positive definite; poses/disps untouched
+                          (the reference produces NaN here, ba.cuh:422) */
+    SLK_E_STATE = 4    /* call order violated (e.g. sample before build) */
+} slk_status;
+
+typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
+
+/* ---------------------------------------------------------------- context */
+
+/* Creates a context on the current HIP device for h x w feature maps with C
+ * channels. corr_scale is alpha of the correlation GEMM (1/16 in the
+ * reference: cublasGemmEx alpha, cuda_slam/main.cu:1506,1572). Allocates the
+ * batched pyramid scratch for max_batch edges ([B,hw,hw] + levels,
+ * main.cu:1413-1418) and the single-edge volume (main.cu:1400-1405).
+ * Replaces CorrBlock::init (cuda_slam/corr.cuh:75) and
+ * BundleAdjustment::init(h, w) (cuda_slam/ba.cuh:408). levels <= 4, radius == 3. */
+int slk_create(slk_ctx** ctx, int h, int w, int C, int max_batch, int levels,
+               int radius, float corr_scale);
+
+/* Releases every buffer (BundleAdjustment::destroy ba.cuh:815,
+ * CorrBlock::destroy corr.cuh:259). */
+int slk_destroy(slk_ctx* ctx);
+
+/* Text of the last failure on this thread ("" if none). */
+const char* slk_last_error(void);
+
+/* ------------------------------------------------------------ correlation */
+
+/* CudaDroid::batch_build_and_sample_correlation(batch_size, edge_start,
+ * coords_2hw, corr_out_196hw), cuda_slam/main.cu:1555-1613 (copy in
+ * cuda_pipeline/slam.cuh:2851-2909). For each edge e < B: volume
+ * alpha * fmaps[ii_host[e]]^T fmaps[jj_host[e]], its 2x2 avg-pool pyramid, and
+ * the radius-3 bilinear lookup at coords[e] into out[e]. fmap_stride is the
+ * element distance between consecutive keyframes (C*h*w for a dense buffer).
+ * ii_host/jj_host are read before the call returns. B is not capped:
+ * batches above max_batch run in max_batch chunks. */
+int slk_corr_batch_build_and_sample(slk_ctx* ctx, const void* fmaps, int dtype,
+                                    long fmap_stride, const int* ii_host,
+                                    const int* jj_host, int B, const float* coords,
+                                    float* out, hipStream_t stream);
+
+/* Same with device-resident edge indices ii_dev/jj_dev [B]. */
+int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fmaps, int dtype,
+                                        long fmap_stride, const int* ii_dev,
+                                        const int* jj_dev, int B,
+                                        const float* coords, float* out,
+                                        hipStream_t stream);
+
+/* CudaDroid::build_correlation(i, j), main.cu:1500-1526 (and
+ * CorrBlock::build for one edge, corr.cuh:84): volume of (f_i, f_j) and its
+ * pyramid into the context's persistent single-edge buffers. */
+int slk_corr_build(slk_ctx* ctx, const void* f_i, const void* f_j, int dtype,
+                   hipStream_t stream);
+
+/* CudaDroid::sample_correlation(coords_2hw, corr_out), main.cu:1529-1552
+ * (CorrBlock::sample_single, corr.cuh:234): lookup of the last built volume. */
+int slk_corr_sample(slk_ctx* ctx, const float* coords, float* out,
+                    hipStream_t stream);
+
+/* Device pointer and shape of single-edge level l ([h*w][h2][w2]); the
+ * reference exposes these as corr_volume / corr_pyramid[l] (main.cu:1324-1326)
+ * for its debug dump (main.cu:2859-2871). */
+int slk_corr_level(slk_ctx* ctx, int level, const float** ptr, int* h2, int* w2);
+
+/* Standalone kernels with the reference's argument lists: */
+/* avg_pool_2x2_kernel(in, out, N, H, W), main.cu:1150-1170 */
+int slk_avg_pool_2x2(const float* in, float* out, long N, int H, int W,
+                     hipStream_t stream);
+/* batch_corr_sample_kernel(volumes, coords, corr_out, M, r, H1, W1, H2, W2, hw,
+ * coord_scale, level_idx), main.cu:1175-1217: writes channels
+ * level_idx*49 .. +48 of corr_out (overwrite; the reference adds into a
+ * zeroed buffer). r must be 3. */
+int slk_corr_sample_level(const float* volumes, const float* coords, float* corr_out,
+                          int M, int r, int H1, int W1, int H2, int W2, int hw,
+                          float coord_scale, int level_idx, hipStream_t stream);
+/* batch_coords_hw2_to_2hw(hw2, chw, M, HW), main.cu:1135-1146 */
+int slk_coords_hw2_to_2hw(const float* hw2, float* chw, int M, int HW,
+                          hipStream_t stream);
+
+/* -------------------------------------------------------------------- SE3 */
+
+/* projmap_kernel(poses, disps, intrinsics, ii, jj, coords, valid, M, H, W),
+ * cuda_slam/se3.cuh:118-177: coords [M][H][W][2], valid [M][H][W]. */
+int slk_projmap(const float* poses, const float* disps, const float* intrinsics,
+                const int* ii, const int* jj, float* coords, float* valid, int M,
+                int H, int W, hipStream_t stream);
+/* pose_retr_kernel(poses, dx, t0, t1), se3.cuh:179-193 */
+int slk_pose_retr(float* poses, const float* dx, int t0, int t1, hipStream_t stream);
+/* disp_retr_kernel(disps, dz, inds, HW) over num_inds rows, se3.cuh:195-206 */
+int slk_disp_retr(float* disps, const float* dz, const int* inds, int num_inds,
+                  int HW, hipStream_t stream);
+/* frame_distance_kernel(poses, disps, intrinsics, ii, jj, dist, M, H, W, beta),
+ * se3.cuh:209-277 */
+int slk_frame_distance(const float* poses, const float* disps,
+                       const float* intrinsics, const int* ii, const int* jj,
+                       float* dist, int M, int H, int W, float beta,
+                       hipStream_t stream);
+/* clamp_disps_kernel(disps, n, min_val), main.cu (caller :2392-2397) */
+int slk_clamp_disps(float* disps, int n, float min_val, hipStream_t stream);
+
+/* --------------------------------------------------------------------- BA */
+
+/* BundleAdjustment::iterate(poses, disps, intrinsics, target, weight, eta,
+ * ii_gpu, jj_gpu, ii_host, jj_host, num_edges, t0, t1, lm, ep, motion_only),
+ * cuda_slam/ba.cuh:476-803; with motion_only=1 also the pipeline variant
+ * slam::BundleAdjustment::iterate (cuda_pipeline/slam.cuh:1475-1592).
+ * One Gauss-Newton step: linearization, Schur complement over the depths of
+ * the keyframes in ii (unless motion_only), LM damping S_ii += ep + lm*S_ii,
+ * fp64 Cholesky on the GPU, pose retraction of [t0,t1), depth
+ * back-substitution. Stream-ordered and asynchronous (the reference is
+ * synchronous); the index structures built from ii_host/jj_host are cached
+ * while the edge set is unchanged. An indefinite system leaves poses/disps
+ * untouched and is reported by slk_ba_status(). */
+int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const float* intrinsics,
+                   const float* target, const float* weight, const float* eta,
+                   const int* ii_gpu, const int* jj_gpu, const int* ii_host,
+                   const int* jj_host, int num_edges, int t0, int t1, float lm,
+                   float ep, int motion_only, hipStream_t stream);
+
+/* Synchronises `stream` and returns SLK_E_NOT_SPD if any iterate since the
+ * last call met an indefinite system, else SLK_OK; clears the flag. */
+int slk_ba_status(slk_ctx* ctx, hipStream_t stream);
+
+/* Debug copy of the last iterate's system (synchronising): S_host [(6P)^2]
+ * after Schur + damping, b_host [6P], dx_host [6P]; any may be NULL. *n gets
+ * 6P. Replaces the reference's stale S/b dumps read by
+ * compare_ba_hessian.py:215-221. */
+int slk_ba_last_system(slk_ctx* ctx, double* S_host, double* b_host, double* dx_host,
+                       int* n, hipStream_t stream);
+
+/* Stage kernels with the reference's argument lists (fp64 arithmetic inside,
+ * fp32 storage as in the reference): */
+/* projective_transform_kernel, ba.cuh:39-221: Hs [4][M][36], vs [2][M][6],
+ * Eii/Eij [M][6][H*W], Cii/bz [M][H*W] */
+int slk_ba_projective_transform(const float* target, const float* weight,
+                                const float* poses, const float* disps,
+                                const float* intrinsics, const int* ii, const int* jj,
+                                float* Hs, float* vs, float* Eii, float* Eij,
+                                float* Cii, float* bz, int M, int H, int W,
+                                hipStream_t stream);
+/* accum_kernel / accum_add_kernel(inps, ptrs, idxs, outs, D) over N_out rows,
+ * ba.cuh:226-263 (add != 0 selects accum_add) */
+int slk_ba_accum(const float* inps, const int* ptrs, const int* idxs, float* outs,
+                 int N_out, int D, int add, hipStream_t stream);
+/* damping_Q_kernel(C, eta, kf_map, Q, N_kf, HW, ep), ba.cuh:266-281 */
+int slk_ba_damping_q(float* C, const float* eta, const int* kf_map, float* Q,
+                     int N_kf, int HW, float ep, hipStream_t stream);
+/* EEt6x6_kernel(E, Q, idx, S, D, N_pairs), ba.cuh:303-342 */
+int slk_ba_eet6x6(const float* E, const float* Q, const int* idx, float* S, int D,
+                  int N_pairs, hipStream_t stream);
+/* Ev6x1_kernel(E, Q, w, idx, v, D, N_v), ba.cuh:346-372 (v += ...) */
+int slk_ba_ev6x1(const float* E, const float* Q, const float* w, const int* idx,
+                 float* v, int D, int N_v, hipStream_t stream);
+/* EvT6x1_kernel(E, x, idx, w, D, N_E, P), ba.cuh:376-393 */
+int slk_ba_evt6x1(const float* E, const float* x, const int* idx, float* w, int D,
+                  int N_E, int P, hipStream_t stream);
+/* depth_update_kernel(Q, w, dw, disps, kf_map, N_kf, HW), ba.cuh:284-299 */
+int slk_ba_depth_update(const float* Q, const float* w, const float* dw, float* disps,
+                        const int* kf_map, int N_kf, int HW, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLK_H */

@@ -1,0 +1,264 @@
+"""numpy front-end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker. The product library in
+slam-hands_amd/ never imports this module.
+
+Each wrapper names the reference function it restates (file:line in
+vibekernels/slam-hands); the C side (oracle.c) carries statement-level
+citations. Internals are fp64.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with gcc (make in oracle/)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-B" if force else "-s", "-C", _HERE, "liboracle.so"],
+                       check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        c_int, c_long, c_float, c_double = ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_double
+        sig = {
+            "orc_corr_volume": [_f32p, _f32p, c_int, c_int, c_double, _f32p],
+            "orc_corr_volume_f16": [_u16p, _u16p, c_int, c_int, c_double, _f32p],
+            "orc_avg_pool_2x2": [_f32p, _f32p, c_long, c_int, c_int],
+            "orc_corr_lookup_level": [_f32p, _f32p, _f32p, c_int, c_int, c_int, c_int, c_int,
+                                      c_float, c_int],
+            "orc_corr_batch": [_f32p, c_int, c_int, c_int, _i32p, _i32p, c_int, _f32p, _f32p,
+                               c_int, c_int, c_double],
+            "orc_act_se3": [_f64p, _f64p, _f64p, _f64p],
+            "orc_adj_se3": [_f64p, _f64p, _f64p, _f64p],
+            "orc_rel_se3": [_f64p, _f64p, _f64p, _f64p, _f64p, _f64p],
+            "orc_exp_se3": [_f64p, _f64p, _f64p],
+            "orc_retr_se3": [_f64p, _f64p, _f64p, _f64p, _f64p],
+            "orc_projmap": [_f32p, _f32p, _f32p, _i32p, _i32p, _f32p, _f32p, c_int, c_int, c_int],
+            "orc_pose_retr": [_f32p, _f32p, c_int, c_int],
+            "orc_disp_retr": [_f32p, _f32p, _i32p, c_int, c_int],
+            "orc_frame_distance": [_f32p, _f32p, _f32p, _i32p, _i32p, _f32p, c_int, c_int, c_int,
+                                   c_float],
+            "orc_ba_linearize": [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _i32p, _f64p, _f64p,
+                                 _f64p, _f64p, _f64p, _f64p, c_int, c_int, c_int],
+            "orc_cholesky_solve": [_f64p, _f64p, c_int],
+        }
+        for name, argtypes in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = None
+        L.orc_cholesky_solve.restype = c_int
+        # orc_ba_iterate takes optional (NULL-able) debug outputs
+        L.orc_ba_iterate.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _i32p,
+                                     c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float,
+                                     c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p]
+        L.orc_ba_iterate.restype = c_int
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# ----------------------------------------------------------------- correlation
+def corr_volume(fi, fj, alpha):
+    """cuda_slam/main.cu:1500-1515: vol[p, q] = alpha * sum_c fi[c, p] fj[c, q]."""
+    if fi.dtype == np.float16:
+        C = fi.shape[0]
+        HW = fi.size // C
+        out = np.empty((HW, HW), np.float32)
+        lib().orc_corr_volume_f16(_c(fi, np.float16).view(np.uint16).reshape(-1),
+                                  _c(fj, np.float16).view(np.uint16).reshape(-1), C, HW,
+                                  float(alpha), out)
+        return out
+    C = fi.shape[0]
+    HW = fi.size // C
+    out = np.empty((HW, HW), np.float32)
+    lib().orc_corr_volume(_c(fi, np.float32), _c(fj, np.float32), C, HW, float(alpha), out)
+    return out
+
+
+def avg_pool_2x2(x):
+    """cuda_slam/main.cu:1150-1170 over the last two axes, floor shapes."""
+    x = _c(x, np.float32)
+    H, W = x.shape[-2:]
+    N = x.size // (H * W)
+    out = np.empty(x.shape[:-2] + (H // 2, W // 2), np.float32)
+    lib().orc_avg_pool_2x2(x, out, N, H, W)
+    return out
+
+
+def pyramid(vol, h, w, levels=4):
+    """Levels of one edge: [HW, h>>l, w>>l] (main.cu:1519-1524, 1584-1597)."""
+    HW = vol.shape[0]
+    pyr = [vol.reshape(HW, h, w)]
+    for _ in range(1, levels):
+        pyr.append(avg_pool_2x2(pyr[-1]))
+    return pyr
+
+
+def lookup(pyr, coords, r=3):
+    """main.cu:1529-1552 / 1599-1612: [levels*(2r+1)^2, HW] for one edge.
+    coords: [2, h, w] or [2, HW] (x plane, y plane)."""
+    levels = len(pyr)
+    HW1, H1, W1 = pyr[0].shape[0], pyr[0].shape[1], pyr[0].shape[2]
+    D = 2 * r + 1
+    out = np.zeros((levels * D * D, HW1), np.float32)
+    cc = _c(coords, np.float32).reshape(2, HW1)
+    for l, lev in enumerate(pyr):
+        H2, W2 = lev.shape[1], lev.shape[2]
+        lib().orc_corr_lookup_level(_c(lev, np.float32).reshape(-1), cc.reshape(-1), out, r,
+                                    H1, W1, H2, W2, float(np.float32(1.0 / (1 << l))), l)
+    return out
+
+
+def corr_batch(fmaps, ii, jj, coords, alpha, levels=4, r=3):
+    """batch_build_and_sample_correlation (main.cu:1555-1613) on fp32 fmaps
+    [nframes, C, h, w], coords [B, 2, h*w] -> [B, levels*(2r+1)^2, h*w]."""
+    n, C, h, w = fmaps.shape
+    B = len(ii)
+    D = 2 * r + 1
+    out = np.zeros((B, levels * D * D, h * w), np.float32)
+    lib().orc_corr_batch(_c(fmaps, np.float32).reshape(-1), C, h, w, _c(ii, np.int32),
+                         _c(jj, np.int32), B, _c(coords, np.float32).reshape(-1), out, levels, r,
+                         float(alpha))
+    return out
+
+
+# ------------------------------------------------------------------------- SE3
+def act_se3(t, q, X):
+    Y = np.zeros(4)
+    lib().orc_act_se3(_c(t, np.float64), _c(q, np.float64), _c(X, np.float64), Y)
+    return Y
+
+
+def adj_se3(t, q, X):
+    Y = np.zeros(6)
+    lib().orc_adj_se3(_c(t, np.float64), _c(q, np.float64), _c(X, np.float64), Y)
+    return Y
+
+
+def rel_se3(ti, qi, tj, qj):
+    tij, qij = np.zeros(3), np.zeros(4)
+    lib().orc_rel_se3(_c(ti, np.float64), _c(qi, np.float64), _c(tj, np.float64),
+                      _c(qj, np.float64), tij, qij)
+    return tij, qij
+
+
+def exp_se3(xi):
+    t, q = np.zeros(3), np.zeros(4)
+    lib().orc_exp_se3(_c(xi, np.float64), t, q)
+    return t, q
+
+
+def retr_se3(xi, t, q):
+    t1, q1 = np.zeros(3), np.zeros(4)
+    lib().orc_retr_se3(_c(xi, np.float64), _c(t, np.float64), _c(q, np.float64), t1, q1)
+    return t1, q1
+
+
+def projmap(poses, disps, intr, ii, jj, H, W):
+    """se3.cuh:118-177 -> coords [M, H, W, 2], valid [M, H, W]."""
+    M = len(ii)
+    coords = np.zeros((M, H, W, 2), np.float32)
+    valid = np.zeros((M, H, W), np.float32)
+    lib().orc_projmap(_c(poses, np.float32).reshape(-1), _c(disps, np.float32).reshape(-1),
+                      _c(intr, np.float32), _c(ii, np.int32), _c(jj, np.int32), coords, valid,
+                      M, H, W)
+    return coords, valid
+
+
+def pose_retr(poses, dx, t0, t1):
+    """se3.cuh:179-193, returns the updated copy."""
+    p = _c(poses, np.float32).copy()
+    lib().orc_pose_retr(p.reshape(-1), _c(dx, np.float32).reshape(-1), t0, t1)
+    return p
+
+
+def disp_retr(disps, dz, inds):
+    d = _c(disps, np.float32).copy()
+    HW = d[0].size
+    lib().orc_disp_retr(d.reshape(-1), _c(dz, np.float32).reshape(-1), _c(inds, np.int32),
+                        len(inds), HW)
+    return d
+
+
+def frame_distance(poses, disps, intr, ii, jj, H, W, beta):
+    dist = np.zeros(len(ii), np.float32)
+    lib().orc_frame_distance(_c(poses, np.float32).reshape(-1),
+                             _c(disps, np.float32).reshape(-1), _c(intr, np.float32),
+                             _c(ii, np.int32), _c(jj, np.int32), dist, len(ii), H, W,
+                             float(beta))
+    return dist
+
+
+# -------------------------------------------------------------------------- BA
+def ba_linearize(target, weight, poses, disps, intr, ii, jj, H, W):
+    """projective_transform_kernel (ba.cuh:39-221), fp64 outputs."""
+    M = len(ii)
+    HW = H * W
+    Hs = np.zeros((4, M, 6, 6))
+    vs = np.zeros((2, M, 6))
+    Eii = np.zeros((M, 6, HW))
+    Eij = np.zeros((M, 6, HW))
+    Cii = np.zeros((M, HW))
+    bz = np.zeros((M, HW))
+    lib().orc_ba_linearize(_c(target, np.float32).reshape(-1),
+                           _c(weight, np.float32).reshape(-1),
+                           _c(poses, np.float32).reshape(-1), _c(disps, np.float32).reshape(-1),
+                           _c(intr, np.float32), _c(ii, np.int32), _c(jj, np.int32),
+                           Hs.reshape(-1), vs.reshape(-1), Eii.reshape(-1), Eij.reshape(-1),
+                           Cii.reshape(-1), bz.reshape(-1), M, H, W)
+    return Hs, vs, Eii, Eij, Cii, bz
+
+
+def ba_iterate(poses, disps, intr, target, weight, eta, ii, jj, H, W, t0, t1, lm, ep,
+               motion_only=False):
+    """One BundleAdjustment::iterate (ba.cuh:476-803). Returns a dict with the
+    updated poses/disps (copies) and the debug system S, b, dx, dz."""
+    poses = _c(poses, np.float32).copy()
+    disps = _c(disps, np.float32).copy()
+    nframes = poses.shape[0]
+    HW = H * W
+    n = 6 * (t1 - t0)
+    S = np.zeros((n, n))
+    b = np.zeros(n)
+    dx = np.zeros(n)
+    dz = np.zeros((nframes, HW))
+    st = lib().orc_ba_iterate(poses.reshape(-1), disps.reshape(-1), _c(intr, np.float32),
+                              _c(target, np.float32).reshape(-1),
+                              _c(weight, np.float32).reshape(-1),
+                              _c(eta, np.float32).reshape(-1), _c(ii, np.int32),
+                              _c(jj, np.int32), len(ii), nframes, H, W, t0, t1, float(lm),
+                              float(ep), int(bool(motion_only)), S.ctypes.data, b.ctypes.data,
+                              dx.ctypes.data, dz.ctypes.data)
+    return {"status": st, "poses": poses, "disps": disps, "S": S, "b": b, "dx": dx, "dz": dz}
+
+
+def cholesky_solve(S, b):
+    S = _c(S, np.float64).copy()
+    b = _c(b, np.float64).copy()
+    st = lib().orc_cholesky_solve(S, b, len(b))
+    return st, b

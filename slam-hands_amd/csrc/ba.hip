@@ -1,0 +1,1047 @@
+// Bundle adjustment for gfx950: linearization, Schur complement over the
+// depths, fp64 Cholesky pose solve and depth back-substitution, entirely on
+// the GPU with no host round trip inside an iteration.
+//
+// Reference semantics: cuda_slam/ba.cuh:39-803 (projective_transform_kernel,
+// accum, damping_Q, EEt6x6, Ev6x1, EvT6x1, depth_update, and the host
+// orchestration BundleAdjustment::iterate) with se3.cuh for the geometry.
+//
+// Iteration = 4 kernels on one stream:
+//   k_ba_lin_kf   grid (pixel chunk, keyframe): every edge whose depth owner
+//                 (ii) is that keyframe is linearized for the chunk's pixels in
+//                 fp64. Per-edge 12x12 Hessian + gradients are reduced per
+//                 workgroup; the depth terms (C, w), Q = 1/(C + 0.2 eta + 1e-7)
+//                 and the E rows of the keyframe are accumulated in place, so
+//                 the per-edge Eii/Eij/Cii/bz arrays of the reference never
+//                 exist.
+//   k_ba_schur    grid (pixel chunk, item): E_r1 Q E_r2^T for the upper pairs
+//                 of E rows sharing a keyframe, and E_r Q w per row.
+//   k_ba_solve_*  one workgroup: assembles S, b from the partial sums through
+//                 a per-block contribution list built on the host (no
+//                 atomics, fixed order), applies S_ii += ep + lm*S_ii,
+//                 factorizes (LDL^T, fp64), solves, rounds dx to fp32 and
+//                 retracts the poses [t0, t1).
+//   k_ba_backsub  grid (pixel chunk, keyframe): dz = Q (w - E^T dx),
+//                 disps += dz.
+// Host work per iteration is limited to comparing the edge list with the
+// cached one; index structures are rebuilt and uploaded only when it changes.
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <utility>
+
+#include "reduce.hpp"
+#include "se3.hpp"
+#include "slk_internal.hpp"
+
+namespace slk {
+
+namespace {
+
+constexpr int kLinWG = 256;
+constexpr int kLinPx = 512;  // pixels per k_ba_lin_kf workgroup (2 per thread)
+constexpr int kSchWG = 256;
+constexpr int kSchPx = 512;
+constexpr int kNH = 90;      // 78 upper-triangle Hessian entries + vi(6) + vj(6)
+constexpr int kSmallN = 90;  // LDS solve up to 90x90 fp64 (64800 bytes)
+constexpr double kMinDepth = 0.25;  // se3.cuh:6
+
+__host__ __device__ __forceinline__ int tri(int n, int m) { return n * (n + 1) / 2 + m; }
+
+// Offsets of the packed int plan (device copy of the host-built index data).
+struct PlanDev {
+    const int* kf_list;   // [N_kf] absolute keyframe of compact kf
+    const int* kf_eptr;   // [N_kf+1] edges of each kf (ii == kf), edge order
+    const int* kf_eidx;   // [M]
+    const int* edge_ri;   // [M] E row of (ii-t0, ii) or -1
+    const int* edge_rj;   // [M] E row of (jj-t0, ii) or -1
+    const int* row_pose;  // [N_E]
+    const int* row_kf;    // [N_E] compact kf
+    const int* kf_rptr;   // [N_kf+1]
+    const int* kf_rows;   // [N_E]
+    const int* pairs;     // [N_pu][3] = r1, r2, kc (r1 <= r2)
+    const int* sblk;      // [n_blk] a*P + b
+    const int* sblk_ptr;  // [n_blk+1]
+    const int* sblk_src;  // contributions (see encode_*)
+    const int* bv_ptr;    // [P+1]
+    const int* bv_src;
+};
+
+// contribution codes: type in bits 30..31
+__host__ __device__ __forceinline__ int code(int type, int v) { return (type << 30) | v; }
+__host__ __device__ __forceinline__ int code_type(int c) { return (int)((unsigned)c >> 30); }
+__host__ __device__ __forceinline__ int code_val(int c) { return c & 0x3fffffff; }
+
+struct Lin {
+    double Ji[2][6], Jj[2][6], Jz[2], w[2], r[2];
+};
+
+// Per-pixel linearization of one edge (ba.cuh:104-189), fp64.
+__device__ __forceinline__ void lin_pixel(const double* tij, const double* qij, double fx,
+                                          double fy, double cx, double cy, int k, int W,
+                                          double disp, double tgu, double tgv, double wtu,
+                                          double wtv, Lin& L) {
+    const int i = k / W, j = k - (k / W) * W;
+    const double u = (double)j, v = (double)i;
+    double Xi[4], Xj[4];
+    Xi[0] = (u - cx) / fx;
+    Xi[1] = (v - cy) / fy;
+    Xi[2] = 1.0;
+    Xi[3] = disp;
+    act_se3(tij, qij, Xi, Xj);
+    const double x = Xj[0], y = Xj[1], h = Xj[3];
+    const bool bad = Xj[2] < kMinDepth;
+    const double d = bad ? 0.0 : 1.0 / Xj[2];
+    const double d2 = d * d;
+    L.w[0] = bad ? 0.0 : 0.001 * wtu;
+    L.w[1] = bad ? 0.0 : 0.001 * wtv;
+    L.r[0] = tgu - (fx * d * x + cx);
+    L.r[1] = tgv - (fy * d * y + cy);
+    double* Jj = L.Jj[0];
+    Jj[0] = fx * (h * d);
+    Jj[1] = 0.0;
+    Jj[2] = fx * (-x * h * d2);
+    Jj[3] = fx * (-x * y * d2);
+    Jj[4] = fx * (1.0 + x * x * d2);
+    Jj[5] = fx * (-y * d);
+    L.Jz[0] = fx * (tij[0] * d - tij[2] * (x * d2));
+    adj_se3(tij, qij, Jj, L.Ji[0]);
+    Jj = L.Jj[1];
+    Jj[0] = 0.0;
+    Jj[1] = fy * (h * d);
+    Jj[2] = fy * (-y * h * d2);
+    Jj[3] = fy * (-1.0 - y * y * d2);
+    Jj[4] = fy * (x * y * d2);
+    Jj[5] = fy * (x * d);
+    L.Jz[1] = fy * (tij[1] * d - tij[2] * (y * d2));
+    adj_se3(tij, qij, Jj, L.Ji[1]);
+#pragma unroll
+    for (int n = 0; n < 6; n++) {
+        L.Ji[0][n] = -L.Ji[0][n];
+        L.Ji[1][n] = -L.Ji[1][n];
+    }
+}
+
+// acc[0..77] += weff J J^T (upper triangle of [Ji, Jj]), acc[78..89] += weff r J
+__device__ __forceinline__ void accum_hessian(const Lin& L, bool stereo, double (&acc)[kNH]) {
+#pragma unroll
+    for (int row = 0; row < 2; row++) {
+        const double we = stereo ? 0.0 : L.w[row];
+        double Jx[12];
+#pragma unroll
+        for (int n = 0; n < 6; n++) {
+            Jx[n] = L.Ji[row][n];
+            Jx[6 + n] = L.Jj[row][n];
+        }
+        int l = 0;
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            const double wn = we * Jx[n];
+#pragma unroll
+            for (int m = 0; m <= n; m++) acc[l++] += wn * Jx[m];
+        }
+        const double wr = we * L.r[row];
+#pragma unroll
+        for (int n = 0; n < 12; n++) acc[78 + n] += wr * Jx[n];
+    }
+}
+
+__device__ __forceinline__ void edge_rel(const float* poses, int ix, int jx, double* tij,
+                                         double* qij) {
+    if (ix == jx) {  // stereo pair (ba.cuh:73-78)
+        tij[0] = -0.1;
+        tij[1] = 0.0;
+        tij[2] = 0.0;
+        qij[0] = 0.0;
+        qij[1] = 0.0;
+        qij[2] = 0.0;
+        qij[3] = 1.0;
+    } else {
+        double ti[3], qi[4], tj[3], qj[4];
+        load_pose(poses, ix, ti, qi);
+        load_pose(poses, jx, tj, qj);
+        rel_se3(ti, qi, tj, qj, tij, qij);
+    }
+}
+
+// ------------------------------------------------------- k_ba_lin_kf ----
+__global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
+    PlanDev plan, const float* __restrict__ target, const float* __restrict__ weight,
+    const float* __restrict__ poses, const float* __restrict__ disps,
+    const float* __restrict__ intr, const int* __restrict__ ii, const int* __restrict__ jj,
+    const float* __restrict__ eta, double* __restrict__ hpart, double* __restrict__ E,
+    double* __restrict__ Qo, double* __restrict__ Wo, int HW, int W, int nch, int motion_only) {
+    __shared__ double red[kNH * (kLinWG / 64)];
+    __shared__ double rel[7];
+    const int chunk = blockIdx.x;
+    const int kc = blockIdx.y;
+    const int kf = plan.kf_list[kc];
+    const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
+    int kpx[2];
+    bool vpx[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        kpx[s] = chunk * kLinPx + s * kLinWG + threadIdx.x;
+        vpx[s] = kpx[s] < HW;
+    }
+    const int r0 = plan.kf_rptr[kc], r1 = plan.kf_rptr[kc + 1];
+    if (!motion_only) {
+        for (int r = r0; r < r1; r++) {
+            double* er = E + (size_t)plan.kf_rows[r] * 6 * HW;
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+                if (vpx[s])
+                    for (int n = 0; n < 6; n++) er[(size_t)n * HW + kpx[s]] = 0.0;
+        }
+    }
+    double Cacc[2] = {0.0, 0.0}, Wacc[2] = {0.0, 0.0};
+    double dsp[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) dsp[s] = vpx[s] ? (double)disps[(size_t)kf * HW + kpx[s]] : 1.0;
+
+    const int e0 = plan.kf_eptr[kc], e1 = plan.kf_eptr[kc + 1];
+    for (int ei = e0; ei < e1; ei++) {
+        const int e = plan.kf_eidx[ei];
+        const int ix = ii[e], jx = jj[e];
+        const bool stereo = ix == jx;
+        __syncthreads();
+        if (threadIdx.x == 0) edge_rel(poses, ix, jx, rel, rel + 3);
+        __syncthreads();
+        double tij[3] = {rel[0], rel[1], rel[2]};
+        double qij[4] = {rel[3], rel[4], rel[5], rel[6]};
+        const int ri = plan.edge_ri[e], rj = plan.edge_rj[e];
+        double acc[kNH];
+#pragma unroll
+        for (int n = 0; n < kNH; n++) acc[n] = 0.0;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            if (!vpx[s]) continue;
+            const int k = kpx[s];
+            const size_t base = (size_t)e * 2 * HW + k;
+            Lin L;
+            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)target[base],
+                      (double)target[base + HW], (double)weight[base], (double)weight[base + HW],
+                      L);
+            accum_hessian(L, stereo, acc);
+            if (!motion_only) {
+                Cacc[s] += L.w[0] * L.Jz[0] * L.Jz[0];
+                Cacc[s] += L.w[1] * L.Jz[1] * L.Jz[1];
+                Wacc[s] += L.w[0] * L.r[0] * L.Jz[0];
+                Wacc[s] += L.w[1] * L.r[1] * L.Jz[1];
+                const double a0 = stereo ? 0.0 : L.w[0] * L.Jz[0];
+                const double a1 = stereo ? 0.0 : L.w[1] * L.Jz[1];
+                if (ri >= 0) {
+                    double* er = E + (size_t)ri * 6 * HW + k;
+#pragma unroll
+                    for (int n = 0; n < 6; n++)
+                        er[(size_t)n * HW] += a0 * L.Ji[0][n] + a1 * L.Ji[1][n];
+                }
+                if (rj >= 0) {
+                    double* er = E + (size_t)rj * 6 * HW + k;
+#pragma unroll
+                    for (int n = 0; n < 6; n++)
+                        er[(size_t)n * HW] += a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                }
+            }
+        }
+        block_sum(acc, red);
+        if (threadIdx.x < kNH) {
+            double v = 0.0;
+#pragma unroll
+            for (int n = 0; n < kNH; n++)
+                if (n == (int)threadIdx.x) v = acc[n];
+            hpart[((size_t)e * nch + chunk) * kNH + threadIdx.x] = v;
+        }
+    }
+    if (!motion_only) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            if (!vpx[s]) continue;
+            const int k = kpx[s];
+            // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
+            const double c = Cacc[s] + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7;
+            Qo[(size_t)kc * HW + k] = 1.0 / c;
+            Wo[(size_t)kc * HW + k] = Wacc[s];
+        }
+    }
+}
+
+// -------------------------------------------------------- k_ba_schur ----
+__global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double* __restrict__ E,
+                                                     const double* __restrict__ Q,
+                                                     const double* __restrict__ Wv,
+                                                     double* __restrict__ spart, int HW,
+                                                     int nchS, int N_pu) {
+    __shared__ double red[36 * (kSchWG / 64)];
+    const int chunk = blockIdx.x;
+    const int item = blockIdx.y;
+    double acc[36];
+#pragma unroll
+    for (int n = 0; n < 36; n++) acc[n] = 0.0;
+    if (item < N_pu) {
+        const int r1 = plan.pairs[item * 3 + 0], r2 = plan.pairs[item * 3 + 1];
+        const int kc = plan.pairs[item * 3 + 2];
+        const double* e1 = E + (size_t)r1 * 6 * HW;
+        const double* e2 = E + (size_t)r2 * 6 * HW;
+        for (int k = chunk * kSchPx + threadIdx.x; k < min(HW, (chunk + 1) * kSchPx);
+             k += kSchWG) {
+            const double q = Q[(size_t)kc * HW + k];
+            double a[6], b[6];
+#pragma unroll
+            for (int n = 0; n < 6; n++) {
+                a[n] = e1[(size_t)n * HW + k] * q;
+                b[n] = e2[(size_t)n * HW + k];
+            }
+#pragma unroll
+            for (int n = 0; n < 6; n++)
+#pragma unroll
+                for (int m = 0; m < 6; m++) acc[n * 6 + m] += a[n] * b[m];
+        }
+    } else {
+        const int r = item - N_pu;
+        const int kc = plan.row_kf[r];
+        const double* er = E + (size_t)r * 6 * HW;
+        for (int k = chunk * kSchPx + threadIdx.x; k < min(HW, (chunk + 1) * kSchPx);
+             k += kSchWG) {
+            const double qw = Q[(size_t)kc * HW + k] * Wv[(size_t)kc * HW + k];
+#pragma unroll
+            for (int n = 0; n < 6; n++) acc[n] += qw * er[(size_t)n * HW + k];
+        }
+    }
+    block_sum(acc, red);
+    if (threadIdx.x < 36) {
+        double v = 0.0;
+#pragma unroll
+        for (int n = 0; n < 36; n++)
+            if (n == (int)threadIdx.x) v = acc[n];
+        spart[((size_t)item * nchS + chunk) * 36 + threadIdx.x] = v;
+    }
+}
+
+// ----------------------------------------------------------- solve ------
+struct SolveArgs {
+    PlanDev plan;
+    const double* hpart;
+    const double* spart;
+    int nch, nchS, N_pu, P, n, n_blk, t0, t1;
+    float lm, ep;
+    double* S;      // working matrix (global variant) [n*n]
+    double* S_dbg;  // [n*n] system before factorization
+    double* b_dbg;  // [n]
+    double* dx_dbg; // [n]
+    float* dx;      // [n] fp32 step used by retraction and back-substitution
+    int* flags;     // [0] this iteration not SPD, [1] sticky
+    float* poses;
+};
+
+// value of entry (r, c) of Hessian block `which` of edge e, summed over chunks
+__device__ __forceinline__ double hs_entry(const SolveArgs& A, int e, int which, int r, int c) {
+    int idx;
+    if (which == 0) idx = tri(max(r, c), min(r, c));
+    else if (which == 1) idx = tri(6 + c, r);
+    else if (which == 2) idx = tri(6 + r, c);
+    else idx = tri(6 + max(r, c), 6 + min(r, c));
+    const double* h = A.hpart + (size_t)e * A.nch * kNH + idx;
+    double s = 0.0;
+    for (int ch = 0; ch < A.nch; ch++) s += h[(size_t)ch * kNH];
+    return s;
+}
+
+__device__ __forceinline__ double sp_entry(const SolveArgs& A, int item, int e36) {
+    const double* s = A.spart + (size_t)item * A.nchS * 36 + e36;
+    double v = 0.0;
+    for (int ch = 0; ch < A.nchS; ch++) v += s[(size_t)ch * 36];
+    return v;
+}
+
+// Fills S (row-major n x n, zero outside listed blocks) and b; LM damping.
+__device__ void assemble(const SolveArgs& A, double* S, double* b) {
+    const int n = A.n, P = A.P;
+    for (int t = threadIdx.x; t < n * n; t += blockDim.x) S[t] = 0.0;
+    __syncthreads();
+    for (int t = threadIdx.x; t < A.n_blk * 36; t += blockDim.x) {
+        const int blk = t / 36, ent = t - blk * 36;
+        const int r = ent / 6, c = ent - r * 6;
+        const int ab = A.plan.sblk[blk];
+        const int a = ab / P, bb = ab - a * P;
+        double s = 0.0;
+        for (int q = A.plan.sblk_ptr[blk]; q < A.plan.sblk_ptr[blk + 1]; q++) {
+            const int cd = A.plan.sblk_src[q];
+            const int ty = code_type(cd), v = code_val(cd);
+            if (ty == 0) s += hs_entry(A, v >> 2, v & 3, r, c);
+            else if (ty == 1) s -= sp_entry(A, v, r * 6 + c);
+            else s -= sp_entry(A, v, c * 6 + r);
+        }
+        S[(size_t)(a * 6 + r) * n + bb * 6 + c] = s;
+    }
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        const int a = t / 6, k = t - a * 6;
+        double s = 0.0;
+        for (int q = A.plan.bv_ptr[a]; q < A.plan.bv_ptr[a + 1]; q++) {
+            const int cd = A.plan.bv_src[q];
+            const int ty = code_type(cd), v = code_val(cd);
+            if (ty == 0) {
+                const int e = v >> 1, which = v & 1;
+                const double* h = A.hpart + (size_t)e * A.nch * kNH + 78 + which * 6 + k;
+                for (int ch = 0; ch < A.nch; ch++) s += h[(size_t)ch * kNH];
+            } else {
+                s -= sp_entry(A, A.N_pu + v, k);
+            }
+        }
+        b[t] = s;
+    }
+    __syncthreads();
+    // LM damping after the Schur step (ba.cuh:749-750)
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        const double d = S[(size_t)t * n + t];
+        S[(size_t)t * n + t] = d + (double)A.ep + (double)A.lm * d;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < n * n; t += blockDim.x) A.S_dbg[t] = S[t];
+    for (int t = threadIdx.x; t < n; t += blockDim.x) A.b_dbg[t] = b[t];
+}
+
+// In-place LDL^T of the lower triangle: after it, S[j][j] = d_j and
+// S[i][j] = d_j * L[i][j] (i > j). One barrier per column. Returns false if a
+// pivot is not positive (same criterion as the Cholesky sqrt, ba.cuh:422).
+__device__ bool ldl_factor(double* S, int n) {
+    bool ok = true;
+    for (int j = 0; j < n; j++) {
+        const double d = S[(size_t)j * n + j];
+        if (!(d > 0.0)) ok = false;
+        const double inv = 1.0 / d;
+        const int m = n - j - 1;
+        for (int t = threadIdx.x; t < m * m; t += blockDim.x) {
+            const int i = j + 1 + t / m, k = j + 1 + t % m;
+            if (k <= i) S[(size_t)i * n + k] -= S[(size_t)i * n + j] * S[(size_t)k * n + j] * inv;
+        }
+        __syncthreads();
+    }
+    return ok;
+}
+
+// Solves L D L^T x = b (factor from ldl_factor), x in y[]. All threads call.
+__device__ void ldl_solve(const double* S, double* y, int n) {
+    for (int k = 0; k < n; k++) {
+        const double yk = y[k];
+        const double inv = 1.0 / S[(size_t)k * n + k];
+        __syncthreads();
+        for (int i = k + 1 + threadIdx.x; i < n; i += blockDim.x)
+            y[i] -= S[(size_t)i * n + k] * inv * yk;
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] /= S[(size_t)i * n + i];
+    __syncthreads();
+    for (int k = n - 1; k >= 0; k--) {
+        const double xk = y[k];
+        __syncthreads();
+        for (int i = threadIdx.x; i < k; i += blockDim.x)
+            y[i] -= S[(size_t)k * n + i] / S[(size_t)i * n + i] * xk;
+        __syncthreads();
+    }
+}
+
+__device__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
+    const int n = A.n;
+    if (threadIdx.x == 0) {
+        A.flags[0] = ok ? 0 : 1;
+        if (!ok) A.flags[1] = 1;
+    }
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        A.dx_dbg[t] = ok ? x[t] : 0.0;
+        A.dx[t] = ok ? (float)x[t] : 0.0f;
+    }
+    if (!ok) return;
+    // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
+    for (int k = A.t0 + threadIdx.x; k < A.t1; k += blockDim.x) {
+        double t[3], q[4], xi[6], t1[3], q1[4];
+        load_pose(A.poses, k, t, q);
+        for (int m = 0; m < 6; m++) xi[m] = (double)(float)x[(k - A.t0) * 6 + m];
+        retr_se3(xi, t, q, t1, q1);
+        for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
+        for (int m = 0; m < 4; m++) A.poses[k * 7 + 3 + m] = (float)q1[m];
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_ba_solve_small(SolveArgs A) {
+    extern __shared__ double smem[];
+    double* S = smem;
+    double* b = smem + (size_t)A.n * A.n;
+    assemble(A, S, b);
+    const bool ok = ldl_factor(S, A.n);
+    if (ok) ldl_solve(S, b, A.n);
+    __syncthreads();
+    finish_solve(A, b, ok);
+}
+
+__global__ __launch_bounds__(1024) void k_ba_solve_large(SolveArgs A) {
+    extern __shared__ double smem[];
+    double* b = smem;
+    double* S = A.S;
+    assemble(A, S, b);
+    const bool ok = ldl_factor(S, A.n);
+    if (ok) ldl_solve(S, b, A.n);
+    __syncthreads();
+    finish_solve(A, b, ok);
+}
+
+// ------------------------------------------------------ k_ba_backsub ----
+// EvT6x1 + accum + depth_update (ba.cuh:762-783) fused per keyframe pixel.
+__global__ __launch_bounds__(256) void k_ba_backsub(PlanDev plan, const double* __restrict__ E,
+                                                    const double* __restrict__ Q,
+                                                    const double* __restrict__ Wv,
+                                                    const float* __restrict__ dx,
+                                                    const int* __restrict__ flags,
+                                                    float* __restrict__ disps, int HW) {
+    if (flags[0]) return;
+    const int kc = blockIdx.y;
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= HW) return;
+    double dw = 0.0;
+    for (int r = plan.kf_rptr[kc]; r < plan.kf_rptr[kc + 1]; r++) {
+        const int row = plan.kf_rows[r];
+        const double* er = E + (size_t)row * 6 * HW + k;
+        const float* x = dx + plan.row_pose[row] * 6;
+#pragma unroll
+        for (int n = 0; n < 6; n++) dw += er[(size_t)n * HW] * (double)x[n];
+    }
+    const double dz = Q[(size_t)kc * HW + k] * (Wv[(size_t)kc * HW + k] - dw);
+    float* d = disps + (size_t)plan.kf_list[kc] * HW + k;
+    *d = (float)((double)*d + dz);
+}
+
+}  // namespace
+
+// ----------------------------------------------------------- host side ---
+struct BaState {
+    // cached plan key
+    bool valid = false;
+    std::vector<int> key_ii, key_jj;
+    int key_t0 = 0, key_t1 = 0, key_motion = 0, key_HW = 0;
+    // plan sizes
+    int M = 0, P = 0, n = 0, N_kf = 0, N_E = 0, N_pu = 0, n_blk = 0, nch = 1, nchS = 1;
+    std::vector<int> host;  // packed plan
+    size_t off[15] = {0};
+    DevBuf plan_dev, hpart, E, Q, Wv, spart, S, S_dbg, b_dbg, dx_dbg, dx, flags;
+    HostStage stage;
+    bool has_system = false;
+};
+
+namespace {
+
+PlanDev plan_ptrs(BaState* s) {
+    const int* base = s->plan_dev.as<int>();
+    PlanDev p;
+    const int** f[15] = {&p.kf_list, &p.kf_eptr, &p.kf_eidx, &p.edge_ri, &p.edge_rj,
+                         &p.row_pose, &p.row_kf, &p.kf_rptr, &p.kf_rows, &p.pairs,
+                         &p.sblk, &p.sblk_ptr, &p.sblk_src, &p.bv_ptr, &p.bv_src};
+    for (int i = 0; i < 15; i++) *f[i] = base + s->off[i];
+    return p;
+}
+
+// Builds the index structures of ba.cuh:520-663 once per edge set: keyframes
+// (unique ii, ascending), E rows keyed by (pose, kf) in order of first
+// appearance, upper pairs of rows per keyframe, and the contribution lists of
+// every 6x6 block of S and every 6-vector of b.
+int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, int motion_only,
+               int HW) {
+    const int P = t1 - t0;
+    s->M = M;
+    s->P = P;
+    s->n = 6 * P;
+    int maxf = 0;
+    for (int e = 0; e < M; e++) {
+        if (ii[e] < 0 || jj[e] < 0) return fail(SLK_E_ARG, "ba_iterate: negative frame index");
+        maxf = std::max(maxf, std::max(ii[e], jj[e]));
+    }
+    std::vector<int> kf_compact(maxf + 1, -1), kf_list;
+    for (int e = 0; e < M; e++) kf_compact[ii[e]] = 0;
+    for (int k = 0; k <= maxf; k++)
+        if (kf_compact[k] == 0) {
+            kf_compact[k] = (int)kf_list.size();
+            kf_list.push_back(k);
+        }
+    const int N_kf = (int)kf_list.size();
+    std::vector<int> kf_eptr(N_kf + 1, 0), kf_eidx(M);
+    for (int e = 0; e < M; e++) kf_eptr[kf_compact[ii[e]] + 1]++;
+    for (int k = 0; k < N_kf; k++) kf_eptr[k + 1] += kf_eptr[k];
+    {
+        std::vector<int> fill(kf_eptr.begin(), kf_eptr.end() - 1);
+        for (int e = 0; e < M; e++) kf_eidx[fill[kf_compact[ii[e]]]++] = e;
+    }
+    std::map<std::pair<int, int>, int> rowmap;
+    std::vector<int> row_pose, row_kf, edge_ri(M, -1), edge_rj(M, -1);
+    if (!motion_only) {
+        auto get_row = [&](int p, int kfabs) {
+            auto key = std::make_pair(p, kfabs);
+            auto it = rowmap.find(key);
+            if (it != rowmap.end()) return it->second;
+            const int r = (int)row_pose.size();
+            rowmap[key] = r;
+            row_pose.push_back(p);
+            row_kf.push_back(kf_compact[kfabs]);
+            return r;
+        };
+        for (int e = 0; e < M; e++) {
+            const int pi = ii[e] - t0, pj = jj[e] - t0;
+            if (pi >= 0 && pi < P) edge_ri[e] = get_row(pi, ii[e]);
+            if (pj >= 0 && pj < P) edge_rj[e] = get_row(pj, ii[e]);
+        }
+    }
+    const int N_E = (int)row_pose.size();
+    std::vector<int> kf_rptr(N_kf + 1, 0), kf_rows(N_E);
+    for (int r = 0; r < N_E; r++) kf_rptr[row_kf[r] + 1]++;
+    for (int k = 0; k < N_kf; k++) kf_rptr[k + 1] += kf_rptr[k];
+    {
+        std::vector<int> fill(kf_rptr.begin(), kf_rptr.end() - 1);
+        for (int r = 0; r < N_E; r++) kf_rows[fill[row_kf[r]]++] = r;
+    }
+    std::vector<int> pairs;
+    for (int kc = 0; kc < N_kf; kc++)
+        for (int a = kf_rptr[kc]; a < kf_rptr[kc + 1]; a++)
+            for (int b = a; b < kf_rptr[kc + 1]; b++) {
+                pairs.push_back(kf_rows[a]);
+                pairs.push_back(kf_rows[b]);
+                pairs.push_back(kc);
+            }
+    const int N_pu = (int)pairs.size() / 3;
+    // contributions per destination block a*P+b
+    std::map<int, std::vector<int>> blocks;
+    for (int e = 0; e < M; e++) {
+        const int a = ii[e] - t0, b = jj[e] - t0;
+        const bool va = a >= 0 && a < P, vb = b >= 0 && b < P;
+        if (va) blocks[a * P + a].push_back(code(0, e * 4 + 0));
+        if (va && vb) {
+            blocks[a * P + b].push_back(code(0, e * 4 + 1));
+            blocks[b * P + a].push_back(code(0, e * 4 + 2));
+        }
+        if (vb) blocks[b * P + b].push_back(code(0, e * 4 + 3));
+    }
+    for (int p = 0; p < N_pu; p++) {
+        const int r1 = pairs[3 * p], r2 = pairs[3 * p + 1];
+        const int a = row_pose[r1], b = row_pose[r2];
+        blocks[a * P + b].push_back(code(1, p));
+        if (r1 != r2) blocks[b * P + a].push_back(code(2, p));
+    }
+    std::vector<int> sblk, sblk_ptr(1, 0), sblk_src;
+    for (auto& kv : blocks) {
+        sblk.push_back(kv.first);
+        sblk_src.insert(sblk_src.end(), kv.second.begin(), kv.second.end());
+        sblk_ptr.push_back((int)sblk_src.size());
+    }
+    std::vector<std::vector<int>> bl(P);
+    for (int e = 0; e < M; e++) {
+        const int a = ii[e] - t0, b = jj[e] - t0;
+        if (a >= 0 && a < P) bl[a].push_back(code(0, e * 2 + 0));
+        if (b >= 0 && b < P) bl[b].push_back(code(0, e * 2 + 1));
+    }
+    for (int r = 0; r < N_E; r++) bl[row_pose[r]].push_back(code(1, r));
+    std::vector<int> bv_ptr(1, 0), bv_src;
+    for (int a = 0; a < P; a++) {
+        bv_src.insert(bv_src.end(), bl[a].begin(), bl[a].end());
+        bv_ptr.push_back((int)bv_src.size());
+    }
+    s->N_kf = N_kf;
+    s->N_E = N_E;
+    s->N_pu = N_pu;
+    s->n_blk = (int)sblk.size();
+    s->nch = (HW + kLinPx - 1) / kLinPx;
+    s->nchS = (HW + kSchPx - 1) / kSchPx;
+    const std::vector<int>* parts[15] = {&kf_list, &kf_eptr, &kf_eidx, &edge_ri, &edge_rj,
+                                         &row_pose, &row_kf, &kf_rptr, &kf_rows, &pairs,
+                                         &sblk, &sblk_ptr, &sblk_src, &bv_ptr, &bv_src};
+    s->host.clear();
+    for (int i = 0; i < 15; i++) {
+        s->off[i] = s->host.size();
+        s->host.insert(s->host.end(), parts[i]->begin(), parts[i]->end());
+        s->host.push_back(0);  // keeps every array non-empty
+    }
+    return SLK_OK;
+}
+
+}  // namespace
+
+int ba_create(slk_ctx* ctx) {
+    ctx->ba = new BaState();
+    SLK_TRY(ctx->ba->flags.ensure(4 * sizeof(int)));
+    SLK_HIP(hipMemset(ctx->ba->flags.ptr, 0, 4 * sizeof(int)));
+    return SLK_OK;
+}
+
+void ba_destroy(slk_ctx* ctx) {
+    BaState* s = ctx->ba;
+    if (!s) return;
+    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->E, &s->Q, &s->Wv, &s->spart,
+                      &s->S, &s->S_dbg, &s->b_dbg, &s->dx_dbg, &s->dx, &s->flags};
+    for (DevBuf* b : bufs) b->release();
+    s->stage.release();
+    delete s;
+    ctx->ba = nullptr;
+}
+
+}  // namespace slk
+
+using namespace slk;
+
+extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const float* intrinsics,
+                              const float* target, const float* weight, const float* eta,
+                              const int* ii_gpu, const int* jj_gpu, const int* ii_host,
+                              const int* jj_host, int num_edges, int t0, int t1, float lm,
+                              float ep, int motion_only, hipStream_t stream) {
+    if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_iterate: null context");
+    const int M = num_edges;
+    if (M < 1 || t0 < 0 || t1 <= t0) return fail(SLK_E_ARG, "ba_iterate: need M >= 1, 0 <= t0 < t1");
+    if (!poses || !disps || !intrinsics || !target || !weight || !ii_gpu || !jj_gpu ||
+        !ii_host || !jj_host || (!motion_only && !eta))
+        return fail(SLK_E_ARG, "ba_iterate: null argument");
+    BaState* s = ctx->ba;
+    const int HW = ctx->HW;
+    motion_only = motion_only ? 1 : 0;
+    const bool same = s->valid && s->key_t0 == t0 && s->key_t1 == t1 &&
+                      s->key_motion == motion_only && s->key_HW == HW &&
+                      (int)s->key_ii.size() == M &&
+                      std::memcmp(s->key_ii.data(), ii_host, sizeof(int) * M) == 0 &&
+                      std::memcmp(s->key_jj.data(), jj_host, sizeof(int) * M) == 0;
+    if (!same) {
+        s->valid = false;
+        SLK_TRY(build_plan(s, ii_host, jj_host, M, t0, t1, motion_only, HW));
+        if (s->n > 0x7fff) return fail(SLK_E_ARG, "ba_iterate: too many free poses");
+        const size_t pbytes = s->host.size() * sizeof(int);
+        SLK_TRY(s->stage.ensure(pbytes));
+        std::memcpy(s->stage.ptr, s->host.data(), pbytes);
+        SLK_TRY(s->plan_dev.ensure(pbytes));
+        SLK_HIP(hipMemcpyAsync(s->plan_dev.ptr, s->stage.ptr, pbytes, hipMemcpyHostToDevice,
+                               stream));
+        SLK_HIP(hipEventRecord(s->stage.done, stream));
+        s->stage.pending = true;
+        const size_t n = (size_t)s->n;
+        SLK_TRY(s->hpart.ensure((size_t)M * s->nch * kNH * sizeof(double)));
+        SLK_TRY(s->E.ensure(std::max<size_t>(1, (size_t)s->N_E * 6 * HW) * sizeof(double)));
+        SLK_TRY(s->Q.ensure((size_t)s->N_kf * HW * sizeof(double)));
+        SLK_TRY(s->Wv.ensure((size_t)s->N_kf * HW * sizeof(double)));
+        SLK_TRY(s->spart.ensure(
+            std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * s->nchS * 36) * sizeof(double)));
+        if (n > (size_t)kSmallN) SLK_TRY(s->S.ensure(n * n * sizeof(double)));
+        SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
+        SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
+        SLK_TRY(s->dx_dbg.ensure(n * sizeof(double)));
+        SLK_TRY(s->dx.ensure(n * sizeof(float)));
+        s->key_ii.assign(ii_host, ii_host + M);
+        s->key_jj.assign(jj_host, jj_host + M);
+        s->key_t0 = t0;
+        s->key_t1 = t1;
+        s->key_motion = motion_only;
+        s->key_HW = HW;
+        s->valid = true;
+    }
+    const PlanDev plan = plan_ptrs(s);
+    hipLaunchKernelGGL(k_ba_lin_kf, dim3(s->nch, s->N_kf), dim3(kLinWG), 0, stream, plan, target,
+                       weight, poses, disps, intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
+                       s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW, ctx->w,
+                       s->nch, motion_only);
+    SLK_HIP(hipGetLastError());
+    if (!motion_only && s->N_pu + s->N_E > 0) {
+        hipLaunchKernelGGL(k_ba_schur, dim3(s->nchS, s->N_pu + s->N_E), dim3(kSchWG), 0, stream,
+                           plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
+                           s->spart.as<double>(), HW, s->nchS, s->N_pu);
+        SLK_HIP(hipGetLastError());
+    }
+    SolveArgs A;
+    A.plan = plan;
+    A.hpart = s->hpart.as<double>();
+    A.spart = s->spart.as<double>();
+    A.nch = s->nch;
+    A.nchS = s->nchS;
+    A.N_pu = s->N_pu;
+    A.P = s->P;
+    A.n = s->n;
+    A.n_blk = s->n_blk;
+    A.t0 = t0;
+    A.t1 = t1;
+    A.lm = lm;
+    A.ep = ep;
+    A.S = s->S.as<double>();
+    A.S_dbg = s->S_dbg.as<double>();
+    A.b_dbg = s->b_dbg.as<double>();
+    A.dx_dbg = s->dx_dbg.as<double>();
+    A.dx = s->dx.as<float>();
+    A.flags = s->flags.as<int>();
+    A.poses = poses;
+    if (s->n <= kSmallN) {
+        const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);
+        hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(1024), shm, stream, A);
+    } else {
+        const size_t shm = (size_t)s->n * sizeof(double);
+        hipLaunchKernelGGL(k_ba_solve_large, dim3(1), dim3(1024), shm, stream, A);
+    }
+    SLK_HIP(hipGetLastError());
+    if (!motion_only && s->N_E > 0) {
+        hipLaunchKernelGGL(k_ba_backsub, dim3((HW + 255) / 256, s->N_kf), dim3(256), 0, stream,
+                           plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
+                           s->dx.as<float>(), s->flags.as<int>(), disps, HW);
+        SLK_HIP(hipGetLastError());
+    }
+    s->has_system = true;
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_status(slk_ctx* ctx, hipStream_t stream) {
+    if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_status: null context");
+    int f[4];
+    SLK_HIP(hipMemcpyAsync(f, ctx->ba->flags.ptr, sizeof f, hipMemcpyDeviceToHost, stream));
+    SLK_HIP(hipStreamSynchronize(stream));
+    const int bad = f[1];
+    SLK_HIP(hipMemsetAsync(ctx->ba->flags.ptr, 0, sizeof f, stream));
+    SLK_HIP(hipStreamSynchronize(stream));
+    return bad ? fail(SLK_E_NOT_SPD, "ba_iterate: system not positive definite") : SLK_OK;
+}
+
+extern "C" int slk_ba_last_system(slk_ctx* ctx, double* S_host, double* b_host, double* dx_host,
+                                  int* n_out, hipStream_t stream) {
+    if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_last_system: null context");
+    BaState* s = ctx->ba;
+    if (!s->has_system) return fail(SLK_E_STATE, "ba_last_system: no iterate yet");
+    const size_t n = (size_t)s->n;
+    if (n_out) *n_out = (int)n;
+    if (S_host)
+        SLK_HIP(hipMemcpyAsync(S_host, s->S_dbg.ptr, n * n * sizeof(double), hipMemcpyDeviceToHost,
+                               stream));
+    if (b_host)
+        SLK_HIP(hipMemcpyAsync(b_host, s->b_dbg.ptr, n * sizeof(double), hipMemcpyDeviceToHost,
+                               stream));
+    if (dx_host)
+        SLK_HIP(hipMemcpyAsync(dx_host, s->dx_dbg.ptr, n * sizeof(double), hipMemcpyDeviceToHost,
+                               stream));
+    SLK_HIP(hipStreamSynchronize(stream));
+    return SLK_OK;
+}
+
+// ----------------------------------------------- reference stage kernels ---
+namespace {
+
+// projective_transform_kernel (ba.cuh:39-221): one workgroup per edge.
+__global__ __launch_bounds__(256) void k_pt(const float* __restrict__ target,
+                                            const float* __restrict__ weight,
+                                            const float* __restrict__ poses,
+                                            const float* __restrict__ disps,
+                                            const float* __restrict__ intr,
+                                            const int* __restrict__ ii, const int* __restrict__ jj,
+                                            float* __restrict__ Hs, float* __restrict__ vs,
+                                            float* __restrict__ Eii, float* __restrict__ Eij,
+                                            float* __restrict__ Cii, float* __restrict__ bz, int M,
+                                            int H, int W) {
+    __shared__ double red[kNH * 4];
+    __shared__ double rel[7];
+    __shared__ double tot[kNH];
+    const int e = blockIdx.x;
+    const int ix = ii[e], jx = jj[e];
+    const bool stereo = ix == jx;
+    const int HW = H * W;
+    if (threadIdx.x == 0) edge_rel(poses, ix, jx, rel, rel + 3);
+    __syncthreads();
+    const double tij[3] = {rel[0], rel[1], rel[2]};
+    const double qij[4] = {rel[3], rel[4], rel[5], rel[6]};
+    const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
+    double acc[kNH];
+#pragma unroll
+    for (int n = 0; n < kNH; n++) acc[n] = 0.0;
+    for (int k = threadIdx.x; k < HW; k += blockDim.x) {
+        const size_t base = (size_t)e * 2 * HW + k;
+        Lin L;
+        lin_pixel(tij, qij, fx, fy, cx, cy, k, W, (double)disps[(size_t)ix * HW + k],
+                  (double)target[base], (double)target[base + HW], (double)weight[base],
+                  (double)weight[base + HW], L);
+        accum_hessian(L, stereo, acc);
+        Cii[(size_t)e * HW + k] = (float)(L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1]);
+        bz[(size_t)e * HW + k] =
+            (float)(L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1]);
+        const double a0 = stereo ? 0.0 : L.w[0] * L.Jz[0];
+        const double a1 = stereo ? 0.0 : L.w[1] * L.Jz[1];
+        for (int n = 0; n < 6; n++) {
+            Eii[((size_t)e * 6 + n) * HW + k] = (float)(a0 * L.Ji[0][n] + a1 * L.Ji[1][n]);
+            Eij[((size_t)e * 6 + n) * HW + k] = (float)(a0 * L.Jj[0][n] + a1 * L.Jj[1][n]);
+        }
+    }
+    block_sum(acc, red);
+    if (threadIdx.x == 0)
+        for (int n = 0; n < kNH; n++) tot[n] = acc[n];
+    __syncthreads();
+    for (int t = threadIdx.x; t < 144; t += blockDim.x) {
+        const int blk = t / 36, r = (t % 36) / 6, c = t % 6;
+        int idx;
+        if (blk == 0) idx = tri(max(r, c), min(r, c));
+        else if (blk == 1) idx = tri(6 + c, r);
+        else if (blk == 2) idx = tri(6 + r, c);
+        else idx = tri(6 + max(r, c), 6 + min(r, c));
+        Hs[(size_t)blk * M * 36 + e * 36 + r * 6 + c] = (float)tot[idx];
+    }
+    if (threadIdx.x < 12) {
+        const int which = threadIdx.x / 6, n = threadIdx.x % 6;
+        vs[(size_t)which * M * 6 + e * 6 + n] = (float)tot[78 + which * 6 + n];
+    }
+}
+
+__global__ void k_accum(const float* __restrict__ inps, const int* __restrict__ ptrs,
+                        const int* __restrict__ idxs, float* __restrict__ outs, int D, int add) {
+    const int row = blockIdx.y;
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= D) return;
+    double x = 0.0;
+    for (int i = ptrs[row]; i < ptrs[row + 1]; i++) x += (double)inps[(size_t)idxs[i] * D + k];
+    float* o = outs + (size_t)row * D + k;
+    *o = add ? (float)((double)*o + x) : (float)x;
+}
+
+__global__ void k_damping_q(float* __restrict__ C, const float* __restrict__ eta,
+                            const int* __restrict__ kf_map, float* __restrict__ Q, int N_kf, int HW,
+                            float ep) {
+    const long idx = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (idx >= (long)N_kf * HW) return;
+    const int kf = (int)(idx / HW), d = (int)(idx % HW);
+    const double c = (double)C[idx] + 0.2 * (double)eta[(size_t)kf_map[kf] * HW + d] + (double)ep;
+    C[idx] = (float)c;
+    Q[idx] = (float)(1.0 / c);
+}
+
+__global__ __launch_bounds__(256) void k_eet(const float* __restrict__ E,
+                                             const float* __restrict__ Q,
+                                             const int* __restrict__ idx, float* __restrict__ S,
+                                             int D) {
+    __shared__ double red[36 * 4];
+    const int p = blockIdx.x;
+    const int ix = idx[p * 3], jx = idx[p * 3 + 1], kx = idx[p * 3 + 2];
+    double acc[36];
+#pragma unroll
+    for (int n = 0; n < 36; n++) acc[n] = 0.0;
+    for (int k = threadIdx.x; k < D; k += blockDim.x) {
+        const double q = Q[(size_t)kx * D + k];
+        double a[6], b[6];
+        for (int n = 0; n < 6; n++) {
+            a[n] = (double)E[((size_t)ix * 6 + n) * D + k] * q;
+            b[n] = (double)E[((size_t)jx * 6 + n) * D + k];
+        }
+#pragma unroll
+        for (int n = 0; n < 6; n++)
+#pragma unroll
+            for (int m = 0; m < 6; m++) acc[n * 6 + m] += a[n] * b[m];
+    }
+    block_sum(acc, red);
+    if (threadIdx.x == 0)
+        for (int n = 0; n < 36; n++) S[(size_t)p * 36 + n] = (float)acc[n];
+}
+
+__global__ __launch_bounds__(256) void k_ev(const float* __restrict__ E, const float* __restrict__ Q,
+                                            const float* __restrict__ w,
+                                            const int* __restrict__ idx, float* __restrict__ v,
+                                            int D) {
+    __shared__ double red[6 * 4];
+    const int r = blockIdx.x;
+    const int kx = idx[r];
+    double acc[6] = {0, 0, 0, 0, 0, 0};
+    for (int k = threadIdx.x; k < D; k += blockDim.x) {
+        const double qw = (double)Q[(size_t)kx * D + k] * (double)w[(size_t)kx * D + k];
+        for (int n = 0; n < 6; n++) acc[n] += qw * (double)E[((size_t)r * 6 + n) * D + k];
+    }
+    block_sum(acc, red);
+    if (threadIdx.x == 0)
+        for (int n = 0; n < 6; n++) v[r * 6 + n] = (float)((double)v[r * 6 + n] + acc[n]);
+}
+
+__global__ void k_evt(const float* __restrict__ E, const float* __restrict__ x,
+                      const int* __restrict__ idx, float* __restrict__ w, int D, int P) {
+    const int r = blockIdx.y;
+    const int ix = idx[r];
+    if (ix < 0 || ix >= P) return;
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= D) return;
+    double dw = 0.0;
+    for (int n = 0; n < 6; n++) dw += (double)E[((size_t)r * 6 + n) * D + k] * (double)x[ix * 6 + n];
+    w[(size_t)r * D + k] = (float)dw;
+}
+
+__global__ void k_depth_update(const float* __restrict__ Q, const float* __restrict__ w,
+                               const float* __restrict__ dw, float* __restrict__ disps,
+                               const int* __restrict__ kf_map, int N_kf, int HW) {
+    const long idx = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (idx >= (long)N_kf * HW) return;
+    const int kf = (int)(idx / HW), d = (int)(idx % HW);
+    const double dz = (double)Q[idx] * ((double)w[idx] - (double)dw[idx]);
+    float* o = disps + (size_t)kf_map[kf] * HW + d;
+    *o = (float)((double)*o + dz);
+}
+
+}  // namespace
+
+extern "C" int slk_ba_projective_transform(const float* target, const float* weight,
+                                           const float* poses, const float* disps,
+                                           const float* intrinsics, const int* ii, const int* jj,
+                                           float* Hs, float* vs, float* Eii, float* Eij, float* Cii,
+                                           float* bz, int M, int H, int W, hipStream_t stream) {
+    if (M <= 0) return SLK_OK;
+    if (!target || !weight || !poses || !disps || !intrinsics || !ii || !jj || !Hs || !vs ||
+        !Eii || !Eij || !Cii || !bz || H < 1 || W < 1)
+        return fail(SLK_E_ARG, "ba_projective_transform: bad args");
+    hipLaunchKernelGGL(k_pt, dim3(M), dim3(256), 0, stream, target, weight, poses, disps,
+                       intrinsics, ii, jj, Hs, vs, Eii, Eij, Cii, bz, M, H, W);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_accum(const float* inps, const int* ptrs, const int* idxs, float* outs,
+                            int N_out, int D, int add, hipStream_t stream) {
+    if (N_out <= 0 || D <= 0) return SLK_OK;
+    if (!inps || !ptrs || !idxs || !outs) return fail(SLK_E_ARG, "ba_accum: null argument");
+    hipLaunchKernelGGL(k_accum, dim3((D + 255) / 256, N_out), dim3(256), 0, stream, inps, ptrs,
+                       idxs, outs, D, add);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_damping_q(float* C, const float* eta, const int* kf_map, float* Q, int N_kf,
+                                int HW, float ep, hipStream_t stream) {
+    const long total = (long)N_kf * HW;
+    if (total <= 0) return SLK_OK;
+    if (!C || !eta || !kf_map || !Q) return fail(SLK_E_ARG, "ba_damping_q: null argument");
+    hipLaunchKernelGGL(k_damping_q, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, C,
+                       eta, kf_map, Q, N_kf, HW, ep);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_eet6x6(const float* E, const float* Q, const int* idx, float* S, int D,
+                             int N_pairs, hipStream_t stream) {
+    if (N_pairs <= 0) return SLK_OK;
+    if (!E || !Q || !idx || !S || D <= 0) return fail(SLK_E_ARG, "ba_eet6x6: bad args");
+    hipLaunchKernelGGL(k_eet, dim3(N_pairs), dim3(256), 0, stream, E, Q, idx, S, D);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_ev6x1(const float* E, const float* Q, const float* w, const int* idx,
+                            float* v, int D, int N_v, hipStream_t stream) {
+    if (N_v <= 0) return SLK_OK;
+    if (!E || !Q || !w || !idx || !v || D <= 0) return fail(SLK_E_ARG, "ba_ev6x1: bad args");
+    hipLaunchKernelGGL(k_ev, dim3(N_v), dim3(256), 0, stream, E, Q, w, idx, v, D);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_evt6x1(const float* E, const float* x, const int* idx, float* w, int D,
+                             int N_E, int P, hipStream_t stream) {
+    if (N_E <= 0 || D <= 0) return SLK_OK;
+    if (!E || !x || !idx || !w) return fail(SLK_E_ARG, "ba_evt6x1: null argument");
+    hipLaunchKernelGGL(k_evt, dim3((D + 255) / 256, N_E), dim3(256), 0, stream, E, x, idx, w, D, P);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_ba_depth_update(const float* Q, const float* w, const float* dw, float* disps,
+                                   const int* kf_map, int N_kf, int HW, hipStream_t stream) {
+    const long total = (long)N_kf * HW;
+    if (total <= 0) return SLK_OK;
+    if (!Q || !w || !dw || !disps || !kf_map) return fail(SLK_E_ARG, "ba_depth_update: null argument");
+    hipLaunchKernelGGL(k_depth_update, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       Q, w, dw, disps, kf_map, N_kf, HW);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}

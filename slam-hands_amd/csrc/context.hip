@@ -1,0 +1,112 @@
+// Context lifetime, error reporting and buffer helpers of libslk.
+#include <cstdio>
+
+#include "slk_internal.hpp"
+
+namespace slk {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int DevBuf::ensure(size_t n) {
+    if (n <= bytes && ptr) return SLK_OK;
+    release();
+    if (n == 0) return SLK_OK;
+    SLK_HIP(hipMalloc(&ptr, n));
+    bytes = n;
+    return SLK_OK;
+}
+
+void DevBuf::release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+int HostStage::ensure(size_t n) {
+    SLK_TRY(wait());
+    if (!done) SLK_HIP(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+    if (n <= bytes && ptr) return SLK_OK;
+    if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+    SLK_HIP(hipHostMalloc(&ptr, n, hipHostMallocDefault));
+    bytes = n;
+    return SLK_OK;
+}
+
+int HostStage::wait() {
+    if (pending) {
+        pending = false;
+        SLK_HIP(hipEventSynchronize(done));
+    }
+    return SLK_OK;
+}
+
+void HostStage::release() {
+    if (pending) (void)hipEventSynchronize(done);
+    pending = false;
+    if (ptr) (void)hipHostFree(ptr);
+    if (done) (void)hipEventDestroy(done);
+    ptr = nullptr;
+    done = nullptr;
+    bytes = 0;
+}
+
+}  // namespace slk
+
+extern "C" const char* slk_last_error(void) { return slk::g_last_error.c_str(); }
+
+extern "C" int slk_create(slk_ctx** out, int h, int w, int C, int max_batch, int levels,
+                          int radius, float corr_scale) {
+    using namespace slk;
+    if (!out) return fail(SLK_E_ARG, "slk_create: null output pointer");
+    *out = nullptr;
+    if (h < 1 || w < 1 || C < 2 || (C & 1) || max_batch < 1)
+        return fail(SLK_E_ARG, "slk_create: need h,w >= 1, even C >= 2, max_batch >= 1");
+    if (levels < 1 || levels > kMaxLevels)
+        return fail(SLK_E_ARG, "slk_create: levels must be in [1, 4]");
+    if (radius != 3) return fail(SLK_E_ARG, "slk_create: only radius 3 is implemented");
+    if ((h >> (levels - 1)) < 1 || (w >> (levels - 1)) < 1)
+        return fail(SLK_E_ARG, "slk_create: feature map too small for the pyramid depth");
+    if ((long)h * w > (1L << 24)) return fail(SLK_E_ARG, "slk_create: h*w too large");
+    slk_ctx* ctx = new slk_ctx();
+    ctx->h = h;
+    ctx->w = w;
+    ctx->HW = h * w;
+    ctx->C = C;
+    ctx->levels = levels;
+    ctx->radius = radius;
+    ctx->max_batch = max_batch;
+    ctx->alpha = corr_scale;
+    for (int l = 0; l < levels; l++) {
+        ctx->lh[l] = h >> l;
+        ctx->lw[l] = w >> l;
+    }
+    int st = hipGetDevice(&ctx->device) == hipSuccess ? SLK_OK
+                                                       : fail(SLK_E_HIP, "hipGetDevice failed");
+    if (st == SLK_OK) st = corr_alloc(ctx);
+    if (st == SLK_OK) st = ba_create(ctx);
+    if (st != SLK_OK) {
+        slk_destroy(ctx);
+        return st;
+    }
+    *out = ctx;
+    return SLK_OK;
+}
+
+extern "C" int slk_destroy(slk_ctx* ctx) {
+    if (!ctx) return SLK_OK;
+    slk::ba_destroy(ctx);
+    for (int l = 0; l < slk::kMaxLevels; l++) {
+        ctx->batch_lvl[l].release();
+        ctx->single_lvl[l].release();
+    }
+    ctx->zero_idx.release();
+    delete ctx;
+    return SLK_OK;
+}

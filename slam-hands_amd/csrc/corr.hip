@@ -1,0 +1,510 @@
+// All-pairs correlation, 2x2 average-pool pyramid and radius-3 bilinear
+// lookup for gfx950 (MI355X).
+//
+// Reference semantics: cuda_slam/main.cu:1077-1217 (kernels) and :1500-1613
+// (build_correlation, sample_correlation, batch_build_and_sample_correlation).
+//
+// k_corr_pyramid: vol[e][p][q] = alpha * sum_c fa[c][p] * fb[c][q] on fp32
+// MFMA (v_mfma_f32_32x32x2f32), with every pyramid level produced in the
+// epilogue from the tile still in registers. A workgroup is 4 waves stacked
+// over 4x32 source pixels; each wave owns an 8-row x 32-column band of the
+// target image (eight 32x32 accumulator blocks), which is exactly one level-3
+// cell column group, so levels 1..3 never need data from another wave:
+//   x-pairs come from the neighbouring lane (lane ^ 1, ^ 2, ^ 4),
+//   y-pairs from the accumulator block of the next target row.
+// Both operands are read straight from global memory in the MFMA operand
+// layout (consecutive lanes = consecutive pixels of one channel), so loads
+// and level-0 stores are 128-byte coalesced per half-wave.
+#include <cmath>
+
+#include "slk_internal.hpp"
+
+namespace slk {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWG = 256;           // 4 waves
+constexpr int kWaveSrc = 32;       // source pixels per wave
+constexpr int kTileSrc = 128;      // source pixels per workgroup
+constexpr int kBand = 8;           // target rows per tile (2^(levels-1) for 4 levels)
+constexpr int kCols = 32;          // target columns per tile
+constexpr int kMaxEdgesPerLaunch = 64;
+
+struct EdgeIdx {
+    int ii[kMaxEdgesPerLaunch];
+    int jj[kMaxEdgesPerLaunch];
+};
+
+struct LevelOut {
+    float* p[kMaxLevels];
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs; remap the linear id so
+// each XCD walks a contiguous range of (edge, tile) ids and its L2 holds the
+// few feature maps of the edges it is working on.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+    constexpr int X = 8;
+    const int q = total / X, rem = total % X;
+    const int xcd = bid % X, local = bid / X;
+    return (xcd < rem) ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
+__device__ __forceinline__ float ldf(const float* p) { return *p; }
+__device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
+
+template <typename Tin>
+__global__ __launch_bounds__(kWG) void k_corr_pyramid(
+    const Tin* __restrict__ fa, const Tin* __restrict__ fb, long fstride,
+    const int* __restrict__ ia, const int* __restrict__ ib, EdgeIdx eidx, LevelOut lo,
+    int slot0, int h, int w, int C, float alpha, int levels, int mtiles, int nbands,
+    int ncb) {
+    const int HW = h * w;
+    const int tpe = mtiles * nbands * ncb;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int e = bid / tpe;
+    int t = bid - e * tpe;
+    const int cb = t % ncb;
+    t /= ncb;
+    const int band = t % nbands;
+    const int mt = t / nbands;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int p0 = mt * kTileSrc + wave * kWaveSrc;
+    if (p0 >= HW) return;  // whole wave outside (no LDS, no barriers)
+    const int y0 = band * kBand, x0 = cb * kCols;
+    const int col = lane & 31, khalf = lane >> 5;
+
+    const int fi = ia ? ia[e] : eidx.ii[e];
+    const int fj = ib ? ib[e] : eidx.jj[e];
+    const int pa = p0 + col;
+    const bool va = pa < HW;
+    const Tin* A = fa + (long)fi * fstride + (long)khalf * HW + (va ? pa : 0);
+    const int xb = x0 + col;
+    const Tin* Bp = fb + (long)fj * fstride + (long)khalf * HW;
+    int boff[kBand];
+    bool vb[kBand];
+#pragma unroll
+    for (int r = 0; r < kBand; r++) {
+        const int y = y0 + r;
+        vb[r] = (y < h) && (xb < w);
+        boff[r] = vb[r] ? y * w + xb : 0;
+    }
+
+    f32x16 acc[kBand];
+#pragma unroll
+    for (int r = 0; r < kBand; r++) acc[r] = (f32x16){0};
+
+#pragma unroll 4
+    for (int c = 0; c < C; c += 2) {
+        const long off = (long)c * HW;
+        float a = ldf(A + off);
+        a = va ? a : 0.0f;
+        float b[kBand];
+#pragma unroll
+        for (int r = 0; r < kBand; r++) {
+            const float v = ldf(Bp + off + boff[r]);
+            b[r] = vb[r] ? v : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < kBand; r++)
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b[r], acc[r], 0, 0, 0);
+    }
+
+    // Accumulator layout of v_mfma_f32_32x32x2f32: lane l, register v holds
+    // D[i][j] with j = l % 32 (target column) and
+    // i = 8*(v/4) + 4*(l/32) + v%4 (source row of the wave's 32).
+    const int slot = slot0 + e;
+    float* out0 = lo.p[0] + (size_t)slot * HW * HW;
+#pragma unroll
+    for (int r = 0; r < kBand; r++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[r][v] *= alpha;
+    }
+#pragma unroll
+    for (int r = 0; r < kBand; r++) {
+        if (!vb[r]) continue;
+        const int q = (y0 + r) * w + xb;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
+            if (p < HW) __builtin_nontemporal_store(acc[r][v], out0 + (size_t)p * HW + q);
+        }
+    }
+    if (levels < 2) return;
+
+    // level 1: 0.25f*(((in[y][x] + in[y][x+1]) + in[y+1][x]) + in[y+1][x+1]),
+    // the order of avg_pool_2x2_kernel (main.cu:1166-1167)
+    const int h1 = h >> 1, w1 = w >> 1;
+    float l1[4][16];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float a = acc[2 * r][v];
+            const float c = acc[2 * r + 1][v];
+            const float b = __shfl_xor(a, 1);
+            const float d = __shfl_xor(c, 1);
+            float s = a + b;
+            s = s + c;
+            s = s + d;
+            l1[r][v] = 0.25f * s;
+        }
+    }
+    {
+        float* out1 = lo.p[1] + (size_t)slot * HW * (h1 * w1);
+        const int x1 = xb >> 1;
+        const bool lane_ok = ((col & 1) == 0) && x1 < w1;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int y1 = (y0 >> 1) + r;
+            if (!lane_ok || y1 >= h1) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
+                if (p < HW)
+                    __builtin_nontemporal_store(l1[r][v],
+                                                out1 + (size_t)p * (h1 * w1) + y1 * w1 + x1);
+            }
+        }
+    }
+    if (levels < 3) return;
+
+    const int h2 = h >> 2, w2 = w >> 2;
+    float l2[2][16];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float a = l1[2 * r][v];
+            const float c = l1[2 * r + 1][v];
+            const float b = __shfl_xor(a, 2);
+            const float d = __shfl_xor(c, 2);
+            float s = a + b;
+            s = s + c;
+            s = s + d;
+            l2[r][v] = 0.25f * s;
+        }
+    }
+    {
+        float* out2 = lo.p[2] + (size_t)slot * HW * (h2 * w2);
+        const int x2 = xb >> 2;
+        const bool lane_ok = ((col & 3) == 0) && x2 < w2;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int y2 = (y0 >> 2) + r;
+            if (!lane_ok || y2 >= h2) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
+                if (p < HW)
+                    __builtin_nontemporal_store(l2[r][v],
+                                                out2 + (size_t)p * (h2 * w2) + y2 * w2 + x2);
+            }
+        }
+    }
+    if (levels < 4) return;
+
+    const int h3 = h >> 3, w3 = w >> 3;
+    float* out3 = lo.p[3] + (size_t)slot * HW * (h3 * w3);
+    const int x3 = xb >> 3, y3 = y0 >> 3;
+    const bool lane_ok = ((col & 7) == 0) && x3 < w3 && y3 < h3;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const float a = l2[0][v];
+        const float c = l2[1][v];
+        const float b = __shfl_xor(a, 4);
+        const float d = __shfl_xor(c, 4);
+        float s = a + b;
+        s = s + c;
+        s = s + d;
+        const float l3 = 0.25f * s;
+        const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
+        if (lane_ok && p < HW)
+            __builtin_nontemporal_store(l3, out3 + (size_t)p * (h3 * w3) + y3 * w3 + x3);
+    }
+}
+
+// ---------------------------------------------------------------- lookup --
+struct LevelIn {
+    const float* p[kMaxLevels];
+    int h[kMaxLevels];
+    int w[kMaxLevels];
+};
+
+// One thread per (source pixel, level, edge): zero-padded bilinear samples at
+// (x0 - 3 + a, y0 - 3 + b), a,b in [0,7), from that pixel's own row of the
+// level (main.cu:1175-1217). The four corner terms of a channel are added in
+// the reference's loop order (i outer = x, j inner = y): (a,b), (a,b+1),
+// (a+1,b), (a+1,b+1). Non-finite coordinates give zeros.
+__global__ __launch_bounds__(256) void k_corr_lookup(LevelIn lv, const float* __restrict__ coords,
+                                                     float* __restrict__ out, int HW1,
+                                                     int level_base, int nch) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    const int l = blockIdx.y;
+    const int e = blockIdx.z;
+    if (p >= HW1) return;
+    const int H2 = lv.h[l], W2 = lv.w[l];
+    const float scale = 1.0f / (float)(1 << (level_base + l));
+    const float x0 = coords[(size_t)e * 2 * HW1 + p] * scale;
+    const float y0 = coords[(size_t)e * 2 * HW1 + HW1 + p] * scale;
+    float* o = out + ((size_t)e * nch + (size_t)(level_base + l) * 49) * HW1 + p;
+    if (!(isfinite(x0) && isfinite(y0))) {
+#pragma unroll
+        for (int k = 0; k < 49; k++) o[(size_t)k * HW1] = 0.0f;
+        return;
+    }
+    const float fx = floorf(x0), fy = floorf(y0);
+    const float dx = x0 - fx, dy = y0 - fy;
+    const int ix = (int)fminf(fmaxf(fx, -1048576.0f), 1048576.0f) - 3;
+    const int iy = (int)fminf(fmaxf(fy, -1048576.0f), 1048576.0f) - 3;
+    const float* vol = lv.p[l] + ((size_t)e * HW1 + p) * (size_t)(H2 * W2);
+    float win[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int y = iy + j;
+        const bool vy = (unsigned)y < (unsigned)H2;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int x = ix + i;
+            const bool ok = vy && (unsigned)x < (unsigned)W2;
+            win[j][i] = ok ? vol[y * W2 + x] : 0.0f;
+        }
+    }
+    const float wx1 = dx, wx0 = 1.0f - dx, wy1 = dy, wy0 = 1.0f - dy;
+#pragma unroll
+    for (int a = 0; a < 7; a++) {
+#pragma unroll
+        for (int b = 0; b < 7; b++) {
+            float s = win[b][a] * wx0 * wy0;
+            s = s + win[b + 1][a] * wx0 * wy1;
+            s = s + win[b][a + 1] * wx1 * wy0;
+            s = s + win[b + 1][a + 1] * wx1 * wy1;
+            o[(size_t)(a * 7 + b) * HW1] = s;
+        }
+    }
+}
+
+template <typename Tin>
+int launch_pyramid(slk_ctx* ctx, const Tin* fa, const Tin* fb, long fstride, const int* ia,
+                   const int* ib, const EdgeIdx& eidx, int n, float* const* lvl, int slot0,
+                   hipStream_t stream) {
+    const int mtiles = (ctx->HW + kTileSrc - 1) / kTileSrc;
+    const int nbands = (ctx->h + kBand - 1) / kBand;
+    const int ncb = (ctx->w + kCols - 1) / kCols;
+    const long total = (long)n * mtiles * nbands * ncb;
+    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
+    LevelOut lo;
+    for (int l = 0; l < kMaxLevels; l++) lo.p[l] = l < ctx->levels ? lvl[l] : nullptr;
+    hipLaunchKernelGGL(k_corr_pyramid<Tin>, dim3((unsigned)total), dim3(kWG), 0, stream, fa, fb,
+                       fstride, ia, ib, eidx, lo, slot0, ctx->h, ctx->w, ctx->C, ctx->alpha,
+                       ctx->levels, mtiles, nbands, ncb);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+int launch_lookup(const LevelIn& lv, int nlev, int level_base, int nch, const float* coords,
+                  float* out, int B, int HW1, hipStream_t stream) {
+    if (B <= 0) return SLK_OK;
+    dim3 grid((HW1 + 255) / 256, nlev, B);
+    hipLaunchKernelGGL(k_corr_lookup, grid, dim3(256), 0, stream, lv, coords, out, HW1, level_base,
+                       nch);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+LevelIn level_in(slk_ctx* ctx, DevBuf* bufs) {
+    LevelIn lv{};
+    for (int l = 0; l < ctx->levels; l++) {
+        lv.p[l] = bufs[l].as<float>();
+        lv.h[l] = ctx->lh[l];
+        lv.w[l] = ctx->lw[l];
+    }
+    return lv;
+}
+
+int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, const int* ii_host,
+                    const int* jj_host, const int* ii_dev, const int* jj_dev, int B,
+                    const float* coords, float* out, hipStream_t stream) {
+    if (!ctx || !fmaps || !coords || !out || B < 0)
+        return fail(SLK_E_ARG, "corr_batch: null argument");
+    if (dtype != SLK_F32 && dtype != SLK_F16) return fail(SLK_E_ARG, "corr_batch: bad dtype");
+    if (fstride < (long)ctx->C * ctx->HW) return fail(SLK_E_ARG, "corr_batch: fmap_stride < C*h*w");
+    const int HW = ctx->HW;
+    const int nch = ctx->levels * 49;
+    float* lvl[kMaxLevels];
+    for (int l = 0; l < ctx->levels; l++) lvl[l] = ctx->batch_lvl[l].as<float>();
+    const LevelIn lv = level_in(ctx, ctx->batch_lvl);
+    for (int b0 = 0; b0 < B; b0 += ctx->max_batch) {
+        const int nb = B - b0 < ctx->max_batch ? B - b0 : ctx->max_batch;
+        for (int s0 = 0; s0 < nb; s0 += kMaxEdgesPerLaunch) {
+            const int n = nb - s0 < kMaxEdgesPerLaunch ? nb - s0 : kMaxEdgesPerLaunch;
+            EdgeIdx eidx{};
+            if (ii_host) {
+                for (int k = 0; k < n; k++) {
+                    eidx.ii[k] = ii_host[b0 + s0 + k];
+                    eidx.jj[k] = jj_host[b0 + s0 + k];
+                    if (eidx.ii[k] < 0 || eidx.jj[k] < 0)
+                        return fail(SLK_E_ARG, "corr_batch: negative frame index");
+                }
+            }
+            const int* ia = ii_host ? nullptr : ii_dev + b0 + s0;
+            const int* ib = ii_host ? nullptr : jj_dev + b0 + s0;
+            if (dtype == SLK_F32) {
+                const float* f = static_cast<const float*>(fmaps);
+                SLK_TRY(launch_pyramid<float>(ctx, f, f, fstride, ia, ib, eidx, n, lvl, s0, stream));
+            } else {
+                const _Float16* f = static_cast<const _Float16*>(fmaps);
+                SLK_TRY(launch_pyramid<_Float16>(ctx, f, f, fstride, ia, ib, eidx, n, lvl, s0,
+                                                 stream));
+            }
+        }
+        SLK_TRY(launch_lookup(lv, ctx->levels, 0, nch, coords + (size_t)b0 * 2 * HW,
+                              out + (size_t)b0 * nch * HW, nb, HW, stream));
+    }
+    return SLK_OK;
+}
+
+}  // namespace
+
+int corr_alloc(slk_ctx* ctx) {
+    const size_t HW = (size_t)ctx->HW;
+    for (int l = 0; l < ctx->levels; l++) {
+        const size_t plane = (size_t)ctx->lh[l] * ctx->lw[l];
+        SLK_TRY(ctx->batch_lvl[l].ensure((size_t)ctx->max_batch * HW * plane * sizeof(float)));
+        SLK_TRY(ctx->single_lvl[l].ensure(HW * plane * sizeof(float)));
+    }
+    SLK_TRY(ctx->zero_idx.ensure(sizeof(int) * 4));
+    SLK_HIP(hipMemset(ctx->zero_idx.ptr, 0, sizeof(int) * 4));
+    return SLK_OK;
+}
+
+}  // namespace slk
+
+using namespace slk;
+
+extern "C" int slk_corr_batch_build_and_sample(slk_ctx* ctx, const void* fmaps, int dtype,
+                                               long fmap_stride, const int* ii_host,
+                                               const int* jj_host, int B, const float* coords,
+                                               float* out, hipStream_t stream) {
+    if (B > 0 && (!ii_host || !jj_host)) return fail(SLK_E_ARG, "corr_batch: null indices");
+    return corr_batch_impl(ctx, fmaps, dtype, fmap_stride, ii_host, jj_host, nullptr, nullptr, B,
+                           coords, out, stream);
+}
+
+extern "C" int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fmaps, int dtype,
+                                                   long fmap_stride, const int* ii_dev,
+                                                   const int* jj_dev, int B,
+                                                   const float* coords, float* out,
+                                                   hipStream_t stream) {
+    if (B > 0 && (!ii_dev || !jj_dev)) return fail(SLK_E_ARG, "corr_batch: null indices");
+    return corr_batch_impl(ctx, fmaps, dtype, fmap_stride, nullptr, nullptr, ii_dev, jj_dev, B,
+                           coords, out, stream);
+}
+
+extern "C" int slk_corr_build(slk_ctx* ctx, const void* f_i, const void* f_j, int dtype,
+                              hipStream_t stream) {
+    if (!ctx || !f_i || !f_j) return fail(SLK_E_ARG, "corr_build: null argument");
+    float* lvl[kMaxLevels];
+    for (int l = 0; l < ctx->levels; l++) lvl[l] = ctx->single_lvl[l].as<float>();
+    const int* z = ctx->zero_idx.as<int>();
+    EdgeIdx eidx{};
+    if (dtype == SLK_F32) {
+        SLK_TRY(launch_pyramid<float>(ctx, static_cast<const float*>(f_i),
+                                      static_cast<const float*>(f_j), 0, z, z, eidx, 1, lvl, 0,
+                                      stream));
+    } else if (dtype == SLK_F16) {
+        SLK_TRY(launch_pyramid<_Float16>(ctx, static_cast<const _Float16*>(f_i),
+                                         static_cast<const _Float16*>(f_j), 0, z, z, eidx, 1, lvl,
+                                         0, stream));
+    } else {
+        return fail(SLK_E_ARG, "corr_build: bad dtype");
+    }
+    ctx->single_built = true;
+    return SLK_OK;
+}
+
+extern "C" int slk_corr_sample(slk_ctx* ctx, const float* coords, float* out, hipStream_t stream) {
+    if (!ctx || !coords || !out) return fail(SLK_E_ARG, "corr_sample: null argument");
+    if (!ctx->single_built) return fail(SLK_E_STATE, "corr_sample: no volume built");
+    const LevelIn lv = level_in(ctx, ctx->single_lvl);
+    return launch_lookup(lv, ctx->levels, 0, ctx->levels * 49, coords, out, 1, ctx->HW, stream);
+}
+
+extern "C" int slk_corr_level(slk_ctx* ctx, int level, const float** ptr, int* h2, int* w2) {
+    if (!ctx || level < 0 || level >= ctx->levels) return fail(SLK_E_ARG, "corr_level: bad level");
+    if (ptr) *ptr = ctx->single_lvl[level].as<float>();
+    if (h2) *h2 = ctx->lh[level];
+    if (w2) *w2 = ctx->lw[level];
+    return SLK_OK;
+}
+
+namespace {
+__global__ void k_avg_pool_2x2(const float* __restrict__ in, float* __restrict__ out, long N, int H,
+                               int W) {
+    const int oH = H / 2, oW = W / 2;
+    const long total = N * oH * oW;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        const long n = idx / (oH * oW);
+        const int rem = (int)(idx - n * oH * oW);
+        const int oy = rem / oW, ox = rem % oW;
+        const float* src = in + (size_t)n * H * W + (2 * oy) * W + 2 * ox;
+        float s = src[0] + src[1];
+        s = s + src[W];
+        s = s + src[W + 1];
+        out[idx] = 0.25f * s;
+    }
+}
+
+__global__ void k_coords_hw2_to_2hw(const float* __restrict__ hw2, float* __restrict__ chw, int M,
+                                    int HW) {
+    const long idx = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (idx >= (long)M * HW) return;
+    const long e = idx / HW, k = idx % HW;
+    chw[e * 2 * HW + k] = hw2[idx * 2 + 0];
+    chw[e * 2 * HW + HW + k] = hw2[idx * 2 + 1];
+}
+}  // namespace
+
+extern "C" int slk_avg_pool_2x2(const float* in, float* out, long N, int H, int W,
+                                hipStream_t stream) {
+    if (!in || !out || N < 0 || H < 0 || W < 0) return fail(SLK_E_ARG, "avg_pool_2x2: bad args");
+    const long total = N * (H / 2) * (W / 2);
+    if (total == 0) return SLK_OK;
+    long blocks = (total + 255) / 256;
+    if (blocks > 65536 * 4) blocks = 65536 * 4;
+    hipLaunchKernelGGL(k_avg_pool_2x2, dim3((unsigned)blocks), dim3(256), 0, stream, in, out, N, H,
+                       W);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_corr_sample_level(const float* volumes, const float* coords, float* corr_out,
+                                     int M, int r, int H1, int W1, int H2, int W2, int hw,
+                                     float coord_scale, int level_idx, hipStream_t stream) {
+    if (r != 3) return fail(SLK_E_ARG, "corr_sample_level: only r = 3");
+    if (!volumes || !coords || !corr_out || M < 0 || H1 * W1 != hw || level_idx < 0 ||
+        level_idx >= kMaxLevels)
+        return fail(SLK_E_ARG, "corr_sample_level: bad args");
+    if (coord_scale != 1.0f / (float)(1 << level_idx))
+        return fail(SLK_E_ARG, "corr_sample_level: coord_scale must be 2^-level_idx");
+    LevelIn lv{};
+    lv.p[0] = volumes;
+    lv.h[0] = H2;
+    lv.w[0] = W2;
+    // channels [level_idx*49, +49) of a [M][196][hw] buffer, like the reference
+    return launch_lookup(lv, 1, level_idx, 196, coords, corr_out, M, hw, stream);
+}
+
+extern "C" int slk_coords_hw2_to_2hw(const float* hw2, float* chw, int M, int HW,
+                                     hipStream_t stream) {
+    if (!hw2 || !chw || M < 0 || HW < 0) return fail(SLK_E_ARG, "coords_hw2_to_2hw: bad args");
+    const long total = (long)M * HW;
+    if (total == 0) return SLK_OK;
+    hipLaunchKernelGGL(k_coords_hw2_to_2hw, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, hw2, chw, M, HW);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}

@@ -1,0 +1,80 @@
+// Internal declarations of libslk (MI355X / gfx950 DROID-SLAM per-edge path).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "slk.h"
+
+namespace slk {
+
+// Records a failure message for slk_last_error() and returns `code`.
+int fail(int code, const std::string& msg);
+
+#define SLK_HIP(expr)                                                              \
+    do {                                                                           \
+        hipError_t _e = (expr);                                                    \
+        if (_e != hipSuccess)                                                      \
+            return ::slk::fail(SLK_E_HIP, std::string(#expr " -> ") +             \
+                                              hipGetErrorString(_e));             \
+    } while (0)
+
+#define SLK_TRY(expr)                      \
+    do {                                   \
+        int _s = (expr);                   \
+        if (_s != SLK_OK) return _s;       \
+    } while (0)
+
+// Grow-only device buffer owned by a context (no allocation in steady state).
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int ensure(size_t n);
+    void release();
+    template <typename T>
+    T* as() const { return static_cast<T*>(ptr); }
+};
+
+// Pinned host staging buffer, guarded by an event so a new upload never
+// overwrites bytes an earlier asynchronous copy may still be reading.
+struct HostStage {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+    int ensure(size_t n);
+    int wait();
+    void release();
+};
+
+struct BaState;  // ba.hip
+
+constexpr int kMaxLevels = 4;
+
+}  // namespace slk
+
+struct slk_ctx {
+    int device = 0;
+    int h = 0, w = 0, HW = 0, C = 0, levels = 4, radius = 3, max_batch = 48;
+    float alpha = 1.0f / 16.0f;
+    int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
+    // correlation scratch: batched pyramid [max_batch][HW][lh*lw] per level
+    slk::DevBuf batch_lvl[slk::kMaxLevels];
+    // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
+    slk::DevBuf single_lvl[slk::kMaxLevels];
+    bool single_built = false;
+    slk::DevBuf zero_idx;  // device int {0}
+    slk::BaState* ba = nullptr;
+};
+
+namespace slk {
+// corr.hip
+int corr_alloc(slk_ctx* ctx);
+// ba.hip
+int ba_create(slk_ctx* ctx);
+void ba_destroy(slk_ctx* ctx);
+}  // namespace slk

@@ -1,0 +1,331 @@
+"""ctypes binding of libslk (include/slk.h) plus the minimal HIP runtime calls
+the tests and the benchmark need (device buffers, streams, events).
+
+This is plumbing around the C ABI, not a second implementation: every compute
+call goes to the gfx950 kernels in libslk.so, and a missing library or GPU is
+an error, never a fallback.
+
+Names mirror the reference's C++ members (cuda_slam/main.cu CudaDroid,
+cuda_slam/ba.cuh BundleAdjustment, cuda_slam/corr.cuh CorrBlock).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libslk.so")
+HIP_LIB = "libamdhip64.so"
+
+SLK_OK, SLK_E_ARG, SLK_E_HIP, SLK_E_NOT_SPD, SLK_E_STATE = range(5)
+SLK_F32, SLK_F16 = 0, 1
+
+# every entry point declared in include/slk.h
+EXPORTS = [
+    "slk_create", "slk_destroy", "slk_last_error",
+    "slk_corr_batch_build_and_sample", "slk_corr_batch_build_and_sample_dev",
+    "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
+    "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
+    "slk_projmap", "slk_pose_retr", "slk_disp_retr", "slk_frame_distance", "slk_clamp_disps",
+    "slk_ba_iterate", "slk_ba_status", "slk_ba_last_system", "slk_ba_projective_transform",
+    "slk_ba_accum", "slk_ba_damping_q", "slk_ba_eet6x6", "slk_ba_ev6x1", "slk_ba_evt6x1",
+    "slk_ba_depth_update",
+]
+
+
+class SlkError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"slk error {code}: {msg}")
+        self.code = code
+
+
+def build():
+    """Compile libslk.so for gfx950 (make in slam-hands_amd/)."""
+    subprocess.run(["make", "-s", "-j8", "-C", HERE, "libslk.so"], check=True)
+    return LIB_PATH
+
+
+_lib = None
+_hip = None
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+L = ctypes.c_long
+F = ctypes.c_float
+
+
+def lib():
+    """The loaded libslk.so. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                               "(there is no CPU fallback)")
+        L_ = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "slk_create": [ctypes.POINTER(P), I, I, I, I, I, I, F],
+            "slk_destroy": [P],
+            "slk_corr_batch_build_and_sample": [P, P, I, L, P, P, I, P, P, P],
+            "slk_corr_batch_build_and_sample_dev": [P, P, I, L, P, P, I, P, P, P],
+            "slk_corr_build": [P, P, P, I, P],
+            "slk_corr_sample": [P, P, P, P],
+            "slk_corr_level": [P, I, ctypes.POINTER(P), ctypes.POINTER(I), ctypes.POINTER(I)],
+            "slk_avg_pool_2x2": [P, P, L, I, I, P],
+            "slk_corr_sample_level": [P, P, P, I, I, I, I, I, I, I, F, I, P],
+            "slk_coords_hw2_to_2hw": [P, P, I, I, P],
+            "slk_projmap": [P, P, P, P, P, P, P, I, I, I, P],
+            "slk_pose_retr": [P, P, I, I, P],
+            "slk_disp_retr": [P, P, P, I, I, P],
+            "slk_frame_distance": [P, P, P, P, P, P, I, I, I, F, P],
+            "slk_clamp_disps": [P, I, F, P],
+            "slk_ba_iterate": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, F, F, I, P],
+            "slk_ba_status": [P, P],
+            "slk_ba_last_system": [P, P, P, P, ctypes.POINTER(I), P],
+            "slk_ba_projective_transform": [P] * 13 + [I, I, I, P],
+            "slk_ba_accum": [P, P, P, P, I, I, I, P],
+            "slk_ba_damping_q": [P, P, P, P, I, I, F, P],
+            "slk_ba_eet6x6": [P, P, P, P, I, I, P],
+            "slk_ba_ev6x1": [P, P, P, P, P, I, I, P],
+            "slk_ba_evt6x1": [P, P, P, P, I, I, I, P],
+            "slk_ba_depth_update": [P, P, P, P, P, I, I, P],
+        }
+        for name, args in sig.items():
+            fn = getattr(L_, name)
+            fn.argtypes = args
+            fn.restype = I
+        L_.slk_last_error.argtypes = []
+        L_.slk_last_error.restype = ctypes.c_char_p
+        _lib = L_
+    return _lib
+
+
+def check(code):
+    if code != SLK_OK:
+        raise SlkError(code, lib().slk_last_error().decode())
+    return code
+
+
+# ------------------------------------------------------------ HIP runtime --
+class Hip:
+    """The few libamdhip64 calls used by tests and bench."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        self.h = ctypes.CDLL(HIP_LIB)
+        h = self.h
+        h.hipMalloc.argtypes = [ctypes.POINTER(P), ctypes.c_size_t]
+        h.hipFree.argtypes = [P]
+        h.hipMemcpy.argtypes = [P, P, ctypes.c_size_t, I]
+        h.hipMemcpyAsync.argtypes = [P, P, ctypes.c_size_t, I, P]
+        h.hipMemset.argtypes = [P, I, ctypes.c_size_t]
+        h.hipDeviceSynchronize.argtypes = []
+        h.hipStreamCreate.argtypes = [ctypes.POINTER(P)]
+        h.hipStreamDestroy.argtypes = [P]
+        h.hipStreamSynchronize.argtypes = [P]
+        h.hipEventCreate.argtypes = [ctypes.POINTER(P)]
+        h.hipEventDestroy.argtypes = [P]
+        h.hipEventRecord.argtypes = [P, P]
+        h.hipEventSynchronize.argtypes = [P]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(F), P, P]
+        h.hipGetDeviceCount.argtypes = [ctypes.POINTER(I)]
+        h.hipGetErrorString.argtypes = [I]
+        h.hipGetErrorString.restype = ctypes.c_char_p
+        for fn in ("hipMalloc", "hipFree", "hipMemcpy", "hipMemcpyAsync", "hipMemset",
+                   "hipDeviceSynchronize", "hipStreamCreate", "hipStreamDestroy",
+                   "hipStreamSynchronize", "hipEventCreate", "hipEventDestroy", "hipEventRecord",
+                   "hipEventSynchronize", "hipEventElapsedTime", "hipGetDeviceCount"):
+            getattr(h, fn).restype = I
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.h.hipGetErrorString(rc).decode()} ({rc})")
+
+    def device_count(self):
+        n = I(0)
+        rc = self.h.hipGetDeviceCount(ctypes.byref(n))
+        return n.value if rc == 0 else 0
+
+    def malloc(self, nbytes):
+        p = P()
+        self.ok(self.h.hipMalloc(ctypes.byref(p), max(int(nbytes), 1)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        self.ok(self.h.hipFree(P(p)), "hipFree")
+
+    def htod(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self.ok(self.h.hipMemcpy(P(dst), arr.ctypes.data, arr.nbytes, self.H2D), "hipMemcpy H2D")
+
+    def dtoh(self, arr, src):
+        self.ok(self.h.hipMemcpy(arr.ctypes.data, P(src), arr.nbytes, self.D2H), "hipMemcpy D2H")
+        return arr
+
+    def memset(self, p, value, nbytes):
+        self.ok(self.h.hipMemset(P(p), value, nbytes), "hipMemset")
+
+    def sync(self):
+        self.ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def stream(self):
+        s = P()
+        self.ok(self.h.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def stream_sync(self, s):
+        self.ok(self.h.hipStreamSynchronize(P(s)), "hipStreamSynchronize")
+
+    def event(self):
+        e = P()
+        self.ok(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, ev, stream=None):
+        self.ok(self.h.hipEventRecord(P(ev), P(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, e0, e1):
+        self.ok(self.h.hipEventSynchronize(P(e1)), "hipEventSynchronize")
+        ms = F(0)
+        self.ok(self.h.hipEventElapsedTime(ctypes.byref(ms), P(e0), P(e1)), "hipEventElapsedTime")
+        return ms.value
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        _hip = Hip()
+    return _hip
+
+
+class DeviceArray:
+    """A device buffer with a numpy shape/dtype."""
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) else shape
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = hip().malloc(self.nbytes)
+
+    @classmethod
+    def from_host(cls, arr, dtype=None):
+        arr = np.ascontiguousarray(arr, dtype=dtype)
+        d = cls(arr.shape, arr.dtype)
+        hip().htod(d.ptr, arr)
+        return d
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert arr.nbytes == self.nbytes
+        hip().htod(self.ptr, arr)
+
+    def to_host(self):
+        return hip().dtoh(np.empty(self.shape, self.dtype), self.ptr)
+
+    def zero(self):
+        hip().memset(self.ptr, 0, self.nbytes)
+
+    def free(self):
+        if self.ptr:
+            hip().free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(x):
+    if x is None:
+        return None
+    if isinstance(x, DeviceArray):
+        return x.ptr
+    return x
+
+
+def _host_i32(a):
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data
+
+
+class Context:
+    """slk_ctx: correlation scratch + BA state for h x w feature maps."""
+
+    def __init__(self, h, w, C=128, max_batch=48, levels=4, radius=3, corr_scale=1.0 / 16.0):
+        self.h, self.w, self.C, self.levels = h, w, C, levels
+        self.ptr = P()
+        check(lib().slk_create(ctypes.byref(self.ptr), h, w, C, max_batch, levels, radius,
+                               float(corr_scale)))
+
+    def close(self):
+        if self.ptr:
+            lib().slk_destroy(self.ptr)
+            self.ptr = P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # main.cu:1555 batch_build_and_sample_correlation
+    def batch_build_and_sample_correlation(self, fmaps, ii, jj, coords, out, dtype=SLK_F32,
+                                           fmap_stride=None, stream=None):
+        ii_h, ii_p = _host_i32(ii)
+        jj_h, jj_p = _host_i32(jj)
+        stride = fmap_stride if fmap_stride is not None else self.C * self.h * self.w
+        check(lib().slk_corr_batch_build_and_sample(self.ptr, _p(fmaps), dtype, stride, ii_p,
+                                                    jj_p, len(ii_h), _p(coords), _p(out), stream))
+
+    def batch_build_and_sample_correlation_dev(self, fmaps, ii_dev, jj_dev, B, coords, out,
+                                               dtype=SLK_F32, fmap_stride=None, stream=None):
+        stride = fmap_stride if fmap_stride is not None else self.C * self.h * self.w
+        check(lib().slk_corr_batch_build_and_sample_dev(self.ptr, _p(fmaps), dtype, stride,
+                                                        _p(ii_dev), _p(jj_dev), B, _p(coords),
+                                                        _p(out), stream))
+
+    # main.cu:1500 build_correlation / :1529 sample_correlation
+    def build_correlation(self, f_i, f_j, dtype=SLK_F32, stream=None):
+        check(lib().slk_corr_build(self.ptr, _p(f_i), _p(f_j), dtype, stream))
+
+    def sample_correlation(self, coords, out, stream=None):
+        check(lib().slk_corr_sample(self.ptr, _p(coords), _p(out), stream))
+
+    def level(self, l):
+        ptr, h2, w2 = P(), I(), I()
+        check(lib().slk_corr_level(self.ptr, l, ctypes.byref(ptr), ctypes.byref(h2),
+                                   ctypes.byref(w2)))
+        return ptr.value, h2.value, w2.value
+
+    def level_to_host(self, l):
+        ptr, h2, w2 = self.level(l)
+        HW = self.h * self.w
+        return hip().dtoh(np.empty((HW, h2, w2), np.float32), ptr)
+
+    # ba.cuh:476 BundleAdjustment::iterate
+    def ba_iterate(self, poses, disps, intr, target, weight, eta, ii_dev, jj_dev, ii, jj, t0,
+                   t1, lm, ep, motion_only=False, stream=None):
+        ii_h, ii_p = _host_i32(ii)
+        jj_h, jj_p = _host_i32(jj)
+        check(lib().slk_ba_iterate(self.ptr, _p(poses), _p(disps), _p(intr), _p(target),
+                                   _p(weight), _p(eta), _p(ii_dev), _p(jj_dev), ii_p, jj_p,
+                                   len(ii_h), t0, t1, float(lm), float(ep), int(bool(motion_only)),
+                                   stream))
+
+    def ba_status(self, stream=None):
+        return lib().slk_ba_status(self.ptr, stream)
+
+    def ba_last_system(self, stream=None):
+        n = I()
+        check(lib().slk_ba_last_system(self.ptr, None, None, None, ctypes.byref(n), stream))
+        S = np.zeros((n.value, n.value))
+        b = np.zeros(n.value)
+        dx = np.zeros(n.value)
+        check(lib().slk_ba_last_system(self.ptr, S.ctypes.data, b.ctypes.data, dx.ctypes.data,
+                                       ctypes.byref(n), stream))
+        return S, b, dx

@@ -1,0 +1,66 @@
+"""CPU checks of the drop-in boundary: libslk.so loads, exports exactly the
+entry points include/slk.h declares, rejects bad arguments before touching
+the GPU, and the host-side plumbing (workload generator) is deterministic."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import slk
+import workloads as wl
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    src = open(os.path.join(ROOT, "include", "slk.h")).read()
+    return sorted(set(re.findall(r"\b(slk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_matches_binding_list():
+    assert declared() == sorted(slk.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(slk.LIB_PATH), "run __graft_entry__.build() first"
+    out = subprocess.run(["nm", "-D", "--defined-only", slk.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (slk_\w+)", out))
+    missing = [s for s in declared() if s not in exported]
+    assert not missing, missing
+    lib = slk.lib()  # loads with ctypes and binds every signature
+    for s in declared():
+        assert hasattr(lib, s)
+
+
+def test_argument_errors_need_no_gpu():
+    lib = slk.lib()
+    import ctypes
+    p = ctypes.c_void_p()
+    assert lib.slk_create(ctypes.byref(p), 48, 64, 128, 48, 4, 2, 0.0625) == slk.SLK_E_ARG
+    assert b"radius" in lib.slk_last_error()
+    assert lib.slk_create(ctypes.byref(p), 48, 64, 127, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    assert lib.slk_create(ctypes.byref(p), 4, 64, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    assert lib.slk_create(None, 48, 64, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    assert lib.slk_ba_iterate(None, *([None] * 10), 1, 0, 1, 1e-4, 0.1, 0, None) == slk.SLK_E_ARG
+    assert lib.slk_corr_sample_level(None, None, None, 1, 2, 4, 4, 4, 4, 16, 1.0, 0,
+                                     None) == slk.SLK_E_ARG
+    # empty work is a no-op, not an error
+    assert lib.slk_projmap(None, None, None, None, None, None, None, 0, 4, 4, None) == slk.SLK_OK
+
+
+def test_workloads_are_deterministic():
+    a = wl.frames(2, h=6, w=8, seed=1)
+    b = wl.frames(2, h=6, w=8, seed=1)
+    np.testing.assert_array_equal(a, b)
+    ii, jj = wl.cyclic_edges(12)
+    assert len(ii) == 48 and len(set(zip(ii, jj))) == 48
+    d = np.abs(ii - jj)
+    assert np.all((np.minimum(d, 12 - d) >= 1) & (np.minimum(d, 12 - d) <= 2))
+    ii, jj = wl.backend_edges(200, 2000)
+    assert len(ii) == 2000 and len(set(zip(ii, jj))) == 2000
+    p = wl.ba_problem()
+    assert p["target"].shape == (48, 2, 48 * 64) and p["t0"] == 2 and p["t1"] == 12
+    np.testing.assert_array_equal(p["poses"][:2], [[0, 0, 0, 0, 0, 0, 1]] * 2)

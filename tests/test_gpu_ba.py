@@ -1,0 +1,249 @@
+"""GPU parity of bundle adjustment (cuda_slam/ba.cuh) through the C ABI against
+the CPU oracle on identical seeded inputs.
+
+The GPU evaluates the linearization and all reductions in fp64 from the fp32
+inputs, so S and b agree with the fp64 oracle to summation-order rounding
+(asserted at 1e-7 normwise) and dx to 1e-5 normwise
+(1e-4 relative) is asserted on the updated poses and disparities after 1 and
+3 chained iterations. Stage kernels with the reference's fp32 storage are
+held to 1e-5 relative (their outputs are fp32-rounded fp64 values).
+"""
+import numpy as np
+import pytest
+
+from helpers import TOL, Pins, announce, assert_close_rel, gpu_or_fail, norm_rel
+from oracle import oracle as orc
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def slk():
+    orc.build()
+    return gpu_or_fail()
+
+
+class Dev:
+    """Device copies of a BA problem."""
+
+    def __init__(self, slk, p):
+        self.slk = slk
+        self.p = p
+        self.d = {k: slk.DeviceArray.from_host(p[k])
+                  for k in ("poses", "disps", "intr", "target", "weight", "eta", "ii", "jj")}
+        self.keep = []  # index copies stay alive while queued work may read them
+
+    def iterate(self, ctx, lm, ep, motion_only=False, ii=None, jj=None):
+        d = self.d
+        ii = self.p["ii"] if ii is None else ii
+        jj = self.p["jj"] if jj is None else jj
+        iid = d["ii"] if ii is self.p["ii"] else self.slk.DeviceArray.from_host(ii)
+        jjd = d["jj"] if jj is self.p["jj"] else self.slk.DeviceArray.from_host(jj)
+        self.keep += [iid, jjd]
+        ctx.ba_iterate(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                       iid, jjd, ii, jj, self.p["t0"], self.p["t1"], lm, ep, motion_only)
+
+    def poses(self):
+        return self.d["poses"].to_host()
+
+    def disps(self):
+        return self.d["disps"].to_host()
+
+
+def oracle_iter(p, poses, disps, lm, ep, motion_only=False):
+    return orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"], p["ii"],
+                          p["jj"], p["h"], p["w"], p["t0"], p["t1"], lm, ep, motion_only)
+
+
+@pytest.mark.parametrize("motion_only", [False, True])
+def test_one_iteration_system_and_update(slk, motion_only):
+    announce(f"ba_window one iteration motion_only={motion_only}")
+    p = wl.ba_problem()
+    dev = Dev(slk, p)
+    ctx = slk.Context(p["h"], p["w"], max_batch=1)
+    dev.iterate(ctx, 1e-4, 0.1, motion_only)
+    assert ctx.ba_status() == slk.SLK_OK
+    S, b, dx = ctx.ba_last_system()
+    ref = oracle_iter(p, p["poses"], p["disps"], 1e-4, 0.1, motion_only)
+    assert ref["status"] == 0
+    assert norm_rel(S, ref["S"]) < 1e-7, norm_rel(S, ref["S"])
+    assert norm_rel(b, ref["b"]) < 1e-7, norm_rel(b, ref["b"])
+    assert norm_rel(dx, ref["dx"]) < 1e-5, norm_rel(dx, ref["dx"])
+    assert_close_rel(dev.poses(), ref["poses"], what="poses")
+    assert_close_rel(dev.disps(), ref["disps"], what="disps")
+    if motion_only:
+        np.testing.assert_array_equal(dev.disps(), p["disps"])
+    ctx.close()
+
+
+def test_three_iterations_chained(slk):
+    announce("ba_window three chained iterations")
+    p = wl.ba_problem()
+    dev = Dev(slk, p)
+    ctx = slk.Context(p["h"], p["w"], max_batch=1)
+    poses, disps = p["poses"], p["disps"]
+    for _ in range(3):
+        dev.iterate(ctx, 1e-4, 0.1)
+        ref = oracle_iter(p, poses, disps, 1e-4, 0.1)
+        poses, disps = ref["poses"], ref["disps"]
+    assert ctx.ba_status() == slk.SLK_OK
+    assert norm_rel(dev.poses(), poses) < TOL
+    assert norm_rel(dev.disps(), disps) < TOL
+    assert_close_rel(dev.poses(), poses, what="poses after 3")
+    assert_close_rel(dev.disps(), disps, what="disps after 3")
+    # the pose updates themselves (not only the updated values)
+    assert norm_rel(dev.poses() - p["poses"], poses - p["poses"]) < TOL
+    ctx.close()
+
+
+def test_edge_cases_stereo_duplicates_absent_frame(slk):
+    ii = np.array([0, 1, 2, 1, 2, 0, 1, 2], np.int32)
+    jj = np.array([1, 2, 3, 0, 1, 2, 1, 3], np.int32)
+    p = wl.ba_problem(n=4, h=6, w=8, ii=ii, jj=jj, seed=8, fixed=1)
+    p["eta"] = np.random.default_rng(9).uniform(0, 1e-3, p["eta"].shape).astype(np.float32)
+    dev = Dev(slk, p)
+    ctx = slk.Context(6, 8, C=128, max_batch=1, levels=2)
+    dev.iterate(ctx, 1e-4, 0.1)
+    S, b, dx = ctx.ba_last_system()
+    ref = oracle_iter(p, p["poses"], p["disps"], 1e-4, 0.1)
+    assert norm_rel(S, ref["S"]) < 1e-7
+    assert norm_rel(dx, ref["dx"]) < 1e-5
+    assert_close_rel(dev.poses(), ref["poses"])
+    assert_close_rel(dev.disps(), ref["disps"])
+    np.testing.assert_array_equal(dev.disps()[3], p["disps"][3])  # frame 3 not in ii
+    ctx.close()
+
+
+def test_not_spd_leaves_state_untouched(slk):
+    p = wl.ba_problem(n=4, h=6, w=8, seed=2)
+    p["weight"] = np.zeros_like(p["weight"])
+    dev = Dev(slk, p)
+    ctx = slk.Context(6, 8, C=128, max_batch=1, levels=2)
+    dev.iterate(ctx, 0.0, 0.0)
+    assert ctx.ba_status() == slk.SLK_E_NOT_SPD
+    assert ctx.ba_status() == slk.SLK_OK  # flag cleared
+    np.testing.assert_array_equal(dev.poses(), p["poses"])
+    np.testing.assert_array_equal(dev.disps(), p["disps"])
+    with pytest.raises(slk.SlkError):
+        ctx.ba_iterate(*([dev.d["poses"]] * 6), dev.d["ii"], dev.d["jj"], p["ii"], p["jj"], 3, 3,
+                       1e-4, 0.1)
+    ctx.close()
+
+
+def test_large_system_and_plan_cache(slk):
+    """30 frames, P = 28 free poses (n = 168, the global-memory solve), then a
+    different edge set and back (index structures rebuilt and reused)."""
+    announce("ba large n=168 + plan cache")
+    n = 30
+    ii, jj = wl.cyclic_edges(n)
+    p = wl.ba_problem(n=n, h=24, w=32, ii=ii, jj=jj, seed=12)
+    dev = Dev(slk, p)
+    ctx = slk.Context(24, 32, max_batch=1)
+    poses, disps = p["poses"], p["disps"]
+    for step, sel in enumerate([slice(None), slice(0, 80), slice(None)]):
+        q = dict(p, ii=ii[sel], jj=jj[sel], target=p["target"][sel], weight=p["weight"][sel],
+                 poses=poses, disps=disps)
+        dev.d["target"].upload(np.ascontiguousarray(np.concatenate(
+            [q["target"], np.zeros((len(ii) - len(q["ii"]),) + p["target"].shape[1:], np.float32)])))
+        dev.d["weight"].upload(np.ascontiguousarray(np.concatenate(
+            [q["weight"], np.zeros((len(ii) - len(q["ii"]),) + p["weight"].shape[1:], np.float32)])))
+        dev.iterate(ctx, 1e-4, 0.1, ii=np.ascontiguousarray(q["ii"]), jj=np.ascontiguousarray(q["jj"]))
+        ref = orc.ba_iterate(poses, disps, p["intr"], q["target"], q["weight"], p["eta"], q["ii"],
+                             q["jj"], 24, 32, p["t0"], p["t1"], 1e-4, 0.1)
+        S, b, dx = ctx.ba_last_system()
+        assert S.shape == (168, 168)
+        assert norm_rel(S, ref["S"]) < 1e-7, step
+        assert norm_rel(dx, ref["dx"]) < 1e-5, step
+        poses, disps = ref["poses"], ref["disps"]
+        assert_close_rel(dev.poses(), poses, what=f"poses step {step}")
+        assert_close_rel(dev.disps(), disps, what=f"disps step {step}")
+    ctx.close()
+
+
+# ------------------------------------------------------------ stage kernels --
+def test_projective_transform_stage(slk):
+    p = wl.ba_problem(n=6, h=24, w=32, seed=4)
+    M = len(p["ii"])
+    HW = 24 * 32
+    d = {k: slk.DeviceArray.from_host(p[k])
+         for k in ("target", "weight", "poses", "disps", "intr", "ii", "jj")}
+    outs = {"Hs": (4, M, 36), "vs": (2, M, 6), "Eii": (M, 6, HW), "Eij": (M, 6, HW),
+            "Cii": (M, HW), "bz": (M, HW)}
+    o = {k: slk.DeviceArray(s) for k, s in outs.items()}
+    slk.check(slk.lib().slk_ba_projective_transform(
+        d["target"].ptr, d["weight"].ptr, d["poses"].ptr, d["disps"].ptr, d["intr"].ptr,
+        d["ii"].ptr, d["jj"].ptr, o["Hs"].ptr, o["vs"].ptr, o["Eii"].ptr, o["Eij"].ptr,
+        o["Cii"].ptr, o["bz"].ptr, M, 24, 32, None))
+    slk.hip().sync()
+    ref = orc.ba_linearize(p["target"], p["weight"], p["poses"], p["disps"], p["intr"], p["ii"],
+                           p["jj"], 24, 32)
+    for name, r in zip(("Hs", "vs", "Eii", "Eij", "Cii", "bz"), ref):
+        assert_close_rel(o[name].to_host().reshape(r.shape), r, tol=1e-5, what=name)
+
+
+def test_schur_stage_kernels(slk):
+    pin = Pins(slk)
+    rng = np.random.default_rng(7)
+    D, NE, NK = 300, 5, 3
+    E = rng.normal(size=(NE, 6, D)).astype(np.float32)
+    C = rng.uniform(0.5, 2.0, (NK, D)).astype(np.float32)
+    eta = rng.uniform(0, 1, (7, D)).astype(np.float32)
+    kf_map = np.array([6, 2, 4], np.int32)
+    w = rng.normal(size=(NK, D)).astype(np.float32)
+    dE = slk.DeviceArray.from_host(E)
+    dC = slk.DeviceArray.from_host(C)
+    dQ = slk.DeviceArray((NK, D))
+    lib = slk.lib()
+    slk.check(lib.slk_ba_damping_q(dC.ptr, pin(eta),
+                                   pin(kf_map), dQ.ptr, NK, D, 1e-7, None))
+    slk.hip().sync()
+    Cref = C.astype(np.float64) + 0.2 * eta[kf_map] + 1e-7
+    assert_close_rel(dC.to_host(), Cref, tol=1e-6)
+    Q = dQ.to_host()
+    assert_close_rel(Q, 1.0 / Cref, tol=1e-6)
+    idx = np.array([[0, 1, 0], [2, 2, 1], [4, 3, 2]], np.int32)
+    S = slk.DeviceArray((3, 36))
+    slk.check(lib.slk_ba_eet6x6(dE.ptr, dQ.ptr, pin(idx), S.ptr, D, 3,
+                                None))
+    v = slk.DeviceArray.from_host(np.ones((NE, 6), np.float32))
+    ev_idx = np.array([0, 0, 1, 2, 2], np.int32)
+    dw = slk.DeviceArray.from_host(w)
+    slk.check(lib.slk_ba_ev6x1(dE.ptr, dQ.ptr, dw.ptr, pin(ev_idx), v.ptr,
+                               D, NE, None))
+    x = rng.normal(size=(4, 6)).astype(np.float32)
+    evt_idx = np.array([0, 3, 1, -1, 2], np.int32)
+    wout = slk.DeviceArray((NE, D))
+    wout.zero()
+    slk.check(lib.slk_ba_evt6x1(dE.ptr, pin(x),
+                                pin(evt_idx), wout.ptr, D, NE, 4, None))
+    slk.hip().sync()
+    E64, Q64 = E.astype(np.float64), Q.astype(np.float64)
+    for k, (a, b_, c) in enumerate(idx):
+        assert_close_rel(S.to_host()[k].reshape(6, 6), (E64[a] * Q64[c]) @ E64[b_].T, tol=1e-5)
+    vref = 1.0 + np.stack([(E64[r] * Q64[ev_idx[r]] * w[ev_idx[r]]).sum(-1) for r in range(NE)])
+    assert_close_rel(v.to_host(), vref, tol=1e-5)
+    wref = np.stack([x[evt_idx[r]].astype(np.float64) @ E64[r] if evt_idx[r] >= 0 else np.zeros(D)
+                     for r in range(NE)])
+    assert_close_rel(wout.to_host(), wref, tol=1e-5)
+    # accum / accum_add (CSR gather-sum) and depth_update
+    ptrs = np.array([0, 2, 2, 5], np.int32)
+    idxs = np.array([4, 0, 1, 3, 2], np.int32)
+    src = rng.normal(size=(5, D)).astype(np.float32)
+    out = slk.DeviceArray.from_host(np.full((3, D), 2.0, np.float32))
+    for add in (0, 1):
+        slk.check(lib.slk_ba_accum(pin(src),
+                                   pin(ptrs),
+                                   pin(idxs), out.ptr, 3, D, add, None))
+    slk.hip().sync()
+    acc = np.stack([src[idxs[ptrs[r]:ptrs[r + 1]]].astype(np.float64).sum(0) for r in range(3)])
+    assert_close_rel(out.to_host(), 2 * acc, tol=1e-6)
+    disps = rng.uniform(0.5, 1, (7, D)).astype(np.float32)
+    dd = slk.DeviceArray.from_host(disps)
+    dwv = rng.normal(size=(NK, D)).astype(np.float32)
+    slk.check(lib.slk_ba_depth_update(dQ.ptr, dw.ptr, pin(dwv), dd.ptr,
+                                      pin(kf_map), NK, D, None))
+    slk.hip().sync()
+    want = disps.astype(np.float64).copy()
+    want[kf_map] += Q64 * (w.astype(np.float64) - dwv)
+    assert_close_rel(dd.to_host(), want, tol=1e-6)

@@ -1,0 +1,222 @@
+"""GPU parity of the correlation path (volume, pyramid, lookup) through the C ABI
+against the CPU oracle on the same seeded inputs.
+
+Bars: indexing, shapes and the pyramid of a given level 0 are bitwise; with
+integer-coded features (exact fp32 products and sums, alpha = 1/16) the whole
+chain is bitwise; fp32 N(0,1) values are within helpers.TOL = 1e-4 of the
+oracle's fp64-accumulated result, relative to max(|r|, rms(r)).
+"""
+import numpy as np
+import pytest
+
+from helpers import TOL, announce, assert_close_rel, gpu_or_fail, norm_rel
+from oracle import oracle as orc
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def slk():
+    orc.build()
+    return gpu_or_fail()
+
+
+def run_single(slk, f, coords, alpha, levels=4, dtype=None):
+    C, h, w = f.shape[1:]
+    dt = slk.SLK_F16 if f.dtype == np.float16 else slk.SLK_F32
+    ctx = slk.Context(h, w, C=C, max_batch=1, levels=levels, corr_scale=alpha)
+    fi = slk.DeviceArray.from_host(f[0])
+    fj = slk.DeviceArray.from_host(f[1])
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((levels * 49, h * w))
+    ctx.build_correlation(fi, fj, dtype=dt)
+    ctx.sample_correlation(cd, out)
+    slk.hip().sync()
+    pyr = [ctx.level_to_host(l) for l in range(levels)]
+    res = out.to_host()
+    ctx.close()
+    return pyr, res
+
+
+@pytest.mark.parametrize("h,w,levels", [(48, 64, 4), (54, 96, 4), (12, 20, 3), (7, 9, 1)])
+def test_single_edge_volume_pyramid_lookup(slk, h, w, levels):
+    announce(f"single edge h={h} w={w} levels={levels}")
+    f = wl.frames(2, C=128, h=h, w=w, seed=100 + h)
+    coords = wl.flow_coords(1, h, w, seed=7)[0]
+    alpha = 1.0 / np.sqrt(128.0)
+    pyr, out = run_single(slk, f, coords, alpha, levels)
+    vol = orc.corr_volume(f[0].reshape(128, -1), f[1].reshape(128, -1), alpha)
+    # level shapes: floor halving
+    for l, lev in enumerate(pyr):
+        assert lev.shape == (h * w, h >> l, w >> l)
+    assert_close_rel(pyr[0].reshape(h * w, -1), vol, what="level 0")
+    # pyramid of the GPU's own level 0: bitwise
+    for l in range(1, levels):
+        np.testing.assert_array_equal(pyr[l], orc.avg_pool_2x2(pyr[l - 1]), err_msg=f"level {l}")
+    # lookup of the GPU's own pyramid: fp32 vs fp64 weights only
+    assert_close_rel(out, orc.lookup(pyr, coords), tol=1e-5, what="lookup(own pyramid)")
+    # whole chain vs the oracle
+    ref = orc.lookup(orc.pyramid(vol, h, w, levels), coords)
+    assert_close_rel(out, ref, what="chain")
+
+
+def test_integer_coded_chain_is_bitwise(slk):
+    """Small-integer features: every product and partial sum is exact in fp32,
+    so volume, pyramid and integer-coordinate lookups must match bitwise."""
+    h, w = 48, 64
+    rng = np.random.default_rng(3)
+    f = rng.integers(-3, 4, size=(2, 128, h, w)).astype(np.float32)
+    coords = (wl.grid_coords(h, w) + rng.integers(-6, 7, size=(2, h * w))).astype(np.float32)
+    coords *= 1.0  # integer at level 0
+    pyr, out = run_single(slk, f, coords, 1.0 / 16.0)
+    vol = orc.corr_volume(f[0].reshape(128, -1), f[1].reshape(128, -1), 1.0 / 16.0)
+    np.testing.assert_array_equal(pyr[0].reshape(h * w, -1), vol)
+    ref_pyr = orc.pyramid(vol, h, w)
+    for l in range(4):
+        np.testing.assert_array_equal(pyr[l], ref_pyr[l])
+    # level 0 channels with integer coords: pure window copy -> bitwise
+    np.testing.assert_array_equal(out[:49], orc.lookup(ref_pyr, coords)[:49])
+    # multiples of 8: integer at every level -> bitwise everywhere
+    c8 = (wl.grid_coords(h, w) // 8 * 8 + 8 * rng.integers(-1, 2, size=(2, h * w))).astype(np.float32)
+    _, out8 = run_single(slk, f, c8, 1.0 / 16.0)
+    np.testing.assert_array_equal(out8, orc.lookup(ref_pyr, c8))
+
+
+def test_fp16_features(slk):
+    h, w = 48, 64
+    f = wl.frames(2, C=128, h=h, w=w, seed=8).astype(np.float16)
+    coords = wl.flow_coords(1, h, w, seed=9)[0]
+    pyr, out = run_single(slk, f, coords, 1.0 / 16.0)
+    vol = orc.corr_volume(f[0].reshape(128, -1), f[1].reshape(128, -1), 1.0 / 16.0)
+    assert_close_rel(pyr[0].reshape(h * w, -1), vol, what="f16 level 0")
+    assert_close_rel(out, orc.lookup(orc.pyramid(vol, h, w), coords), what="f16 chain")
+
+
+def test_nonfinite_and_far_coords_give_zeros(slk):
+    h, w = 12, 16
+    f = wl.frames(2, C=128, h=h, w=w, seed=10)
+    coords = wl.grid_coords(h, w)
+    coords[0, 0] = np.nan
+    coords[1, 1] = np.inf
+    coords[0, 2] = -np.inf
+    coords[0, 3] = 3e9
+    coords[1, 4] = -3e9
+    coords[0, 5] = 40.0
+    pyr, out = run_single(slk, f, coords, 1.0 / 16.0)
+    assert np.all(out[:, :6] == 0.0)
+    assert np.all(np.isfinite(out))
+    assert_close_rel(out, orc.lookup(pyr, coords), tol=1e-5)
+
+
+def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, dtype=np.float32):
+    f = wl.frames(nframes, C=128, h=h, w=w, seed=seed)
+    ii, jj = wl.cyclic_edges(nframes)
+    ii, jj = ii[:B], jj[:B]
+    coords = wl.flow_coords(B, h, w, seed=seed + 1)
+    alpha = 1.0 / 16.0
+    ctx = slk.Context(h, w, C=128, max_batch=max_batch, corr_scale=alpha)
+    fd = slk.DeviceArray.from_host(f)
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((B, 196, h * w))
+    if dev_idx:
+        iid = slk.DeviceArray.from_host(ii)
+        jjd = slk.DeviceArray.from_host(jj)
+        ctx.batch_build_and_sample_correlation_dev(fd, iid, jjd, B, cd, out)
+    else:
+        ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, out)
+    slk.hip().sync()
+    res = out.to_host()
+    ctx.close()
+    return f, ii, jj, coords, res
+
+
+def test_window_48_edges_matches_oracle(slk):
+    """Config corr_window: 12 frames, 48 edges; every edge checked on sampled
+    pixels plus 6 edges in full."""
+    announce("corr window 48 edges")
+    h, w = 48, 64
+    f, ii, jj, coords, out = _window(slk, 12, h, w, 48, seed=20)
+    assert np.all(np.isfinite(out))
+    full = [0, 7, 18, 29, 40, 47]
+    ref = orc.corr_batch(f, ii[full], jj[full], coords[full], 1.0 / 16.0)
+    for k, e in enumerate(full):
+        assert_close_rel(out[e], ref[k], what=f"edge {e}")
+    # all 48 edges on 64 random pixels: direct fp64 evaluation of the windows
+    rng = np.random.default_rng(0)
+    pix = rng.choice(h * w, 64, replace=False)
+    for e in range(48):
+        fi = f[ii[e]].reshape(128, -1).astype(np.float64)
+        fj = f[jj[e]].reshape(128, -1).astype(np.float64)
+        vol = (fi[:, pix].T @ fj) / 16.0
+        pyr = [vol.reshape(64, h, w).astype(np.float32)]
+        for _ in range(3):
+            pyr.append(orc.avg_pool_2x2(pyr[-1]))
+        ref_sub = _lookup_rows(pyr, coords[e][:, pix])
+        assert_close_rel(out[e][:, pix], ref_sub, what=f"edge {e} sampled")
+
+
+def _lookup_rows(pyr, coords):
+    """Lookup of selected source rows: pyr[l] is [n, h>>l, w>>l] for n chosen
+    pixels whose coords are [2, n]; uses the oracle's level routine."""
+    n = pyr[0].shape[0]
+    out = np.zeros((len(pyr) * 49, n), np.float32)
+    for l, lev in enumerate(pyr):
+        H2, W2 = lev.shape[1:]
+        orc.lib().orc_corr_lookup_level(np.ascontiguousarray(lev).reshape(-1),
+                                        np.ascontiguousarray(coords, np.float32).reshape(-1), out,
+                                        3, 1, n, H2, W2, float(np.float32(1.0 / (1 << l))), l)
+    return out
+
+
+def test_device_indices_and_chunking(slk):
+    """Device-resident ii/jj, and B above max_batch (processed in chunks)."""
+    h, w = 24, 32
+    f, ii, jj, coords, out_a = _window(slk, 6, h, w, 10, seed=30, max_batch=4)
+    _, _, _, _, out_b = _window(slk, 6, h, w, 10, seed=30, max_batch=48, dev_idx=True)
+    np.testing.assert_array_equal(out_a, out_b)
+    ref = orc.corr_batch(f, ii, jj, coords, 1.0 / 16.0)
+    assert_close_rel(out_a, ref)
+
+
+def test_highres_shape(slk):
+    """Config highres geometry: 54x96 (HW = 5184, not a multiple of the 128-pixel tile)."""
+    announce("highres 54x96, 3 edges")
+    h, w = 54, 96
+    f, ii, jj, coords, out = _window(slk, 16, h, w, 3, seed=40)
+    ref = orc.corr_batch(f, ii, jj, coords, 1.0 / 16.0)
+    assert_close_rel(out, ref)
+
+
+def test_standalone_pool_sample_and_layout_kernels(slk):
+    rng = np.random.default_rng(5)
+    h, w, M = 12, 16, 3
+    HW = h * w
+    vol = rng.standard_normal((M * HW, h, w)).astype(np.float32)
+    vd = slk.DeviceArray.from_host(vol)
+    pd = slk.DeviceArray((M * HW, h // 2, w // 2))
+    slk.check(slk.lib().slk_avg_pool_2x2(vd.ptr, pd.ptr, M * HW, h, w, None))
+    slk.hip().sync()
+    np.testing.assert_array_equal(pd.to_host(), orc.avg_pool_2x2(vol))
+    coords = wl.flow_coords(M, h, w, seed=6)
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((M, 196, HW))
+    out.zero()
+    lvl1 = pd.to_host()
+    slk.check(slk.lib().slk_corr_sample_level(pd.ptr, cd.ptr, out.ptr, M, 3, h, w, h // 2, w // 2,
+                                              HW, 0.5, 1, None))
+    slk.hip().sync()
+    got = out.to_host()
+    for e in range(M):
+        ref = np.zeros((196, HW), np.float32)
+        orc.lib().orc_corr_lookup_level(np.ascontiguousarray(lvl1[e * HW:(e + 1) * HW]).reshape(-1),
+                                        np.ascontiguousarray(coords[e]).reshape(-1), ref, 3, h, w,
+                                        h // 2, w // 2, 0.5, 1)
+        assert_close_rel(got[e], ref, tol=1e-5)
+        assert not got[e][:49].any() and not got[e][98:].any()
+    hw2 = rng.standard_normal((M, HW, 2)).astype(np.float32)
+    hd = slk.DeviceArray.from_host(hw2)
+    chw = slk.DeviceArray((M, 2, HW))
+    slk.check(slk.lib().slk_coords_hw2_to_2hw(hd.ptr, chw.ptr, M, HW, None))
+    slk.hip().sync()
+    np.testing.assert_array_equal(chw.to_host(), hw2.transpose(0, 2, 1))
