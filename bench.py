@@ -1,0 +1,209 @@
+#!/usr/bin/env python3
+"""Benchmark of the DROID-SLAM per-edge update path on one MI355X.
+
+One step = the frontend-window workload the reference's run_update_pass
+(cuda_slam/main.cu:2171-2405) drives through this path:
+  * batched correlation volume + 4-level pyramid + radius-3 lookup for the
+    48 edges of a 12-frame window of 128x48x64 fp32 features
+    (batch_build_and_sample_correlation, main.cu:1555-1613), then
+  * 3 Gauss-Newton bundle-adjustment iterations on the same window
+    (BundleAdjustment::iterate, ba.cuh:476-803; Schur over depths, 10 free
+    poses).
+Inputs are synthetic (workloads.py), already resident in HBM when the timed
+region starts.
+
+Printed: one JSON line. `value` is edges/s of the full step (48 edges per
+step); corr-only edges/s and BA-only iterations/s are timed separately in the
+same run. `roofline` is for the dominant kernel (the correlation GEMM with its
+pyramid epilogue), its average launch duration measured with hipEvents on the
+launch stream. `cpu_baseline` times the CPU oracle (oracle/, a C port with
+OpenMP) on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "slam-hands_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "corr edges/sec + BA iters/sec (48-edge window, 1 MI355X); % roofline"
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (matrix and vector)
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-edges", type=int, default=48,
+                    help="edges of the window the CPU baseline runs (bounded sample)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path "
+              "would shard by edge across GPUs (see DESIGN.md) but no multi-GPU run is "
+              "implemented.", file=sys.stderr)
+        sys.exit(2)
+    import slk
+    import workloads as wl
+
+    H = slk.hip()
+    if H.device_count() < 1:
+        raise SystemExit("bench.py: no GPU visible")
+    slk.lib()  # fails loudly if libslk.so is missing
+
+    h, w, C, n, B = 48, 64, 128, 12, 48
+    HW = h * w
+    iters = 3
+    lm, ep = 1e-4, 0.1
+    fm = wl.frames(n, C, h, w, seed=0)
+    ii, jj = wl.cyclic_edges(n)
+    coords = wl.flow_coords(B, h, w, seed=1)
+    p = wl.ba_problem(n=n, h=h, w=w, ii=ii, jj=jj, seed=3)
+
+    ctx = slk.Context(h, w, C=C, max_batch=B, corr_scale=wl.CORR_ALPHA_REF)
+    D = slk.DeviceArray.from_host
+    d_f, d_c = D(fm), D(coords)
+    d_out = slk.DeviceArray((B, 196, HW))
+    dp = {k: D(p[k]) for k in ("poses", "disps", "intr", "target", "weight", "eta", "ii", "jj")}
+    stream = H.stream()
+
+    def corr():
+        ctx.batch_build_and_sample_correlation(d_f, ii, jj, d_c, d_out, stream=stream)
+
+    def ba():
+        ctx.ba_iterate(dp["poses"], dp["disps"], dp["intr"], dp["target"], dp["weight"],
+                       dp["eta"], dp["ii"], dp["jj"], ii, jj, p["t0"], p["t1"], lm, ep,
+                       stream=stream)
+
+    def step():
+        corr()
+        for _ in range(iters):
+            ba()
+
+    def timed(fn, k):
+        H.sync()
+        e0, e1 = H.event(), H.event()
+        H.record(e0, stream)
+        for _ in range(k):
+            fn()
+        H.record(e1, stream)
+        ms = H.elapsed_ms(e0, e1)
+        H.sync()
+        return ms
+
+    for _ in range(args.warmup):
+        step()
+    H.sync()
+    if ctx.ba_status(stream) != slk.SLK_OK:
+        raise SystemExit("bench.py: BA system not positive definite during warmup")
+    t0 = time.perf_counter()
+    total_ms = timed(step, args.steps)
+    wall = time.perf_counter() - t0
+    ms_step = total_ms / args.steps
+    value = B * args.steps / (total_ms / 1e3)
+
+    corr_ms = timed(corr, args.steps) / args.steps
+    ba_ms = timed(ba, args.steps * iters) / (args.steps * iters)
+
+    # per-kernel durations (events on the launch stream around each kernel)
+    ctx.profile_enable(True)
+    for _ in range(max(5, args.steps // 5)):
+        step()
+    H.sync()
+    prof = ctx.profile()
+    ctx.profile_enable(False)
+    kern = {k: {"avg_us": 1e3 * v[0] / v[1], "launches": v[1]} for k, v in prof.items()}
+
+    flop = 2.0 * HW * HW * C * B
+    gemm_s = kern["corr_pyramid"]["avg_us"] * 1e-6
+    achieved = flop / gemm_s / 1e12
+    pool_lvl = sum((h >> l) * (w >> l) for l in range(1, 4))
+    roof = {
+        "kernel": "corr_pyramid (fp32 MFMA GEMM + 2x2 pyramid epilogue, 48 edges)",
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_FP32_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+        "traffic": None,
+        "algorithmic_bytes_per_launch": int(B * (2 * C * HW * 4 + HW * (HW + pool_lvl) * 4)),
+    }
+    look_bytes = B * (2 * HW * 4 + HW * 4 * 64 * 4 + 196 * HW * 4)
+    look_s = kern["corr_lookup"]["avg_us"] * 1e-6
+    # reference roofline of one step: the GEMM at fp32 MFMA peak (BA is latency-bound)
+    step_roof_ms = flop / (PEAK_FP32_TFLOPS * 1e12) * 1e3
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (correlation, MFMA) / f64 (BA arithmetic, f32 storage)",
+        "data": "synthetic (seeded N(0,1) features, U(-8,8) flow, BA window of workloads.py)",
+        "config": {"workload": "corr_window + 3x ba_window", "frames": n, "edges": B, "h": h,
+                   "w": w, "C": C, "levels": 4, "radius": 3, "ba_iters_per_step": iters,
+                   "free_poses": p["t1"] - p["t0"], "lm": lm, "ep": ep,
+                   "corr_scale": wl.CORR_ALPHA_REF, "parallelism": "single GPU"},
+        "corr_edges_per_s": round(B / (corr_ms / 1e3), 1),
+        "ba_iters_per_s": round(1e3 / ba_ms, 1),
+        "corr_ms": round(corr_ms, 4),
+        "ba_iter_ms": round(ba_ms, 4),
+        "step_roofline_frac": round(step_roof_ms / ms_step, 4),
+        "roofline": roof,
+        "lookup_hbm": {"achieved_GBs": round(look_bytes / look_s / 1e9, 1), "peak": PEAK_HBM_GBS,
+                       "frac": round(look_bytes / look_s / 1e9 / PEAK_HBM_GBS, 4)},
+        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kern.items()},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, args.cpu_edges)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, nedges):
+    """The CPU oracle (oracle/liboracle.so, C + OpenMP, fp64 accumulation)
+    on a bounded sample: correlation+lookup of `nedges` of the 48 edges (all
+    of them by default) and the step's BA iterations on the full window,
+    scaled to the step's edges/s (~10 s of CPU work on 8 cores)."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    orc.lib()
+    B = len(ii)
+    t0 = time.perf_counter()
+    orc.corr_batch(fm, ii[:nedges], jj[:nedges], coords[:nedges], 1.0 / 16.0)
+    t_corr = (time.perf_counter() - t0) / nedges
+    t0 = time.perf_counter()
+    poses, disps = p["poses"], p["disps"]
+    for _ in range(iters):
+        r = orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"], p["ii"],
+                           p["jj"], p["h"], p["w"], p["t0"], p["t1"], lm, ep)
+        poses, disps = r["poses"], r["disps"]
+    t_ba = (time.perf_counter() - t0) / iters
+    step_s = B * t_corr + iters * t_ba
+    return {"value": round(B / step_s, 2), "unit": "edges/s", "cores": orc.num_threads(),
+            "kind": "port",
+            "sample": f"oracle corr+pyramid+lookup of {nedges}/{B} edges + {iters} BA iterations "
+                      f"(full 12-frame window), scaled to the {B}-edge + {iters}-iteration step",
+            "corr_s_per_edge": round(t_corr, 4), "ba_s_per_iter": round(t_ba, 4)}
+
+
+if __name__ == "__main__":
+    main()

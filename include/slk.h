@@ -61,6 +61,17 @@ int slk_destroy(slk_ctx* ctx);
 /* Text of the last failure on this thread ("" if none). */
 const char* slk_last_error(void);
 
+/* Per-kernel timing of the launches this context makes (hipEvents recorded on
+ * the launch stream around each kernel). Enabling (or disabling) clears the
+ * totals. Replaces the reference's CudaTimer totals (cuda_slam/main.cu:41-59,
+ * print_timing :2493-2507) and BundleAdjustment::print_profile (ba.cuh:805). */
+int slk_profile_enable(slk_ctx* ctx, int on);
+
+/* Totals of the idx-th distinct kernel name (synchronises on the recorded
+ * events); SLK_E_ARG once idx runs past the last name. */
+int slk_profile_kernel(slk_ctx* ctx, int idx, const char** name, double* total_ms,
+                       int* launches);
+
 /* ------------------------------------------------------------ correlation */
 
 /* CudaDroid::batch_build_and_sample_correlation(batch_size, edge_start,

@@ -21,6 +21,9 @@
 extern "C" {
 #endif
 
+/* OpenMP threads the oracle's parallel loops use. */
+int orc_num_threads(void);
+
 /* ---------------- correlation (cuda_slam/main.cu:1077-1217, 1500-1613) ---- */
 
 /* vol[p][q] = alpha * sum_c fi[c][p] * fj[c][q]; fi, fj are [C][HW]

@@ -68,6 +68,8 @@ def lib():
             fn.argtypes = argtypes
             fn.restype = None
         L.orc_cholesky_solve.restype = c_int
+        L.orc_num_threads.argtypes = []
+        L.orc_num_threads.restype = c_int
         # orc_ba_iterate takes optional (NULL-able) debug outputs
         L.orc_ba_iterate.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _i32p,
                                      c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float,
@@ -76,6 +78,10 @@ def lib():
         L.orc_ba_iterate.restype = c_int
         _lib = L
     return _lib
+
+
+def num_threads():
+    return lib().orc_num_threads()
 
 
 def _c(a, dt):

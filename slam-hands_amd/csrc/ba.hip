@@ -735,12 +735,16 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         s->valid = true;
     }
     const PlanDev plan = plan_ptrs(s);
-    hipLaunchKernelGGL(k_ba_lin_kf, dim3(s->nch, s->N_kf), dim3(kLinWG), 0, stream, plan, target,
+    {
+        ProfScope ps(ctx, "ba_lin_kf", stream);
+        hipLaunchKernelGGL(k_ba_lin_kf, dim3(s->nch, s->N_kf), dim3(kLinWG), 0, stream, plan, target,
                        weight, poses, disps, intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
                        s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW, ctx->w,
                        s->nch, motion_only);
+    }
     SLK_HIP(hipGetLastError());
     if (!motion_only && s->N_pu + s->N_E > 0) {
+        ProfScope ps(ctx, "ba_schur", stream);
         hipLaunchKernelGGL(k_ba_schur, dim3(s->nchS, s->N_pu + s->N_E), dim3(kSchWG), 0, stream,
                            plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
                            s->spart.as<double>(), HW, s->nchS, s->N_pu);
@@ -768,14 +772,17 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     A.flags = s->flags.as<int>();
     A.poses = poses;
     if (s->n <= kSmallN) {
+        ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);
         hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(1024), shm, stream, A);
     } else {
+        ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = (size_t)s->n * sizeof(double);
         hipLaunchKernelGGL(k_ba_solve_large, dim3(1), dim3(1024), shm, stream, A);
     }
     SLK_HIP(hipGetLastError());
     if (!motion_only && s->N_E > 0) {
+        ProfScope ps(ctx, "ba_backsub", stream);
         hipLaunchKernelGGL(k_ba_backsub, dim3((HW + 255) / 256, s->N_kf), dim3(256), 0, stream,
                            plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
                            s->dx.as<float>(), s->flags.as<int>(), disps, HW);

@@ -99,8 +99,66 @@ extern "C" int slk_create(slk_ctx** out, int h, int w, int C, int max_batch, int
     return SLK_OK;
 }
 
+namespace {
+void prof_clear(slk_ctx* ctx) {
+    for (auto& r : ctx->prof_recs) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    ctx->prof_recs.clear();
+    ctx->prof_names.clear();
+    ctx->prof_ms.clear();
+    ctx->prof_count.clear();
+    ctx->prof_dirty = false;
+}
+
+// Folds finished launch records into per-name totals (synchronises on them).
+int prof_fold(slk_ctx* ctx) {
+    using namespace slk;
+    for (auto& r : ctx->prof_recs) {
+        SLK_HIP(hipEventSynchronize(r.b));
+        float ms = 0.0f;
+        SLK_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+        size_t k = 0;
+        while (k < ctx->prof_names.size() && ctx->prof_names[k] != r.name) k++;
+        if (k == ctx->prof_names.size()) {
+            ctx->prof_names.emplace_back(r.name);
+            ctx->prof_ms.push_back(0.0);
+            ctx->prof_count.push_back(0);
+        }
+        ctx->prof_ms[k] += ms;
+        ctx->prof_count[k] += 1;
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    ctx->prof_recs.clear();
+    ctx->prof_dirty = false;
+    return SLK_OK;
+}
+}  // namespace
+
+extern "C" int slk_profile_enable(slk_ctx* ctx, int on) {
+    if (!ctx) return slk::fail(SLK_E_ARG, "profile_enable: null context");
+    prof_clear(ctx);
+    ctx->prof = on != 0;
+    return SLK_OK;
+}
+
+extern "C" int slk_profile_kernel(slk_ctx* ctx, int idx, const char** name, double* total_ms,
+                                  int* launches) {
+    if (!ctx) return slk::fail(SLK_E_ARG, "profile_kernel: null context");
+    if (ctx->prof_dirty) SLK_TRY(prof_fold(ctx));
+    if (idx < 0 || idx >= (int)ctx->prof_names.size())
+        return slk::fail(SLK_E_ARG, "profile_kernel: index out of range");
+    if (name) *name = ctx->prof_names[idx].c_str();
+    if (total_ms) *total_ms = ctx->prof_ms[idx];
+    if (launches) *launches = ctx->prof_count[idx];
+    return SLK_OK;
+}
+
 extern "C" int slk_destroy(slk_ctx* ctx) {
     if (!ctx) return SLK_OK;
+    prof_clear(ctx);
     slk::ba_destroy(ctx);
     for (int l = 0; l < slk::kMaxLevels; l++) {
         ctx->batch_lvl[l].release();

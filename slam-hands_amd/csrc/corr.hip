@@ -297,17 +297,21 @@ int launch_pyramid(slk_ctx* ctx, const Tin* fa, const Tin* fb, long fstride, con
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
     LevelOut lo;
     for (int l = 0; l < kMaxLevels; l++) lo.p[l] = l < ctx->levels ? lvl[l] : nullptr;
-    hipLaunchKernelGGL(k_corr_pyramid<Tin>, dim3((unsigned)total), dim3(kWG), 0, stream, fa, fb,
-                       fstride, ia, ib, eidx, lo, slot0, ctx->h, ctx->w, ctx->C, ctx->alpha,
-                       ctx->levels, mtiles, nbands, ncb);
+    {
+        ProfScope ps(ctx, "corr_pyramid", stream);
+        hipLaunchKernelGGL(k_corr_pyramid<Tin>, dim3((unsigned)total), dim3(kWG), 0, stream, fa,
+                           fb, fstride, ia, ib, eidx, lo, slot0, ctx->h, ctx->w, ctx->C,
+                           ctx->alpha, ctx->levels, mtiles, nbands, ncb);
+    }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
 
-int launch_lookup(const LevelIn& lv, int nlev, int level_base, int nch, const float* coords,
-                  float* out, int B, int HW1, hipStream_t stream) {
+int launch_lookup(slk_ctx* ctx, const LevelIn& lv, int nlev, int level_base, int nch,
+                  const float* coords, float* out, int B, int HW1, hipStream_t stream) {
     if (B <= 0) return SLK_OK;
     dim3 grid((HW1 + 255) / 256, nlev, B);
+    ProfScope ps(ctx, "corr_lookup", stream);
     hipLaunchKernelGGL(k_corr_lookup, grid, dim3(256), 0, stream, lv, coords, out, HW1, level_base,
                        nch);
     SLK_HIP(hipGetLastError());
@@ -360,7 +364,7 @@ int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, co
                                                  stream));
             }
         }
-        SLK_TRY(launch_lookup(lv, ctx->levels, 0, nch, coords + (size_t)b0 * 2 * HW,
+        SLK_TRY(launch_lookup(ctx, lv, ctx->levels, 0, nch, coords + (size_t)b0 * 2 * HW,
                               out + (size_t)b0 * nch * HW, nb, HW, stream));
     }
     return SLK_OK;
@@ -429,7 +433,8 @@ extern "C" int slk_corr_sample(slk_ctx* ctx, const float* coords, float* out, hi
     if (!ctx || !coords || !out) return fail(SLK_E_ARG, "corr_sample: null argument");
     if (!ctx->single_built) return fail(SLK_E_STATE, "corr_sample: no volume built");
     const LevelIn lv = level_in(ctx, ctx->single_lvl);
-    return launch_lookup(lv, ctx->levels, 0, ctx->levels * 49, coords, out, 1, ctx->HW, stream);
+    return launch_lookup(ctx, lv, ctx->levels, 0, ctx->levels * 49, coords, out, 1, ctx->HW,
+                         stream);
 }
 
 extern "C" int slk_corr_level(slk_ctx* ctx, int level, const float** ptr, int* h2, int* w2) {
@@ -495,7 +500,7 @@ extern "C" int slk_corr_sample_level(const float* volumes, const float* coords, 
     lv.h[0] = H2;
     lv.w[0] = W2;
     // channels [level_idx*49, +49) of a [M][196][hw] buffer, like the reference
-    return launch_lookup(lv, 1, level_idx, 196, coords, corr_out, M, hw, stream);
+    return launch_lookup(nullptr, lv, 1, level_idx, 196, coords, corr_out, M, hw, stream);
 }
 
 extern "C" int slk_coords_hw2_to_2hw(const float* hw2, float* chw, int M, int HW,

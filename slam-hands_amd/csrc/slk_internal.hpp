@@ -55,6 +55,14 @@ struct BaState;  // ba.hip
 
 constexpr int kMaxLevels = 4;
 
+// Per-kernel timing on the launch stream (hipEvents around each launch),
+// enabled by slk_profile_enable; the reference's counterparts are CudaTimer
+// (cuda_slam/main.cu:41-59) and BundleAdjustment::print_profile (ba.cuh:805).
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+
 }  // namespace slk
 
 struct slk_ctx {
@@ -69,7 +77,37 @@ struct slk_ctx {
     bool single_built = false;
     slk::DevBuf zero_idx;  // device int {0}
     slk::BaState* ba = nullptr;
+    bool prof = false;
+    std::vector<slk::ProfRec> prof_recs;
+    std::vector<std::string> prof_names;
+    std::vector<double> prof_ms;
+    std::vector<int> prof_count;
+    bool prof_dirty = false;
 };
+
+namespace slk {
+// RAII bracket of one kernel launch for the profiler (no-op when disabled).
+struct ProfScope {
+    slk_ctx* ctx;
+    const char* name;
+    hipStream_t stream;
+    hipEvent_t a = nullptr;
+    ProfScope(slk_ctx* c, const char* n, hipStream_t s) : ctx(c), name(n), stream(s) {
+        if (ctx && ctx->prof && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, stream);
+    }
+    ~ProfScope() {
+        if (!a) return;
+        hipEvent_t b = nullptr;
+        if (hipEventCreate(&b) == hipSuccess && hipEventRecord(b, stream) == hipSuccess) {
+            ctx->prof_recs.push_back({name, a, b});
+            ctx->prof_dirty = true;
+        } else {
+            (void)hipEventDestroy(a);
+            if (b) (void)hipEventDestroy(b);
+        }
+    }
+};
+}  // namespace slk
 
 namespace slk {
 // corr.hip

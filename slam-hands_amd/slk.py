@@ -25,7 +25,7 @@ SLK_F32, SLK_F16 = 0, 1
 
 # every entry point declared in include/slk.h
 EXPORTS = [
-    "slk_create", "slk_destroy", "slk_last_error",
+    "slk_create", "slk_destroy", "slk_last_error", "slk_profile_enable", "slk_profile_kernel",
     "slk_corr_batch_build_and_sample", "slk_corr_batch_build_and_sample_dev",
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
@@ -68,6 +68,9 @@ def lib():
         sig = {
             "slk_create": [ctypes.POINTER(P), I, I, I, I, I, I, F],
             "slk_destroy": [P],
+            "slk_profile_enable": [P, I],
+            "slk_profile_kernel": [P, I, ctypes.POINTER(ctypes.c_char_p),
+                                   ctypes.POINTER(ctypes.c_double), ctypes.POINTER(I)],
             "slk_corr_batch_build_and_sample": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_batch_build_and_sample_dev": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_build": [P, P, P, I, P],
@@ -316,6 +319,23 @@ class Context:
                                    _p(weight), _p(eta), _p(ii_dev), _p(jj_dev), ii_p, jj_p,
                                    len(ii_h), t0, t1, float(lm), float(ep), int(bool(motion_only)),
                                    stream))
+
+    def profile_enable(self, on=True):
+        check(lib().slk_profile_enable(self.ptr, int(bool(on))))
+
+    def profile(self):
+        """{kernel name: (total ms, launches)} since profile_enable."""
+        out = {}
+        k = 0
+        while True:
+            name, ms, n = ctypes.c_char_p(), ctypes.c_double(), I()
+            rc = lib().slk_profile_kernel(self.ptr, k, ctypes.byref(name), ctypes.byref(ms),
+                                          ctypes.byref(n))
+            if rc == SLK_E_ARG:
+                return out
+            check(rc)
+            out[name.value.decode()] = (ms.value, n.value)
+            k += 1
 
     def ba_status(self, stream=None):
         return lib().slk_ba_status(self.ptr, stream)
