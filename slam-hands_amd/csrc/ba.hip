@@ -6,7 +6,7 @@
 // accum, damping_Q, EEt6x6, Ev6x1, EvT6x1, depth_update, and the host
 // orchestration BundleAdjustment::iterate) with se3.cuh for the geometry.
 //
-// Iteration = 4 kernels on one stream:
+// Iteration = 5 kernels on one stream:
 //   k_ba_lin_kf   grid (pixel chunk, keyframe): every edge whose depth owner
 //                 (ii) is that keyframe is linearized for the chunk's pixels in
 //                 fp64. Per-edge 12x12 Hessian + gradients are reduced per
@@ -16,11 +16,12 @@
 //                 exist.
 //   k_ba_schur    grid (pixel chunk, item): E_r1 Q E_r2^T for the upper pairs
 //                 of E rows sharing a keyframe, and E_r Q w per row.
-//   k_ba_solve_*  one workgroup: assembles S, b from the partial sums through
-//                 a per-block contribution list built on the host (no
-//                 atomics, fixed order), applies S_ii += ep + lm*S_ii,
-//                 factorizes (LDL^T, fp64), solves, rounds dx to fp32 and
-//                 retracts the poses [t0, t1).
+//   k_ba_assemble one thread per entry of S and b: sums the chunk partials of
+//                 the contributions listed for its 6x6 block (list built on
+//                 the host; no atomics, fixed order), then S_ii += ep + lm*S_ii.
+//   k_ba_solve_*  one workgroup: blocked fp64 Cholesky (S in LDS up to
+//                 90x90, else global), solve, dx rounded to fp32, retraction
+//                 of the poses [t0, t1).
 //   k_ba_backsub  grid (pixel chunk, keyframe): dz = Q (w - E^T dx),
 //                 disps += dz.
 // Host work per iteration is limited to comparing the edge list with the
@@ -39,11 +40,12 @@ namespace slk {
 namespace {
 
 constexpr int kLinWG = 256;
-constexpr int kLinPx = 512;  // pixels per k_ba_lin_kf workgroup (2 per thread)
+constexpr int kLinPx = 256;  // pixels per k_ba_lin_kf workgroup (1 per thread)
+constexpr int kLinPPT = kLinPx / kLinWG;
 constexpr int kSchWG = 256;
 constexpr int kSchPx = 512;
 constexpr int kNH = 90;      // 78 upper-triangle Hessian entries + vi(6) + vj(6)
-constexpr int kSmallN = 90;  // LDS solve up to 90x90 fp64 (64800 bytes)
+constexpr int kSmallN = 90;  // workgroup LDS solve up to 90x90 fp64 (64800 bytes)
 constexpr double kMinDepth = 0.25;  // se3.cuh:6
 
 __host__ __device__ __forceinline__ int tri(int n, int m) { return n * (n + 1) / 2 + m; }
@@ -65,7 +67,9 @@ struct PlanDev {
     const int* sblk_src;  // contributions (see encode_*)
     const int* bv_ptr;    // [P+1]
     const int* bv_src;
+    const int* blkmap;    // [P*P] block id of (a, b) in sblk, or -1
 };
+constexpr int kPlanParts = 16;
 
 // contribution codes: type in bits 30..31
 __host__ __device__ __forceinline__ int code(int type, int v) { return (type << 30) | v; }
@@ -177,10 +181,10 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
     const int kc = blockIdx.y;
     const int kf = plan.kf_list[kc];
     const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
-    int kpx[2];
-    bool vpx[2];
+    int kpx[kLinPPT];
+    bool vpx[kLinPPT];
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
+    for (int s = 0; s < kLinPPT; s++) {
         kpx[s] = chunk * kLinPx + s * kLinWG + threadIdx.x;
         vpx[s] = kpx[s] < HW;
     }
@@ -189,15 +193,18 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
         for (int r = r0; r < r1; r++) {
             double* er = E + (size_t)plan.kf_rows[r] * 6 * HW;
 #pragma unroll
-            for (int s = 0; s < 2; s++)
+            for (int s = 0; s < kLinPPT; s++)
                 if (vpx[s])
                     for (int n = 0; n < 6; n++) er[(size_t)n * HW + kpx[s]] = 0.0;
         }
     }
-    double Cacc[2] = {0.0, 0.0}, Wacc[2] = {0.0, 0.0};
-    double dsp[2];
+    double Cacc[kLinPPT], Wacc[kLinPPT], dsp[kLinPPT];
 #pragma unroll
-    for (int s = 0; s < 2; s++) dsp[s] = vpx[s] ? (double)disps[(size_t)kf * HW + kpx[s]] : 1.0;
+    for (int s = 0; s < kLinPPT; s++) {
+        Cacc[s] = 0.0;
+        Wacc[s] = 0.0;
+        dsp[s] = vpx[s] ? (double)disps[(size_t)kf * HW + kpx[s]] : 1.0;
+    }
 
     const int e0 = plan.kf_eptr[kc], e1 = plan.kf_eptr[kc + 1];
     for (int ei = e0; ei < e1; ei++) {
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
 #pragma unroll
         for (int n = 0; n < kNH; n++) acc[n] = 0.0;
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
+        for (int s = 0; s < kLinPPT; s++) {
             if (!vpx[s]) continue;
             const int k = kpx[s];
             const size_t base = (size_t)e * 2 * HW + k;
@@ -244,18 +251,11 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
                 }
             }
         }
-        block_sum(acc, red);
-        if (threadIdx.x < kNH) {
-            double v = 0.0;
-#pragma unroll
-            for (int n = 0; n < kNH; n++)
-                if (n == (int)threadIdx.x) v = acc[n];
-            hpart[((size_t)e * nch + chunk) * kNH + threadIdx.x] = v;
-        }
+        block_sum_to(acc, red, hpart + ((size_t)e * nch + chunk) * kNH);
     }
     if (!motion_only) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
+        for (int s = 0; s < kLinPPT; s++) {
             if (!vpx[s]) continue;
             const int k = kpx[s];
             // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
@@ -308,25 +308,18 @@ __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double*
             for (int n = 0; n < 6; n++) acc[n] += qw * er[(size_t)n * HW + k];
         }
     }
-    block_sum(acc, red);
-    if (threadIdx.x < 36) {
-        double v = 0.0;
-#pragma unroll
-        for (int n = 0; n < 36; n++)
-            if (n == (int)threadIdx.x) v = acc[n];
-        spart[((size_t)item * nchS + chunk) * 36 + threadIdx.x] = v;
-    }
+    block_sum_to(acc, red, spart + ((size_t)item * nchS + chunk) * 36);
 }
 
 // ----------------------------------------------------------- solve ------
 struct SolveArgs {
     PlanDev plan;
-    const double* hpart;
-    const double* spart;
+    const double* hpart;  // [M][nch][90] per-edge Hessian/gradient chunk partials
+    const double* spart;  // [N_pu + N_E][nchS][36] Schur pair / row chunk partials
     int nch, nchS, N_pu, P, n, n_blk, t0, t1;
     float lm, ep;
-    double* S;      // working matrix (global variant) [n*n]
-    double* S_dbg;  // [n*n] system before factorization
+    double* S;      // working matrix of the global-memory variant [n*n]
+    double* S_dbg;  // [n*n] assembled system (after damping), input of the solve
     double* b_dbg;  // [n]
     double* dx_dbg; // [n]
     float* dx;      // [n] fp32 step used by retraction and back-substitution
@@ -334,114 +327,249 @@ struct SolveArgs {
     float* poses;
 };
 
-// value of entry (r, c) of Hessian block `which` of edge e, summed over chunks
-__device__ __forceinline__ double hs_entry(const SolveArgs& A, int e, int which, int r, int c) {
-    int idx;
-    if (which == 0) idx = tri(max(r, c), min(r, c));
-    else if (which == 1) idx = tri(6 + c, r);
-    else if (which == 2) idx = tri(6 + r, c);
-    else idx = tri(6 + max(r, c), 6 + min(r, c));
-    const double* h = A.hpart + (size_t)e * A.nch * kNH + idx;
-    double s = 0.0;
-    for (int ch = 0; ch < A.nch; ch++) s += h[(size_t)ch * kNH];
-    return s;
+// index into an edge's 90 totals of entry (r, c) of Hessian block `which`
+__device__ __forceinline__ int hs_index(int which, int r, int c) {
+    if (which == 0) return tri(max(r, c), min(r, c));
+    if (which == 1) return tri(6 + c, r);
+    if (which == 2) return tri(6 + r, c);
+    return tri(6 + max(r, c), 6 + min(r, c));
 }
 
-__device__ __forceinline__ double sp_entry(const SolveArgs& A, int item, int e36) {
-    const double* s = A.spart + (size_t)item * A.nchS * 36 + e36;
-    double v = 0.0;
-    for (int ch = 0; ch < A.nchS; ch++) v += s[(size_t)ch * 36];
-    return v;
-}
-
-// Fills S (row-major n x n, zero outside listed blocks) and b; LM damping.
-__device__ void assemble(const SolveArgs& A, double* S, double* b) {
-    const int n = A.n, P = A.P;
-    for (int t = threadIdx.x; t < n * n; t += blockDim.x) S[t] = 0.0;
-    __syncthreads();
-    for (int t = threadIdx.x; t < A.n_blk * 36; t += blockDim.x) {
-        const int blk = t / 36, ent = t - blk * 36;
-        const int r = ent / 6, c = ent - r * 6;
-        const int ab = A.plan.sblk[blk];
-        const int a = ab / P, bb = ab - a * P;
-        double s = 0.0;
-        for (int q = A.plan.sblk_ptr[blk]; q < A.plan.sblk_ptr[blk + 1]; q++) {
-            const int cd = A.plan.sblk_src[q];
-            const int ty = code_type(cd), v = code_val(cd);
-            if (ty == 0) s += hs_entry(A, v >> 2, v & 3, r, c);
-            else if (ty == 1) s -= sp_entry(A, v, r * 6 + c);
-            else s -= sp_entry(A, v, c * 6 + r);
-        }
-        S[(size_t)(a * 6 + r) * n + bb * 6 + c] = s;
+// Sum of the n chunk partials p[0], p[stride], ... with four loads in flight
+// (fixed order: deterministic).
+__device__ __forceinline__ double sum_parts(const double* p, int n, int stride) {
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    int c = 0;
+    for (; c + 4 <= n; c += 4) {
+        s0 += p[(size_t)c * stride];
+        s1 += p[(size_t)(c + 1) * stride];
+        s2 += p[(size_t)(c + 2) * stride];
+        s3 += p[(size_t)(c + 3) * stride];
     }
-    for (int t = threadIdx.x; t < n; t += blockDim.x) {
-        const int a = t / 6, k = t - a * 6;
+    for (; c < n; c++) s0 += p[(size_t)c * stride];
+    return (s0 + s1) + (s2 + s3);
+}
+
+// signed value of one contribution code to entry (r, c) of a block of S
+__device__ __forceinline__ double contrib(const SolveArgs& A, int cd, int r, int c) {
+    const int ty = code_type(cd), v = code_val(cd);
+    if (ty == 0)
+        return sum_parts(A.hpart + (size_t)(v >> 2) * A.nch * kNH + hs_index(v & 3, r, c), A.nch,
+                         kNH);
+    const int e36 = ty == 1 ? r * 6 + c : c * 6 + r;
+    return -sum_parts(A.spart + (size_t)v * A.nchS * 36 + e36, A.nchS, 36);
+}
+
+// One thread per entry of S (row-major n x n) and of b: S = sum of the listed
+// Hessian blocks minus the Schur pair blocks (ba.cuh:520-548, 722-742), then
+// the LM damping S_ii += ep + lm*S_ii after the Schur step (ba.cuh:749-750).
+__global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
+    const int n = A.n, P = A.P;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n * n) {
+        const int row = t / n, col = t - (t / n) * n;
+        const int a = row / 6, r = row - (row / 6) * 6;
+        const int bb = col / 6, c = col - (col / 6) * 6;
+        const int blk = A.plan.blkmap[a * P + bb];
+        double s = 0.0;
+        if (blk >= 0) {
+            // contributions in list order, four loads in flight at a time
+            const int q0 = A.plan.sblk_ptr[blk], q1 = A.plan.sblk_ptr[blk + 1];
+            int q = q0;
+            for (; q + 4 <= q1; q += 4) {
+                const double v0 = contrib(A, A.plan.sblk_src[q], r, c);
+                const double v1 = contrib(A, A.plan.sblk_src[q + 1], r, c);
+                const double v2 = contrib(A, A.plan.sblk_src[q + 2], r, c);
+                const double v3 = contrib(A, A.plan.sblk_src[q + 3], r, c);
+                s += v0;
+                s += v1;
+                s += v2;
+                s += v3;
+            }
+            for (; q < q1; q++) s += contrib(A, A.plan.sblk_src[q], r, c);
+        }
+        if (row == col) s = s + (double)A.ep + (double)A.lm * s;
+        A.S_dbg[t] = s;
+    } else if (t < n * n + n) {
+        const int i = t - n * n;
+        const int a = i / 6, k = i - (i / 6) * 6;
         double s = 0.0;
         for (int q = A.plan.bv_ptr[a]; q < A.plan.bv_ptr[a + 1]; q++) {
             const int cd = A.plan.bv_src[q];
-            const int ty = code_type(cd), v = code_val(cd);
-            if (ty == 0) {
-                const int e = v >> 1, which = v & 1;
-                const double* h = A.hpart + (size_t)e * A.nch * kNH + 78 + which * 6 + k;
-                for (int ch = 0; ch < A.nch; ch++) s += h[(size_t)ch * kNH];
-            } else {
-                s -= sp_entry(A, A.N_pu + v, k);
+            const int v = code_val(cd);
+            if (code_type(cd) == 0)
+                s += sum_parts(A.hpart + (size_t)(v >> 1) * A.nch * kNH + 78 + (v & 1) * 6 + k,
+                               A.nch, kNH);
+            else
+                s -= sum_parts(A.spart + (size_t)(A.N_pu + v) * A.nchS * 36 + k, A.nchS, 36);
+        }
+        A.b_dbg[i] = s;
+    }
+}
+
+// ---- blocked Cholesky S = L L^T (lower, row-major, leading dimension n) ----
+// Block columns of kNB: (1) the diagonal block is factored by wave 0 with one
+// row per lane in registers (broadcasts by readlane, no memory round trips);
+// (2) the panel below it is solved row-parallel; (3) the trailing triangle is
+// updated entry-parallel. Three barriers per block column instead of one per
+// column. Works on S in LDS or in global memory. The SPD test is the
+// reference's: every pivot must be positive before its sqrt (ba.cuh:422).
+constexpr int kNB = 16;
+
+__device__ __forceinline__ double bcast(double v, int src) {
+    const int lo = __builtin_amdgcn_readlane(__double2loint(v), src);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(v), src);
+    return __hiloint2double(hi, lo);
+}
+
+// packed lower-triangle index t -> (i, k), 0 <= k <= i
+__device__ __forceinline__ void tri_unpack(int t, int& i, int& k) {
+    int r = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
+    while (r * (r + 1) / 2 > t) r--;
+    while ((r + 1) * (r + 2) / 2 <= t) r++;
+    i = r;
+    k = t - r * (r + 1) / 2;
+}
+
+__device__ __forceinline__ bool chol_blocked(double* S, int n, int* sh_flag) {
+    const int tid = threadIdx.x;
+    if (tid == 0) *sh_flag = 1;
+    __syncthreads();
+    for (int j0 = 0; j0 < n; j0 += kNB) {
+        const int jb = min(kNB, n - j0);
+        if (tid < 64) {  // (1) diagonal block, wave 0
+            const int lane = tid;
+            double d[kNB];
+#pragma unroll
+            for (int m = 0; m < kNB; m++)
+                d[m] = (lane < jb && m <= lane) ? S[(size_t)(j0 + lane) * n + j0 + m] : 0.0;
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                if (k < jb) {
+                    const double dkk = bcast(d[k], k);
+                    ok = ok && (dkk > 0.0);
+                    const double lkk = sqrt(dkk);
+                    d[k] = lane == k ? lkk : (lane > k ? d[k] / lkk : d[k]);
+#pragma unroll
+                    for (int m = k + 1; m < kNB; m++) {
+                        if (m < jb) {
+                            const double lmk = bcast(d[k], m);
+                            if (lane >= m) d[m] -= d[k] * lmk;
+                        }
+                    }
+                }
             }
-        }
-        b[t] = s;
-    }
-    __syncthreads();
-    // LM damping after the Schur step (ba.cuh:749-750)
-    for (int t = threadIdx.x; t < n; t += blockDim.x) {
-        const double d = S[(size_t)t * n + t];
-        S[(size_t)t * n + t] = d + (double)A.ep + (double)A.lm * d;
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < n * n; t += blockDim.x) A.S_dbg[t] = S[t];
-    for (int t = threadIdx.x; t < n; t += blockDim.x) A.b_dbg[t] = b[t];
-}
-
-// In-place LDL^T of the lower triangle: after it, S[j][j] = d_j and
-// S[i][j] = d_j * L[i][j] (i > j). One barrier per column. Returns false if a
-// pivot is not positive (same criterion as the Cholesky sqrt, ba.cuh:422).
-__device__ bool ldl_factor(double* S, int n) {
-    bool ok = true;
-    for (int j = 0; j < n; j++) {
-        const double d = S[(size_t)j * n + j];
-        if (!(d > 0.0)) ok = false;
-        const double inv = 1.0 / d;
-        const int m = n - j - 1;
-        for (int t = threadIdx.x; t < m * m; t += blockDim.x) {
-            const int i = j + 1 + t / m, k = j + 1 + t % m;
-            if (k <= i) S[(size_t)i * n + k] -= S[(size_t)i * n + j] * S[(size_t)k * n + j] * inv;
+#pragma unroll
+            for (int m = 0; m < kNB; m++)
+                if (lane < jb && m <= lane) S[(size_t)(j0 + lane) * n + j0 + m] = d[m];
+            if (lane == 0 && !ok) *sh_flag = 0;
         }
         __syncthreads();
+        if (!*sh_flag) return false;
+        const int r0 = j0 + jb;
+        // (2) panel rows r0..n-1: x L_D^T = S[i][j0:j0+jb]
+        for (int i = r0 + tid; i < n; i += blockDim.x) {
+            double x[kNB];
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                if (k < jb) {
+                    double s = S[(size_t)i * n + j0 + k];
+#pragma unroll
+                    for (int m = 0; m < k; m++) s -= x[m] * S[(size_t)(j0 + k) * n + j0 + m];
+                    x[k] = s / S[(size_t)(j0 + k) * n + j0 + k];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kNB; k++)
+                if (k < jb) S[(size_t)i * n + j0 + k] = x[k];
+        }
+        __syncthreads();
+        // (3) trailing triangle S[i][k] -= L[i][J] . L[k][J], r0 <= k <= i < n
+        const int mm = n - r0;
+        const int cnt = mm * (mm + 1) / 2;
+        for (int t = tid; t < cnt; t += blockDim.x) {
+            int ii, kk;
+            tri_unpack(t, ii, kk);
+            const double* li = S + (size_t)(r0 + ii) * n + j0;
+            const double* lk = S + (size_t)(r0 + kk) * n + j0;
+            double s = 0.0;
+#pragma unroll
+            for (int m = 0; m < kNB; m++)
+                if (m < jb) s += li[m] * lk[m];
+            S[(size_t)(r0 + ii) * n + r0 + kk] -= s;
+        }
+        __syncthreads();
     }
-    return ok;
+    return true;
 }
 
-// Solves L D L^T x = b (factor from ldl_factor), x in y[]. All threads call.
-__device__ void ldl_solve(const double* S, double* y, int n) {
-    for (int k = 0; k < n; k++) {
-        const double yk = y[k];
-        const double inv = 1.0 / S[(size_t)k * n + k];
+// Solves L L^T x = b in place in y[] (y in LDS), factor from chol_blocked.
+__device__ __forceinline__ void chol_solve_blocked(const double* S, double* y, int n) {
+    const int tid = threadIdx.x;
+    for (int j0 = 0; j0 < n; j0 += kNB) {  // forward: L z = b
+        const int jb = min(kNB, n - j0);
+        if (tid < 64) {
+            const int lane = tid;
+            double v = lane < jb ? y[j0 + lane] : 0.0;
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                if (k < jb) {
+                    if (lane == k) v = v / S[(size_t)(j0 + k) * n + j0 + k];
+                    const double zk = bcast(v, k);
+                    if (lane > k && lane < jb) v -= S[(size_t)(j0 + lane) * n + j0 + k] * zk;
+                }
+            }
+            if (lane < jb) y[j0 + lane] = v;
+        }
         __syncthreads();
-        for (int i = k + 1 + threadIdx.x; i < n; i += blockDim.x)
-            y[i] -= S[(size_t)i * n + k] * inv * yk;
+        for (int i = j0 + jb + tid; i < n; i += blockDim.x) {
+            double s = y[i];
+            for (int m = 0; m < jb; m++) s -= S[(size_t)i * n + j0 + m] * y[j0 + m];
+            y[i] = s;
+        }
         __syncthreads();
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] /= S[(size_t)i * n + i];
-    __syncthreads();
-    for (int k = n - 1; k >= 0; k--) {
-        const double xk = y[k];
+    for (int j0 = ((n - 1) / kNB) * kNB; j0 >= 0; j0 -= kNB) {  // backward: L^T x = z
+        const int jb = min(kNB, n - j0);
+        if (tid < 64) {
+            const int lane = tid;
+            double v = lane < jb ? y[j0 + lane] : 0.0;
+#pragma unroll
+            for (int k = kNB - 1; k >= 0; k--) {
+                if (k < jb) {
+                    if (lane == k) v = v / S[(size_t)(j0 + k) * n + j0 + k];
+                    const double xk = bcast(v, k);
+                    if (lane < k) v -= S[(size_t)(j0 + k) * n + j0 + lane] * xk;
+                }
+            }
+            if (lane < jb) y[j0 + lane] = v;
+        }
         __syncthreads();
-        for (int i = threadIdx.x; i < k; i += blockDim.x)
-            y[i] -= S[(size_t)k * n + i] / S[(size_t)i * n + i] * xk;
+        for (int i = tid; i < j0; i += blockDim.x) {
+            double s = y[i];
+            for (int m = 0; m < jb; m++) s -= S[(size_t)(j0 + m) * n + i] * y[j0 + m];
+            y[i] = s;
+        }
         __syncthreads();
     }
 }
 
-__device__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
+// Workgroup copy with eight loads in flight per thread.
+__device__ __forceinline__ void copy_in(double* dst, const double* src, int count) {
+    const int step = blockDim.x;
+    int t = threadIdx.x;
+    for (; t + 7 * step < count; t += 8 * step) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = src[t + u * step];
+#pragma unroll
+        for (int u = 0; u < 8; u++) dst[t + u * step] = v[u];
+    }
+    for (; t < count; t += step) dst[t] = src[t];
+}
+
+__device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
     const int n = A.n;
     if (threadIdx.x == 0) {
         A.flags[0] = ok ? 0 : 1;
@@ -463,24 +591,34 @@ __device__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
     }
 }
 
-__global__ __launch_bounds__(1024) void k_ba_solve_small(SolveArgs A) {
+// S and b in LDS (n <= 90), one workgroup of 256 threads.
+__global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
     extern __shared__ double smem[];
+    const int n = A.n;
     double* S = smem;
-    double* b = smem + (size_t)A.n * A.n;
-    assemble(A, S, b);
-    const bool ok = ldl_factor(S, A.n);
-    if (ok) ldl_solve(S, b, A.n);
+    double* b = smem + (size_t)n * n;
+    copy_in(S, A.S_dbg, n * n);
+    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
+    __syncthreads();
+    __shared__ int sh_flag;
+    const bool ok = chol_blocked(S, n, &sh_flag);
+    if (ok) chol_solve_blocked(S, b, n);
     __syncthreads();
     finish_solve(A, b, ok);
 }
 
-__global__ __launch_bounds__(1024) void k_ba_solve_large(SolveArgs A) {
+// S in global memory (n > 90), b in LDS.
+__global__ __launch_bounds__(1024) void k_ba_solve_global(SolveArgs A) {
     extern __shared__ double smem[];
+    const int n = A.n;
     double* b = smem;
     double* S = A.S;
-    assemble(A, S, b);
-    const bool ok = ldl_factor(S, A.n);
-    if (ok) ldl_solve(S, b, A.n);
+    copy_in(S, A.S_dbg, n * n);
+    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
+    __syncthreads();
+    __shared__ int sh_flag;
+    const bool ok = chol_blocked(S, n, &sh_flag);
+    if (ok) chol_solve_blocked(S, b, n);
     __syncthreads();
     finish_solve(A, b, ok);
 }
@@ -521,7 +659,7 @@ struct BaState {
     // plan sizes
     int M = 0, P = 0, n = 0, N_kf = 0, N_E = 0, N_pu = 0, n_blk = 0, nch = 1, nchS = 1;
     std::vector<int> host;  // packed plan
-    size_t off[15] = {0};
+    size_t off[kPlanParts] = {0};
     DevBuf plan_dev, hpart, E, Q, Wv, spart, S, S_dbg, b_dbg, dx_dbg, dx, flags;
     HostStage stage;
     bool has_system = false;
@@ -532,10 +670,11 @@ namespace {
 PlanDev plan_ptrs(BaState* s) {
     const int* base = s->plan_dev.as<int>();
     PlanDev p;
-    const int** f[15] = {&p.kf_list, &p.kf_eptr, &p.kf_eidx, &p.edge_ri, &p.edge_rj,
-                         &p.row_pose, &p.row_kf, &p.kf_rptr, &p.kf_rows, &p.pairs,
-                         &p.sblk, &p.sblk_ptr, &p.sblk_src, &p.bv_ptr, &p.bv_src};
-    for (int i = 0; i < 15; i++) *f[i] = base + s->off[i];
+    const int** f[kPlanParts] = {&p.kf_list, &p.kf_eptr, &p.kf_eidx, &p.edge_ri, &p.edge_rj,
+                                 &p.row_pose, &p.row_kf, &p.kf_rptr, &p.kf_rows, &p.pairs,
+                                 &p.sblk, &p.sblk_ptr, &p.sblk_src, &p.bv_ptr, &p.bv_src,
+                                 &p.blkmap};
+    for (int i = 0; i < kPlanParts; i++) *f[i] = base + s->off[i];
     return p;
 }
 
@@ -647,11 +786,14 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
     s->n_blk = (int)sblk.size();
     s->nch = (HW + kLinPx - 1) / kLinPx;
     s->nchS = (HW + kSchPx - 1) / kSchPx;
-    const std::vector<int>* parts[15] = {&kf_list, &kf_eptr, &kf_eidx, &edge_ri, &edge_rj,
-                                         &row_pose, &row_kf, &kf_rptr, &kf_rows, &pairs,
-                                         &sblk, &sblk_ptr, &sblk_src, &bv_ptr, &bv_src};
+    std::vector<int> blkmap((size_t)P * P, -1);
+    for (size_t k = 0; k < sblk.size(); k++) blkmap[sblk[k]] = (int)k;
+    const std::vector<int>* parts[kPlanParts] = {&kf_list, &kf_eptr, &kf_eidx, &edge_ri,
+                                                 &edge_rj, &row_pose, &row_kf, &kf_rptr,
+                                                 &kf_rows, &pairs, &sblk, &sblk_ptr,
+                                                 &sblk_src, &bv_ptr, &bv_src, &blkmap};
     s->host.clear();
-    for (int i = 0; i < 15; i++) {
+    for (int i = 0; i < kPlanParts; i++) {
         s->off[i] = s->host.size();
         s->host.insert(s->host.end(), parts[i]->begin(), parts[i]->end());
         s->host.push_back(0);  // keeps every array non-empty
@@ -671,8 +813,8 @@ int ba_create(slk_ctx* ctx) {
 void ba_destroy(slk_ctx* ctx) {
     BaState* s = ctx->ba;
     if (!s) return;
-    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->E, &s->Q, &s->Wv, &s->spart,
-                      &s->S, &s->S_dbg, &s->b_dbg, &s->dx_dbg, &s->dx, &s->flags};
+    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->E,      &s->Q,  &s->Wv,   &s->spart,
+                      &s->S,        &s->S_dbg, &s->b_dbg,  &s->dx_dbg, &s->dx, &s->flags};
     for (DevBuf* b : bufs) b->release();
     s->stage.release();
     delete s;
@@ -771,14 +913,21 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     A.dx = s->dx.as<float>();
     A.flags = s->flags.as<int>();
     A.poses = poses;
+    {
+        ProfScope ps(ctx, "ba_assemble", stream);
+        const int items = s->n * s->n + s->n;
+        hipLaunchKernelGGL(k_ba_assemble, dim3((items + 255) / 256), dim3(256), 0, stream, A);
+    }
+    SLK_HIP(hipGetLastError());
     if (s->n <= kSmallN) {
         ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);
-        hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(1024), shm, stream, A);
+        const int threads = 256;
+        hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(threads), shm, stream, A);
     } else {
         ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = (size_t)s->n * sizeof(double);
-        hipLaunchKernelGGL(k_ba_solve_large, dim3(1), dim3(1024), shm, stream, A);
+        hipLaunchKernelGGL(k_ba_solve_global, dim3(1), dim3(1024), shm, stream, A);
     }
     SLK_HIP(hipGetLastError());
     if (!motion_only && s->N_E > 0) {

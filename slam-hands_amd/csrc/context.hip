@@ -160,10 +160,8 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     if (!ctx) return SLK_OK;
     prof_clear(ctx);
     slk::ba_destroy(ctx);
-    for (int l = 0; l < slk::kMaxLevels; l++) {
-        ctx->batch_lvl[l].release();
-        ctx->single_lvl[l].release();
-    }
+    ctx->batch_win.release();
+    for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();
     ctx->zero_idx.release();
     delete ctx;
     return SLK_OK;

@@ -4,17 +4,26 @@
 // Reference semantics: cuda_slam/main.cu:1077-1217 (kernels) and :1500-1613
 // (build_correlation, sample_correlation, batch_build_and_sample_correlation).
 //
-// k_corr_pyramid: vol[e][p][q] = alpha * sum_c fa[c][p] * fb[c][q] on fp32
-// MFMA (v_mfma_f32_32x32x2f32), with every pyramid level produced in the
-// epilogue from the tile still in registers. A workgroup is 4 waves stacked
-// over 4x32 source pixels; each wave owns an 8-row x 32-column band of the
-// target image (eight 32x32 accumulator blocks), which is exactly one level-3
-// cell column group, so levels 1..3 never need data from another wave:
-//   x-pairs come from the neighbouring lane (lane ^ 1, ^ 2, ^ 4),
-//   y-pairs from the accumulator block of the next target row.
-// Both operands are read straight from global memory in the MFMA operand
-// layout (consecutive lanes = consecutive pixels of one channel), so loads
-// and level-0 stores are 128-byte coalesced per half-wave.
+// k_corr_tile: vol[e][p][q] = alpha * sum_c fa[c][p] * fb[c][q] on fp32 MFMA
+// (v_mfma_f32_32x32x2f32), with every pyramid level produced in the epilogue
+// from the tile still in registers. A workgroup is 4 waves stacked over 4x32
+// source pixels; each wave owns an 8-row x 32-column band of the target image
+// (eight 32x32 accumulator blocks), which is exactly one group of level-3
+// cells, so levels 1..3 never need data from another wave: x-pairs come from
+// the neighbouring lane (lane ^ 1, ^ 2, ^ 4), y-pairs from the accumulator
+// block of the next target row. Operands are read straight from global memory
+// in the MFMA operand layout (consecutive lanes = consecutive pixels of one
+// channel: 128-byte coalesced per half-wave), double-buffered in registers so
+// the next 8 channels are in flight while the MFMAs of the current 8 run.
+//
+// Two epilogues:
+//   * materializing (single-edge build_correlation): every level is stored in
+//     the reference's layout [HW][h>>l][w>>l] (debug dump, sample_correlation);
+//   * windowed (batched build_and_sample): the caller never sees the volume,
+//     so each tile stores only the cells that fall in some source pixel's 8x8
+//     lookup window at that level, into a compact [HW][levels][8][8] buffer.
+//     The volume and pyramid (~50 MB per 48x64 edge) never reach HBM; the
+//     windows are 1 KB per source pixel.
 #include <cmath>
 
 #include "slk_internal.hpp"
@@ -29,7 +38,9 @@ constexpr int kWaveSrc = 32;       // source pixels per wave
 constexpr int kTileSrc = 128;      // source pixels per workgroup
 constexpr int kBand = 8;           // target rows per tile (2^(levels-1) for 4 levels)
 constexpr int kCols = 32;          // target columns per tile
+constexpr int kKU = 4;             // 2-channel MFMA steps per prefetch group
 constexpr int kMaxEdgesPerLaunch = 64;
+constexpr int kWinCells = 64;      // 8x8 window cells per level
 
 struct EdgeIdx {
     int ii[kMaxEdgesPerLaunch];
@@ -53,12 +64,39 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
 
+// First window cell of a lookup at level l: floor(c * 2^-l) - 3, with the
+// coordinate scaled in fp32 as main.cu:1189-1190 does. Clamped so that far or
+// non-finite coordinates give an origin no cell can match.
+__device__ __forceinline__ int win_origin(float c, int l) {
+    const float s = c * (1.0f / (float)(1 << l));
+    return (int)fminf(fmaxf(floorf(s), -1048576.0f), 1048576.0f) - 3;
+}
+
+// Operands of kKU 2-channel steps. Lanes of sources past HW or targets outside
+// the image read a clamped in-bounds address instead of being zeroed: an MFMA
+// output D[i][j] only combines row i of A with column j of B, so such lanes
+// only reach accumulator rows/columns that are never stored, and never a
+// stored pooled cell (a pooled cell inside the level only averages targets
+// inside the image). Leaving the values unselected lets the loads stay in
+// flight under the previous group's MFMAs.
 template <typename Tin>
-__global__ __launch_bounds__(kWG) void k_corr_pyramid(
+__device__ __forceinline__ void load_group(const Tin* A, const Tin* Bp, const int* boff, long HW,
+                                           int c0, float* a, float (*b)[kBand]) {
+#pragma unroll
+    for (int u = 0; u < kKU; u++) {
+        const long off = (long)(c0 + 2 * u) * HW;
+        a[u] = ldf(A + off);
+#pragma unroll
+        for (int r = 0; r < kBand; r++) b[u][r] = ldf(Bp + off + boff[r]);
+    }
+}
+
+template <typename Tin, bool WIN>
+__global__ __launch_bounds__(kWG) void k_corr_tile(
     const Tin* __restrict__ fa, const Tin* __restrict__ fb, long fstride,
     const int* __restrict__ ia, const int* __restrict__ ib, EdgeIdx eidx, LevelOut lo,
-    int slot0, int h, int w, int C, float alpha, int levels, int mtiles, int nbands,
-    int ncb) {
+    const float* __restrict__ coords, float* __restrict__ win, int slot0, int h, int w, int C,
+    float alpha, int levels, int mtiles, int nbands, int ncb) {
     const int HW = h * w;
     const int tpe = mtiles * nbands * ncb;
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
@@ -96,41 +134,79 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
 #pragma unroll
     for (int r = 0; r < kBand; r++) acc[r] = (f32x16){0};
 
-#pragma unroll 4
-    for (int c = 0; c < C; c += 2) {
-        const long off = (long)c * HW;
-        float a = ldf(A + off);
-        a = va ? a : 0.0f;
-        float b[kBand];
+    // main loop: groups of kKU 2-channel steps, next group loaded before the
+    // current group's MFMAs are issued
+    // Two register sets used in ping-pong (no copies, which would make every
+    // group wait for its own loads).
+    const int ngroups = C / (2 * kKU);
+    float a0[kKU], b0[kKU][kBand], a1[kKU], b1[kKU][kBand];
+    auto mfma_group = [&](const float* a, const float (*b)[kBand]) {
 #pragma unroll
-        for (int r = 0; r < kBand; r++) {
-            const float v = ldf(Bp + off + boff[r]);
-            b[r] = vb[r] ? v : 0.0f;
-        }
+        for (int u = 0; u < kKU; u++)
+#pragma unroll
+            for (int r = 0; r < kBand; r++)
+                acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], b[u][r], acc[r], 0, 0, 0);
+    };
+    if (ngroups > 0) load_group(A, Bp, boff, HW, 0, a0, b0);
+    for (int g = 0; g < ngroups; g += 2) {
+        if (g + 1 < ngroups) load_group(A, Bp, boff, HW, (g + 1) * 2 * kKU, a1, b1);
+        mfma_group(a0, b0);
+        if (g + 2 < ngroups) load_group(A, Bp, boff, HW, (g + 2) * 2 * kKU, a0, b0);
+        if (g + 1 < ngroups) mfma_group(a1, b1);
+    }
+    for (int c = ngroups * 2 * kKU; c < C; c += 2) {  // C not a multiple of 2*kKU
+        const long off = (long)c * HW;
+        const float a = ldf(A + off);
 #pragma unroll
         for (int r = 0; r < kBand; r++)
-            acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b[r], acc[r], 0, 0, 0);
+            acc[r] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, ldf(Bp + off + boff[r]), acc[r], 0,
+                                                          0, 0);
     }
 
     // Accumulator layout of v_mfma_f32_32x32x2f32: lane l, register v holds
     // D[i][j] with j = l % 32 (target column) and
     // i = 8*(v/4) + 4*(l/32) + v%4 (source row of the wave's 32).
     const int slot = slot0 + e;
-    float* out0 = lo.p[0] + (size_t)slot * HW * HW;
 #pragma unroll
     for (int r = 0; r < kBand; r++) {
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[r][v] *= alpha;
     }
+    int prow[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) prow[v] = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
+    float cxs[16], cys[16];
+    float* wbase = nullptr;
+    if constexpr (WIN) {
+        const float* cc = coords + (size_t)e * 2 * HW;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int q = prow[v] < HW ? prow[v] : 0;
+            cxs[v] = cc[q];
+            cys[v] = cc[HW + q];
+        }
+        wbase = win + (size_t)slot * HW * (kMaxLevels * kWinCells);
+    }
+    // store of one cell (y, x) of level l for source row register v
+    auto put = [&](int l, int v, int y, int x, float val, float* plane, int hl, int wl) {
+        const int p = prow[v];
+        if (p >= HW) return;
+        if constexpr (WIN) {
+            const int ox = x - win_origin(cxs[v], l);
+            const int oy = y - win_origin(cys[v], l);
+            if ((unsigned)ox < 8u && (unsigned)oy < 8u)
+                wbase[((size_t)p * kMaxLevels + l) * kWinCells + oy * 8 + ox] = val;
+        } else {
+            __builtin_nontemporal_store(val, plane + (size_t)p * (hl * wl) + y * wl + x);
+        }
+    };
+
+    float* out0 = WIN ? nullptr : lo.p[0] + (size_t)slot * HW * HW;
 #pragma unroll
     for (int r = 0; r < kBand; r++) {
         if (!vb[r]) continue;
-        const int q = (y0 + r) * w + xb;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
-            if (p < HW) __builtin_nontemporal_store(acc[r][v], out0 + (size_t)p * HW + q);
-        }
+        for (int v = 0; v < 16; v++) put(0, v, y0 + r, xb, acc[r][v], out0, h, w);
     }
     if (levels < 2) return;
 
@@ -153,7 +229,7 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
         }
     }
     {
-        float* out1 = lo.p[1] + (size_t)slot * HW * (h1 * w1);
+        float* out1 = WIN ? nullptr : lo.p[1] + (size_t)slot * HW * (h1 * w1);
         const int x1 = xb >> 1;
         const bool lane_ok = ((col & 1) == 0) && x1 < w1;
 #pragma unroll
@@ -161,12 +237,7 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
             const int y1 = (y0 >> 1) + r;
             if (!lane_ok || y1 >= h1) continue;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
-                if (p < HW)
-                    __builtin_nontemporal_store(l1[r][v],
-                                                out1 + (size_t)p * (h1 * w1) + y1 * w1 + x1);
-            }
+            for (int v = 0; v < 16; v++) put(1, v, y1, x1, l1[r][v], out1, h1, w1);
         }
     }
     if (levels < 3) return;
@@ -188,7 +259,7 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
         }
     }
     {
-        float* out2 = lo.p[2] + (size_t)slot * HW * (h2 * w2);
+        float* out2 = WIN ? nullptr : lo.p[2] + (size_t)slot * HW * (h2 * w2);
         const int x2 = xb >> 2;
         const bool lane_ok = ((col & 3) == 0) && x2 < w2;
 #pragma unroll
@@ -196,18 +267,13 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
             const int y2 = (y0 >> 2) + r;
             if (!lane_ok || y2 >= h2) continue;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
-                if (p < HW)
-                    __builtin_nontemporal_store(l2[r][v],
-                                                out2 + (size_t)p * (h2 * w2) + y2 * w2 + x2);
-            }
+            for (int v = 0; v < 16; v++) put(2, v, y2, x2, l2[r][v], out2, h2, w2);
         }
     }
     if (levels < 4) return;
 
     const int h3 = h >> 3, w3 = w >> 3;
-    float* out3 = lo.p[3] + (size_t)slot * HW * (h3 * w3);
+    float* out3 = WIN ? nullptr : lo.p[3] + (size_t)slot * HW * (h3 * w3);
     const int x3 = xb >> 3, y3 = y0 >> 3;
     const bool lane_ok = ((col & 7) == 0) && x3 < w3 && y3 < h3;
 #pragma unroll
@@ -219,10 +285,7 @@ __global__ __launch_bounds__(kWG) void k_corr_pyramid(
         float s = a + b;
         s = s + c;
         s = s + d;
-        const float l3 = 0.25f * s;
-        const int p = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
-        if (lane_ok && p < HW)
-            __builtin_nontemporal_store(l3, out3 + (size_t)p * (h3 * w3) + y3 * w3 + x3);
+        if (lane_ok) put(3, v, y3, x3, 0.25f * s, out3, h3, w3);
     }
 }
 
@@ -233,11 +296,29 @@ struct LevelIn {
     int w[kMaxLevels];
 };
 
+// Bilinear combination of an 8x8 window (rows = y offset, cols = x offset):
+// channel a*7 + b (a the x offset, b the y offset); the four corner terms are
+// added in the reference's loop order (i outer = x, j inner = y): (a,b),
+// (a,b+1), (a+1,b), (a+1,b+1) (main.cu:1200-1216).
+__device__ __forceinline__ void window_to_channels(const float (&win)[8][8], float dx, float dy,
+                                                   float* o, int stride) {
+    const float wx1 = dx, wx0 = 1.0f - dx, wy1 = dy, wy0 = 1.0f - dy;
+#pragma unroll
+    for (int a = 0; a < 7; a++) {
+#pragma unroll
+        for (int b = 0; b < 7; b++) {
+            float s = win[b][a] * wx0 * wy0;
+            s = s + win[b + 1][a] * wx0 * wy1;
+            s = s + win[b][a + 1] * wx1 * wy0;
+            s = s + win[b + 1][a + 1] * wx1 * wy1;
+            o[(size_t)(a * 7 + b) * stride] = s;
+        }
+    }
+}
+
 // One thread per (source pixel, level, edge): zero-padded bilinear samples at
 // (x0 - 3 + a, y0 - 3 + b), a,b in [0,7), from that pixel's own row of the
-// level (main.cu:1175-1217). The four corner terms of a channel are added in
-// the reference's loop order (i outer = x, j inner = y): (a,b), (a,b+1),
-// (a+1,b), (a+1,b+1). Non-finite coordinates give zeros.
+// level (main.cu:1175-1217). Non-finite coordinates give zeros.
 __global__ __launch_bounds__(256) void k_corr_lookup(LevelIn lv, const float* __restrict__ coords,
                                                      float* __restrict__ out, int HW1,
                                                      int level_base, int nch) {
@@ -246,19 +327,18 @@ __global__ __launch_bounds__(256) void k_corr_lookup(LevelIn lv, const float* __
     const int e = blockIdx.z;
     if (p >= HW1) return;
     const int H2 = lv.h[l], W2 = lv.w[l];
-    const float scale = 1.0f / (float)(1 << (level_base + l));
-    const float x0 = coords[(size_t)e * 2 * HW1 + p] * scale;
-    const float y0 = coords[(size_t)e * 2 * HW1 + HW1 + p] * scale;
-    float* o = out + ((size_t)e * nch + (size_t)(level_base + l) * 49) * HW1 + p;
+    const int lvl = level_base + l;
+    const float cx = coords[(size_t)e * 2 * HW1 + p];
+    const float cy = coords[(size_t)e * 2 * HW1 + HW1 + p];
+    const float x0 = cx * (1.0f / (float)(1 << lvl));
+    const float y0 = cy * (1.0f / (float)(1 << lvl));
+    float* o = out + ((size_t)e * nch + (size_t)lvl * 49) * HW1 + p;
     if (!(isfinite(x0) && isfinite(y0))) {
 #pragma unroll
         for (int k = 0; k < 49; k++) o[(size_t)k * HW1] = 0.0f;
         return;
     }
-    const float fx = floorf(x0), fy = floorf(y0);
-    const float dx = x0 - fx, dy = y0 - fy;
-    const int ix = (int)fminf(fmaxf(fx, -1048576.0f), 1048576.0f) - 3;
-    const int iy = (int)fminf(fmaxf(fy, -1048576.0f), 1048576.0f) - 3;
+    const int ix = win_origin(cx, lvl), iy = win_origin(cy, lvl);
     const float* vol = lv.p[l] + ((size_t)e * HW1 + p) * (size_t)(H2 * W2);
     float win[8][8];
 #pragma unroll
@@ -272,36 +352,66 @@ __global__ __launch_bounds__(256) void k_corr_lookup(LevelIn lv, const float* __
             win[j][i] = ok ? vol[y * W2 + x] : 0.0f;
         }
     }
-    const float wx1 = dx, wx0 = 1.0f - dx, wy1 = dy, wy0 = 1.0f - dy;
-#pragma unroll
-    for (int a = 0; a < 7; a++) {
-#pragma unroll
-        for (int b = 0; b < 7; b++) {
-            float s = win[b][a] * wx0 * wy0;
-            s = s + win[b + 1][a] * wx0 * wy1;
-            s = s + win[b][a + 1] * wx1 * wy0;
-            s = s + win[b + 1][a + 1] * wx1 * wy1;
-            o[(size_t)(a * 7 + b) * HW1] = s;
-        }
-    }
+    window_to_channels(win, x0 - floorf(x0), y0 - floorf(y0), o, HW1);
 }
 
-template <typename Tin>
-int launch_pyramid(slk_ctx* ctx, const Tin* fa, const Tin* fb, long fstride, const int* ia,
-                   const int* ib, const EdgeIdx& eidx, int n, float* const* lvl, int slot0,
-                   hipStream_t stream) {
+// Same lookup from the compact windows of the batched path: cells inside the
+// level are read from the window buffer (contiguous 256 bytes per pixel and
+// level), cells outside it are zero (they were never written).
+__global__ __launch_bounds__(256) void k_corr_lookup_win(LevelIn lv, const float* __restrict__ wb,
+                                                         const float* __restrict__ coords,
+                                                         float* __restrict__ out, int HW1,
+                                                         int nch) {
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    const int l = blockIdx.y;
+    const int e = blockIdx.z;
+    if (p >= HW1) return;
+    const int H2 = lv.h[l], W2 = lv.w[l];
+    const float cx = coords[(size_t)e * 2 * HW1 + p];
+    const float cy = coords[(size_t)e * 2 * HW1 + HW1 + p];
+    const float x0 = cx * (1.0f / (float)(1 << l));
+    const float y0 = cy * (1.0f / (float)(1 << l));
+    float* o = out + ((size_t)e * nch + (size_t)l * 49) * HW1 + p;
+    if (!(isfinite(x0) && isfinite(y0))) {
+#pragma unroll
+        for (int k = 0; k < 49; k++) o[(size_t)k * HW1] = 0.0f;
+        return;
+    }
+    const int ix = win_origin(cx, l), iy = win_origin(cy, l);
+    const float4* src = reinterpret_cast<const float4*>(
+        wb + (((size_t)e * HW1 + p) * kMaxLevels + l) * kWinCells);
+    float win[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const bool vy = (unsigned)(iy + j) < (unsigned)H2;
+        const float4 lo4 = src[2 * j], hi4 = src[2 * j + 1];
+        const float cell[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const bool ok = vy && (unsigned)(ix + i) < (unsigned)W2;
+            win[j][i] = ok ? cell[i] : 0.0f;
+        }
+    }
+    window_to_channels(win, x0 - floorf(x0), y0 - floorf(y0), o, HW1);
+}
+
+template <typename Tin, bool WIN>
+int launch_tile(slk_ctx* ctx, const Tin* fa, const Tin* fb, long fstride, const int* ia,
+                const int* ib, const EdgeIdx& eidx, int n, float* const* lvl,
+                const float* coords, float* win, int slot0, hipStream_t stream) {
     const int mtiles = (ctx->HW + kTileSrc - 1) / kTileSrc;
     const int nbands = (ctx->h + kBand - 1) / kBand;
     const int ncb = (ctx->w + kCols - 1) / kCols;
     const long total = (long)n * mtiles * nbands * ncb;
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
-    LevelOut lo;
-    for (int l = 0; l < kMaxLevels; l++) lo.p[l] = l < ctx->levels ? lvl[l] : nullptr;
+    LevelOut lo{};
+    if (lvl)
+        for (int l = 0; l < kMaxLevels; l++) lo.p[l] = l < ctx->levels ? lvl[l] : nullptr;
     {
-        ProfScope ps(ctx, "corr_pyramid", stream);
-        hipLaunchKernelGGL(k_corr_pyramid<Tin>, dim3((unsigned)total), dim3(kWG), 0, stream, fa,
-                           fb, fstride, ia, ib, eidx, lo, slot0, ctx->h, ctx->w, ctx->C,
-                           ctx->alpha, ctx->levels, mtiles, nbands, ncb);
+        ProfScope ps(ctx, WIN ? "corr_window" : "corr_pyramid", stream);
+        hipLaunchKernelGGL((k_corr_tile<Tin, WIN>), dim3((unsigned)total), dim3(kWG), 0, stream,
+                           fa, fb, fstride, ia, ib, eidx, lo, coords, win, slot0, ctx->h, ctx->w,
+                           ctx->C, ctx->alpha, ctx->levels, mtiles, nbands, ncb);
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
@@ -321,7 +431,7 @@ int launch_lookup(slk_ctx* ctx, const LevelIn& lv, int nlev, int level_base, int
 LevelIn level_in(slk_ctx* ctx, DevBuf* bufs) {
     LevelIn lv{};
     for (int l = 0; l < ctx->levels; l++) {
-        lv.p[l] = bufs[l].as<float>();
+        lv.p[l] = bufs ? bufs[l].as<float>() : nullptr;
         lv.h[l] = ctx->lh[l];
         lv.w[l] = ctx->lw[l];
     }
@@ -337,9 +447,8 @@ int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, co
     if (fstride < (long)ctx->C * ctx->HW) return fail(SLK_E_ARG, "corr_batch: fmap_stride < C*h*w");
     const int HW = ctx->HW;
     const int nch = ctx->levels * 49;
-    float* lvl[kMaxLevels];
-    for (int l = 0; l < ctx->levels; l++) lvl[l] = ctx->batch_lvl[l].as<float>();
-    const LevelIn lv = level_in(ctx, ctx->batch_lvl);
+    float* win = ctx->batch_win.as<float>();
+    const LevelIn lv = level_in(ctx, nullptr);
     for (int b0 = 0; b0 < B; b0 += ctx->max_batch) {
         const int nb = B - b0 < ctx->max_batch ? B - b0 : ctx->max_batch;
         for (int s0 = 0; s0 < nb; s0 += kMaxEdgesPerLaunch) {
@@ -355,17 +464,22 @@ int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, co
             }
             const int* ia = ii_host ? nullptr : ii_dev + b0 + s0;
             const int* ib = ii_host ? nullptr : jj_dev + b0 + s0;
+            const float* cc = coords + (size_t)(b0 + s0) * 2 * HW;
             if (dtype == SLK_F32) {
                 const float* f = static_cast<const float*>(fmaps);
-                SLK_TRY(launch_pyramid<float>(ctx, f, f, fstride, ia, ib, eidx, n, lvl, s0, stream));
+                SLK_TRY((launch_tile<float, true>(ctx, f, f, fstride, ia, ib, eidx, n, nullptr, cc,
+                                                  win, s0, stream)));
             } else {
                 const _Float16* f = static_cast<const _Float16*>(fmaps);
-                SLK_TRY(launch_pyramid<_Float16>(ctx, f, f, fstride, ia, ib, eidx, n, lvl, s0,
-                                                 stream));
+                SLK_TRY((launch_tile<_Float16, true>(ctx, f, f, fstride, ia, ib, eidx, n, nullptr,
+                                                     cc, win, s0, stream)));
             }
         }
-        SLK_TRY(launch_lookup(ctx, lv, ctx->levels, 0, nch, coords + (size_t)b0 * 2 * HW,
-                              out + (size_t)b0 * nch * HW, nb, HW, stream));
+        dim3 grid((HW + 255) / 256, ctx->levels, nb);
+        ProfScope ps(ctx, "corr_lookup_win", stream);
+        hipLaunchKernelGGL(k_corr_lookup_win, grid, dim3(256), 0, stream, lv, win,
+                           coords + (size_t)b0 * 2 * HW, out + (size_t)b0 * nch * HW, HW, nch);
+        SLK_HIP(hipGetLastError());
     }
     return SLK_OK;
 }
@@ -374,9 +488,10 @@ int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, co
 
 int corr_alloc(slk_ctx* ctx) {
     const size_t HW = (size_t)ctx->HW;
+    SLK_TRY(ctx->batch_win.ensure((size_t)ctx->max_batch * HW * kMaxLevels * kWinCells *
+                                  sizeof(float)));
     for (int l = 0; l < ctx->levels; l++) {
         const size_t plane = (size_t)ctx->lh[l] * ctx->lw[l];
-        SLK_TRY(ctx->batch_lvl[l].ensure((size_t)ctx->max_batch * HW * plane * sizeof(float)));
         SLK_TRY(ctx->single_lvl[l].ensure(HW * plane * sizeof(float)));
     }
     SLK_TRY(ctx->zero_idx.ensure(sizeof(int) * 4));
@@ -415,13 +530,13 @@ extern "C" int slk_corr_build(slk_ctx* ctx, const void* f_i, const void* f_j, in
     const int* z = ctx->zero_idx.as<int>();
     EdgeIdx eidx{};
     if (dtype == SLK_F32) {
-        SLK_TRY(launch_pyramid<float>(ctx, static_cast<const float*>(f_i),
-                                      static_cast<const float*>(f_j), 0, z, z, eidx, 1, lvl, 0,
-                                      stream));
+        SLK_TRY((launch_tile<float, false>(ctx, static_cast<const float*>(f_i),
+                                           static_cast<const float*>(f_j), 0, z, z, eidx, 1, lvl,
+                                           nullptr, nullptr, 0, stream)));
     } else if (dtype == SLK_F16) {
-        SLK_TRY(launch_pyramid<_Float16>(ctx, static_cast<const _Float16*>(f_i),
-                                         static_cast<const _Float16*>(f_j), 0, z, z, eidx, 1, lvl,
-                                         0, stream));
+        SLK_TRY((launch_tile<_Float16, false>(ctx, static_cast<const _Float16*>(f_i),
+                                              static_cast<const _Float16*>(f_j), 0, z, z, eidx, 1,
+                                              lvl, nullptr, nullptr, 0, stream)));
     } else {
         return fail(SLK_E_ARG, "corr_build: bad dtype");
     }

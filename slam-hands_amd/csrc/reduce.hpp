@@ -44,4 +44,73 @@ __device__ __forceinline__ void block_sum(T (&v)[N], T* scratch) {
     __syncthreads();
 }
 
+// Butterfly reduce-scatter of N values over the 64 lanes of a wave. At each
+// of the 6 levels (lane masks 32..1) a lane keeps one half of its values and
+// trades the other half with its partner, so the whole reduction costs about
+// N shuffles instead of the 6N of N independent wave_sum()s. On return lane l
+// holds the wave totals of `valid` consecutive value indices starting at
+// `base` in v[0..valid).
+template <typename T, int C, int M>
+__device__ __forceinline__ void rs_level(T* v, int lane, int& base, int& valid) {
+    constexpr int H = (C + 1) / 2;
+    const bool up = (lane & M) != 0;
+#pragma unroll
+    for (int k = 0; k < H; k++) {
+        const T lo = v[k];
+        const T hi = (k + H < C) ? v[k + H] : T(0);
+        const T send = up ? lo : hi;
+        const T keep = up ? hi : lo;
+        v[k] = keep + __shfl_xor(send, M);
+    }
+    if (up) {
+        base += H;
+        valid = valid > H ? valid - H : 0;
+    } else {
+        valid = valid < H ? valid : H;
+    }
+}
+
+template <int N>
+struct RsCounts {
+    static constexpr int c0 = N, c1 = (c0 + 1) / 2, c2 = (c1 + 1) / 2, c3 = (c2 + 1) / 2,
+                         c4 = (c3 + 1) / 2, c5 = (c4 + 1) / 2, c6 = (c5 + 1) / 2;
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void wave_reduce_scatter(T (&v)[N], int lane, int& base, int& valid) {
+    using R = RsCounts<N>;
+    base = 0;
+    valid = N;
+    rs_level<T, R::c0, 32>(v, lane, base, valid);
+    rs_level<T, R::c1, 16>(v, lane, base, valid);
+    rs_level<T, R::c2, 8>(v, lane, base, valid);
+    rs_level<T, R::c3, 4>(v, lane, base, valid);
+    rs_level<T, R::c4, 2>(v, lane, base, valid);
+    rs_level<T, R::c5, 1>(v, lane, base, valid);
+}
+
+// Workgroup totals of N values per thread into tot[0..N) (LDS or global),
+// deterministic: reduce-scatter inside each wave, then a fixed-order sum over
+// the waves. `scratch` holds N * (blockDim.x / 64) elements of LDS. Contains
+// barriers: call from all threads. v[] is clobbered.
+template <typename T, int N>
+__device__ __forceinline__ void block_sum_to(T (&v)[N], T* scratch, T* tot) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    int base, valid;
+    wave_reduce_scatter(v, lane, base, valid);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < RsCounts<N>::c6; k++)
+        if (k < valid) scratch[(base + k) * nw + wave] = v[k];
+    __syncthreads();
+    for (int t = threadIdx.x; t < N; t += blockDim.x) {
+        T s = scratch[t * nw];
+        for (int w = 1; w < nw; w++) s += scratch[t * nw + w];
+        tot[t] = s;
+    }
+    __syncthreads();
+}
+
 }  // namespace slk

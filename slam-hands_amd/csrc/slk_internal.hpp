@@ -70,8 +70,8 @@ struct slk_ctx {
     int h = 0, w = 0, HW = 0, C = 0, levels = 4, radius = 3, max_batch = 48;
     float alpha = 1.0f / 16.0f;
     int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
-    // correlation scratch: batched pyramid [max_batch][HW][lh*lw] per level
-    slk::DevBuf batch_lvl[slk::kMaxLevels];
+    // batched-path scratch: 8x8 lookup windows [max_batch][HW][4 levels][64]
+    slk::DevBuf batch_win;
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
     bool single_built = false;
