@@ -34,6 +34,10 @@ import numpy as np  # noqa: E402
 
 METRIC = "corr edges/sec + BA iters/sec (48-edge window, 1 MI355X); % roofline"
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (matrix and vector)
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+# HBM bytes per corr_window launch from rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE
+# (profiles/corr_window_pmc_traffic.md); None until measured
+TRAFFIC_BYTES = None
 PEAK_HBM_GBS = 8000.0
 
 
@@ -127,20 +131,31 @@ def main():
     kern = {k: {"avg_us": 1e3 * v[0] / v[1], "launches": v[1]} for k, v in prof.items()}
 
     # dominant kernel: the correlation GEMM of the batched path (corr_window:
-    # all-pairs fp32 MFMA contraction + 4-level pyramid in the epilogue, only
-    # the lookup windows stored). Algorithmic work per edge: 2*HW^2*C flops.
+    # all-pairs contraction + 4-level pyramid in the epilogue, only the lookup
+    # windows stored). Algorithmic work per edge: 2*HW^2*C flops. The fp32
+    # features are contracted as three bf16 MFMA passes (hi*hi + hi*lo + lo*hi
+    # of a bf16 hi/lo split, fp32 accumulation), so the MFMA work executed is
+    # 3x the algorithmic flops and the bound is the dense bf16 MFMA peak.
     flop = 2.0 * HW * HW * C * B
     gemm_s = kern["corr_window"]["avg_us"] * 1e-6
-    achieved = flop / gemm_s / 1e12
+    fp32_equiv = flop / gemm_s / 1e12
+    passes = 3 if ctx.corr_precision == slk.SLK_PREC_BF16X3 else 1
+    peak = PEAK_BF16_TFLOPS if passes == 3 else PEAK_FP32_TFLOPS
+    achieved = passes * fp32_equiv
     roof = {
-        "kernel": "corr_window (fp32 MFMA all-pairs GEMM + pyramid epilogue, 48 edges)",
+        "kernel": ("corr_window (bf16x3-split MFMA all-pairs GEMM + pyramid epilogue, 48 edges)"
+                   if passes == 3 else
+                   "corr_window (fp32 MFMA all-pairs GEMM + pyramid epilogue, 48 edges)"),
         "bound": "mfma",
         "achieved": round(achieved, 2),
-        "peak": PEAK_FP32_TFLOPS,
+        "peak": peak,
         "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-        "traffic": None,
+        "frac": round(achieved / peak, 4),
+        "traffic": TRAFFIC_BYTES,
         "algorithmic_flop_per_launch": flop,
+        "mfma_flop_per_launch": passes * flop,
+        "fp32_equivalent_TFLOPs": round(fp32_equiv, 2),
+        "frac_of_fp32_peak": round(fp32_equiv / PEAK_FP32_TFLOPS, 4),
     }
     # lookup: coords + four 8x8 windows read, 196 channels written per pixel
     look_bytes = B * HW * (2 * 4 + 4 * 64 * 4 + 196 * 4)
@@ -159,7 +174,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (correlation, MFMA) / f64 (BA arithmetic, f32 storage)",
+        "dtype": ("f32 (correlation: f32 features as a 3-pass bf16 hi/lo MFMA split, f32 "
+                  "accumulation) / f64 (BA arithmetic, f32 storage)"),
         "data": "synthetic (seeded N(0,1) features, U(-8,8) flow, BA window of workloads.py)",
         "config": {"workload": "corr_window + 3x ba_window", "frames": n, "edges": B, "h": h,
                    "w": w, "C": C, "levels": 4, "radius": 3, "ba_iters_per_step": iters,

@@ -42,6 +42,14 @@ typedef enum {
 
 typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
 
+/* Contraction used for fp32 features (fp16 features always use exact fp16
+ * products with fp32 accumulation, the arithmetic of the reference's
+ * cublasGemmEx on its fp16 fmaps, main.cu:1508-1515):
+ *  SLK_PREC_BF16X3 (default) -- hi/lo bf16 split, three bf16 MFMA passes,
+ *                               ~1e-5 relative to the row scale;
+ *  SLK_PREC_FP32             -- fp32 MFMA (v_mfma_f32_32x32x2f32). */
+typedef enum { SLK_PREC_BF16X3 = 0, SLK_PREC_FP32 = 1 } slk_corr_precision;
+
 /* ---------------------------------------------------------------- context */
 
 /* Creates a context on the current HIP device for h x w feature maps with C
@@ -73,6 +81,10 @@ int slk_profile_kernel(slk_ctx* ctx, int idx, const char** name, double* total_m
                        int* launches);
 
 /* ------------------------------------------------------------ correlation */
+
+/* Selects the contraction for fp32 features (slk_corr_precision). The
+ * reference has no such switch: it always contracts fp16 fmaps. */
+int slk_set_corr_precision(slk_ctx* ctx, int precision);
 
 /* CudaDroid::batch_build_and_sample_correlation(batch_size, edge_start,
  * coords_2hw, corr_out_196hw), cuda_slam/main.cu:1555-1613 (copy in

@@ -25,6 +25,7 @@
 //     The volume and pyramid (~50 MB per 48x64 edge) never reach HBM; the
 //     windows are 1 KB per source pixel.
 #include <cmath>
+#include <type_traits>
 
 #include "slk_internal.hpp"
 
@@ -289,6 +290,326 @@ __global__ __launch_bounds__(kWG) void k_corr_tile(
     }
 }
 
+// ------------------------------------------ split-precision MFMA kernel --
+// k_corr_mx: same tile, pyramid and epilogues as k_corr_tile, with the
+// contraction on the 16-wide-K matrix instructions of gfx950:
+//   fp32 features: each value is split into bf16 hi + lo (hi = rne(x),
+//     lo = rne(x - hi)) and vol = hi.hi + hi.lo + lo.hi on
+//     v_mfma_f32_32x32x16_bf16 (exact products, fp32 accumulation; the
+//     dropped lo.lo term and the rounding of lo are ~2^-16 relative per
+//     product) -- fp32-grade accuracy at 16x the fp32 MFMA rate, 3 passes;
+//   fp16 features: one v_mfma_f32_32x32x16_f16 pass (exact products, fp32
+//     accumulation: the arithmetic of the reference's cublasGemmEx on its
+//     fp16 fmaps, main.cu:1508-1515).
+// Operands are staged through LDS in 16-channel chunks, double-buffered: each
+// chunk is read once from global memory per workgroup, converted once, and
+// the global loads of chunk k+1 are in flight during the MFMAs of chunk k.
+// LDS rows are 48 bytes (16 values + pad) so the 128-bit operand reads of a
+// 32x32x16 MFMA (lane l: row l%32, 8 consecutive k at 8*(l/32)) hit
+// distinct banks. Waves form a 2x2 grid over the workgroup's 128 sources x
+// 8 target rows: wave (wm, wn) owns sources wm*64..+63 and rows wn*4..+3
+// (eight 32x32 accumulator blocks); level 3 pools across the two row halves
+// through LDS.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kKC = 16;        // channels per LDS stage
+constexpr int kRowU = 24;      // u16 per LDS operand row (16 used + 8 pad)
+constexpr int kTileTgt = 256;  // targets per workgroup tile (8 rows x 32 cols)
+enum { kModeBF16x3 = 0, kModeF16 = 1 };
+
+template <int MODE>
+struct MxSmem {
+    static constexpr int NP = MODE == kModeBF16x3 ? 2 : 1;  // hi (+ lo)
+    unsigned short A[2][NP][kTileSrc][kRowU];
+    unsigned short B[2][NP][kTileTgt][kRowU];
+};
+
+// hi = rne_bf16(x), lo = rne_bf16(x - hi), packed as lo << 16 | hi
+__device__ __forceinline__ unsigned split_bf16(float x) {
+    const __bf16 h = (__bf16)x;
+    const __bf16 l = (__bf16)(x - (float)h);
+    return (unsigned)__builtin_bit_cast(unsigned short, h) |
+           ((unsigned)__builtin_bit_cast(unsigned short, l) << 16);
+}
+
+template <int MODE>
+__device__ __forceinline__ f32x16 mfma16(u16x8_t a, u16x8_t b, f32x16 c) {
+    if constexpr (MODE == kModeBF16x3)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0,
+                                                       0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int MODE, bool WIN>
+__global__ __launch_bounds__(kWG) void k_corr_mx(
+    const void* __restrict__ fa_, const void* __restrict__ fb_, long fstride,
+    const int* __restrict__ ia, const int* __restrict__ ib, EdgeIdx eidx, LevelOut lo,
+    const float* __restrict__ coords, float* __restrict__ win, int slot0, int h, int w, int C,
+    float alpha, int levels, int mtiles, int nbands, int ncb) {
+    using Tin = typename std::conditional<MODE == kModeBF16x3, float, _Float16>::type;
+    constexpr int NP = MxSmem<MODE>::NP;
+    __shared__ MxSmem<MODE> sm;
+    const int HW = h * w;
+    const int tpe = mtiles * nbands * ncb;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int e = bid / tpe;
+    int t = bid - e * tpe;
+    const int cb = t % ncb;
+    t /= ncb;
+    const int band = t % nbands;
+    const int mt = t / nbands;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int y0 = band * kBand, x0 = cb * kCols;
+    const int fi = ia ? ia[e] : eidx.ii[e];
+    const int fj = ib ? ib[e] : eidx.jj[e];
+    const Tin* Ab = static_cast<const Tin*>(fa_) + (long)fi * fstride;
+    const Tin* Bb = static_cast<const Tin*>(fb_) + (long)fj * fstride;
+
+    // staging roles: A -- source tid%128, channels (tid/128)*8..+7 of the
+    // chunk; B -- target tid (row tid/32, column tid%32), all 16 channels.
+    // Out-of-range pixels read a clamped address (see load_group).
+    const int a_src = tid & (kTileSrc - 1), a_half = tid >> 7;
+    const int pa = mt * kTileSrc + a_src;
+    const Tin* a_ptr = Ab + (long)(a_half * 8) * HW + (pa < HW ? pa : 0);
+    const int by = y0 + (tid >> 5), bx = x0 + (tid & 31);
+    const Tin* b_ptr = Bb + ((by < h && bx < w) ? by * w + bx : 0);
+    Tin ra[8], rb[kKC];
+    auto gload = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) ra[u] = a_ptr[(long)(c0 + u) * HW];
+#pragma unroll
+        for (int u = 0; u < kKC; u++) rb[u] = b_ptr[(long)(c0 + u) * HW];
+    };
+    auto lstore = [&](int st) {
+        u16x8_t hi, lo8;
+        if constexpr (MODE == kModeBF16x3) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const unsigned s = split_bf16(ra[u]);
+                hi[u] = (unsigned short)(s & 0xffffu);
+                lo8[u] = (unsigned short)(s >> 16);
+            }
+            *reinterpret_cast<u16x8_t*>(&sm.A[st][0][a_src][a_half * 8]) = hi;
+            *reinterpret_cast<u16x8_t*>(&sm.A[st][1][a_src][a_half * 8]) = lo8;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const unsigned s = split_bf16(rb[half * 8 + u]);
+                    hi[u] = (unsigned short)(s & 0xffffu);
+                    lo8[u] = (unsigned short)(s >> 16);
+                }
+                *reinterpret_cast<u16x8_t*>(&sm.B[st][0][tid][half * 8]) = hi;
+                *reinterpret_cast<u16x8_t*>(&sm.B[st][1][tid][half * 8]) = lo8;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; u++) hi[u] = __builtin_bit_cast(unsigned short, ra[u]);
+            *reinterpret_cast<u16x8_t*>(&sm.A[st][0][a_src][a_half * 8]) = hi;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    hi[u] = __builtin_bit_cast(unsigned short, rb[half * 8 + u]);
+                *reinterpret_cast<u16x8_t*>(&sm.B[st][0][tid][half * 8]) = hi;
+            }
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) acc[sb][tb] = (f32x16){0};
+    const int orow = lane & 31, okk = (lane >> 5) * 8;
+    auto compute = [&](int st) {
+        u16x8_t ah[2], al[2], bh[4], bl[4];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            ah[sb] = *reinterpret_cast<const u16x8_t*>(&sm.A[st][0][wm * 64 + sb * 32 + orow][okk]);
+            if constexpr (NP == 2)
+                al[sb] =
+                    *reinterpret_cast<const u16x8_t*>(&sm.A[st][NP - 1][wm * 64 + sb * 32 + orow][okk]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            bh[tb] = *reinterpret_cast<const u16x8_t*>(&sm.B[st][0][(wn * 4 + tb) * 32 + orow][okk]);
+            if constexpr (NP == 2)
+                bl[tb] = *reinterpret_cast<const u16x8_t*>(
+                    &sm.B[st][NP - 1][(wn * 4 + tb) * 32 + orow][okk]);
+        }
+        if constexpr (MODE == kModeBF16x3) {
+            // small cross terms first, then hi.hi; eight independent
+            // accumulators between dependent MFMAs
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+                    acc[sb][tb] = mfma16<MODE>(al[sb], bh[tb], acc[sb][tb]);
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+                    acc[sb][tb] = mfma16<MODE>(ah[sb], bl[tb], acc[sb][tb]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma16<MODE>(ah[sb], bh[tb], acc[sb][tb]);
+    };
+
+    const int nchunks = C / kKC;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ch++) {
+        if (ch + 1 < nchunks) gload((ch + 1) * kKC);
+        compute(ch & 1);
+        if (ch + 1 < nchunks) lstore((ch + 1) & 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue (accumulator layout as in k_corr_tile) ----
+    const int slot = slot0 + e;
+    const int col = lane & 31, khalf = lane >> 5, xb = x0 + col;
+    const int ps0 = mt * kTileSrc + wm * 64;
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[sb][tb][v] *= alpha;
+    auto prow = [&](int sb, int v) { return ps0 + sb * 32 + 8 * (v >> 2) + 4 * khalf + (v & 3); };
+    float* wbase = WIN ? win + (size_t)slot * HW * (kMaxLevels * kWinCells) : nullptr;
+    // coordinates of the lane's 32 source rows, loaded once before any store
+    // (the window stores would otherwise order every later coordinate load)
+    float cxs[2][16], cys[2][16];
+    if constexpr (WIN) {
+        const float* cc = coords + (size_t)e * 2 * HW;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int p = prow(sb, v);
+                const int q = p < HW ? p : 0;
+                cxs[sb][v] = cc[q];
+                cys[sb][v] = cc[HW + q];
+            }
+    }
+    auto put = [&](int l, int sb, int v, int y, int x, float val, float* plane, int hl, int wl) {
+        const int p = prow(sb, v);
+        if (p >= HW) return;
+        if constexpr (WIN) {
+            const int ox = x - win_origin(cxs[sb][v], l);
+            const int oy = y - win_origin(cys[sb][v], l);
+            if ((unsigned)ox < 8u && (unsigned)oy < 8u)
+                wbase[((size_t)p * kMaxLevels + l) * kWinCells + oy * 8 + ox] = val;
+        } else {
+            __builtin_nontemporal_store(val, plane + (size_t)p * (hl * wl) + y * wl + x);
+        }
+    };
+    const int yw = y0 + wn * 4;  // first target row of this wave
+    {
+        float* out0 = WIN ? nullptr : lo.p[0] + (size_t)slot * HW * HW;
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            const int y = yw + tb;
+            if (y >= h || xb >= w) continue;
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) put(0, sb, v, y, xb, acc[sb][tb][v], out0, h, w);
+        }
+    }
+    float l2[2][16];
+    if (levels >= 2) {
+        const int h1 = h >> 1, w1 = w >> 1, x1 = xb >> 1;
+        float* out1 = WIN ? nullptr : lo.p[1] + (size_t)slot * HW * (h1 * w1);
+        float l1[2][2][16];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    // 0.25f*(((in[y][x] + in[y][x+1]) + in[y+1][x]) + in[y+1][x+1]),
+                    // the order of avg_pool_2x2_kernel (main.cu:1166-1167)
+                    const float a = acc[sb][2 * r][v], c = acc[sb][2 * r + 1][v];
+                    const float b = __shfl_xor(a, 1), d = __shfl_xor(c, 1);
+                    float s = a + b;
+                    s = s + c;
+                    s = s + d;
+                    l1[sb][r][v] = 0.25f * s;
+                }
+        const bool ok1 = ((col & 1) == 0) && x1 < w1;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int y1 = (yw >> 1) + r;
+            if (!ok1 || y1 >= h1) continue;
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) put(1, sb, v, y1, x1, l1[sb][r][v], out1, h1, w1);
+        }
+        if (levels >= 3) {
+            const int h2 = h >> 2, w2 = w >> 2, x2 = xb >> 2, y2 = yw >> 2;
+            float* out2 = WIN ? nullptr : lo.p[2] + (size_t)slot * HW * (h2 * w2);
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const float a = l1[sb][0][v], c = l1[sb][1][v];
+                    const float b = __shfl_xor(a, 2), d = __shfl_xor(c, 2);
+                    float s = a + b;
+                    s = s + c;
+                    s = s + d;
+                    l2[sb][v] = 0.25f * s;
+                }
+            if (((col & 3) == 0) && x2 < w2 && y2 < h2) {
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) put(2, sb, v, y2, x2, l2[sb][v], out2, h2, w2);
+            }
+        }
+    }
+    if (levels >= 4) {
+        // level-2 rows 2*y3 (waves wn = 0) and 2*y3 + 1 (wn = 1) meet in LDS
+        float* xch = reinterpret_cast<float*>(&sm);  // [wm][sb][v][lane], 16 KB
+        if (wn == 1) {
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) xch[((wm * 2 + sb) * 16 + v) * 64 + lane] = l2[sb][v];
+        }
+        __syncthreads();
+        if (wn == 0) {
+            const int h3 = h >> 3, w3 = w >> 3, x3 = xb >> 3, y3 = y0 >> 3;
+            float* out3 = WIN ? nullptr : lo.p[3] + (size_t)slot * HW * (h3 * w3);
+            const bool ok3 = ((col & 7) == 0) && x3 < w3 && y3 < h3;
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const float a = l2[sb][v];
+                    const float b = __shfl_xor(a, 4);
+                    const float* xr = xch + ((wm * 2 + sb) * 16 + v) * 64;
+                    const float c = xr[lane], d = xr[lane ^ 4];
+                    float s = a + b;
+                    s = s + c;
+                    s = s + d;
+                    if (ok3) put(3, sb, v, y3, x3, 0.25f * s, out3, h3, w3);
+                }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- lookup --
 struct LevelIn {
     const float* p[kMaxLevels];
@@ -409,9 +730,20 @@ int launch_tile(slk_ctx* ctx, const Tin* fa, const Tin* fb, long fstride, const 
         for (int l = 0; l < kMaxLevels; l++) lo.p[l] = l < ctx->levels ? lvl[l] : nullptr;
     {
         ProfScope ps(ctx, WIN ? "corr_window" : "corr_pyramid", stream);
-        hipLaunchKernelGGL((k_corr_tile<Tin, WIN>), dim3((unsigned)total), dim3(kWG), 0, stream,
-                           fa, fb, fstride, ia, ib, eidx, lo, coords, win, slot0, ctx->h, ctx->w,
-                           ctx->C, ctx->alpha, ctx->levels, mtiles, nbands, ncb);
+        constexpr bool f32 = std::is_same<Tin, float>::value;
+        const bool split = (ctx->C % kKC == 0) && !(f32 && ctx->corr_prec == SLK_PREC_FP32);
+        if (split) {
+            constexpr int MODE = f32 ? kModeBF16x3 : kModeF16;
+            hipLaunchKernelGGL((k_corr_mx<MODE, WIN>), dim3((unsigned)total), dim3(kWG), 0,
+                               stream, fa, fb, fstride, ia, ib, eidx, lo, coords, win, slot0,
+                               ctx->h, ctx->w, ctx->C, ctx->alpha, ctx->levels, mtiles, nbands,
+                               ncb);
+        } else {
+            hipLaunchKernelGGL((k_corr_tile<Tin, WIN>), dim3((unsigned)total), dim3(kWG), 0,
+                               stream, fa, fb, fstride, ia, ib, eidx, lo, coords, win, slot0,
+                               ctx->h, ctx->w, ctx->C, ctx->alpha, ctx->levels, mtiles, nbands,
+                               ncb);
+        }
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
@@ -502,6 +834,13 @@ int corr_alloc(slk_ctx* ctx) {
 }  // namespace slk
 
 using namespace slk;
+
+extern "C" int slk_set_corr_precision(slk_ctx* ctx, int precision) {
+    if (!ctx || (precision != SLK_PREC_BF16X3 && precision != SLK_PREC_FP32))
+        return fail(SLK_E_ARG, "set_corr_precision: bad argument");
+    ctx->corr_prec = precision;
+    return SLK_OK;
+}
 
 extern "C" int slk_corr_batch_build_and_sample(slk_ctx* ctx, const void* fmaps, int dtype,
                                                long fmap_stride, const int* ii_host,

@@ -69,6 +69,7 @@ struct slk_ctx {
     int device = 0;
     int h = 0, w = 0, HW = 0, C = 0, levels = 4, radius = 3, max_batch = 48;
     float alpha = 1.0f / 16.0f;
+    int corr_prec = SLK_PREC_BF16X3;  // contraction of fp32 features
     int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
     // batched-path scratch: 8x8 lookup windows [max_batch][HW][4 levels][64]
     slk::DevBuf batch_win;

@@ -22,10 +22,12 @@ HIP_LIB = "libamdhip64.so"
 
 SLK_OK, SLK_E_ARG, SLK_E_HIP, SLK_E_NOT_SPD, SLK_E_STATE = range(5)
 SLK_F32, SLK_F16 = 0, 1
+SLK_PREC_BF16X3, SLK_PREC_FP32 = 0, 1
 
 # every entry point declared in include/slk.h
 EXPORTS = [
     "slk_create", "slk_destroy", "slk_last_error", "slk_profile_enable", "slk_profile_kernel",
+    "slk_set_corr_precision",
     "slk_corr_batch_build_and_sample", "slk_corr_batch_build_and_sample_dev",
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
@@ -71,6 +73,7 @@ def lib():
             "slk_profile_enable": [P, I],
             "slk_profile_kernel": [P, I, ctypes.POINTER(ctypes.c_char_p),
                                    ctypes.POINTER(ctypes.c_double), ctypes.POINTER(I)],
+            "slk_set_corr_precision": [P, I],
             "slk_corr_batch_build_and_sample": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_batch_build_and_sample_dev": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_build": [P, P, P, I, P],
@@ -261,6 +264,7 @@ class Context:
 
     def __init__(self, h, w, C=128, max_batch=48, levels=4, radius=3, corr_scale=1.0 / 16.0):
         self.h, self.w, self.C, self.levels = h, w, C, levels
+        self.corr_precision = SLK_PREC_BF16X3  # the library's default
         self.ptr = P()
         check(lib().slk_create(ctypes.byref(self.ptr), h, w, C, max_batch, levels, radius,
                                float(corr_scale)))
@@ -275,6 +279,10 @@ class Context:
             self.close()
         except Exception:
             pass
+
+    def set_corr_precision(self, precision):
+        check(lib().slk_set_corr_precision(self.ptr, int(precision)))
+        self.corr_precision = int(precision)
 
     # main.cu:1555 batch_build_and_sample_correlation
     def batch_build_and_sample_correlation(self, fmaps, ii, jj, coords, out, dtype=SLK_F32,

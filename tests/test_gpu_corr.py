@@ -22,10 +22,11 @@ def slk():
     return gpu_or_fail()
 
 
-def run_single(slk, f, coords, alpha, levels=4, dtype=None):
+def run_single(slk, f, coords, alpha, levels=4, prec=0):
     C, h, w = f.shape[1:]
     dt = slk.SLK_F16 if f.dtype == np.float16 else slk.SLK_F32
     ctx = slk.Context(h, w, C=C, max_batch=1, levels=levels, corr_scale=alpha)
+    ctx.set_corr_precision(prec)
     fi = slk.DeviceArray.from_host(f[0])
     fj = slk.DeviceArray.from_host(f[1])
     cd = slk.DeviceArray.from_host(coords)
@@ -39,13 +40,15 @@ def run_single(slk, f, coords, alpha, levels=4, dtype=None):
     return pyr, res
 
 
-@pytest.mark.parametrize("h,w,levels", [(48, 64, 4), (54, 96, 4), (12, 20, 3), (7, 9, 1)])
-def test_single_edge_volume_pyramid_lookup(slk, h, w, levels):
-    announce(f"single edge h={h} w={w} levels={levels}")
+@pytest.mark.parametrize("h,w,levels,prec", [(48, 64, 4, 0), (48, 64, 4, 1), (54, 96, 4, 0),
+                                             (54, 96, 4, 1), (12, 20, 3, 0), (7, 9, 1, 0)])
+def test_single_edge_volume_pyramid_lookup(slk, h, w, levels, prec):
+    """prec 0: bf16x3 split contraction (default), 1: fp32 MFMA."""
+    announce(f"single edge h={h} w={w} levels={levels} prec={prec}")
     f = wl.frames(2, C=128, h=h, w=w, seed=100 + h)
     coords = wl.flow_coords(1, h, w, seed=7)[0]
     alpha = 1.0 / np.sqrt(128.0)
-    pyr, out = run_single(slk, f, coords, alpha, levels)
+    pyr, out = run_single(slk, f, coords, alpha, levels, prec)
     vol = orc.corr_volume(f[0].reshape(128, -1), f[1].reshape(128, -1), alpha)
     # level shapes: floor halving
     for l, lev in enumerate(pyr):
@@ -109,13 +112,14 @@ def test_nonfinite_and_far_coords_give_zeros(slk):
     assert_close_rel(out, orc.lookup(pyr, coords), tol=1e-5)
 
 
-def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, dtype=np.float32):
+def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, prec=0):
     f = wl.frames(nframes, C=128, h=h, w=w, seed=seed)
     ii, jj = wl.cyclic_edges(nframes)
     ii, jj = ii[:B], jj[:B]
     coords = wl.flow_coords(B, h, w, seed=seed + 1)
     alpha = 1.0 / 16.0
     ctx = slk.Context(h, w, C=128, max_batch=max_batch, corr_scale=alpha)
+    ctx.set_corr_precision(prec)
     fd = slk.DeviceArray.from_host(f)
     cd = slk.DeviceArray.from_host(coords)
     out = slk.DeviceArray((B, 196, h * w))
@@ -131,12 +135,13 @@ def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, dtype=np.f
     return f, ii, jj, coords, res
 
 
-def test_window_48_edges_matches_oracle(slk):
+@pytest.mark.parametrize("prec", [0, 1])
+def test_window_48_edges_matches_oracle(slk, prec):
     """Config corr_window: 12 frames, 48 edges; every edge checked on sampled
-    pixels plus 6 edges in full."""
-    announce("corr window 48 edges")
+    pixels plus 6 edges in full (prec 0: bf16x3, 1: fp32 MFMA)."""
+    announce(f"corr window 48 edges prec={prec}")
     h, w = 48, 64
-    f, ii, jj, coords, out = _window(slk, 12, h, w, 48, seed=20)
+    f, ii, jj, coords, out = _window(slk, 12, h, w, 48, seed=20, prec=prec)
     assert np.all(np.isfinite(out))
     full = [0, 7, 18, 29, 40, 47]
     ref = orc.corr_batch(f, ii[full], jj[full], coords[full], 1.0 / 16.0)
