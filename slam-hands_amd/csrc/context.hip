@@ -73,7 +73,8 @@ extern "C" int slk_create(slk_ctx** out, int h, int w, int C, int max_batch, int
     if (radius != 3) return fail(SLK_E_ARG, "slk_create: only radius 3 is implemented");
     if ((h >> (levels - 1)) < 1 || (w >> (levels - 1)) < 1)
         return fail(SLK_E_ARG, "slk_create: feature map too small for the pyramid depth");
-    if ((long)h * w > (1L << 24)) return fail(SLK_E_ARG, "slk_create: h*w too large");
+    if ((long)h * w > (1L << 24) || h > 65536 || w > 65536)
+        return fail(SLK_E_ARG, "slk_create: h*w above 2^24 or a side above 2^16");
     slk_ctx* ctx = new slk_ctx();
     ctx->h = h;
     ctx->w = w;
@@ -161,6 +162,8 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     prof_clear(ctx);
     slk::ba_destroy(ctx);
     ctx->batch_win.release();
+    ctx->split_feat.release();
+    ctx->split_pool.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();
     ctx->zero_idx.release();
     delete ctx;

@@ -27,12 +27,10 @@
 #include <cmath>
 #include <type_traits>
 
-#include "slk_internal.hpp"
+#include "corr_common.hpp"
 
 namespace slk {
 namespace {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWG = 256;           // 4 waves
 constexpr int kWaveSrc = 32;       // source pixels per wave
@@ -40,8 +38,6 @@ constexpr int kTileSrc = 128;      // source pixels per workgroup
 constexpr int kBand = 8;           // target rows per tile (2^(levels-1) for 4 levels)
 constexpr int kCols = 32;          // target columns per tile
 constexpr int kKU = 4;             // 2-channel MFMA steps per prefetch group
-constexpr int kMaxEdgesPerLaunch = 64;
-constexpr int kWinCells = 64;      // 8x8 window cells per level
 
 struct EdgeIdx {
     int ii[kMaxEdgesPerLaunch];
@@ -52,26 +48,8 @@ struct LevelOut {
     float* p[kMaxLevels];
 };
 
-// Workgroups are dispatched round-robin over the 8 XCDs; remap the linear id so
-// each XCD walks a contiguous range of (edge, tile) ids and its L2 holds the
-// few feature maps of the edges it is working on.
-__device__ __forceinline__ int xcd_remap(int bid, int total) {
-    constexpr int X = 8;
-    const int q = total / X, rem = total % X;
-    const int xcd = bid % X, local = bid / X;
-    return (xcd < rem) ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-}
-
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
-
-// First window cell of a lookup at level l: floor(c * 2^-l) - 3, with the
-// coordinate scaled in fp32 as main.cu:1189-1190 does. Clamped so that far or
-// non-finite coordinates give an origin no cell can match.
-__device__ __forceinline__ int win_origin(float c, int l) {
-    const float s = c * (1.0f / (float)(1 << l));
-    return (int)fminf(fmaxf(floorf(s), -1048576.0f), 1048576.0f) - 3;
-}
 
 // Operands of kKU 2-channel steps. Lanes of sources past HW or targets outside
 // the image read a clamped in-bounds address instead of being zeroed: an MFMA
@@ -310,9 +288,6 @@ __global__ __launch_bounds__(kWG) void k_corr_tile(
 // 8 target rows: wave (wm, wn) owns sources wm*64..+63 and rows wn*4..+3
 // (eight 32x32 accumulator blocks); level 3 pools across the two row halves
 // through LDS.
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kKC = 16;        // channels per LDS stage
 constexpr int kRowU = 24;      // u16 per LDS operand row (16 used + 8 pad)
@@ -325,14 +300,6 @@ struct MxSmem {
     unsigned short A[2][NP][kTileSrc][kRowU];
     unsigned short B[2][NP][kTileTgt][kRowU];
 };
-
-// hi = rne_bf16(x), lo = rne_bf16(x - hi), packed as lo << 16 | hi
-__device__ __forceinline__ unsigned split_bf16(float x) {
-    const __bf16 h = (__bf16)x;
-    const __bf16 l = (__bf16)(x - (float)h);
-    return (unsigned)__builtin_bit_cast(unsigned short, h) |
-           ((unsigned)__builtin_bit_cast(unsigned short, l) << 16);
-}
 
 template <int MODE>
 __device__ __forceinline__ f32x16 mfma16(u16x8_t a, u16x8_t b, f32x16 c) {
@@ -797,7 +764,13 @@ int corr_batch_impl(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, co
             const int* ia = ii_host ? nullptr : ii_dev + b0 + s0;
             const int* ib = ii_host ? nullptr : jj_dev + b0 + s0;
             const float* cc = coords + (size_t)(b0 + s0) * 2 * HW;
-            if (dtype == SLK_F32) {
+            if (corr_split_supported(ctx) &&
+                !(dtype == SLK_F32 && ctx->corr_prec == SLK_PREC_FP32)) {
+                SLK_TRY(corr_split_windows(ctx, fmaps, dtype, fstride,
+                                           ii_host ? eidx.ii : nullptr,
+                                           ii_host ? eidx.jj : nullptr, ia, ib, n, cc, win, s0,
+                                           stream));
+            } else if (dtype == SLK_F32) {
                 const float* f = static_cast<const float*>(fmaps);
                 SLK_TRY((launch_tile<float, true>(ctx, f, f, fstride, ia, ib, eidx, n, nullptr, cc,
                                                   win, s0, stream)));
@@ -822,6 +795,7 @@ int corr_alloc(slk_ctx* ctx) {
     const size_t HW = (size_t)ctx->HW;
     SLK_TRY(ctx->batch_win.ensure((size_t)ctx->max_batch * HW * kMaxLevels * kWinCells *
                                   sizeof(float)));
+    SLK_TRY(corr_split_alloc(ctx));
     for (int l = 0; l < ctx->levels; l++) {
         const size_t plane = (size_t)ctx->lh[l] * ctx->lw[l];
         SLK_TRY(ctx->single_lvl[l].ensure(HW * plane * sizeof(float)));

@@ -1,0 +1,471 @@
+// Batched correlation lookup windows from pre-split features (gfx950).
+//
+// Reference semantics: the volume vol[p][q] = alpha * sum_c fi[c][p] * fj[c][q]
+// (cublasGemmBatchedEx, cuda_slam/main.cu:1573-1581), its 2x2 average-pool
+// pyramid over the target dims (avg_pool_2x2_kernel, main.cu:1150-1170) and
+// the radius-3 lookup that batch_corr_sample_kernel (main.cu:1175-1217) makes
+// of every level. The lookup of source pixel p at level l only reads the 8x8
+// cells from (floor(x*2^-l) - 3, floor(y*2^-l) - 3); those windows are all this
+// path produces, into [slot][HW][4 levels][8][8] (k_corr_lookup_win then
+// weights them into the 196 output channels).
+//
+// Pooling is linear in the target, so level l of the pyramid is the product of
+// the source features with the pooled target features:
+//     pool_l(vol)[p][q] = alpha * fi[:,p] . pool_l(fj)[:,q]
+// Every level is therefore one GEMM over a concatenated target set (level-0
+// pixels, then level 1, 2, 3: HW + HW/4 + ... rows), with no pooling of the
+// product at all. This re-associates the reference's fp32 sums (the pyramid
+// cells agree to fp32 rounding, ~1e-7 relative); with integer-coded features
+// every intermediate is exact and the windows are bitwise equal.
+//
+// Stage 1 (k_feat_pool, k_feat_split), once per frame a launch uses: the fp32
+// pooled features of levels 1..3, then a bf16 hi/lo split of all levels
+// (hi = rne(x), lo = rne(x - hi)), stored chunk-major [plane][C/16][rows][16]
+// so a 16-channel chunk of consecutive rows is one contiguous block.
+// Stage 2 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
+// hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_bf16 (exact products, fp32
+// accumulation; the dropped lo.lo term is ~2^-16 relative), staging 16-channel
+// chunks through LDS, double-buffered so the global loads of chunk k+1 are in
+// flight during the MFMAs of chunk k. The accumulator tile is then transposed
+// through LDS ([target][source]) and, per source and level, one wave writes
+// the window cells that fall inside the tile, one lane per cell: one masked
+// store of 64 consecutive floats. Only ~2% of the level-0 products are window
+// cells, and none of them costs more than its LDS round trip.
+#include <algorithm>
+#include <climits>
+#include <type_traits>
+
+#include "corr_common.hpp"
+
+namespace slk {
+namespace {
+
+constexpr int kSrcTile = 128;  // sources per workgroup
+constexpr int kTgtTile = 256;  // targets per workgroup
+constexpr int kChunk = 16;     // channels per LDS stage
+constexpr int kRowU = 24;      // u16 per LDS operand row (16 used + 8 pad)
+constexpr int kTStride = 68;   // floats per transposed-tile row (64 sources + 4 pad)
+constexpr int kMaxSlots = 2 * kMaxEdgesPerLaunch;
+
+struct Geom {
+    int HW, Ttot, C, levels;
+    int off[kMaxLevels];   // first row of level l in the concatenated target set
+    int h[kMaxLevels], w[kMaxLevels];
+    int poff[kMaxLevels];  // offset of level l (>= 1) in a pooled-feature channel row
+    int pool_hw;           // HW_1 + HW_2 + HW_3
+};
+
+// Frame of each feature slot: a host-built list, or (device edge indices)
+// slot s < nb -> da[s], else db[s - nb].
+struct SlotFrames {
+    const int* da;
+    const int* db;
+    int nb;
+    int f[kMaxSlots];
+};
+
+struct EdgeSlots {
+    int si[kMaxEdgesPerLaunch];  // source slot of edge e
+    int sj[kMaxEdgesPerLaunch];  // target slot of edge e
+};
+
+__device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
+    if (m.da) return s < m.nb ? m.da[s] : m.db[s - m.nb];
+    return m.f[s];
+}
+
+__device__ __forceinline__ float ldf(const float* p) { return *p; }
+__device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
+
+// Level l >= 1 of the pooled features of one slot: 0.25f*(((a+b)+c)+d) over
+// the 2x2 block of level l-1, the order of avg_pool_2x2_kernel
+// (main.cu:1166-1167), floor dims. Grid (ceil(HW_l / 256), C, slots).
+template <typename Tin>
+__global__ __launch_bounds__(256) void k_feat_pool(const Tin* __restrict__ fm, long fstride,
+                                                   SlotFrames sf, int slot_lo,
+                                                   float* __restrict__ pool, Geom g, int l) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    const int wl = g.w[l];
+    if (q >= g.h[l] * wl) return;
+    const int c = blockIdx.y, s = slot_lo + blockIdx.z;
+    const int y = q / wl, x = q - y * wl;
+    float* prow = pool + ((size_t)s * g.C + c) * g.pool_hw;
+    float a, b, cc, d;
+    if (l == 1) {
+        const int wp = g.w[0];
+        const Tin* r0 = fm + (long)slot_frame(sf, s) * fstride + (long)c * g.HW + (2 * y) * wp +
+                        2 * x;
+        a = ldf(r0);
+        b = ldf(r0 + 1);
+        cc = ldf(r0 + wp);
+        d = ldf(r0 + wp + 1);
+    } else {
+        const int wp = g.w[l - 1];
+        const float* r0 = prow + g.poff[l - 1] + (2 * y) * wp + 2 * x;
+        a = r0[0];
+        b = r0[1];
+        cc = r0[wp];
+        d = r0[wp + 1];
+    }
+    float sum = a + b;
+    sum = sum + cc;
+    sum = sum + d;
+    prow[g.poff[l] + q] = 0.25f * sum;
+}
+
+// bf16 hi/lo split of rows [0, trows) of one slot's concatenated target set,
+// into out[slot][plane][C/16][Ttot][16]. Grid (ceil(trows / 256), C/16, slots).
+template <typename Tin>
+__global__ __launch_bounds__(256) void k_feat_split(const Tin* __restrict__ fm, long fstride,
+                                                    SlotFrames sf, int slot_lo,
+                                                    const float* __restrict__ pool,
+                                                    unsigned short* __restrict__ out, Geom g,
+                                                    int trows) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= trows) return;
+    const int k = blockIdx.y, s = slot_lo + blockIdx.z;
+    int l = 0;
+#pragma unroll
+    for (int m = 1; m < kMaxLevels; m++)
+        if (m < g.levels && t >= g.off[m]) l = m;
+    const int q = t - g.off[l];
+    float v[kChunk];
+    if (l == 0) {
+        const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW + q;
+#pragma unroll
+        for (int u = 0; u < kChunk; u++) v[u] = ldf(src + (long)u * g.HW);
+    } else {
+        const float* src = pool + ((size_t)s * g.C + k * kChunk) * g.pool_hw + g.poff[l] + q;
+#pragma unroll
+        for (int u = 0; u < kChunk; u++) v[u] = src[(size_t)u * g.pool_hw];
+    }
+    u16x8_t hi[2], lo[2];
+#pragma unroll
+    for (int u = 0; u < kChunk; u++) {
+        const unsigned pk = split_bf16(v[u]);
+        hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
+        lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+    }
+    const size_t plane = (size_t)g.C * g.Ttot;
+    unsigned short* o = out + (size_t)s * 2 * plane + ((size_t)k * g.Ttot + t) * kChunk;
+    *reinterpret_cast<u16x8_t*>(o) = hi[0];
+    *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
+    *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
+    *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+}
+
+struct alignas(16) SplitSmem {
+    union {
+        struct {
+            unsigned short A[2][2][kSrcTile][kRowU];  // [stage][hi/lo][source][k]
+            unsigned short B[2][2][kTgtTile][kRowU];  // [stage][hi/lo][target][k]
+        } st;
+        float T[kTgtTile][kTStride];  // [target][source] of one 64-source half
+    } u;
+    int org[kSrcTile][2];  // floor_clamped(x), floor_clamped(y) of each source
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Grid: n_edges * mtiles * ntiles workgroups of 256 threads (target tile
+// fastest). Waves form a 2x2 grid: wave (wm, wn) owns sources wm*64..+63 and
+// targets wn*128..+127 of the tile, eight 32x32 accumulator blocks.
+__global__ __launch_bounds__(256, 2) void k_corr_split_win(
+    const unsigned short* __restrict__ feat, EdgeSlots es, const float* __restrict__ coords,
+    float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles) {
+    __shared__ SplitSmem sm;
+    const int tpe = mtiles * ntiles;
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int e = bid / tpe;
+    const int r = bid - e * tpe;
+    const int mt = r / ntiles, nt = r - mt * ntiles;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int HW = g.HW, Ttot = g.Ttot;
+    const int p0 = mt * kSrcTile, t0 = nt * kTgtTile;
+    const size_t plane = (size_t)g.C * Ttot;
+    const unsigned short* fa = feat + (size_t)es.si[e] * 2 * plane;
+    const unsigned short* fb = feat + (size_t)es.sj[e] * 2 * plane;
+
+    if (tid < kSrcTile) {
+        const int p = p0 + tid;
+        int fx = -(1 << 20), fy = -(1 << 20);  // matches no cell
+        if (p < HW) {
+            const float* cc = coords + (size_t)e * 2 * HW;
+            fx = floor_clamped(cc[p]);
+            fy = floor_clamped(cc[HW + p]);
+        }
+        sm.org[tid][0] = fx;
+        sm.org[tid][1] = fy;
+    }
+
+    // staging: thread -> row tid/2 (and 128 + tid/2 for targets), 8-value half
+    // tid%2 of the 16-channel row; consecutive threads read consecutive 16-byte
+    // pieces. Rows past the source/target range read a clamped in-range row:
+    // an MFMA output D[i][j] only combines row i of A with column j of B, so
+    // such rows only reach accumulator cells that are never read.
+    const int hr = tid >> 1, hh = (tid & 1) * 8;
+    const unsigned short* ga = fa + (size_t)std::min(p0 + hr, HW - 1) * kChunk + hh;
+    const unsigned short* gb0 = fb + (size_t)std::min(t0 + hr, Ttot - 1) * kChunk + hh;
+    const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
+    const size_t kstep = (size_t)Ttot * kChunk;
+    u16x8_t ra[2], rb[4];
+    auto gload = [&](int k) {
+        const size_t o = (size_t)k * kstep;
+        ra[0] = *reinterpret_cast<const u16x8_t*>(ga + o);
+        ra[1] = *reinterpret_cast<const u16x8_t*>(ga + plane + o);
+        rb[0] = *reinterpret_cast<const u16x8_t*>(gb0 + o);
+        rb[1] = *reinterpret_cast<const u16x8_t*>(gb1 + o);
+        rb[2] = *reinterpret_cast<const u16x8_t*>(gb0 + plane + o);
+        rb[3] = *reinterpret_cast<const u16x8_t*>(gb1 + plane + o);
+    };
+    auto lstore = [&](int st) {
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.A[st][0][hr][hh]) = ra[0];
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.A[st][1][hr][hh]) = ra[1];
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][0][hr][hh]) = rb[0];
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][0][128 + hr][hh]) = rb[1];
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][1][hr][hh]) = rb[2];
+        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][1][128 + hr][hh]) = rb[3];
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) acc[sb][tb] = (f32x16){0};
+    // MFMA operand layout: lane l holds row l%32, k = 8*(l/32)..+7
+    const int orow = lane & 31, okk = (lane >> 5) * 8;
+    auto compute = [&](int st) {
+        u16x8_t ah[2], al[2], bh[4], bl[4];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            const int row = wm * 64 + sb * 32 + orow;
+            ah[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][0][row][okk]);
+            al[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][1][row][okk]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            const int row = wn * 128 + tb * 32 + orow;
+            bh[tb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][0][row][okk]);
+            bl[tb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][1][row][okk]);
+        }
+        // small cross terms first, then hi.hi; eight independent accumulators
+        // between dependent MFMAs
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(al[sb], bh[tb], acc[sb][tb]);
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(ah[sb], bl[tb], acc[sb][tb]);
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(ah[sb], bh[tb], acc[sb][tb]);
+    };
+
+    const int nk = g.C / kChunk;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int k = 0; k < nk; k++) {
+        if (k + 1 < nk) gload(k + 1);
+        compute(k & 1);
+        if (k + 1 < nk) lstore((k + 1) & 1);
+        __syncthreads();
+    }
+
+    // ---- window extraction ----
+    // rows of level l inside this tile: [lr0[l], lr1[l]] (empty: lr0 > lr1)
+    int lr0[kMaxLevels], lr1[kMaxLevels];
+#pragma unroll
+    for (int l = 0; l < kMaxLevels; l++) {
+        lr0[l] = 1 << 30;
+        lr1[l] = -(1 << 30);
+        if (l < g.levels) {
+            const int a = std::max(t0, g.off[l]) - g.off[l];
+            const int b = std::min(t0 + kTgtTile, g.off[l] + g.h[l] * g.w[l]) - 1 - g.off[l];
+            if (a <= b) {
+                lr0[l] = a / g.w[l];
+                lr1[l] = b / g.w[l];
+            }
+        }
+    }
+    // accumulator layout of the 32x32 MFMA: lane l, register v holds
+    // D[i][j] with j = l % 32 (target) and i = 8*(v/4) + 4*(l/32) + v%4 (source)
+    const int khalf = lane >> 5;
+    // lane = window cell (cx, cy); its offset from the window origin in the
+    // level's row-major target order
+    const int cx = lane & 7, cy = lane >> 3;
+    int lanec[kMaxLevels];
+#pragma unroll
+    for (int l = 0; l < kMaxLevels; l++) lanec[l] = cy * g.w[l] + cx;
+    float* wbase = win + (size_t)(slot0 + e) * HW * (kMaxLevels * kWinCells) + lane;
+#pragma unroll
+    for (int sb = 0; sb < 2; sb++) {
+        if (sb) __syncthreads();  // the first half's cells have all been read
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++) {
+                const int t = wn * 128 + tb * 32 + orow;
+                const int s = wm * 32 + gq * 8 + khalf * 4;
+                *reinterpret_cast<float4*>(&sm.u.T[t][s]) =
+                    make_float4(acc[sb][tb][4 * gq], acc[sb][tb][4 * gq + 1],
+                                acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
+            }
+        __syncthreads();
+        // this wave's 16 columns of T (sources): origins fetched once, one per
+        // lane, then broadcast with readlane; each (source, level) is one
+        // branch-free masked read of T and store of the window row block
+        const int li = wave * 16 + (lane & 15);
+        const int lsrc = (li >> 5) * 64 + sb * 32 + (li & 31);
+        const int ofx = sm.org[lsrc][0], ofy = sm.org[lsrc][1];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int sl = wave * 16 + i;                          // column of T
+            const int src = (sl >> 5) * 64 + sb * 32 + (sl & 31);  // source in the tile
+            const int p = p0 + src;
+            const int fx = __builtin_amdgcn_readlane(ofx, i);
+            const int fy = __builtin_amdgcn_readlane(ofy, i);
+            float* wp = wbase + (size_t)std::min(p, HW - 1) * (kMaxLevels * kWinCells);
+#pragma unroll
+            for (int l = 0; l < kMaxLevels; l++) {
+                if (lr0[l] > lr1[l]) continue;  // level not in this tile
+                const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
+                const int xs = ox + cx, ys = oy + cy;
+                // wraps harmlessly for far origins (then xs/ys are out of range)
+                const unsigned tl = (unsigned)(g.off[l] - t0) +
+                                    (unsigned)oy * (unsigned)g.w[l] + (unsigned)ox +
+                                    (unsigned)lanec[l];
+                const bool ok = p < HW && (unsigned)xs < (unsigned)g.w[l] &&
+                                (unsigned)ys < (unsigned)g.h[l] && tl < (unsigned)kTgtTile;
+                const float v = sm.u.T[ok ? tl : 0][sl];
+                if (ok) wp[l * kWinCells] = alpha * v;
+            }
+        }
+    }
+}
+
+Geom make_geom(const slk_ctx* ctx) {
+    Geom g{};
+    g.HW = ctx->HW;
+    g.C = ctx->C;
+    g.levels = ctx->levels;
+    int t = 0, pt = 0;
+    for (int l = 0; l < kMaxLevels; l++) {
+        g.h[l] = l < ctx->levels ? ctx->lh[l] : 0;
+        g.w[l] = l < ctx->levels ? ctx->lw[l] : 1;
+        g.off[l] = t;
+        g.poff[l] = l >= 1 ? pt : 0;
+        if (l < ctx->levels) {
+            t += g.h[l] * g.w[l];
+            if (l >= 1) pt += g.h[l] * g.w[l];
+        }
+    }
+    g.Ttot = t;
+    g.pool_hw = pt;
+    return g;
+}
+
+template <typename Tin>
+int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
+               int slot_lo, int nslots, int trows, bool pooled, hipStream_t stream) {
+    if (nslots <= 0) return SLK_OK;
+    float* pool = ctx->split_pool.as<float>();
+    if (pooled) {
+        for (int l = 1; l < g.levels; l++) {
+            const int n = g.h[l] * g.w[l];
+            hipLaunchKernelGGL(k_feat_pool<Tin>, dim3((n + 255) / 256, g.C, nslots), dim3(256),
+                               0, stream, fm, fstride, sf, slot_lo, pool, g, l);
+        }
+    }
+    hipLaunchKernelGGL(k_feat_split<Tin>, dim3((trows + 255) / 256, g.C / kChunk, nslots),
+                       dim3(256), 0, stream, fm, fstride, sf, slot_lo, pool,
+                       ctx->split_feat.as<unsigned short>(), g, trows);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+template <typename Tin>
+int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
+                  const int* jj_host, const int* ii_dev, const int* jj_dev, int n,
+                  const float* coords, float* win, int slot0, hipStream_t stream) {
+    const Geom g = make_geom(ctx);
+    SlotFrames sf{};
+    EdgeSlots es{};
+    {
+        ProfScope ps(ctx, "corr_feat_prep", stream);
+        if (ii_host) {
+            int ns = 0;
+            auto slot_of = [&](int f) {
+                for (int s = 0; s < ns; s++)
+                    if (sf.f[s] == f) return s;
+                sf.f[ns] = f;
+                return ns++;
+            };
+            for (int e = 0; e < n; e++) {
+                es.si[e] = slot_of(ii_host[e]);
+                es.sj[e] = slot_of(jj_host[e]);
+            }
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, g.Ttot, true, stream));
+        } else {
+            sf.da = ii_dev;
+            sf.db = jj_dev;
+            sf.nb = n;
+            for (int e = 0; e < n; e++) {
+                es.si[e] = e;
+                es.sj[e] = n + e;
+            }
+            // sources only need level 0; targets need every level
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, g.HW, false, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, g.Ttot, true, stream));
+        }
+    }
+    const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
+    const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
+    const long total = (long)n * mtiles * ntiles;
+    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
+    {
+        ProfScope ps(ctx, "corr_window", stream);
+        hipLaunchKernelGGL(k_corr_split_win, dim3((unsigned)total), dim3(256), 0, stream,
+                           ctx->split_feat.as<unsigned short>(), es, coords, win, slot0, g,
+                           ctx->alpha, mtiles, ntiles);
+    }
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+}  // namespace
+
+bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
+
+int corr_split_alloc(slk_ctx* ctx) {
+    if (!corr_split_supported(ctx)) return SLK_OK;
+    const Geom g = make_geom(ctx);
+    const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
+    SLK_TRY(ctx->split_feat.ensure(slots * 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short)));
+    SLK_TRY(ctx->split_pool.ensure(slots * (size_t)g.C * std::max(g.pool_hw, 1) * sizeof(float)));
+    return SLK_OK;
+}
+
+int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
+                       const int* ii_host, const int* jj_host, const int* ii_dev,
+                       const int* jj_dev, int n, const float* coords, float* win, int slot0,
+                       hipStream_t stream) {
+    if (n <= 0) return SLK_OK;
+    if (n > kMaxEdgesPerLaunch || n > ctx->max_batch)
+        return fail(SLK_E_ARG, "corr_split_windows: too many edges for one launch");
+    if (dtype == SLK_F32)
+        return split_windows(ctx, static_cast<const float*>(fmaps), fstride, ii_host, jj_host,
+                             ii_dev, jj_dev, n, coords, win, slot0, stream);
+    return split_windows(ctx, static_cast<const _Float16*>(fmaps), fstride, ii_host, jj_host,
+                         ii_dev, jj_dev, n, coords, win, slot0, stream);
+}
+
+}  // namespace slk

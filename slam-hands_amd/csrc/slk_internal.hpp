@@ -73,6 +73,9 @@ struct slk_ctx {
     int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
     // batched-path scratch: 8x8 lookup windows [max_batch][HW][4 levels][64]
     slk::DevBuf batch_win;
+    // batched-path operands: bf16 hi/lo split of every level's features per
+    // frame slot, and the fp32 pooled features they are split from
+    slk::DevBuf split_feat, split_pool;
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
     bool single_built = false;
@@ -113,6 +116,13 @@ struct ProfScope {
 namespace slk {
 // corr.hip
 int corr_alloc(slk_ctx* ctx);
+// corr_split.hip
+bool corr_split_supported(const slk_ctx* ctx);
+int corr_split_alloc(slk_ctx* ctx);
+int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
+                       const int* ii_host, const int* jj_host, const int* ii_dev,
+                       const int* jj_dev, int n, const float* coords, float* win, int slot0,
+                       hipStream_t stream);
 // ba.hip
 int ba_create(slk_ctx* ctx);
 void ba_destroy(slk_ctx* ctx);

@@ -174,6 +174,55 @@ def _lookup_rows(pyr, coords):
     return out
 
 
+def test_window_integer_coded_is_bitwise(slk):
+    """Batched path with small-integer features: products, partial sums and the
+    2x2 means of features and of the volume are all exact, so with coordinates
+    that are multiples of 8 (integer at every level) all 196 channels match the
+    oracle bitwise, and with integer coordinates the level-0 channels do."""
+    announce("corr window integer-coded bitwise")
+    h, w, n = 48, 64, 6
+    rng = np.random.default_rng(11)
+    f = rng.integers(-3, 4, size=(n, 128, h, w)).astype(np.float32)
+    ii, jj = wl.cyclic_edges(n)
+    B = len(ii)
+    g = wl.grid_coords(h, w)[None]
+    c1 = (g + rng.integers(-6, 7, size=(B, 2, h * w))).astype(np.float32)
+    c8 = (g // 8 * 8 + 8 * rng.integers(-1, 2, size=(B, 2, h * w))).astype(np.float32)
+    ctx = slk.Context(h, w, C=128, max_batch=B, corr_scale=1.0 / 16.0)
+    fd = slk.DeviceArray.from_host(f)
+    outs = []
+    for c in (c1, c8):
+        cd = slk.DeviceArray.from_host(c)
+        out = slk.DeviceArray((B, 196, h * w))
+        ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, out)
+        slk.hip().sync()
+        outs.append(out.to_host())
+    ctx.close()
+    ref1 = orc.corr_batch(f, ii, jj, c1, 1.0 / 16.0)
+    np.testing.assert_array_equal(outs[0][:, :49], ref1[:, :49])
+    ref8 = orc.corr_batch(f, ii, jj, c8, 1.0 / 16.0)
+    np.testing.assert_array_equal(outs[1], ref8)
+
+
+def test_window_fp16_features(slk):
+    """fp16 feature maps (the reference's fmap storage) through the batched path."""
+    h, w, n = 24, 32, 5
+    f = wl.frames(n, C=128, h=h, w=w, seed=12).astype(np.float16)
+    ii, jj = wl.cyclic_edges(n)
+    B = len(ii)
+    coords = wl.flow_coords(B, h, w, seed=13)
+    ctx = slk.Context(h, w, C=128, max_batch=B, corr_scale=1.0 / 16.0)
+    fd = slk.DeviceArray.from_host(f)
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((B, 196, h * w))
+    ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, out, dtype=slk.SLK_F16)
+    slk.hip().sync()
+    got = out.to_host()
+    ctx.close()
+    ref = orc.corr_batch(f.astype(np.float32), ii, jj, coords, 1.0 / 16.0)
+    assert_close_rel(got, ref, what="fp16 window")
+
+
 def test_device_indices_and_chunking(slk):
     """Device-resident ii/jj, and B above max_batch (processed in chunks)."""
     h, w = 24, 32
