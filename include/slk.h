@@ -42,12 +42,14 @@ typedef enum {
 
 typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
 
-/* Contraction used for fp32 features (fp16 features always use exact fp16
- * products with fp32 accumulation, the arithmetic of the reference's
- * cublasGemmEx on its fp16 fmaps, main.cu:1508-1515):
+/* Contraction used for fp32 features:
  *  SLK_PREC_BF16X3 (default) -- hi/lo bf16 split, three bf16 MFMA passes,
- *                               ~1e-5 relative to the row scale;
- *  SLK_PREC_FP32             -- fp32 MFMA (v_mfma_f32_32x32x2f32). */
+ *                               ~3e-5 relative to the row scale;
+ *  SLK_PREC_FP32             -- fp32 MFMA (v_mfma_f32_32x32x2f32).
+ * fp16 features are exact in either form: the batched path splits them like
+ * fp32 (hi + lo represents every fp16 value), the single-edge path uses fp16
+ * MFMA products with fp32 accumulation (the arithmetic of the reference's
+ * cublasGemmEx on its fp16 fmaps, main.cu:1508-1515). */
 typedef enum { SLK_PREC_BF16X3 = 0, SLK_PREC_FP32 = 1 } slk_corr_precision;
 
 /* ---------------------------------------------------------------- context */
@@ -55,8 +57,10 @@ typedef enum { SLK_PREC_BF16X3 = 0, SLK_PREC_FP32 = 1 } slk_corr_precision;
 /* Creates a context on the current HIP device for h x w feature maps with C
  * channels. corr_scale is alpha of the correlation GEMM (1/16 in the
  * reference: cublasGemmEx alpha, cuda_slam/main.cu:1506,1572). Allocates the
- * batched pyramid scratch for max_batch edges ([B,hw,hw] + levels,
- * main.cu:1413-1418) and the single-edge volume (main.cu:1400-1405).
+ * batched scratch for max_batch edges (the reference's [B,hw,hw] volumes +
+ * levels, main.cu:1413-1418, become 8x8 lookup windows per pixel and level
+ * plus the split features of the frames in flight) and the single-edge volume
+ * and pyramid (main.cu:1400-1405). h, w <= 65536 and h*w <= 2^24.
  * Replaces CorrBlock::init (cuda_slam/corr.cuh:75) and
  * BundleAdjustment::init(h, w) (cuda_slam/ba.cuh:408). levels <= 4, radius == 3. */
 int slk_create(slk_ctx** ctx, int h, int w, int C, int max_batch, int levels,
