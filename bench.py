@@ -35,9 +35,10 @@ import numpy as np  # noqa: E402
 METRIC = "corr edges/sec + BA iters/sec (48-edge window, 1 MI355X); % roofline"
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (matrix and vector)
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
-# HBM bytes per corr_window launch from rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE
-# (profiles/corr_window_pmc_traffic.md); None until measured
-TRAFFIC_BYTES = None
+# HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
+# (profiles/corr_window48_pmc_traffic.md)
+TRAFFIC_BYTES = 300988286
 PEAK_HBM_GBS = 8000.0
 
 
@@ -47,6 +48,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the run, one device-to-device copy of MIB MiB (the plain "
+                         "copy kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--cpu-edges", type=int, default=48,
                     help="edges of the window the CPU baseline runs (bounded sample)")
     return ap.parse_args()
@@ -195,6 +199,17 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, args.cpu_edges)
     print(json.dumps(out), flush=True)
+    if args.calibrate_copy > 0:
+        nbytes = args.calibrate_copy << 20
+        src, dst = H.malloc(nbytes), H.malloc(nbytes)
+        H.memset(src, 1, nbytes)
+        H.sync()
+        H.dtod(dst, src, nbytes)
+        H.sync()
+        H.free(src)
+        H.free(dst)
+        print(f"bench.py: copy calibration {nbytes} bytes device-to-device", file=sys.stderr,
+              flush=True)
 
 
 def cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, nedges):

@@ -174,6 +174,9 @@ class Hip:
     def memset(self, p, value, nbytes):
         self.ok(self.h.hipMemset(P(p), value, nbytes), "hipMemset")
 
+    def dtod(self, dst, src, nbytes):
+        self.ok(self.h.hipMemcpy(P(dst), P(src), int(nbytes), self.D2D), "hipMemcpy D2D")
+
     def sync(self):
         self.ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
 
