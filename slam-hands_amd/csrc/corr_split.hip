@@ -43,7 +43,7 @@ namespace {
 constexpr int kSrcTile = 128;  // sources per workgroup
 constexpr int kTgtTile = 256;  // targets per workgroup
 constexpr int kChunk = 16;     // channels per LDS stage
-constexpr int kRowU = 24;      // u16 per LDS operand row (16 used + 8 pad)
+constexpr int kStages = 3;     // LDS stages: chunk k+2 streams in while chunk k is used
 constexpr int kTStride = 68;   // floats per transposed-tile row (64 sources + 4 pad)
 constexpr int kMaxSlots = 2 * kMaxEdgesPerLaunch;
 
@@ -157,13 +157,24 @@ __global__ __launch_bounds__(256) void k_feat_split(const Tin* __restrict__ fm, 
 struct alignas(16) SplitSmem {
     union {
         struct {
-            unsigned short A[2][2][kSrcTile][kRowU];  // [stage][hi/lo][source][k]
-            unsigned short B[2][2][kTgtTile][kRowU];  // [stage][hi/lo][target][k]
+            // [stage][hi/lo][row * 16 + swizzled k]: 32-byte rows, the two
+            // 16-byte halves of row r swapped when bit 2 of r is set, so that
+            // both the staging writes (a pair of lanes per row) and the MFMA
+            // operand reads (8 rows per 128-byte phase) touch 32 distinct banks
+            unsigned short A[kStages][2][kSrcTile * kChunk];
+            unsigned short B[kStages][2][kTgtTile * kChunk];
         } st;
         float T[kTgtTile][kTStride];  // [target][source] of one 64-source half
     } u;
     int org[kSrcTile][2];  // floor_clamped(x), floor_clamped(y) of each source
 };
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8): vmcnt(6) lgkmcnt(0), and vmcnt(0) lgkmcnt(0)
+constexpr int kWaitVm6Lgkm0 = 0x0076;
+constexpr int kWaitVm0Lgkm0 = 0x0070;
 
 __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -191,45 +202,31 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* fa = feat + (size_t)es.si[e] * 2 * plane;
     const unsigned short* fb = feat + (size_t)es.sj[e] * 2 * plane;
 
-    if (tid < kSrcTile) {
-        const int p = p0 + tid;
-        int fx = -(1 << 20), fy = -(1 << 20);  // matches no cell
-        if (p < HW) {
-            const float* cc = coords + (size_t)e * 2 * HW;
-            fx = floor_clamped(cc[p]);
-            fy = floor_clamped(cc[HW + p]);
-        }
-        sm.org[tid][0] = fx;
-        sm.org[tid][1] = fy;
-    }
-
-    // staging: thread -> row tid/2 (and 128 + tid/2 for targets), 8-value half
-    // tid%2 of the 16-channel row; consecutive threads read consecutive 16-byte
-    // pieces. Rows past the source/target range read a clamped in-range row:
-    // an MFMA output D[i][j] only combines row i of A with column j of B, so
-    // such rows only reach accumulator cells that are never read.
-    const int hr = tid >> 1, hh = (tid & 1) * 8;
+    // Staging by direct-to-LDS loads (global_load_lds_dwordx4): lane l of wave
+    // w writes bytes 16*(64w + l) of a 4 KB region, i.e. row tid/2, physical
+    // half tid%2 of the 32-byte-row layout, so each thread loads the logical
+    // half that lands there. Rows past the source/target range read a clamped
+    // in-range row: an MFMA output D[i][j] only combines row i of A with
+    // column j of B, so such rows only reach accumulator cells never read.
+    const int hr = tid >> 1;
+    const int hh = ((tid & 1) ^ ((hr >> 2) & 1)) * 8;  // rows hr and 128 + hr share bit 2
     const unsigned short* ga = fa + (size_t)std::min(p0 + hr, HW - 1) * kChunk + hh;
     const unsigned short* gb0 = fb + (size_t)std::min(t0 + hr, Ttot - 1) * kChunk + hh;
     const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
     const size_t kstep = (size_t)Ttot * kChunk;
-    u16x8_t ra[2], rb[4];
-    auto gload = [&](int k) {
+    const int wdst = wave * 512;  // this wave's 1 KB of a 4 KB region, in u16
+    auto issue = [&](int k, int st) {
         const size_t o = (size_t)k * kstep;
-        ra[0] = *reinterpret_cast<const u16x8_t*>(ga + o);
-        ra[1] = *reinterpret_cast<const u16x8_t*>(ga + plane + o);
-        rb[0] = *reinterpret_cast<const u16x8_t*>(gb0 + o);
-        rb[1] = *reinterpret_cast<const u16x8_t*>(gb1 + o);
-        rb[2] = *reinterpret_cast<const u16x8_t*>(gb0 + plane + o);
-        rb[3] = *reinterpret_cast<const u16x8_t*>(gb1 + plane + o);
-    };
-    auto lstore = [&](int st) {
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.A[st][0][hr][hh]) = ra[0];
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.A[st][1][hr][hh]) = ra[1];
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][0][hr][hh]) = rb[0];
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][0][128 + hr][hh]) = rb[1];
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][1][hr][hh]) = rb[2];
-        *reinterpret_cast<u16x8_t*>(&sm.u.st.B[st][1][128 + hr][hh]) = rb[3];
+        __builtin_amdgcn_global_load_lds(ga + o, (lds_ptr)&sm.u.st.A[st][0][wdst], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ga + plane + o, (lds_ptr)&sm.u.st.A[st][1][wdst], 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(gb0 + o, (lds_ptr)&sm.u.st.B[st][0][wdst], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(gb1 + o, (lds_ptr)&sm.u.st.B[st][0][2048 + wdst], 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(gb0 + plane + o, (lds_ptr)&sm.u.st.B[st][1][wdst], 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(gb1 + plane + o,
+                                         (lds_ptr)&sm.u.st.B[st][1][2048 + wdst], 16, 0, 0);
     };
 
     f32x16 acc[2][4];
@@ -237,48 +234,79 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     for (int sb = 0; sb < 2; sb++)
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) acc[sb][tb] = (f32x16){0};
-    // MFMA operand layout: lane l holds row l%32, k = 8*(l/32)..+7
-    const int orow = lane & 31, okk = (lane >> 5) * 8;
+    // MFMA operand layout: lane l holds row l%32, k = 8*(l/32)..+7; every
+    // operand block starts at a multiple of 32 rows, so the swizzle bit of the
+    // lane's row is bit 2 of l%32
+    const int orow = lane & 31;
+    const int ooff = orow * kChunk + ((((lane >> 5) ^ ((orow >> 2) & 1))) * 8);
     auto compute = [&](int st) {
-        u16x8_t ah[2], al[2], bh[4], bl[4];
+        u16x8_t ah[2], al[2];
 #pragma unroll
         for (int sb = 0; sb < 2; sb++) {
-            const int row = wm * 64 + sb * 32 + orow;
-            ah[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][0][row][okk]);
-            al[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][1][row][okk]);
+            const int o = (wm * 64 + sb * 32) * kChunk + ooff;
+            ah[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][0][o]);
+            al[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][1][o]);
         }
+        // target blocks in pairs: only two blocks' B fragments live at a time,
+        // four independent accumulators between dependent MFMAs; the small
+        // cross terms are added before hi.hi
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) {
-            const int row = wn * 128 + tb * 32 + orow;
-            bh[tb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][0][row][okk]);
-            bl[tb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][1][row][okk]);
+        for (int tp = 0; tp < 4; tp += 2) {
+            u16x8_t bh[2], bl[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int o = (wn * 128 + (tp + u) * 32) * kChunk + ooff;
+                bh[u] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][0][o]);
+                bl[u] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][1][o]);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+                    acc[sb][tp + u] = mfma_bf16(al[sb], bh[u], acc[sb][tp + u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+                    acc[sb][tp + u] = mfma_bf16(ah[sb], bl[u], acc[sb][tp + u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+                    acc[sb][tp + u] = mfma_bf16(ah[sb], bh[u], acc[sb][tp + u]);
         }
-        // small cross terms first, then hi.hi; eight independent accumulators
-        // between dependent MFMAs
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(al[sb], bh[tb], acc[sb][tb]);
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(ah[sb], bl[tb], acc[sb][tb]);
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) acc[sb][tb] = mfma_bf16(ah[sb], bh[tb], acc[sb][tb]);
     };
 
+    // Pipeline: at step k the loads of chunks k and k+1 are in flight; wait
+    // for this thread's chunk k (6 loads) and for every wave at the barrier --
+    // after which chunk k is in LDS and stage (k+2)%3, last read at step k-1,
+    // is free for chunk k+2. The wait and barrier are explicit because a
+    // workgroup fence would also wait for chunk k+1.
     const int nk = g.C / kChunk;
-    gload(0);
-    lstore(0);
-    __syncthreads();
+    issue(0, 0);
+    // coordinates of the tile's sources (one per thread of the first 128),
+    // in flight with the first chunk; written to LDS after the main loop
+    const int pc = std::min(p0 + (tid & (kSrcTile - 1)), HW - 1);
+    const float* cc = coords + (size_t)e * 2 * HW;
+    const float cxv = cc[pc], cyv = cc[HW + pc];
+    if (nk > 1) issue(1, 1);
     for (int k = 0; k < nk; k++) {
-        if (k + 1 < nk) gload(k + 1);
-        compute(k & 1);
-        if (k + 1 < nk) lstore((k + 1) & 1);
-        __syncthreads();
+        if (k + 1 < nk)
+            __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);
+        else
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
+        compute(k % kStages);
     }
+    if (tid < kSrcTile) {
+        const bool in = p0 + tid < HW;
+        sm.org[tid][0] = in ? floor_clamped(cxv) : -(1 << 20);  // -2^20: matches no cell
+        sm.org[tid][1] = in ? floor_clamped(cyv) : -(1 << 20);
+    }
+    __syncthreads();  // every wave is done with the stages before T overwrites them
 
     // ---- window extraction ----
     // rows of level l inside this tile: [lr0[l], lr1[l]] (empty: lr0 > lr1)
@@ -321,32 +349,38 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             }
         __syncthreads();
         // this wave's 16 columns of T (sources): origins fetched once, one per
-        // lane, then broadcast with readlane; each (source, level) is one
-        // branch-free masked read of T and store of the window row block
+        // lane, then broadcast with readlane. Per level present in the tile,
+        // the 16 masked reads of T are issued together, then the 16 masked
+        // stores of 64 consecutive window floats.
         const int li = wave * 16 + (lane & 15);
         const int lsrc = (li >> 5) * 64 + sb * 32 + (li & 31);
         const int ofx = sm.org[lsrc][0], ofy = sm.org[lsrc][1];
+        const int srcw = (wave >> 1) * 64 + sb * 32 + (wave & 1) * 16;  // source of i = 0
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int sl = wave * 16 + i;                          // column of T
-            const int src = (sl >> 5) * 64 + sb * 32 + (sl & 31);  // source in the tile
-            const int p = p0 + src;
-            const int fx = __builtin_amdgcn_readlane(ofx, i);
-            const int fy = __builtin_amdgcn_readlane(ofy, i);
-            float* wp = wbase + (size_t)std::min(p, HW - 1) * (kMaxLevels * kWinCells);
+        for (int l = 0; l < kMaxLevels; l++) {
+            if (lr0[l] > lr1[l]) continue;  // level not in this tile
+            const int wl = g.w[l], hl = g.h[l];
+            const unsigned base = (unsigned)(g.off[l] - t0) + (unsigned)lanec[l];
+            float v[16];
+            unsigned okm = 0;  // bit i: lane's cell of item i is stored
 #pragma unroll
-            for (int l = 0; l < kMaxLevels; l++) {
-                if (lr0[l] > lr1[l]) continue;  // level not in this tile
+            for (int i = 0; i < 16; i++) {
+                const int fx = __builtin_amdgcn_readlane(ofx, i);
+                const int fy = __builtin_amdgcn_readlane(ofy, i);
                 const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
                 const int xs = ox + cx, ys = oy + cy;
                 // wraps harmlessly for far origins (then xs/ys are out of range)
-                const unsigned tl = (unsigned)(g.off[l] - t0) +
-                                    (unsigned)oy * (unsigned)g.w[l] + (unsigned)ox +
-                                    (unsigned)lanec[l];
-                const bool ok = p < HW && (unsigned)xs < (unsigned)g.w[l] &&
-                                (unsigned)ys < (unsigned)g.h[l] && tl < (unsigned)kTgtTile;
-                const float v = sm.u.T[ok ? tl : 0][sl];
-                if (ok) wp[l * kWinCells] = alpha * v;
+                const unsigned tl = base + (unsigned)oy * (unsigned)wl + (unsigned)ox;
+                const bool ok = p0 + srcw + i < HW && (unsigned)xs < (unsigned)wl &&
+                                (unsigned)ys < (unsigned)hl && tl < (unsigned)kTgtTile;
+                v[i] = sm.u.T[ok ? tl : 0][wave * 16 + i];
+                okm |= (unsigned)ok << i;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int p = std::min(p0 + srcw + i, HW - 1);
+                if (okm & (1u << i))
+                    wbase[(size_t)p * (kMaxLevels * kWinCells) + l * kWinCells] = alpha * v[i];
             }
         }
     }
