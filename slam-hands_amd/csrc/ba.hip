@@ -623,6 +623,107 @@ __global__ __launch_bounds__(1024) void k_ba_solve_global(SolveArgs A) {
     finish_solve(A, b, ok);
 }
 
+// One wavefront, n = N <= 64 (the frontend's 6P x 6P systems, P <= 10): lane i
+// holds row i of S in registers and becomes row i of L. Column j: the pivot
+// is read from lane j, lanes below scale by 1/L_jj, the column goes through a
+// 64-entry LDS buffer and every lane subtracts L_ij * L_kj from its entries
+// k > j. Entries above a lane's diagonal receive the same updates unused (no
+// predicate). The forward solve broadcasts z_k by readlane; the backward solve
+// reads L by columns from an LDS copy of the rows. No barrier anywhere: a
+// wave's LDS accesses are performed in program order. Same pivot test as the
+// reference (every pivot > 0 before its sqrt, ba.cuh:422).
+template <int N>
+__global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
+    __shared__ __attribute__((aligned(16))) double col[64];
+    __shared__ double Lrow[N * (N + 1)];  // L rows, leading dimension N + 1
+    const int lane = threadIdx.x;
+    const int li = lane < N ? lane : N - 1;
+    double r[N];
+#pragma unroll
+    for (int m = 0; m < N; m++) r[m] = A.S_dbg[(size_t)li * N + m];
+    bool ok = true;
+    double invd = 0.0;  // 1 / L_ii of this lane's row
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        const double d = bcast(r[j], j);
+        ok = ok && (d > 0.0);
+        const double ljj = sqrt(d);
+        const double inv = 1.0 / ljj;
+        r[j] = lane == j ? ljj : r[j] * inv;
+        if (lane == j) invd = inv;
+        col[lane] = r[j];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = j + 1; k < N; k++) r[k] -= r[j] * col[k];
+        __builtin_amdgcn_wave_barrier();
+    }
+    // forward: L z = b
+    double acc = A.b_dbg[li], z = 0.0;
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        const double zk = bcast(acc * invd, k);
+        if (lane == k) z = zk;
+        acc -= r[k] * zk;
+    }
+    // backward: L^T x = z, column lane of L read from the row copy
+#pragma unroll
+    for (int m = 0; m < N; m++)
+        if (lane < N && m <= lane) Lrow[lane * (N + 1) + m] = r[m];
+    __builtin_amdgcn_wave_barrier();
+    acc = z;
+    double x = 0.0;
+#pragma unroll
+    for (int k = N - 1; k >= 0; k--) {
+        const double xk = bcast(acc * invd, k);
+        if (lane == k) x = xk;
+        if (lane < k) acc -= Lrow[k * (N + 1) + lane] * xk;
+    }
+    col[lane] = x;
+    __builtin_amdgcn_wave_barrier();
+    // finish_solve's outputs with the solution in col[]
+    if (lane == 0) {
+        A.flags[0] = ok ? 0 : 1;
+        if (!ok) A.flags[1] = 1;
+    }
+    if (lane < N) {
+        A.dx_dbg[lane] = ok ? x : 0.0;
+        A.dx[lane] = ok ? (float)x : 0.0f;
+    }
+    if (!ok) return;
+    // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
+    for (int k = A.t0 + lane; k < A.t1; k += 64) {
+        double t[3], q[4], xi[6], t1[3], q1[4];
+        load_pose(A.poses, k, t, q);
+        for (int m = 0; m < 6; m++) xi[m] = (double)(float)col[(k - A.t0) * 6 + m];
+        retr_se3(xi, t, q, t1, q1);
+        for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
+        for (int m = 0; m < 4; m++) A.poses[k * 7 + 3 + m] = (float)q1[m];
+    }
+}
+
+template <int P>
+void launch_solve_wave(const SolveArgs& A, hipStream_t stream) {
+    hipLaunchKernelGGL(k_ba_solve_wave<6 * P>, dim3(1), dim3(64), 0, stream, A);
+}
+
+// 1..kWaveP free poses take the wavefront solver
+constexpr int kWaveP = 10;
+bool solve_wave(int P, const SolveArgs& A, hipStream_t stream) {
+    switch (P) {
+        case 1: launch_solve_wave<1>(A, stream); return true;
+        case 2: launch_solve_wave<2>(A, stream); return true;
+        case 3: launch_solve_wave<3>(A, stream); return true;
+        case 4: launch_solve_wave<4>(A, stream); return true;
+        case 5: launch_solve_wave<5>(A, stream); return true;
+        case 6: launch_solve_wave<6>(A, stream); return true;
+        case 7: launch_solve_wave<7>(A, stream); return true;
+        case 8: launch_solve_wave<8>(A, stream); return true;
+        case 9: launch_solve_wave<9>(A, stream); return true;
+        case 10: launch_solve_wave<10>(A, stream); return true;
+        default: return false;
+    }
+}
+
 // ------------------------------------------------------ k_ba_backsub ----
 // EvT6x1 + accum + depth_update (ba.cuh:762-783) fused per keyframe pixel.
 __global__ __launch_bounds__(256) void k_ba_backsub(PlanDev plan, const double* __restrict__ E,
@@ -919,7 +1020,10 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         hipLaunchKernelGGL(k_ba_assemble, dim3((items + 255) / 256), dim3(256), 0, stream, A);
     }
     SLK_HIP(hipGetLastError());
-    if (s->n <= kSmallN) {
+    if (s->P <= kWaveP) {
+        ProfScope ps(ctx, "ba_solve", stream);
+        solve_wave(s->P, A, stream);
+    } else if (s->n <= kSmallN) {
         ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);
         const int threads = 256;
