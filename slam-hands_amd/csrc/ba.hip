@@ -16,12 +16,14 @@
 //                 exist.
 //   k_ba_schur    grid (pixel chunk, item): E_r1 Q E_r2^T for the upper pairs
 //                 of E rows sharing a keyframe, and E_r Q w per row.
-//   k_ba_assemble one thread per entry of S and b: sums the chunk partials of
-//                 the contributions listed for its 6x6 block (list built on
-//                 the host; no atomics, fixed order), then S_ii += ep + lm*S_ii.
-//   k_ba_solve_*  one workgroup: blocked fp64 Cholesky (S in LDS up to
-//                 90x90, else global), solve, dx rounded to fp32, retraction
-//                 of the poses [t0, t1).
+//   k_ba_assemble one workgroup per 6x6 block of S and per 6 entries of b:
+//                 sums the chunk partials of the contributions listed for the
+//                 block (list built on the host; no atomics, fixed order),
+//                 then S_ii += ep + lm*S_ii.
+//   k_ba_solve_*  fp64 Cholesky, solve, dx rounded to fp32, retraction of the
+//                 poses [t0, t1): one wavefront with S in registers up to 10
+//                 free poses, else one workgroup (blocked, S in LDS up to
+//                 90x90, else in global memory).
 //   k_ba_backsub  grid (pixel chunk, keyframe): dz = Q (w - E^T dx),
 //                 disps += dz.
 // Host work per iteration is limited to comparing the edge list with the
@@ -335,75 +337,81 @@ __device__ __forceinline__ int hs_index(int which, int r, int c) {
     return tri(6 + max(r, c), 6 + min(r, c));
 }
 
-// Sum of the n chunk partials p[0], p[stride], ... with four loads in flight
-// (fixed order: deterministic).
-__device__ __forceinline__ double sum_parts(const double* p, int n, int stride) {
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-    int c = 0;
-    for (; c + 4 <= n; c += 4) {
-        s0 += p[(size_t)c * stride];
-        s1 += p[(size_t)(c + 1) * stride];
-        s2 += p[(size_t)(c + 2) * stride];
-        s3 += p[(size_t)(c + 3) * stride];
-    }
-    for (; c < n; c++) s0 += p[(size_t)c * stride];
-    return (s0 + s1) + (s2 + s3);
+// One workgroup per 6x6 block (a, b) of S (P*P of them) and per 6-entry
+// segment of b (P more): S = sum of the listed Hessian blocks minus the Schur
+// pair blocks (ba.cuh:520-548, 722-742), then the LM damping
+// S_ii += ep + lm*S_ii after the Schur step (ba.cuh:749-750). Every
+// contribution is itself a sum of per-chunk partials; thread (slice, entry)
+// sums the chunks slice, slice + 7, ... of every contribution, and the seven
+// slices are added in a fixed order (deterministic, no atomics).
+constexpr int kAsmSlices = 7;  // 7 x 36 = 252 of the 256 threads
+
+__device__ __forceinline__ double slice_sum(const double* p, int nparts, int stride, int sl) {
+    double s = 0.0;
+    for (int c = sl; c < nparts; c += kAsmSlices) s += p[(size_t)c * stride];
+    return s;
 }
 
-// signed value of one contribution code to entry (r, c) of a block of S
-__device__ __forceinline__ double contrib(const SolveArgs& A, int cd, int r, int c) {
-    const int ty = code_type(cd), v = code_val(cd);
-    if (ty == 0)
-        return sum_parts(A.hpart + (size_t)(v >> 2) * A.nch * kNH + hs_index(v & 3, r, c), A.nch,
-                         kNH);
-    const int e36 = ty == 1 ? r * 6 + c : c * 6 + r;
-    return -sum_parts(A.spart + (size_t)v * A.nchS * 36 + e36, A.nchS, 36);
-}
-
-// One thread per entry of S (row-major n x n) and of b: S = sum of the listed
-// Hessian blocks minus the Schur pair blocks (ba.cuh:520-548, 722-742), then
-// the LM damping S_ii += ep + lm*S_ii after the Schur step (ba.cuh:749-750).
 __global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
+    __shared__ double red[kAsmSlices][36];
     const int n = A.n, P = A.P;
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < n * n) {
-        const int row = t / n, col = t - (t / n) * n;
-        const int a = row / 6, r = row - (row / 6) * 6;
-        const int bb = col / 6, c = col - (col / 6) * 6;
-        const int blk = A.plan.blkmap[a * P + bb];
-        double s = 0.0;
-        if (blk >= 0) {
-            // contributions in list order, four loads in flight at a time
-            const int q0 = A.plan.sblk_ptr[blk], q1 = A.plan.sblk_ptr[blk + 1];
-            int q = q0;
-            for (; q + 4 <= q1; q += 4) {
-                const double v0 = contrib(A, A.plan.sblk_src[q], r, c);
-                const double v1 = contrib(A, A.plan.sblk_src[q + 1], r, c);
-                const double v2 = contrib(A, A.plan.sblk_src[q + 2], r, c);
-                const double v3 = contrib(A, A.plan.sblk_src[q + 3], r, c);
-                s += v0;
-                s += v1;
-                s += v2;
-                s += v3;
+    const int tid = threadIdx.x;
+    const int sl = tid / 36, e = tid - sl * 36;
+    const int g = blockIdx.x;
+    double s = 0.0;
+    if (g < P * P) {
+        const int a = g / P, bb = g - a * P;
+        const int r = e / 6, c = e - r * 6;
+        const int blk = A.plan.blkmap[g];
+        if (sl < kAsmSlices && blk >= 0) {
+            const int q1 = A.plan.sblk_ptr[blk + 1];
+            for (int q = A.plan.sblk_ptr[blk]; q < q1; q++) {
+                const int cd = A.plan.sblk_src[q];
+                const int ty = code_type(cd), v = code_val(cd);
+                if (ty == 0) {
+                    s += slice_sum(A.hpart + (size_t)(v >> 2) * A.nch * kNH +
+                                          hs_index(v & 3, r, c),
+                                      A.nch, kNH, sl);
+                } else {
+                    const int e36 = ty == 1 ? r * 6 + c : c * 6 + r;
+                    s -= slice_sum(A.spart + (size_t)v * A.nchS * 36 + e36, A.nchS, 36, sl);
+                }
             }
-            for (; q < q1; q++) s += contrib(A, A.plan.sblk_src[q], r, c);
         }
-        if (row == col) s = s + (double)A.ep + (double)A.lm * s;
-        A.S_dbg[t] = s;
-    } else if (t < n * n + n) {
-        const int i = t - n * n;
-        const int a = i / 6, k = i - (i / 6) * 6;
-        double s = 0.0;
-        for (int q = A.plan.bv_ptr[a]; q < A.plan.bv_ptr[a + 1]; q++) {
-            const int cd = A.plan.bv_src[q];
-            const int v = code_val(cd);
-            if (code_type(cd) == 0)
-                s += sum_parts(A.hpart + (size_t)(v >> 1) * A.nch * kNH + 78 + (v & 1) * 6 + k,
-                               A.nch, kNH);
-            else
-                s -= sum_parts(A.spart + (size_t)(A.N_pu + v) * A.nchS * 36 + k, A.nchS, 36);
+        if (sl < kAsmSlices) red[sl][e] = s;
+        __syncthreads();
+        if (tid < 36) {
+            double t = red[0][tid];
+#pragma unroll
+            for (int k = 1; k < kAsmSlices; k++) t += red[k][tid];
+            const int row = a * 6 + tid / 6, col = bb * 6 + tid % 6;
+            if (row == col) t = t + (double)A.ep + (double)A.lm * t;
+            A.S_dbg[(size_t)row * n + col] = t;
         }
-        A.b_dbg[i] = s;
+    } else {
+        const int a = g - P * P;
+        const int k = e;  // entries 0..5 of segment a; threads with e >= 6 idle
+        if (sl < kAsmSlices && k < 6) {
+            for (int q = A.plan.bv_ptr[a]; q < A.plan.bv_ptr[a + 1]; q++) {
+                const int cd = A.plan.bv_src[q];
+                const int v = code_val(cd);
+                if (code_type(cd) == 0)
+                    s += slice_sum(A.hpart + (size_t)(v >> 1) * A.nch * kNH + 78 +
+                                          (v & 1) * 6 + k,
+                                      A.nch, kNH, sl);
+                else
+                    s -= slice_sum(A.spart + (size_t)(A.N_pu + v) * A.nchS * 36 + k, A.nchS,
+                                      36, sl);
+            }
+        }
+        if (sl < kAsmSlices) red[sl][e] = s;
+        __syncthreads();
+        if (tid < 6) {
+            double t = red[0][tid];
+#pragma unroll
+            for (int m = 1; m < kAsmSlices; m++) t += red[m][tid];
+            A.b_dbg[a * 6 + tid] = t;
+        }
     }
 }
 
@@ -1016,8 +1024,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     A.poses = poses;
     {
         ProfScope ps(ctx, "ba_assemble", stream);
-        const int items = s->n * s->n + s->n;
-        hipLaunchKernelGGL(k_ba_assemble, dim3((items + 255) / 256), dim3(256), 0, stream, A);
+        hipLaunchKernelGGL(k_ba_assemble, dim3(s->P * s->P + s->P), dim3(256), 0, stream, A);
     }
     SLK_HIP(hipGetLastError());
     if (s->P <= kWaveP) {
