@@ -640,6 +640,16 @@ __global__ __launch_bounds__(1024) void k_ba_solve_global(SolveArgs A) {
 // reads L by columns from an LDS copy of the rows. No barrier anywhere: a
 // wave's LDS accesses are performed in program order. Same pivot test as the
 // reference (every pivot > 0 before its sqrt, ba.cuh:422).
+// 1/sqrt(d) in fp64: hardware estimate + two Newton steps
+// y <- y * (1.5 - 0.5 d y^2), ~1 ulp for positive normal d.
+__device__ __forceinline__ double rsqrt_f64(double d) {
+    double y = __builtin_amdgcn_rsq(d);
+    const double h = 0.5 * d;
+    y = y * (1.5 - h * y * y);
+    y = y * (1.5 - h * y * y);
+    return y;
+}
+
 template <int N>
 __global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
     __shared__ __attribute__((aligned(16))) double col[64];
@@ -655,14 +665,16 @@ __global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
     for (int j = 0; j < N; j++) {
         const double d = bcast(r[j], j);
         ok = ok && (d > 0.0);
-        const double ljj = sqrt(d);
-        const double inv = 1.0 / ljj;
-        r[j] = lane == j ? ljj : r[j] * inv;
+        const double inv = rsqrt_f64(d);  // 1 / L_jj
+        r[j] = lane == j ? d * inv : r[j] * inv;
         if (lane == j) invd = inv;
         col[lane] = r[j];
         __builtin_amdgcn_wave_barrier();
+        // the next pivot's term comes by readlane, keeping the LDS round trip
+        // of the column off the pivot-to-pivot path
+        if (j + 1 < N) r[j + 1] -= r[j] * bcast(r[j], j + 1);
 #pragma unroll
-        for (int k = j + 1; k < N; k++) r[k] -= r[j] * col[k];
+        for (int k = j + 2; k < N; k++) r[k] -= r[j] * col[k];
         __builtin_amdgcn_wave_barrier();
     }
     // forward: L z = b
