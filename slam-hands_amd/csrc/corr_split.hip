@@ -154,6 +154,40 @@ __global__ __launch_bounds__(256) void k_feat_split(const Tin* __restrict__ fm, 
     *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
 }
 
+// Which (edge, source tile, target tile) pairs hold at least one window cell:
+// per source and level present, the window's clipped rows/columns span the
+// concatenated target indices [off + ya*w + xa, off + yb*w + xb], and every
+// target tile in that span is marked (a superset of the tiles holding a cell).
+// Tiles not marked are skipped by k_corr_split_win: they would store nothing.
+// Grid (mtiles, edges), 128 threads (one source each); LDS bitmap of the
+// edge's target tiles.
+__global__ __launch_bounds__(128) void k_tile_mask(const float* __restrict__ coords,
+                                                   unsigned char* __restrict__ mask, Geom g,
+                                                   int mtiles, int ntiles) {
+    extern __shared__ unsigned bits[];
+    const int mt = blockIdx.x, e = blockIdx.y;
+    const int nw = (ntiles + 31) / 32;
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[i] = 0u;
+    __syncthreads();
+    const int p = mt * kSrcTile + threadIdx.x;
+    if (p < g.HW) {
+        const float* cc = coords + (size_t)e * 2 * g.HW;
+        const int fx = floor_clamped(cc[p]), fy = floor_clamped(cc[g.HW + p]);
+        for (int l = 0; l < g.levels; l++) {
+            const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
+            const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
+            const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
+            if (xa > xb || ya > yb) continue;
+            const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
+            const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
+            for (int t = lo; t <= hi; t++) atomicOr(&bits[t >> 5], 1u << (t & 31));
+        }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < ntiles; t += blockDim.x)
+        mask[((size_t)e * mtiles + mt) * ntiles + t] = (unsigned char)((bits[t >> 5] >> (t & 31)) & 1u);
+}
+
 struct alignas(16) SplitSmem {
     union {
         struct {
@@ -186,13 +220,15 @@ __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
 // targets wn*128..+127 of the tile, eight 32x32 accumulator blocks.
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* __restrict__ feat, EdgeSlots es, const float* __restrict__ coords,
-    float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles) {
+    float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles,
+    const unsigned char* __restrict__ tmask) {
     __shared__ SplitSmem sm;
     const int tpe = mtiles * ntiles;
     const int bid = xcd_remap(blockIdx.x, gridDim.x);
     const int e = bid / tpe;
     const int r = bid - e * tpe;
     const int mt = r / ntiles, nt = r - mt * ntiles;
+    if (!tmask[bid]) return;  // no window cell of these sources in this tile
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
@@ -466,10 +502,16 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     const long total = (long)n * mtiles * ntiles;
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
     {
+        ProfScope ps(ctx, "corr_tile_mask", stream);
+        const size_t shm = (size_t)((ntiles + 31) / 32) * sizeof(unsigned);
+        hipLaunchKernelGGL(k_tile_mask, dim3(mtiles, n), dim3(kSrcTile), shm, stream, coords,
+                           ctx->tile_mask.as<unsigned char>(), g, mtiles, ntiles);
+    }
+    {
         ProfScope ps(ctx, "corr_window", stream);
         hipLaunchKernelGGL(k_corr_split_win, dim3((unsigned)total), dim3(256), 0, stream,
                            ctx->split_feat.as<unsigned short>(), es, coords, win, slot0, g,
-                           ctx->alpha, mtiles, ntiles);
+                           ctx->alpha, mtiles, ntiles, ctx->tile_mask.as<unsigned char>());
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
@@ -485,6 +527,10 @@ int corr_split_alloc(slk_ctx* ctx) {
     const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
     SLK_TRY(ctx->split_feat.ensure(slots * 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short)));
     SLK_TRY(ctx->split_pool.ensure(slots * (size_t)g.C * std::max(g.pool_hw, 1) * sizeof(float)));
+    const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
+    const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
+    SLK_TRY(ctx->tile_mask.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles *
+                                  ntiles));
     return SLK_OK;
 }
 

@@ -76,6 +76,7 @@ struct slk_ctx {
     // batched-path operands: bf16 hi/lo split of every level's features per
     // frame slot, and the fp32 pooled features they are split from
     slk::DevBuf split_feat, split_pool;
+    slk::DevBuf tile_mask;  // [edges][source tiles][target tiles] tile holds a window cell
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
     bool single_built = false;
