@@ -161,6 +161,34 @@ def test_large_system_and_plan_cache(slk):
     ctx.close()
 
 
+def test_backend_geometry_1188(slk):
+    """Config backend's BA geometry: 200 keyframes, 2000 edges (|i-j| <= 2 plus
+    random long-range pairs), 198 free poses -> a 1188 x 1188 Schur system, at
+    6x8 pixels per frame so the oracle's dense fp64 Cholesky stays quick. The
+    reference backend's lm = 1e-5, ep = 1e-2 (main.cu:2487-2488); two chained
+    iterations."""
+    announce("ba backend geometry n=1188")
+    ii, jj = wl.backend_edges(200, 2000)
+    p = wl.ba_problem(n=200, h=6, w=8, ii=ii, jj=jj, seed=21)
+    dev = Dev(slk, p)
+    ctx = slk.Context(6, 8, max_batch=1, levels=1)
+    poses, disps = p["poses"], p["disps"]
+    for step in range(2):
+        dev.iterate(ctx, 1e-5, 1e-2)
+        assert ctx.ba_status() == slk.SLK_OK
+        ref = orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"],
+                             p["ii"], p["jj"], 6, 8, p["t0"], p["t1"], 1e-5, 1e-2)
+        assert ref["status"] == 0
+        S, b, dx = ctx.ba_last_system()
+        assert S.shape == (1188, 1188)
+        assert norm_rel(S, ref["S"]) < 1e-7, step
+        assert norm_rel(dx, ref["dx"]) < 1e-5, step
+        poses, disps = ref["poses"], ref["disps"]
+        assert norm_rel(dev.poses(), poses) < TOL, step
+        assert norm_rel(dev.disps(), disps) < TOL, step
+    ctx.close()
+
+
 # ------------------------------------------------------------ stage kernels --
 def test_projective_transform_stage(slk):
     p = wl.ba_problem(n=6, h=24, w=32, seed=4)
