@@ -200,7 +200,8 @@ struct alignas(16) SplitSmem {
         } st;
         float T[kTgtTile][kTStride];  // [target][source] of one 64-source half
     } u;
-    int org[kSrcTile][2];  // floor_clamped(x), floor_clamped(y) of each source
+    int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
+    float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -320,11 +321,15 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // workgroup fence would also wait for chunk k+1.
     const int nk = g.C / kChunk;
     issue(0, 0);
-    // coordinates of the tile's sources (one per thread of the first 128),
-    // in flight with the first chunk; written to LDS after the main loop
-    const int pc = std::min(p0 + (tid & (kSrcTile - 1)), HW - 1);
-    const float* cc = coords + (size_t)e * 2 * HW;
-    const float cxv = cc[pc], cyv = cc[HW + pc];
+    // coordinates of the tile's sources, in flight with the first chunk
+    // (also by a direct-to-LDS load: every load the pipeline waits on with
+    // vmcnt is of the same kind, and those complete in issue order)
+    {
+        const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
+        const int pc = std::min(p0 + half * 64 + lane, HW - 1);
+        __builtin_amdgcn_global_load_lds(coords + ((size_t)e * 2 + comp) * HW + pc,
+                                         (lds_ptr)&sm.crd[comp][half * 64], 4, 0, 0);
+    }
     if (nk > 1) issue(1, 1);
     for (int k = 0; k < nk; k++) {
         if (k + 1 < nk)
@@ -339,8 +344,8 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     }
     if (tid < kSrcTile) {
         const bool in = p0 + tid < HW;
-        sm.org[tid][0] = in ? floor_clamped(cxv) : -(1 << 20);  // -2^20: matches no cell
-        sm.org[tid][1] = in ? floor_clamped(cyv) : -(1 << 20);
+        sm.org[tid][0] = in ? floor_clamped(sm.crd[0][tid]) : -(1 << 20);  // matches no cell
+        sm.org[tid][1] = in ? floor_clamped(sm.crd[1][tid]) : -(1 << 20);
     }
     __syncthreads();  // every wave is done with the stages before T overwrites them
 
