@@ -44,12 +44,44 @@ __device__ __forceinline__ void block_sum(T (&v)[N], T* scratch) {
     __syncthreads();
 }
 
+// Partner exchange for the butterfly: the value of a lane whose index differs
+// in bit log2(M). Bits 0..3 use DPP inside rows of 16 lanes (quad permutes for
+// M = 1, 2; the half-row mirror i <-> 7-i for M = 4 and the row mirror
+// i <-> 15-i for M = 8: involutions that flip that bit), which are plain VALU
+// moves; M = 16, 32 go through ds_bpermute.
+template <int M>
+__device__ __forceinline__ int xchg_i32(int v) {
+    if constexpr (M == 1)
+        return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    else if constexpr (M == 2)
+        return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4)
+        return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    else if constexpr (M == 8)
+        return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+    else
+        return __shfl_xor(v, M);
+}
+
+template <int M>
+__device__ __forceinline__ float xchg(float v) {
+    return __builtin_bit_cast(float, xchg_i32<M>(__builtin_bit_cast(int, v)));
+}
+
+template <int M>
+__device__ __forceinline__ double xchg(double v) {
+    const int lo = xchg_i32<M>(__double2loint(v));
+    const int hi = xchg_i32<M>(__double2hiint(v));
+    return __hiloint2double(hi, lo);
+}
+
 // Butterfly reduce-scatter of N values over the 64 lanes of a wave. At each
-// of the 6 levels (lane masks 32..1) a lane keeps one half of its values and
-// trades the other half with its partner, so the whole reduction costs about
-// N shuffles instead of the 6N of N independent wave_sum()s. On return lane l
-// holds the wave totals of `valid` consecutive value indices starting at
-// `base` in v[0..valid).
+// of the 6 levels (lane bits 3, 2, 1, 0, 4, 5: the many-value levels on DPP)
+// a lane keeps
+// one half of its values and trades the other half with its partner, so the
+// whole reduction costs about N exchanges instead of the 6N of N independent
+// wave_sum()s. On return lane l holds the wave totals of `valid` consecutive
+// value indices starting at `base` in v[0..valid).
 template <typename T, int C, int M>
 __device__ __forceinline__ void rs_level(T* v, int lane, int& base, int& valid) {
     constexpr int H = (C + 1) / 2;
@@ -60,7 +92,7 @@ __device__ __forceinline__ void rs_level(T* v, int lane, int& base, int& valid) 
         const T hi = (k + H < C) ? v[k + H] : T(0);
         const T send = up ? lo : hi;
         const T keep = up ? hi : lo;
-        v[k] = keep + __shfl_xor(send, M);
+        v[k] = keep + xchg<M>(send);
     }
     if (up) {
         base += H;
@@ -81,12 +113,15 @@ __device__ __forceinline__ void wave_reduce_scatter(T (&v)[N], int lane, int& ba
     using R = RsCounts<N>;
     base = 0;
     valid = N;
-    rs_level<T, R::c0, 32>(v, lane, base, valid);
-    rs_level<T, R::c1, 16>(v, lane, base, valid);
-    rs_level<T, R::c2, 8>(v, lane, base, valid);
-    rs_level<T, R::c3, 4>(v, lane, base, valid);
-    rs_level<T, R::c4, 2>(v, lane, base, valid);
-    rs_level<T, R::c5, 1>(v, lane, base, valid);
+    // The partners of a level must agree in every bit already processed: the
+    // mirrors flip all lower bits, so they come first (bit 3, then bit 2),
+    // then the exact bit flips.
+    rs_level<T, R::c0, 8>(v, lane, base, valid);
+    rs_level<T, R::c1, 4>(v, lane, base, valid);
+    rs_level<T, R::c2, 2>(v, lane, base, valid);
+    rs_level<T, R::c3, 1>(v, lane, base, valid);
+    rs_level<T, R::c4, 16>(v, lane, base, valid);
+    rs_level<T, R::c5, 32>(v, lane, base, valid);
 }
 
 // Workgroup totals of N values per thread into tot[0..N) (LDS or global),
