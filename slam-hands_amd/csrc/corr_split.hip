@@ -22,15 +22,18 @@
 // pooled features of levels 1..3, then a bf16 hi/lo split of all levels
 // (hi = rne(x), lo = rne(x - hi)), stored chunk-major [plane][C/16][rows][16]
 // so a 16-channel chunk of consecutive rows is one contiguous block.
-// Stage 2 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
+// Stage 2 (k_tile_mask): which (edge, source tile, target tile) pairs hold any
+// window cell; the others are never computed.
+// Stage 3 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
 // hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_bf16 (exact products, fp32
 // accumulation; the dropped lo.lo term is ~2^-16 relative), staging 16-channel
-// chunks through LDS, double-buffered so the global loads of chunk k+1 are in
-// flight during the MFMAs of chunk k. The accumulator tile is then transposed
-// through LDS ([target][source]) and, per source and level, one wave writes
-// the window cells that fall inside the tile, one lane per cell: one masked
-// store of 64 consecutive floats. Only ~2% of the level-0 products are window
-// cells, and none of them costs more than its LDS round trip.
+// chunks through LDS in a 3-stage ring filled by direct-to-LDS loads, so the
+// loads of chunk k+2 are in flight during the MFMAs of chunk k. The
+// accumulator tile is then transposed through LDS ([target][source]) and, per
+// source and level, one wave writes the window cells that fall inside the
+// tile, one lane per cell: one masked store of 64 consecutive floats. Only ~2%
+// of the level-0 products are window cells, and none of them costs more than
+// its LDS round trip.
 #include <algorithm>
 #include <climits>
 #include <type_traits>
