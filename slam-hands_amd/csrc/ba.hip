@@ -615,22 +615,6 @@ __global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
     finish_solve(A, b, ok);
 }
 
-// S in global memory (n > 90), b in LDS.
-__global__ __launch_bounds__(1024) void k_ba_solve_global(SolveArgs A) {
-    extern __shared__ double smem[];
-    const int n = A.n;
-    double* b = smem;
-    double* S = A.S;
-    copy_in(S, A.S_dbg, n * n);
-    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
-    __syncthreads();
-    __shared__ int sh_flag;
-    const bool ok = chol_blocked(S, n, &sh_flag);
-    if (ok) chol_solve_blocked(S, b, n);
-    __syncthreads();
-    finish_solve(A, b, ok);
-}
-
 // One wavefront, n = N <= 64 (the frontend's 6P x 6P systems, P <= 10): lane i
 // holds row i of S in registers and becomes row i of L. Column j: the pivot
 // is read from lane j, lanes below scale by 1/L_jj, the column goes through a
@@ -742,6 +726,173 @@ bool solve_wave(int P, const SolveArgs& A, hipStream_t stream) {
         case 10: launch_solve_wave<10>(A, stream); return true;
         default: return false;
     }
+}
+
+// ---- blocked Cholesky over many workgroups (n > 90: the backend's systems) ----
+// Right-looking, lower, on the row-major working copy A.S (leading dimension
+// n), in kCB-column steps: (1) k_chol_diag factors the kCB x kCB diagonal
+// block in one wavefront's registers (lane = row, as k_ba_solve_wave); (2)
+// k_chol_panel solves the rows below against it, one thread per row; (3)
+// k_chol_syrk subtracts the new panel's products from the trailing lower
+// triangle in 64 x 64 tiles, one workgroup per tile. k_chol_finish then runs
+// the two triangular solves in one workgroup (they are O(n^2)) and the
+// retraction. A failed pivot is flagged in flags[2] (cleared by k_chol_init);
+// later kernels then do nothing and k_chol_finish reports the system not
+// positive definite, as the one-workgroup solvers do.
+constexpr int kCB = 64;
+
+__global__ __launch_bounds__(256) void k_chol_init(SolveArgs A) {
+    const size_t nn = (size_t)A.n * A.n;
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < nn;
+         t += (size_t)gridDim.x * blockDim.x)
+        A.S[t] = A.S_dbg[t];
+    if (blockIdx.x == 0 && threadIdx.x == 0) A.flags[2] = 0;
+}
+
+__global__ __launch_bounds__(64) void k_chol_diag(SolveArgs A, int j0) {
+    __shared__ __attribute__((aligned(16))) double col[64];
+    if (A.flags[2]) return;
+    const int n = A.n, lane = threadIdx.x;
+    const int nb = min(kCB, n - j0);
+    const int li = min(lane, nb - 1);
+    double* S = A.S;
+    double r[kCB];
+#pragma unroll
+    for (int m = 0; m < kCB; m++) r[m] = m < nb ? S[(size_t)(j0 + li) * n + j0 + m] : 0.0;
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < kCB; j++) {
+        if (j < nb) {  // uniform; a break would keep the loop from unrolling
+            const double d = bcast(r[j], j);
+            ok = ok && (d > 0.0);
+            const double inv = rsqrt_f64(d);
+            r[j] = lane == j ? d * inv : r[j] * inv;
+            col[lane] = r[j];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int k = j + 1; k < kCB; k++) r[k] -= r[j] * col[k];
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    if (lane < nb) {
+#pragma unroll
+        for (int m = 0; m < kCB; m++)
+            if (m <= lane && m < nb) S[(size_t)(j0 + lane) * n + j0 + m] = r[m];
+    }
+    if (lane == 0 && !ok) A.flags[2] = 1;
+}
+
+// rows i >= j0 + nb: x L_jj^T = S[i][j0 .. j0+nb), one thread per row
+__global__ __launch_bounds__(256) void k_chol_panel(SolveArgs A, int j0) {
+    __shared__ double L[kCB][kCB + 1];
+    __shared__ double invd[kCB];
+    if (A.flags[2]) return;
+    const int n = A.n;
+    const int nb = min(kCB, n - j0);
+    double* S = A.S;
+    for (int t = threadIdx.x; t < kCB * kCB; t += blockDim.x) {
+        const int r = t / kCB, c = t - (t / kCB) * kCB;
+        L[r][c] = (r < nb && c <= r) ? S[(size_t)(j0 + r) * n + j0 + c] : 0.0;
+    }
+    __syncthreads();
+    if (threadIdx.x < kCB) invd[threadIdx.x] = threadIdx.x < nb ? 1.0 / L[threadIdx.x][threadIdx.x] : 0.0;
+    __syncthreads();
+    const int i = j0 + nb + blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    double* row = S + (size_t)i * n + j0;
+    double x[kCB];
+#pragma unroll
+    for (int k = 0; k < kCB; k++) {
+        if (k < nb) {
+            double v = row[k];
+#pragma unroll
+            for (int m = 0; m < k; m++) v -= x[m] * L[k][m];
+            x[k] = v * invd[k];
+        } else {
+            x[k] = 0.0;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kCB; k++)
+        if (k < nb) row[k] = x[k];
+}
+
+// trailing S[i][k] -= sum_m L[i][j0+m] L[k][j0+m] for r0 <= k <= i < n (and the
+// upper entries of the diagonal tiles, which are never read), r0 = j0 + nb;
+// one workgroup per lower 64 x 64 tile, 4 x 4 outputs per thread.
+__global__ __launch_bounds__(256) void k_chol_syrk(SolveArgs A, int j0) {
+    __shared__ double Ai[64][kCB + 1], Bk[64][kCB + 1];
+    if (A.flags[2]) return;
+    const int n = A.n;
+    const int nb = min(kCB, n - j0);
+    const int r0 = j0 + nb;
+    // blockIdx.x -> lower tile (ti, tk), tk <= ti
+    int ti = (int)((sqrtf(8.0f * (float)blockIdx.x + 1.0f) - 1.0f) * 0.5f);
+    while (ti * (ti + 1) / 2 > (int)blockIdx.x) ti--;
+    while ((ti + 1) * (ti + 2) / 2 <= (int)blockIdx.x) ti++;
+    const int tk = (int)blockIdx.x - ti * (ti + 1) / 2;
+    const int ri = r0 + ti * 64, rk = r0 + tk * 64;
+    double* S = A.S;
+    for (int t = threadIdx.x; t < 64 * kCB; t += blockDim.x) {
+        const int r = t / kCB, m = t - (t / kCB) * kCB;
+        Ai[r][m] = (ri + r < n && m < nb) ? S[(size_t)(ri + r) * n + j0 + m] : 0.0;
+        Bk[r][m] = (rk + r < n && m < nb) ? S[(size_t)(rk + r) * n + j0 + m] : 0.0;
+    }
+    __syncthreads();
+    const int ty = threadIdx.x >> 4, tx = threadIdx.x & 15;
+    double acc[4][4] = {};
+    for (int m = 0; m < nb; m++) {
+        double a[4], b[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            a[u] = Ai[ty + 16 * u][m];
+            b[u] = Bk[tx + 16 * u][m];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[u][v] += a[u] * b[v];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = ri + ty + 16 * u;
+        if (i >= n) continue;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int k = rk + tx + 16 * v;
+            if (k < n) S[(size_t)i * n + k] -= acc[u][v];
+        }
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_chol_finish(SolveArgs A) {
+    extern __shared__ double smem[];
+    const int n = A.n;
+    double* b = smem;
+    const bool ok = A.flags[2] == 0;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
+    __syncthreads();
+    if (ok) chol_solve_blocked(A.S, b, n);
+    __syncthreads();
+    finish_solve(A, b, ok);
+}
+
+int solve_blocked(const SolveArgs& A, hipStream_t stream) {
+    const int n = A.n;
+    hipLaunchKernelGGL(k_chol_init, dim3(std::min(1024, (n * n + 255) / 256)), dim3(256), 0,
+                       stream, A);
+    for (int j0 = 0; j0 < n; j0 += kCB) {
+        hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(64), 0, stream, A, j0);
+        const int rest = n - std::min(n, j0 + kCB);
+        if (rest <= 0) break;
+        hipLaunchKernelGGL(k_chol_panel, dim3((rest + 255) / 256), dim3(256), 0, stream, A, j0);
+        const int T = (rest + 63) / 64;
+        hipLaunchKernelGGL(k_chol_syrk, dim3(T * (T + 1) / 2), dim3(256), 0, stream, A, j0);
+    }
+    hipLaunchKernelGGL(k_chol_finish, dim3(1), dim3(1024), (size_t)n * sizeof(double), stream,
+                       A);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
 }
 
 // ------------------------------------------------------ k_ba_backsub ----
@@ -1049,8 +1200,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(threads), shm, stream, A);
     } else {
         ProfScope ps(ctx, "ba_solve", stream);
-        const size_t shm = (size_t)s->n * sizeof(double);
-        hipLaunchKernelGGL(k_ba_solve_global, dim3(1), dim3(1024), shm, stream, A);
+        SLK_TRY(solve_blocked(A, stream));
     }
     SLK_HIP(hipGetLastError());
     if (!motion_only && s->N_E > 0) {
