@@ -320,7 +320,7 @@ struct SolveArgs {
     const double* spart;  // [N_pu + N_E][nchS][36] Schur pair / row chunk partials
     int nch, nchS, N_pu, P, n, n_blk, t0, t1;
     float lm, ep;
-    double* S;      // working matrix of the global-memory variant [n*n]
+    double* S;      // working copy of the blocked solver [(n+1)*n]: S, then b^T
     double* S_dbg;  // [n*n] assembled system (after damping), input of the solve
     double* b_dbg;  // [n]
     double* dx_dbg; // [n]
@@ -729,13 +729,16 @@ bool solve_wave(int P, const SolveArgs& A, hipStream_t stream) {
 }
 
 // ---- blocked Cholesky over many workgroups (n > 90: the backend's systems) ----
-// Right-looking, lower, on the row-major working copy A.S (leading dimension
-// n), in kCB-column steps: (1) k_chol_diag factors the kCB x kCB diagonal
-// block in one wavefront's registers (lane = row, as k_ba_solve_wave); (2)
-// k_chol_panel solves the rows below against it, one thread per row; (3)
-// k_chol_syrk subtracts the new panel's products from the trailing lower
-// triangle in 64 x 64 tiles, one workgroup per tile. k_chol_finish then runs
-// the two triangular solves in one workgroup (they are O(n^2)) and the
+// Right-looking, lower, on the row-major working copy A.S, which holds the
+// system in rows 0..n-1 and b^T in row n (leading dimension n): factoring the
+// bordered matrix [S b; b^T *] leaves L^-1 b in row n, so the forward solve
+// costs one more panel row. In kCB-column steps: (1) k_chol_diag factors the
+// kCB x kCB diagonal block in one wavefront's registers (lane = row, as
+// k_ba_solve_wave); (2) k_chol_panel solves the rows below it (b's row
+// included) against it, one thread per row; (3) k_chol_syrk subtracts the
+// new panel's products from the trailing lower triangle in 64 x 64 tiles,
+// one workgroup per tile. k_chol_finish then runs the backward solve
+// L^T x = z in one workgroup (O(n^2), coalesced column reads) and the
 // retraction. A failed pivot is flagged in flags[2] (cleared by k_chol_init);
 // later kernels then do nothing and k_chol_finish reports the system not
 // positive definite, as the one-workgroup solvers do.
@@ -743,9 +746,9 @@ constexpr int kCB = 64;
 
 __global__ __launch_bounds__(256) void k_chol_init(SolveArgs A) {
     const size_t nn = (size_t)A.n * A.n;
-    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < nn;
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < nn + A.n;
          t += (size_t)gridDim.x * blockDim.x)
-        A.S[t] = A.S_dbg[t];
+        A.S[t] = t < nn ? A.S_dbg[t] : A.b_dbg[t - nn];
     if (blockIdx.x == 0 && threadIdx.x == 0) A.flags[2] = 0;
 }
 
@@ -782,7 +785,8 @@ __global__ __launch_bounds__(64) void k_chol_diag(SolveArgs A, int j0) {
     if (lane == 0 && !ok) A.flags[2] = 1;
 }
 
-// rows i >= j0 + nb: x L_jj^T = S[i][j0 .. j0+nb), one thread per row
+// rows j0 + nb <= i <= n (row n is b): x L_jj^T = S[i][j0 .. j0+nb), one
+// thread per row
 __global__ __launch_bounds__(256) void k_chol_panel(SolveArgs A, int j0) {
     __shared__ double L[kCB][kCB + 1];
     __shared__ double invd[kCB];
@@ -795,10 +799,11 @@ __global__ __launch_bounds__(256) void k_chol_panel(SolveArgs A, int j0) {
         L[r][c] = (r < nb && c <= r) ? S[(size_t)(j0 + r) * n + j0 + c] : 0.0;
     }
     __syncthreads();
-    if (threadIdx.x < kCB) invd[threadIdx.x] = threadIdx.x < nb ? 1.0 / L[threadIdx.x][threadIdx.x] : 0.0;
+    if (threadIdx.x < kCB)
+        invd[threadIdx.x] = threadIdx.x < nb ? 1.0 / L[threadIdx.x][threadIdx.x] : 0.0;
     __syncthreads();
     const int i = j0 + nb + blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+    if (i > n) return;
     double* row = S + (size_t)i * n + j0;
     double x[kCB];
 #pragma unroll
@@ -817,9 +822,10 @@ __global__ __launch_bounds__(256) void k_chol_panel(SolveArgs A, int j0) {
         if (k < nb) row[k] = x[k];
 }
 
-// trailing S[i][k] -= sum_m L[i][j0+m] L[k][j0+m] for r0 <= k <= i < n (and the
-// upper entries of the diagonal tiles, which are never read), r0 = j0 + nb;
-// one workgroup per lower 64 x 64 tile, 4 x 4 outputs per thread.
+// trailing S[i][k] -= sum_m L[i][j0+m] L[k][j0+m] for r0 <= k <= i <= n, k < n
+// (row n is b; the upper entries of the diagonal tiles are updated too and
+// never read), r0 = j0 + nb; one workgroup per lower 64 x 64 tile of the
+// (n + 1 - r0)-row trailing block, 4 x 4 outputs per thread.
 __global__ __launch_bounds__(256) void k_chol_syrk(SolveArgs A, int j0) {
     __shared__ double Ai[64][kCB + 1], Bk[64][kCB + 1];
     if (A.flags[2]) return;
@@ -832,10 +838,11 @@ __global__ __launch_bounds__(256) void k_chol_syrk(SolveArgs A, int j0) {
     while ((ti + 1) * (ti + 2) / 2 <= (int)blockIdx.x) ti++;
     const int tk = (int)blockIdx.x - ti * (ti + 1) / 2;
     const int ri = r0 + ti * 64, rk = r0 + tk * 64;
+    if (rk >= n) return;  // a column tile made only of b's row
     double* S = A.S;
     for (int t = threadIdx.x; t < 64 * kCB; t += blockDim.x) {
         const int r = t / kCB, m = t - (t / kCB) * kCB;
-        Ai[r][m] = (ri + r < n && m < nb) ? S[(size_t)(ri + r) * n + j0 + m] : 0.0;
+        Ai[r][m] = (ri + r <= n && m < nb) ? S[(size_t)(ri + r) * n + j0 + m] : 0.0;
         Bk[r][m] = (rk + r < n && m < nb) ? S[(size_t)(rk + r) * n + j0 + m] : 0.0;
     }
     __syncthreads();
@@ -856,7 +863,7 @@ __global__ __launch_bounds__(256) void k_chol_syrk(SolveArgs A, int j0) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int i = ri + ty + 16 * u;
-        if (i >= n) continue;
+        if (i > n) continue;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int k = rk + tx + 16 * v;
@@ -865,32 +872,82 @@ __global__ __launch_bounds__(256) void k_chol_syrk(SolveArgs A, int j0) {
     }
 }
 
-__global__ __launch_bounds__(1024) void k_chol_finish(SolveArgs A) {
+// L^T x = z with L in the lower triangle of S (leading dimension n), z -> x
+// in y (LDS), one workgroup, blocks of kCB rows from the bottom. Per block,
+// wave 0 holds the block's columns of L in registers (loaded up front, so the
+// sequential substitution only waits on readlane broadcasts), then all
+// threads subtract the block's contribution from the entries above it,
+// reading L by rows (coalesced over the threads).
+__device__ void back_solve_blocked(const double* __restrict__ S, double* y, int n) {
+    const int tid = threadIdx.x;
+    for (int j0 = ((n - 1) / kCB) * kCB; j0 >= 0; j0 -= kCB) {  // backward: L^T x = z
+        const int jb = min(kCB, n - j0);
+        if (tid < 64) {
+            // lane c holds column c of the block: L[j0+k][j0+c] for k >= c
+            const int lane = tid, lc = min(lane, jb - 1);
+            double d[kCB];
+#pragma unroll
+            for (int k = 0; k < kCB; k++) d[k] = k < jb ? S[(size_t)(j0 + k) * n + j0 + lc] : 0.0;
+            double dl = 1.0;
+#pragma unroll
+            for (int k = 0; k < kCB; k++)
+                if (k == lc) dl = d[k];
+            const double invl = 1.0 / dl;
+            double v = lane < jb ? y[j0 + lane] : 0.0;
+#pragma unroll
+            for (int k = kCB - 1; k >= 0; k--) {
+                if (k < jb) {
+                    const double xk = bcast(v * invl, k);
+                    if (lane == k) v = xk;
+                    else if (lane < k) v -= d[k] * xk;
+                }
+            }
+            if (lane < jb) y[j0 + lane] = v;
+        }
+        __syncthreads();
+        for (int i = tid; i < j0; i += blockDim.x) {
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+            int m = 0;
+            for (; m + 4 <= jb; m += 4) {
+                s0 += S[(size_t)(j0 + m) * n + i] * y[j0 + m];
+                s1 += S[(size_t)(j0 + m + 1) * n + i] * y[j0 + m + 1];
+                s2 += S[(size_t)(j0 + m + 2) * n + i] * y[j0 + m + 2];
+                s3 += S[(size_t)(j0 + m + 3) * n + i] * y[j0 + m + 3];
+            }
+            for (; m < jb; m++) s0 += S[(size_t)(j0 + m) * n + i] * y[j0 + m];
+            y[i] -= (s0 + s1) + (s2 + s3);
+        }
+        __syncthreads();
+    }
+}
+
+constexpr int kFinishWG = 512;
+__global__ __launch_bounds__(kFinishWG) void k_chol_finish(SolveArgs A) {
     extern __shared__ double smem[];
     const int n = A.n;
     double* b = smem;
     const bool ok = A.flags[2] == 0;
-    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
+    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.S[(size_t)n * n + t];  // z
     __syncthreads();
-    if (ok) chol_solve_blocked(A.S, b, n);
+    if (ok) back_solve_blocked(A.S, b, n);
     __syncthreads();
     finish_solve(A, b, ok);
 }
 
 int solve_blocked(const SolveArgs& A, hipStream_t stream) {
     const int n = A.n;
-    hipLaunchKernelGGL(k_chol_init, dim3(std::min(1024, (n * n + 255) / 256)), dim3(256), 0,
-                       stream, A);
+    hipLaunchKernelGGL(k_chol_init, dim3(std::min(1024, (n * (n + 1) + 255) / 256)), dim3(256),
+                       0, stream, A);
     for (int j0 = 0; j0 < n; j0 += kCB) {
         hipLaunchKernelGGL(k_chol_diag, dim3(1), dim3(64), 0, stream, A, j0);
-        const int rest = n - std::min(n, j0 + kCB);
-        if (rest <= 0) break;
-        hipLaunchKernelGGL(k_chol_panel, dim3((rest + 255) / 256), dim3(256), 0, stream, A, j0);
-        const int T = (rest + 63) / 64;
+        const int rows = n + 1 - std::min(n, j0 + kCB);  // trailing rows, b's included
+        hipLaunchKernelGGL(k_chol_panel, dim3((rows + 255) / 256), dim3(256), 0, stream, A, j0);
+        if (rows <= 1) break;
+        const int T = (rows + 63) / 64;
         hipLaunchKernelGGL(k_chol_syrk, dim3(T * (T + 1) / 2), dim3(256), 0, stream, A, j0);
     }
-    hipLaunchKernelGGL(k_chol_finish, dim3(1), dim3(1024), (size_t)n * sizeof(double), stream,
-                       A);
+    hipLaunchKernelGGL(k_chol_finish, dim3(1), dim3(kFinishWG), (size_t)n * sizeof(double),
+                       stream, A);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -1135,7 +1192,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         SLK_TRY(s->Wv.ensure((size_t)s->N_kf * HW * sizeof(double)));
         SLK_TRY(s->spart.ensure(
             std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * s->nchS * 36) * sizeof(double)));
-        if (n > (size_t)kSmallN) SLK_TRY(s->S.ensure(n * n * sizeof(double)));
+        if (n > (size_t)kSmallN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
         SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
         SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
         SLK_TRY(s->dx_dbg.ensure(n * sizeof(double)));
