@@ -615,15 +615,6 @@ __global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
     finish_solve(A, b, ok);
 }
 
-// One wavefront, n = N <= 64 (the frontend's 6P x 6P systems, P <= 10): lane i
-// holds row i of S in registers and becomes row i of L. Column j: the pivot
-// is read from lane j, lanes below scale by 1/L_jj, the column goes through a
-// 64-entry LDS buffer and every lane subtracts L_ij * L_kj from its entries
-// k > j. Entries above a lane's diagonal receive the same updates unused (no
-// predicate). The forward solve broadcasts z_k by readlane; the backward solve
-// reads L by columns from an LDS copy of the rows. No barrier anywhere: a
-// wave's LDS accesses are performed in program order. Same pivot test as the
-// reference (every pivot > 0 before its sqrt, ba.cuh:422).
 // 1/sqrt(d) in fp64: hardware estimate + two Newton steps
 // y <- y * (1.5 - 0.5 d y^2), ~1 ulp for positive normal d.
 __device__ __forceinline__ double rsqrt_f64(double d) {
@@ -634,53 +625,110 @@ __device__ __forceinline__ double rsqrt_f64(double d) {
     return y;
 }
 
+// Cholesky of an N x N SPD matrix in one wavefront's registers (N <= 64):
+// lane i holds row i in r[] and ends with row i of L in r[0..i] (entries right
+// of the diagonal receive updates too and are left unused, so no lane is ever
+// predicated off). Columns go in panels of W: inside a panel, each column's
+// pivot and its entries in the panel's later columns come by readlane; then
+// every lane publishes its W panel entries to LDS (Lp, one 8W-byte row per
+// lane) and each later column k takes the panel's W updates from one
+// broadcast read of row k. Only the panel steps are sequential; the trailing
+// reads go out together. The arithmetic is the unblocked right-looking order
+// exactly: r[k] -= L[i][j] L[k][j] for j = 0, 1, ... Same pivot test as the
+// reference (every pivot > 0 before its sqrt, ba.cuh:422). inv_diag receives
+// 1/L[lane][lane].
+template <int N, int W, int kAhead = 3>
+__device__ __forceinline__ void wave_cholesky(double (&r)[N], double (*Lp)[W], bool& ok,
+                                              double& inv_diag) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int c0 = 0; c0 < N; c0 += W) {
+        const int cw = N - c0 < W ? N - c0 : W;
+#pragma unroll
+        for (int jj = 0; jj < W; jj++) {
+            if (jj < cw) {
+                const int j = c0 + jj;
+                const double d = bcast(r[j], j);
+                ok = ok && (d > 0.0);
+                const double inv = rsqrt_f64(d);  // 1 / L_jj
+                r[j] = lane == j ? d * inv : r[j] * inv;
+                if (lane == j) inv_diag = inv;
+#pragma unroll
+                for (int kk = jj + 1; kk < W; kk++)
+                    if (kk < cw) r[c0 + kk] -= r[j] * bcast(r[j], c0 + kk);
+            }
+        }
+        if (c0 + W < N) {
+#pragma unroll
+            for (int m = 0; m < W; m++) Lp[lane][m] = r[c0 + m];
+            // rows k of the panel read kAhead columns ahead of their use, in a
+            // register ring; the scheduling barriers keep the compiler from
+            // pulling each read down next to its use
+            double Lk[kAhead + 1][W];
+#pragma unroll
+            for (int q = 0; q < kAhead; q++)
+                if (c0 + W + q < N)
+#pragma unroll
+                    for (int m = 0; m < W; m++) Lk[q][m] = Lp[c0 + W + q][m];
+#pragma unroll
+            for (int k = c0 + W; k < N; k++) {
+                const int q = k - c0 - W;
+                if (k + kAhead < N)
+#pragma unroll
+                    for (int m = 0; m < W; m++) Lk[(q + kAhead) % (kAhead + 1)][m] = Lp[k + kAhead][m];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int m = 0; m < W; m++) r[k] -= r[c0 + m] * Lk[q % (kAhead + 1)][m];
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
+constexpr int kPanelW = 8;
+
+// One wavefront, n = N < 64 (the frontend's 6P x 6P systems, P <= 10). Lane
+// i < N holds row i of S and lane N holds b^T: wave_cholesky on the bordered
+// matrix [S; b^T] leaves z = L^-1 b in lane N's row, so the forward solve
+// costs nothing. The backward solve L^T x = z broadcasts x_k by readlane;
+// lane i's column of L comes from an LDS copy of the rows, read into
+// registers before the sequential part. No barrier anywhere: a wave's LDS
+// accesses are performed in program order.
 template <int N>
 __global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
+    static_assert(N < 64, "lane N carries b");
     __shared__ __attribute__((aligned(16))) double col[64];
+    __shared__ __attribute__((aligned(16))) double Lp[64][kPanelW];
     __shared__ double Lrow[N * (N + 1)];  // L rows, leading dimension N + 1
     const int lane = threadIdx.x;
-    const int li = lane < N ? lane : N - 1;
+    const double* src = lane < N ? A.S_dbg + (size_t)lane * N : A.b_dbg;  // lanes > N: b too
     double r[N];
 #pragma unroll
-    for (int m = 0; m < N; m++) r[m] = A.S_dbg[(size_t)li * N + m];
+    for (int m = 0; m < N; m++) r[m] = src[m];
     bool ok = true;
     double invd = 0.0;  // 1 / L_ii of this lane's row
+    wave_cholesky<N, kPanelW>(r, Lp, ok, invd);
+    // z to LDS (lane N), the rows of L to LDS, then each lane's column of L
+    if (lane == N) {
 #pragma unroll
-    for (int j = 0; j < N; j++) {
-        const double d = bcast(r[j], j);
-        ok = ok && (d > 0.0);
-        const double inv = rsqrt_f64(d);  // 1 / L_jj
-        r[j] = lane == j ? d * inv : r[j] * inv;
-        if (lane == j) invd = inv;
-        col[lane] = r[j];
-        __builtin_amdgcn_wave_barrier();
-        // the next pivot's term comes by readlane, keeping the LDS round trip
-        // of the column off the pivot-to-pivot path
-        if (j + 1 < N) r[j + 1] -= r[j] * bcast(r[j], j + 1);
-#pragma unroll
-        for (int k = j + 2; k < N; k++) r[k] -= r[j] * col[k];
-        __builtin_amdgcn_wave_barrier();
+        for (int m = 0; m < N; m++) col[m] = r[m];
     }
-    // forward: L z = b
-    double acc = A.b_dbg[li], z = 0.0;
+    if (lane < N) {
 #pragma unroll
-    for (int k = 0; k < N; k++) {
-        const double zk = bcast(acc * invd, k);
-        if (lane == k) z = zk;
-        acc -= r[k] * zk;
+        for (int m = 0; m < N; m++) Lrow[lane * (N + 1) + m] = r[m];
     }
-    // backward: L^T x = z, column lane of L read from the row copy
+    const int lc = lane < N ? lane : 0;
+    double c[N];  // c[k] = L[k][lane], used for k > lane
 #pragma unroll
-    for (int m = 0; m < N; m++)
-        if (lane < N && m <= lane) Lrow[lane * (N + 1) + m] = r[m];
-    __builtin_amdgcn_wave_barrier();
-    acc = z;
+    for (int k = 0; k < N; k++) c[k] = Lrow[k * (N + 1) + lc];
+    // backward: L^T x = z; lanes past their own step keep updating unused acc
+    double acc = col[lc];
     double x = 0.0;
 #pragma unroll
     for (int k = N - 1; k >= 0; k--) {
         const double xk = bcast(acc * invd, k);
         if (lane == k) x = xk;
-        if (lane < k) acc -= Lrow[k * (N + 1) + lane] * xk;
+        acc -= c[k] * xk;
     }
     col[lane] = x;
     __builtin_amdgcn_wave_barrier();
@@ -752,35 +800,26 @@ __global__ __launch_bounds__(256) void k_chol_init(SolveArgs A) {
     if (blockIdx.x == 0 && threadIdx.x == 0) A.flags[2] = 0;
 }
 
+// The diagonal block, padded to kCB x kCB with an identity block (whose
+// Cholesky is itself), so wave_cholesky runs at its compile-time size.
 __global__ __launch_bounds__(64) void k_chol_diag(SolveArgs A, int j0) {
-    __shared__ __attribute__((aligned(16))) double col[64];
+    __shared__ __attribute__((aligned(16))) double Lp[64][kPanelW];
     if (A.flags[2]) return;
     const int n = A.n, lane = threadIdx.x;
     const int nb = min(kCB, n - j0);
-    const int li = min(lane, nb - 1);
     double* S = A.S;
     double r[kCB];
 #pragma unroll
-    for (int m = 0; m < kCB; m++) r[m] = m < nb ? S[(size_t)(j0 + li) * n + j0 + m] : 0.0;
+    for (int m = 0; m < kCB; m++)
+        r[m] = (lane < nb && m < nb) ? S[(size_t)(j0 + lane) * n + j0 + m]
+                                     : (m == lane ? 1.0 : 0.0);
     bool ok = true;
-#pragma unroll
-    for (int j = 0; j < kCB; j++) {
-        if (j < nb) {  // uniform; a break would keep the loop from unrolling
-            const double d = bcast(r[j], j);
-            ok = ok && (d > 0.0);
-            const double inv = rsqrt_f64(d);
-            r[j] = lane == j ? d * inv : r[j] * inv;
-            col[lane] = r[j];
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int k = j + 1; k < kCB; k++) r[k] -= r[j] * col[k];
-            __builtin_amdgcn_wave_barrier();
-        }
-    }
+    double invd = 0.0;
+    wave_cholesky<kCB, kPanelW>(r, Lp, ok, invd);
     if (lane < nb) {
 #pragma unroll
         for (int m = 0; m < kCB; m++)
-            if (m <= lane && m < nb) S[(size_t)(j0 + lane) * n + j0 + m] = r[m];
+            if (m <= lane) S[(size_t)(j0 + lane) * n + j0 + m] = r[m];
     }
     if (lane == 0 && !ok) A.flags[2] = 1;
 }
