@@ -371,13 +371,12 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // accumulator layout of the 32x32 MFMA: lane l, register v holds
     // D[i][j] with j = l % 32 (target) and i = 8*(v/4) + 4*(l/32) + v%4 (source)
     const int khalf = lane >> 5;
-    // lane = window cell (cx, cy); its offset from the window origin in the
-    // level's row-major target order
-    const int cx = lane & 7, cy = lane >> 3;
-    int lanec[kMaxLevels];
-#pragma unroll
-    for (int l = 0; l < kMaxLevels; l++) lanec[l] = cy * g.w[l] + cx;
-    float* wbase = win + (size_t)(slot0 + e) * HW * (kMaxLevels * kWinCells) + lane;
+    // extraction: lane = (source g8 of a group of 8, window column cx). A wave
+    // takes its 16 columns of T (sources) as two groups of 8 and walks the 8
+    // window rows, so every read and store instruction covers 8 sources x 8
+    // consecutive cells and all per-source set-up is plain per-lane arithmetic.
+    const int g8 = lane >> 3, cx = lane & 7;
+    float* wout = win + (size_t)(slot0 + e) * HW * (kMaxLevels * kWinCells) + cx;
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
         if (sb) __syncthreads();  // the first half's cells have all been read
@@ -392,39 +391,37 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                                 acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
             }
         __syncthreads();
-        // this wave's 16 columns of T (sources): origins fetched once, one per
-        // lane, then broadcast with readlane. Per level present in the tile,
-        // the 16 masked reads of T are issued together, then the 16 masked
-        // stores of 64 consecutive window floats.
-        const int li = wave * 16 + (lane & 15);
-        const int lsrc = (li >> 5) * 64 + sb * 32 + (li & 31);
-        const int ofx = sm.org[lsrc][0], ofy = sm.org[lsrc][1];
-        const int srcw = (wave >> 1) * 64 + sb * 32 + (wave & 1) * 16;  // source of i = 0
 #pragma unroll
-        for (int l = 0; l < kMaxLevels; l++) {
-            if (lr0[l] > lr1[l]) continue;  // level not in this tile
-            const int wl = g.w[l], hl = g.h[l];
-            const unsigned base = (unsigned)(g.off[l] - t0) + (unsigned)lanec[l];
-            float v[16];
-            unsigned okm = 0;  // bit i: lane's cell of item i is stored
+        for (int grp = 0; grp < 2; grp++) {
+            const int s = wave * 16 + grp * 8 + g8;                 // column of T
+            const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
+            const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
+            const bool pin = p0 + lsrc < HW;
+            float* wp = wout + (size_t)std::min(p0 + lsrc, HW - 1) * (kMaxLevels * kWinCells);
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int fx = __builtin_amdgcn_readlane(ofx, i);
-                const int fy = __builtin_amdgcn_readlane(ofy, i);
+            for (int l = 0; l < kMaxLevels; l++) {
+                if (lr0[l] > lr1[l]) continue;  // level not in this tile
+                const int wl = g.w[l], hl = g.h[l];
                 const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
-                const int xs = ox + cx, ys = oy + cy;
-                // wraps harmlessly for far origins (then xs/ys are out of range)
-                const unsigned tl = base + (unsigned)oy * (unsigned)wl + (unsigned)ox;
-                const bool ok = p0 + srcw + i < HW && (unsigned)xs < (unsigned)wl &&
-                                (unsigned)ys < (unsigned)hl && tl < (unsigned)kTgtTile;
-                v[i] = sm.u.T[ok ? tl : 0][wave * 16 + i];
-                okm |= (unsigned)ok << i;
-            }
+                const int xs = ox + cx;
+                const bool colok = pin && (unsigned)xs < (unsigned)wl;
+                // tile row of cell (cx, 0); wraps harmlessly for far origins
+                // (then xs or the rows are out of range)
+                unsigned tl = (unsigned)(g.off[l] - t0) + (unsigned)oy * (unsigned)wl +
+                              (unsigned)xs;
+                float v[8];
+                unsigned okm = 0;  // bit cy: this lane's cell of window row cy is stored
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int p = std::min(p0 + srcw + i, HW - 1);
-                if (okm & (1u << i))
-                    wbase[(size_t)p * (kMaxLevels * kWinCells) + l * kWinCells] = alpha * v[i];
+                for (int cy = 0; cy < 8; cy++) {
+                    const bool ok = colok && (unsigned)(oy + cy) < (unsigned)hl &&
+                                    tl < (unsigned)kTgtTile;
+                    v[cy] = sm.u.T[ok ? tl : 0][s];
+                    okm |= (unsigned)ok << cy;
+                    tl += (unsigned)wl;
+                }
+#pragma unroll
+                for (int cy = 0; cy < 8; cy++)
+                    if (okm & (1u << cy)) wp[l * kWinCells + cy * 8] = alpha * v[cy];
             }
         }
     }
