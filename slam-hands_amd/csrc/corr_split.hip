@@ -397,6 +397,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
             const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
             const bool pin = p0 + lsrc < HW;
+            const float* Tcol = &sm.u.T[0][s];
             float* wp = wout + (size_t)std::min(p0 + lsrc, HW - 1) * (kMaxLevels * kWinCells);
 #pragma unroll
             for (int l = 0; l < kMaxLevels; l++) {
@@ -409,19 +410,20 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                 // (then xs or the rows are out of range)
                 unsigned tl = (unsigned)(g.off[l] - t0) + (unsigned)oy * (unsigned)wl +
                               (unsigned)xs;
+                unsigned ta = tl * (unsigned)kTStride;  // offset of row tl in T
                 float v[8];
-                unsigned okm = 0;  // bit cy: this lane's cell of window row cy is stored
+                bool ok[8];  // this lane's cell of window row cy is in the tile and grid
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++) {
-                    const bool ok = colok && (unsigned)(oy + cy) < (unsigned)hl &&
-                                    tl < (unsigned)kTgtTile;
-                    v[cy] = sm.u.T[ok ? tl : 0][s];
-                    okm |= (unsigned)ok << cy;
+                    ok[cy] = colok && (unsigned)(oy + cy) < (unsigned)hl &&
+                             tl < (unsigned)kTgtTile;
+                    v[cy] = Tcol[ok[cy] ? ta : 0u];
                     tl += (unsigned)wl;
+                    ta += (unsigned)wl * (unsigned)kTStride;
                 }
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++)
-                    if (okm & (1u << cy)) wp[l * kWinCells + cy * 8] = alpha * v[cy];
+                    if (ok[cy]) wp[l * kWinCells + cy * 8] = alpha * v[cy];
             }
         }
     }
