@@ -210,9 +210,20 @@ struct alignas(16) SplitSmem {
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
-// lgkmcnt 11:8): vmcnt(6) lgkmcnt(0), and vmcnt(0) lgkmcnt(0)
+// lgkmcnt 11:8): vmcnt(6) lgkmcnt(0), vmcnt(0) lgkmcnt(0), and lgkmcnt(0) alone
 constexpr int kWaitVm6Lgkm0 = 0x0076;
 constexpr int kWaitVm0Lgkm0 = 0x0070;
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// Workgroup barrier for LDS hand-offs only: this wave's LDS accesses are
+// complete, but its global stores may still be in flight (__syncthreads'
+// fence would wait for those too).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -350,7 +361,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         sm.org[tid][0] = in ? floor_clamped(sm.crd[0][tid]) : -(1 << 20);  // matches no cell
         sm.org[tid][1] = in ? floor_clamped(sm.crd[1][tid]) : -(1 << 20);
     }
-    __syncthreads();  // every wave is done with the stages before T overwrites them
+    lds_barrier();  // every wave is done with the stages before T overwrites them
 
     // ---- window extraction ----
     // rows of level l inside this tile: [lr0[l], lr1[l]] (empty: lr0 > lr1)
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     float* wout = win + (size_t)(slot0 + e) * HW * (kMaxLevels * kWinCells) + cx;
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
-        if (sb) __syncthreads();  // the first half's cells have all been read
+        if (sb) lds_barrier();  // the first half's cells have all been read
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
@@ -390,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                     make_float4(acc[sb][tb][4 * gq], acc[sb][tb][4 * gq + 1],
                                 acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
             }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int grp = 0; grp < 2; grp++) {
             const int s = wave * 16 + grp * 8 + g8;                 // column of T
