@@ -268,6 +268,121 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
     }
 }
 
+// Same linearization with one wave per edge: a workgroup (pixel chunk,
+// keyframe) gives its keyframe's edges to its four waves in turn, each wave
+// covering all kLinPx pixels (kLinPx / 64 per lane), so no edge waits for
+// another and the per-edge Hessian reduction stays inside one wave. The
+// cross-edge sums (the E row of the keyframe's own pose, and C, w per pixel)
+// go to per-wave LDS slices, added in wave order at the end; the E row of an
+// edge's other pose is stored directly, which needs that row to be the
+// edge's alone (no two edges of a keyframe share jj; the host checks this
+// and otherwise runs k_ba_lin_kf).
+constexpr int kLinWaves = kLinWG / 64;
+constexpr int kLinPPL = kLinPx / 64;  // pixels per lane
+__global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
+    PlanDev plan, const float* __restrict__ target, const float* __restrict__ weight,
+    const float* __restrict__ poses, const float* __restrict__ disps,
+    const float* __restrict__ intr, const int* __restrict__ ii, const int* __restrict__ jj,
+    const float* __restrict__ eta, double* __restrict__ hpart, double* __restrict__ E,
+    double* __restrict__ Qo, double* __restrict__ Wo, int HW, int W, int nch, int motion_only) {
+    __shared__ double eri_s[kLinWaves][6][kLinPx];  // keyframe-pose E row, per wave
+    __shared__ double cw_s[kLinWaves][2][kLinPx];   // C and w, per wave
+    const int chunk = blockIdx.x;
+    const int kc = blockIdx.y;
+    const int kf = plan.kf_list[kc];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
+    int kpx[kLinPPL];
+    bool vpx[kLinPPL];
+    double dsp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        const int px = s * 64 + lane;
+        kpx[s] = chunk * kLinPx + px;
+        vpx[s] = kpx[s] < HW;
+        dsp[s] = vpx[s] ? (double)disps[(size_t)kf * HW + kpx[s]] : 1.0;
+        if (!motion_only) {
+#pragma unroll
+            for (int n = 0; n < 6; n++) eri_s[wave][n][px] = 0.0;
+            cw_s[wave][0][px] = 0.0;
+            cw_s[wave][1][px] = 0.0;
+        }
+    }
+    const int e0 = plan.kf_eptr[kc], e1 = plan.kf_eptr[kc + 1];
+    for (int ei = e0 + wave; ei < e1; ei += kLinWaves) {
+        const int e = plan.kf_eidx[ei];
+        const int ix = ii[e], jx = jj[e];
+        const bool stereo = ix == jx;
+        double tij[3], qij[4];
+        edge_rel(poses, ix, jx, tij, qij);  // uniform: every lane computes it
+        const int ri = plan.edge_ri[e], rj = plan.edge_rj[e];
+        double acc[kNH];
+#pragma unroll
+        for (int n = 0; n < kNH; n++) acc[n] = 0.0;
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            if (!vpx[s]) continue;
+            const int k = kpx[s], px = s * 64 + lane;
+            const size_t base = (size_t)e * 2 * HW + k;
+            Lin L;
+            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)target[base],
+                      (double)target[base + HW], (double)weight[base], (double)weight[base + HW],
+                      L);
+            accum_hessian(L, stereo, acc);
+            if (!motion_only) {
+                cw_s[wave][0][px] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
+                cw_s[wave][1][px] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
+                if (!stereo) {  // a stereo edge adds nothing to E
+                    const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
+                    if (ri >= 0) {
+#pragma unroll
+                        for (int n = 0; n < 6; n++)
+                            eri_s[wave][n][px] += a0 * L.Ji[0][n] + a1 * L.Ji[1][n];
+                    }
+                    if (rj >= 0) {
+                        double* er = E + (size_t)rj * 6 * HW + k;
+#pragma unroll
+                        for (int n = 0; n < 6; n++)
+                            er[(size_t)n * HW] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                    }
+                }
+            }
+        }
+        int rbase, rvalid;
+        wave_reduce_scatter(acc, lane, rbase, rvalid);
+        double* hp = hpart + ((size_t)e * nch + chunk) * kNH;
+#pragma unroll
+        for (int q = 0; q < RsCounts<kNH>::c6; q++)
+            if (q < rvalid) hp[rbase + q] = acc[q];
+    }
+    if (motion_only) return;
+    __syncthreads();
+    // one pixel per thread: the per-wave slices in wave order
+    const int px = threadIdx.x, k = chunk * kLinPx + px;
+    if (k >= HW) return;
+    double c = 0.0, w = 0.0;
+#pragma unroll
+    for (int v = 0; v < kLinWaves; v++) {
+        c += cw_s[v][0][px];
+        w += cw_s[v][1][px];
+    }
+    // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
+    Qo[(size_t)kc * HW + k] = 1.0 / (c + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7);
+    Wo[(size_t)kc * HW + k] = w;
+    const int ri = e1 > e0 ? plan.edge_ri[plan.kf_eidx[e0]] : -1;  // the keyframe's own pose
+    if (ri >= 0) {
+        double* er = E + (size_t)ri * 6 * HW + k;
+#pragma unroll
+        for (int n = 0; n < 6; n++) {
+            double t = 0.0;
+#pragma unroll
+            for (int v = 0; v < kLinWaves; v++) t += eri_s[v][n][px];
+            er[(size_t)n * HW] = t;
+        }
+    }
+}
+
 // -------------------------------------------------------- k_ba_schur ----
 __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double* __restrict__ E,
                                                      const double* __restrict__ Q,
@@ -1031,6 +1146,7 @@ struct BaState {
     DevBuf plan_dev, hpart, E, Q, Wv, spart, S, S_dbg, b_dbg, dx_dbg, dx, flags;
     HostStage stage;
     bool has_system = false;
+    bool lin_by_wave = false;  // no keyframe has two edges to the same free pose
 };
 
 namespace {
@@ -1096,6 +1212,18 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
         }
     }
     const int N_E = (int)row_pose.size();
+    // k_ba_lin_wv stores each non-stereo edge's jj row directly: the row must
+    // belong to that edge alone
+    {
+        std::vector<int> owner(N_E, -1);
+        s->lin_by_wave = true;
+        for (int e = 0; e < M && s->lin_by_wave; e++) {
+            const int r = edge_rj[e];
+            if (r < 0 || ii[e] == jj[e]) continue;
+            if (owner[r] >= 0) s->lin_by_wave = false;
+            owner[r] = e;
+        }
+    }
     std::vector<int> kf_rptr(N_kf + 1, 0), kf_rows(N_E);
     for (int r = 0; r < N_E; r++) kf_rptr[row_kf[r] + 1]++;
     for (int k = 0; k < N_kf; k++) kf_rptr[k + 1] += kf_rptr[k];
@@ -1247,10 +1375,11 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     const PlanDev plan = plan_ptrs(s);
     {
         ProfScope ps(ctx, "ba_lin_kf", stream);
-        hipLaunchKernelGGL(k_ba_lin_kf, dim3(s->nch, s->N_kf), dim3(kLinWG), 0, stream, plan, target,
-                       weight, poses, disps, intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
-                       s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW, ctx->w,
-                       s->nch, motion_only);
+        hipLaunchKernelGGL(s->lin_by_wave ? k_ba_lin_wv : k_ba_lin_kf, dim3(s->nch, s->N_kf),
+                           dim3(kLinWG), 0, stream, plan, target, weight, poses, disps,
+                           intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
+                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW, ctx->w,
+                           s->nch, motion_only);
     }
     SLK_HIP(hipGetLastError());
     if (!motion_only && s->N_pu + s->N_E > 0) {

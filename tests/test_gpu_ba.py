@@ -97,9 +97,12 @@ def test_three_iterations_chained(slk):
     ctx.close()
 
 
-def test_edge_cases_stereo_duplicates_absent_frame(slk):
-    ii = np.array([0, 1, 2, 1, 2, 0, 1, 2], np.int32)
-    jj = np.array([1, 2, 3, 0, 1, 2, 1, 3], np.int32)
+@pytest.mark.parametrize("duplicate", [True, False])
+def test_edge_cases_stereo_duplicates_absent_frame(slk, duplicate):
+    # with the duplicate (2, 3) edge the linearization runs edge by edge per
+    # keyframe (k_ba_lin_kf); without it, one wave per edge (k_ba_lin_wv)
+    ii = np.array([0, 1, 2, 1, 2, 0, 1] + ([2] if duplicate else []), np.int32)
+    jj = np.array([1, 2, 3, 0, 1, 2, 1] + ([3] if duplicate else []), np.int32)
     p = wl.ba_problem(n=4, h=6, w=8, ii=ii, jj=jj, seed=8, fixed=1)
     p["eta"] = np.random.default_rng(9).uniform(0, 1e-3, p["eta"].shape).astype(np.float32)
     dev = Dev(slk, p)
