@@ -317,6 +317,16 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
         double tij[3], qij[4];
         edge_rel(poses, ix, jx, tij, qij);  // uniform: every lane computes it
         const int ri = plan.edge_ri[e], rj = plan.edge_rj[e];
+        // every pixel's target and weight loads go out before any pixel waits
+        float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            const size_t base = (size_t)e * 2 * HW + (vpx[s] ? kpx[s] : 0);
+            tgu[s] = target[base];
+            tgv[s] = target[base + HW];
+            wtu[s] = weight[base];
+            wtv[s] = weight[base + HW];
+        }
         double acc[kNH];
 #pragma unroll
         for (int n = 0; n < kNH; n++) acc[n] = 0.0;
@@ -324,11 +334,9 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
         for (int s = 0; s < kLinPPL; s++) {
             if (!vpx[s]) continue;
             const int k = kpx[s], px = s * 64 + lane;
-            const size_t base = (size_t)e * 2 * HW + k;
             Lin L;
-            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)target[base],
-                      (double)target[base + HW], (double)weight[base], (double)weight[base + HW],
-                      L);
+            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)tgu[s], (double)tgv[s],
+                      (double)wtu[s], (double)wtv[s], L);
             accum_hessian(L, stereo, acc);
             if (!motion_only) {
                 cw_s[wave][0][px] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
