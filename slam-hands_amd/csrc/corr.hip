@@ -155,7 +155,6 @@ __global__ __launch_bounds__(kWG) void k_corr_tile(
 #pragma unroll
     for (int v = 0; v < 16; v++) prow[v] = p0 + 8 * (v >> 2) + 4 * khalf + (v & 3);
     float cxs[16], cys[16];
-    float* wbase = nullptr;
     if constexpr (WIN) {
         const float* cc = coords + (size_t)e * 2 * HW;
 #pragma unroll
@@ -164,7 +163,6 @@ __global__ __launch_bounds__(kWG) void k_corr_tile(
             cxs[v] = cc[q];
             cys[v] = cc[HW + q];
         }
-        wbase = win + (size_t)slot * HW * (kMaxLevels * kWinCells);
     }
     // store of one cell (y, x) of level l for source row register v
     auto put = [&](int l, int v, int y, int x, float val, float* plane, int hl, int wl) {
@@ -174,7 +172,7 @@ __global__ __launch_bounds__(kWG) void k_corr_tile(
             const int ox = x - win_origin(cxs[v], l);
             const int oy = y - win_origin(cys[v], l);
             if ((unsigned)ox < 8u && (unsigned)oy < 8u)
-                wbase[((size_t)p * kMaxLevels + l) * kWinCells + oy * 8 + ox] = val;
+                win[win_index(slot, l, oy * 8 + ox, HW, p)] = val;
         } else {
             __builtin_nontemporal_store(val, plane + (size_t)p * (hl * wl) + y * wl + x);
         }
@@ -453,7 +451,6 @@ __global__ __launch_bounds__(kWG) void k_corr_mx(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[sb][tb][v] *= alpha;
     auto prow = [&](int sb, int v) { return ps0 + sb * 32 + 8 * (v >> 2) + 4 * khalf + (v & 3); };
-    float* wbase = WIN ? win + (size_t)slot * HW * (kMaxLevels * kWinCells) : nullptr;
     // coordinates of the lane's 32 source rows, loaded once before any store
     // (the window stores would otherwise order every later coordinate load)
     float cxs[2][16], cys[2][16];
@@ -476,7 +473,7 @@ __global__ __launch_bounds__(kWG) void k_corr_mx(
             const int ox = x - win_origin(cxs[sb][v], l);
             const int oy = y - win_origin(cys[sb][v], l);
             if ((unsigned)ox < 8u && (unsigned)oy < 8u)
-                wbase[((size_t)p * kMaxLevels + l) * kWinCells + oy * 8 + ox] = val;
+                win[win_index(slot, l, oy * 8 + ox, HW, p)] = val;
         } else {
             __builtin_nontemporal_store(val, plane + (size_t)p * (hl * wl) + y * wl + x);
         }
@@ -666,13 +663,12 @@ __global__ __launch_bounds__(256) void k_corr_lookup_win(LevelIn lv, const float
         return;
     }
     const int ix = win_origin(cx, l), iy = win_origin(cy, l);
-    const float4* src = reinterpret_cast<const float4*>(
-        wb + (((size_t)e * HW1 + p) * kMaxLevels + l) * kWinCells);
     float win[8][8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const bool vy = (unsigned)(iy + j) < (unsigned)H2;
-        const float4 lo4 = src[2 * j], hi4 = src[2 * j + 1];
+        const float4* src = reinterpret_cast<const float4*>(wb + win_index(e, l, j * 8, HW1, p));
+        const float4 lo4 = src[0], hi4 = src[1];
         const float cell[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {

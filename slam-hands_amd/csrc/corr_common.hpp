@@ -15,6 +15,14 @@ typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
 constexpr int kMaxEdgesPerLaunch = 64;
 constexpr int kWinCells = 64;  // 8x8 window cells per level
 
+// Lookup windows of a launch are stored row-major per window row,
+// [slot][level][row][HW][8] (cell = 8*row + column of the 8x8 window): a
+// window row of 8 consecutive sources is 256 contiguous bytes, so the
+// correlation kernel's stores and the lookup's per-pixel reads are coalesced.
+__host__ __device__ __forceinline__ size_t win_index(int slot, int l, int cell, int HW, int p) {
+    return ((((size_t)slot * kMaxLevels + l) * 8 + (cell >> 3)) * HW + p) * 8 + (cell & 7);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs; remap the linear id so
 // each XCD walks a contiguous range of (edge, tile) ids and its L2 holds the
 // few feature maps of the edges it is working on.

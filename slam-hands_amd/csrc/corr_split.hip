@@ -6,7 +6,7 @@
 // the radius-3 lookup that batch_corr_sample_kernel (main.cu:1175-1217) makes
 // of every level. The lookup of source pixel p at level l only reads the 8x8
 // cells from (floor(x*2^-l) - 3, floor(y*2^-l) - 3); those windows are all this
-// path produces, into [slot][HW][4 levels][8][8] (k_corr_lookup_win then
+// path produces, into [slot][4 levels][8 rows][HW][8] (k_corr_lookup_win then
 // weights them into the 196 output channels).
 //
 // Pooling is linear in the target, so level l of the pyramid is the product of
@@ -29,11 +29,11 @@
 // accumulation; the dropped lo.lo term is ~2^-16 relative), staging 16-channel
 // chunks through LDS in a 3-stage ring filled by direct-to-LDS loads, so the
 // loads of chunk k+2 are in flight during the MFMAs of chunk k. The
-// accumulator tile is then transposed through LDS ([target][source]) and, per
-// source and level, one wave writes the window cells that fall inside the
-// tile, one lane per cell: one masked store of 64 consecutive floats. Only ~2%
-// of the level-0 products are window cells, and none of them costs more than
-// its LDS round trip.
+// accumulator tile is then transposed through LDS ([target][source]), and the
+// window cells that fall inside the tile are read back with one lane per
+// (source, window column), walking the 8 window rows: each masked store
+// covers one row of 8 sources' windows. Only ~2% of the level-0 products are
+// window cells, and none of them costs more than its LDS round trip.
 #include <algorithm>
 #include <climits>
 #include <type_traits>
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // window rows, so every read and store instruction covers 8 sources x 8
     // consecutive cells and all per-source set-up is plain per-lane arithmetic.
     const int g8 = lane >> 3, cx = lane & 7;
-    float* wout = win + (size_t)(slot0 + e) * HW * (kMaxLevels * kWinCells) + cx;
+
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
         if (sb) lds_barrier();  // the first half's cells have all been read
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
             const bool pin = p0 + lsrc < HW;
             const float* Tcol = &sm.u.T[0][s];
-            float* wp = wout + (size_t)std::min(p0 + lsrc, HW - 1) * (kMaxLevels * kWinCells);
+            float* wp = win + win_index(slot0 + e, 0, cx, HW, std::min(p0 + lsrc, HW - 1));
 #pragma unroll
             for (int l = 0; l < kMaxLevels; l++) {
                 if (lr0[l] > lr1[l]) continue;  // level not in this tile
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                 }
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++)
-                    if (ok[cy]) wp[l * kWinCells + cy * 8] = alpha * v[cy];
+                    if (ok[cy]) wp[(size_t)(l * 8 + cy) * HW * 8] = alpha * v[cy];
             }
         }
     }

@@ -71,7 +71,7 @@ struct slk_ctx {
     float alpha = 1.0f / 16.0f;
     int corr_prec = SLK_PREC_BF16X3;  // contraction of fp32 features
     int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
-    // batched-path scratch: 8x8 lookup windows [max_batch][HW][4 levels][64]
+    // batched-path scratch: 8x8 lookup windows [max_batch][4 levels][8 rows][HW][8]
     slk::DevBuf batch_win;
     // batched-path operands: bf16 hi/lo split of every level's features per
     // frame slot, and the fp32 pooled features they are split from
