@@ -20,6 +20,11 @@ launch stream. `cpu_baseline` times the CPU oracle (oracle/, a C port with
 OpenMP) on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+`--backend` instead times the backend configuration (200 keyframes, 2000
+edges: correlation + lookup of every edge in 48-edge launches, then 5 BA
+iterations over 198 free poses with the dense 1188x1188 Schur system) and
+prints one JSON line for it; the headline line above is unaffected.
 """
 import argparse
 import json
@@ -38,7 +43,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 # HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
 # (profiles/corr_window48_pmc_traffic.md)
-TRAFFIC_BYTES = 300988286
+TRAFFIC_BYTES = 301194203
 PEAK_HBM_GBS = 8000.0
 
 
@@ -51,6 +56,8 @@ def parse():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the run, one device-to-device copy of MIB MiB (the plain "
                          "copy kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--backend", action="store_true",
+                    help="time the 200-keyframe backend configuration instead")
     ap.add_argument("--cpu-edges", type=int, default=48,
                     help="edges of the window the CPU baseline runs (bounded sample)")
     return ap.parse_args()
@@ -70,6 +77,8 @@ def main():
     if H.device_count() < 1:
         raise SystemExit("bench.py: no GPU visible")
     slk.lib()  # fails loudly if libslk.so is missing
+    if args.backend:
+        return backend(args, slk, wl, H)
 
     h, w, C, n, B = 48, 64, 128, 12, 48
     HW = h * w
@@ -219,6 +228,83 @@ def main():
         H.free(dst)
         print(f"bench.py: copy calibration {nbytes} bytes device-to-device", file=sys.stderr,
               flush=True)
+
+
+def backend(args, slk, wl, H):
+    """The backend configuration: correlation + lookup
+    of all 2000 edges of a 200-keyframe graph in 48-edge launches, then 5 BA
+    iterations over 198 free poses (dense 1188x1188 Schur system, blocked
+    multi-workgroup Cholesky). One JSON line; synthetic inputs resident in HBM."""
+    h, w, C, n, B = 48, 64, 128, 200, 48
+    HW = h * w
+    iters = 5
+    lm, ep = 1e-5, 1e-2
+    ii, jj = wl.backend_edges(n, 2000)
+    M = len(ii)
+    fm = wl.frames(n, C, h, w, seed=0)
+    coords = wl.flow_coords(B, h, w, seed=1)
+    p = wl.ba_problem(n=n, h=h, w=w, ii=ii, jj=jj, seed=21)
+    ctx = slk.Context(h, w, C=C, max_batch=B, corr_scale=wl.CORR_ALPHA_REF)
+    D = slk.DeviceArray.from_host
+    d_f, d_c = D(fm), D(coords)
+    d_out = slk.DeviceArray((B, 196, HW))
+    dp = {k: D(p[k]) for k in ("poses", "disps", "intr", "target", "weight", "eta", "ii", "jj")}
+    stream = H.stream()
+    nb = (M + B - 1) // B
+    batches = [(ii[b * B:(b + 1) * B], jj[b * B:(b + 1) * B]) for b in range(nb)]
+
+    def corr():
+        for bi, bj in batches:
+            ctx.batch_build_and_sample_correlation(d_f, bi, bj, d_c, d_out, stream=stream)
+
+    def ba():
+        ctx.ba_iterate(dp["poses"], dp["disps"], dp["intr"], dp["target"], dp["weight"],
+                       dp["eta"], dp["ii"], dp["jj"], ii, jj, p["t0"], p["t1"], lm, ep,
+                       stream=stream)
+
+    def timed(fn, k):
+        H.sync()
+        e0, e1 = H.event(), H.event()
+        H.record(e0, stream)
+        for _ in range(k):
+            fn()
+        H.record(e1, stream)
+        ms = H.elapsed_ms(e0, e1)
+        H.sync()
+        return ms
+
+    corr()
+    ba()
+    H.sync()
+    if ctx.ba_status(stream) != slk.SLK_OK:
+        raise SystemExit("bench.py: backend BA system not positive definite")
+    steps = max(1, min(args.steps, 5))
+    corr_ms = timed(corr, steps) / steps
+    ba_ms = timed(ba, steps * iters) / (steps * iters)
+    ctx.profile_enable(True)
+    ba()
+    H.sync()
+    prof = ctx.profile()
+    ctx.profile_enable(False)
+    out = {
+        "metric": "backend: corr edges/s + BA iters/s (200 keyframes, 2000 edges, 1 MI355X)",
+        "value": round(M / (corr_ms / 1e3 + iters * ba_ms / 1e3), 1),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "higher_is_better": True,
+        "dtype": "f32 correlation (bf16x3 MFMA) / f64 BA",
+        "data": "synthetic (workloads.py backend graph)",
+        "config": {"workload": "backend corr + 5x ba", "frames": n, "edges": M, "h": h, "w": w,
+                   "C": C, "free_poses": p["t1"] - p["t0"], "system": 6 * (p["t1"] - p["t0"]),
+                   "ba_iters": iters, "lm": lm, "ep": ep},
+        "corr_ms_all_edges": round(corr_ms, 3),
+        "corr_edges_per_s": round(M / (corr_ms / 1e3), 1),
+        "ba_iter_ms": round(ba_ms, 4),
+        "ba_iters_per_s": round(1e3 / ba_ms, 1),
+        "ba_kernels_us": {k: round(1e3 * v[0] / v[1], 1) for k, v in prof.items()},
+    }
+    print(json.dumps(out), flush=True)
 
 
 def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
