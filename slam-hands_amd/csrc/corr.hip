@@ -798,6 +798,9 @@ int corr_alloc(slk_ctx* ctx) {
     }
     SLK_TRY(ctx->zero_idx.ensure(sizeof(int) * 4));
     SLK_HIP(hipMemset(ctx->zero_idx.ptr, 0, sizeof(int) * 4));
+    // the zeroed buffers are in place before work on any stream (also a
+    // non-blocking one) can read them
+    SLK_HIP(hipDeviceSynchronize());
     return SLK_OK;
 }
 

@@ -162,33 +162,106 @@ __global__ __launch_bounds__(256) void k_feat_split(const Tin* __restrict__ fm, 
 // concatenated target indices [off + ya*w + xa, off + yb*w + xb], and every
 // target tile in that span is marked (a superset of the tiles holding a cell).
 // Tiles not marked are skipped by k_corr_split_win: they would store nothing.
-// Grid (mtiles, edges), 128 threads (one source each); LDS bitmap of the
-// edge's target tiles.
-__global__ __launch_bounds__(128) void k_tile_mask(const float* __restrict__ coords,
-                                                   unsigned char* __restrict__ mask, Geom g,
-                                                   int mtiles, int ntiles) {
+// Grid (edges), 1024 threads; an LDS bitmap of the edge's mtiles * ntiles
+// tiles, then the marked ones compacted in tile order into the edge's segment
+// list[e * tpe ..] (ids mt * ntiles + nt) and their number into
+// ctr[kCtrCount + e]. Workgroup 0 also zeroes the tile counters of
+// k_corr_split_win, which runs after this kernel on the same stream.
+constexpr int kMaskThreads = 1024;
+constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
+constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
+constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
+__global__ __launch_bounds__(kMaskThreads) void k_tile_mask(const float* __restrict__ coords,
+                                                            int* __restrict__ list,
+                                                            int* __restrict__ ctr, Geom g,
+                                                            int mtiles, int ntiles) {
     extern __shared__ unsigned bits[];
-    const int mt = blockIdx.x, e = blockIdx.y;
-    const int nw = (ntiles + 31) / 32;
-    for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[i] = 0u;
+    __shared__ int wave_sum[kMaskThreads / 64];
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tpe = mtiles * ntiles;
+    const int nw = (tpe + 31) / 32;
+    for (int i = tid; i < nw; i += kMaskThreads) bits[i] = 0u;
+    if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     __syncthreads();
-    const int p = mt * kSrcTile + threadIdx.x;
-    if (p < g.HW) {
-        const float* cc = coords + (size_t)e * 2 * g.HW;
-        const int fx = floor_clamped(cc[p]), fy = floor_clamped(cc[g.HW + p]);
-        for (int l = 0; l < g.levels; l++) {
-            const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
-            const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
-            const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
-            if (xa > xb || ya > yb) continue;
-            const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
-            const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
-            for (int t = lo; t <= hi; t++) atomicOr(&bits[t >> 5], 1u << (t & 31));
+    // A wave's 64 sources lie in one source tile (kSrcTile is a multiple of
+    // 64). When an edge's target tiles fit a 64-bit mask, each lane builds the
+    // mask of the tiles its windows touch, the wave ORs them by shuffles and
+    // lane 0 merges the result into the bitmap; otherwise every lane marks
+    // its tiles in the bitmap itself.
+    const float* cc = coords + (size_t)e * 2 * g.HW;
+    constexpr int kU = 4;  // sources per thread whose coordinates load together
+    for (int pb = 0; pb < g.HW; pb += kU * kMaskThreads) {
+        int fx[kU], fy[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int p = std::min(pb + u * kMaskThreads + tid, g.HW - 1);
+            fx[u] = floor_clamped(cc[p]);
+            fy[u] = floor_clamped(cc[g.HW + p]);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int pw = pb + u * kMaskThreads + (tid & ~63);  // the wave's first source
+            if (pw >= g.HW) break;                                // uniform
+            const bool in = pw + lane < g.HW;
+            const int row = pw / kSrcTile * ntiles;  // first tile id of the source tile
+            unsigned long long m = 0ull;
+            for (int l = 0; l < g.levels; l++) {
+                const int ox = (fx[u] >> l) - 3, oy = (fy[u] >> l) - 3;
+                const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
+                const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
+                if (!in || xa > xb || ya > yb) continue;
+                const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
+                const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
+                if (ntiles <= 64)
+                    m |= (hi == 63 ? 0ull : (2ull << hi)) - (1ull << lo);
+                else
+                    for (int t = row + lo; t <= row + hi; t++)
+                        atomicOr(&bits[t >> 5], 1u << (t & 31));
+            }
+            if (ntiles > 64) continue;  // uniform
+            unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                m0 |= __shfl_xor(m0, off, 64);
+                m1 |= __shfl_xor(m1, off, 64);
+            }
+            if (lane == 0) {
+                // bit t of (m1:m0) is tile row + t; a word is touched only
+                // when it receives a set bit, so only words below nw are
+                const int w0 = row >> 5, sh = row & 31;
+                const unsigned part[2] = {m0, m1};
+                for (int k = 0; k < 2; k++) {
+                    const unsigned a = part[k] << sh, b = sh ? part[k] >> (32 - sh) : 0u;
+                    if (a) atomicOr(&bits[w0 + k], a);
+                    if (b) atomicOr(&bits[w0 + k + 1], b);
+                }
+            }
         }
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < ntiles; t += blockDim.x)
-        mask[((size_t)e * mtiles + mt) * ntiles + t] = (unsigned char)((bits[t >> 5] >> (t & 31)) & 1u);
+    // compaction, kMaskThreads tiles a round: ballot ranks within a wave,
+    // wave totals through LDS
+    int* seg = list + (size_t)e * tpe;
+    int base = 0;
+    for (int t0 = 0; t0 < tpe; t0 += kMaskThreads) {
+        const int t = t0 + tid;
+        const bool m = t < tpe && ((bits[t >> 5] >> (t & 31)) & 1u);
+        const unsigned long long bal = __ballot(m);
+        const int rank = __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_sum[wv] = __builtin_popcountll(bal);
+        __syncthreads();
+        int before = 0, all = 0;
+#pragma unroll
+        for (int q = 0; q < kMaskThreads / 64; q++) {
+            const int v = wave_sum[q];
+            before += q < wv ? v : 0;
+            all += v;
+        }
+        if (m) seg[base + before + rank] = t;
+        base += all;
+        __syncthreads();  // wave_sum is rewritten by the next round
+    }
+    if (tid == 0) ctr[kCtrCount + e] = base;
 }
 
 struct alignas(16) SplitSmem {
@@ -207,7 +280,19 @@ struct alignas(16) SplitSmem {
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
+// One direct-to-LDS load per lane (16 or 4 bytes): lane l reads p and writes
+// LDS bytes m0 + size*l (m0 = the wave's region). As inline assembly the
+// compiler does not track these LDS writes, so it inserts no waits for them
+// before the LDS accesses it cannot prove disjoint (which, in the tile loop,
+// would mean waiting for every chunk in flight). Every read of staged data is
+// ordered by the explicit vmcnt waits and barriers of the chunk loop.
+__device__ __forceinline__ void dma_x4(const void* p, unsigned lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma_x1(const void* p, unsigned lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(p), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ unsigned lds_addr(const void* p) { return (unsigned)(size_t)p; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8): vmcnt(6) lgkmcnt(0), vmcnt(0) lgkmcnt(0), and lgkmcnt(0) alone
@@ -230,20 +315,53 @@ __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Grid: n_edges * mtiles * ntiles workgroups of 256 threads (target tile
-// fastest). Waves form a 2x2 grid: wave (wm, wn) owns sources wm*64..+63 and
-// targets wn*128..+127 of the tile, eight 32x32 accumulator blocks.
+// Grid: a fixed number of workgroups of 256 threads, two per CU, each taking
+// marked tiles (k_tile_mask) one at a time from its XCD's counter: tile
+// index idx runs over the edges' segments concatenated, workgroup blockIdx % 8
+// runs on that XCD and serves the XCD's contiguous eighth of those indices,
+// so the edges an XCD works on stay in its L2, and no CU idles while tiles
+// remain. Waves form a 2x2 grid: wave (wm, wn) owns sources
+// wm*64..+63 and targets wn*128..+127 of a tile, eight 32x32 accumulator
+// blocks.
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* __restrict__ feat, EdgeSlots es, const float* __restrict__ coords,
     float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles,
-    const unsigned char* __restrict__ tmask) {
+    int nedges, const int* __restrict__ list, int* __restrict__ ctr) {
     __shared__ SplitSmem sm;
+    __shared__ int next_tile;
     const int tpe = mtiles * ntiles;
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int e = bid / tpe;
-    const int r = bid - e * tpe;
+    // lane e of every wave holds pre = the number of marked tiles of the
+    // edges before e (nedges <= 64); cnt = all of them
+    int pre, cnt;
+    {
+        const int ln = threadIdx.x & 63;
+        const int c = ln < nedges ? ctr[kCtrCount + ln] : 0;
+        int incl = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (ln >= off) incl += v;
+        }
+        pre = incl - c;
+        cnt = __builtin_amdgcn_readlane(incl, 63);
+    }
+    const int xcd = blockIdx.x & 7;
+    const int lo = (int)((long long)cnt * xcd / 8), hi = (int)((long long)cnt * (xcd + 1) / 8);
+    // The next tile's index is taken at the start of a tile and published in
+    // LDS after the chunk loop (whose last wait covers the atomic's return).
+    int* const counter = ctr + kCtrXcd + xcd;
+    if (threadIdx.x == 0) next_tile = lo + atomicAdd(counter, 1);
+    lds_barrier();
+    for (int idx = __builtin_amdgcn_readfirstlane(next_tile); idx < hi;
+         idx = __builtin_amdgcn_readfirstlane(next_tile)) {  // uniform
+    int taken;  // thread 0 only
+    if (threadIdx.x == 0) taken = atomicAdd(counter, 1);
+    // the edge of tile idx: the last lane whose prefix is <= idx (edges
+    // with no marked tile share their successor's prefix)
+    const bool before_idx = (int)(threadIdx.x & 63) < nedges && pre <= idx;
+    const int e = __builtin_popcountll(__ballot(before_idx)) - 1;
+    const int r = list[(size_t)e * tpe + (idx - __builtin_amdgcn_readlane(pre, e))];
     const int mt = r / ntiles, nt = r - mt * ntiles;
-    if (!tmask[bid]) return;  // no window cell of these sources in this tile
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
@@ -268,16 +386,12 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int wdst = wave * 512;  // this wave's 1 KB of a 4 KB region, in u16
     auto issue = [&](int k, int st) {
         const size_t o = (size_t)k * kstep;
-        __builtin_amdgcn_global_load_lds(ga + o, (lds_ptr)&sm.u.st.A[st][0][wdst], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(ga + plane + o, (lds_ptr)&sm.u.st.A[st][1][wdst], 16,
-                                         0, 0);
-        __builtin_amdgcn_global_load_lds(gb0 + o, (lds_ptr)&sm.u.st.B[st][0][wdst], 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(gb1 + o, (lds_ptr)&sm.u.st.B[st][0][2048 + wdst], 16,
-                                         0, 0);
-        __builtin_amdgcn_global_load_lds(gb0 + plane + o, (lds_ptr)&sm.u.st.B[st][1][wdst], 16,
-                                         0, 0);
-        __builtin_amdgcn_global_load_lds(gb1 + plane + o,
-                                         (lds_ptr)&sm.u.st.B[st][1][2048 + wdst], 16, 0, 0);
+        dma_x4(ga + o, lds_addr(&sm.u.st.A[st][0][wdst]));
+        dma_x4(ga + plane + o, lds_addr(&sm.u.st.A[st][1][wdst]));
+        dma_x4(gb0 + o, lds_addr(&sm.u.st.B[st][0][wdst]));
+        dma_x4(gb1 + o, lds_addr(&sm.u.st.B[st][0][2048 + wdst]));
+        dma_x4(gb0 + plane + o, lds_addr(&sm.u.st.B[st][1][wdst]));
+        dma_x4(gb1 + plane + o, lds_addr(&sm.u.st.B[st][1][2048 + wdst]));
     };
 
     f32x16 acc[2][4];
@@ -341,8 +455,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     {
         const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
         const int pc = std::min(p0 + half * 64 + lane, HW - 1);
-        __builtin_amdgcn_global_load_lds(coords + ((size_t)e * 2 + comp) * HW + pc,
-                                         (lds_ptr)&sm.crd[comp][half * 64], 4, 0, 0);
+        dma_x1(coords + ((size_t)e * 2 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
     }
     if (nk > 1) issue(1, 1);
     for (int k = 0; k < nk; k++) {
@@ -356,6 +469,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
         compute(k % kStages);
     }
+    if (tid == 0) next_tile = lo + taken;  // read after the end-of-tile barrier
     if (tid < kSrcTile) {
         const bool in = p0 + tid < HW;
         sm.org[tid][0] = in ? floor_clamped(sm.crd[0][tid]) : -(1 << 20);  // matches no cell
@@ -437,6 +551,8 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                     if (ok[cy]) wp[(size_t)(l * 8 + cy) * HW * 8] = alpha * v[cy];
             }
         }
+    }
+    lds_barrier();  // T is free again, next_tile is visible
     }
 }
 
@@ -521,15 +637,16 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
     {
         ProfScope ps(ctx, "corr_tile_mask", stream);
-        const size_t shm = (size_t)((ntiles + 31) / 32) * sizeof(unsigned);
-        hipLaunchKernelGGL(k_tile_mask, dim3(mtiles, n), dim3(kSrcTile), shm, stream, coords,
-                           ctx->tile_mask.as<unsigned char>(), g, mtiles, ntiles);
+        const size_t shm = (size_t)((mtiles * ntiles + 31) / 32) * sizeof(unsigned);
+        hipLaunchKernelGGL(k_tile_mask, dim3(n), dim3(kMaskThreads), shm, stream, coords,
+                           ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), g, mtiles, ntiles);
     }
     {
         ProfScope ps(ctx, "corr_window", stream);
-        hipLaunchKernelGGL(k_corr_split_win, dim3((unsigned)total), dim3(256), 0, stream,
+        hipLaunchKernelGGL(k_corr_split_win, dim3(ctx->ws_grid), dim3(256), 0, stream,
                            ctx->split_feat.as<unsigned short>(), es, coords, win, slot0, g,
-                           ctx->alpha, mtiles, ntiles, ctx->tile_mask.as<unsigned char>());
+                           ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
+                           ctx->tile_ctr.as<int>());
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
@@ -547,8 +664,15 @@ int corr_split_alloc(slk_ctx* ctx) {
     SLK_TRY(ctx->split_pool.ensure(slots * (size_t)g.C * std::max(g.pool_hw, 1) * sizeof(float)));
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
-    SLK_TRY(ctx->tile_mask.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles *
-                                  ntiles));
+    const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
+    SLK_TRY(ctx->tile_list.ensure(tiles * sizeof(int)));
+    SLK_TRY(ctx->tile_ctr.ensure(kCtrInts * sizeof(int)));
+    // the correlation workgroups: two per CU, a multiple of the 8 XCDs
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) !=
+        hipSuccess)
+        return fail(SLK_E_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
+    ctx->ws_grid = std::max(8, cus / 8 * 8) * 2;
     return SLK_OK;
 }
 

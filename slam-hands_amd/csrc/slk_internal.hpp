@@ -76,7 +76,9 @@ struct slk_ctx {
     // batched-path operands: bf16 hi/lo split of every level's features per
     // frame slot, and the fp32 pooled features they are split from
     slk::DevBuf split_feat, split_pool;
-    slk::DevBuf tile_mask;  // [edges][source tiles][target tiles] tile holds a window cell
+    slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
+    slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
+    int ws_grid = 0;        // workgroups of the batched correlation kernel
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
     bool single_built = false;

@@ -161,6 +161,30 @@ def test_window_48_edges_matches_oracle(slk, prec):
         assert_close_rel(out[e][:, pix], ref_sub, what=f"edge {e} sampled")
 
 
+@pytest.mark.parametrize("h,w", [(96, 128), (100, 128)])
+def test_window_large_frames_sampled(slk, h, w):
+    """Large feature maps, 12 edges in one launch. 96x128: 64 target tiles
+    per source tile, the widest the tile marking handles with a 64-bit mask
+    per lane (and the top bit set); 100x128: 67, which takes the per-tile
+    marking path, and 6700 tiles per edge, several rounds of the tile
+    compaction. Every edge is checked on 48 random pixels by direct fp64
+    evaluation of their windows."""
+    announce(f"corr window {h}x{w}, 12 edges")
+    f, ii, jj, coords, out = _window(slk, 6, h, w, 12, seed=50, max_batch=12)
+    assert np.all(np.isfinite(out))
+    rng = np.random.default_rng(1)
+    pix = rng.choice(h * w, 48, replace=False)
+    for e in range(12):
+        fi = f[ii[e]].reshape(128, -1).astype(np.float64)
+        fj = f[jj[e]].reshape(128, -1).astype(np.float64)
+        vol = (fi[:, pix].T @ fj) / 16.0
+        pyr = [vol.reshape(48, h, w).astype(np.float32)]
+        for _ in range(3):
+            pyr.append(orc.avg_pool_2x2(pyr[-1]))
+        assert_close_rel(out[e][:, pix], _lookup_rows(pyr, coords[e][:, pix]),
+                         what=f"edge {e} sampled")
+
+
 def _lookup_rows(pyr, coords):
     """Lookup of selected source rows: pyr[l] is [n, h>>l, w>>l] for n chosen
     pixels whose coords are [2, n]; uses the oracle's level routine."""
