@@ -222,6 +222,63 @@ int slk_ba_evt6x1(const float* E, const float* x, const int* idx, float* w, int 
 int slk_ba_depth_update(const float* Q, const float* w, const float* dw, float* disps,
                         const int* kf_map, int N_kf, int HW, hipStream_t stream);
 
+/* ------------------------------------------------------ update-pass glue */
+/* The steps of CudaDroid::run_update_pass around correlation and BA
+ * (cuda_slam/main.cu:2186-2400, cuda_pipeline/slam.cuh:3090-3170). Rows are
+ * `row` consecutive floats; index arrays without `_host` are on the device. */
+
+/* compute_motion_kernel(motion, coords1, coords0, target, batch, HW),
+ * main.cu:1250-1273: motion [batch][4][h*w] = clamp(coords1 - coords0,
+ * target - coords1 to [-64, 64]). coords0 == NULL takes the identity grid
+ * that alloc_coords0 (main.cu:2150-2163) uploads, without reading it. */
+int slk_compute_motion(float* motion, const float* coords1, const float* coords0,
+                       const float* target, int batch, int h, int w, hipStream_t stream);
+/* alloc_coords0 (main.cu:2150-2163) written on the device: coords0
+ * [batch][2][h*w], x = column, y = row. */
+int slk_fill_coords0(float* coords0, int batch, int h, int w, hipStream_t stream);
+/* compute_target_kernel(target, weight_out, coords, delta, wt_raw, num_edges,
+ * HW), main.cu:1282-1301: delta and wt_raw are [num_edges][3][hw]. */
+int slk_compute_target(float* target, float* weight_out, const float* coords,
+                       const float* delta, const float* wt_raw, int num_edges, int hw,
+                       hipStream_t stream);
+/* dst row e = src row idx[e] (idx == NULL: row e), e < n <= 65535: one launch
+ * for the per-edge cudaMemcpy loops that load hidden states and inps
+ * (main.cu:2216-2224: batch_nets from edge_nets + bs, idx NULL; batch_inps
+ * from inps with idx = ii + bs). */
+int slk_gather_rows(float* dst, const float* src, const int* idx, int n, long row,
+                    hipStream_t stream);
+/* dst row idx[e] = src row e (idx == NULL: row e), idx entries distinct: the
+ * loops that save hidden states and conv1 features (main.cu:2245-2252) and
+ * eta of the active keyframes (main.cu:2303-2309, idx = the active list of
+ * slk_scatter_mean). */
+int slk_scatter_rows(float* dst, const float* src, const int* idx, int n, long row,
+                     hipStream_t stream);
+/* GraphAgg scatter_mean, main.cu:2258-2296: the active keyframes are the
+ * distinct ii_host values ascending (num_active_host of them, optionally
+ * written to active_kf on the device and to active_kf_host); dst row a is the
+ * sum of src rows e with ii_host[e] == active[a], taken in edge order from
+ * zero, then, for more than one row, S + (1/count - 1) * S as one fused
+ * multiply-add (scale_add_kernel under --use_fast_math). Bitwise equal to the
+ * reference's sequence. n <= 65535. */
+int slk_scatter_mean(slk_ctx* ctx, float* dst, const float* src, const int* ii_host, int n,
+                     long row, int* active_kf, int* active_kf_host, int* num_active_host,
+                     hipStream_t stream);
+/* The BA edge set of run_update_pass, main.cu:2312-2390: t0 = forced_t0 if
+ * >= 0, else max(1, min(ii_host) + 1) (num_keyframes + 1 without edges);
+ * the active edges, followed, when use_inactive and n_inac > 0, by the
+ * inactive edges with ii >= t0 - 3 and jj >= t0 - 3 in their order. Writes
+ * the indices to ba_ii_host/ba_jj_host (capacity n + n_inac) and ba_ii/ba_jj,
+ * the target and weight rows [count][2][hw] to ba_target/ba_weight (one
+ * launch), *count and *t0. The BA then runs on (ba_*, count, t0,
+ * num_keyframes) as in the reference. */
+int slk_ba_edge_set(slk_ctx* ctx, const int* ii_host, const int* jj_host, int n,
+                    const int* ii_inac_host, const int* jj_inac_host, int n_inac,
+                    const float* target, const float* weight, const float* target_inac,
+                    const float* weight_inac, int hw, int num_keyframes, int forced_t0,
+                    int use_inactive, int* ba_ii_host, int* ba_jj_host, int* ba_ii,
+                    int* ba_jj, float* ba_target, float* ba_weight, int* count, int* t0,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

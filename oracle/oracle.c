@@ -744,3 +744,114 @@ int orc_ba_iterate(float* poses, float* disps, const float* intr,
     free(E); free(Cq); free(wv);
     return status;
 }
+
+/* ------------------------------------------------------------------------ */
+/* update-pass glue                                                          */
+/* ------------------------------------------------------------------------ */
+
+static float clamp64(float v) { return fminf(fmaxf(v, -64.0f), 64.0f); } /* main.cu:1268 */
+
+void orc_compute_motion(float* motion, const float* coords1, const float* coords0,
+                        const float* target, int batch, int h, int w) {
+    const long HW = (long)h * w;
+    for (int e = 0; e < batch; e++)
+        for (long k = 0; k < HW; k++) {
+            const float* c1 = coords1 + (long)e * 2 * HW;
+            const float* tg = target + (long)e * 2 * HW;
+            /* coords0_buf holds x = pixel column, y = pixel row (main.cu:2157-2158) */
+            const float c0x = coords0 ? coords0[(long)e * 2 * HW + k] : (float)(k % w);
+            const float c0y = coords0 ? coords0[(long)e * 2 * HW + HW + k] : (float)(k / w);
+            float* m = motion + (long)e * 4 * HW;
+            m[k] = clamp64(c1[k] - c0x);                     /* main.cu:1269 */
+            m[HW + k] = clamp64(c1[HW + k] - c0y);           /* main.cu:1270 */
+            m[2 * HW + k] = clamp64(tg[k] - c1[k]);          /* main.cu:1271 */
+            m[3 * HW + k] = clamp64(tg[HW + k] - c1[HW + k]); /* main.cu:1272 */
+        }
+}
+
+void orc_compute_target(float* target, float* weight_out, const float* coords,
+                        const float* delta, const float* wt_raw, int n, int hw) {
+    for (int e = 0; e < n; e++)
+        for (int c = 0; c < 2; c++)
+            for (int k = 0; k < hw; k++) {
+                const long o2 = ((long)e * 2 + c) * hw + k, o3 = ((long)e * 3 + c) * hw + k;
+                target[o2] = coords[o2] + delta[o3]; /* main.cu:1295-1296 */
+                weight_out[o2] = wt_raw[o3];         /* main.cu:1299 */
+            }
+}
+
+void orc_gather_rows(float* dst, const float* src, const int* idx, int n, long row) {
+    for (int e = 0; e < n; e++)
+        memcpy(dst + (long)e * row, src + (long)(idx ? idx[e] : e) * row, row * sizeof(float));
+}
+
+void orc_scatter_rows(float* dst, const float* src, const int* idx, int n, long row) {
+    for (int e = 0; e < n; e++)
+        memcpy(dst + (long)(idx ? idx[e] : e) * row, src + (long)e * row, row * sizeof(float));
+}
+
+static int cmp_int(const void* a, const void* b) {
+    const int x = *(const int*)a, y = *(const int*)b;
+    return (x > y) - (x < y);
+}
+
+int orc_scatter_mean(float* dst, const float* src, const int* ii, int n, long row,
+                     int* active) {
+    /* active keyframes: std::set over ii_host, ascending (main.cu:2265-2269) */
+    int* tmp = (int*)malloc(sizeof(int) * (n > 0 ? n : 1));
+    memcpy(tmp, ii, sizeof(int) * n);
+    qsort(tmp, n, sizeof(int), cmp_int);
+    int na = 0;
+    for (int e = 0; e < n; e++)
+        if (na == 0 || tmp[e] != active[na - 1]) active[na++] = tmp[e];
+    free(tmp);
+    for (int a = 0; a < na; a++) {
+        float* d = dst + (long)a * row;
+        for (long k = 0; k < row; k++) d[k] = 0.0f; /* cudaMemset, main.cu:2272-2273 */
+        int count = 0;
+        for (int e = 0; e < n; e++) /* edge order, main.cu:2281-2288 */
+            if (ii[e] == active[a]) {
+                const float* x = src + (long)e * row;
+                for (long k = 0; k < row; k++) d[k] = fmaf(1.0f, x[k], d[k]);
+                count++;
+            }
+        if (count > 1) { /* main.cu:2291-2296 */
+            const float inv = 1.0f / (float)count;
+            for (long k = 0; k < row; k++) d[k] = fmaf(inv - 1.0f, d[k], d[k]);
+        }
+    }
+    return na;
+}
+
+int orc_ba_edge_set(const int* ii, const int* jj, int n, const int* ii_inac,
+                    const int* jj_inac, int n_inac, const float* target,
+                    const float* weight, const float* target_inac,
+                    const float* weight_inac, int hw, int num_keyframes, int forced_t0,
+                    int use_inactive, int* ba_ii, int* ba_jj, float* ba_target,
+                    float* ba_weight, int* t0_out) {
+    int t0 = forced_t0;
+    if (t0 < 0) { /* main.cu:2312-2322 */
+        int mn = num_keyframes;
+        for (int e = 0; e < n; e++) mn = ii[e] < mn ? ii[e] : mn;
+        t0 = mn + 1 > 1 ? mn + 1 : 1;
+    }
+    *t0_out = t0;
+    const long r = 2L * hw;
+    int m = 0;
+    for (int e = 0; e < n; e++, m++) { /* active edges first, main.cu:2331-2333, 2346-2349 */
+        ba_ii[m] = ii[e];
+        ba_jj[m] = jj[e];
+        memcpy(ba_target + m * r, target + e * r, r * sizeof(float));
+        memcpy(ba_weight + m * r, weight + e * r, r * sizeof(float));
+    }
+    if (use_inactive && n_inac > 0) /* main.cu:2330 */
+        for (int e = 0; e < n_inac; e++)
+            if (ii_inac[e] >= t0 - 3 && jj_inac[e] >= t0 - 3) { /* main.cu:2334-2339, 2351-2361 */
+                ba_ii[m] = ii_inac[e];
+                ba_jj[m] = jj_inac[e];
+                memcpy(ba_target + m * r, target_inac + e * r, r * sizeof(float));
+                memcpy(ba_weight + m * r, weight_inac + e * r, r * sizeof(float));
+                m++;
+            }
+    return m;
+}

@@ -115,6 +115,46 @@ int orc_ba_iterate(float* poses, float* disps, const float* intr,
  * Returns 0, or 3 if a pivot is not positive. S is overwritten with L. */
 int orc_cholesky_solve(double* S, double* b, int n);
 
+/* ---------------- update-pass glue (cuda_slam/main.cu:1246-1301, 2186-2400) */
+
+/* compute_motion_kernel (main.cu:1250-1273): motion [batch][4][h*w] =
+ * clamp([coords1 - coords0, target - coords1], -64, 64) per plane; coords0
+ * NULL is the identity grid of alloc_coords0 (main.cu:2150-2163). */
+void orc_compute_motion(float* motion, const float* coords1, const float* coords0,
+                        const float* target, int batch, int h, int w);
+
+/* compute_target_kernel (main.cu:1282-1301): target = coords + delta[:, :2],
+ * weight_out = wt_raw[:, :2]; delta and wt_raw are [n][3][hw]. */
+void orc_compute_target(float* target, float* weight_out, const float* coords,
+                        const float* delta, const float* wt_raw, int n, int hw);
+
+/* The per-edge cudaMemcpy loops of run_update_pass (main.cu:2216-2224,
+ * 2245-2252, 2305-2309): gather dst[e] = src[idx[e]], scatter dst[idx[e]] =
+ * src[e]; idx NULL is the identity; rows of `row` floats. */
+void orc_gather_rows(float* dst, const float* src, const int* idx, int n, long row);
+void orc_scatter_rows(float* dst, const float* src, const int* idx, int n, long row);
+
+/* GraphAgg scatter_mean (main.cu:2258-2296): active = ascending distinct ii
+ * (capacity n); dst row a = rows e with ii[e] == active[a] summed in edge
+ * order from zero (scale_add_kernel with scale 1, nn.cuh:382-385), then for a
+ * count above one dst = fma(1/count - 1, dst, dst) (scale_add_kernel with
+ * src == dst, built with --use_fast_math, so a fused multiply-add).
+ * Returns the number of active keyframes. */
+int orc_scatter_mean(float* dst, const float* src, const int* ii, int n, long row,
+                     int* active);
+
+/* BA edge set of run_update_pass (main.cu:2312-2390): t0 = forced_t0 if
+ * >= 0, else max(1, min(ii) + 1); with use_inactive and n_inac > 0 the edges
+ * are the active ones followed by the inactive ones with ii >= t0 - 3 and
+ * jj >= t0 - 3, in order, and their target/weight rows [2][hw]; otherwise
+ * the active edges alone. Returns the edge count; *t0_out = t0. */
+int orc_ba_edge_set(const int* ii, const int* jj, int n, const int* ii_inac,
+                    const int* jj_inac, int n_inac, const float* target,
+                    const float* weight, const float* target_inac,
+                    const float* weight_inac, int hw, int num_keyframes, int forced_t0,
+                    int use_inactive, int* ba_ii, int* ba_jj, float* ba_target,
+                    float* ba_weight, int* t0_out);
+
 #ifdef __cplusplus
 }
 #endif

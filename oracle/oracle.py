@@ -76,6 +76,21 @@ def lib():
                                      c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_void_p]
         L.orc_ba_iterate.restype = c_int
+        vp = ctypes.c_void_p
+        glue = {
+            "orc_compute_motion": ([_f32p, _f32p, vp, _f32p, c_int, c_int, c_int], None),
+            "orc_compute_target": ([_f32p, _f32p, _f32p, _f32p, _f32p, c_int, c_int], None),
+            "orc_gather_rows": ([_f32p, _f32p, vp, c_int, c_long], None),
+            "orc_scatter_rows": ([_f32p, _f32p, vp, c_int, c_long], None),
+            "orc_scatter_mean": ([_f32p, _f32p, _i32p, c_int, c_long, _i32p], c_int),
+            "orc_ba_edge_set": ([_i32p, _i32p, c_int, _i32p, _i32p, c_int, _f32p, _f32p,
+                                 _f32p, _f32p, c_int, c_int, c_int, c_int, _i32p, _i32p,
+                                 _f32p, _f32p, ctypes.POINTER(c_int)], c_int),
+        }
+        for name, (argtypes, restype) in glue.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
         _lib = L
     return _lib
 
@@ -268,3 +283,93 @@ def cholesky_solve(S, b):
     b = _c(b, np.float64).copy()
     st = lib().orc_cholesky_solve(S, b, len(b))
     return st, b
+
+
+# ------------------------------------------------------------ update glue
+def _ptr_or_null(a, dtype):
+    return None if a is None else _c(a, dtype).ctypes.data
+
+
+def compute_motion(coords1, target, h, w, coords0=None):
+    """compute_motion_kernel (main.cu:1250-1273): [B][4][h*w]; coords0 None
+    is the identity grid of alloc_coords0 (main.cu:2150-2163)."""
+    c1 = _c(coords1, np.float32)
+    B = c1.shape[0]
+    c0 = None if coords0 is None else _c(coords0, np.float32)
+    m = np.zeros((B, 4, h * w), np.float32)
+    lib().orc_compute_motion(m.reshape(-1), c1.reshape(-1),
+                             None if c0 is None else c0.ctypes.data,
+                             _c(target, np.float32).reshape(-1), B, h, w)
+    return m
+
+
+def compute_target(coords, delta, wt_raw):
+    """compute_target_kernel (main.cu:1282-1301): (target, weight) [n][2][hw]."""
+    coords = _c(coords, np.float32)
+    n, _, hw = coords.shape
+    t = np.zeros((n, 2, hw), np.float32)
+    wo = np.zeros((n, 2, hw), np.float32)
+    lib().orc_compute_target(t.reshape(-1), wo.reshape(-1), coords.reshape(-1),
+                             _c(delta, np.float32).reshape(-1),
+                             _c(wt_raw, np.float32).reshape(-1), n, hw)
+    return t, wo
+
+
+def gather_rows(src, idx, n=None):
+    """dst[e] = src[idx[e]] (the per-edge copy loops, main.cu:2216-2224)."""
+    src = _c(src, np.float32)
+    row = int(np.prod(src.shape[1:]))
+    idx = None if idx is None else _c(idx, np.int32)
+    n = len(idx) if idx is not None else n
+    dst = np.zeros((n,) + src.shape[1:], np.float32)
+    lib().orc_gather_rows(dst.reshape(-1), src.reshape(-1),
+                          None if idx is None else idx.ctypes.data, n, row)
+    return dst
+
+
+def scatter_rows(dst, src, idx):
+    """dst[idx[e]] = src[e] (main.cu:2245-2252, 2305-2309), on a copy of dst."""
+    dst = _c(dst, np.float32).copy()
+    src = _c(src, np.float32)
+    row = int(np.prod(src.shape[1:]))
+    idx = None if idx is None else _c(idx, np.int32)
+    lib().orc_scatter_rows(dst.reshape(-1), src.reshape(-1),
+                           None if idx is None else idx.ctypes.data, src.shape[0], row)
+    return dst
+
+
+def scatter_mean(src, ii):
+    """GraphAgg scatter_mean (main.cu:2258-2296): (dst [na][...], active [na])."""
+    src = _c(src, np.float32)
+    ii = _c(ii, np.int32)
+    n = len(ii)
+    row = int(np.prod(src.shape[1:]))
+    dst = np.zeros((max(n, 1),) + src.shape[1:], np.float32)
+    active = np.zeros(max(n, 1), np.int32)
+    na = lib().orc_scatter_mean(dst.reshape(-1), src.reshape(-1), ii, n, row, active)
+    return dst[:na], active[:na]
+
+
+def ba_edge_set(ii, jj, ii_inac, jj_inac, target, weight, target_inac, weight_inac,
+                num_keyframes, forced_t0=-1, use_inactive=True):
+    """BA edge set of run_update_pass (main.cu:2312-2390): dict with ii, jj,
+    target, weight of the combined edges and t0."""
+    ii, jj = _c(ii, np.int32), _c(jj, np.int32)
+    ii_inac, jj_inac = _c(ii_inac, np.int32), _c(jj_inac, np.int32)
+    target, weight = _c(target, np.float32), _c(weight, np.float32)
+    hw = target.shape[2]
+    target_inac = _c(target_inac, np.float32).reshape(-1, 2, hw)
+    weight_inac = _c(weight_inac, np.float32).reshape(-1, 2, hw)
+    cap = max(len(ii) + len(ii_inac), 1)
+    bi = np.zeros(cap, np.int32)
+    bj = np.zeros(cap, np.int32)
+    bt = np.zeros((cap, 2, hw), np.float32)
+    bw = np.zeros((cap, 2, hw), np.float32)
+    t0 = ctypes.c_int(0)
+    m = lib().orc_ba_edge_set(ii, jj, len(ii), ii_inac, jj_inac, len(ii_inac),
+                              target.reshape(-1), weight.reshape(-1),
+                              np.ascontiguousarray(target_inac).reshape(-1),
+                              np.ascontiguousarray(weight_inac).reshape(-1), hw,
+                              int(num_keyframes), int(forced_t0), int(bool(use_inactive)),
+                              bi, bj, bt.reshape(-1), bw.reshape(-1), ctypes.byref(t0))
+    return {"ii": bi[:m], "jj": bj[:m], "target": bt[:m], "weight": bw[:m], "t0": t0.value}

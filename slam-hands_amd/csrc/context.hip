@@ -168,6 +168,8 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     ctx->tile_list.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();
     ctx->zero_idx.release();
+    ctx->glue_stage.release();
+    ctx->glue_idx.release();
     delete ctx;
     return SLK_OK;
 }

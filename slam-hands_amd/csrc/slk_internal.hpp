@@ -83,6 +83,9 @@ struct slk_ctx {
     slk::DevBuf single_lvl[slk::kMaxLevels];
     bool single_built = false;
     slk::DevBuf zero_idx;  // device int {0}
+    // update-pass glue: index lists uploaded through a pinned stage
+    slk::HostStage glue_stage;
+    slk::DevBuf glue_idx;
     slk::BaState* ba = nullptr;
     bool prof = false;
     std::vector<slk::ProfRec> prof_recs;

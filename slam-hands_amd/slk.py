@@ -35,6 +35,8 @@ EXPORTS = [
     "slk_ba_iterate", "slk_ba_status", "slk_ba_last_system", "slk_ba_projective_transform",
     "slk_ba_accum", "slk_ba_damping_q", "slk_ba_eet6x6", "slk_ba_ev6x1", "slk_ba_evt6x1",
     "slk_ba_depth_update",
+    "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
+    "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set",
 ]
 
 
@@ -97,6 +99,14 @@ def lib():
             "slk_ba_ev6x1": [P, P, P, P, P, I, I, P],
             "slk_ba_evt6x1": [P, P, P, P, I, I, I, P],
             "slk_ba_depth_update": [P, P, P, P, P, I, I, P],
+            "slk_compute_motion": [P, P, P, P, I, I, I, P],
+            "slk_fill_coords0": [P, I, I, I, P],
+            "slk_compute_target": [P, P, P, P, P, I, I, P],
+            "slk_gather_rows": [P, P, P, I, L, P],
+            "slk_scatter_rows": [P, P, P, I, L, P],
+            "slk_scatter_mean": [P, P, P, P, I, L, P, P, ctypes.POINTER(I), P],
+            "slk_ba_edge_set": [P, P, P, I, P, P, I, P, P, P, P, I, I, I, I, P, P, P, P, P,
+                                P, ctypes.POINTER(I), ctypes.POINTER(I), P],
         }
         for name, args in sig.items():
             fn = getattr(L_, name)
