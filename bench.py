@@ -21,6 +21,10 @@ OpenMP) on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
+`--glue` times the update-pass glue around the path (motion/target kernels,
+hidden-state gathers and scatters, the keyframe scatter-mean, the BA edge
+set) for one 48-edge batch and prints one JSON line for it.
+
 `--backend` instead times the backend configuration (200 keyframes, 2000
 edges: correlation + lookup of every edge in 48-edge launches, then 5 BA
 iterations over 198 free poses with the dense 1188x1188 Schur system) and
@@ -58,6 +62,8 @@ def parse():
                          "copy kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--backend", action="store_true",
                     help="time the 200-keyframe backend configuration instead")
+    ap.add_argument("--glue", action="store_true",
+                    help="time the update-pass glue of one 48-edge batch instead")
     ap.add_argument("--cpu-edges", type=int, default=48,
                     help="edges of the window the CPU baseline runs (bounded sample)")
     return ap.parse_args()
@@ -79,6 +85,8 @@ def main():
     slk.lib()  # fails loudly if libslk.so is missing
     if args.backend:
         return backend(args, slk, wl, H)
+    if args.glue:
+        return glue(args, slk, wl, H)
 
     h, w, C, n, B = 48, 64, 128, 12, 48
     HW = h * w
@@ -303,6 +311,186 @@ def backend(args, slk, wl, H):
         "ba_iter_ms": round(ba_ms, 4),
         "ba_iters_per_s": round(1e3 / ba_ms, 1),
         "ba_kernels_us": {k: round(1e3 * v[0] / v[1], 1) for k, v in prof.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def glue(args, slk, wl, H):
+    """The update-pass glue of one 48-edge batch of run_update_pass
+    (cuda_slam/main.cu:2186-2390) around correlation and BA, on the 48x64
+    window with 128-channel hidden states: motion features, hidden-state and
+    inps loads, target/weight, hidden-state and conv1 saves, the keyframe
+    scatter-mean and eta write-back, and the BA edge set with 24 inactive
+    edges. One JSON line: the whole glue per batch, each call, the dominant
+    row-copy kernel against HBM peak, the same copies issued the reference's
+    way (one copy per edge and array), and the CPU oracle on the same data."""
+    import ctypes
+
+    h, w, B, nkf, ninac = 48, 64, 48, 12, 24
+    HW = h * w
+    row = 128 * HW
+    L = slk.lib()
+    rng = np.random.default_rng(0)
+    ii, jj = wl.cyclic_edges(nkf)
+    ii_in = rng.integers(0, nkf, ninac).astype(np.int32)
+    jj_in = rng.integers(0, nkf, ninac).astype(np.int32)
+    host = {
+        "coords1": wl.flow_coords(B, h, w, seed=1),
+        "target": wl.flow_coords(B, h, w, seed=2),
+        "nets": rng.normal(size=(B, row)).astype(np.float32),
+        "inps": rng.normal(size=(nkf, row)).astype(np.float32),
+        "agg1": rng.normal(size=(B, row)).astype(np.float32),
+        "delta": rng.normal(size=(B, 3, HW)).astype(np.float32),
+        "wt": rng.random((B, 3, HW)).astype(np.float32),
+        "kf_eta": rng.random((nkf, HW)).astype(np.float32),
+        "target_inac": rng.normal(size=(ninac, 2, HW)).astype(np.float32),
+        "weight_inac": rng.random((ninac, 2, HW)).astype(np.float32),
+    }
+    ctx = slk.Context(h, w, C=128, max_batch=B)
+    D = slk.DeviceArray.from_host
+    d = {k: D(v) for k, v in host.items()}
+    d["ii"] = D(ii.astype(np.int32))
+    for k, shape in [("motion", (B, 4, HW)), ("batch_nets", (B, row)), ("batch_inps", (B, row)),
+                     ("tgt", (B, 2, HW)), ("wgt", (B, 2, HW)), ("all_agg1", (B, row)),
+                     ("kf_agg", (nkf, row)), ("damping", (nkf, HW)),
+                     ("ba_target", (B + ninac, 2, HW)), ("ba_weight", (B + ninac, 2, HW))]:
+        d[k] = slk.DeviceArray(shape)
+    d["act"] = slk.DeviceArray((B,), np.int32)
+    d["ba_ii"] = slk.DeviceArray((B + ninac,), np.int32)
+    d["ba_jj"] = slk.DeviceArray((B + ninac,), np.int32)
+    ii_h, jj_h = np.ascontiguousarray(ii, np.int32), np.ascontiguousarray(jj, np.int32)
+    bi_h, bj_h = np.zeros(B + ninac, np.int32), np.zeros(B + ninac, np.int32)
+    na, cnt, t0 = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    stream = H.stream()
+    ck = slk.check
+
+    calls = {
+        "compute_motion": lambda: ck(L.slk_compute_motion(
+            d["motion"].ptr, d["coords1"].ptr, None, d["target"].ptr, B, h, w, stream)),
+        "gather_nets": lambda: ck(L.slk_gather_rows(
+            d["batch_nets"].ptr, d["nets"].ptr, None, B, row, stream)),
+        "gather_inps": lambda: ck(L.slk_gather_rows(
+            d["batch_inps"].ptr, d["inps"].ptr, d["ii"].ptr, B, row, stream)),
+        "compute_target": lambda: ck(L.slk_compute_target(
+            d["tgt"].ptr, d["wgt"].ptr, d["coords1"].ptr, d["delta"].ptr, d["wt"].ptr, B, HW,
+            stream)),
+        "scatter_nets": lambda: ck(L.slk_scatter_rows(
+            d["nets"].ptr, d["batch_nets"].ptr, None, B, row, stream)),
+        "scatter_agg1": lambda: ck(L.slk_scatter_rows(
+            d["all_agg1"].ptr, d["agg1"].ptr, None, B, row, stream)),
+        "scatter_mean": lambda: ck(L.slk_scatter_mean(
+            ctx.ptr, d["kf_agg"].ptr, d["all_agg1"].ptr, ii_h.ctypes.data, B, row, d["act"].ptr,
+            None, ctypes.byref(na), stream)),
+        "scatter_eta": lambda: ck(L.slk_scatter_rows(
+            d["damping"].ptr, d["kf_eta"].ptr, d["act"].ptr, nkf, HW, stream)),
+        "ba_edge_set": lambda: ck(L.slk_ba_edge_set(
+            ctx.ptr, ii_h.ctypes.data, jj_h.ctypes.data, B, ii_in.ctypes.data,
+            jj_in.ctypes.data, ninac, d["tgt"].ptr, d["wgt"].ptr, d["target_inac"].ptr,
+            d["weight_inac"].ptr, HW, nkf, -1, 1, bi_h.ctypes.data, bj_h.ctypes.data,
+            d["ba_ii"].ptr, d["ba_jj"].ptr, d["ba_target"].ptr, d["ba_weight"].ptr,
+            ctypes.byref(cnt), ctypes.byref(t0), stream)),
+    }
+
+    def step():
+        for fn in calls.values():
+            fn()
+
+    def reference_copies():
+        # the reference's per-edge cudaMemcpy loops of one batch
+        # (main.cu:2216-2224, 2245-2252, 2305-2309) as async device copies
+        rb = row * 4
+        for e in range(B):
+            H.dtod_async(d["batch_nets"].ptr + e * rb, d["nets"].ptr + e * rb, rb, stream)
+            H.dtod_async(d["batch_inps"].ptr + e * rb, d["inps"].ptr + int(ii[e]) * rb, rb,
+                         stream)
+        for e in range(B):
+            H.dtod_async(d["nets"].ptr + e * rb, d["batch_nets"].ptr + e * rb, rb, stream)
+            H.dtod_async(d["all_agg1"].ptr + e * rb, d["agg1"].ptr + e * rb, rb, stream)
+        for a in range(nkf):
+            H.dtod_async(d["damping"].ptr + a * HW * 4, d["kf_eta"].ptr + a * HW * 4, HW * 4,
+                         stream)
+
+    def timed(fn, k):
+        H.sync()
+        e0, e1 = H.event(), H.event()
+        H.record(e0, stream)
+        for _ in range(k):
+            fn()
+        H.record(e1, stream)
+        ms = H.elapsed_ms(e0, e1)
+        H.sync()
+        return ms / k
+
+    for _ in range(max(1, args.warmup)):
+        step()
+        reference_copies()
+    H.sync()
+    k = max(5, min(args.steps, 50))
+    t0w = time.perf_counter()
+    step_ms = timed(step, k)
+    wall = time.perf_counter() - t0w
+    per_call = {name: round(timed(fn, k) * 1e3, 2) for name, fn in calls.items()}
+    copies_ms = timed(lambda: [calls[c]() for c in ("gather_nets", "gather_inps", "scatter_nets",
+                                                     "scatter_agg1", "scatter_eta")], k)
+    ref_ms = timed(reference_copies, max(2, k // 5))
+
+    # algorithmic HBM bytes of each call (read once + written once)
+    f4 = 4
+    nbytes = {
+        "compute_motion": B * HW * f4 * (2 + 2 + 4),
+        "gather_nets": 2 * B * row * f4, "gather_inps": 2 * B * row * f4,
+        "compute_target": B * HW * f4 * (2 + 2 + 2 + 2 + 2),
+        "scatter_nets": 2 * B * row * f4, "scatter_agg1": 2 * B * row * f4,
+        "scatter_mean": (B + nkf) * row * f4, "scatter_eta": 2 * nkf * HW * f4,
+        "ba_edge_set": 2 * 2 * cnt.value * 2 * HW * f4,
+    }
+    total_bytes = sum(nbytes.values())
+    copy_bytes = sum(nbytes[c] for c in ("gather_nets", "gather_inps", "scatter_nets",
+                                         "scatter_agg1", "scatter_eta"))
+    # gather_nets: 48 distinct rows read once and written once (gather_inps
+    # reads 12 rows four times each, partly from cache)
+    dom = "gather_nets"
+    dom_gbs = nbytes[dom] / (per_call[dom] * 1e-6) / 1e9
+
+    # CPU oracle on the same arrays (one batch; memcpy loops, a sequential mean)
+    from oracle import oracle as orc
+    orc.build()
+    t = time.perf_counter()
+    orc.compute_motion(host["coords1"], host["target"], h, w)
+    orc.gather_rows(host["nets"], None, n=B)
+    orc.gather_rows(host["inps"], ii)
+    orc.compute_target(host["coords1"], host["delta"], host["wt"])
+    orc.scatter_rows(host["nets"], host["nets"], None)
+    orc.scatter_rows(host["agg1"], host["agg1"], None)
+    orc.scatter_mean(host["agg1"], ii)
+    orc.ba_edge_set(ii, jj, ii_in, jj_in, host["target"], host["target"],
+                    host["target_inac"], host["weight_inac"], nkf)
+    cpu_ms = (time.perf_counter() - t) * 1e3
+
+    out = {
+        "metric": "update-pass glue of one 48-edge batch (48x64, 128-channel rows), 1 MI355X",
+        "value": round(step_ms * 1e3, 2),
+        "unit": "us per batch",
+        "n_gpus": 1,
+        "steps": k,
+        "higher_is_better": False,
+        "dtype": "f32 (copies; scatter-mean sums in f32 with one fused multiply-add)",
+        "data": "synthetic (seeded N(0,1) rows, U(-8,8) flow)",
+        "config": {"workload": "update-pass glue", "edges": B, "keyframes": nkf,
+                   "inactive_edges": ninac, "h": h, "w": w, "row_floats": row},
+        "algorithmic_bytes": total_bytes,
+        "achieved_GBs": round(total_bytes / (step_ms * 1e-3) / 1e9, 1),
+        "calls_us": per_call,
+        "roofline": {"kernel": f"k_rows ({dom}: 48 rows of 128x3072 floats)",
+                     "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": nbytes[dom]},
+        "row_copies": {"one_launch_per_array_us": round(copies_ms * 1e3, 2),
+                       "per_edge_async_copies_us": round(ref_ms * 1e3, 2),
+                       "copies": 4 * B + nkf, "bytes": copy_bytes},
+        "cpu_baseline": {"value": round(cpu_ms * 1e3, 1), "unit": "us per batch", "cores": 1,
+                         "kind": "port", "sample": "the same batch through the C oracle"},
+        "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(out), flush=True)
 

@@ -187,6 +187,10 @@ class Hip:
     def dtod(self, dst, src, nbytes):
         self.ok(self.h.hipMemcpy(P(dst), P(src), int(nbytes), self.D2D), "hipMemcpy D2D")
 
+    def dtod_async(self, dst, src, nbytes, stream=None):
+        self.ok(self.h.hipMemcpyAsync(P(dst), P(src), int(nbytes), self.D2D, P(stream)),
+                "hipMemcpyAsync D2D")
+
     def sync(self):
         self.ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
 
