@@ -13,6 +13,10 @@
 //   projmap, pose_retr, frame_distance, clamp_disps
 //                     the SE3 kernel launches with the reference's argument
 //                     lists (se3.cuh:118-277, main.cu:2392-2397).
+//   UpdateGlue        the steps of run_update_pass around correlation and BA
+//                     (main.cu:2186-2390): motion and target kernels, the
+//                     hidden-state loads and saves, GraphAgg's scatter-mean
+//                     and eta write-back, and the BA edge set.
 //
 // Error behaviour follows the reference: its *_CHECK macros print and exit(1)
 // (nn.cuh:17-41), and so does every adapter on a nonzero status. The single
@@ -28,6 +32,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <vector>
 
 #include <hip/hip_runtime_api.h>
 
@@ -188,5 +193,105 @@ inline void frame_distance(float* poses, float* disps, float* intrinsics, int* i
 inline void clamp_disps(float* disps, int n, float min_val) {
     check(slk_clamp_disps(disps, n, min_val, nullptr), "clamp_disps");
 }
+
+// The update-pass glue of CudaDroid::run_update_pass for h x w maps with the
+// reference's 128-channel hidden states (rows of 128*h*w floats), ordered on
+// the legacy default stream like the reference's launches and copies.
+class UpdateGlue {
+  public:
+    void init(int h, int w) {
+        h_ = h;
+        w_ = w;
+        check(slk_create(&ctx_, h, w, 128, 1, 1, 3, 1.0f / 16.0f), "UpdateGlue::init");
+    }
+
+    // compute_motion_kernel (main.cu:2204-2213); coords0 == nullptr is the
+    // identity grid coords0_buf holds
+    void compute_motion(float* motion, const float* coords1, const float* coords0,
+                        const float* target, int batch) {
+        check(slk_compute_motion(motion, coords1, coords0, target, batch, h_, w_, nullptr),
+              "compute_motion");
+    }
+
+    // compute_target_kernel (main.cu:2234-2242)
+    void compute_target(float* target, float* weight_out, const float* coords,
+                        const float* delta, const float* wt_raw, int num_edges) {
+        check(slk_compute_target(target, weight_out, coords, delta, wt_raw, num_edges,
+                                 h_ * w_, nullptr),
+              "compute_target");
+    }
+
+    // step 5, main.cu:2216-2224: batch_nets[e] = edge_nets[bs + e],
+    // batch_inps[e] = inps[ii[bs + e]] (ii_gpu: the device copy of ii_host)
+    void load_hidden(float* batch_nets, float* batch_inps, const float* edge_nets,
+                     const float* inps, const int* ii_gpu, int bs, int batch_size) {
+        const long row = 128L * h_ * w_;
+        check(slk_gather_rows(batch_nets, edge_nets + bs * row, nullptr, batch_size, row,
+                              nullptr),
+              "load_hidden");
+        check(slk_gather_rows(batch_inps, inps, ii_gpu + bs, batch_size, row, nullptr),
+              "load_hidden");
+    }
+
+    // step 8, main.cu:2245-2252: edge_nets[bs + e] = batch_nets[e],
+    // all_agg1[bs + e] = batch_agg1[e]
+    void save_hidden(float* edge_nets, float* all_agg1, const float* batch_nets,
+                     const float* batch_agg1, int bs, int batch_size) {
+        const long row = 128L * h_ * w_;
+        check(slk_scatter_rows(edge_nets + bs * row, batch_nets, nullptr, batch_size, row,
+                               nullptr),
+              "save_hidden");
+        check(slk_scatter_rows(all_agg1 + bs * row, batch_agg1, nullptr, batch_size, row,
+                               nullptr),
+              "save_hidden");
+    }
+
+    // GraphAgg scatter_mean (main.cu:2258-2296) into kf_agg; returns the
+    // active keyframes (ascending) and writes them to active_kf_gpu
+    std::vector<int> scatter_mean(float* kf_agg, const float* all_agg1, const int* ii_host,
+                                  int total_edges, int* active_kf_gpu) {
+        std::vector<int> act(total_edges > 0 ? total_edges : 1);
+        int na = 0;
+        check(slk_scatter_mean(ctx_, kf_agg, all_agg1, ii_host, total_edges,
+                               128L * h_ * w_, active_kf_gpu, act.data(), &na, nullptr),
+              "scatter_mean");
+        act.resize(na);
+        return act;
+    }
+
+    // main.cu:2303-2309: damping[active[i]] = kf_eta[i]
+    void write_eta(float* damping, const float* kf_eta, const int* active_kf_gpu,
+                   int num_active) {
+        check(slk_scatter_rows(damping, kf_eta, active_kf_gpu, num_active, (long)h_ * w_,
+                               nullptr),
+              "write_eta");
+    }
+
+    // steps 9-10, main.cu:2312-2369: t0 and the combined edge set; returns
+    // the edge count (ba_ii_host/ba_jj_host sized n + n_inac)
+    int ba_edge_set(const int* ii_host, const int* jj_host, int n, const int* ii_inac,
+                    const int* jj_inac, int n_inac, const float* target, const float* weight,
+                    const float* target_inac, const float* weight_inac, int num_keyframes,
+                    int forced_t0, bool use_inactive, int* ba_ii_host, int* ba_jj_host,
+                    int* ba_ii_gpu, int* ba_jj_gpu, float* ba_target, float* ba_weight,
+                    int* t0) {
+        int count = 0;
+        check(slk_ba_edge_set(ctx_, ii_host, jj_host, n, ii_inac, jj_inac, n_inac, target,
+                              weight, target_inac, weight_inac, h_ * w_, num_keyframes,
+                              forced_t0, use_inactive ? 1 : 0, ba_ii_host, ba_jj_host,
+                              ba_ii_gpu, ba_jj_gpu, ba_target, ba_weight, &count, t0, nullptr),
+              "ba_edge_set");
+        return count;
+    }
+
+    void destroy() {
+        if (ctx_) slk_destroy(ctx_);
+        ctx_ = nullptr;
+    }
+
+  private:
+    int h_ = 0, w_ = 0;
+    slk_ctx* ctx_ = nullptr;
+};
 
 }  // namespace slk_droid

@@ -97,3 +97,104 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
         (void)hipFree(p);
     return bad;
 }
+
+// One batch of run_update_pass's glue through UpdateGlue, in the reference's
+// order: motion (identity coords0), hidden-state loads, target/weight, saves,
+// GraphAgg scatter-mean over all edges, eta write-back, BA edge set. Inputs
+// and outputs are host arrays; rows are 128*h*w floats. Sizes: coords1,
+// target_prev [B][2][hw]; edge_nets, all_agg1 [E][row] (updated in place);
+// inps [nkf][row]; batch_agg1 [B][row]; delta, wt [B][3][hw]; kf_eta
+// [nkf][hw]; damping [nkf][hw] (updated); inactive: [n_inac] edges with rows
+// [n_inac][2][hw]. Outputs: motion [B][4][hw], batch_nets, batch_inps
+// [B][row], target/weight of the batch [B][2][hw] (written at bs), kf_agg
+// [na][row], active [na], ba_ii/ba_jj [cap], ba_target/ba_weight [cap][2][hw].
+extern "C" int adapter_glue(int h, int w, int E, int bs, int B, int nkf, const int* ii,
+                            const int* jj, const float* coords1, const float* target_prev,
+                            float* edge_nets, const float* inps, const float* batch_agg1,
+                            float* all_agg1, const float* delta, const float* wt,
+                            const float* kf_eta, float* damping, int n_inac, const int* ii_inac,
+                            const int* jj_inac, const float* target_inac,
+                            const float* weight_inac, float* motion, float* batch_nets,
+                            float* batch_inps, float* target_all, float* weight_all,
+                            float* kf_agg, int* active, int* num_active, int* ba_ii,
+                            int* ba_jj, float* ba_target, float* ba_weight, int* count,
+                            int* t0) {
+    const size_t hw = (size_t)h * w, row = 128 * hw;
+    float* d_c1 = upload(coords1, B * 2 * hw);
+    float* d_tp = upload(target_prev, B * 2 * hw);
+    float* d_nets = upload(edge_nets, E * row);
+    float* d_inps = upload(inps, nkf * row);
+    float* d_bagg = upload(batch_agg1, B * row);
+    float* d_agg = upload(all_agg1, E * row);
+    float* d_delta = upload(delta, B * 3 * hw);
+    float* d_wt = upload(wt, B * 3 * hw);
+    float* d_eta = upload(kf_eta, nkf * hw);
+    float* d_damp = upload(damping, nkf * hw);
+    int* d_ii = upload(ii, E);
+    float* d_ti = upload(target_inac, (size_t)(n_inac > 0 ? n_inac : 1) * 2 * hw);
+    float* d_wi = upload(weight_inac, (size_t)(n_inac > 0 ? n_inac : 1) * 2 * hw);
+    std::vector<float> zeros_t((size_t)E * 2 * hw, 0.0f);
+    float* d_tall = upload(zeros_t.data(), E * 2 * hw);
+    float* d_wall = upload(zeros_t.data(), E * 2 * hw);
+    const size_t cap = (size_t)E + n_inac;
+    std::vector<float> zcap(cap * 2 * hw, 0.0f);
+    float* d_bt = upload(zcap.data(), cap * 2 * hw);
+    float* d_bw = upload(zcap.data(), cap * 2 * hw);
+    std::vector<int> zi(cap > 0 ? cap : 1, 0);
+    int* d_bi = upload(zi.data(), zi.size());
+    int* d_bj = upload(zi.data(), zi.size());
+    int* d_act = upload(zi.data(), zi.size());
+    float *d_mot = nullptr, *d_bn = nullptr, *d_bi2 = nullptr, *d_kf = nullptr;
+    if (hipMalloc(&d_mot, B * 4 * hw * sizeof(float)) != hipSuccess ||
+        hipMalloc(&d_bn, B * row * sizeof(float)) != hipSuccess ||
+        hipMalloc(&d_bi2, B * row * sizeof(float)) != hipSuccess ||
+        hipMalloc(&d_kf, (size_t)nkf * row * sizeof(float)) != hipSuccess)
+        return 1;
+    if (!d_c1 || !d_tp || !d_nets || !d_inps || !d_bagg || !d_agg || !d_delta || !d_wt ||
+        !d_eta || !d_damp || !d_ii || !d_ti || !d_wi || !d_tall || !d_wall || !d_bt || !d_bw ||
+        !d_bi || !d_bj || !d_act)
+        return 1;
+
+    slk_droid::UpdateGlue glue;
+    glue.init(h, w);
+    glue.compute_motion(d_mot, d_c1, nullptr, d_tp, B);
+    glue.load_hidden(d_bn, d_bi2, d_nets, d_inps, d_ii, bs, B);
+    int bad = download(batch_nets, d_bn, B * row);
+    bad |= download(batch_inps, d_bi2, B * row);
+    // the GRU updates batch_nets in place; here it adds 1 (host side)
+    std::vector<float> upd(B * row);
+    for (size_t k = 0; k < upd.size(); k++) upd[k] = batch_nets[k] + 1.0f;
+    bad |= hipMemcpy(d_bn, upd.data(), upd.size() * sizeof(float), hipMemcpyHostToDevice) !=
+           hipSuccess;
+    glue.compute_target(d_tall + bs * 2 * hw, d_wall + bs * 2 * hw, d_c1, d_delta, d_wt, B);
+    glue.save_hidden(d_nets, d_agg, d_bn, d_bagg, bs, B);
+    std::vector<int> ii_h(ii, ii + E), jj_h(jj, jj + E);
+    std::vector<int> act = glue.scatter_mean(d_kf, d_agg, ii_h.data(), E, d_act);
+    glue.write_eta(d_damp, d_eta, d_act, (int)act.size());
+    std::vector<int> bi_h(cap > 0 ? cap : 1), bj_h(cap > 0 ? cap : 1);
+    *count = glue.ba_edge_set(ii_h.data(), jj_h.data(), E, ii_inac, jj_inac, n_inac, d_tall,
+                              d_wall, d_ti, d_wi, nkf, -1, true, bi_h.data(), bj_h.data(),
+                              d_bi, d_bj, d_bt, d_bw, t0);
+    *num_active = (int)act.size();
+    std::copy(act.begin(), act.end(), active);
+    bad |= download(motion, d_mot, B * 4 * hw);
+    bad |= download(edge_nets, d_nets, E * row);
+    bad |= download(all_agg1, d_agg, E * row);
+    bad |= download(target_all, d_tall, E * 2 * hw);
+    bad |= download(weight_all, d_wall, E * 2 * hw);
+    bad |= download(kf_agg, d_kf, act.size() * row);
+    bad |= download(damping, d_damp, nkf * hw);
+    bad |= download(ba_ii, d_bi, *count);
+    bad |= download(ba_jj, d_bj, *count);
+    bad |= download(ba_target, d_bt, (size_t)*count * 2 * hw);
+    bad |= download(ba_weight, d_bw, (size_t)*count * 2 * hw);
+    for (int k = 0; k < *count; k++) bad |= (bi_h[k] != ba_ii[k] || bj_h[k] != ba_jj[k]);
+    glue.destroy();
+    for (void* p : {(void*)d_c1, (void*)d_tp, (void*)d_nets, (void*)d_inps, (void*)d_bagg,
+                    (void*)d_agg, (void*)d_delta, (void*)d_wt, (void*)d_eta, (void*)d_damp,
+                    (void*)d_ii, (void*)d_ti, (void*)d_wi, (void*)d_tall, (void*)d_wall,
+                    (void*)d_bt, (void*)d_bw, (void*)d_bi, (void*)d_bj, (void*)d_act,
+                    (void*)d_mot, (void*)d_bn, (void*)d_bi2, (void*)d_kf})
+        (void)hipFree(p);
+    return bad;
+}

@@ -31,6 +31,7 @@ def harness():
     I, F = ctypes.c_int, ctypes.c_float
     lib.adapter_corr.argtypes = [P, I, I, I, I, P, P, I, P, P, P]
     lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I]
+    lib.adapter_glue.argtypes = [I, I, I, I, I, I] + [P] * 12 + [I] + [P] * 4 + [P] * 14
     return lib
 
 
@@ -76,3 +77,68 @@ def test_bundle_adjustment_iterate(harness, motion_only):
     rd = np.maximum(rd, 0.001)
     assert norm_rel(poses, rp) < TOL
     assert norm_rel(disps, rd) < TOL
+
+
+def test_update_glue_batch(harness):
+    """UpdateGlue through one batch of run_update_pass (main.cu:2186-2369):
+    motion with the identity grid, hidden-state loads at edge_start 4, the
+    saved hidden states (the stand-in GRU adds 1), target/weight, GraphAgg
+    over all 20 edges, eta write-back and the BA edge set with 7 inactive
+    edges; every output bitwise against the oracle's composition."""
+    h, w, E, bs, B, nkf, ni = 12, 16, 20, 4, 8, 6, 7
+    hw = h * w
+    row = 128 * hw
+    rng = np.random.default_rng(40)
+    ii = rng.integers(1, nkf, E).astype(np.int32)
+    jj = rng.integers(0, nkf, E).astype(np.int32)
+    ii_in = rng.integers(0, nkf, ni).astype(np.int32)
+    jj_in = rng.integers(0, nkf, ni).astype(np.int32)
+    f = lambda *s: rng.normal(size=s).astype(np.float32)  # noqa: E731
+    coords1, tprev = f(B, 2, hw) * 20, f(B, 2, hw) * 20
+    nets, inps, bagg, agg = f(E, row), f(nkf, row), f(B, row), f(E, row)
+    delta, wt, kf_eta, damp = f(B, 3, hw), f(B, 3, hw), f(nkf, hw), f(nkf, hw)
+    ti, wi = f(ni, 2, hw), f(ni, 2, hw)
+    nets0, agg0, damp0 = nets.copy(), agg.copy(), damp.copy()
+    cap = E + ni
+    out = {"motion": np.zeros((B, 4, hw), np.float32), "bn": np.zeros((B, row), np.float32),
+           "bi": np.zeros((B, row), np.float32), "tall": np.zeros((E, 2, hw), np.float32),
+           "wall": np.zeros((E, 2, hw), np.float32), "kf": np.zeros((nkf, row), np.float32),
+           "act": np.zeros(nkf, np.int32), "bii": np.zeros(cap, np.int32),
+           "bjj": np.zeros(cap, np.int32), "bt": np.zeros((cap, 2, hw), np.float32),
+           "bw": np.zeros((cap, 2, hw), np.float32)}
+    na, cnt, t0 = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert harness.adapter_glue(
+        h, w, E, bs, B, nkf, _p(ii), _p(jj), _p(coords1), _p(tprev), _p(nets), _p(inps),
+        _p(bagg), _p(agg), _p(delta), _p(wt), _p(kf_eta), _p(damp), ni, _p(ii_in), _p(jj_in),
+        _p(ti), _p(wi), _p(out["motion"]), _p(out["bn"]), _p(out["bi"]), _p(out["tall"]),
+        _p(out["wall"]), _p(out["kf"]), _p(out["act"]), ctypes.addressof(na), _p(out["bii"]),
+        _p(out["bjj"]), _p(out["bt"]), _p(out["bw"]), ctypes.addressof(cnt),
+        ctypes.addressof(t0)) == 0
+    np.testing.assert_array_equal(out["motion"], orc.compute_motion(coords1, tprev, h, w))
+    np.testing.assert_array_equal(out["bn"], orc.gather_rows(nets0[bs:], None, n=B))
+    np.testing.assert_array_equal(out["bi"], orc.gather_rows(inps, ii[bs:bs + B]))
+    ref_nets = nets0.copy()
+    ref_nets[bs:bs + B] = nets0[bs:bs + B] + np.float32(1.0)
+    np.testing.assert_array_equal(nets, ref_nets)
+    ref_agg = agg0.copy()
+    ref_agg[bs:bs + B] = bagg
+    np.testing.assert_array_equal(agg, ref_agg)
+    t_b, w_b = orc.compute_target(coords1, delta, wt)
+    ref_t, ref_w = np.zeros((E, 2, hw), np.float32), np.zeros((E, 2, hw), np.float32)
+    ref_t[bs:bs + B], ref_w[bs:bs + B] = t_b, w_b
+    np.testing.assert_array_equal(out["tall"], ref_t)
+    np.testing.assert_array_equal(out["wall"], ref_w)
+    kf_ref, act_ref = orc.scatter_mean(ref_agg, ii)
+    assert na.value == len(act_ref)
+    np.testing.assert_array_equal(out["act"][:na.value], act_ref)
+    np.testing.assert_array_equal(out["kf"][:na.value], kf_ref)
+    ref_damp = damp0.copy()
+    ref_damp[act_ref] = kf_eta[:len(act_ref)]
+    np.testing.assert_array_equal(damp, ref_damp)
+    es = orc.ba_edge_set(ii, jj, ii_in, jj_in, ref_t, ref_w, ti, wi, nkf)
+    assert cnt.value == len(es["ii"]) and t0.value == es["t0"]
+    m = cnt.value
+    np.testing.assert_array_equal(out["bii"][:m], es["ii"])
+    np.testing.assert_array_equal(out["bjj"][:m], es["jj"])
+    np.testing.assert_array_equal(out["bt"][:m], es["target"])
+    np.testing.assert_array_equal(out["bw"][:m], es["weight"])
