@@ -47,7 +47,10 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 # HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
 # (profiles/corr_window48_pmc_traffic.md)
-TRAFFIC_BYTES = 301194203
+TRAFFIC_BYTES = 312169575
+# HBM bytes of the glue's 48-row copy (gather of 48 distinct 128x3072-float
+# rows): the same passes over bench.py --glue (profiles/glue48_kernel_stats.md)
+GLUE_ROWS_TRAFFIC_BYTES = 151029965
 PEAK_HBM_GBS = 8000.0
 
 
@@ -484,7 +487,8 @@ def glue(args, slk, wl, H):
         "roofline": {"kernel": f"k_rows ({dom}: 48 rows of 128x3072 floats)",
                      "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(dom_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": nbytes[dom]},
+                     "traffic": GLUE_ROWS_TRAFFIC_BYTES,
+                     "algorithmic_bytes_per_launch": nbytes[dom]},
         "row_copies": {"one_launch_per_array_us": round(copies_ms * 1e3, 2),
                        "per_edge_async_copies_us": round(ref_ms * 1e3, 2),
                        "copies": 4 * B + nkf, "bytes": copy_bytes},
