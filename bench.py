@@ -25,6 +25,10 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 hidden-state gathers and scatters, the keyframe scatter-mean, the BA edge
 set) for one 48-edge batch and prints one JSON line for it.
 
+`--graph` times the backend's proximity-factor selection (frame distances of
+all pairs of a 200-keyframe graph in one launch, then the reference's
+selection) and prints one JSON line for it.
+
 `--backend` instead times the backend configuration (200 keyframes, 2000
 edges: correlation + lookup of every edge in 48-edge launches, then 5 BA
 iterations over 198 free poses with the dense 1188x1188 Schur system) and
@@ -65,6 +69,8 @@ def parse():
                          "copy kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--backend", action="store_true",
                     help="time the 200-keyframe backend configuration instead")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the backend proximity-factor selection (200 keyframes) instead")
     ap.add_argument("--glue", action="store_true",
                     help="time the update-pass glue of one 48-edge batch instead")
     ap.add_argument("--cpu-edges", type=int, default=48,
@@ -90,6 +96,8 @@ def main():
         return backend(args, slk, wl, H)
     if args.glue:
         return glue(args, slk, wl, H)
+    if args.graph:
+        return graph(args, slk, wl, H)
 
     h, w, C, n, B = 48, 64, 128, 12, 48
     HW = h * w
@@ -495,6 +503,126 @@ def glue(args, slk, wl, H):
         "cpu_baseline": {"value": round(cpu_ms * 1e3, 1), "unit": "us per batch", "cores": 1,
                          "kind": "port", "sample": "the same batch through the C oracle"},
         "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(out), flush=True)
+
+
+def graph(args, slk, wl, H):
+    """The backend's add_proximity_factors(0, 0, radius 2, nms 3, thresh 20)
+    (cuda_slam/main.cu:2462-2471, 1679-1779) over a 200-keyframe graph with
+    its 2000 active edges: frame distances of all 40000 pairs plus the
+    selection, through slk_proximity_factors (one launch, one read-back).
+    Beside it: the same distances fetched the reference's way
+    (compute_frame_distances_batch, main.cu:1655-1676: 1024 pairs per
+    upload + launch + synchronise + read-back), and the CPU oracle's
+    distances and selection on the same inputs."""
+    import ctypes
+
+    h, w, t, rad, nms, thresh, beta = 48, 64, 200, 2, 3, 20.0, 0.3
+    HW = h * w
+    L = slk.lib()
+    rng = np.random.default_rng(0)
+    poses = np.zeros((t, 7), np.float32)
+    poses[:, 0] = 0.02 * np.arange(t) + rng.normal(0, 0.01, t)
+    poses[:, 1:3] = rng.normal(0, 0.01, (t, 2))
+    poses[:, 3:] = wl.quat_from_rotvec(rng.normal(0, 0.02, (t, 3)))
+    disps = rng.uniform(0.2, 2.0, (t, h, w)).astype(np.float32)
+    intr = np.array([60.0, 60.0, 32.0, 24.0], np.float32)
+    ii, jj = wl.backend_edges(t, 2000)
+    ii, jj = np.ascontiguousarray(ii, np.int32), np.ascontiguousarray(jj, np.int32)
+    ctx = slk.Context(h, w, C=128, max_batch=1)
+    D = slk.DeviceArray.from_host
+    dp, dd, di = D(poses), D(disps), D(intr)
+    stream = H.stream()
+    npairs = t * t
+    cap = 2 * t * (t + rad + 1)
+    ni, nj = np.zeros(cap, np.int32), np.zeros(cap, np.int32)
+    dist = np.zeros(npairs, np.float32)
+    n_new, n_es = ctypes.c_int(0), ctypes.c_int(0)
+
+    def ours():
+        slk.check(L.slk_proximity_factors(
+            ctx.ptr, dp.ptr, dd.ptr, di.ptr, t, 0, 0, rad, nms, thresh, beta, ii.ctypes.data,
+            jj.ctypes.data, len(ii), None, None, 0, 0, ni.ctypes.data, nj.ctypes.data, cap,
+            ctypes.byref(n_new), ctypes.byref(n_es), dist.ctypes.data, stream))
+
+    pi = np.repeat(np.arange(t), t).astype(np.int32)
+    pj = np.tile(np.arange(t), t).astype(np.int32)
+    bi, bj = slk.DeviceArray((1024,), np.int32), slk.DeviceArray((1024,), np.int32)
+    bd = slk.DeviceArray((1024,))
+    ref_d = np.zeros(npairs, np.float32)
+
+    def reference_batches():
+        for off in range(0, npairs, 1024):
+            b = min(1024, npairs - off)
+            H.htod(bi.ptr, pi[off:off + b])
+            H.htod(bj.ptr, pj[off:off + b])
+            slk.check(L.slk_frame_distance(dp.ptr, dd.ptr, di.ptr, bi.ptr, bj.ptr, bd.ptr, b, h,
+                                           w, beta, None))
+            H.sync()
+            H.dtoh(ref_d[off:off + b], bd.ptr)
+
+    ours()
+    reference_batches()
+    k = max(3, min(args.steps, 20))
+    t0w = time.perf_counter()
+    for _ in range(k):
+        ours()
+    ours_ms = (time.perf_counter() - t0w) * 1e3 / k
+    t0w = time.perf_counter()
+    for _ in range(max(2, k // 4)):
+        reference_batches()
+    ref_ms = (time.perf_counter() - t0w) * 1e3 / max(2, k // 4)
+    # distance kernel alone (hipEvents on the stream)
+    dpi, dpj = D(pi), D(pj)
+    dall = slk.DeviceArray((npairs,))
+    H.sync()
+    e0, e1 = H.event(), H.event()
+    H.record(e0, stream)
+    for _ in range(k):
+        slk.check(L.slk_frame_distance(dp.ptr, dd.ptr, di.ptr, dpi.ptr, dpj.ptr, dall.ptr, npairs,
+                                       h, w, beta, stream))
+    H.record(e1, stream)
+    kern_ms = H.elapsed_ms(e0, e1) / k
+    H.sync()
+    assert np.array_equal(ref_d, dist), "batched and one-launch distances differ"
+    # ~80 flops per pixel-pair (two projections; divisions and square roots
+    # counted as one flop each)
+    flops = 80.0 * npairs * HW
+    gflops = flops / (kern_ms * 1e-3) / 1e9
+
+    from oracle import oracle as orc
+    orc.build()
+    sample = 4000  # bounded CPU sample: the first 4000 pairs' distances
+    tc = time.perf_counter()
+    orc.frame_distance(poses, disps, intr, pi[:sample], pj[:sample], h, w, beta)
+    cpu_dist_ms = (time.perf_counter() - tc) * 1e3 * npairs / sample
+    tc = time.perf_counter()
+    orc.proximity_select(dist, t, 0, 0, rad, nms, thresh, ii, jj)
+    cpu_sel_ms = (time.perf_counter() - tc) * 1e3
+    out = {
+        "metric": "backend proximity factors (200 keyframes, 40000 pairs, 2000 edges), 1 MI355X",
+        "value": round(ours_ms, 3),
+        "unit": "ms per call",
+        "n_gpus": 1,
+        "steps": k,
+        "higher_is_better": False,
+        "dtype": "f32",
+        "data": "synthetic (200-keyframe trajectory, backend edge graph of workloads.py)",
+        "config": {"workload": "proximity factors", "keyframes": t, "pairs": npairs,
+                   "edges": len(ii), "rad": rad, "nms": nms, "thresh": thresh, "h": h, "w": w},
+        "new_edges": n_new.value,
+        "greedy_edges": n_es.value,
+        "frame_distance_kernel_ms": round(kern_ms, 4),
+        "roofline": {"kernel": "k_frame_distance (40000 pairs x 3072 pixels)", "bound": "valu",
+                     "achieved": round(gflops / 1e3, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gflops / 1e3 / PEAK_FP32_TFLOPS, 4),
+                     "traffic": None, "flop_per_pixel_pair": 80},
+        "reference_pattern_ms": round(ref_ms, 3),
+        "cpu_baseline": {"value": round(cpu_dist_ms + cpu_sel_ms, 1), "unit": "ms per call",
+                         "cores": orc.lib().orc_num_threads(), "kind": "port",
+                         "sample": f"oracle distances of {sample} pairs scaled to {npairs}, "
+                                   "plus the selection"},
     }
     print(json.dumps(out), flush=True)
 

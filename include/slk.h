@@ -279,6 +279,30 @@ int slk_ba_edge_set(slk_ctx* ctx, const int* ii_host, const int* jj_host, int n,
                     int* ba_jj, float* ba_target, float* ba_weight, int* count, int* t0,
                     hipStream_t stream);
 
+/* ----------------------------------------------------------- factor graph */
+/* CudaDroid::add_proximity_factors(t0, t1, rad, nms, thresh, remove_old)
+ * (cuda_slam/main.cu:1679-1779) up to the edge-state update, with the
+ * frame distances of compute_frame_distances_batch (main.cu:1655-1676) in
+ * one launch and one read-back for all pairs i in [t0, t), j in [t1, t)
+ * (t = num_keyframes; poses/disps/intrinsics on the device, the context's
+ * h x w maps). The existing edges are the active (ii_host/jj_host) and
+ * inactive (ii_inac_host/jj_inac_host) lists. Writes the edges the update
+ * appends (main.cu:1773-1781: the chosen edges not present yet, each once,
+ * in the reference's order) to new_ii_host/new_jj_host (capacity
+ * `capacity`; 2*(t - t0)*(t - t1 + rad + 1) always suffices), their number
+ * to *n_new and the greedy step's edge count (es.size(), which the caller's
+ * age-based removal compares with max_factors, main.cu:1758-1771) to *n_es;
+ * dists_host, if not NULL, receives the (t - t0)*(t - t1) raw distances.
+ * Equal distances are taken in pair order (the reference's std::sort leaves
+ * their order unspecified). Synchronises `stream` once. */
+int slk_proximity_factors(slk_ctx* ctx, const float* poses, const float* disps,
+                          const float* intrinsics, int num_keyframes, int t0, int t1, int rad,
+                          int nms, float thresh, float beta, const int* ii_host,
+                          const int* jj_host, int n_edges, const int* ii_inac_host,
+                          const int* jj_inac_host, int n_inac, int max_factors,
+                          int* new_ii_host, int* new_jj_host, int capacity, int* n_new,
+                          int* n_es, float* dists_host, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

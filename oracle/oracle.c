@@ -855,3 +855,102 @@ int orc_ba_edge_set(const int* ii, const int* jj, int n, const int* ii_inac,
             }
     return m;
 }
+
+/* ------------------------------------------------------------------------ */
+/* factor graph                                                              */
+/* ------------------------------------------------------------------------ */
+
+static int has_pair(const int* a, const int* b, int n, int i, int j) {
+    for (int e = 0; e < n; e++)
+        if (a[e] == i && b[e] == j) return 1;
+    return 0;
+}
+
+static const float* g_sort_d; /* qsort context (single-threaded use) */
+static int cmp_dist_then_index(const void* pa, const void* pb) {
+    const int a = *(const int*)pa, b = *(const int*)pb;
+    if (g_sort_d[a] < g_sort_d[b]) return -1;
+    if (g_sort_d[a] > g_sort_d[b]) return 1;
+    return (a > b) - (a < b);
+}
+
+static void nms_suppress(float* d, int i, int j, int nms, int t0, int t1, int t, int jrange,
+                         int np) {
+    /* main.cu:1709-1721 */
+    int r = abs(i - j) - 2;
+    r = r < nms ? r : nms;
+    r = r > 0 ? r : 0;
+    for (int di = -nms; di <= nms; di++)
+        for (int dj = -nms; dj <= nms; dj++)
+            if (abs(di) + abs(dj) <= r) {
+                const int i1 = i + di, j1 = j + dj;
+                if (i1 >= t0 && i1 < t && j1 >= t1 && j1 < t) {
+                    const int idx = (i1 - t0) * jrange + (j1 - t1);
+                    if (idx >= 0 && idx < np) d[idx] = 1e6f;
+                }
+            }
+}
+
+int orc_proximity_select(const float* dr, int t, int t0, int t1, int rad, int nms,
+                         float thresh, const int* ii, const int* jj, int n,
+                         const int* ii_inac, const int* jj_inac, int n_inac,
+                         int max_factors, int* new_ii, int* new_jj, int cap, int* n_new) {
+    *n_new = 0;
+    if (t < 2) return 0; /* main.cu:1682 */
+    t0 = t0 > 0 ? t0 : 0;
+    t1 = t1 > 0 ? t1 : 0;
+    const int jrange = t - t1 > 0 ? t - t1 : 0;
+    const int np = (t - t0 > 0 ? t - t0 : 0) * jrange;
+    if (np == 0) return 0;
+    float* d = (float*)malloc(sizeof(float) * np);
+    memcpy(d, dr, sizeof(float) * np);
+    for (int k = 0; k < np; k++) { /* main.cu:1702-1706 */
+        const int i = t0 + k / jrange, j = t1 + k % jrange;
+        if (i - rad < j) d[k] = 1e6f;
+        if (d[k] > 100.0f) d[k] = 1e6f;
+    }
+    for (int e = 0; e < n; e++) nms_suppress(d, ii[e], jj[e], nms, t0, t1, t, jrange, np);
+    for (int e = 0; e < n_inac; e++)
+        nms_suppress(d, ii_inac[e], jj_inac[e], nms, t0, t1, t, jrange, np);
+    /* es: up to 2 edges per neighbour slot and per pair */
+    const int es_cap = 2 * ((t - t0) * (rad + 1) + np) + 2;
+    int* ei = (int*)malloc(sizeof(int) * es_cap);
+    int* ej = (int*)malloc(sizeof(int) * es_cap);
+    int ne = 0;
+    for (int i = t0; i < t; i++) /* main.cu:1729-1736 */
+        for (int j = (i - rad - 1 > 0 ? i - rad - 1 : 0); j < i; j++) {
+            if (!has_pair(ii, jj, n, i, j) && !has_pair(ii_inac, jj_inac, n_inac, i, j)) {
+                ei[ne] = i; ej[ne++] = j;
+                ei[ne] = j; ej[ne++] = i;
+            }
+            const int idx = (i - t0) * jrange + (j - t1);
+            if (idx >= 0 && idx < np) d[idx] = 1e6f;
+        }
+    int* order = (int*)malloc(sizeof(int) * np);
+    for (int k = 0; k < np; k++) order[k] = k;
+    g_sort_d = d;
+    qsort(order, np, sizeof(int), cmp_dist_then_index); /* main.cu:1739-1742 */
+    for (int q = 0; q < np; q++) { /* main.cu:1744-1755 */
+        const int k = order[q];
+        if (d[k] > thresh) continue;
+        if (max_factors > 0 && n + ne > max_factors) break;
+        const int i = t0 + k / jrange, j = t1 + k % jrange;
+        ei[ne] = i; ej[ne++] = j;
+        ei[ne] = j; ej[ne++] = i;
+        nms_suppress(d, i, j, nms, t0, t1, t, jrange, np);
+    }
+    /* main.cu:1773-1781: append what has_edge does not find, growing the set */
+    int m = 0;
+    for (int q = 0; q < ne; q++) {
+        int dup = has_pair(ii, jj, n, ei[q], ej[q]) ||
+                  has_pair(ii_inac, jj_inac, n_inac, ei[q], ej[q]);
+        for (int r = 0; r < m && !dup && r < cap; r++)
+            dup = new_ii[r] == ei[q] && new_jj[r] == ej[q];
+        if (dup) continue;
+        if (m < cap) { new_ii[m] = ei[q]; new_jj[m] = ej[q]; }
+        m++;
+    }
+    *n_new = m;
+    free(d); free(ei); free(ej); free(order);
+    return ne;
+}

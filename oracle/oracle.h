@@ -155,6 +155,20 @@ int orc_ba_edge_set(const int* ii, const int* jj, int n, const int* ii_inac,
                     int use_inactive, int* ba_ii, int* ba_jj, float* ba_target,
                     float* ba_weight, int* t0_out);
 
+/* ---------------- factor graph (cuda_slam/main.cu:1655-1781) ------------- */
+
+/* add_proximity_factors (main.cu:1679-1779) from the raw frame distances of
+ * the pairs i in [t0, t), j in [t1, t) (d[(i-t0)*(t-t1) + j-t1], t =
+ * num_keyframes): invalidation, NMS around the active and inactive edges,
+ * mandatory neighbour edges, greedy best-distance edges (ascending distance,
+ * ties in pair order), then the edges not present yet, each once, written
+ * to new_ii/new_jj (up to cap). Returns the number of edges the greedy step
+ * produced (both directions counted), *n_new the number of new edges. */
+int orc_proximity_select(const float* d, int t, int t0, int t1, int rad, int nms,
+                         float thresh, const int* ii, const int* jj, int n,
+                         const int* ii_inac, const int* jj_inac, int n_inac,
+                         int max_factors, int* new_ii, int* new_jj, int cap, int* n_new);
+
 #ifdef __cplusplus
 }
 #endif

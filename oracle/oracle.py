@@ -83,6 +83,9 @@ def lib():
             "orc_gather_rows": ([_f32p, _f32p, vp, c_int, c_long], None),
             "orc_scatter_rows": ([_f32p, _f32p, vp, c_int, c_long], None),
             "orc_scatter_mean": ([_f32p, _f32p, _i32p, c_int, c_long, _i32p], c_int),
+            "orc_proximity_select": ([_f32p, c_int, c_int, c_int, c_int, c_int, c_float,
+                                      _i32p, _i32p, c_int, _i32p, _i32p, c_int, c_int, _i32p,
+                                      _i32p, c_int, ctypes.POINTER(c_int)], c_int),
             "orc_ba_edge_set": ([_i32p, _i32p, c_int, _i32p, _i32p, c_int, _f32p, _f32p,
                                  _f32p, _f32p, c_int, c_int, c_int, c_int, _i32p, _i32p,
                                  _f32p, _f32p, ctypes.POINTER(c_int)], c_int),
@@ -373,3 +376,22 @@ def ba_edge_set(ii, jj, ii_inac, jj_inac, target, weight, target_inac, weight_in
                               int(num_keyframes), int(forced_t0), int(bool(use_inactive)),
                               bi, bj, bt.reshape(-1), bw.reshape(-1), ctypes.byref(t0))
     return {"ii": bi[:m], "jj": bj[:m], "target": bt[:m], "weight": bw[:m], "t0": t0.value}
+
+
+# ---------------------------------------------------------------- factor graph
+def proximity_select(d, t, t0, t1, rad, nms, thresh, ii, jj, ii_inac=(), jj_inac=(),
+                     max_factors=0):
+    """add_proximity_factors (main.cu:1679-1779) from raw pair distances d
+    [(t-t0)*(t-t1)]: (new edges [m][2], number of greedy-step edges)."""
+    d = _c(d, np.float32).reshape(-1)
+    ii, jj = _c(ii, np.int32), _c(jj, np.int32)
+    ii_inac, jj_inac = _c(ii_inac, np.int32), _c(jj_inac, np.int32)
+    cap = 2 * (max(t - t0, 0) * (rad + 1) + d.size) + 2
+    ni = np.zeros(cap, np.int32)
+    nj = np.zeros(cap, np.int32)
+    m = ctypes.c_int(0)
+    ne = lib().orc_proximity_select(d, int(t), int(t0), int(t1), int(rad), int(nms),
+                                    float(thresh), ii, jj, len(ii), ii_inac, jj_inac,
+                                    len(ii_inac), int(max_factors), ni, nj, cap,
+                                    ctypes.byref(m))
+    return np.stack([ni[:m.value], nj[:m.value]], 1), ne

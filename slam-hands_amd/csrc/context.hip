@@ -170,6 +170,8 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     ctx->zero_idx.release();
     ctx->glue_stage.release();
     ctx->glue_idx.release();
+    ctx->graph_pairs.release();
+    ctx->graph_dist.release();
     delete ctx;
     return SLK_OK;
 }

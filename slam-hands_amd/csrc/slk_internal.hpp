@@ -86,6 +86,8 @@ struct slk_ctx {
     // update-pass glue: index lists uploaded through a pinned stage
     slk::HostStage glue_stage;
     slk::DevBuf glue_idx;
+    // proximity factors: the pair lists and their frame distances
+    slk::DevBuf graph_pairs, graph_dist;
     slk::BaState* ba = nullptr;
     bool prof = false;
     std::vector<slk::ProfRec> prof_recs;

@@ -36,7 +36,7 @@ EXPORTS = [
     "slk_ba_accum", "slk_ba_damping_q", "slk_ba_eet6x6", "slk_ba_ev6x1", "slk_ba_evt6x1",
     "slk_ba_depth_update",
     "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
-    "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set",
+    "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set", "slk_proximity_factors",
 ]
 
 
@@ -107,6 +107,8 @@ def lib():
             "slk_scatter_mean": [P, P, P, P, I, L, P, P, ctypes.POINTER(I), P],
             "slk_ba_edge_set": [P, P, P, I, P, P, I, P, P, P, P, I, I, I, I, P, P, P, P, P,
                                 P, ctypes.POINTER(I), ctypes.POINTER(I), P],
+            "slk_proximity_factors": [P, P, P, P, I, I, I, I, I, F, F, P, P, I, P, P, I, I, P,
+                                      P, I, ctypes.POINTER(I), ctypes.POINTER(I), P, P],
         }
         for name, args in sig.items():
             fn = getattr(L_, name)

@@ -1,0 +1,80 @@
+"""Pins of the oracle's proximity-factor selection (oracle.c,
+orc_proximity_select; cuda_slam/main.cu:1679-1779) by hand-worked cases on a
+6-keyframe window (t0 = t1 = 0, rad = 1, nms = 1, thresh = 16) whose edge
+lists were derived by hand from the reference's steps: invalidation of
+pairs with j > i - rad and of distances above 100, NMS of L1 radius
+max(min(|i - j| - 2, nms), 0) around existing and chosen edges, mandatory
+neighbour edges (both directions, skipped when (i, j) exists), greedy picks
+in ascending distance, the max_factors cut and the final de-duplication.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    orc.build()
+
+
+def _d():
+    # raw distances; only pairs with j <= i - 3 survive invalidation and seeding
+    d = np.full((6, 6), 50.0, np.float32)
+    d[3, 0], d[4, 0], d[4, 1] = 5.0, 20.0, 3.0
+    d[5, 0], d[5, 1], d[5, 2] = 4.0, 2.0, 1.0
+    d[2, 0] = 200.0  # above 100 (also a mandatory neighbour)
+    return d
+
+
+SEEDS = [(1, 0), (0, 1), (2, 0), (0, 2), (2, 1), (1, 2), (3, 1), (1, 3), (3, 2), (2, 3),
+         (4, 2), (2, 4), (4, 3), (3, 4), (5, 3), (3, 5), (5, 4), (4, 5)]
+
+
+def test_hand_worked_no_existing_edges():
+    new, ne = orc.proximity_select(_d(), 6, 0, 0, 1, 1, 16.0, [], [])
+    # greedy: (5,2) suppresses (5,1); (4,1) suppresses (4,0); (5,0); (3,0); (4,0) is 20 > 16
+    greedy = [(5, 2), (2, 5), (4, 1), (1, 4), (5, 0), (0, 5), (3, 0), (0, 3)]
+    assert ne == 26
+    assert [tuple(e) for e in new] == SEEDS + greedy
+
+
+def test_hand_worked_existing_active_and_inactive_edges():
+    new, ne = orc.proximity_select(_d(), 6, 0, 0, 1, 1, 16.0, [1], [0], ii_inac=[5],
+                                   jj_inac=[2])
+    # (1,0) exists: its seed pair is skipped in both directions; (5,2) inactive
+    # suppresses itself and (5,1)
+    seeds = SEEDS[2:]
+    greedy = [(4, 1), (1, 4), (5, 0), (0, 5), (3, 0), (0, 3)]
+    assert ne == 22
+    assert [tuple(e) for e in new] == seeds + greedy
+
+
+def test_max_factors_cut():
+    new, ne = orc.proximity_select(_d(), 6, 0, 0, 1, 1, 16.0, [], [], max_factors=20)
+    # 18 seed edges; (5,2) taken (18 <= 20), (5,1) suppressed, (4,1) taken
+    # (20 <= 20), then 22 > 20 stops the greedy loop
+    assert ne == 22
+    assert [tuple(e) for e in new] == SEEDS + [(5, 2), (2, 5), (4, 1), (1, 4)]
+
+
+def test_invariants_on_random_windows():
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        t = int(rng.integers(4, 14))
+        t0, t1 = int(rng.integers(0, t)), int(rng.integers(0, t))
+        rad, nms = int(rng.integers(0, 3)), int(rng.integers(0, 3))
+        d = rng.uniform(0, 30, (t - t0) * (t - t1)).astype(np.float32)
+        ii = rng.integers(0, t, 5)
+        jj = rng.integers(0, t, 5)
+        new, ne = orc.proximity_select(d, t, t0, t1, rad, nms, 16.0, ii, jj)
+        have = set(zip(ii.tolist(), jj.tolist()))
+        got = [tuple(e) for e in new]
+        assert len(got) == len(set(got)) and not (set(got) & have)
+        for i, j in got:
+            # every new edge is a neighbour edge or a candidate pair kept by the rules
+            assert abs(i - j) <= rad + 1 or (j, i) in got or (j, i) in have
+        picked = [(i, j) for i, j in got if i - j > rad + 1]
+        for i, j in picked:
+            k = (i - t0) * (t - t1) + (j - t1)
+            assert t0 <= i < t and t1 <= j < t and d[k] <= 16.0
