@@ -163,7 +163,6 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     slk::ba_destroy(ctx);
     ctx->batch_win.release();
     ctx->split_feat.release();
-    ctx->split_pool.release();
     ctx->tile_ctr.release();
     ctx->tile_list.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();

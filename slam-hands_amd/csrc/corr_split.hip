@@ -18,10 +18,11 @@
 // cells agree to fp32 rounding, ~1e-7 relative); with integer-coded features
 // every intermediate is exact and the windows are bitwise equal.
 //
-// Stage 1 (k_feat_pool, k_feat_split), once per frame a launch uses: the fp32
-// pooled features of levels 1..3, then a bf16 hi/lo split of all levels
-// (hi = rne(x), lo = rne(x - hi)), stored chunk-major [plane][C/16][rows][16]
-// so a 16-channel chunk of consecutive rows is one contiguous block.
+// Stage 1 (k_feat_prep), once per frame a launch uses: the fp32 pooled
+// features of levels 1..3 (formed in LDS from level 0) and a bf16 hi/lo split
+// of all levels (hi = rne(x), lo = rne(x - hi)), stored chunk-major
+// [plane][C/16][rows][16] so a 16-channel chunk of consecutive rows is one
+// contiguous block.
 // Stage 2 (k_tile_mask): which (edge, source tile, target tile) pairs hold any
 // window cell; the others are never computed.
 // Stage 3 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
@@ -54,8 +55,6 @@ struct Geom {
     int HW, Ttot, C, levels;
     int off[kMaxLevels];   // first row of level l in the concatenated target set
     int h[kMaxLevels], w[kMaxLevels];
-    int poff[kMaxLevels];  // offset of level l (>= 1) in a pooled-feature channel row
-    int pool_hw;           // HW_1 + HW_2 + HW_3
 };
 
 // Frame of each feature slot: a host-built list, or (device edge indices)
@@ -80,81 +79,98 @@ __device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
 
-// Level l >= 1 of the pooled features of one slot: 0.25f*(((a+b)+c)+d) over
-// the 2x2 block of level l-1, the order of avg_pool_2x2_kernel
-// (main.cu:1166-1167), floor dims. Grid (ceil(HW_l / 256), C, slots).
+// Feature preparation of one frame slot, one launch: a workgroup takes a
+// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
+// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
+// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
+// a pooled pixel's parents always lie in the block), and writes the bf16
+// hi/lo split of every pixel of the levels present, 16 channels = 32 bytes
+// per pixel and plane, into out[slot][plane][C/16][Ttot][16]. `pooled` = 0
+// writes level 0 only (source slots). Grid (blocks, C/16, slots).
+constexpr int kPrepRows = 8, kPrepCols = 64;
 template <typename Tin>
-__global__ __launch_bounds__(256) void k_feat_pool(const Tin* __restrict__ fm, long fstride,
+__global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
                                                    SlotFrames sf, int slot_lo,
-                                                   float* __restrict__ pool, Geom g, int l) {
-    const int q = blockIdx.x * 256 + threadIdx.x;
-    const int wl = g.w[l];
-    if (q >= g.h[l] * wl) return;
-    const int c = blockIdx.y, s = slot_lo + blockIdx.z;
-    const int y = q / wl, x = q - y * wl;
-    float* prow = pool + ((size_t)s * g.C + c) * g.pool_hw;
-    float a, b, cc, d;
-    if (l == 1) {
-        const int wp = g.w[0];
-        const Tin* r0 = fm + (long)slot_frame(sf, s) * fstride + (long)c * g.HW + (2 * y) * wp +
-                        2 * x;
-        a = ldf(r0);
-        b = ldf(r0 + 1);
-        cc = ldf(r0 + wp);
-        d = ldf(r0 + wp + 1);
-    } else {
-        const int wp = g.w[l - 1];
-        const float* r0 = prow + g.poff[l - 1] + (2 * y) * wp + 2 * x;
-        a = r0[0];
-        b = r0[1];
-        cc = r0[wp];
-        d = r0[wp + 1];
-    }
-    float sum = a + b;
-    sum = sum + cc;
-    sum = sum + d;
-    prow[g.poff[l] + q] = 0.25f * sum;
-}
-
-// bf16 hi/lo split of rows [0, trows) of one slot's concatenated target set,
-// into out[slot][plane][C/16][Ttot][16]. Grid (ceil(trows / 256), C/16, slots).
-template <typename Tin>
-__global__ __launch_bounds__(256) void k_feat_split(const Tin* __restrict__ fm, long fstride,
-                                                    SlotFrames sf, int slot_lo,
-                                                    const float* __restrict__ pool,
-                                                    unsigned short* __restrict__ out, Geom g,
-                                                    int trows) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= trows) return;
+                                                   unsigned short* __restrict__ out, Geom g,
+                                                   int pooled, int nbx) {
+    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
+    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
+    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
+    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
+    const int tid = threadIdx.x;
+    const int bx = blockIdx.x % nbx, by = blockIdx.x / nbx;
     const int k = blockIdx.y, s = slot_lo + blockIdx.z;
-    int l = 0;
+    const int W = g.w[0], H = g.h[0];
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
+    // all of a thread's loads are issued before the first is used
+    constexpr int kPer = kChunk * kPrepRows * kPrepCols / 256;
+    float ld[kPer];
 #pragma unroll
-    for (int m = 1; m < kMaxLevels; m++)
-        if (m < g.levels && t >= g.off[m]) l = m;
-    const int q = t - g.off[l];
-    float v[kChunk];
-    if (l == 0) {
-        const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW + q;
-#pragma unroll
-        for (int u = 0; u < kChunk; u++) v[u] = ldf(src + (long)u * g.HW);
-    } else {
-        const float* src = pool + ((size_t)s * g.C + k * kChunk) * g.pool_hw + g.poff[l] + q;
-#pragma unroll
-        for (int u = 0; u < kChunk; u++) v[u] = src[(size_t)u * g.pool_hw];
+    for (int u = 0; u < kPer; u++) {
+        const int i = tid + u * 256;
+        const int c = i / (kPrepRows * kPrepCols);
+        const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+        const bool in = yy < H && xx < W;
+        ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+        if (!in) ld[u] = 0.0f;
     }
-    u16x8_t hi[2], lo[2];
 #pragma unroll
-    for (int u = 0; u < kChunk; u++) {
-        const unsigned pk = split_bf16(v[u]);
-        hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
-        lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+    for (int u = 0; u < kPer; u++) {
+        const int i = tid + u * 256;
+        l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
     }
+    __syncthreads();
     const size_t plane = (size_t)g.C * g.Ttot;
-    unsigned short* o = out + (size_t)s * 2 * plane + ((size_t)k * g.Ttot + t) * kChunk;
-    *reinterpret_cast<u16x8_t*>(o) = hi[0];
-    *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
-    *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
-    *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+    unsigned short* const base = out + (size_t)s * 2 * plane + (size_t)k * g.Ttot * kChunk;
+    auto emit = [&](int t, const float (&v)[kChunk]) {
+        u16x8_t hi[2], lo[2];
+#pragma unroll
+        for (int u = 0; u < kChunk; u++) {
+            const unsigned pk = split_bf16(v[u]);
+            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
+            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+        }
+        unsigned short* o = base + (size_t)t * kChunk;
+        *reinterpret_cast<u16x8_t*>(o) = hi[0];
+        *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
+        *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
+        *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+    };
+    // level 0
+    for (int p = tid; p < kPrepRows * kPrepCols; p += 256) {
+        const int r = p / kPrepCols, x = p % kPrepCols;
+        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+        if (yy >= H || xx >= W) continue;
+        float v[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
+        emit(yy * W + xx, v);
+    }
+    if (!pooled) return;
+    // pooled levels: level l from level l-1 in LDS, then its pixels out
+    auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
+        for (int i = tid; i < kChunk * rows * cols; i += 256) {
+            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
+            float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
+            sum = sum + src[c][2 * r + 1][2 * x];
+            sum = sum + src[c][2 * r + 1][2 * x + 1];
+            dst[c][r][x] = 0.25f * sum;
+        }
+        __syncthreads();
+        for (int p = tid; p < rows * cols; p += 256) {
+            const int r = p / cols, x = p % cols;
+            const int yy = by * rows + r, xx = bx * cols + x;
+            if (yy >= g.h[l] || xx >= g.w[l]) continue;
+            float v[kChunk];
+#pragma unroll
+            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
+            emit(g.off[l] + yy * g.w[l] + xx, v);
+        }
+    };
+    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
+    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
+    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
 }
 
 // Which (edge, source tile, target tile) pairs hold at least one window cell:
@@ -561,37 +577,28 @@ Geom make_geom(const slk_ctx* ctx) {
     g.HW = ctx->HW;
     g.C = ctx->C;
     g.levels = ctx->levels;
-    int t = 0, pt = 0;
+    int t = 0;
     for (int l = 0; l < kMaxLevels; l++) {
         g.h[l] = l < ctx->levels ? ctx->lh[l] : 0;
         g.w[l] = l < ctx->levels ? ctx->lw[l] : 1;
         g.off[l] = t;
-        g.poff[l] = l >= 1 ? pt : 0;
         if (l < ctx->levels) {
             t += g.h[l] * g.w[l];
-            if (l >= 1) pt += g.h[l] * g.w[l];
         }
     }
     g.Ttot = t;
-    g.pool_hw = pt;
     return g;
 }
 
 template <typename Tin>
 int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
-               int slot_lo, int nslots, int trows, bool pooled, hipStream_t stream) {
+               int slot_lo, int nslots, bool pooled, hipStream_t stream) {
     if (nslots <= 0) return SLK_OK;
-    float* pool = ctx->split_pool.as<float>();
-    if (pooled) {
-        for (int l = 1; l < g.levels; l++) {
-            const int n = g.h[l] * g.w[l];
-            hipLaunchKernelGGL(k_feat_pool<Tin>, dim3((n + 255) / 256, g.C, nslots), dim3(256),
-                               0, stream, fm, fstride, sf, slot_lo, pool, g, l);
-        }
-    }
-    hipLaunchKernelGGL(k_feat_split<Tin>, dim3((trows + 255) / 256, g.C / kChunk, nslots),
-                       dim3(256), 0, stream, fm, fstride, sf, slot_lo, pool,
-                       ctx->split_feat.as<unsigned short>(), g, trows);
+    const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
+    const int nby = (g.h[0] + kPrepRows - 1) / kPrepRows;
+    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3(nbx * nby, g.C / kChunk, nslots), dim3(256), 0,
+                       stream, fm, fstride, sf, slot_lo, ctx->split_feat.as<unsigned short>(), g,
+                       pooled ? 1 : 0, nbx);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -617,7 +624,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
                 es.si[e] = slot_of(ii_host[e]);
                 es.sj[e] = slot_of(jj_host[e]);
             }
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, g.Ttot, true, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, true, stream));
         } else {
             sf.da = ii_dev;
             sf.db = jj_dev;
@@ -627,8 +634,8 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
                 es.sj[e] = n + e;
             }
             // sources only need level 0; targets need every level
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, g.HW, false, stream));
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, g.Ttot, true, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, true, stream));
         }
     }
     const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
@@ -661,7 +668,6 @@ int corr_split_alloc(slk_ctx* ctx) {
     const Geom g = make_geom(ctx);
     const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
     SLK_TRY(ctx->split_feat.ensure(slots * 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short)));
-    SLK_TRY(ctx->split_pool.ensure(slots * (size_t)g.C * std::max(g.pool_hw, 1) * sizeof(float)));
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;

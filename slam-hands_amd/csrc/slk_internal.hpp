@@ -74,8 +74,8 @@ struct slk_ctx {
     // batched-path scratch: 8x8 lookup windows [max_batch][4 levels][8 rows][HW][8]
     slk::DevBuf batch_win;
     // batched-path operands: bf16 hi/lo split of every level's features per
-    // frame slot, and the fp32 pooled features they are split from
-    slk::DevBuf split_feat, split_pool;
+    // frame slot
+    slk::DevBuf split_feat;
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
     int ws_grid = 0;        // workgroups of the batched correlation kernel
