@@ -284,9 +284,10 @@ struct alignas(16) SplitSmem {
     union {
         struct {
             // [stage][hi/lo][row * 16 + swizzled k]: 32-byte rows, the two
-            // 16-byte halves of row r swapped when bit 2 of r is set, so that
-            // both the staging writes (a pair of lanes per row) and the MFMA
-            // operand reads (8 rows per 128-byte phase) touch 32 distinct banks
+            // 16-byte halves of row r swapped when bit 2 xor bit 3 of r is
+            // set, so that the MFMA operand reads (16 lanes = 16 rows per
+            // 256-byte pass of a 128-bit read over 64 banks) touch 64
+            // distinct banks; the staging writes are contiguous 1 KB blocks
             unsigned short A[kStages][2][kSrcTile * kChunk];
             unsigned short B[kStages][2][kTgtTile * kChunk];
         } st;
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // in-range row: an MFMA output D[i][j] only combines row i of A with
     // column j of B, so such rows only reach accumulator cells never read.
     const int hr = tid >> 1;
-    const int hh = ((tid & 1) ^ ((hr >> 2) & 1)) * 8;  // rows hr and 128 + hr share bit 2
+    const int hh = ((tid & 1) ^ (((hr >> 2) ^ (hr >> 3)) & 1)) * 8;  // rows hr, 128 + hr alike
     const unsigned short* ga = fa + (size_t)std::min(p0 + hr, HW - 1) * kChunk + hh;
     const unsigned short* gb0 = fb + (size_t)std::min(t0 + hr, Ttot - 1) * kChunk + hh;
     const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
@@ -417,9 +418,9 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         for (int tb = 0; tb < 4; tb++) acc[sb][tb] = (f32x16){0};
     // MFMA operand layout: lane l holds row l%32, k = 8*(l/32)..+7; every
     // operand block starts at a multiple of 32 rows, so the swizzle bit of the
-    // lane's row is bit 2 of l%32
+    // lane's row is bit 2 xor bit 3 of l%32
     const int orow = lane & 31;
-    const int ooff = orow * kChunk + ((((lane >> 5) ^ ((orow >> 2) & 1))) * 8);
+    const int ooff = orow * kChunk + ((((lane >> 5) ^ (((orow >> 2) ^ (orow >> 3)) & 1))) * 8);
     auto compute = [&](int st) {
         u16x8_t ah[2], al[2];
 #pragma unroll
