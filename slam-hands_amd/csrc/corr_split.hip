@@ -23,8 +23,9 @@
 // of all levels (hi = rne(x), lo = rne(x - hi)), stored chunk-major
 // [plane][C/16][rows][16] so a 16-channel chunk of consecutive rows is one
 // contiguous block.
-// Stage 2 (k_tile_mask): which (edge, source tile, target tile) pairs hold any
-// window cell; the others are never computed.
+// Stage 2 (tile_mask_edge, workgroups of the same launch as stage 1): which
+// (edge, source tile, target tile) pairs hold any window cell; the others are
+// never computed.
 // Stage 3 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
 // hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_bf16 (exact products, fp32
 // accumulation; the dropped lo.lo term is ~2^-16 relative), staging 16-channel
@@ -79,121 +80,35 @@ __device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
 
-// Feature preparation of one frame slot, one launch: a workgroup takes a
-// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
-// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
-// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
-// a pooled pixel's parents always lie in the block), and writes the bf16
-// hi/lo split of every pixel of the levels present, 16 channels = 32 bytes
-// per pixel and plane, into out[slot][plane][C/16][Ttot][16]. `pooled` = 0
-// writes level 0 only (source slots). Grid (blocks, C/16, slots).
-constexpr int kPrepRows = 8, kPrepCols = 64;
-template <typename Tin>
-__global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
-                                                   SlotFrames sf, int slot_lo,
-                                                   unsigned short* __restrict__ out, Geom g,
-                                                   int pooled, int nbx) {
-    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
-    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
-    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
-    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
-    const int tid = threadIdx.x;
-    const int bx = blockIdx.x % nbx, by = blockIdx.x / nbx;
-    const int k = blockIdx.y, s = slot_lo + blockIdx.z;
-    const int W = g.w[0], H = g.h[0];
-    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
-    // all of a thread's loads are issued before the first is used
-    constexpr int kPer = kChunk * kPrepRows * kPrepCols / 256;
-    float ld[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = tid + u * 256;
-        const int c = i / (kPrepRows * kPrepCols);
-        const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-        const bool in = yy < H && xx < W;
-        ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-        if (!in) ld[u] = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = tid + u * 256;
-        l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
-    }
-    __syncthreads();
-    const size_t plane = (size_t)g.C * g.Ttot;
-    unsigned short* const base = out + (size_t)s * 2 * plane + (size_t)k * g.Ttot * kChunk;
-    auto emit = [&](int t, const float (&v)[kChunk]) {
-        u16x8_t hi[2], lo[2];
-#pragma unroll
-        for (int u = 0; u < kChunk; u++) {
-            const unsigned pk = split_bf16(v[u]);
-            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
-            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
-        }
-        unsigned short* o = base + (size_t)t * kChunk;
-        *reinterpret_cast<u16x8_t*>(o) = hi[0];
-        *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
-        *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
-        *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
-    };
-    // level 0
-    for (int p = tid; p < kPrepRows * kPrepCols; p += 256) {
-        const int r = p / kPrepCols, x = p % kPrepCols;
-        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-        if (yy >= H || xx >= W) continue;
-        float v[kChunk];
-#pragma unroll
-        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
-        emit(yy * W + xx, v);
-    }
-    if (!pooled) return;
-    // pooled levels: level l from level l-1 in LDS, then its pixels out
-    auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
-        for (int i = tid; i < kChunk * rows * cols; i += 256) {
-            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
-            float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
-            sum = sum + src[c][2 * r + 1][2 * x];
-            sum = sum + src[c][2 * r + 1][2 * x + 1];
-            dst[c][r][x] = 0.25f * sum;
-        }
-        __syncthreads();
-        for (int p = tid; p < rows * cols; p += 256) {
-            const int r = p / cols, x = p % cols;
-            const int yy = by * rows + r, xx = bx * cols + x;
-            if (yy >= g.h[l] || xx >= g.w[l]) continue;
-            float v[kChunk];
-#pragma unroll
-            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
-            emit(g.off[l] + yy * g.w[l] + xx, v);
-        }
-    };
-    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
-    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
-    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
-}
-
 // Which (edge, source tile, target tile) pairs hold at least one window cell:
 // per source and level present, the window's clipped rows/columns span the
 // concatenated target indices [off + ya*w + xa, off + yb*w + xb], and every
 // target tile in that span is marked (a superset of the tiles holding a cell).
 // Tiles not marked are skipped by k_corr_split_win: they would store nothing.
-// Grid (edges), 1024 threads; an LDS bitmap of the edge's mtiles * ntiles
-// tiles, then the marked ones compacted in tile order into the edge's segment
-// list[e * tpe ..] (ids mt * ntiles + nt) and their number into
-// ctr[kCtrCount + e]. Workgroup 0 also zeroes the tile counters of
-// k_corr_split_win, which runs after this kernel on the same stream.
-constexpr int kMaskThreads = 1024;
+// One workgroup of kMaskThreads per edge: an LDS bitmap (`bits`, at least
+// ceil(mtiles * ntiles / 32) words) of the edge's tiles, then the marked ones
+// compacted in tile order into the edge's segment list[e * tpe ..] (ids
+// mt * ntiles + nt) and their number into ctr[kCtrCount + e]. Edge 0 also
+// zeroes the tile counters of k_corr_split_win, which runs after this on the
+// same stream. These workgroups run in the launch of k_feat_prep, beside the
+// feature preparation they do not depend on.
+constexpr int kMaskThreads = 256;
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
 constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
 constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
-__global__ __launch_bounds__(kMaskThreads) void k_tile_mask(const float* __restrict__ coords,
-                                                            int* __restrict__ list,
-                                                            int* __restrict__ ctr, Geom g,
-                                                            int mtiles, int ntiles) {
-    extern __shared__ unsigned bits[];
-    __shared__ int wave_sum[kMaskThreads / 64];
-    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+struct MaskArgs {
+    const float* coords;
+    int* list;
+    int* ctr;
+    int mtiles, ntiles, nedges;
+};
+__device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* bits,
+                               int* wave_sum) {
+    const float* coords = a.coords;
+    int* list = a.list;
+    int* ctr = a.ctr;
+    const int mtiles = a.mtiles, ntiles = a.ntiles;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int tpe = mtiles * ntiles;
     const int nw = (tpe + 31) / 32;
     for (int i = tid; i < nw; i += kMaskThreads) bits[i] = 0u;
@@ -280,6 +195,114 @@ __global__ __launch_bounds__(kMaskThreads) void k_tile_mask(const float* __restr
     if (tid == 0) ctr[kCtrCount + e] = base;
 }
 
+// Feature preparation of one frame slot, one launch: a workgroup takes a
+// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
+// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
+// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
+// a pooled pixel's parents always lie in the block), and writes the bf16
+// hi/lo split of every pixel of the levels present, 16 channels = 32 bytes
+// per pixel and plane, into out[slot][plane][C/16][Ttot][16]. `pooled` = 0
+// writes level 0 only (source slots). One-dimensional grid: first, when
+// mk.list is set, one tile-mask workgroup per edge (tile_mask_edge, whose
+// bitmap is the level-0 LDS array; they are the longer chains, so they are
+// dispatched first), then the blocks x C/16 x slots preparation workgroups
+// (block fastest).
+constexpr int kPrepRows = 8, kPrepCols = 64;
+constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;  // level 0 / tile bitmap
+static_assert(kMaskThreads == 256, "the tile-mask workgroups share k_feat_prep's size");
+template <typename Tin>
+__global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
+                                                   SlotFrames sf, int slot_lo,
+                                                   unsigned short* __restrict__ out, Geom g,
+                                                   int pooled, int nbx, int nblk, int nmask,
+                                                   MaskArgs mk) {
+    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
+    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
+    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
+    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
+    __shared__ int wave_sum[kMaskThreads / 64];
+    if ((int)blockIdx.x < nmask) {  // uniform
+        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum);
+        return;
+    }
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x - nmask;
+    const int blk = b % nblk, rest = b / nblk;
+    const int bx = blk % nbx, by = blk / nbx;
+    const int k = rest % (g.C / kChunk), s = slot_lo + rest / (g.C / kChunk);
+    const int W = g.w[0], H = g.h[0];
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
+    // all of a thread's loads are issued before the first is used
+    constexpr int kPer = kChunk * kPrepRows * kPrepCols / 256;
+    float ld[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int i = tid + u * 256;
+        const int c = i / (kPrepRows * kPrepCols);
+        const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+        const bool in = yy < H && xx < W;
+        ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+        if (!in) ld[u] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int i = tid + u * 256;
+        l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
+    }
+    __syncthreads();
+    const size_t plane = (size_t)g.C * g.Ttot;
+    unsigned short* const base = out + (size_t)s * 2 * plane + (size_t)k * g.Ttot * kChunk;
+    auto emit = [&](int t, const float (&v)[kChunk]) {
+        u16x8_t hi[2], lo[2];
+#pragma unroll
+        for (int u = 0; u < kChunk; u++) {
+            const unsigned pk = split_bf16(v[u]);
+            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
+            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+        }
+        unsigned short* o = base + (size_t)t * kChunk;
+        *reinterpret_cast<u16x8_t*>(o) = hi[0];
+        *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
+        *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
+        *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+    };
+    // level 0
+    for (int p = tid; p < kPrepRows * kPrepCols; p += 256) {
+        const int r = p / kPrepCols, x = p % kPrepCols;
+        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+        if (yy >= H || xx >= W) continue;
+        float v[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
+        emit(yy * W + xx, v);
+    }
+    if (!pooled) return;
+    // pooled levels: level l from level l-1 in LDS, then its pixels out
+    auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
+        for (int i = tid; i < kChunk * rows * cols; i += 256) {
+            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
+            float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
+            sum = sum + src[c][2 * r + 1][2 * x];
+            sum = sum + src[c][2 * r + 1][2 * x + 1];
+            dst[c][r][x] = 0.25f * sum;
+        }
+        __syncthreads();
+        for (int p = tid; p < rows * cols; p += 256) {
+            const int r = p / cols, x = p % cols;
+            const int yy = by * rows + r, xx = bx * cols + x;
+            if (yy >= g.h[l] || xx >= g.w[l]) continue;
+            float v[kChunk];
+#pragma unroll
+            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
+            emit(g.off[l] + yy * g.w[l] + xx, v);
+        }
+    };
+    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
+    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
+    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
+}
+
 struct alignas(16) SplitSmem {
     union {
         struct {
@@ -333,7 +356,7 @@ __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
 }
 
 // Grid: a fixed number of workgroups of 256 threads, two per CU, each taking
-// marked tiles (k_tile_mask) one at a time from its XCD's counter: tile
+// marked tiles (tile_mask_edge) one at a time from its XCD's counter: tile
 // index idx runs over the edges' segments concatenated, workgroup blockIdx % 8
 // runs on that XCD and serves the XCD's contiguous eighth of those indices,
 // so the edges an XCD works on stay in its L2, and no CU idles while tiles
@@ -591,15 +614,20 @@ Geom make_geom(const slk_ctx* ctx) {
     return g;
 }
 
+// the preparation of nslots frame slots and, when mk.list is set, the tile
+// mask of mk.nedges edges, in one launch
 template <typename Tin>
 int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
-               int slot_lo, int nslots, bool pooled, hipStream_t stream) {
-    if (nslots <= 0) return SLK_OK;
+               int slot_lo, int nslots, bool pooled, const MaskArgs& mk, hipStream_t stream) {
     const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
-    const int nby = (g.h[0] + kPrepRows - 1) / kPrepRows;
-    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3(nbx * nby, g.C / kChunk, nslots), dim3(256), 0,
-                       stream, fm, fstride, sf, slot_lo, ctx->split_feat.as<unsigned short>(), g,
-                       pooled ? 1 : 0, nbx);
+    const int nblk = nbx * ((g.h[0] + kPrepRows - 1) / kPrepRows);
+    const long nprep = (long)nblk * (g.C / kChunk) * std::max(nslots, 0);
+    const long nmask = mk.list ? mk.nedges : 0;
+    if (nprep + nmask == 0) return SLK_OK;
+    if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
+    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(256), 0, stream,
+                       fm, fstride, sf, slot_lo, ctx->split_feat.as<unsigned short>(), g,
+                       pooled ? 1 : 0, nbx, nblk, (int)nmask, mk);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -611,7 +639,16 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     const Geom g = make_geom(ctx);
     SlotFrames sf{};
     EdgeSlots es{};
+    const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
+    const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
+    const long total = (long)n * mtiles * ntiles;
+    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
+    if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
+        return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
+    MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), mtiles, ntiles, n};
+    const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
     {
+        // feature preparation and the tile mask, one launch
         ProfScope ps(ctx, "corr_feat_prep", stream);
         if (ii_host) {
             int ns = 0;
@@ -625,7 +662,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
                 es.si[e] = slot_of(ii_host[e]);
                 es.sj[e] = slot_of(jj_host[e]);
             }
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, true, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, true, mk, stream));
         } else {
             sf.da = ii_dev;
             sf.db = jj_dev;
@@ -635,19 +672,9 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
                 es.sj[e] = n + e;
             }
             // sources only need level 0; targets need every level
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, stream));
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, true, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
+            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, true, mk, stream));
         }
-    }
-    const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
-    const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
-    const long total = (long)n * mtiles * ntiles;
-    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
-    {
-        ProfScope ps(ctx, "corr_tile_mask", stream);
-        const size_t shm = (size_t)((mtiles * ntiles + 31) / 32) * sizeof(unsigned);
-        hipLaunchKernelGGL(k_tile_mask, dim3(n), dim3(kMaskThreads), shm, stream, coords,
-                           ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), g, mtiles, ntiles);
     }
     {
         ProfScope ps(ctx, "corr_window", stream);
