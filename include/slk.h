@@ -109,6 +109,22 @@ int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fmaps, int dty
                                         const int* jj_dev, int B,
                                         const float* coords, float* out,
                                         hipStream_t stream);
+/* The same batched correlation over frames split once per pass: the
+ * reference's backend update (run_update_pass over batches of 48 edges,
+ * main.cu:2197-2203) rebuilds each frame's operands in every batch that
+ * touches it. slk_corr_prepare_frames splits frames [0, nframes) of fmaps
+ * (all levels, bf16 hi/lo; 2*C*(h*w*85/64) bytes per frame, held by the
+ * context until the next call or slk_destroy); the _prepared calls then
+ * take ii_host/jj_host as frame indices into them and compute the batches
+ * without that step. Call it again whenever fmaps change. Results are
+ * bitwise those of slk_corr_batch_build_and_sample on the same fmaps. Needs
+ * the split contraction (C a multiple of 16; fp16 fmaps, or fp32 with
+ * SLK_PREC_BF16X3). */
+int slk_corr_prepare_frames(slk_ctx* ctx, const void* fmaps, int dtype, long fmap_stride,
+                            int nframes, hipStream_t stream);
+int slk_corr_batch_build_and_sample_prepared(slk_ctx* ctx, const int* ii_host,
+                                             const int* jj_host, int B, const float* coords,
+                                             float* out, hipStream_t stream);
 
 /* CudaDroid::build_correlation(i, j), main.cu:1500-1526 (and
  * CorrBlock::build for one edge, corr.cuh:84): volume of (f_i, f_j) and its

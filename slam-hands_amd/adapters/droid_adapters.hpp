@@ -82,11 +82,28 @@ class CorrEngine {
     // edge arrays; coords [B][2][h*w] -> corr_out [B][196][h*w].
     void batch_build_and_sample_correlation(int batch_size, int edge_start, float* coords_2hw,
                                             float* corr_out_196hw) {
-        check(slk_corr_batch_build_and_sample(ctx_, fmaps_, dtype_, frame_stride(),
-                                              ii_host_ + edge_start, jj_host_ + edge_start,
-                                              batch_size, coords_2hw, corr_out_196hw, nullptr),
-              "batch_build_and_sample_correlation");
+        if (prepared_ > 0)
+            check(slk_corr_batch_build_and_sample_prepared(
+                      ctx_, ii_host_ + edge_start, jj_host_ + edge_start, batch_size,
+                      coords_2hw, corr_out_196hw, nullptr),
+                  "batch_build_and_sample_correlation");
+        else
+            check(slk_corr_batch_build_and_sample(ctx_, fmaps_, dtype_, frame_stride(),
+                                                  ii_host_ + edge_start, jj_host_ + edge_start,
+                                                  batch_size, coords_2hw, corr_out_196hw,
+                                                  nullptr),
+                  "batch_build_and_sample_correlation");
     }
+
+    // Optional: split keyframes [0, nframes) once (at the start of an update
+    // pass); the batched calls then skip per-call feature preparation until
+    // unprepare() or the next prepare_frames(). Call it again when fmaps change.
+    void prepare_frames(int nframes) {
+        check(slk_corr_prepare_frames(ctx_, fmaps_, dtype_, frame_stride(), nframes, nullptr),
+              "prepare_frames");
+        prepared_ = nframes;
+    }
+    void unprepare() { prepared_ = 0; }
 
     // corr_volume (l = 0) / corr_pyramid[l] of the last build (main.cu:1324-1326).
     const float* corr_level(int l, int* h2 = nullptr, int* w2 = nullptr) {
@@ -106,6 +123,7 @@ class CorrEngine {
     slk_ctx* context() const { return ctx_; }
 
   private:
+    int prepared_ = 0;
     long frame_stride() const { return (long)C_ * h_ * w_; }
     const void* frame(int k) const {
         const size_t esz = dtype_ == SLK_F16 ? 2 : 4;

@@ -163,6 +163,7 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     slk::ba_destroy(ctx);
     ctx->batch_win.release();
     ctx->split_feat.release();
+    ctx->prep_feat.release();
     ctx->tile_ctr.release();
     ctx->tile_list.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();

@@ -834,6 +834,52 @@ extern "C" int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fma
                            coords, out, stream);
 }
 
+extern "C" int slk_corr_prepare_frames(slk_ctx* ctx, const void* fmaps, int dtype,
+                                       long fmap_stride, int nframes, hipStream_t stream) {
+    if (!ctx || !fmaps) return fail(SLK_E_ARG, "corr_prepare_frames: null argument");
+    if (dtype != SLK_F32 && dtype != SLK_F16)
+        return fail(SLK_E_ARG, "corr_prepare_frames: bad dtype");
+    if (fmap_stride < (long)ctx->C * ctx->HW)
+        return fail(SLK_E_ARG, "corr_prepare_frames: fmap_stride < C*h*w");
+    if (!corr_split_supported(ctx) || (dtype == SLK_F32 && ctx->corr_prec == SLK_PREC_FP32))
+        return fail(SLK_E_ARG, "corr_prepare_frames: needs the split contraction (C % 16 == 0, "
+                               "not SLK_PREC_FP32)");
+    return corr_split_prepare(ctx, fmaps, dtype, fmap_stride, nframes, stream);
+}
+
+extern "C" int slk_corr_batch_build_and_sample_prepared(slk_ctx* ctx, const int* ii_host,
+                                                        const int* jj_host, int B,
+                                                        const float* coords, float* out,
+                                                        hipStream_t stream) {
+    if (!ctx || !coords || !out || B < 0 || (B > 0 && (!ii_host || !jj_host)))
+        return fail(SLK_E_ARG, "corr_batch_prepared: null argument");
+    if (ctx->prep_nframes <= 0)
+        return fail(SLK_E_STATE, "corr_batch_prepared: no frames prepared");
+    for (int e = 0; e < B; e++)
+        if (ii_host[e] < 0 || jj_host[e] < 0 || ii_host[e] >= ctx->prep_nframes ||
+            jj_host[e] >= ctx->prep_nframes)
+            return fail(SLK_E_ARG, "corr_batch_prepared: frame index outside the prepared frames");
+    const int HW = ctx->HW;
+    const int nch = ctx->levels * 49;
+    float* win = ctx->batch_win.as<float>();
+    const LevelIn lv = level_in(ctx, nullptr);
+    for (int b0 = 0; b0 < B; b0 += ctx->max_batch) {
+        const int nb = B - b0 < ctx->max_batch ? B - b0 : ctx->max_batch;
+        for (int s0 = 0; s0 < nb; s0 += kMaxEdgesPerLaunch) {
+            const int n = nb - s0 < kMaxEdgesPerLaunch ? nb - s0 : kMaxEdgesPerLaunch;
+            SLK_TRY(corr_split_windows_prepared(ctx, ii_host + b0 + s0, jj_host + b0 + s0, n,
+                                                coords + (size_t)(b0 + s0) * 2 * HW, win, s0,
+                                                stream));
+        }
+        dim3 grid((HW + 255) / 256, ctx->levels, nb);
+        ProfScope ps(ctx, "corr_lookup_win", stream);
+        hipLaunchKernelGGL(k_corr_lookup_win, grid, dim3(256), 0, stream, lv, win,
+                           coords + (size_t)b0 * 2 * HW, out + (size_t)b0 * nch * HW, HW, nch);
+        SLK_HIP(hipGetLastError());
+    }
+    return SLK_OK;
+}
+
 extern "C" int slk_corr_build(slk_ctx* ctx, const void* f_i, const void* f_j, int dtype,
                               hipStream_t stream) {
     if (!ctx || !f_i || !f_j) return fail(SLK_E_ARG, "corr_build: null argument");

@@ -64,6 +64,7 @@ struct SlotFrames {
     const int* da;
     const int* db;
     int nb;
+    int ident;  // slot s holds frame s (prepared frames)
     int f[kMaxSlots];
 };
 
@@ -73,6 +74,7 @@ struct EdgeSlots {
 };
 
 __device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
+    if (m.ident) return s;
     if (m.da) return s < m.nb ? m.da[s] : m.db[s - m.nb];
     return m.f[s];
 }
@@ -617,8 +619,9 @@ Geom make_geom(const slk_ctx* ctx) {
 // the preparation of nslots frame slots and, when mk.list is set, the tile
 // mask of mk.nedges edges, in one launch
 template <typename Tin>
-int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
-               int slot_lo, int nslots, bool pooled, const MaskArgs& mk, hipStream_t stream) {
+int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
+                  int slot_lo, int nslots, bool pooled, const MaskArgs& mk, unsigned short* out,
+                  hipStream_t stream) {
     const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
     const int nblk = nbx * ((g.h[0] + kPrepRows - 1) / kPrepRows);
     const long nprep = (long)nblk * (g.C / kChunk) * std::max(nslots, 0);
@@ -626,8 +629,44 @@ int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, 
     if (nprep + nmask == 0) return SLK_OK;
     if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
     hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(256), 0, stream,
-                       fm, fstride, sf, slot_lo, ctx->split_feat.as<unsigned short>(), g,
-                       pooled ? 1 : 0, nbx, nblk, (int)nmask, mk);
+                       fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, nbx, nblk, (int)nmask,
+                       mk);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+template <typename Tin>
+int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
+               int slot_lo, int nslots, bool pooled, const MaskArgs& mk, hipStream_t stream) {
+    return prep_slots_to(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk,
+                         ctx->split_feat.as<unsigned short>(), stream);
+}
+
+// The tile-mask workgroups (with the preparation of nslots slots when
+// nslots > 0) and the window kernel over `feat`, for edges whose slots are es.
+template <typename Tin>
+int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf,
+                     const Geom& g, int slot_lo, int nslots, bool pooled, const EdgeSlots& es,
+                     const unsigned short* feat, int n, const float* coords, float* win,
+                     int slot0, hipStream_t stream) {
+    const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
+    const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
+    const long total = (long)n * mtiles * ntiles;
+    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
+    if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
+        return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
+    MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), mtiles, ntiles, n};
+    {
+        // feature preparation and the tile mask, one launch
+        ProfScope ps(ctx, "corr_feat_prep", stream);
+        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, stream));
+    }
+    {
+        ProfScope ps(ctx, "corr_window", stream);
+        hipLaunchKernelGGL(k_corr_split_win, dim3(ctx->ws_grid), dim3(256), 0, stream, feat, es,
+                           coords, win, slot0, g, ctx->alpha, mtiles, ntiles, n,
+                           ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>());
+    }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -639,52 +678,37 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     const Geom g = make_geom(ctx);
     SlotFrames sf{};
     EdgeSlots es{};
-    const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
-    const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
-    const long total = (long)n * mtiles * ntiles;
-    if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
-    if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
-        return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
-    MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), mtiles, ntiles, n};
-    const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
-    {
-        // feature preparation and the tile mask, one launch
-        ProfScope ps(ctx, "corr_feat_prep", stream);
-        if (ii_host) {
-            int ns = 0;
-            auto slot_of = [&](int f) {
-                for (int s = 0; s < ns; s++)
-                    if (sf.f[s] == f) return s;
-                sf.f[ns] = f;
-                return ns++;
-            };
-            for (int e = 0; e < n; e++) {
-                es.si[e] = slot_of(ii_host[e]);
-                es.sj[e] = slot_of(jj_host[e]);
-            }
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, ns, true, mk, stream));
-        } else {
-            sf.da = ii_dev;
-            sf.db = jj_dev;
-            sf.nb = n;
-            for (int e = 0; e < n; e++) {
-                es.si[e] = e;
-                es.sj[e] = n + e;
-            }
-            // sources only need level 0; targets need every level
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
-            SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, n, n, true, mk, stream));
+    const unsigned short* feat = ctx->split_feat.as<unsigned short>();
+    if (ii_host) {
+        int ns = 0;
+        auto slot_of = [&](int f) {
+            for (int s = 0; s < ns; s++)
+                if (sf.f[s] == f) return s;
+            sf.f[ns] = f;
+            return ns++;
+        };
+        for (int e = 0; e < n; e++) {
+            es.si[e] = slot_of(ii_host[e]);
+            es.sj[e] = slot_of(jj_host[e]);
         }
+        return mask_and_windows(ctx, fm, fstride, sf, g, 0, ns, true, es, feat, n, coords, win,
+                                slot0, stream);
     }
+    sf.da = ii_dev;
+    sf.db = jj_dev;
+    sf.nb = n;
+    for (int e = 0; e < n; e++) {
+        es.si[e] = e;
+        es.sj[e] = n + e;
+    }
+    // sources only need level 0 (their own launch); targets need every level
     {
-        ProfScope ps(ctx, "corr_window", stream);
-        hipLaunchKernelGGL(k_corr_split_win, dim3(ctx->ws_grid), dim3(256), 0, stream,
-                           ctx->split_feat.as<unsigned short>(), es, coords, win, slot0, g,
-                           ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
-                           ctx->tile_ctr.as<int>());
+        ProfScope ps(ctx, "corr_feat_prep", stream);
+        const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
+        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
     }
-    SLK_HIP(hipGetLastError());
-    return SLK_OK;
+    return mask_and_windows(ctx, fm, fstride, sf, g, n, n, true, es, feat, n, coords, win, slot0,
+                            stream);
 }
 
 }  // namespace
@@ -722,6 +746,45 @@ int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
                              ii_dev, jj_dev, n, coords, win, slot0, stream);
     return split_windows(ctx, static_cast<const _Float16*>(fmaps), fstride, ii_host, jj_host,
                          ii_dev, jj_dev, n, coords, win, slot0, stream);
+}
+
+
+int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, int nframes,
+                       hipStream_t stream) {
+    if (nframes <= 0) return fail(SLK_E_ARG, "corr_prepare_frames: nframes <= 0");
+    const Geom g = make_geom(ctx);
+    const size_t bytes = (size_t)nframes * 2 * g.C * g.Ttot * sizeof(unsigned short);
+    if (bytes > ctx->prep_feat.bytes && ctx->prep_feat.ptr)
+        SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old frames
+    SLK_TRY(ctx->prep_feat.ensure(bytes));
+    SlotFrames sf{};
+    sf.ident = 1;
+    const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
+    ProfScope ps(ctx, "corr_prepare_frames", stream);
+    if (dtype == SLK_F32)
+        SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,
+                              true, none, ctx->prep_feat.as<unsigned short>(), stream));
+    else
+        SLK_TRY(prep_slots_to(ctx, static_cast<const _Float16*>(fmaps), fstride, sf, g, 0,
+                              nframes, true, none, ctx->prep_feat.as<unsigned short>(), stream));
+    ctx->prep_nframes = nframes;
+    return SLK_OK;
+}
+
+int corr_split_windows_prepared(slk_ctx* ctx, const int* ii_host, const int* jj_host, int n,
+                                const float* coords, float* win, int slot0, hipStream_t stream) {
+    if (n <= 0) return SLK_OK;
+    if (n > kMaxEdgesPerLaunch || n > ctx->max_batch)
+        return fail(SLK_E_ARG, "corr_split_windows: too many edges for one launch");
+    const Geom g = make_geom(ctx);
+    EdgeSlots es{};
+    for (int e = 0; e < n; e++) {
+        es.si[e] = ii_host[e];
+        es.sj[e] = jj_host[e];
+    }
+    const SlotFrames none{};
+    return mask_and_windows(ctx, static_cast<const float*>(nullptr), 0, none, g, 0, 0, true, es,
+                            ctx->prep_feat.as<unsigned short>(), n, coords, win, slot0, stream);
 }
 
 }  // namespace slk

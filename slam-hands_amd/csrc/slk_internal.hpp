@@ -76,6 +76,9 @@ struct slk_ctx {
     // batched-path operands: bf16 hi/lo split of every level's features per
     // frame slot
     slk::DevBuf split_feat;
+    // frames split once by slk_corr_prepare_frames (slot = frame index)
+    slk::DevBuf prep_feat;
+    int prep_nframes = 0;
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
     int ws_grid = 0;        // workgroups of the batched correlation kernel
@@ -131,6 +134,10 @@ int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
                        const int* ii_host, const int* jj_host, const int* ii_dev,
                        const int* jj_dev, int n, const float* coords, float* win, int slot0,
                        hipStream_t stream);
+int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride, int nframes,
+                       hipStream_t stream);
+int corr_split_windows_prepared(slk_ctx* ctx, const int* ii_host, const int* jj_host, int n,
+                                const float* coords, float* win, int slot0, hipStream_t stream);
 // ba.hip
 int ba_create(slk_ctx* ctx);
 void ba_destroy(slk_ctx* ctx);

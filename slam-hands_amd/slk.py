@@ -29,6 +29,7 @@ EXPORTS = [
     "slk_create", "slk_destroy", "slk_last_error", "slk_profile_enable", "slk_profile_kernel",
     "slk_set_corr_precision",
     "slk_corr_batch_build_and_sample", "slk_corr_batch_build_and_sample_dev",
+    "slk_corr_prepare_frames", "slk_corr_batch_build_and_sample_prepared",
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
     "slk_projmap", "slk_pose_retr", "slk_disp_retr", "slk_frame_distance", "slk_clamp_disps",
@@ -78,6 +79,8 @@ def lib():
             "slk_set_corr_precision": [P, I],
             "slk_corr_batch_build_and_sample": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_batch_build_and_sample_dev": [P, P, I, L, P, P, I, P, P, P],
+            "slk_corr_prepare_frames": [P, P, I, L, I, P],
+            "slk_corr_batch_build_and_sample_prepared": [P, P, P, I, P, P, P],
             "slk_corr_build": [P, P, P, I, P],
             "slk_corr_sample": [P, P, P, P],
             "slk_corr_level": [P, I, ctypes.POINTER(P), ctypes.POINTER(I), ctypes.POINTER(I)],
@@ -318,6 +321,16 @@ class Context:
         check(lib().slk_corr_batch_build_and_sample_dev(self.ptr, _p(fmaps), dtype, stride,
                                                         _p(ii_dev), _p(jj_dev), B, _p(coords),
                                                         _p(out), stream))
+
+    # frames split once per pass, then batches over them (slk_corr_prepare_frames)
+    def prepare_frames(self, fmaps, nframes, dtype=SLK_F32, fmap_stride=None, stream=None):
+        stride = fmap_stride if fmap_stride is not None else self.C * self.h * self.w
+        check(lib().slk_corr_prepare_frames(self.ptr, _p(fmaps), dtype, stride, nframes, stream))
+
+    def batch_build_and_sample_prepared(self, ii, jj, coords, out, stream=None):
+        (ii, iip), (_jj, jjp) = _host_i32(ii), _host_i32(jj)
+        check(lib().slk_corr_batch_build_and_sample_prepared(
+            self.ptr, iip, jjp, len(ii), _p(coords), _p(out), stream))
 
     # main.cu:1500 build_correlation / :1529 sample_correlation
     def build_correlation(self, f_i, f_j, dtype=SLK_F32, stream=None):

@@ -298,3 +298,47 @@ def test_standalone_pool_sample_and_layout_kernels(slk):
     slk.check(slk.lib().slk_coords_hw2_to_2hw(hd.ptr, chw.ptr, M, HW, None))
     slk.hip().sync()
     np.testing.assert_array_equal(chw.to_host(), hw2.transpose(0, 2, 1))
+
+
+def test_prepared_frames_match_per_call_preparation(slk):
+    """slk_corr_prepare_frames + _prepared batches: bitwise the windows and
+    lookups of slk_corr_batch_build_and_sample on the same fmaps, for a
+    100-keyframe graph whose batches touch more frames than one launch
+    prepares (B = 130 > max_batch = 48: several launches), with fp32 and
+    fp16 fmaps; frame indices outside the prepared frames are rejected."""
+    announce("prepared frames, 100 keyframes, 130 edges")
+    h, w, n, B = 24, 32, 100, 130
+    rng = np.random.default_rng(60)
+    ii = rng.integers(0, n, B).astype(np.int32)
+    jj = rng.integers(0, n, B).astype(np.int32)
+    coords = wl.flow_coords(B, h, w, seed=61)
+    cd = slk.DeviceArray.from_host(coords)
+    for dtype, f in [(slk.SLK_F32, wl.frames(n, C=128, h=h, w=w, seed=62)),
+                     (slk.SLK_F16, wl.frames(n, C=128, h=h, w=w, seed=63).astype(np.float16))]:
+        ctx = slk.Context(h, w, C=128, max_batch=48, corr_scale=1.0 / 16.0)
+        fd = slk.DeviceArray.from_host(f)
+        a = slk.DeviceArray((B, 196, h * w))
+        b = slk.DeviceArray((B, 196, h * w))
+        ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, a, dtype=dtype)
+        ctx.prepare_frames(fd, n, dtype=dtype)
+        ctx.batch_build_and_sample_prepared(ii, jj, cd, b)
+        slk.hip().sync()
+        np.testing.assert_array_equal(b.to_host(), a.to_host())
+        with pytest.raises(slk.SlkError):
+            ctx.batch_build_and_sample_prepared(np.array([n], np.int32), np.array([0], np.int32),
+                                                cd, b)
+        ctx.close()
+    # and against the oracle on a few edges
+    full = [0, 57, 129]
+    f = wl.frames(n, C=128, h=h, w=w, seed=62)
+    ref = orc.corr_batch(f, ii[full], jj[full], coords[full], 1.0 / 16.0)
+    ctx = slk.Context(h, w, C=128, max_batch=48, corr_scale=1.0 / 16.0)
+    fd = slk.DeviceArray.from_host(f)
+    out = slk.DeviceArray((B, 196, h * w))
+    ctx.prepare_frames(fd, n)
+    ctx.batch_build_and_sample_prepared(ii, jj, cd, out)
+    slk.hip().sync()
+    got = out.to_host()
+    ctx.close()
+    for k, e in enumerate(full):
+        assert_close_rel(got[e], ref[k], what=f"prepared edge {e}")
