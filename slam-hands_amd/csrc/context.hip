@@ -101,10 +101,12 @@ extern "C" int slk_create(slk_ctx** out, int h, int w, int C, int max_batch, int
 }
 
 namespace {
+// Unfolded records' events go back to the pool once they have completed.
 void prof_clear(slk_ctx* ctx) {
     for (auto& r : ctx->prof_recs) {
-        (void)hipEventDestroy(r.a);
-        (void)hipEventDestroy(r.b);
+        (void)hipEventSynchronize(r.b);
+        ctx->prof_pool.push_back(r.a);
+        ctx->prof_pool.push_back(r.b);
     }
     ctx->prof_recs.clear();
     ctx->prof_names.clear();
@@ -129,8 +131,8 @@ int prof_fold(slk_ctx* ctx) {
         }
         ctx->prof_ms[k] += ms;
         ctx->prof_count[k] += 1;
-        (void)hipEventDestroy(r.a);
-        (void)hipEventDestroy(r.b);
+        ctx->prof_pool.push_back(r.a);
+        ctx->prof_pool.push_back(r.b);
     }
     ctx->prof_recs.clear();
     ctx->prof_dirty = false;
@@ -160,6 +162,8 @@ extern "C" int slk_profile_kernel(slk_ctx* ctx, int idx, const char** name, doub
 extern "C" int slk_destroy(slk_ctx* ctx) {
     if (!ctx) return SLK_OK;
     prof_clear(ctx);
+    for (hipEvent_t e : ctx->prof_pool) (void)hipEventDestroy(e);
+    ctx->prof_pool.clear();
     slk::ba_destroy(ctx);
     ctx->batch_win.release();
     ctx->split_feat.release();

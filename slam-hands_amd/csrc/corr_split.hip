@@ -49,6 +49,12 @@ constexpr int kSrcTile = 128;  // sources per workgroup
 constexpr int kTgtTile = 256;  // targets per workgroup
 constexpr int kChunk = 16;     // channels per LDS stage
 constexpr int kStages = 3;     // LDS stages: chunk k+2 streams in while chunk k is used
+// word 3 of a raw buffer resource on gfx9-family parts (32-bit data format,
+// no swizzle; range checking against num_records)
+constexpr int kBufWord3 = 0x00020000;
+// an offset past any buffer this file builds a resource for: such a store is
+// discarded by the range check
+constexpr int kBufDiscard = 0x7FFFFFF0;
 constexpr int kTStride = 68;   // floats per transposed-tile row (64 sources + 4 pad)
 constexpr int kMaxSlots = 2 * kMaxEdgesPerLaunch;
 
@@ -543,6 +549,14 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // window rows, so every read and store instruction covers 8 sources x 8
     // consecutive cells and all per-source set-up is plain per-lane arithmetic.
     const int g8 = lane >> 3, cx = lane & 7;
+    // Window stores go through a buffer resource over this edge's window slot:
+    // a lane whose cell is not stored (outside the tile, the grid or the
+    // source range) gets an offset past the slot's size, and the hardware
+    // discards the store. Every store instruction is then issued without a
+    // branch around it.
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        win + win_index(slot0 + e, 0, 0, HW, 0), 0, kMaxLevels * 64 * HW * (int)sizeof(float),
+        kBufWord3);
 
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
@@ -565,7 +579,8 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
             const bool pin = p0 + lsrc < HW;
             const float* Tcol = &sm.u.T[0][s];
-            float* wp = win + win_index(slot0 + e, 0, cx, HW, std::min(p0 + lsrc, HW - 1));
+            // byte offset of cell (cx, row 0) of level 0 in the slot
+            const int woff = (int)win_index(0, 0, cx, HW, std::min(p0 + lsrc, HW - 1)) * 4;
 #pragma unroll
             for (int l = 0; l < kMaxLevels; l++) {
                 if (lr0[l] > lr1[l]) continue;  // level not in this tile
@@ -590,7 +605,9 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                 }
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++)
-                    if (ok[cy]) wp[(size_t)(l * 8 + cy) * HW * 8] = alpha * v[cy];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __builtin_bit_cast(unsigned, alpha * v[cy]), wrs,
+                        ok[cy] ? woff + (l * 8 + cy) * HW * 32 : kBufDiscard, 0, 0);
             }
         }
     }

@@ -98,6 +98,9 @@ struct slk_ctx {
     std::vector<double> prof_ms;
     std::vector<int> prof_count;
     bool prof_dirty = false;
+    // events of folded records, reused so that a profiled launch sequence
+    // creates no events once the pool holds enough of them
+    std::vector<hipEvent_t> prof_pool;
 };
 
 namespace slk {
@@ -107,18 +110,27 @@ struct ProfScope {
     const char* name;
     hipStream_t stream;
     hipEvent_t a = nullptr;
+    static hipEvent_t take(slk_ctx* c) {
+        if (!c->prof_pool.empty()) {
+            hipEvent_t e = c->prof_pool.back();
+            c->prof_pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+    }
     ProfScope(slk_ctx* c, const char* n, hipStream_t s) : ctx(c), name(n), stream(s) {
-        if (ctx && ctx->prof && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, stream);
+        if (ctx && ctx->prof && (a = take(ctx)) != nullptr) (void)hipEventRecord(a, stream);
     }
     ~ProfScope() {
         if (!a) return;
-        hipEvent_t b = nullptr;
-        if (hipEventCreate(&b) == hipSuccess && hipEventRecord(b, stream) == hipSuccess) {
+        hipEvent_t b = take(ctx);
+        if (b && hipEventRecord(b, stream) == hipSuccess) {
             ctx->prof_recs.push_back({name, a, b});
             ctx->prof_dirty = true;
         } else {
-            (void)hipEventDestroy(a);
-            if (b) (void)hipEventDestroy(b);
+            ctx->prof_pool.push_back(a);
+            if (b) ctx->prof_pool.push_back(b);
         }
     }
 };
