@@ -393,6 +393,16 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         pre = incl - c;
         cnt = __builtin_amdgcn_readlane(incl, 63);
     }
+    // Workgroups b and b + gridDim.x / 2 are dispatched to the same CU. Started
+    // together they run their chunk loops together and then both extract,
+    // leaving the matrix cores idle; the second half starts about half a tile
+    // later (three sleeps of 64 x 64 clocks), when there are enough tiles for
+    // the offset to pay for itself.
+    if (blockIdx.x >= gridDim.x / 2 && cnt >= 4 * (int)gridDim.x) {
+        __builtin_amdgcn_s_sleep(64);
+        __builtin_amdgcn_s_sleep(64);
+        __builtin_amdgcn_s_sleep(64);
+    }
     const int xcd = blockIdx.x & 7;
     const int lo = (int)((long long)cnt * xcd / 8), hi = (int)((long long)cnt * (xcd + 1) / 8);
     // The next tile's index is taken at the start of a tile and published in
@@ -453,41 +463,43 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int orow = lane & 31;
     const int ooff = orow * kChunk + ((((lane >> 5) ^ (((orow >> 2) ^ (orow >> 3)) & 1))) * 8);
     auto compute = [&](int st) {
-        u16x8_t ah[2], al[2];
+        // every operand read of the step goes out first, in the order the
+        // MFMAs use them, so the matrix cores wait for the first reads only;
+        // each accumulator takes lo.hi, hi.lo, then hi.hi (the small cross
+        // terms before the large one)
+        u16x8_t ah[2], al[2], bh[4], bl[4];
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++) {
-            const int o = (wm * 64 + sb * 32) * kChunk + ooff;
-            ah[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][0][o]);
-            al[sb] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.A[st][1][o]);
-        }
-        // target blocks in pairs: only two blocks' B fragments live at a time,
-        // four independent accumulators between dependent MFMAs; the small
-        // cross terms are added before hi.hi
+        for (int sb = 0; sb < 2; sb++)
+            al[sb] = *reinterpret_cast<const u16x8_t*>(
+                &sm.u.st.A[st][1][(wm * 64 + sb * 32) * kChunk + ooff]);
 #pragma unroll
-        for (int tp = 0; tp < 4; tp += 2) {
-            u16x8_t bh[2], bl[2];
+        for (int tb = 0; tb < 4; tb++)
+            bh[tb] = *reinterpret_cast<const u16x8_t*>(
+                &sm.u.st.B[st][0][(wn * 128 + tb * 32) * kChunk + ooff]);
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int o = (wn * 128 + (tp + u) * 32) * kChunk + ooff;
-                bh[u] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][0][o]);
-                bl[u] = *reinterpret_cast<const u16x8_t*>(&sm.u.st.B[st][1][o]);
-            }
+        for (int sb = 0; sb < 2; sb++)
+            ah[sb] = *reinterpret_cast<const u16x8_t*>(
+                &sm.u.st.A[st][0][(wm * 64 + sb * 32) * kChunk + ooff]);
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+        for (int tb = 0; tb < 4; tb++)
+            bl[tb] = *reinterpret_cast<const u16x8_t*>(
+                &sm.u.st.B[st][1][(wn * 128 + tb * 32) * kChunk + ooff]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int sb = 0; sb < 2; sb++)
-                    acc[sb][tp + u] = mfma_bf16(al[sb], bh[u], acc[sb][tp + u]);
+        for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+            for (int sb = 0; sb < 2; sb++)
+                acc[sb][tb] = mfma_bf16(al[sb], bh[tb], acc[sb][tb]);
 #pragma unroll
-                for (int sb = 0; sb < 2; sb++)
-                    acc[sb][tp + u] = mfma_bf16(ah[sb], bl[u], acc[sb][tp + u]);
+        for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+            for (int sb = 0; sb < 2; sb++)
+                acc[sb][tb] = mfma_bf16(ah[sb], bl[tb], acc[sb][tb]);
 #pragma unroll
-                for (int sb = 0; sb < 2; sb++)
-                    acc[sb][tp + u] = mfma_bf16(ah[sb], bh[u], acc[sb][tp + u]);
-        }
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+                acc[sb][tb] = mfma_bf16(ah[sb], bh[tb], acc[sb][tb]);
     };
 
     // Pipeline: at step k the loads of chunks k and k+1 are in flight; wait
