@@ -51,7 +51,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 # HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
 # (profiles/corr_window48_pmc_traffic.md)
-TRAFFIC_BYTES = 312169575
+TRAFFIC_BYTES = 311036804
 # HBM bytes of the glue's 48-row copy (gather of 48 distinct 128x3072-float
 # rows): the same passes over bench.py --glue (profiles/glue48_kernel_stats.md)
 GLUE_ROWS_TRAFFIC_BYTES = 151029965
@@ -62,7 +62,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=30,
+                    help="untimed steps first (the clock settles over the first few dozen)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the run, one device-to-device copy of MIB MiB (the plain "
@@ -651,7 +652,7 @@ def graph(args, slk, wl, H):
 def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
     """(active, total) 128-source x 256-target tiles of the batched correlation:
     a tile is active when some source's 8x8 window at some level has a cell in
-    its targets (the test k_tile_mask makes on the GPU, restated in numpy)."""
+    its targets (the test tile_mask_edge makes on the GPU, restated in numpy)."""
     B, HW = coords.shape[0], h * w
     hl = [h >> l for l in range(levels)]
     wl = [w >> l for l in range(levels)]
