@@ -416,7 +416,10 @@ void orc_frame_distance(const float* poses, const float* disps, const float* int
                 valid += (1 - beta);
             }
         }
-        dist[e] = (valid / (total + 1e-8) < 0.75) ? 1000.0f : (float)(accum / valid);
+        /* the final test and mean in fp32 as in se3.cuh:274-276: there 4.0f + 1e-8f
+           is 4.0f, so a coverage of exactly 0.75 passes (in fp64 it would not) */
+        const float vf = (float)valid, tf = (float)total;
+        dist[e] = (vf / (tf + 1e-8f) < 0.75f) ? 1000.0f : (float)accum / vf;
     }
 }
 

@@ -76,3 +76,38 @@ def test_frame_distance(slk):
     slk.hip().sync()
     ref = orc.frame_distance(p["poses"], p["disps"], p["intr"], ii, jj, 48, 64, 0.3)
     np.testing.assert_allclose(dist.to_host(), ref, rtol=TOL, atol=1e-5)
+
+
+@pytest.mark.parametrize("case", ["translation", "rotation", "coverage_0.8", "coverage_0.6",
+                                  "coverage_0.75"])
+def test_frame_distance_known_answers(slk, case):
+    """The hand-derived cases of the oracle's pins (test_oracle_se3_ba.py), on
+    the GPU: fx = fy = 10, cx = cy = 0, frame 0 at the identity."""
+    announce(f"frame_distance known answer {case}")
+    th = 0.1
+    cases = {
+        "translation": ([0.2, 0, 0, 0, 0, 0, 1], [0.5] * 6, 2, 1.0),
+        "rotation": ([0, 0, 0, 0.0, np.sin(th / 2), 0.0, np.cos(th / 2)], [0.7], 1,
+                     0.3 * 10.0 * np.tan(th)),
+        "coverage_0.8": ([0, 0, -0.5, 0, 0, 0, 1], [1, 1, 1, 1, 10], 1, 1.5),
+        "coverage_0.6": ([0, 0, -0.5, 0, 0, 0, 1], [1, 1, 1, 10, 10], 1, 1000.0),
+        "coverage_0.75": ([0, 0, -0.5, 0, 0, 0, 1], [1, 1, 1, 1.5], 1, 1.0),
+    }
+    pose_j, row, H, want = cases[case]
+    W = len(row) // H
+    poses = np.array([[0, 0, 0, 0, 0, 0, 1], pose_j], np.float32)
+    disps = np.zeros((2, H, W), np.float32)
+    disps[0] = np.asarray(row, np.float32).reshape(H, W)
+    intr = np.array([10.0, 10.0, 0.0, 0.0], np.float32)
+    pin = Pins(slk)
+    D = slk.DeviceArray.from_host
+    dp, dd, di = D(poses), D(disps), D(intr)
+    dist = slk.DeviceArray((1,))
+    slk.check(slk.lib().slk_frame_distance(dp.ptr, dd.ptr, di.ptr, pin(np.array([0], np.int32)),
+                                           pin(np.array([1], np.int32)), dist.ptr, 1, H, W, 0.3,
+                                           None))
+    slk.hip().sync()
+    got = float(dist.to_host()[0])
+    assert got == pytest.approx(want, rel=1e-5)
+    assert got == pytest.approx(float(orc.frame_distance(poses, disps, intr, [0], [1], H, W,
+                                                         0.3)[0]), rel=1e-5)

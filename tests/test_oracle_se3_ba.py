@@ -360,3 +360,65 @@ def test_cholesky_solve_and_not_spd():
     S[5, 5] = -1.0
     st, _ = orc.cholesky_solve(S, b)
     assert st == 3
+
+
+# ------------------------------------------- frame distance: known answers ---
+# Hand-derived values of frame_distance_kernel's rule (se3.cuh:209-277): per
+# pixel a beta-weighted full reprojection term and a (1 - beta)-weighted
+# translation-only term, each counted when its depth Z > 0.25; the mean over
+# the counted weights, or 1000 when they are under 0.75 of all the weights.
+# Intrinsics fx = fy = 10, cx = cy = 0, frame i at the identity, so that the
+# relative pose is frame j's own and every flow below is closed-form.
+_INTR = np.array([10.0, 10.0, 0.0, 0.0], np.float32)
+
+
+def _fd(pose_j, disp_row, beta, H=1):
+    poses = np.array([[0, 0, 0, 0, 0, 0, 1], pose_j], np.float32)
+    disps = np.zeros((2, H, len(disp_row) // H), np.float32)
+    disps[0] = np.asarray(disp_row, np.float32).reshape(H, -1)
+    return float(orc.frame_distance(poses, disps, _INTR, np.array([0]), np.array([1]), H,
+                                    len(disp_row) // H, beta)[0])
+
+
+def test_frame_distance_translation_is_beta_independent():
+    # tx = 0.2, disparity 0.5: every pixel moves by fx * d * tx = 1 px in both terms
+    for beta in (0.0, 0.3, 1.0):
+        assert _fd([0.2, 0, 0, 0, 0, 0, 1], [0.5] * 6, beta, H=2) == pytest.approx(1.0, rel=1e-6)
+
+
+def test_frame_distance_rotation_weights_the_full_term_by_beta():
+    # one pixel at the principal point, rotation by theta about y: the full term
+    # moves it by fx * tan(theta), the translation-only term not at all, so the
+    # distance is beta * fx * tan(theta) (a swapped mix would give (1 - beta) * ...)
+    th = 0.1
+    q = [0.0, np.sin(th / 2), 0.0, np.cos(th / 2)]
+    got = _fd([0, 0, 0] + q, [0.7], 0.3)
+    assert got == pytest.approx(0.3 * 10.0 * np.tan(th), rel=1e-5)
+    assert _fd([0, 0, 0] + q, [0.7], 1.0) == pytest.approx(10.0 * np.tan(th), rel=1e-5)
+    assert _fd([0, 0, 0] + q, [0.7], 0.0) == 0.0
+
+
+def test_frame_distance_depth_mask_and_coverage():
+    # tz = -0.5 along a row u = 0..W-1: Z = 1 - 0.5 d, and a counted pixel moves
+    # from u to u / Z, i.e. by u when d = 1 (Z = 0.5)
+    tz = [0, 0, -0.5, 0, 0, 0, 1]
+    # 4 of 5 counted (d = 10 gives Z = -4): coverage 0.8, mean flow (0+1+2+3)/4
+    assert _fd(tz, [1, 1, 1, 1, 10], 0.3) == pytest.approx(1.5, rel=1e-6)
+    # 3 of 5 counted: coverage 0.6 < 0.75
+    assert _fd(tz, [1, 1, 1, 10, 10], 0.3) == 1000.0
+    # d = 1.5 gives Z = 0.25 exactly, which is not counted (Z > 0.25 strictly);
+    # coverage 3/4 = 0.75 is enough (the test is < 0.75): mean (0+1+2)/3. A
+    # mask of Z >= 0.25 would count u = 3 (flow 3/0.25 - 3 = 9): mean 3.
+    assert _fd(tz, [1, 1, 1, 1.5], 0.3) == pytest.approx(1.0, rel=1e-6)
+
+
+def test_disp_retr_known_answers():
+    # fmaxf(d + dz, 0.001) per pixel of the listed frames (se3.cuh:195-206);
+    # fmaxf returns the number when the sum is NaN (IEEE maxNum), unlike np.maximum
+    d = np.array([[0.5, 0.5, 0.5, 0.5], [2.0, 2.0, 2.0, 2.0], [1.0, 1.0, 1.0, 1.0]],
+                 np.float32)
+    dz = np.array([[0.25, -0.75, -0.9995, np.nan], [-1.0, 0.5, 0.0, -2.0]], np.float32)
+    r = orc.disp_retr(d, dz, np.array([2, 0], np.int32))
+    np.testing.assert_array_equal(r[1], d[1])  # not listed
+    np.testing.assert_array_equal(r[2], np.float32([1.25, 0.25, 0.001, 0.001]))
+    np.testing.assert_array_equal(r[0], np.float32([0.001, 1.0, 0.5, 0.001]))
