@@ -613,6 +613,61 @@ def graph(args, slk, wl, H):
     flops = 80.0 * npairs * HW
     gflops = flops / (kern_ms * 1e-3) / 1e9
 
+    # edge-state update of a 48-edge frontend window (main.cu:1757-1796): the
+    # 8 oldest edges stored as inactive and the other 40 closed up, hidden
+    # states (128 x 48 x 64 floats), targets and weights moving with them;
+    # against the reference's pattern, one device copy per row and array
+    ne, eh, ew = 48, 48, 64
+    ehw = eh * ew
+    rng = np.random.default_rng(21)
+    e_age = rng.integers(0, 30, ne).astype(np.int32)
+    e_mask = np.zeros(ne, np.uint8)
+    L.slk_oldest_edges_mask(e_age.ctypes.data, ne, 8, e_mask.ctypes.data)
+    e_nets = slk.DeviceArray((ne, 128, ehw))
+    e_tg, e_wt = slk.DeviceArray((ne, 2, ehw)), slk.DeviceArray((ne, 2, ehw))
+    e_tin, e_win = slk.DeviceArray((64, 2, ehw)), slk.DeviceArray((64, 2, ehw))
+    ectx = slk.Context(eh, ew, C=128, max_batch=48)
+    e_ii = rng.integers(0, 12, ne).astype(np.int32)
+
+    def edge_state():
+        hii, hjj, hage = e_ii.copy(), e_ii.copy(), e_age.copy()
+        iin, jin = np.zeros(64, np.int32), np.zeros(64, np.int32)
+        ni, nk = ctypes.c_int(0), ctypes.c_int(0)
+        slk.check(L.slk_store_and_remove_edges(
+            ectx.ptr, e_mask.ctypes.data, ne, hii.ctypes.data, hjj.ctypes.data, hage.ctypes.data,
+            iin.ctypes.data, jin.ctypes.data, ctypes.byref(ni), 64, e_nets.ptr, 128 * ehw,
+            e_tg.ptr, e_wt.ptr, e_tin.ptr, e_win.ptr, 2 * ehw, ctypes.byref(nk), stream))
+        H.sync()
+
+    def edge_state_reference():
+        kept, ni = 0, 0
+        for e in range(ne):
+            if e_mask[e]:
+                for a, b in ((e_tin, e_tg), (e_win, e_wt)):
+                    H.dtod_async(a.ptr + ni * 8 * ehw, b.ptr + e * 8 * ehw, 8 * ehw, stream)
+                ni += 1
+            else:
+                if kept != e:
+                    H.dtod_async(e_nets.ptr + kept * 512 * ehw, e_nets.ptr + e * 512 * ehw,
+                                 512 * ehw, stream)
+                    for a in (e_tg, e_wt):
+                        H.dtod_async(a.ptr + kept * 8 * ehw, a.ptr + e * 8 * ehw, 8 * ehw,
+                                     stream)
+                kept += 1
+        H.sync()
+
+    edge_state()
+    edge_state_reference()
+    t0w = time.perf_counter()
+    for _ in range(k):
+        edge_state()
+    es_ms = (time.perf_counter() - t0w) * 1e3 / k
+    t0w = time.perf_counter()
+    for _ in range(k):
+        edge_state_reference()
+    es_ref_ms = (time.perf_counter() - t0w) * 1e3 / k
+    ectx.close()
+
     from oracle import oracle as orc
     orc.build()
     sample = 4000  # bounded CPU sample: the first 4000 pairs' distances
@@ -641,6 +696,9 @@ def graph(args, slk, wl, H):
                      "unit": "TFLOP/s", "frac": round(gflops / 1e3 / PEAK_FP32_TFLOPS, 4),
                      "traffic": None, "flop_per_pixel_pair": 80},
         "reference_pattern_ms": round(ref_ms, 3),
+        "edge_state_update": {"workload": "48 active edges, the 8 oldest stored as inactive, "
+                                          "40 closed up (hidden states 128x48x64)",
+                              "ms": round(es_ms, 3), "reference_pattern_ms": round(es_ref_ms, 3)},
         "cpu_baseline": {"value": round(cpu_dist_ms + cpu_sel_ms, 1), "unit": "ms per call",
                          "cores": orc.lib().orc_num_threads(), "kind": "port",
                          "sample": f"oracle distances of {sample} pairs scaled to {npairs}, "

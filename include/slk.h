@@ -319,6 +319,35 @@ int slk_proximity_factors(slk_ctx* ctx, const float* poses, const float* disps,
                           int* new_ii_host, int* new_jj_host, int capacity, int* n_new,
                           int* n_es, float* dists_host, hipStream_t stream);
 
+/* The edge-state update that follows the selection (main.cu:1757-1796).
+ * slk_oldest_edges_mask: mask_host[e] = 1 for the to_remove oldest active
+ * edges (largest age first; equal ages in edge order, where the reference's
+ * std::sort leaves them unspecified), the selection of add_proximity_factors'
+ * step 5 (main.cu:1758-1770). Host only. */
+void slk_oldest_edges_mask(const int* age_host, int n, int to_remove, unsigned char* mask_host);
+/* CudaDroid::store_and_remove_edges (main.cu:795-836): each masked edge,
+ * while the inactive list holds fewer than max_inac, is appended to it
+ * (ii_inac_host/jj_inac_host at *num_inac, its target and weight rows copied
+ * to target_inac/weight_inac); masked edges beyond that are dropped. Kept
+ * edges close up in order: ii_host/jj_host/age_host (age may be NULL) are
+ * compacted in place, and so are their rows of edge_nets (net_row floats,
+ * 128*h*w in the reference), target and weight (tw_row floats, 2*h*w).
+ * *num_inac and *n_kept are updated. The reference issues a cudaMemcpy per
+ * row; here each array's rows move in one gather and one scatter launch
+ * through a staging buffer (a destination row can be the source of an
+ * earlier move). */
+int slk_store_and_remove_edges(slk_ctx* ctx, const unsigned char* mask_host, int n,
+                               int* ii_host, int* jj_host, int* age_host, int* ii_inac_host,
+                               int* jj_inac_host, int* num_inac, int max_inac, float* edge_nets,
+                               long net_row, float* target, float* weight, float* target_inac,
+                               float* weight_inac, long tw_row, int* n_kept,
+                               hipStream_t stream);
+/* Hidden states of newly added edges (main.cu:1786-1796): edge_nets row e =
+ * nets row ii_host[e] and weight row e = 0 for e in [first, first + count). */
+int slk_init_new_edges(slk_ctx* ctx, const float* nets, float* edge_nets, float* weight,
+                       const int* ii_host, int first, int count, long net_row, long tw_row,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

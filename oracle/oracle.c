@@ -957,3 +957,71 @@ int orc_proximity_select(const float* dr, int t, int t0, int t1, int rad, int nm
     free(d); free(ei); free(ej); free(order);
     return ne;
 }
+
+/* ------------------------------------------------------------------------ */
+/* factor-graph edge state (main.cu:795-836, 1757-1796)                      */
+/* ------------------------------------------------------------------------ */
+
+void orc_oldest_mask(const int* age, int n, int to_remove, unsigned char* mask) {
+    /* main.cu:1762-1769: indices sorted by age, largest first, the first
+       to_remove masked; equal ages keep edge order (a stable insertion sort,
+       where the reference's std::sort leaves their order unspecified) */
+    int* order = (int*)malloc(sizeof(int) * (n > 0 ? n : 1));
+    for (int e = 0; e < n; e++) {
+        int k = e;
+        while (k > 0 && age[order[k - 1]] < age[e]) {
+            order[k] = order[k - 1];
+            k--;
+        }
+        order[k] = e;
+    }
+    for (int e = 0; e < n; e++) mask[e] = 0;
+    for (int r = 0; r < to_remove && r < n; r++) mask[order[r]] = 1;
+    free(order);
+}
+
+int orc_store_and_remove_edges(const unsigned char* mask, int n, int* ii, int* jj, int* age,
+                               int* ii_inac, int* jj_inac, int* num_inac, int max_inac,
+                               float* nets, long net_row, float* target, float* weight,
+                               float* target_inac, float* weight_inac, long tw_row) {
+    /* main.cu:795-836, one edge at a time with one row copy per array, as
+       the reference's cudaMemcpy calls; returns the number of edges kept */
+    int kept = 0;
+    for (int e = 0; e < n; e++) {
+        if (mask[e]) {
+            if (*num_inac < max_inac) {
+                memcpy(target_inac + (size_t)*num_inac * tw_row, target + (size_t)e * tw_row,
+                       sizeof(float) * tw_row);
+                memcpy(weight_inac + (size_t)*num_inac * tw_row, weight + (size_t)e * tw_row,
+                       sizeof(float) * tw_row);
+                ii_inac[*num_inac] = ii[e];
+                jj_inac[*num_inac] = jj[e];
+                (*num_inac)++;
+            }
+        } else {
+            if (kept != e) {
+                memcpy(nets + (size_t)kept * net_row, nets + (size_t)e * net_row,
+                       sizeof(float) * net_row);
+                memcpy(target + (size_t)kept * tw_row, target + (size_t)e * tw_row,
+                       sizeof(float) * tw_row);
+                memcpy(weight + (size_t)kept * tw_row, weight + (size_t)e * tw_row,
+                       sizeof(float) * tw_row);
+            }
+            ii[kept] = ii[e];
+            jj[kept] = jj[e];
+            age[kept] = age[e];
+            kept++;
+        }
+    }
+    return kept;
+}
+
+void orc_init_new_edges(const float* nets, float* edge_nets, float* weight, const int* ii,
+                        int first, int count, long net_row, long tw_row) {
+    /* main.cu:1786-1796: edge_nets[e] = nets[ii[e]], weight[e] = 0 */
+    for (int e = first; e < first + count; e++) {
+        memcpy(edge_nets + (size_t)e * net_row, nets + (size_t)ii[e] * net_row,
+               sizeof(float) * net_row);
+        memset(weight + (size_t)e * tw_row, 0, sizeof(float) * tw_row);
+    }
+}

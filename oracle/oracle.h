@@ -169,6 +169,16 @@ int orc_proximity_select(const float* d, int t, int t0, int t1, int rad, int nms
                          const int* ii_inac, const int* jj_inac, int n_inac,
                          int max_factors, int* new_ii, int* new_jj, int cap, int* n_new);
 
+/* factor-graph edge state: step 5's age selection, store_and_remove_edges
+   and the new edges' hidden states (main.cu:795-836, 1757-1796) */
+void orc_oldest_mask(const int* age, int n, int to_remove, unsigned char* mask);
+int orc_store_and_remove_edges(const unsigned char* mask, int n, int* ii, int* jj, int* age,
+                               int* ii_inac, int* jj_inac, int* num_inac, int max_inac,
+                               float* nets, long net_row, float* target, float* weight,
+                               float* target_inac, float* weight_inac, long tw_row);
+void orc_init_new_edges(const float* nets, float* edge_nets, float* weight, const int* ii,
+                        int first, int count, long net_row, long tw_row);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,7 @@ _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 
 
 def build(force: bool = False) -> str:
@@ -89,6 +90,12 @@ def lib():
             "orc_ba_edge_set": ([_i32p, _i32p, c_int, _i32p, _i32p, c_int, _f32p, _f32p,
                                  _f32p, _f32p, c_int, c_int, c_int, c_int, _i32p, _i32p,
                                  _f32p, _f32p, ctypes.POINTER(c_int)], c_int),
+            "orc_oldest_mask": ([_i32p, c_int, c_int, _u8p], None),
+            "orc_store_and_remove_edges": ([_u8p, c_int, _i32p, _i32p, _i32p, _i32p, _i32p,
+                                            ctypes.POINTER(c_int), c_int, _f32p, c_long, _f32p,
+                                            _f32p, _f32p, _f32p, c_long], c_int),
+            "orc_init_new_edges": ([_f32p, _f32p, _f32p, _i32p, c_int, c_int, c_long, c_long],
+                                   None),
         }
         for name, (argtypes, restype) in glue.items():
             fn = getattr(L, name)
@@ -395,3 +402,58 @@ def proximity_select(d, t, t0, t1, rad, nms, thresh, ii, jj, ii_inac=(), jj_inac
                                     len(ii_inac), int(max_factors), ni, nj, cap,
                                     ctypes.byref(m))
     return np.stack([ni[:m.value], nj[:m.value]], 1), ne
+
+
+def oldest_mask(age, to_remove):
+    """Step 5 of add_proximity_factors (main.cu:1762-1769): uint8 mask of the
+    to_remove oldest edges, equal ages in edge order."""
+    age = _c(age, np.int32)
+    mask = np.zeros(max(len(age), 1), np.uint8)
+    lib().orc_oldest_mask(age, len(age), int(to_remove), mask)
+    return mask[:len(age)]
+
+
+def store_and_remove_edges(mask, ii, jj, age, ii_inac, jj_inac, max_inac, nets, target,
+                           weight, target_inac, weight_inac):
+    """store_and_remove_edges (main.cu:795-836) on copies: dict with the kept
+    ii, jj, age, nets, target, weight (their first n_kept rows), the grown
+    inactive ii, jj, target, weight, and n_kept / num_inac."""
+    mask = np.ascontiguousarray(mask, np.uint8)
+    ii, jj, age = (np.array(a, np.int32) for a in (ii, jj, age))
+    n = len(ii)
+    ni = ctypes.c_int(len(ii_inac))
+    cap = max(max_inac, 1)
+    iin = np.zeros(cap, np.int32)
+    jin = np.zeros(cap, np.int32)
+    iin[:len(ii_inac)] = ii_inac
+    jin[:len(jj_inac)] = jj_inac
+    nets, target, weight = (np.array(a, np.float32) for a in (nets, target, weight))
+    net_row = nets[0].size if n else 0
+    tw_row = target[0].size if n else 0
+    tin = np.zeros((cap, tw_row), np.float32)
+    win = np.zeros((cap, tw_row), np.float32)
+    if len(target_inac):
+        tin[:len(target_inac)] = np.asarray(target_inac, np.float32).reshape(len(target_inac),
+                                                                             tw_row)
+        win[:len(weight_inac)] = np.asarray(weight_inac, np.float32).reshape(len(weight_inac),
+                                                                             tw_row)
+    kept = lib().orc_store_and_remove_edges(mask, n, ii, jj, age, iin, jin, ctypes.byref(ni),
+                                            int(max_inac), nets.reshape(-1), net_row,
+                                            target.reshape(-1), weight.reshape(-1),
+                                            tin.reshape(-1), win.reshape(-1), tw_row)
+    m = ni.value
+    return {"n_kept": kept, "ii": ii[:kept], "jj": jj[:kept], "age": age[:kept],
+            "nets": nets[:kept], "target": target[:kept], "weight": weight[:kept],
+            "num_inac": m, "ii_inac": iin[:m], "jj_inac": jin[:m],
+            "target_inac": tin[:m].reshape((m,) + np.shape(target)[1:]),
+            "weight_inac": win[:m].reshape((m,) + np.shape(weight)[1:])}
+
+
+def init_new_edges(nets, edge_nets, weight, ii, first, count):
+    """Hidden states of new edges (main.cu:1786-1796) on copies: (edge_nets,
+    weight) with rows [first, first + count) set."""
+    nets = _c(nets, np.float32)
+    en, w = np.array(edge_nets, np.float32), np.array(weight, np.float32)
+    lib().orc_init_new_edges(nets.reshape(-1), en.reshape(-1), w.reshape(-1), _c(ii, np.int32),
+                             int(first), int(count), en[0].size, w[0].size)
+    return en, w

@@ -174,6 +174,7 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     ctx->zero_idx.release();
     ctx->glue_stage.release();
     ctx->glue_idx.release();
+    ctx->edge_stage.release();
     ctx->graph_pairs.release();
     ctx->graph_dist.release();
     delete ctx;

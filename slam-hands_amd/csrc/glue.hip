@@ -417,3 +417,153 @@ extern "C" int slk_ba_edge_set(slk_ctx* ctx, const int* ii_host, const int* jj_h
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
+
+// --------------------------------------------- edge state of the factor graph
+namespace slk {
+namespace {
+// dst rows [0, n) = 0
+template <int kV>
+__global__ __launch_bounds__(256) void k_zero_rows(float* __restrict__ dst, long row) {
+    using V = typename std::conditional<kV == 4, float4, float>::type;
+    V* d = reinterpret_cast<V*>(dst + (long)blockIdx.y * row);
+    V z;
+    if constexpr (kV == 4)
+        z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    else
+        z = 0.0f;
+    const long nv = row / kV;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < nv;
+         i += (long)gridDim.x * blockDim.x)
+        d[i] = z;
+}
+
+// Moves rows src[e_k] -> dst[d_k] of one array in place (d_k < e_k, both
+// increasing) through the context's staging buffer: a row that is the
+// destination of one move can be the source of an earlier one, so all
+// sources are read before any destination is written.
+int move_rows(slk_ctx* ctx, float* base, long row, const int* d_src, const int* d_dst, int k,
+              hipStream_t stream) {
+    if (k == 0 || row == 0) return SLK_OK;
+    const size_t bytes = (size_t)k * row * sizeof(float);
+    if (bytes > ctx->edge_stage.bytes && ctx->edge_stage.ptr)
+        SLK_HIP(hipDeviceSynchronize());  // earlier moves may still use the old buffer
+    SLK_TRY(ctx->edge_stage.ensure(bytes));
+    float* stage = ctx->edge_stage.as<float>();
+    SLK_TRY(rows_launch(stage, base, d_src, k, row, 0, stream, "store_and_remove_edges"));
+    SLK_TRY(rows_launch(base, stage, d_dst, k, row, 1, stream, "store_and_remove_edges"));
+    return SLK_OK;
+}
+}  // namespace
+}  // namespace slk
+
+extern "C" void slk_oldest_edges_mask(const int* age_host, int n, int to_remove,
+                                      unsigned char* mask_host) {
+    if (!mask_host || n <= 0) return;
+    std::fill(mask_host, mask_host + n, (unsigned char)0);
+    if (!age_host || to_remove <= 0) return;
+    std::vector<int> order(n);
+    for (int e = 0; e < n; e++) order[e] = e;
+    // oldest first; equal ages in edge order (std::sort leaves them unspecified)
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return age_host[a] > age_host[b]; });
+    for (int r = 0; r < std::min(to_remove, n); r++) mask_host[order[r]] = 1;
+}
+
+extern "C" int slk_store_and_remove_edges(slk_ctx* ctx, const unsigned char* mask_host, int n,
+                                          int* ii_host, int* jj_host, int* age_host,
+                                          int* ii_inac_host, int* jj_inac_host, int* num_inac,
+                                          int max_inac, float* edge_nets, long net_row,
+                                          float* target, float* weight, float* target_inac,
+                                          float* weight_inac, long tw_row, int* n_kept,
+                                          hipStream_t stream) {
+    if (!ctx || !n_kept || !num_inac) return fail(SLK_E_ARG, "store_and_remove_edges: null argument");
+    if (n < 0 || *num_inac < 0 || max_inac < 0 || net_row < 0 || tw_row < 0)
+        return fail(SLK_E_ARG, "store_and_remove_edges: bad sizes");
+    *n_kept = n;
+    if (n == 0) return SLK_OK;
+    if (!mask_host || !ii_host || !jj_host)
+        return fail(SLK_E_ARG, "store_and_remove_edges: null edge lists");
+    // the reference's loop (main.cu:795-836): masked edges go to the inactive
+    // list while it has room (beyond it they are dropped), kept edges close up
+    // in order; rows move with their edges
+    std::vector<int> stored, src, dst;
+    int kept = 0, ni = *num_inac;
+    for (int e = 0; e < n; e++) {
+        if (mask_host[e]) {
+            if (ni < max_inac) {
+                if (!ii_inac_host || !jj_inac_host)
+                    return fail(SLK_E_ARG, "store_and_remove_edges: null inactive lists");
+                ii_inac_host[ni] = ii_host[e];
+                jj_inac_host[ni] = jj_host[e];
+                stored.push_back(e);
+                ni++;
+            }
+        } else {
+            if (kept != e) {
+                src.push_back(e);
+                dst.push_back(kept);
+                ii_host[kept] = ii_host[e];
+                jj_host[kept] = jj_host[e];
+                if (age_host) age_host[kept] = age_host[e];
+            }
+            kept++;
+        }
+    }
+    const int s = (int)stored.size(), k = (int)src.size();
+    if (s > 0 && (!target || !weight || !target_inac || !weight_inac) && tw_row > 0)
+        return fail(SLK_E_ARG, "store_and_remove_edges: null target/weight rows");
+    if (k > 0 && ((net_row > 0 && !edge_nets) || (tw_row > 0 && (!target || !weight))))
+        return fail(SLK_E_ARG, "store_and_remove_edges: null edge rows");
+    if (s > 65535 || k > 65535) return fail(SLK_E_ARG, "store_and_remove_edges: too many rows");
+    const int first_inac = *num_inac;
+    *num_inac = ni;
+    *n_kept = kept;
+    if (s + k == 0) return SLK_OK;
+    // one upload: [stored][src][dst]
+    std::vector<int> buf((size_t)s + 2 * k);
+    std::copy(stored.begin(), stored.end(), buf.begin());
+    std::copy(src.begin(), src.end(), buf.begin() + s);
+    std::copy(dst.begin(), dst.end(), buf.begin() + s + k);
+    SLK_TRY(upload(ctx, buf.data(), buf.size() * sizeof(int), stream));
+    const int* d = ctx->glue_idx.as<int>();
+    // the stored rows are read before the moves overwrite them (stream order)
+    if (s > 0 && tw_row > 0) {
+        SLK_TRY(rows_launch(target_inac + (long)first_inac * tw_row, target, d, s, tw_row, 0,
+                            stream, "store_and_remove_edges"));
+        SLK_TRY(rows_launch(weight_inac + (long)first_inac * tw_row, weight, d, s, tw_row, 0,
+                            stream, "store_and_remove_edges"));
+    }
+    if (k > 0) {
+        SLK_TRY(move_rows(ctx, edge_nets, net_row, d + s, d + s + k, k, stream));
+        SLK_TRY(move_rows(ctx, target, tw_row, d + s, d + s + k, k, stream));
+        SLK_TRY(move_rows(ctx, weight, tw_row, d + s, d + s + k, k, stream));
+    }
+    return SLK_OK;
+}
+
+extern "C" int slk_init_new_edges(slk_ctx* ctx, const float* nets, float* edge_nets,
+                                  float* weight, const int* ii_host, int first, int count,
+                                  long net_row, long tw_row, hipStream_t stream) {
+    if (count <= 0) return SLK_OK;
+    if (!ctx || !ii_host || first < 0 || net_row < 0 || tw_row < 0)
+        return fail(SLK_E_ARG, "init_new_edges: bad argument");
+    if (count > 65535) return fail(SLK_E_ARG, "init_new_edges: more than 65535 edges");
+    if (net_row > 0) {
+        if (!nets || !edge_nets) return fail(SLK_E_ARG, "init_new_edges: null hidden states");
+        SLK_TRY(upload(ctx, ii_host + first, (size_t)count * sizeof(int), stream));
+        SLK_TRY(rows_launch(edge_nets + (long)first * net_row, nets, ctx->glue_idx.as<int>(),
+                            count, net_row, 0, stream, "init_new_edges"));
+    }
+    if (tw_row > 0) {
+        if (!weight) return fail(SLK_E_ARG, "init_new_edges: null weight");
+        float* w0 = weight + (long)first * tw_row;
+        if (tw_row % 4 == 0 && al16(w0))
+            hipLaunchKernelGGL(k_zero_rows<4>, row_grid(tw_row / 4, count), dim3(256), 0, stream,
+                               w0, tw_row);
+        else
+            hipLaunchKernelGGL(k_zero_rows<1>, row_grid(tw_row, count), dim3(256), 0, stream,
+                               w0, tw_row);
+        SLK_HIP(hipGetLastError());
+    }
+    return SLK_OK;
+}

@@ -89,6 +89,7 @@ struct slk_ctx {
     // update-pass glue: index lists uploaded through a pinned stage
     slk::HostStage glue_stage;
     slk::DevBuf glue_idx;
+    slk::DevBuf edge_stage;  // rows in transit of slk_store_and_remove_edges
     // proximity factors: the pair lists and their frame distances
     slk::DevBuf graph_pairs, graph_dist;
     slk::BaState* ba = nullptr;

@@ -38,6 +38,7 @@ EXPORTS = [
     "slk_ba_depth_update",
     "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
     "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set", "slk_proximity_factors",
+    "slk_oldest_edges_mask", "slk_store_and_remove_edges", "slk_init_new_edges",
 ]
 
 
@@ -112,11 +113,16 @@ def lib():
                                 P, ctypes.POINTER(I), ctypes.POINTER(I), P],
             "slk_proximity_factors": [P, P, P, P, I, I, I, I, I, F, F, P, P, I, P, P, I, I, P,
                                       P, I, ctypes.POINTER(I), ctypes.POINTER(I), P, P],
+            "slk_store_and_remove_edges": [P, P, I, P, P, P, P, P, ctypes.POINTER(I), I, P, L,
+                                           P, P, P, P, L, ctypes.POINTER(I), P],
+            "slk_init_new_edges": [P, P, P, P, P, I, I, L, L, P],
         }
         for name, args in sig.items():
             fn = getattr(L_, name)
             fn.argtypes = args
             fn.restype = I
+        L_.slk_oldest_edges_mask.argtypes = [P, I, I, P]
+        L_.slk_oldest_edges_mask.restype = None
         L_.slk_last_error.argtypes = []
         L_.slk_last_error.restype = ctypes.c_char_p
         _lib = L_

@@ -64,3 +64,19 @@ def test_workloads_are_deterministic():
     p = wl.ba_problem()
     assert p["target"].shape == (48, 2, 48 * 64) and p["t0"] == 2 and p["t1"] == 12
     np.testing.assert_array_equal(p["poses"][:2], [[0, 0, 0, 0, 0, 0, 1]] * 2)
+
+
+def test_oldest_edges_mask_host_helper_matches_oracle():
+    """slk_oldest_edges_mask runs on the host only: compared with the oracle's
+    step-5 selection (main.cu:1762-1769) on random ages with many ties."""
+    import ctypes
+    import numpy as np
+    from oracle import oracle as orc
+    orc.build()
+    rng = np.random.default_rng(5)
+    for n, k in [(1, 1), (7, 3), (48, 10), (64, 70), (30, 0)]:
+        age = rng.integers(0, 6, n).astype(np.int32)
+        got = np.zeros(n, np.uint8)
+        slk.lib().slk_oldest_edges_mask(age.ctypes.data_as(ctypes.c_void_p), n, k,
+                                        got.ctypes.data_as(ctypes.c_void_p))
+        np.testing.assert_array_equal(got, orc.oldest_mask(age, k))

@@ -78,3 +78,88 @@ def test_proximity_factors(slk, case):
     got = np.stack([new_i[:n_new.value], new_j[:n_new.value]], 1)
     np.testing.assert_array_equal(got, ref_new)
     assert np.sum(dist[(pi - pj) > rad + 1] <= thresh) > 0  # the greedy step had candidates
+
+
+# ------------------------------------------- edge-state update (main.cu:795-836)
+EDGE_CASES = [  # (name, n, removed, inactive already held, max_inac)
+    ("age_removal", 48, [3, 17, 18, 40], 5, 64),
+    ("first_edge_chain", 48, [0], 0, 64),
+    ("inactive_full", 32, [1, 2, 9, 30, 31], 62, 64),  # room for two; three dropped
+    ("nothing_masked", 16, [], 3, 64),
+]
+
+
+@pytest.mark.parametrize("case", EDGE_CASES, ids=[c[0] for c in EDGE_CASES])
+def test_store_and_remove_edges_matches_oracle(slk, case):
+    name, n, removed, n_in, max_inac = case
+    h, w = 48, 64
+    hw = h * w
+    announce(f"store_and_remove_edges {name}: n={n} removed={removed} inac={n_in}/{max_inac}")
+    rng = np.random.default_rng(11)
+    ii = rng.integers(0, 20, n).astype(np.int32)
+    jj = rng.integers(0, 20, n).astype(np.int32)
+    age = rng.integers(0, 30, n).astype(np.int32)
+    nets = rng.normal(size=(n, 128, hw)).astype(np.float32)
+    tg = rng.normal(size=(n, 2, hw)).astype(np.float32)
+    wt = rng.uniform(size=(n, 2, hw)).astype(np.float32)
+    tin = np.zeros((max_inac, 2, hw), np.float32)
+    win = np.zeros((max_inac, 2, hw), np.float32)
+    tin[:n_in] = rng.normal(size=(n_in, 2, hw))
+    win[:n_in] = rng.uniform(size=(n_in, 2, hw))
+    iin = np.zeros(max_inac, np.int32)
+    jin = np.zeros(max_inac, np.int32)
+    iin[:n_in] = rng.integers(0, 20, n_in)
+    jin[:n_in] = rng.integers(0, 20, n_in)
+    mask = np.zeros(n, np.uint8)
+    mask[removed] = 1
+    ref = orc.store_and_remove_edges(mask, ii, jj, age, iin[:n_in], jin[:n_in], max_inac, nets,
+                                     tg, wt, tin[:n_in], win[:n_in])
+    D = slk.DeviceArray.from_host
+    dn, dt, dw, dti, dwi = D(nets), D(tg), D(wt), D(tin), D(win)
+    hii, hjj, hage, hiin, hjin = ii.copy(), jj.copy(), age.copy(), iin.copy(), jin.copy()
+    num_inac, n_kept = ctypes.c_int(n_in), ctypes.c_int(-1)
+    ctx = slk.Context(h, w, C=128, max_batch=48)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    slk.check(slk.lib().slk_store_and_remove_edges(
+        ctx.ptr, P(mask), n, P(hii), P(hjj), P(hage), P(hiin), P(hjin), ctypes.byref(num_inac),
+        max_inac, dn.ptr, 128 * hw, dt.ptr, dw.ptr, dti.ptr, dwi.ptr, 2 * hw,
+        ctypes.byref(n_kept), None))
+    slk.hip().sync()
+    k, m = n_kept.value, num_inac.value
+    assert (k, m) == (ref["n_kept"], ref["num_inac"])
+    np.testing.assert_array_equal(hii[:k], ref["ii"])
+    np.testing.assert_array_equal(hjj[:k], ref["jj"])
+    np.testing.assert_array_equal(hage[:k], ref["age"])
+    np.testing.assert_array_equal(hiin[:m], ref["ii_inac"])
+    np.testing.assert_array_equal(hjin[:m], ref["jj_inac"])
+    # rows are copies: bitwise
+    np.testing.assert_array_equal(dn.to_host()[:k], ref["nets"])
+    np.testing.assert_array_equal(dt.to_host()[:k], ref["target"])
+    np.testing.assert_array_equal(dw.to_host()[:k], ref["weight"])
+    np.testing.assert_array_equal(dti.to_host()[:m], ref["target_inac"])
+    np.testing.assert_array_equal(dwi.to_host()[:m], ref["weight_inac"])
+    # rows past the kept ones and past the inactive ones are left as they were
+    np.testing.assert_array_equal(dti.to_host()[m:], tin[m:])
+    ctx.close()
+
+
+def test_init_new_edges_matches_oracle(slk):
+    h, w = 48, 64
+    hw = h * w
+    announce("init_new_edges: 40 edges, 8 new")
+    rng = np.random.default_rng(12)
+    nets = rng.normal(size=(12, 128, hw)).astype(np.float32)
+    en = rng.normal(size=(40, 128, hw)).astype(np.float32)
+    wt = rng.uniform(size=(40, 2, hw)).astype(np.float32)
+    ii = rng.integers(0, 12, 40).astype(np.int32)
+    ref_en, ref_w = orc.init_new_edges(nets, en, wt, ii, 32, 8)
+    D = slk.DeviceArray.from_host
+    dn, de, dw = D(nets), D(en), D(wt)
+    ctx = slk.Context(h, w, C=128, max_batch=48)
+    slk.check(slk.lib().slk_init_new_edges(ctx.ptr, dn.ptr, de.ptr, dw.ptr,
+                                           ii.ctypes.data_as(ctypes.c_void_p), 32, 8, 128 * hw,
+                                           2 * hw, None))
+    slk.hip().sync()
+    np.testing.assert_array_equal(de.to_host(), ref_en)
+    np.testing.assert_array_equal(dw.to_host(), ref_w)
+    ctx.close()

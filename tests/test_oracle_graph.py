@@ -78,3 +78,69 @@ def test_invariants_on_random_windows():
         for i, j in picked:
             k = (i - t0) * (t - t1) + (j - t1)
             assert t0 <= i < t and t1 <= j < t and d[k] <= 16.0
+
+
+# ----------------------------------------------------- edge-state update ---
+def _coded_rows(n, shape, base):
+    # row e holds base + 100 e + (element index): shows which row went where
+    k = int(np.prod(shape))
+    return (base + 100.0 * np.arange(n)[:, None] + np.arange(k)[None, :]).reshape(
+        (n,) + shape).astype(np.float32)
+
+
+def test_oldest_mask_hand_worked():
+    # ages 5 at edges 1, 2, 4: the two oldest are 1 and 2 (edge order among equals)
+    np.testing.assert_array_equal(orc.oldest_mask([3, 5, 5, 1, 5, 0], 2), [0, 1, 1, 0, 0, 0])
+    np.testing.assert_array_equal(orc.oldest_mask([3, 5, 5, 1, 5, 0], 4), [1, 1, 1, 0, 1, 0])
+    np.testing.assert_array_equal(orc.oldest_mask([2, 7], 9), [1, 1])
+    np.testing.assert_array_equal(orc.oldest_mask([2, 7], 0), [0, 0])
+
+
+def test_store_and_remove_edges_hand_worked():
+    # 6 edges, mask 1, 3, 4; the inactive list holds one edge and has room for
+    # two more: 1 and 3 are stored, 4 is dropped; 0, 2, 5 close up in order
+    ii, jj = [10, 11, 12, 13, 14, 15], [20, 21, 22, 23, 24, 25]
+    age = [0, 1, 2, 3, 4, 5]
+    nets, tg, wt = (_coded_rows(6, (3, 4), b) for b in (0.0, 1000.0, 2000.0))
+    tin, win = _coded_rows(1, (2, 2), 5000.0), _coded_rows(1, (2, 2), 6000.0)
+    tg, wt = tg[:, :2, :2].copy(), wt[:, :2, :2].copy()
+    r = orc.store_and_remove_edges([0, 1, 0, 1, 1, 0], ii, jj, age, [7], [8], 3, nets, tg, wt,
+                                   tin, win)
+    assert r["n_kept"] == 3 and r["num_inac"] == 3
+    np.testing.assert_array_equal(r["ii"], [10, 12, 15])
+    np.testing.assert_array_equal(r["jj"], [20, 22, 25])
+    np.testing.assert_array_equal(r["age"], [0, 2, 5])
+    np.testing.assert_array_equal(r["nets"], nets[[0, 2, 5]])
+    np.testing.assert_array_equal(r["target"], tg[[0, 2, 5]])
+    np.testing.assert_array_equal(r["weight"], wt[[0, 2, 5]])
+    np.testing.assert_array_equal(r["ii_inac"], [7, 11, 13])
+    np.testing.assert_array_equal(r["jj_inac"], [8, 21, 23])
+    np.testing.assert_array_equal(r["target_inac"], np.concatenate([tin, tg[[1, 3]]]))
+    np.testing.assert_array_equal(r["weight_inac"], np.concatenate([win, wt[[1, 3]]]))
+
+
+def test_store_and_remove_edges_chain_of_moves():
+    # removing edge 0 shifts every other edge down by one: each destination row
+    # is the source of the move before it
+    nets = _coded_rows(5, (2, 3), 0.0)
+    tw = _coded_rows(5, (2, 3), 500.0)
+    r = orc.store_and_remove_edges([1, 0, 0, 0, 0], range(5), range(5), range(5), [], [], 0,
+                                   nets, tw, tw + 1, np.zeros((0, 2, 3)), np.zeros((0, 2, 3)))
+    assert r["n_kept"] == 4 and r["num_inac"] == 0  # no room: edge 0 is dropped
+    np.testing.assert_array_equal(r["nets"], nets[1:])
+    np.testing.assert_array_equal(r["target"], tw[1:])
+    np.testing.assert_array_equal(r["weight"], tw[1:] + 1)
+    np.testing.assert_array_equal(r["ii"], [1, 2, 3, 4])
+
+
+def test_init_new_edges_hand_worked():
+    nets = _coded_rows(4, (2, 3), 0.0)
+    en = _coded_rows(5, (2, 3), 9000.0)
+    w = _coded_rows(5, (2, 3), 7000.0)
+    ii = [1, 2, 3, 0, 2]
+    en2, w2 = orc.init_new_edges(nets, en, w, ii, 3, 2)
+    np.testing.assert_array_equal(en2[:3], en[:3])      # untouched
+    np.testing.assert_array_equal(en2[3], nets[0])      # ii[3] = 0
+    np.testing.assert_array_equal(en2[4], nets[2])      # ii[4] = 2
+    np.testing.assert_array_equal(w2[:3], w[:3])
+    np.testing.assert_array_equal(w2[3:], 0.0)
