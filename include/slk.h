@@ -347,6 +347,22 @@ int slk_store_and_remove_edges(slk_ctx* ctx, const unsigned char* mask_host, int
 int slk_init_new_edges(slk_ctx* ctx, const float* nets, float* edge_nets, float* weight,
                        const int* ii_host, int first, int count, long net_row, long tw_row,
                        hipStream_t stream);
+/* CudaDroid::rm_keyframe(ix) (main.cu:866-941), for 0 <= ix < num_keyframes
+ * (otherwise nothing changes): keyframe rows ix+1 .. t-1 of poses (7 floats),
+ * disps (h*w), fmaps (C*h*w of fmap_dtype), nets and inps (net_row floats)
+ * move down by one; active edges touching ix are removed, indices above ix
+ * drop by one, and the others close up in order (ii/jj/age host lists in
+ * place, *n_kept) with their rows of edge_nets (net_row), target and weight
+ * (2*h*w); the inactive edges likewise (*n_inac_kept) with target_inac and
+ * weight_inac. A null array pointer skips that array. Every array's rows move
+ * in one gather and one scatter launch in place of the reference's per-row
+ * copies; the caller drops its own timestamp and decrements num_keyframes. */
+int slk_rm_keyframe(slk_ctx* ctx, int ix, int num_keyframes, float* poses, float* disps,
+                    void* fmaps, int fmap_dtype, float* nets, float* inps, long net_row,
+                    int* ii_host, int* jj_host, int* age_host, int n, int* n_kept,
+                    int* ii_inac_host, int* jj_inac_host, int n_inac, int* n_inac_kept,
+                    float* edge_nets, float* target, float* weight, float* target_inac,
+                    float* weight_inac, hipStream_t stream);
 
 #ifdef __cplusplus
 }

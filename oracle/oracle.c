@@ -1025,3 +1025,51 @@ void orc_init_new_edges(const float* nets, float* edge_nets, float* weight, cons
         memset(weight + (size_t)e * tw_row, 0, sizeof(float) * tw_row);
     }
 }
+
+static int rm_kf_edges(int ix, int* ii, int* jj, int* age, int n, float* r1, float* r2,
+                       float* r3, long row1, long row23) {
+    /* main.cu:889-917 / 920-940: edges touching ix go, indices above ix drop
+       by one, the others close up with one copy per row and array */
+    int kept = 0;
+    for (int e = 0; e < n; e++) {
+        int ei = ii[e], ej = jj[e];
+        if (ei == ix || ej == ix) continue;
+        if (ei > ix) ei--;
+        if (ej > ix) ej--;
+        if (kept != e) {
+            if (r1) memcpy(r1 + (size_t)kept * row1, r1 + (size_t)e * row1, sizeof(float) * row1);
+            if (r2) memcpy(r2 + (size_t)kept * row23, r2 + (size_t)e * row23, sizeof(float) * row23);
+            if (r3) memcpy(r3 + (size_t)kept * row23, r3 + (size_t)e * row23, sizeof(float) * row23);
+        }
+        ii[kept] = ei;
+        jj[kept] = ej;
+        if (age) age[kept] = age[e];
+        kept++;
+    }
+    return kept;
+}
+
+void orc_rm_keyframe(int ix, int t, float* poses, float* disps, float* fmaps, long fmap_row,
+                     float* nets, float* inps, long net_row, long hw, int* ii, int* jj,
+                     int* age, int n, int* n_kept, int* ii_inac, int* jj_inac, int n_inac,
+                     int* n_inac_kept, float* edge_nets, float* target, float* weight,
+                     float* target_inac, float* weight_inac) {
+    /* CudaDroid::rm_keyframe, main.cu:866-941 (fmaps as fmap_row floats of
+       raw bytes, whatever their element type) */
+    *n_kept = n;
+    *n_inac_kept = n_inac;
+    if (ix < 0 || ix >= t) return;
+    for (int k = ix; k < t - 1; k++) {
+        memcpy(poses + (size_t)k * 7, poses + (size_t)(k + 1) * 7, sizeof(float) * 7);
+        memcpy(disps + (size_t)k * hw, disps + (size_t)(k + 1) * hw, sizeof(float) * hw);
+        memcpy(fmaps + (size_t)k * fmap_row, fmaps + (size_t)(k + 1) * fmap_row,
+               sizeof(float) * fmap_row);
+        memcpy(nets + (size_t)k * net_row, nets + (size_t)(k + 1) * net_row,
+               sizeof(float) * net_row);
+        memcpy(inps + (size_t)k * net_row, inps + (size_t)(k + 1) * net_row,
+               sizeof(float) * net_row);
+    }
+    *n_kept = rm_kf_edges(ix, ii, jj, age, n, edge_nets, target, weight, net_row, 2 * hw);
+    *n_inac_kept = rm_kf_edges(ix, ii_inac, jj_inac, NULL, n_inac, NULL, target_inac,
+                               weight_inac, 0, 2 * hw);
+}

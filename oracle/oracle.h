@@ -178,6 +178,12 @@ int orc_store_and_remove_edges(const unsigned char* mask, int n, int* ii, int* j
                                float* target_inac, float* weight_inac, long tw_row);
 void orc_init_new_edges(const float* nets, float* edge_nets, float* weight, const int* ii,
                         int first, int count, long net_row, long tw_row);
+/* CudaDroid::rm_keyframe (main.cu:866-941) */
+void orc_rm_keyframe(int ix, int t, float* poses, float* disps, float* fmaps, long fmap_row,
+                     float* nets, float* inps, long net_row, long hw, int* ii, int* jj,
+                     int* age, int n, int* n_kept, int* ii_inac, int* jj_inac, int n_inac,
+                     int* n_inac_kept, float* edge_nets, float* target, float* weight,
+                     float* target_inac, float* weight_inac);
 
 #ifdef __cplusplus
 }

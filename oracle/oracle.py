@@ -96,6 +96,11 @@ def lib():
                                             _f32p, _f32p, _f32p, c_long], c_int),
             "orc_init_new_edges": ([_f32p, _f32p, _f32p, _i32p, c_int, c_int, c_long, c_long],
                                    None),
+            "orc_rm_keyframe": ([c_int, c_int, _f32p, _f32p, _f32p, c_long, _f32p, _f32p,
+                                 c_long, c_long, _i32p, _i32p, _i32p, c_int,
+                                 ctypes.POINTER(c_int), _i32p, _i32p, c_int,
+                                 ctypes.POINTER(c_int), _f32p, _f32p, _f32p, _f32p, _f32p],
+                                None),
         }
         for name, (argtypes, restype) in glue.items():
             fn = getattr(L, name)
@@ -457,3 +462,36 @@ def init_new_edges(nets, edge_nets, weight, ii, first, count):
     lib().orc_init_new_edges(nets.reshape(-1), en.reshape(-1), w.reshape(-1), _c(ii, np.int32),
                              int(first), int(count), en[0].size, w[0].size)
     return en, w
+
+
+def rm_keyframe(ix, st):
+    """CudaDroid::rm_keyframe (main.cu:866-941) on copies of the state dict
+    st (poses [t,7], disps [t,hw], fmaps [t,...] any dtype, nets/inps [t,...],
+    ii/jj/age, ii_inac/jj_inac, edge_nets/target/weight, target_inac/
+    weight_inac): the same dict after the removal (lists cut to their new
+    lengths; arrays keep their row counts)."""
+    o = {k: np.array(v) for k, v in st.items()}
+    t = len(o["poses"])
+    fm = np.ascontiguousarray(o["fmaps"]).view(np.float32).reshape(t, -1)
+    hw = o["disps"][0].size
+    net_row = o["nets"][0].size
+    for k in ("poses", "disps", "nets", "inps", "edge_nets", "target", "weight", "target_inac",
+              "weight_inac"):
+        o[k] = np.ascontiguousarray(o[k], np.float32)
+    for k in ("ii", "jj", "age", "ii_inac", "jj_inac"):
+        o[k] = np.ascontiguousarray(o[k], np.int32)
+    nk, nik = ctypes.c_int(0), ctypes.c_int(0)
+    flat = lambda a: a.reshape(-1) if a.size else np.zeros(1, a.dtype)
+    lib().orc_rm_keyframe(int(ix), t, flat(o["poses"]), flat(o["disps"]), flat(fm),
+                          fm.shape[1], flat(o["nets"]), flat(o["inps"]), net_row, hw,
+                          flat(o["ii"]), flat(o["jj"]), flat(o["age"]), len(o["ii"]),
+                          ctypes.byref(nk), flat(o["ii_inac"]), flat(o["jj_inac"]),
+                          len(o["ii_inac"]), ctypes.byref(nik), flat(o["edge_nets"]),
+                          flat(o["target"]), flat(o["weight"]), flat(o["target_inac"]),
+                          flat(o["weight_inac"]))
+    o["fmaps"] = fm.view(np.asarray(st["fmaps"]).dtype).reshape(np.shape(st["fmaps"]))
+    for k in ("ii", "jj", "age"):
+        o[k] = o[k][:nk.value]
+    for k in ("ii_inac", "jj_inac"):
+        o[k] = o[k][:nik.value]
+    return o

@@ -567,3 +567,88 @@ extern "C" int slk_init_new_edges(slk_ctx* ctx, const float* nets, float* edge_n
     }
     return SLK_OK;
 }
+
+extern "C" int slk_rm_keyframe(slk_ctx* ctx, int ix, int num_keyframes, float* poses,
+                               float* disps, void* fmaps, int fmap_dtype, float* nets,
+                               float* inps, long net_row, int* ii_host, int* jj_host,
+                               int* age_host, int n, int* n_kept, int* ii_inac_host,
+                               int* jj_inac_host, int n_inac, int* n_inac_kept,
+                               float* edge_nets, float* target, float* weight,
+                               float* target_inac, float* weight_inac, hipStream_t stream) {
+    if (!ctx || !n_kept || !n_inac_kept) return fail(SLK_E_ARG, "rm_keyframe: null argument");
+    if (n < 0 || n_inac < 0 || net_row < 0 || num_keyframes < 0)
+        return fail(SLK_E_ARG, "rm_keyframe: bad sizes");
+    if (fmap_dtype != SLK_F32 && fmap_dtype != SLK_F16)
+        return fail(SLK_E_ARG, "rm_keyframe: fmap dtype must be SLK_F32 or SLK_F16");
+    *n_kept = n;
+    *n_inac_kept = n_inac;
+    const int t = num_keyframes;
+    if (ix < 0 || ix >= t) return SLK_OK;  // main.cu:871
+    if ((n > 0 && (!ii_host || !jj_host)) || (n_inac > 0 && (!ii_inac_host || !jj_inac_host)))
+        return fail(SLK_E_ARG, "rm_keyframe: null edge lists");
+    // keyframe rows ix+1 .. t-1 move down by one (main.cu:874-885)
+    std::vector<int> kf_src, kf_dst;
+    for (int k = ix; k < t - 1; k++) {
+        kf_src.push_back(k + 1);
+        kf_dst.push_back(k);
+    }
+    // edges: those touching ix go, indices above ix drop by one, the rest
+    // close up in order with their rows (main.cu:889-917, 920-940)
+    auto filter = [ix](int* a, int* b, int* age, int cnt, std::vector<int>& src,
+                       std::vector<int>& dst) {
+        int kept = 0;
+        for (int e = 0; e < cnt; e++) {
+            int ei = a[e], ej = b[e];
+            if (ei == ix || ej == ix) continue;
+            if (ei > ix) ei--;
+            if (ej > ix) ej--;
+            if (kept != e) {
+                src.push_back(e);
+                dst.push_back(kept);
+            }
+            a[kept] = ei;
+            b[kept] = ej;
+            if (age) age[kept] = age[e];
+            kept++;
+        }
+        return kept;
+    };
+    std::vector<int> a_src, a_dst, i_src, i_dst;
+    const int ka = filter(ii_host, jj_host, age_host, n, a_src, a_dst);
+    const int ki = filter(ii_inac_host, jj_inac_host, nullptr, n_inac, i_src, i_dst);
+    *n_kept = ka;
+    *n_inac_kept = ki;
+    const int nk = (int)kf_src.size(), na = (int)a_src.size(), nin = (int)i_src.size();
+    if (std::max(nk, std::max(na, nin)) > 65535)
+        return fail(SLK_E_ARG, "rm_keyframe: too many rows");
+    if (nk + na + nin == 0) return SLK_OK;
+    std::vector<int> buf;
+    for (auto* v : {&kf_src, &kf_dst, &a_src, &a_dst, &i_src, &i_dst})
+        buf.insert(buf.end(), v->begin(), v->end());
+    SLK_TRY(upload(ctx, buf.data(), buf.size() * sizeof(int), stream));
+    const int* d = ctx->glue_idx.as<int>();
+    const int *dks = d, *dkd = dks + nk, *das = dkd + nk, *dad = das + na, *dis = dad + na,
+              *did = dis + nin;
+    const long hw = ctx->HW;
+    // each array present is moved; a null pointer skips it
+    if (nk > 0) {
+        if (poses) SLK_TRY(move_rows(ctx, poses, 7, dks, dkd, nk, stream));
+        if (disps) SLK_TRY(move_rows(ctx, disps, hw, dks, dkd, nk, stream));
+        if (fmaps) {
+            const long frow = fmap_dtype == SLK_F16 ? (long)ctx->C * hw / 2 : (long)ctx->C * hw;
+            SLK_TRY(move_rows(ctx, static_cast<float*>(fmaps), frow, dks, dkd, nk, stream));
+        }
+        if (nets) SLK_TRY(move_rows(ctx, nets, net_row, dks, dkd, nk, stream));
+        if (inps) SLK_TRY(move_rows(ctx, inps, net_row, dks, dkd, nk, stream));
+    }
+    if (na > 0) {
+        if (edge_nets) SLK_TRY(move_rows(ctx, edge_nets, net_row, das, dad, na, stream));
+        if (target) SLK_TRY(move_rows(ctx, target, 2 * hw, das, dad, na, stream));
+        if (weight) SLK_TRY(move_rows(ctx, weight, 2 * hw, das, dad, na, stream));
+    }
+    if (nin > 0) {
+        if (target_inac) SLK_TRY(move_rows(ctx, target_inac, 2 * hw, dis, did, nin, stream));
+        if (weight_inac) SLK_TRY(move_rows(ctx, weight_inac, 2 * hw, dis, did, nin, stream));
+    }
+    return SLK_OK;
+}

@@ -39,6 +39,7 @@ EXPORTS = [
     "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
     "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set", "slk_proximity_factors",
     "slk_oldest_edges_mask", "slk_store_and_remove_edges", "slk_init_new_edges",
+    "slk_rm_keyframe",
 ]
 
 
@@ -116,6 +117,8 @@ def lib():
             "slk_store_and_remove_edges": [P, P, I, P, P, P, P, P, ctypes.POINTER(I), I, P, L,
                                            P, P, P, P, L, ctypes.POINTER(I), P],
             "slk_init_new_edges": [P, P, P, P, P, I, I, L, L, P],
+            "slk_rm_keyframe": [P, I, I, P, P, P, I, P, P, L, P, P, P, I, ctypes.POINTER(I), P,
+                                P, I, ctypes.POINTER(I), P, P, P, P, P, P],
         }
         for name, args in sig.items():
             fn = getattr(L_, name)

@@ -163,3 +163,55 @@ def test_init_new_edges_matches_oracle(slk):
     np.testing.assert_array_equal(de.to_host(), ref_en)
     np.testing.assert_array_equal(dw.to_host(), ref_w)
     ctx.close()
+
+
+@pytest.mark.parametrize("ix", [9, 0, 11])
+def test_rm_keyframe_matches_oracle(slk, ix):
+    """CudaDroid::rm_keyframe (main.cu:866-941) on a 12-keyframe window with
+    48 active and 20 inactive edges at 48x64: every array and list bitwise
+    equal to the oracle's (ix = 9 is the frontend's nk - 3)."""
+    h, w, t, ne, ni = 48, 64, 12, 48, 20
+    hw = h * w
+    announce(f"rm_keyframe ix={ix}")
+    rng = np.random.default_rng(13 + ix)
+    st = {"poses": rng.normal(size=(t, 7)).astype(np.float32),
+          "disps": rng.uniform(size=(t, hw)).astype(np.float32),
+          "fmaps": rng.normal(size=(t, 128, hw)).astype(np.float16),
+          "nets": rng.normal(size=(t, 128, hw)).astype(np.float32),
+          "inps": rng.normal(size=(t, 128, hw)).astype(np.float32),
+          "ii": rng.integers(0, t, ne).astype(np.int32),
+          "jj": rng.integers(0, t, ne).astype(np.int32),
+          "age": rng.integers(0, 25, ne).astype(np.int32),
+          "ii_inac": rng.integers(0, t, ni).astype(np.int32),
+          "jj_inac": rng.integers(0, t, ni).astype(np.int32),
+          "edge_nets": rng.normal(size=(ne, 128, hw)).astype(np.float32),
+          "target": rng.normal(size=(ne, 2, hw)).astype(np.float32),
+          "weight": rng.uniform(size=(ne, 2, hw)).astype(np.float32),
+          "target_inac": rng.normal(size=(ni, 2, hw)).astype(np.float32),
+          "weight_inac": rng.uniform(size=(ni, 2, hw)).astype(np.float32)}
+    ref = orc.rm_keyframe(ix, st)
+    D = slk.DeviceArray.from_host
+    arrs = ("poses", "disps", "nets", "inps", "edge_nets", "target", "weight", "target_inac",
+            "weight_inac")
+    dv = {k: D(st[k]) for k in arrs}
+    dfm = D(st["fmaps"].view(np.uint16))
+    lists = {k: st[k].copy() for k in ("ii", "jj", "age", "ii_inac", "jj_inac")}
+    nk, nik = ctypes.c_int(-1), ctypes.c_int(-1)
+    ctx = slk.Context(h, w, C=128, max_batch=48)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    slk.check(slk.lib().slk_rm_keyframe(
+        ctx.ptr, ix, t, dv["poses"].ptr, dv["disps"].ptr, dfm.ptr, slk.SLK_F16, dv["nets"].ptr,
+        dv["inps"].ptr, 128 * hw, P(lists["ii"]), P(lists["jj"]), P(lists["age"]), ne,
+        ctypes.byref(nk), P(lists["ii_inac"]), P(lists["jj_inac"]), ni, ctypes.byref(nik),
+        dv["edge_nets"].ptr, dv["target"].ptr, dv["weight"].ptr, dv["target_inac"].ptr,
+        dv["weight_inac"].ptr, None))
+    slk.hip().sync()
+    assert (nk.value, nik.value) == (len(ref["ii"]), len(ref["ii_inac"]))
+    for k in ("ii", "jj", "age"):
+        np.testing.assert_array_equal(lists[k][:nk.value], ref[k])
+    for k in ("ii_inac", "jj_inac"):
+        np.testing.assert_array_equal(lists[k][:nik.value], ref[k])
+    for k in arrs:
+        np.testing.assert_array_equal(dv[k].to_host(), ref[k], err_msg=k)
+    np.testing.assert_array_equal(dfm.to_host().view(np.float16), ref["fmaps"])
+    ctx.close()

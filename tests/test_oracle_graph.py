@@ -144,3 +144,43 @@ def test_init_new_edges_hand_worked():
     np.testing.assert_array_equal(en2[4], nets[2])      # ii[4] = 2
     np.testing.assert_array_equal(w2[:3], w[:3])
     np.testing.assert_array_equal(w2[3:], 0.0)
+
+
+def _kf_state(t, ne, ni, hw, seed=0, fdtype=np.float16):
+    rng = np.random.default_rng(seed)
+    return {
+        "poses": _coded_rows(t, (7,), 0.0), "disps": _coded_rows(t, (hw,), 10000.0),
+        "fmaps": rng.normal(size=(t, 4, hw)).astype(fdtype),
+        "nets": _coded_rows(t, (3, hw), 20000.0), "inps": _coded_rows(t, (3, hw), 30000.0),
+        "ii": rng.integers(0, t, ne), "jj": rng.integers(0, t, ne),
+        "age": np.arange(ne), "ii_inac": rng.integers(0, t, ni), "jj_inac": rng.integers(0, t, ni),
+        "edge_nets": _coded_rows(ne, (3, hw), 40000.0), "target": _coded_rows(ne, (2, hw), 5e4),
+        "weight": _coded_rows(ne, (2, hw), 6e4), "target_inac": _coded_rows(ni, (2, hw), 7e4),
+        "weight_inac": _coded_rows(ni, (2, hw), 8e4)}
+
+
+def test_rm_keyframe_hand_worked():
+    st = _kf_state(5, 6, 3, 4)
+    st["ii"], st["jj"] = np.array([0, 2, 1, 3, 4, 2]), np.array([1, 3, 0, 4, 2, 1])
+    st["ii_inac"], st["jj_inac"] = np.array([2, 4, 0]), np.array([0, 3, 1])
+    r = orc.rm_keyframe(2, st)
+    # keyframes 3, 4 move to 2, 3; row 4 keeps its old content
+    for k in ("poses", "disps", "fmaps", "nets", "inps"):
+        np.testing.assert_array_equal(r[k][:2], st[k][:2])
+        np.testing.assert_array_equal(r[k][2:4], st[k][3:5])
+        np.testing.assert_array_equal(r[k][4], st[k][4])
+    # edges touching 2 (1, 4, 5) go; 3 -> 2, 4 -> 3
+    np.testing.assert_array_equal(r["ii"], [0, 1, 2])
+    np.testing.assert_array_equal(r["jj"], [1, 0, 3])
+    np.testing.assert_array_equal(r["age"], [0, 2, 3])
+    for k in ("edge_nets", "target", "weight"):
+        np.testing.assert_array_equal(r[k][:3], st[k][[0, 2, 3]])
+    # inactive: (2,0) goes; (4,3) -> (3,2); (0,1) stays
+    np.testing.assert_array_equal(r["ii_inac"], [3, 0])
+    np.testing.assert_array_equal(r["jj_inac"], [2, 1])
+    for k in ("target_inac", "weight_inac"):
+        np.testing.assert_array_equal(r[k][:2], st[k][[1, 2]])
+    # out of range: nothing changes
+    r = orc.rm_keyframe(5, st)
+    np.testing.assert_array_equal(r["ii"], st["ii"])
+    np.testing.assert_array_equal(r["nets"], st["nets"])
