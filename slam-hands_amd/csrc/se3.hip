@@ -100,6 +100,10 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
     const float tij[3] = {rel[0], rel[1], rel[2]};
     const float qij[4] = {rel[3], rel[4], rel[5], rel[6]};
     const float fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
+    // the reference builds with --use_fast_math (approximate divisions); here
+    // each projection takes one hardware reciprocal (v_rcp_f32, 1 ulp) of the
+    // depth and the normalised coordinates one reciprocal of each focal length
+    const float ifx = 1.0f / fx, ify = 1.0f / fy;
     const int HW = H * W;
     const int ix = ii[e];
     float acc[3] = {0.0f, 0.0f, 0.0f};  // accum, valid, total
@@ -107,12 +111,13 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
         const int i = k / W, j = k - (k / W) * W;
         const float u = (float)j, v = (float)i;
         float Xi[4], Xj[4];
-        Xi[0] = (u - cx) / fx;
-        Xi[1] = (v - cy) / fy;
+        Xi[0] = (u - cx) * ifx;
+        Xi[1] = (v - cy) * ify;
         Xi[2] = 1.0f;
         Xi[3] = disps[(size_t)ix * HW + k];
         act_se3(tij, qij, Xi, Xj);
-        float du = fx * (Xj[0] / Xj[2]) + cx - u, dv = fy * (Xj[1] / Xj[2]) + cy - v;
+        float iz = __builtin_amdgcn_rcpf(Xj[2]);
+        float du = fx * (Xj[0] * iz) + cx - u, dv = fy * (Xj[1] * iz) + cy - v;
         float d = sqrtf(du * du + dv * dv);
         acc[2] += beta;
         if (Xj[2] > kMinDepth) {
@@ -122,8 +127,9 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
         Xj[0] = Xi[0] + Xi[3] * tij[0];
         Xj[1] = Xi[1] + Xi[3] * tij[1];
         Xj[2] = Xi[2] + Xi[3] * tij[2];
-        du = fx * (Xj[0] / Xj[2]) + cx - u;
-        dv = fy * (Xj[1] / Xj[2]) + cy - v;
+        iz = __builtin_amdgcn_rcpf(Xj[2]);
+        du = fx * (Xj[0] * iz) + cx - u;
+        dv = fy * (Xj[1] * iz) + cy - v;
         d = sqrtf(du * du + dv * dv);
         acc[2] += (1.0f - beta);
         if (Xj[2] > kMinDepth) {
