@@ -483,39 +483,42 @@ extern "C" int slk_store_and_remove_edges(slk_ctx* ctx, const unsigned char* mas
     if (n == 0) return SLK_OK;
     if (!mask_host || !ii_host || !jj_host)
         return fail(SLK_E_ARG, "store_and_remove_edges: null edge lists");
+    if (n > 65535) return fail(SLK_E_ARG, "store_and_remove_edges: more than 65535 edges");
     // the reference's loop (main.cu:795-836): masked edges go to the inactive
     // list while it has room (beyond it they are dropped), kept edges close up
-    // in order; rows move with their edges
+    // in order; rows move with their edges. The moves are listed first and
+    // every argument checked before any list changes.
     std::vector<int> stored, src, dst;
-    int kept = 0, ni = *num_inac;
+    int kept = 0;
     for (int e = 0; e < n; e++) {
         if (mask_host[e]) {
-            if (ni < max_inac) {
-                if (!ii_inac_host || !jj_inac_host)
-                    return fail(SLK_E_ARG, "store_and_remove_edges: null inactive lists");
-                ii_inac_host[ni] = ii_host[e];
-                jj_inac_host[ni] = jj_host[e];
-                stored.push_back(e);
-                ni++;
-            }
+            if (*num_inac + (int)stored.size() < max_inac) stored.push_back(e);
         } else {
             if (kept != e) {
                 src.push_back(e);
                 dst.push_back(kept);
-                ii_host[kept] = ii_host[e];
-                jj_host[kept] = jj_host[e];
-                if (age_host) age_host[kept] = age_host[e];
             }
             kept++;
         }
     }
     const int s = (int)stored.size(), k = (int)src.size();
-    if (s > 0 && (!target || !weight || !target_inac || !weight_inac) && tw_row > 0)
+    if (s > 0 && (!ii_inac_host || !jj_inac_host))
+        return fail(SLK_E_ARG, "store_and_remove_edges: null inactive lists");
+    if (s > 0 && tw_row > 0 && (!target || !weight || !target_inac || !weight_inac))
         return fail(SLK_E_ARG, "store_and_remove_edges: null target/weight rows");
     if (k > 0 && ((net_row > 0 && !edge_nets) || (tw_row > 0 && (!target || !weight))))
         return fail(SLK_E_ARG, "store_and_remove_edges: null edge rows");
-    if (s > 65535 || k > 65535) return fail(SLK_E_ARG, "store_and_remove_edges: too many rows");
     const int first_inac = *num_inac;
+    for (int q = 0; q < s; q++) {
+        ii_inac_host[first_inac + q] = ii_host[stored[q]];
+        jj_inac_host[first_inac + q] = jj_host[stored[q]];
+    }
+    for (int q = 0; q < k; q++) {  // src[q] > dst[q], both increasing: in place
+        ii_host[dst[q]] = ii_host[src[q]];
+        jj_host[dst[q]] = jj_host[src[q]];
+        if (age_host) age_host[dst[q]] = age_host[src[q]];
+    }
+    const int ni = first_inac + s;
     *num_inac = ni;
     *n_kept = kept;
     if (s + k == 0) return SLK_OK;
@@ -586,6 +589,7 @@ extern "C" int slk_rm_keyframe(slk_ctx* ctx, int ix, int num_keyframes, float* p
     if (ix < 0 || ix >= t) return SLK_OK;  // main.cu:871
     if ((n > 0 && (!ii_host || !jj_host)) || (n_inac > 0 && (!ii_inac_host || !jj_inac_host)))
         return fail(SLK_E_ARG, "rm_keyframe: null edge lists");
+    if (t > 65536 || n > 65535 || n_inac > 65535) return fail(SLK_E_ARG, "rm_keyframe: too many rows");
     // keyframe rows ix+1 .. t-1 move down by one (main.cu:874-885)
     std::vector<int> kf_src, kf_dst;
     for (int k = ix; k < t - 1; k++) {
@@ -619,8 +623,6 @@ extern "C" int slk_rm_keyframe(slk_ctx* ctx, int ix, int num_keyframes, float* p
     *n_kept = ka;
     *n_inac_kept = ki;
     const int nk = (int)kf_src.size(), na = (int)a_src.size(), nin = (int)i_src.size();
-    if (std::max(nk, std::max(na, nin)) > 65535)
-        return fail(SLK_E_ARG, "rm_keyframe: too many rows");
     if (nk + na + nin == 0) return SLK_OK;
     std::vector<int> buf;
     for (auto* v : {&kf_src, &kf_dst, &a_src, &a_dst, &i_src, &i_dst})
