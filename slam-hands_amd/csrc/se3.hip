@@ -79,7 +79,10 @@ __global__ void k_disp_retr(float* __restrict__ disps, const float* __restrict__
 }
 
 // Mean flow magnitude of the full and the translation-only reprojection
-// (se3.cuh:209-277), one workgroup per pair, deterministic reduction.
+// (se3.cuh:209-277), one wavefront per pair (four pairs per workgroup): every
+// lane forms the pair's relative pose itself (uniform arithmetic, no barrier),
+// takes pixels lane, lane + 64, ... and the three sums are reduced across the
+// wavefront in a fixed order (deterministic).
 __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict__ poses,
                                                         const float* __restrict__ disps,
                                                         const float* __restrict__ intr,
@@ -87,18 +90,16 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
                                                         const int* __restrict__ jj,
                                                         float* __restrict__ dist, int M, int H,
                                                         int W, float beta) {
-    const int e = blockIdx.x;
-    __shared__ float rel[7];
-    __shared__ float red[3 * 4];
-    if (threadIdx.x == 0) {
+    const int e = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (e >= M) return;  // uniform over the wavefront
+    const int lane = threadIdx.x & 63;
+    float tij[3], qij[4];
+    {
         float ti[3], qi[4], tj[3], qj[4];
         load_pose(poses, ii[e], ti, qi);
         load_pose(poses, jj[e], tj, qj);
-        rel_se3(ti, qi, tj, qj, rel, rel + 3);
+        rel_se3(ti, qi, tj, qj, tij, qij);
     }
-    __syncthreads();
-    const float tij[3] = {rel[0], rel[1], rel[2]};
-    const float qij[4] = {rel[3], rel[4], rel[5], rel[6]};
     const float fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
     // the reference builds with --use_fast_math (approximate divisions); here
     // each projection takes one hardware reciprocal (v_rcp_f32, 1 ulp) of the
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
     const int HW = H * W;
     const int ix = ii[e];
     float acc[3] = {0.0f, 0.0f, 0.0f};  // accum, valid, total
-    for (int k = threadIdx.x; k < HW; k += blockDim.x) {
+    for (int k = lane; k < HW; k += 64) {
         const int i = k / W, j = k - (k / W) * W;
         const float u = (float)j, v = (float)i;
         float Xi[4], Xj[4];
@@ -137,10 +138,14 @@ __global__ __launch_bounds__(256) void k_frame_distance(const float* __restrict_
             acc[1] += (1.0f - beta);
         }
     }
-    block_sum(acc, red);
-    if (threadIdx.x == 0)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+        for (int q = 0; q < 3; q++) acc[q] += __shfl_xor(acc[q], off, 64);
+    if (lane == 0)
         dist[e] = (acc[1] / (acc[2] + 1e-8f) < 0.75f) ? 1000.0f : acc[0] / acc[1];
 }
+
 
 __global__ void k_clamp(float* __restrict__ d, int n, float lo) {
     const int k = blockIdx.x * blockDim.x + threadIdx.x;
@@ -191,8 +196,8 @@ extern "C" int slk_frame_distance(const float* poses, const float* disps, const 
     if (M <= 0) return SLK_OK;
     if (!poses || !disps || !intrinsics || !ii || !jj || !dist || H < 1 || W < 1)
         return fail(SLK_E_ARG, "frame_distance: bad args");
-    hipLaunchKernelGGL(k_frame_distance, dim3(M), dim3(256), 0, stream, poses, disps, intrinsics,
-                       ii, jj, dist, M, H, W, beta);
+    hipLaunchKernelGGL(k_frame_distance, dim3((M + 3) / 4), dim3(256), 0, stream, poses, disps,
+                       intrinsics, ii, jj, dist, M, H, W, beta);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
