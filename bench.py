@@ -83,7 +83,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the path "
-              "would shard by edge across GPUs (see DESIGN.md) but no multi-GPU run is "
+              "would shard by edge across GPUs, each holding the frames its edges touch, "
+              "but no multi-GPU run is "
               "implemented.", file=sys.stderr)
         sys.exit(2)
     import slk
@@ -261,7 +262,7 @@ def main():
 
 
 def backend(args, slk, wl, H):
-    """The backend configuration: correlation + lookup
+    """The backend configuration (200 keyframes, ~2000 edges): correlation + lookup
     of all 2000 edges of a 200-keyframe graph in 48-edge launches (every
     keyframe's operands split once per pass, slk_corr_prepare_frames; the
     per-call preparation is timed beside it), then 5 BA
