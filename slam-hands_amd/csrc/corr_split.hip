@@ -518,6 +518,10 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         dma_x1(coords + ((size_t)e * 2 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
     }
     if (nk > 1) issue(1, 1);
+    // While in its chunk loop a wave issues at raised priority, so that on a
+    // SIMD shared with the other workgroup's extracting wave the MFMA issue
+    // goes first and the extraction takes the slots left over.
+    __builtin_amdgcn_s_setprio(1);
     for (int k = 0; k < nk; k++) {
         if (k + 1 < nk)
             __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);
@@ -529,6 +533,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
         compute(k % kStages);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (tid == 0) next_tile = lo + taken;  // read after the end-of-tile barrier
     if (tid < kSrcTile) {
         const bool in = p0 + tid < HW;
