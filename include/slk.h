@@ -60,7 +60,8 @@ typedef enum { SLK_PREC_BF16X3 = 0, SLK_PREC_FP32 = 1 } slk_corr_precision;
  * batched scratch for max_batch edges (the reference's [B,hw,hw] volumes +
  * levels, main.cu:1413-1418, become 8x8 lookup windows per pixel and level
  * plus the split features of the frames in flight) and the single-edge volume
- * and pyramid (main.cu:1400-1405). h, w <= 65536 and h*w <= 2^24.
+ * and pyramid (main.cu:1400-1405). h, w <= 65536 and h*w < 2^21 (the
+ * batched path's per-slot window offsets are 32-bit).
  * Replaces CorrBlock::init (cuda_slam/corr.cuh:75) and
  * BundleAdjustment::init(h, w) (cuda_slam/ba.cuh:408). levels <= 4, radius == 3. */
 int slk_create(slk_ctx** ctx, int h, int w, int C, int max_batch, int levels,

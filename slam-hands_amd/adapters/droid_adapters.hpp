@@ -9,6 +9,8 @@
 //                     reading the same state (fmaps [n][128][h][w], the host
 //                     edge arrays ii_host/jj_host) the reference reads from
 //                     DroidState.
+//   CorrBlock         init / build / sample_single / destroy of the
+//                     standalone correlation block (corr.cuh:61-263).
 //   BundleAdjustment  init / iterate / print_profile / destroy (ba.cuh:397-819).
 //   projmap, pose_retr, frame_distance, clamp_disps
 //                     the SE3 kernel launches with the reference's argument
@@ -32,6 +34,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include <hip/hip_runtime_api.h>
@@ -138,6 +141,68 @@ class CorrEngine {
     const int* jj_host_ = nullptr;
 };
 
+// CorrBlock of cuda_slam/corr.cuh:61-263 with its member signatures. The
+// reference passes cuBLAS and cuDNN handles to init; this path has no such
+// handles, so the two parameters are opaque pointers that are accepted and
+// ignored. build(fmap1, fmap2, bn, c, h, w) keeps the volume of pair n = 0,
+// the one sample_single reads (corr.cuh:234-256 samples corr_pyramid[l] from
+// its start); the reference's batched sample() mis-addresses its output
+// (corr.cuh:186-231) and is not offered. The scale is the one the live
+// correlation path uses, 1/16 (main.cu:1506,1572), not corr.cuh:100's 1/c;
+// set_scale() changes it. The context is created on the first build and
+// again whenever (c, h, w) change.
+class CorrBlock {
+  public:
+    using BlasHandle = void*;
+    using DnnHandle = void*;
+
+    void init(BlasHandle /*cublas*/, DnnHandle /*cudnn*/, int num_lvl = 4, int rad = 3) {
+        num_levels = num_lvl;
+        radius = rad;
+    }
+
+    void set_scale(float alpha) {
+        if (alpha != scale_) release();
+        scale_ = alpha;
+    }
+
+    // fmap1, fmap2: [bn][c][h][w] fp32 device arrays (corr.cuh:84).
+    void build(float* fmap1, float* fmap2, int bn, int c, int h, int w) {
+        if (bn < 1) check(SLK_E_ARG, "CorrBlock::build (bn < 1)");
+        if (!ctx_ || c != C || h != H || w != W) {
+            release();
+            check(slk_create(&ctx_, h, w, c, 1, num_levels, radius, scale_),
+                  "CorrBlock::build");
+        }
+        BN = bn;
+        C = c;
+        H = h;
+        W = w;
+        check(slk_corr_build(ctx_, fmap1, fmap2, SLK_F32, nullptr), "CorrBlock::build");
+    }
+
+    // coords [2][H][W] -> output [num_levels * 49][H][W] (corr.cuh:234-256);
+    // coords_scaled_buf is the reference's scratch and is not used here.
+    void sample_single(float* coords, float* output, float* /*coords_scaled_buf*/) {
+        if (!ctx_) check(SLK_E_STATE, "CorrBlock::sample_single before build");
+        check(slk_corr_sample(ctx_, coords, output, nullptr), "CorrBlock::sample_single");
+    }
+
+    void destroy() { release(); }
+
+    int num_levels = 4;
+    int radius = 3;
+    int BN = 0, H = 0, W = 0, C = 0;
+
+  private:
+    void release() {
+        if (ctx_) slk_destroy(ctx_);
+        ctx_ = nullptr;
+    }
+    slk_ctx* ctx_ = nullptr;
+    float scale_ = 1.0f / 16.0f;
+};
+
 // BundleAdjustment of cuda_slam/ba.cuh:397-819 (and, with motion_only, the
 // pipeline variant cuda_pipeline/slam.cuh:1475-1592).
 class BundleAdjustment {
@@ -149,7 +214,6 @@ class BundleAdjustment {
     void iterate(float* poses, float* disps, float* intrinsics, float* target, float* weight,
                  float* eta, int* ii_gpu, int* jj_gpu, int* ii_host, int* jj_host,
                  int num_edges, int t0, int t1, float lm, float ep, bool motion_only) {
-        if (profile_) check(slk_profile_enable(ctx_, 1), "profile");
         check(slk_ba_iterate(ctx_, poses, disps, intrinsics, target, weight, eta, ii_gpu, jj_gpu,
                              ii_host, jj_host, num_edges, t0, t1, lm, ep, motion_only ? 1 : 0,
                              nullptr),
@@ -162,7 +226,8 @@ class BundleAdjustment {
             check(st, "BundleAdjustment::iterate");
     }
 
-    // Totals per kernel since the first profiled iterate (ba.cuh:805).
+    // Totals per kernel over the iterates since enable_profile(true)
+    // (ba.cuh:805 prints its totals over prof_count iterations).
     void print_profile() {
         for (int k = 0;; k++) {
             const char* name = nullptr;
@@ -173,7 +238,19 @@ class BundleAdjustment {
         }
     }
 
-    void enable_profile(bool on) { profile_ = on; }
+    // Starts (clearing earlier totals) or stops the per-kernel timing.
+    void enable_profile(bool on) { check(slk_profile_enable(ctx_, on ? 1 : 0), "profile"); }
+
+    // Launch count of the named kernel in the current totals (0 if none).
+    int profiled_launches(const char* kernel) {
+        for (int k = 0;; k++) {
+            const char* name = nullptr;
+            double ms = 0.0;
+            int n = 0;
+            if (slk_profile_kernel(ctx_, k, &name, &ms, &n) != SLK_OK || !name) return 0;
+            if (std::strcmp(name, kernel) == 0) return n;
+        }
+    }
 
     void destroy() {
         if (ctx_) slk_destroy(ctx_);
@@ -184,7 +261,6 @@ class BundleAdjustment {
 
   private:
     slk_ctx* ctx_ = nullptr;
-    bool profile_ = false;
 };
 
 // projmap_kernel<<<M, 256>>>(poses, disps, intr, ii, jj, coords, valid, M, H, W)

@@ -73,8 +73,12 @@ extern "C" int slk_create(slk_ctx** out, int h, int w, int C, int max_batch, int
     if (radius != 3) return fail(SLK_E_ARG, "slk_create: only radius 3 is implemented");
     if ((h >> (levels - 1)) < 1 || (w >> (levels - 1)) < 1)
         return fail(SLK_E_ARG, "slk_create: feature map too small for the pyramid depth");
-    if ((long)h * w > (1L << 24) || h > 65536 || w > 65536)
-        return fail(SLK_E_ARG, "slk_create: h*w above 2^24 or a side above 2^16");
+    // The batched path addresses a slot of lookup windows (1 KB per source
+    // pixel) with 32-bit byte offsets and a buffer-resource range of
+    // 1024*h*w bytes, so h*w stays below 2^21 (the single-edge volume,
+    // (h*w)^2 floats, is far beyond memory long before that).
+    if ((long)h * w >= (1L << 21) || h > 65536 || w > 65536)
+        return fail(SLK_E_ARG, "slk_create: h*w must be below 2^21 and each side at most 2^16");
     slk_ctx* ctx = new slk_ctx();
     ctx->h = h;
     ctx->w = w;

@@ -65,13 +65,53 @@ extern "C" int adapter_corr(const void* fmaps, int dtype, int nframes, int h, in
     return bad;
 }
 
+// CorrBlock (corr.cuh:61-263) as a host would drive it: init with (absent)
+// library handles, build(fmap1, fmap2, bn, c, h, w) of bn pairs, then
+// sample_single(coords, output, scratch), which reads pair 0. A second build
+// at another size rebuilds the context. fmap1/fmap2 [bn][c][h][w] fp32,
+// coords [2][h*w], out [196][h*w]; out2 receives the lookup of a second build
+// with (h2, w2) maps fmap1b/fmap2b [c][h2][w2] and coords2 [2][h2*w2].
+extern "C" int adapter_corrblock(const float* fmap1, const float* fmap2, int bn, int c, int h,
+                                 int w, const float* coords, float* out, const float* fmap1b,
+                                 const float* fmap2b, int h2, int w2, const float* coords2,
+                                 float* out2) {
+    const size_t hw = (size_t)h * w, hw2 = (size_t)h2 * w2;
+    float* d_a = upload(fmap1, (size_t)bn * c * hw);
+    float* d_b = upload(fmap2, (size_t)bn * c * hw);
+    float* d_c = upload(coords, 2 * hw);
+    float* d_a2 = upload(fmap1b, (size_t)c * hw2);
+    float* d_b2 = upload(fmap2b, (size_t)c * hw2);
+    float* d_c2 = upload(coords2, 2 * hw2);
+    float *d_o = nullptr, *d_o2 = nullptr, *d_s = nullptr;
+    if (!d_a || !d_b || !d_c || !d_a2 || !d_b2 || !d_c2 ||
+        hipMalloc(&d_o, 196 * hw * 4) != hipSuccess ||
+        hipMalloc(&d_o2, 196 * hw2 * 4) != hipSuccess ||
+        hipMalloc(&d_s, 2 * hw * 4) != hipSuccess)
+        return 1;
+    slk_droid::CorrBlock cb;
+    cb.init(nullptr, nullptr, 4, 3);
+    cb.build(d_a, d_b, bn, c, h, w);
+    cb.sample_single(d_c, d_o, d_s);
+    cb.build(d_a2, d_b2, 1, c, h2, w2);
+    cb.sample_single(d_c2, d_o2, d_s);
+    int bad = download(out, d_o, 196 * hw);
+    bad |= download(out2, d_o2, 196 * hw2);
+    cb.destroy();
+    for (void* p : {(void*)d_a, (void*)d_b, (void*)d_c, (void*)d_a2, (void*)d_b2, (void*)d_c2,
+                    (void*)d_o, (void*)d_o2, (void*)d_s})
+        (void)hipFree(p);
+    return bad;
+}
+
 // `iters` BundleAdjustment::iterate calls followed by clamp_disps(0.001), as
 // run_update_pass does (main.cu:2371-2397). poses [N][7] and disps [N][h*w]
-// are updated in place.
+// are updated in place. With launches != NULL the iterates run profiled and
+// launches[0..1] receive the total launch counts of the linearization and
+// solve kernels.
 extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const float* intr,
                           const float* target, const float* weight, const float* eta,
                           const int* ii, const int* jj, int M, int t0, int t1, float lm,
-                          float ep, int motion_only, int iters) {
+                          float ep, int motion_only, int iters, int* launches) {
     const size_t hw = (size_t)h * w;
     float* d_p = upload(poses, (size_t)N * 7);
     float* d_d = upload(disps, (size_t)N * hw);
@@ -85,9 +125,16 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
     std::vector<int> ii_h(ii, ii + M), jj_h(jj, jj + M);
     slk_droid::BundleAdjustment ba;
     ba.init(h, w);
+    if (launches) ba.enable_profile(true);
     for (int k = 0; k < iters; k++)
         ba.iterate(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M, t0,
                    t1, lm, ep, motion_only != 0);
+    if (launches) {
+        // launches of the linearization and of the solve over all iterates
+        launches[0] = ba.profiled_launches("ba_lin_kf");
+        launches[1] = ba.profiled_launches("ba_solve");
+        ba.print_profile();
+    }
     slk_droid::clamp_disps(d_d, (int)(N * hw), 0.001f);
     int bad = download(poses, d_p, (size_t)N * 7);
     bad |= download(disps, d_d, (size_t)N * hw);

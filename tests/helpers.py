@@ -56,3 +56,24 @@ class Pins:
         d = self.slk.DeviceArray.from_host(arr)
         self.bufs.append(d)
         return d.ptr
+
+
+def assert_valid_mask(valid, poses, disps, intr, ii, jj, h, w, band=1e-5):
+    """projmap's valid mask (se3.cuh:174: homogeneous Z > 0.25) must match
+    exactly, except for pixels whose Z lies within `band` of 0.25 (where fp32
+    rounding of the projection decides). Z is the camera-j depth of the
+    independent fp64 pinhole model (workloads.project) times frame ii's
+    inverse depth, i.e. the homogeneous Z the kernel tests."""
+    import workloads as wl
+    valid = np.asarray(valid).reshape(len(ii), h * w)
+    _, depth = wl.project(poses, disps, intr, ii, jj, h, w)
+    z = depth * np.asarray(disps, np.float64).reshape(len(poses), h * w)[np.asarray(ii)]
+    want = (z > 0.25).astype(np.float32)
+    near = np.abs(z - 0.25) < band
+    bad = (valid != want) & ~near
+    if bad.any():
+        idx = np.argwhere(bad)[:10].tolist()
+        raise AssertionError(f"valid mask: {int(bad.sum())} entries differ outside the "
+                             f"|Z - 0.25| < {band} band; first (edge, pixel): {idx}")
+    assert np.all((valid == 0.0) | (valid == 1.0))
+    return int(near.sum())

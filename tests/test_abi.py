@@ -44,6 +44,11 @@ def test_argument_errors_need_no_gpu():
     assert lib.slk_create(ctypes.byref(p), 48, 64, 127, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
     assert lib.slk_create(ctypes.byref(p), 4, 64, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
     assert lib.slk_create(None, 48, 64, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    # h*w at 2^21 would overflow the batched path's 32-bit window offsets
+    assert lib.slk_create(ctypes.byref(p), 1024, 2048, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    assert b"2^21" in lib.slk_last_error()
+    assert lib.slk_create(ctypes.byref(p), 2048, 1024, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
+    assert lib.slk_create(ctypes.byref(p), 8, 65537, 128, 48, 4, 3, 0.0625) == slk.SLK_E_ARG
     assert lib.slk_ba_iterate(None, *([None] * 10), 1, 0, 1, 1e-4, 0.1, 0, None) == slk.SLK_E_ARG
     assert lib.slk_corr_sample_level(None, None, None, 1, 2, 4, 4, 4, 4, 16, 1.0, 0,
                                      None) == slk.SLK_E_ARG

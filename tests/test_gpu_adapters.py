@@ -30,7 +30,8 @@ def harness():
     P = ctypes.c_void_p
     I, F = ctypes.c_int, ctypes.c_float
     lib.adapter_corr.argtypes = [P, I, I, I, I, P, P, I, P, P, P]
-    lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I]
+    lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, P]
+    lib.adapter_corrblock.argtypes = [P, P, I, I, I, I, P, P, P, P, I, I, P, P]
     lib.adapter_glue.argtypes = [I, I, I, I, I, I] + [P] * 12 + [I] + [P] * 4 + [P] * 14
     return lib
 
@@ -58,16 +59,48 @@ def test_corr_engine_fp16_window(harness):
     assert_close_rel(single, ref[0], what="build+sample via CorrEngine")
 
 
+def test_corr_block(harness):
+    """CorrBlock (corr.cuh:61-263): build of bn = 3 pairs then sample_single,
+    which reads pair 0's pyramid, at the live scale 1/16; a second build at
+    another size (the context follows the new shape)."""
+    announce("adapters: CorrBlock build + sample_single, two sizes")
+    rng = np.random.default_rng(53)
+    h, w, bn, c = 24, 32, 3, 128
+    f1 = rng.standard_normal((bn, c, h, w), dtype=np.float32)
+    f2 = rng.standard_normal((bn, c, h, w), dtype=np.float32)
+    coords = wl.flow_coords(1, h, w, seed=54)[0]
+    h2, w2 = 12, 20
+    g1 = rng.standard_normal((c, h2, w2), dtype=np.float32)
+    g2 = rng.standard_normal((c, h2, w2), dtype=np.float32)
+    coords2 = wl.flow_coords(1, h2, w2, seed=55)[0]
+    out = np.zeros((196, h * w), np.float32)
+    out2 = np.zeros((196, h2 * w2), np.float32)
+    st = harness.adapter_corrblock(_p(f1), _p(f2), bn, c, h, w, _p(coords), _p(out), _p(g1),
+                                   _p(g2), h2, w2, _p(coords2), _p(out2))
+    assert st == 0
+    fr = np.stack([f1[0], f2[0]])
+    ref = orc.corr_batch(fr, np.array([0], np.int32), np.array([1], np.int32), coords[None],
+                         1.0 / 16.0)[0]
+    assert_close_rel(out, ref, what="CorrBlock pair 0")
+    gr = np.stack([g1, g2])
+    ref2 = orc.corr_batch(gr, np.array([0], np.int32), np.array([1], np.int32), coords2[None],
+                          1.0 / 16.0)[0]
+    assert_close_rel(out2, ref2, what="CorrBlock after resize")
+
+
 @pytest.mark.parametrize("motion_only", [0, 1])
 def test_bundle_adjustment_iterate(harness, motion_only):
     announce(f"adapters: BundleAdjustment motion_only={motion_only}")
     p = wl.ba_problem(n=6, h=12, w=16, seed=52)
     poses, disps = p["poses"].copy(), p["disps"].copy()
     ii, jj = p["ii"].astype(np.int32), p["jj"].astype(np.int32)
+    launches = np.zeros(2, np.int32)
     st = harness.adapter_ba(len(poses), p["h"], p["w"], _p(poses), _p(disps), _p(p["intr"]),
                             _p(p["target"]), _p(p["weight"]), _p(p["eta"]), _p(ii), _p(jj),
-                            len(ii), p["t0"], p["t1"], 1e-4, 0.1, motion_only, 2)
+                            len(ii), p["t0"], p["t1"], 1e-4, 0.1, motion_only, 2, _p(launches))
     assert st == 0
+    # print_profile's totals cover both iterates: one launch per kernel each
+    np.testing.assert_array_equal(launches, [2, 2])
     rp, rd = p["poses"], p["disps"]
     for _ in range(2):
         r = orc.ba_iterate(rp, rd, p["intr"], p["target"], p["weight"], p["eta"], p["ii"],

@@ -134,6 +134,65 @@ def test_not_spd_leaves_state_untouched(slk):
     ctx.close()
 
 
+@pytest.mark.parametrize("P", [11, 15])
+def test_lds_solver_sizes(slk, P):
+    """P = 11 and 15 free poses (n = 66 and 90): the edges of the one-workgroup
+    solve with S in LDS (65,520 B of dynamic LDS at n = 90), one iteration
+    against the oracle, then a second from the updated state."""
+    announce(f"ba lds solver P={P} (n={6 * P})")
+    n = P + 2
+    p = wl.ba_problem(n=n, h=12, w=16, seed=30 + P)
+    dev = Dev(slk, p)
+    ctx = slk.Context(12, 16, max_batch=1, levels=2)
+    poses, disps = p["poses"], p["disps"]
+    for it in range(2):
+        dev.iterate(ctx, 1e-4, 0.1)
+        ref = orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"],
+                             p["ii"], p["jj"], 12, 16, p["t0"], p["t1"], 1e-4, 0.1)
+        assert ref["status"] == 0
+        S, b, dx = ctx.ba_last_system()
+        assert S.shape == (6 * P, 6 * P)
+        assert norm_rel(S, ref["S"]) < 1e-7, it
+        assert norm_rel(b, ref["b"]) < 1e-7, it
+        assert norm_rel(dx, ref["dx"]) < 1e-5, it
+        poses, disps = ref["poses"], ref["disps"]
+        assert_close_rel(dev.poses(), poses, what=f"poses it {it}")
+        assert_close_rel(dev.disps(), disps, what=f"disps it {it}")
+    assert ctx.ba_status() == slk.SLK_OK
+    ctx.close()
+
+
+def test_lds_solver_not_spd_late_pivot(slk):
+    """P = 12 (n = 72, the LDS solve) with every edge that touches frames 12
+    and 13 at zero weight and no damping: the rows of those two poses are
+    zero, so the factorization fails at pivot 60, in a later column block than
+    the first. Reported as SLK_E_NOT_SPD, poses and inverse depths untouched."""
+    announce("ba lds solver P=12 late-pivot not SPD")
+    p = wl.ba_problem(n=14, h=12, w=16, seed=41)
+    dead = (p["ii"] >= 12) | (p["jj"] >= 12)
+    assert dead.any() and not dead.all()
+    p["weight"][dead] = 0.0
+    ref = orc.ba_iterate(p["poses"], p["disps"], p["intr"], p["target"], p["weight"], p["eta"],
+                         p["ii"], p["jj"], 12, 16, p["t0"], p["t1"], 0.0, 0.0)
+    assert ref["status"] != 0
+    dev = Dev(slk, p)
+    ctx = slk.Context(12, 16, max_batch=1, levels=2)
+    dev.iterate(ctx, 0.0, 0.0)
+    assert ctx.ba_status() == slk.SLK_E_NOT_SPD
+    np.testing.assert_array_equal(dev.poses(), p["poses"])
+    np.testing.assert_array_equal(dev.disps(), p["disps"])
+    # the same context then solves a well-posed system of the same size
+    dev.d["weight"].upload(wl.ba_problem(n=14, h=12, w=16, seed=41)["weight"])
+    q = wl.ba_problem(n=14, h=12, w=16, seed=41)
+    dev.iterate(ctx, 1e-4, 0.1)
+    assert ctx.ba_status() == slk.SLK_OK
+    ref = orc.ba_iterate(q["poses"], q["disps"], q["intr"], q["target"], q["weight"], q["eta"],
+                         q["ii"], q["jj"], 12, 16, q["t0"], q["t1"], 1e-4, 0.1)
+    assert_close_rel(dev.poses(), ref["poses"], what="poses after recovery")
+    assert_close_rel(dev.disps(), ref["disps"], what="disps after recovery")
+    ctx.close()
+
+
 def test_large_system_and_plan_cache(slk):
     """30 frames, P = 28 free poses (n = 168, the global-memory solve), then a
     different edge set and back (index structures rebuilt and reused)."""

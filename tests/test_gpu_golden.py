@@ -8,7 +8,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import TOL, Pins, announce, assert_close_rel, gpu_or_fail, norm_rel
+from helpers import TOL, Pins, announce, assert_close_rel, assert_valid_mask, gpu_or_fail, norm_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -62,7 +62,7 @@ def test_se3_fixture(slk):
     slk.check(slk.lib().slk_pose_retr(poses.ptr, D(g["dx"]), int(g["t0"]), int(g["t1"]), None))
     slk.hip().sync()
     assert_close_rel(coords.to_host(), g["coords"], what="projmap")
-    assert np.mean(valid.to_host() == g["valid"]) > 0.999
+    assert_valid_mask(valid.to_host(), g["poses"], g["disps"], g["intr"], g["ii"], g["jj"], h, w)
     assert_close_rel(dist.to_host(), g["dist"], what="frame_distance")
     np.testing.assert_allclose(poses.to_host(), g["poses_retr"], rtol=1e-6, atol=1e-6)
 
