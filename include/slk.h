@@ -127,6 +127,24 @@ int slk_corr_batch_build_and_sample_prepared(slk_ctx* ctx, const int* ii_host,
                                              const int* jj_host, int B, const float* coords,
                                              float* out, hipStream_t stream);
 
+/* No counterpart in the reference. The batched correlation with
+ * device-resident edge indices, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): it takes no context and calls no allocator. Its scratch
+ * (feature slots, tile lists and counters, lookup windows) is one static
+ * 64 MiB device array per GPU, held until the process ends; batches run in
+ * launches of as many edges as fit in it (9 at 48x64, 5 at 54x96). Map sizes
+ * whose one-edge scratch exceeds 64 MiB are rejected with SLK_E_ARG (e.g.
+ * 256x256). Needs C a positive multiple of 16, 8 <= h, w and h*w < 2^21;
+ * fp32 features take the bf16x3 split. Results are bitwise those of
+ * slk_corr_batch_build_and_sample_dev. Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams or threads)
+ * race and must be serialised by the caller. */
+int slk_corr_batch_build_and_sample_dev_noalloc(const void* fmaps, int dtype, long fmap_stride,
+                                                const int* ii_dev, const int* jj_dev, int B,
+                                                const float* coords, float* out, int h, int w,
+                                                int C, float corr_scale, hipStream_t stream);
+
 /* CudaDroid::build_correlation(i, j), main.cu:1500-1526 (and
  * CorrBlock::build for one edge, corr.cuh:84): volume of (f_i, f_j) and its
  * pyramid into the context's persistent single-edge buffers. */

@@ -24,7 +24,9 @@
 //     lookup window at that level, into a compact [HW][levels][8][8] buffer.
 //     The volume and pyramid (~50 MB per 48x64 edge) never reach HBM; the
 //     windows are 1 KB per source pixel.
+#include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "corr_common.hpp"
@@ -985,4 +987,103 @@ extern "C" int slk_coords_hw2_to_2hw(const float* hw2, float* chw, int M, int HW
                        stream, hw2, chw, M, HW);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
+}
+
+// ------------------------------------------------ no-allocation batched path
+// slk_corr_batch_build_and_sample_dev_noalloc runs the batched path with its
+// scratch (feature slots, tile lists and counters, lookup windows) carved
+// from one file-scope device array instead of a context's buffers. The array
+// is a host-side stand-in in host code: its device address on the current
+// device comes from hipGetSymbolAddress, taken once per device on the first
+// call there, and only that address is handed to kernels.
+namespace {
+constexpr size_t kNoAllocBytes = size_t(64) << 20;
+constexpr int kNoAllocDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+std::mutex g_noalloc_mu;
+unsigned char* g_noalloc_ptr[kNoAllocDevices];
+int g_noalloc_cus[kNoAllocDevices];
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Device address of `scratch` and the CU count of the current device.
+int noalloc_scratch(unsigned char** ptr, int* cus, int* device) {
+    int dev = 0;
+    SLK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kNoAllocDevices)
+        return fail(SLK_E_ARG, "corr_noalloc: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        SLK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        int n = 0;
+        SLK_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        g_noalloc_cus[dev] = n;
+        g_noalloc_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    *ptr = g_noalloc_ptr[dev];
+    *cus = g_noalloc_cus[dev];
+    *device = dev;
+    return SLK_OK;
+}
+}  // namespace
+
+extern "C" int slk_corr_batch_build_and_sample_dev_noalloc(
+    const void* fmaps, int dtype, long fmap_stride, const int* ii_dev, const int* jj_dev, int B,
+    const float* coords, float* out, int h, int w, int C, float corr_scale,
+    hipStream_t stream) {
+    if (B < 0 || (B > 0 && (!ii_dev || !jj_dev)))
+        return fail(SLK_E_ARG, "corr_noalloc: null indices or B < 0");
+    if (h < 8 || w < 8 || h > 65536 || w > 65536 || (long)h * w >= (1L << 21))
+        return fail(SLK_E_ARG, "corr_noalloc: need 8 <= h, w <= 2^16 and h*w < 2^21");
+    if (C < 16 || C % 16 != 0)
+        return fail(SLK_E_ARG, "corr_noalloc: C must be a positive multiple of 16");
+    if (dtype != SLK_F32 && dtype != SLK_F16) return fail(SLK_E_ARG, "corr_noalloc: bad dtype");
+    slk_ctx c;  // a stack context over the static scratch: nothing here allocates
+    c.h = h;
+    c.w = w;
+    c.HW = h * w;
+    c.C = C;
+    c.levels = kMaxLevels;
+    c.radius = 3;
+    c.alpha = corr_scale;
+    c.corr_prec = SLK_PREC_BF16X3;
+    for (int l = 0; l < kMaxLevels; l++) {
+        c.lh[l] = h >> l;
+        c.lw[l] = w >> l;
+    }
+    size_t slot = 0, tiles = 0, ctr = 0;
+    corr_split_footprint(&c, &slot, &tiles, &ctr);
+    const size_t win = (size_t)c.HW * kMaxLevels * kWinCells * sizeof(float);
+    const size_t per_edge = 2 * align256(slot) + align256(tiles) + align256(win);
+    const size_t fixed = align256(ctr);
+    const size_t fit = per_edge + fixed <= kNoAllocBytes ? (kNoAllocBytes - fixed) / per_edge : 0;
+    if (fit < 1)
+        return fail(SLK_E_ARG, "corr_noalloc: one edge of this map size needs more than the "
+                               "64 MiB static scratch");
+    if (B == 0) return SLK_OK;
+    unsigned char* base = nullptr;
+    int cus = 0, dev = 0;
+    SLK_TRY(noalloc_scratch(&base, &cus, &dev));
+    c.device = dev;
+    const int n = (int)std::min<size_t>(fit, kMaxEdgesPerLaunch);
+    c.max_batch = n;
+    size_t at = 0;
+    auto carve = [&](DevBuf& b, size_t bytes) {
+        b.ptr = base + at;
+        b.bytes = bytes;
+        at += align256(bytes);
+    };
+    carve(c.split_feat, 2 * (size_t)n * align256(slot));
+    carve(c.tile_list, (size_t)n * tiles);
+    carve(c.tile_ctr, ctr);
+    carve(c.batch_win, (size_t)n * win);
+    if (at > kNoAllocBytes) return fail(SLK_E_ARG, "corr_noalloc: scratch layout overflow");
+    c.ws_grid = corr_split_grid(cus);
+    return corr_batch_impl(&c, fmaps, dtype, fmap_stride, nullptr, nullptr, ii_dev, jj_dev, B,
+                           coords, out, stream);
 }

@@ -749,6 +749,18 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
 
 bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
 
+void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
+                          size_t* ctr_bytes) {
+    const Geom g = make_geom(ctx);
+    const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
+    const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
+    *slot_bytes = 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short);
+    *tiles_per_edge = mtiles * ntiles * sizeof(int);
+    *ctr_bytes = kCtrInts * sizeof(int);
+}
+
+int corr_split_grid(int cus) { return std::max(8, cus / 8 * 8) * 2; }
+
 int corr_split_alloc(slk_ctx* ctx) {
     if (!corr_split_supported(ctx)) return SLK_OK;
     const Geom g = make_geom(ctx);
@@ -764,7 +776,7 @@ int corr_split_alloc(slk_ctx* ctx) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) !=
         hipSuccess)
         return fail(SLK_E_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
-    ctx->ws_grid = std::max(8, cus / 8 * 8) * 2;
+    ctx->ws_grid = corr_split_grid(cus);
     return SLK_OK;
 }
 

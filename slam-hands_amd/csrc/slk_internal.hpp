@@ -143,6 +143,12 @@ int corr_alloc(slk_ctx* ctx);
 // corr_split.hip
 bool corr_split_supported(const slk_ctx* ctx);
 int corr_split_alloc(slk_ctx* ctx);
+// bytes of one feature slot (two per edge of a launch), of one edge's tile
+// list, and of the launch's tile counters
+void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
+                          size_t* ctr_bytes);
+// workgroups of the batched correlation kernel on a part with `cus` CUs
+int corr_split_grid(int cus);
 int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
                        const int* ii_host, const int* jj_host, const int* ii_dev,
                        const int* jj_dev, int n, const float* coords, float* win, int slot0,

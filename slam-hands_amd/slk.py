@@ -29,7 +29,7 @@ EXPORTS = [
     "slk_create", "slk_destroy", "slk_last_error", "slk_profile_enable", "slk_profile_kernel",
     "slk_set_corr_precision",
     "slk_corr_batch_build_and_sample", "slk_corr_batch_build_and_sample_dev",
-    "slk_corr_prepare_frames", "slk_corr_batch_build_and_sample_prepared",
+    "slk_corr_batch_build_and_sample_dev_noalloc", "slk_corr_prepare_frames", "slk_corr_batch_build_and_sample_prepared",
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
     "slk_projmap", "slk_pose_retr", "slk_disp_retr", "slk_frame_distance", "slk_clamp_disps",
@@ -81,6 +81,8 @@ def lib():
             "slk_set_corr_precision": [P, I],
             "slk_corr_batch_build_and_sample": [P, P, I, L, P, P, I, P, P, P],
             "slk_corr_batch_build_and_sample_dev": [P, P, I, L, P, P, I, P, P, P],
+            "slk_corr_batch_build_and_sample_dev_noalloc": [P, I, L, P, P, I, P, P, I, I, I,
+                                                            F, P],
             "slk_corr_prepare_frames": [P, P, I, L, I, P],
             "slk_corr_batch_build_and_sample_prepared": [P, P, P, I, P, P, P],
             "slk_corr_build": [P, P, P, I, P],
