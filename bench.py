@@ -16,8 +16,9 @@ Printed: one JSON line. `value` is edges/s of the full step (48 edges per
 step); corr-only edges/s and BA-only iterations/s are timed separately in the
 same run. `roofline` is for the dominant kernel (the correlation GEMM with its
 pyramid epilogue), its average launch duration measured with hipEvents on the
-launch stream. `cpu_baseline` times the CPU oracle (oracle/, a C port with
-OpenMP) on a bounded sample of the same workload.
+launch stream. `cpu_baseline` times the path's PyTorch-CPU equivalents
+(oracle/torch_baseline.py, in a child process on the host's cores) on a
+bounded sample of the same workload, with the C oracle beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
@@ -764,10 +765,43 @@ def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
 
 
 def cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, nedges):
+    """The CPU baseline: the path's PyTorch-CPU equivalents (oracle/
+    torch_baseline.py: torch.bmm fp32 correlation, F.avg_pool2d pyramid, an
+    8x8 gather lookup, float64 einsum / index_add_ / Cholesky BA; checked
+    against the C oracle by tests/test_torch_baseline.py), timed in a child
+    process on this host's cores with CPU tensors only: the median of 5
+    repetitions of `nedges` of the window's edges and its BA iterations,
+    scaled to edges/s of the step. The C oracle (C + OpenMP, fp64
+    accumulation) is timed beside it as a second, labelled figure; it alone is
+    reported if the child cannot run torch."""
+    import subprocess
+    B = len(ii)
+    n, C, h, w = fm.shape
+    sample = (f"{nedges}/{B} edges (corr + pyramid + lookup, 8 edges per bmm) + {iters} BA "
+              f"iterations on the full {n}-frame window, median of 5 after a warm-up, scaled "
+              f"to the {B}-edge + {iters}-iteration step")
+    oracle_fig = cpu_baseline_oracle(fm, ii, jj, coords, p, iters, lm, ep, min(nedges, 8))
+    cmd = [sys.executable, os.path.join(ROOT, "oracle", "torch_baseline.py"), "--frames",
+           str(n), "--h", str(h), "--w", str(w), "--edges", str(B), "--sample-edges",
+           str(nedges), "--iters", str(iters), "--reps", "5"]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=600, check=True)
+        t = json.loads(r.stdout.strip().splitlines()[-1])
+    except (subprocess.SubprocessError, ValueError, IndexError) as exc:
+        out = dict(oracle_fig)
+        out["note"] = f"PyTorch-CPU baseline unavailable ({type(exc).__name__}); C oracle only"
+        return out
+    return {"value": round(t["edges_per_s"], 2), "unit": "edges/s", "cores": t["threads"],
+            "kind": "port", "impl": "pytorch-cpu", "torch": t["torch"],
+            "os_cpu_count": t["os_cpu_count"], "affinity_cpus": t["affinity_cpus"],
+            "sample": sample, "corr_s_per_edge": round(t["corr_s_per_edge"], 5),
+            "ba_s_per_iter": round(t["ba_s_per_iter"], 5), "c_oracle": oracle_fig}
+
+
+def cpu_baseline_oracle(fm, ii, jj, coords, p, iters, lm, ep, nedges):
     """The CPU oracle (oracle/liboracle.so, C + OpenMP, fp64 accumulation)
-    on a bounded sample: correlation+lookup of `nedges` of the 48 edges (all
-    of them by default) and the step's BA iterations on the full window,
-    scaled to the step's edges/s (~10 s of CPU work on 8 cores)."""
+    on a bounded sample: correlation+lookup of `nedges` edges and the step's
+    BA iterations on the full window, scaled to the step's edges/s."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     orc.lib()
@@ -784,9 +818,10 @@ def cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, nedges):
     t_ba = (time.perf_counter() - t0) / iters
     step_s = B * t_corr + iters * t_ba
     return {"value": round(B / step_s, 2), "unit": "edges/s", "cores": orc.num_threads(),
-            "kind": "port",
-            "sample": f"oracle corr+pyramid+lookup of {nedges}/{B} edges + {iters} BA iterations "
-                      f"(full window), scaled to the {B}-edge + {iters}-iteration step",
+            "kind": "port", "impl": "C oracle (OpenMP, fp64 accumulation)",
+            "sample": f"oracle corr+pyramid+lookup of {nedges}/{B} edges + {iters} BA "
+                      f"iterations (full window), scaled to the {B}-edge + {iters}-iteration "
+                      "step",
             "corr_s_per_edge": round(t_corr, 4), "ba_s_per_iter": round(t_ba, 4)}
 
 

@@ -14,10 +14,13 @@ def assert_close_rel(got, ref, tol=TOL, what=""):
     assert got.shape == ref.shape, (what, got.shape, ref.shape)
     rms = np.sqrt(np.mean(ref * ref)) if ref.size else 0.0
     bound = tol * np.maximum(np.abs(ref), rms) + 1e-30
-    err = np.abs(got - ref)
-    bad = err > bound
+    with np.errstate(invalid="ignore"):
+        err = np.abs(got - ref)
+        same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+        bad = ~same & ~(err <= bound)  # a NaN where the reference is finite fails
     if bad.any():
-        i = np.unravel_index(np.argmax(err / bound), err.shape)
+        i = np.unravel_index(np.argmax(np.where(bad, np.nan_to_num(err / bound, nan=np.inf),
+                                                -1.0)), err.shape)
         raise AssertionError(f"{what}: {bad.sum()} / {bad.size} outside tol {tol}; worst at {i}: "
                              f"got {got[i]!r} ref {ref[i]!r} (rms {rms:.3g})")
 
