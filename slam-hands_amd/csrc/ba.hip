@@ -7,23 +7,25 @@
 // orchestration BundleAdjustment::iterate) with se3.cuh for the geometry.
 //
 // Iteration = 5 kernels on one stream:
-//   k_ba_lin_kf   grid (pixel chunk, keyframe): every edge whose depth owner
+//   k_ba_lin_*    grid (pixel chunk, keyframe): every edge whose depth owner
 //                 (ii) is that keyframe is linearized for the chunk's pixels in
-//                 fp64. Per-edge 12x12 Hessian + gradients are reduced per
-//                 workgroup; the depth terms (C, w), Q = 1/(C + 0.2 eta + 1e-7)
-//                 and the E rows of the keyframe are accumulated in place, so
-//                 the per-edge Eii/Eij/Cii/bz arrays of the reference never
-//                 exist.
-//   k_ba_schur    grid (pixel chunk, item): E_r1 Q E_r2^T for the upper pairs
-//                 of E rows sharing a keyframe, and E_r Q w per row.
+//                 fp64. Per edge and chunk only Hjj (21) and vj (6) are
+//                 reduced, since Ji = -Adj(Tij) Jj gives Hii = Adj Hjj Adj^T,
+//                 Hij = -Adj Hjj and vi = -Adj vj; the depth terms (C, w),
+//                 Q = 1/(C + 0.2 eta + 1e-7) and the E rows of the keyframe
+//                 are accumulated in place, so the per-edge Eii/Eij/Cii/bz
+//                 arrays of the reference never exist.
+//   k_ba_schur    one workgroup per item over all pixels: E_r1 Q E_r2^T for
+//                 the upper pairs of E rows sharing a keyframe, E_r Q w per
+//                 row; then one workgroup per edge sums its chunk partials and
+//                 expands them to the four blocks with the edge's Adj.
 //   k_ba_assemble one workgroup per 6x6 block of S and per 6 entries of b:
-//                 sums the chunk partials of the contributions listed for the
-//                 block (list built on the host; no atomics, fixed order),
-//                 then S_ii += ep + lm*S_ii.
+//                 sums the totals listed for the block (lists built on the
+//                 host; fixed order, no atomics), then S_ii += ep + lm*S_ii.
 //   k_ba_solve_*  fp64 Cholesky, solve, dx rounded to fp32, retraction of the
 //                 poses [t0, t1): one wavefront with S in registers up to 10
-//                 free poses, else one workgroup (blocked, S in LDS up to
-//                 90x90, else in global memory).
+//                 free poses, one workgroup blocked in LDS up to 84x84, else
+//                 blocked over many workgroups in global memory.
 //   k_ba_backsub  grid (pixel chunk, keyframe): dz = Q (w - E^T dx),
 //                 disps += dz.
 // Host work per iteration is limited to comparing the edge list with the
@@ -43,11 +45,18 @@ namespace {
 
 constexpr int kLinWG = 256;
 constexpr int kLinPx = 256;  // pixels per k_ba_lin_kf workgroup (1 per thread)
-constexpr int kLinPPT = kLinPx / kLinWG;
 constexpr int kSchWG = 256;
-constexpr int kSchPx = 512;
 constexpr int kNH = 90;      // 78 upper-triangle Hessian entries + vi(6) + vj(6)
-constexpr int kSmallN = 90;  // workgroup LDS solve up to 90x90 fp64 (64800 bytes)
+// Per (edge, pixel chunk) the linearization reduces only Hjj = sum w Jj Jj^T
+// (21 upper entries) and vj = sum w r Jj (6): Ji = -Adj(Tij) Jj per pixel
+// (ba.cuh:139-140, 167-168) with one 6x6 matrix Adj per edge, so
+// Hii = Adj Hjj Adj^T, Hij = -Adj Hjj, Hji = Hij^T and vi = -Adj vj follow
+// from the edge totals.
+constexpr int kNJ = 27;
+// per-edge totals: Hii (36), Hij (36), Hjj (36), vi (6), vj (6)
+constexpr int kNT = 120;
+constexpr int kTotHii = 0, kTotHij = 36, kTotHjj = 72, kTotVi = 108, kTotVj = 114;
+constexpr int kSmallN = 84;  // one-workgroup LDS solve up to 84x84 (85 x 84 fp64, 57 KB)
 constexpr double kMinDepth = 0.25;  // se3.cuh:6
 
 __host__ __device__ __forceinline__ int tri(int n, int m) { return n * (n + 1) / 2 + m; }
@@ -79,10 +88,11 @@ __host__ __device__ __forceinline__ int code_type(int c) { return (int)((unsigne
 __host__ __device__ __forceinline__ int code_val(int c) { return c & 0x3fffffff; }
 
 struct Lin {
-    double Ji[2][6], Jj[2][6], Jz[2], w[2], r[2];
+    double Jj[2][6], Jz[2], w[2], r[2];
 };
 
-// Per-pixel linearization of one edge (ba.cuh:104-189), fp64.
+// Per-pixel linearization of one edge (ba.cuh:104-189), fp64, without Ji
+// (= -Adj Jj, applied per edge or per E row by the callers).
 __device__ __forceinline__ void lin_pixel(const double* tij, const double* qij, double fx,
                                           double fy, double cx, double cy, int k, int W,
                                           double disp, double tgu, double tgv, double wtu,
@@ -111,7 +121,6 @@ __device__ __forceinline__ void lin_pixel(const double* tij, const double* qij, 
     Jj[4] = fx * (1.0 + x * x * d2);
     Jj[5] = fx * (-y * d);
     L.Jz[0] = fx * (tij[0] * d - tij[2] * (x * d2));
-    adj_se3(tij, qij, Jj, L.Ji[0]);
     Jj = L.Jj[1];
     Jj[0] = 0.0;
     Jj[1] = fy * (h * d);
@@ -120,35 +129,23 @@ __device__ __forceinline__ void lin_pixel(const double* tij, const double* qij, 
     Jj[4] = fy * (x * y * d2);
     Jj[5] = fy * (x * d);
     L.Jz[1] = fy * (tij[1] * d - tij[2] * (y * d2));
-    adj_se3(tij, qij, Jj, L.Ji[1]);
-#pragma unroll
-    for (int n = 0; n < 6; n++) {
-        L.Ji[0][n] = -L.Ji[0][n];
-        L.Ji[1][n] = -L.Ji[1][n];
-    }
 }
 
-// acc[0..77] += weff J J^T (upper triangle of [Ji, Jj]), acc[78..89] += weff r J
-__device__ __forceinline__ void accum_hessian(const Lin& L, bool stereo, double (&acc)[kNH]) {
+// acc[0..20] += weff Jj Jj^T (upper triangle), acc[21..26] += weff r Jj
+__device__ __forceinline__ void accum_hjj(const Lin& L, bool stereo, double (&acc)[kNJ]) {
 #pragma unroll
     for (int row = 0; row < 2; row++) {
         const double we = stereo ? 0.0 : L.w[row];
-        double Jx[12];
+        const double* J = L.Jj[row];
 #pragma unroll
         for (int n = 0; n < 6; n++) {
-            Jx[n] = L.Ji[row][n];
-            Jx[6 + n] = L.Jj[row][n];
-        }
-        int l = 0;
+            const double wn = we * J[n];
 #pragma unroll
-        for (int n = 0; n < 12; n++) {
-            const double wn = we * Jx[n];
-#pragma unroll
-            for (int m = 0; m <= n; m++) acc[l++] += wn * Jx[m];
+            for (int m = 0; m <= n; m++) acc[tri(n, m)] += wn * J[m];
         }
         const double wr = we * L.r[row];
 #pragma unroll
-        for (int n = 0; n < 12; n++) acc[78 + n] += wr * Jx[n];
+        for (int n = 0; n < 6; n++) acc[21 + n] += wr * J[n];
     }
 }
 
@@ -170,44 +167,89 @@ __device__ __forceinline__ void edge_rel(const float* poses, int ix, int jx, dou
     }
 }
 
+// Totals of edge e over the nch pixel chunks (summed in chunk order),
+// expanded to the four Hessian blocks and both gradients of ba.cuh:198-220
+// with the edge's Adj: etot[e] = Hii, Hij, Hjj, vi, vj. One wave; `sh` holds
+// 27 + 36 + 36 doubles.
+__device__ void edge_totals(int e, const float* __restrict__ poses, const int* __restrict__ ii,
+                            const int* __restrict__ jj, const double* __restrict__ hpart,
+                            double* __restrict__ etot, int nch, double* sh) {
+    const int lane = threadIdx.x & 63;
+    double* tot = sh;
+    double* adj = tot + kNJ;
+    double* ah = adj + 36;
+    if (lane < kNJ) {
+        const double* hp = hpart + (size_t)e * nch * kNJ + lane;
+        double t = 0.0;
+        for (int c = 0; c < nch; c++) t += hp[(size_t)c * kNJ];
+        tot[lane] = t;
+    }
+    double tij[3], qij[4];
+    edge_rel(poses, ii[e], jj[e], tij, qij);
+    // Adj column by column: adj_se3 of the unit vectors (se3.cuh:28-41)
+#pragma unroll 1
+    for (int c = 0; c < 6; c++) {
+        double u[6], y[6];
+        for (int m = 0; m < 6; m++) u[m] = m == c ? 1.0 : 0.0;
+        adj_se3(tij, qij, u, y);
+#pragma unroll
+        for (int r = 0; r < 6; r++)
+            if (lane == r) adj[r * 6 + c] = y[r];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int r = lane / 6, c = lane - (lane / 6) * 6;
+    double* et = etot + (size_t)e * kNT;
+    if (lane < 36) {
+        double t = 0.0;  // (Adj Hjj)[r][c]
+#pragma unroll
+        for (int k = 0; k < 6; k++) t += adj[r * 6 + k] * tot[tri(max(k, c), min(k, c))];
+        ah[lane] = t;
+        et[kTotHij + lane] = -t;
+        et[kTotHjj + lane] = tot[tri(max(r, c), min(r, c))];
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < 36) {
+        double t = 0.0;  // (Adj Hjj Adj^T)[r][c]
+#pragma unroll
+        for (int k = 0; k < 6; k++) t += ah[r * 6 + k] * adj[c * 6 + k];
+        et[kTotHii + lane] = t;
+    }
+    if (lane < 6) {
+        double t = 0.0;
+#pragma unroll
+        for (int k = 0; k < 6; k++) t += adj[lane * 6 + k] * tot[21 + k];
+        et[kTotVi + lane] = -t;
+        et[kTotVj + lane] = tot[21 + lane];
+    }
+}
+
 // ------------------------------------------------------- k_ba_lin_kf ----
+// Edge-serial linearization (a keyframe with two edges to one free pose):
+// grid (pixel chunk, keyframe), the workgroup walks the keyframe's edges in
+// order, accumulating E rows in place.
 __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
     PlanDev plan, const float* __restrict__ target, const float* __restrict__ weight,
     const float* __restrict__ poses, const float* __restrict__ disps,
     const float* __restrict__ intr, const int* __restrict__ ii, const int* __restrict__ jj,
     const float* __restrict__ eta, double* __restrict__ hpart, double* __restrict__ E,
     double* __restrict__ Qo, double* __restrict__ Wo, int HW, int W, int nch, int motion_only) {
-    __shared__ double red[kNH * (kLinWG / 64)];
+    __shared__ double red[kNJ * (kLinWG / 64)];
     __shared__ double rel[7];
     const int chunk = blockIdx.x;
     const int kc = blockIdx.y;
     const int kf = plan.kf_list[kc];
     const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
-    int kpx[kLinPPT];
-    bool vpx[kLinPPT];
-#pragma unroll
-    for (int s = 0; s < kLinPPT; s++) {
-        kpx[s] = chunk * kLinPx + s * kLinWG + threadIdx.x;
-        vpx[s] = kpx[s] < HW;
-    }
+    const int k = chunk * kLinPx + threadIdx.x;
+    const bool vpx = k < HW;
     const int r0 = plan.kf_rptr[kc], r1 = plan.kf_rptr[kc + 1];
-    if (!motion_only) {
+    if (!motion_only && vpx) {
         for (int r = r0; r < r1; r++) {
             double* er = E + (size_t)plan.kf_rows[r] * 6 * HW;
-#pragma unroll
-            for (int s = 0; s < kLinPPT; s++)
-                if (vpx[s])
-                    for (int n = 0; n < 6; n++) er[(size_t)n * HW + kpx[s]] = 0.0;
+            for (int n = 0; n < 6; n++) er[(size_t)n * HW + k] = 0.0;
         }
     }
-    double Cacc[kLinPPT], Wacc[kLinPPT], dsp[kLinPPT];
-#pragma unroll
-    for (int s = 0; s < kLinPPT; s++) {
-        Cacc[s] = 0.0;
-        Wacc[s] = 0.0;
-        dsp[s] = vpx[s] ? (double)disps[(size_t)kf * HW + kpx[s]] : 1.0;
-    }
-
+    double Cacc = 0.0, Wacc = 0.0;
+    const double dsp = vpx ? (double)disps[(size_t)kf * HW + k] : 1.0;
     const int e0 = plan.kf_eptr[kc], e1 = plan.kf_eptr[kc + 1];
     for (int ei = e0; ei < e1; ei++) {
         const int e = plan.kf_eidx[ei];
@@ -219,64 +261,59 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
         double tij[3] = {rel[0], rel[1], rel[2]};
         double qij[4] = {rel[3], rel[4], rel[5], rel[6]};
         const int ri = plan.edge_ri[e], rj = plan.edge_rj[e];
-        double acc[kNH];
+        double acc[kNJ];
 #pragma unroll
-        for (int n = 0; n < kNH; n++) acc[n] = 0.0;
-#pragma unroll
-        for (int s = 0; s < kLinPPT; s++) {
-            if (!vpx[s]) continue;
-            const int k = kpx[s];
+        for (int n = 0; n < kNJ; n++) acc[n] = 0.0;
+        if (vpx) {
             const size_t base = (size_t)e * 2 * HW + k;
             Lin L;
-            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)target[base],
+            lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp, (double)target[base],
                       (double)target[base + HW], (double)weight[base], (double)weight[base + HW],
                       L);
-            accum_hessian(L, stereo, acc);
+            accum_hjj(L, stereo, acc);
             if (!motion_only) {
-                Cacc[s] += L.w[0] * L.Jz[0] * L.Jz[0];
-                Cacc[s] += L.w[1] * L.Jz[1] * L.Jz[1];
-                Wacc[s] += L.w[0] * L.r[0] * L.Jz[0];
-                Wacc[s] += L.w[1] * L.r[1] * L.Jz[1];
+                Cacc += L.w[0] * L.Jz[0] * L.Jz[0];
+                Cacc += L.w[1] * L.Jz[1] * L.Jz[1];
+                Wacc += L.w[0] * L.r[0] * L.Jz[0];
+                Wacc += L.w[1] * L.r[1] * L.Jz[1];
                 const double a0 = stereo ? 0.0 : L.w[0] * L.Jz[0];
                 const double a1 = stereo ? 0.0 : L.w[1] * L.Jz[1];
-                if (ri >= 0) {
+                double g[6];
+#pragma unroll
+                for (int n = 0; n < 6; n++) g[n] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                if (ri >= 0) {  // Ji-row contribution -Adj g (ba.cuh:139-140)
+                    double gi[6];
+                    adj_se3(tij, qij, g, gi);
                     double* er = E + (size_t)ri * 6 * HW + k;
 #pragma unroll
-                    for (int n = 0; n < 6; n++)
-                        er[(size_t)n * HW] += a0 * L.Ji[0][n] + a1 * L.Ji[1][n];
+                    for (int n = 0; n < 6; n++) er[(size_t)n * HW] -= gi[n];
                 }
                 if (rj >= 0) {
                     double* er = E + (size_t)rj * 6 * HW + k;
 #pragma unroll
-                    for (int n = 0; n < 6; n++)
-                        er[(size_t)n * HW] += a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                    for (int n = 0; n < 6; n++) er[(size_t)n * HW] += g[n];
                 }
             }
         }
-        block_sum_to(acc, red, hpart + ((size_t)e * nch + chunk) * kNH);
+        block_sum_to(acc, red, hpart + ((size_t)e * nch + chunk) * kNJ);
     }
-    if (!motion_only) {
-#pragma unroll
-        for (int s = 0; s < kLinPPT; s++) {
-            if (!vpx[s]) continue;
-            const int k = kpx[s];
-            // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
-            const double c = Cacc[s] + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7;
-            Qo[(size_t)kc * HW + k] = 1.0 / c;
-            Wo[(size_t)kc * HW + k] = Wacc[s];
-        }
+    if (!motion_only && vpx) {
+        // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
+        const double c = Cacc + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7;
+        Qo[(size_t)kc * HW + k] = 1.0 / c;
+        Wo[(size_t)kc * HW + k] = Wacc;
     }
 }
 
 // Same linearization with one wave per edge: a workgroup (pixel chunk,
 // keyframe) gives its keyframe's edges to its four waves in turn, each wave
 // covering all kLinPx pixels (kLinPx / 64 per lane), so no edge waits for
-// another and the per-edge Hessian reduction stays inside one wave. The
-// cross-edge sums (the E row of the keyframe's own pose, and C, w per pixel)
-// go to per-wave LDS slices, added in wave order at the end; the E row of an
-// edge's other pose is stored directly, which needs that row to be the
-// edge's alone (no two edges of a keyframe share jj; the host checks this
-// and otherwise runs k_ba_lin_kf).
+// another and the per-edge reduction stays inside one wave. The cross-edge
+// sums (the E row of the keyframe's own pose, and C, w per pixel) go to
+// per-wave LDS slices, added in wave order at the end; the E row of an edge's
+// other pose is stored directly, which needs that row to be the edge's alone
+// (no two edges of a keyframe share jj; the host checks this and otherwise
+// runs k_ba_lin_kf).
 constexpr int kLinWaves = kLinWG / 64;
 constexpr int kLinPPL = kLinPx / 64;  // pixels per lane
 __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
@@ -327,9 +364,9 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
             wtu[s] = weight[base];
             wtv[s] = weight[base + HW];
         }
-        double acc[kNH];
+        double acc[kNJ];
 #pragma unroll
-        for (int n = 0; n < kNH; n++) acc[n] = 0.0;
+        for (int n = 0; n < kNJ; n++) acc[n] = 0.0;
 #pragma unroll
         for (int s = 0; s < kLinPPL; s++) {
             if (!vpx[s]) continue;
@@ -337,69 +374,88 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
             Lin L;
             lin_pixel(tij, qij, fx, fy, cx, cy, k, W, dsp[s], (double)tgu[s], (double)tgv[s],
                       (double)wtu[s], (double)wtv[s], L);
-            accum_hessian(L, stereo, acc);
+            accum_hjj(L, stereo, acc);
             if (!motion_only) {
                 cw_s[wave][0][px] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
                 cw_s[wave][1][px] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
                 if (!stereo) {  // a stereo edge adds nothing to E
                     const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
-                    if (ri >= 0) {
+                    double g[6];
 #pragma unroll
-                        for (int n = 0; n < 6; n++)
-                            eri_s[wave][n][px] += a0 * L.Ji[0][n] + a1 * L.Ji[1][n];
+                    for (int n = 0; n < 6; n++) g[n] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                    if (ri >= 0) {  // Ji-row contribution -Adj g (ba.cuh:139-140)
+                        double gi[6];
+                        adj_se3(tij, qij, g, gi);
+#pragma unroll
+                        for (int n = 0; n < 6; n++) eri_s[wave][n][px] -= gi[n];
                     }
                     if (rj >= 0) {
                         double* er = E + (size_t)rj * 6 * HW + k;
 #pragma unroll
-                        for (int n = 0; n < 6; n++)
-                            er[(size_t)n * HW] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                        for (int n = 0; n < 6; n++) er[(size_t)n * HW] = g[n];
                     }
                 }
             }
         }
         int rbase, rvalid;
         wave_reduce_scatter(acc, lane, rbase, rvalid);
-        double* hp = hpart + ((size_t)e * nch + chunk) * kNH;
+        double* hp = hpart + ((size_t)e * nch + chunk) * kNJ;
 #pragma unroll
-        for (int q = 0; q < RsCounts<kNH>::c6; q++)
+        for (int q = 0; q < RsCounts<kNJ>::c6; q++)
             if (q < rvalid) hp[rbase + q] = acc[q];
     }
-    if (motion_only) return;
     __syncthreads();
-    // one pixel per thread: the per-wave slices in wave order
-    const int px = threadIdx.x, k = chunk * kLinPx + px;
-    if (k >= HW) return;
-    double c = 0.0, w = 0.0;
+    if (!motion_only) {
+        // one pixel per thread: the per-wave slices in wave order
+        const int px = threadIdx.x, k = chunk * kLinPx + px;
+        if (k < HW) {
+            double c = 0.0, w = 0.0;
 #pragma unroll
-    for (int v = 0; v < kLinWaves; v++) {
-        c += cw_s[v][0][px];
-        w += cw_s[v][1][px];
-    }
-    // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
-    Qo[(size_t)kc * HW + k] = 1.0 / (c + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7);
-    Wo[(size_t)kc * HW + k] = w;
-    const int ri = e1 > e0 ? plan.edge_ri[plan.kf_eidx[e0]] : -1;  // the keyframe's own pose
-    if (ri >= 0) {
-        double* er = E + (size_t)ri * 6 * HW + k;
+            for (int v = 0; v < kLinWaves; v++) {
+                c += cw_s[v][0][px];
+                w += cw_s[v][1][px];
+            }
+            // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
+            Qo[(size_t)kc * HW + k] = 1.0 / (c + 0.2 * (double)eta[(size_t)kf * HW + k] + 1e-7);
+            Wo[(size_t)kc * HW + k] = w;
+            // the keyframe's own pose row
+            const int ri = e1 > e0 ? plan.edge_ri[plan.kf_eidx[e0]] : -1;
+            if (ri >= 0) {
+                double* er = E + (size_t)ri * 6 * HW + k;
 #pragma unroll
-        for (int n = 0; n < 6; n++) {
-            double t = 0.0;
+                for (int n = 0; n < 6; n++) {
+                    double t = 0.0;
 #pragma unroll
-            for (int v = 0; v < kLinWaves; v++) t += eri_s[v][n][px];
-            er[(size_t)n * HW] = t;
+                    for (int v = 0; v < kLinWaves; v++) t += eri_s[v][n][px];
+                    er[(size_t)n * HW] = t;
+                }
+            }
         }
     }
 }
 
 // -------------------------------------------------------- k_ba_schur ----
+// One workgroup per item over all pixels: E_r1 Q E_r2^T for an upper pair of
+// E rows sharing a keyframe (EEt6x6_kernel, ba.cuh:303-342), or E_r Q w for a
+// row (Ev6x1_kernel, ba.cuh:346-372); the 36 (or 6) totals go to stot[item].
+// Workgroups past the N_items Schur items each form one edge's totals
+// (edge_totals, wave 0), which need only the linearization's partials.
 __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double* __restrict__ E,
                                                      const double* __restrict__ Q,
                                                      const double* __restrict__ Wv,
-                                                     double* __restrict__ spart, int HW,
-                                                     int nchS, int N_pu) {
+                                                     double* __restrict__ stot, int HW,
+                                                     int N_pu, int N_items,
+                                                     const float* __restrict__ poses,
+                                                     const int* __restrict__ ii,
+                                                     const int* __restrict__ jj,
+                                                     const double* __restrict__ hpart,
+                                                     double* __restrict__ etot, int nch) {
     __shared__ double red[36 * (kSchWG / 64)];
-    const int chunk = blockIdx.x;
-    const int item = blockIdx.y;
+    const int item = blockIdx.x;
+    if (item >= N_items) {
+        if (threadIdx.x < 64) edge_totals(item - N_items, poses, ii, jj, hpart, etot, nch, red);
+        return;
+    }
     double acc[36];
 #pragma unroll
     for (int n = 0; n < 36; n++) acc[n] = 0.0;
@@ -408,9 +464,9 @@ __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double*
         const int kc = plan.pairs[item * 3 + 2];
         const double* e1 = E + (size_t)r1 * 6 * HW;
         const double* e2 = E + (size_t)r2 * 6 * HW;
-        for (int k = chunk * kSchPx + threadIdx.x; k < min(HW, (chunk + 1) * kSchPx);
-             k += kSchWG) {
-            const double q = Q[(size_t)kc * HW + k];
+        const double* qk = Q + (size_t)kc * HW;
+        for (int k = threadIdx.x; k < HW; k += kSchWG) {
+            const double q = qk[k];
             double a[6], b[6];
 #pragma unroll
             for (int n = 0; n < 6; n++) {
@@ -426,22 +482,21 @@ __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double*
         const int r = item - N_pu;
         const int kc = plan.row_kf[r];
         const double* er = E + (size_t)r * 6 * HW;
-        for (int k = chunk * kSchPx + threadIdx.x; k < min(HW, (chunk + 1) * kSchPx);
-             k += kSchWG) {
+        for (int k = threadIdx.x; k < HW; k += kSchWG) {
             const double qw = Q[(size_t)kc * HW + k] * Wv[(size_t)kc * HW + k];
 #pragma unroll
             for (int n = 0; n < 6; n++) acc[n] += qw * er[(size_t)n * HW + k];
         }
     }
-    block_sum_to(acc, red, spart + ((size_t)item * nchS + chunk) * 36);
+    block_sum_to(acc, red, stot + (size_t)item * 36);
 }
 
 // ----------------------------------------------------------- solve ------
 struct SolveArgs {
     PlanDev plan;
-    const double* hpart;  // [M][nch][90] per-edge Hessian/gradient chunk partials
-    const double* spart;  // [N_pu + N_E][nchS][36] Schur pair / row chunk partials
-    int nch, nchS, N_pu, P, n, n_blk, t0, t1;
+    const double* etot;   // [M][120] per-edge Hii, Hij, Hjj, vi, vj
+    const double* stot;   // [N_pu + N_E][36] Schur pair blocks / row gradients
+    int N_pu, P, n, n_blk, t0, t1;
     float lm, ep;
     double* S;      // working copy of the blocked solver [(n+1)*n]: S, then b^T
     double* S_dbg;  // [n*n] assembled system (after damping), input of the solve
@@ -452,29 +507,28 @@ struct SolveArgs {
     float* poses;
 };
 
-// index into an edge's 90 totals of entry (r, c) of Hessian block `which`
-__device__ __forceinline__ int hs_index(int which, int r, int c) {
-    if (which == 0) return tri(max(r, c), min(r, c));
-    if (which == 1) return tri(6 + c, r);
-    if (which == 2) return tri(6 + r, c);
-    return tri(6 + max(r, c), 6 + min(r, c));
+// One edge-block or Schur-item contribution to entry (r, c) of a 6x6 block of
+// S (ba.cuh:520-548, 722-742): code cd of the block's contribution list.
+__device__ __forceinline__ double s_contrib(const SolveArgs& A, int cd, int r, int c) {
+    const int ty = code_type(cd), v = code_val(cd);
+    if (ty == 0) {
+        const double* et = A.etot + (size_t)(v >> 2) * kNT;
+        const int w = v & 3;
+        return w == 0 ? et[kTotHii + r * 6 + c]
+             : w == 1 ? et[kTotHij + r * 6 + c]
+             : w == 2 ? et[kTotHij + c * 6 + r]
+                      : et[kTotHjj + r * 6 + c];
+    }
+    return -A.stot[(size_t)v * 36 + (ty == 1 ? r * 6 + c : c * 6 + r)];
 }
 
 // One workgroup per 6x6 block (a, b) of S (P*P of them) and per 6-entry
-// segment of b (P more): S = sum of the listed Hessian blocks minus the Schur
-// pair blocks (ba.cuh:520-548, 722-742), then the LM damping
-// S_ii += ep + lm*S_ii after the Schur step (ba.cuh:749-750). Every
-// contribution is itself a sum of per-chunk partials; thread (slice, entry)
-// sums the chunks slice, slice + 7, ... of every contribution, and the seven
-// slices are added in a fixed order (deterministic, no atomics).
+// segment of b (P more): S = sum of the listed edge blocks minus the Schur
+// pair blocks, then the LM damping S_ii += ep + lm*S_ii after the Schur step
+// (ba.cuh:749-750); b = the edges' gradients minus E Q w of the pose's rows.
+// Thread (slice, entry) sums contributions slice, slice + 7, ... of the list,
+// and the seven slices are added in a fixed order (deterministic, no atomics).
 constexpr int kAsmSlices = 7;  // 7 x 36 = 252 of the 256 threads
-
-__device__ __forceinline__ double slice_sum(const double* p, int nparts, int stride, int sl) {
-    double s = 0.0;
-    for (int c = sl; c < nparts; c += kAsmSlices) s += p[(size_t)c * stride];
-    return s;
-}
-
 __global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
     __shared__ double red[kAsmSlices][36];
     const int n = A.n, P = A.P;
@@ -488,18 +542,8 @@ __global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
         const int blk = A.plan.blkmap[g];
         if (sl < kAsmSlices && blk >= 0) {
             const int q1 = A.plan.sblk_ptr[blk + 1];
-            for (int q = A.plan.sblk_ptr[blk]; q < q1; q++) {
-                const int cd = A.plan.sblk_src[q];
-                const int ty = code_type(cd), v = code_val(cd);
-                if (ty == 0) {
-                    s += slice_sum(A.hpart + (size_t)(v >> 2) * A.nch * kNH +
-                                          hs_index(v & 3, r, c),
-                                      A.nch, kNH, sl);
-                } else {
-                    const int e36 = ty == 1 ? r * 6 + c : c * 6 + r;
-                    s -= slice_sum(A.spart + (size_t)v * A.nchS * 36 + e36, A.nchS, 36, sl);
-                }
-            }
+            for (int q = A.plan.sblk_ptr[blk] + sl; q < q1; q += kAsmSlices)
+                s += s_contrib(A, A.plan.sblk_src[q], r, c);
         }
         if (sl < kAsmSlices) red[sl][e] = s;
         __syncthreads();
@@ -515,16 +559,13 @@ __global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
         const int a = g - P * P;
         const int k = e;  // entries 0..5 of segment a; threads with e >= 6 idle
         if (sl < kAsmSlices && k < 6) {
-            for (int q = A.plan.bv_ptr[a]; q < A.plan.bv_ptr[a + 1]; q++) {
+            for (int q = A.plan.bv_ptr[a] + sl; q < A.plan.bv_ptr[a + 1]; q += kAsmSlices) {
                 const int cd = A.plan.bv_src[q];
                 const int v = code_val(cd);
                 if (code_type(cd) == 0)
-                    s += slice_sum(A.hpart + (size_t)(v >> 1) * A.nch * kNH + 78 +
-                                          (v & 1) * 6 + k,
-                                      A.nch, kNH, sl);
+                    s += A.etot[(size_t)(v >> 1) * kNT + ((v & 1) ? kTotVj : kTotVi) + k];
                 else
-                    s -= slice_sum(A.spart + (size_t)(A.N_pu + v) * A.nchS * 36 + k, A.nchS,
-                                      36, sl);
+                    s -= A.stot[(size_t)(A.N_pu + v) * 36 + k];
             }
         }
         if (sl < kAsmSlices) red[sl][e] = s;
@@ -538,166 +579,10 @@ __global__ __launch_bounds__(256) void k_ba_assemble(SolveArgs A) {
     }
 }
 
-// ---- blocked Cholesky S = L L^T (lower, row-major, leading dimension n) ----
-// Block columns of kNB: (1) the diagonal block is factored by wave 0 with one
-// row per lane in registers (broadcasts by readlane, no memory round trips);
-// (2) the panel below it is solved row-parallel; (3) the trailing triangle is
-// updated entry-parallel. Three barriers per block column instead of one per
-// column. Works on S in LDS or in global memory. The SPD test is the
-// reference's: every pivot must be positive before its sqrt (ba.cuh:422).
-constexpr int kNB = 16;
-
 __device__ __forceinline__ double bcast(double v, int src) {
     const int lo = __builtin_amdgcn_readlane(__double2loint(v), src);
     const int hi = __builtin_amdgcn_readlane(__double2hiint(v), src);
     return __hiloint2double(hi, lo);
-}
-
-// packed lower-triangle index t -> (i, k), 0 <= k <= i
-__device__ __forceinline__ void tri_unpack(int t, int& i, int& k) {
-    int r = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
-    while (r * (r + 1) / 2 > t) r--;
-    while ((r + 1) * (r + 2) / 2 <= t) r++;
-    i = r;
-    k = t - r * (r + 1) / 2;
-}
-
-__device__ __forceinline__ bool chol_blocked(double* S, int n, int* sh_flag) {
-    const int tid = threadIdx.x;
-    if (tid == 0) *sh_flag = 1;
-    __syncthreads();
-    for (int j0 = 0; j0 < n; j0 += kNB) {
-        const int jb = min(kNB, n - j0);
-        if (tid < 64) {  // (1) diagonal block, wave 0
-            const int lane = tid;
-            double d[kNB];
-#pragma unroll
-            for (int m = 0; m < kNB; m++)
-                d[m] = (lane < jb && m <= lane) ? S[(size_t)(j0 + lane) * n + j0 + m] : 0.0;
-            bool ok = true;
-#pragma unroll
-            for (int k = 0; k < kNB; k++) {
-                if (k < jb) {
-                    const double dkk = bcast(d[k], k);
-                    ok = ok && (dkk > 0.0);
-                    const double lkk = sqrt(dkk);
-                    d[k] = lane == k ? lkk : (lane > k ? d[k] / lkk : d[k]);
-#pragma unroll
-                    for (int m = k + 1; m < kNB; m++) {
-                        if (m < jb) {
-                            const double lmk = bcast(d[k], m);
-                            if (lane >= m) d[m] -= d[k] * lmk;
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < kNB; m++)
-                if (lane < jb && m <= lane) S[(size_t)(j0 + lane) * n + j0 + m] = d[m];
-            if (lane == 0 && !ok) *sh_flag = 0;
-        }
-        __syncthreads();
-        if (!*sh_flag) return false;
-        const int r0 = j0 + jb;
-        // (2) panel rows r0..n-1: x L_D^T = S[i][j0:j0+jb]
-        for (int i = r0 + tid; i < n; i += blockDim.x) {
-            double x[kNB];
-#pragma unroll
-            for (int k = 0; k < kNB; k++) {
-                if (k < jb) {
-                    double s = S[(size_t)i * n + j0 + k];
-#pragma unroll
-                    for (int m = 0; m < k; m++) s -= x[m] * S[(size_t)(j0 + k) * n + j0 + m];
-                    x[k] = s / S[(size_t)(j0 + k) * n + j0 + k];
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kNB; k++)
-                if (k < jb) S[(size_t)i * n + j0 + k] = x[k];
-        }
-        __syncthreads();
-        // (3) trailing triangle S[i][k] -= L[i][J] . L[k][J], r0 <= k <= i < n
-        const int mm = n - r0;
-        const int cnt = mm * (mm + 1) / 2;
-        for (int t = tid; t < cnt; t += blockDim.x) {
-            int ii, kk;
-            tri_unpack(t, ii, kk);
-            const double* li = S + (size_t)(r0 + ii) * n + j0;
-            const double* lk = S + (size_t)(r0 + kk) * n + j0;
-            double s = 0.0;
-#pragma unroll
-            for (int m = 0; m < kNB; m++)
-                if (m < jb) s += li[m] * lk[m];
-            S[(size_t)(r0 + ii) * n + r0 + kk] -= s;
-        }
-        __syncthreads();
-    }
-    return true;
-}
-
-// Solves L L^T x = b in place in y[] (y in LDS), factor from chol_blocked.
-__device__ __forceinline__ void chol_solve_blocked(const double* S, double* y, int n) {
-    const int tid = threadIdx.x;
-    for (int j0 = 0; j0 < n; j0 += kNB) {  // forward: L z = b
-        const int jb = min(kNB, n - j0);
-        if (tid < 64) {
-            const int lane = tid;
-            double v = lane < jb ? y[j0 + lane] : 0.0;
-#pragma unroll
-            for (int k = 0; k < kNB; k++) {
-                if (k < jb) {
-                    if (lane == k) v = v / S[(size_t)(j0 + k) * n + j0 + k];
-                    const double zk = bcast(v, k);
-                    if (lane > k && lane < jb) v -= S[(size_t)(j0 + lane) * n + j0 + k] * zk;
-                }
-            }
-            if (lane < jb) y[j0 + lane] = v;
-        }
-        __syncthreads();
-        for (int i = j0 + jb + tid; i < n; i += blockDim.x) {
-            double s = y[i];
-            for (int m = 0; m < jb; m++) s -= S[(size_t)i * n + j0 + m] * y[j0 + m];
-            y[i] = s;
-        }
-        __syncthreads();
-    }
-    for (int j0 = ((n - 1) / kNB) * kNB; j0 >= 0; j0 -= kNB) {  // backward: L^T x = z
-        const int jb = min(kNB, n - j0);
-        if (tid < 64) {
-            const int lane = tid;
-            double v = lane < jb ? y[j0 + lane] : 0.0;
-#pragma unroll
-            for (int k = kNB - 1; k >= 0; k--) {
-                if (k < jb) {
-                    if (lane == k) v = v / S[(size_t)(j0 + k) * n + j0 + k];
-                    const double xk = bcast(v, k);
-                    if (lane < k) v -= S[(size_t)(j0 + k) * n + j0 + lane] * xk;
-                }
-            }
-            if (lane < jb) y[j0 + lane] = v;
-        }
-        __syncthreads();
-        for (int i = tid; i < j0; i += blockDim.x) {
-            double s = y[i];
-            for (int m = 0; m < jb; m++) s -= S[(size_t)(j0 + m) * n + i] * y[j0 + m];
-            y[i] = s;
-        }
-        __syncthreads();
-    }
-}
-
-// Workgroup copy with eight loads in flight per thread.
-__device__ __forceinline__ void copy_in(double* dst, const double* src, int count) {
-    const int step = blockDim.x;
-    int t = threadIdx.x;
-    for (; t + 7 * step < count; t += 8 * step) {
-        double v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = src[t + u * step];
-#pragma unroll
-        for (int u = 0; u < 8; u++) dst[t + u * step] = v[u];
-    }
-    for (; t < count; t += step) dst[t] = src[t];
 }
 
 __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
@@ -720,22 +605,6 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
         for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
         for (int m = 0; m < 4; m++) A.poses[k * 7 + 3 + m] = (float)q1[m];
     }
-}
-
-// S and b in LDS (n <= 90), one workgroup of 256 threads.
-__global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
-    extern __shared__ double smem[];
-    const int n = A.n;
-    double* S = smem;
-    double* b = smem + (size_t)n * n;
-    copy_in(S, A.S_dbg, n * n);
-    for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.b_dbg[t];
-    __syncthreads();
-    __shared__ int sh_flag;
-    const bool ok = chol_blocked(S, n, &sh_flag);
-    if (ok) chol_solve_blocked(S, b, n);
-    __syncthreads();
-    finish_solve(A, b, ok);
 }
 
 // 1/sqrt(d) in fp64: hardware estimate + two Newton steps
@@ -1083,6 +952,107 @@ __device__ void back_solve_blocked(const double* __restrict__ S, double* y, int 
     }
 }
 
+// One workgroup, kWaveP < P and n <= kSmallN: the damped system is copied
+// into LDS as the bordered matrix [S; b^T] (rows 0..n-1, b in row n, leading
+// dimension n) and factored right-looking in kMB-column steps: (1) wave 0
+// factors the diagonal block with one row per lane in registers; (2) one
+// thread per row below it (b's row included) solves that row against it;
+// (3) the trailing lower triangle takes the panel's products in 4 x 4
+// register blocks, one block per thread. Row n ends as z = L^-1 b; the
+// backward solve is back_solve_blocked on the factor in LDS.
+constexpr int kMB = 16;
+__global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
+    extern __shared__ double S[];
+    __shared__ double invd[kMB];
+    __shared__ int ok_sh;
+    const int n = A.n, tid = threadIdx.x;
+    for (int t = tid; t < n * n + n; t += blockDim.x)
+        S[t] = t < n * n ? A.S_dbg[t] : A.b_dbg[t - n * n];
+    if (tid == 0) ok_sh = 1;
+    for (int j0 = 0; j0 < n; j0 += kMB) {
+        const int nb = min(kMB, n - j0);
+        __syncthreads();
+        if (tid < 64) {  // (1) the diagonal block, padded with an identity block
+            const int lane = tid;
+            double r[kMB];
+#pragma unroll
+            for (int m = 0; m < kMB; m++)
+                r[m] = (lane < nb && m < nb) ? S[(size_t)(j0 + lane) * n + j0 + m]
+                                             : (m == lane ? 1.0 : 0.0);
+            bool ok = true;
+            double inv = 0.0;
+            wave_cholesky<kMB, kMB>(r, static_cast<double (*)[kMB]>(nullptr), ok, inv);
+            if (lane < nb) {
+#pragma unroll
+                for (int m = 0; m < kMB; m++)
+                    if (m <= lane) S[(size_t)(j0 + lane) * n + j0 + m] = r[m];
+                invd[lane] = inv;
+            }
+            if (lane == 0 && !ok) ok_sh = 0;
+        }
+        __syncthreads();
+        if (!ok_sh) break;
+        const int r0 = j0 + nb;
+        // (2) panel rows r0..n (b's row is row n): x L_D^T = S[i][j0..j0+nb)
+        for (int i = r0 + tid; i <= n; i += blockDim.x) {
+            double* row = S + (size_t)i * n + j0;
+            double x[kMB];
+#pragma unroll
+            for (int k = 0; k < kMB; k++) {
+                if (k < nb) {
+                    double v = row[k];
+#pragma unroll
+                    for (int m = 0; m < k; m++) v -= x[m] * S[(size_t)(j0 + k) * n + j0 + m];
+                    x[k] = v * invd[k];
+                } else {
+                    x[k] = 0.0;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kMB; k++)
+                if (k < nb) row[k] = x[k];
+        }
+        __syncthreads();
+        // (3) S[i][k] -= L[i][J] . L[k][J] for r0 <= k <= i <= n, k < n
+        const int nbi = (n + 1 - r0 + 3) / 4;
+        const int cnt = nbi * (nbi + 1) / 2;
+        for (int t = tid; t < cnt; t += blockDim.x) {
+            int bi = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
+            while (bi * (bi + 1) / 2 > t) bi--;
+            while ((bi + 1) * (bi + 2) / 2 <= t) bi++;
+            const int bk = t - bi * (bi + 1) / 2;
+            const int i0 = r0 + 4 * bi, k0 = r0 + 4 * bk;
+            if (k0 >= n) continue;
+            double acc[4][4] = {};
+            for (int m = 0; m < nb; m++) {
+                double a[4], b[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    a[u] = i0 + u <= n ? S[(size_t)(i0 + u) * n + j0 + m] : 0.0;
+                    b[u] = k0 + u < n ? S[(size_t)(k0 + u) * n + j0 + m] : 0.0;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[u][v] += a[u] * b[v];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int i = i0 + u, k = k0 + v;
+                    if (i <= n && k < n && k <= i) S[(size_t)i * n + k] -= acc[u][v];
+                }
+        }
+    }
+    __syncthreads();
+    const bool ok = ok_sh != 0;
+    double* y = S + (size_t)n * n;  // z, then x
+    if (ok) back_solve_blocked(S, y, n);
+    __syncthreads();
+    finish_solve(A, y, ok);
+}
+
 constexpr int kFinishWG = 512;
 __global__ __launch_bounds__(kFinishWG) void k_chol_finish(SolveArgs A) {
     extern __shared__ double smem[];
@@ -1148,10 +1118,10 @@ struct BaState {
     std::vector<int> key_ii, key_jj;
     int key_t0 = 0, key_t1 = 0, key_motion = 0, key_HW = 0;
     // plan sizes
-    int M = 0, P = 0, n = 0, N_kf = 0, N_E = 0, N_pu = 0, n_blk = 0, nch = 1, nchS = 1;
+    int M = 0, P = 0, n = 0, N_kf = 0, N_E = 0, N_pu = 0, n_blk = 0, nch = 1;
     std::vector<int> host;  // packed plan
     size_t off[kPlanParts] = {0};
-    DevBuf plan_dev, hpart, E, Q, Wv, spart, S, S_dbg, b_dbg, dx_dbg, dx, flags;
+    DevBuf plan_dev, hpart, etot, stot, E, Q, Wv, S, S_dbg, b_dbg, dx_dbg, dx, flags;
     HostStage stage;
     bool has_system = false;
     bool lin_by_wave = false;  // no keyframe has two edges to the same free pose
@@ -1289,7 +1259,6 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
     s->N_pu = N_pu;
     s->n_blk = (int)sblk.size();
     s->nch = (HW + kLinPx - 1) / kLinPx;
-    s->nchS = (HW + kSchPx - 1) / kSchPx;
     std::vector<int> blkmap((size_t)P * P, -1);
     for (size_t k = 0; k < sblk.size(); k++) blkmap[sblk[k]] = (int)k;
     const std::vector<int>* parts[kPlanParts] = {&kf_list, &kf_eptr, &kf_eidx, &edge_ri,
@@ -1317,8 +1286,9 @@ int ba_create(slk_ctx* ctx) {
 void ba_destroy(slk_ctx* ctx) {
     BaState* s = ctx->ba;
     if (!s) return;
-    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->E,      &s->Q,  &s->Wv,   &s->spart,
-                      &s->S,        &s->S_dbg, &s->b_dbg,  &s->dx_dbg, &s->dx, &s->flags};
+    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->etot, &s->stot,   &s->E,  &s->Q,
+                      &s->Wv,       &s->S,     &s->S_dbg, &s->b_dbg, &s->dx_dbg, &s->dx,
+                      &s->flags};
     for (DevBuf* b : bufs) b->release();
     s->stage.release();
     delete s;
@@ -1361,12 +1331,14 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         SLK_HIP(hipEventRecord(s->stage.done, stream));
         s->stage.pending = true;
         const size_t n = (size_t)s->n;
-        SLK_TRY(s->hpart.ensure((size_t)M * s->nch * kNH * sizeof(double)));
+        SLK_TRY(s->hpart.ensure((size_t)M * s->nch * kNJ * sizeof(double)));
+        SLK_TRY(s->etot.ensure((size_t)M * kNT * sizeof(double)));
+        SLK_TRY(s->stot.ensure(std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * 36) *
+                               sizeof(double)));
+
         SLK_TRY(s->E.ensure(std::max<size_t>(1, (size_t)s->N_E * 6 * HW) * sizeof(double)));
         SLK_TRY(s->Q.ensure((size_t)s->N_kf * HW * sizeof(double)));
         SLK_TRY(s->Wv.ensure((size_t)s->N_kf * HW * sizeof(double)));
-        SLK_TRY(s->spart.ensure(
-            std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * s->nchS * 36) * sizeof(double)));
         if (n > (size_t)kSmallN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
         SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
         SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
@@ -1386,23 +1358,24 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         hipLaunchKernelGGL(s->lin_by_wave ? k_ba_lin_wv : k_ba_lin_kf, dim3(s->nch, s->N_kf),
                            dim3(kLinWG), 0, stream, plan, target, weight, poses, disps,
                            intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
-                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW, ctx->w,
-                           s->nch, motion_only);
+                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW,
+                           ctx->w, s->nch, motion_only);
     }
     SLK_HIP(hipGetLastError());
-    if (!motion_only && s->N_pu + s->N_E > 0) {
+    {
+        // the Schur items, then one workgroup per edge for its totals
+        const int items = motion_only ? 0 : s->N_pu + s->N_E;
         ProfScope ps(ctx, "ba_schur", stream);
-        hipLaunchKernelGGL(k_ba_schur, dim3(s->nchS, s->N_pu + s->N_E), dim3(kSchWG), 0, stream,
-                           plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
-                           s->spart.as<double>(), HW, s->nchS, s->N_pu);
+        hipLaunchKernelGGL(k_ba_schur, dim3(items + M), dim3(kSchWG), 0, stream, plan,
+                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
+                           s->stot.as<double>(), HW, s->N_pu, items, poses, ii_gpu, jj_gpu,
+                           s->hpart.as<double>(), s->etot.as<double>(), s->nch);
         SLK_HIP(hipGetLastError());
     }
     SolveArgs A;
     A.plan = plan;
-    A.hpart = s->hpart.as<double>();
-    A.spart = s->spart.as<double>();
-    A.nch = s->nch;
-    A.nchS = s->nchS;
+    A.etot = s->etot.as<double>();
+    A.stot = s->stot.as<double>();
     A.N_pu = s->N_pu;
     A.P = s->P;
     A.n = s->n;
@@ -1428,7 +1401,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         solve_wave(s->P, A, stream);
     } else if (s->n <= kSmallN) {
         ProfScope ps(ctx, "ba_solve", stream);
-        const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);
+        const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);  // [S; b^T]
         const int threads = 256;
         hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(threads), shm, stream, A);
     } else {
@@ -1481,6 +1454,32 @@ extern "C" int slk_ba_last_system(slk_ctx* ctx, double* S_host, double* b_host, 
 // ----------------------------------------------- reference stage kernels ---
 namespace {
 
+// acc[0..77] += weff J J^T (upper triangle of [Ji, Jj]), acc[78..89] += weff r J,
+// with Ji[row] = -adj_se3(Jj[row]) per pixel as the reference evaluates it
+__device__ __forceinline__ void accum_hessian(const Lin& L, const double (*Ji)[6], bool stereo,
+                                              double (&acc)[kNH]) {
+#pragma unroll
+    for (int row = 0; row < 2; row++) {
+        const double we = stereo ? 0.0 : L.w[row];
+        double Jx[12];
+#pragma unroll
+        for (int n = 0; n < 6; n++) {
+            Jx[n] = Ji[row][n];
+            Jx[6 + n] = L.Jj[row][n];
+        }
+        int l = 0;
+#pragma unroll
+        for (int n = 0; n < 12; n++) {
+            const double wn = we * Jx[n];
+#pragma unroll
+            for (int m = 0; m <= n; m++) acc[l++] += wn * Jx[m];
+        }
+        const double wr = we * L.r[row];
+#pragma unroll
+        for (int n = 0; n < 12; n++) acc[78 + n] += wr * Jx[n];
+    }
+}
+
 // projective_transform_kernel (ba.cuh:39-221): one workgroup per edge.
 __global__ __launch_bounds__(256) void k_pt(const float* __restrict__ target,
                                             const float* __restrict__ weight,
@@ -1513,14 +1512,21 @@ __global__ __launch_bounds__(256) void k_pt(const float* __restrict__ target,
         lin_pixel(tij, qij, fx, fy, cx, cy, k, W, (double)disps[(size_t)ix * HW + k],
                   (double)target[base], (double)target[base + HW], (double)weight[base],
                   (double)weight[base + HW], L);
-        accum_hessian(L, stereo, acc);
+        double Ji[2][6];
+#pragma unroll
+        for (int row = 0; row < 2; row++) {
+            adj_se3(tij, qij, L.Jj[row], Ji[row]);
+#pragma unroll
+            for (int n = 0; n < 6; n++) Ji[row][n] = -Ji[row][n];
+        }
+        accum_hessian(L, Ji, stereo, acc);
         Cii[(size_t)e * HW + k] = (float)(L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1]);
         bz[(size_t)e * HW + k] =
             (float)(L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1]);
         const double a0 = stereo ? 0.0 : L.w[0] * L.Jz[0];
         const double a1 = stereo ? 0.0 : L.w[1] * L.Jz[1];
         for (int n = 0; n < 6; n++) {
-            Eii[((size_t)e * 6 + n) * HW + k] = (float)(a0 * L.Ji[0][n] + a1 * L.Ji[1][n]);
+            Eii[((size_t)e * 6 + n) * HW + k] = (float)(a0 * Ji[0][n] + a1 * Ji[1][n]);
             Eij[((size_t)e * 6 + n) * HW + k] = (float)(a0 * L.Jj[0][n] + a1 * L.Jj[1][n]);
         }
     }

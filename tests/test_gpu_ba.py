@@ -134,11 +134,12 @@ def test_not_spd_leaves_state_untouched(slk):
     ctx.close()
 
 
-@pytest.mark.parametrize("P", [11, 15])
+@pytest.mark.parametrize("P", [11, 14, 15])
 def test_lds_solver_sizes(slk, P):
-    """P = 11 and 15 free poses (n = 66 and 90): the edges of the one-workgroup
-    solve with S in LDS (65,520 B of dynamic LDS at n = 90), one iteration
-    against the oracle, then a second from the updated state."""
+    """P = 11 and 14 free poses (n = 66 and 84): the edges of the one-workgroup
+    solve with the bordered system in LDS (59,640 B at n = 84); P = 15
+    (n = 90): the first size of the blocked solve over many workgroups. One
+    iteration against the oracle, then a second from the updated state."""
     announce(f"ba lds solver P={P} (n={6 * P})")
     n = P + 2
     p = wl.ba_problem(n=n, h=12, w=16, seed=30 + P)
