@@ -383,6 +383,54 @@ int slk_rm_keyframe(slk_ctx* ctx, int ix, int num_keyframes, float* poses, float
                     float* edge_nets, float* target, float* weight, float* target_inac,
                     float* weight_inac, hipStream_t stream);
 
+/* -------------------------------------------------------- update operator */
+/* UpdateModule with its ConvGRU (cuda_slam/main.cu:385-667): the network that
+ * turns the 196-channel correlation lookup into delta / weight for the BA,
+ * the new hidden state and the GraphAgg features. Tensors are NCHW fp32 like
+ * the reference's buffers; the convolutions run as fp16-operand MFMA GEMMs
+ * with fp32 accumulation (the reference's tensor-op convolutions of fp32
+ * data, nn.cuh:146, round the operands to the same 10-bit mantissa), and
+ * every activation the reference rounds to fp16 is rounded where it does. */
+typedef struct slk_update slk_update;
+
+/* UpdateModule::init (main.cu:552-603) for batches of up to max_batch edges
+ * of h x w maps: allocates the activations. Weights are set separately. */
+int slk_update_create(slk_update** um, int max_batch, int h, int w);
+int slk_update_destroy(slk_update* um);
+
+/* The 18 convolutions the forward pass uses, in a fixed order: layer i has
+ * the reference's weight-file name (update_corr_encoder_0, ...;
+ * WeightStore::load_conv, main.cu:81-86) and shape [co][ci][k][k]. */
+int slk_update_num_layers(void);
+const char* slk_update_layer_name(int layer);
+int slk_update_layer_shape(int layer, int* co, int* ci, int* k);
+
+/* Weights of one layer as host fp32 arrays in the reference's layout
+ * (weight [co][ci][k][k], bias [co]; ConvLayer::init, nn.cuh:124-139). They
+ * are repacked for the GPU before the next forward. */
+int slk_update_set_conv(slk_update* um, int layer, const float* weight_host,
+                        const float* bias_host);
+
+/* Every layer from the reference's exported tensor files
+ * <dir>/<name>_weight.bin and <name>_bias.bin (int32 ndim, int32 dims,
+ * float32 data; export_weights.py:14-22, load_tensor nn.cuh:91-107). */
+int slk_update_load_dir(slk_update* um, const char* dir);
+
+/* UpdateModule::forward(corr_features, motion, net, inp, delta_out,
+ * weight_out, agg_conv1_out, ..., batch, h, w), main.cu:606-650: corr
+ * [B][196][hw], motion [B][4][hw], net [B][128][hw] (updated in place: the
+ * GRU state, fp16-valued), inp [B][128][hw] -> delta_out [B][3][hw],
+ * weight_out [B][3][hw], agg_conv1_out [B][128][hw]. B <= max_batch. */
+int slk_update_forward(slk_update* um, const float* corr, const float* motion, float* net,
+                       const float* inp, float* delta_out, float* weight_out,
+                       float* agg_conv1_out, int batch, hipStream_t stream);
+
+/* UpdateModule::compute_eta(agg_features, eta_out, ..., num_kf, h, w),
+ * main.cu:654-667: agg_features [K][128][hw] (rounded to fp16 in place, as
+ * the reference does) -> eta_out [K][hw] = 0.01 * softplus(eta conv). */
+int slk_update_compute_eta(slk_update* um, float* agg_features, float* eta_out, int num_kf,
+                           hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

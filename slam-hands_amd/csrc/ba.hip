@@ -1402,8 +1402,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     } else if (s->n <= kSmallN) {
         ProfScope ps(ctx, "ba_solve", stream);
         const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);  // [S; b^T]
-        const int threads = 256;
-        hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(threads), shm, stream, A);
+        hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(256), shm, stream, A);
     } else {
         ProfScope ps(ctx, "ba_solve", stream);
         SLK_TRY(solve_blocked(A, stream));

@@ -1,0 +1,817 @@
+// The DROID-SLAM update operator for gfx950: UpdateModule::forward with its
+// ConvGRU, and UpdateModule::compute_eta (cuda_slam/main.cu:385-667).
+//
+// Every convolution runs as an implicit GEMM on v_mfma_f32_32x32x16_f16:
+// output channels are the GEMM rows, pixels its columns, and K walks
+// 16-channel chunks of the input times the kernel taps. The reference's
+// convolutions are cuDNN tensor-op convolutions of fp32 tensors
+// (CUDNN_TENSOR_OP_MATH, nn.cuh:146): products of operands rounded to a
+// 10-bit mantissa, accumulated in fp32. fp16 operands carry the same 10-bit
+// mantissa, so weights and activations are rounded to fp16 once and the
+// MFMA accumulates in fp32. Every activation the reference rounds to fp16
+// (round_to_fp16, nn.cuh:563-569) is stored as fp16 here, so nothing is lost
+// by keeping the intermediates in half the bytes.
+//
+// Activation layout "CK": [image][C/16][h*w][16] fp16: a 16-channel chunk of
+// consecutive pixels is contiguous, so a workgroup's input patch of one chunk
+// is a few contiguous rows, and every MFMA operand read is 16 bytes.
+// Concatenations of the reference (concat4_kernel, nn.cuh:497) are chunk
+// ranges of one CK buffer, written in place by their producers.
+//
+// The GRU's elementwise steps are epilogues of the convolutions that produce
+// their inputs: z and r (sigmoid of conv + global term, rounded) and r*net
+// in the epilogue of the fused convz|convr GEMM, the gated global pooling
+// input in the epilogue of w, q and the state update (1-z) net + z q in the
+// epilogue of convq, and the three 128-channel heads of the new state
+// (delta_0 | weight_0 | agg_conv1) as one 384-row GEMM.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "slk_internal.hpp"
+
+namespace slk {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTH = 8;    // output rows per workgroup tile
+constexpr int kTW = 32;   // output columns per workgroup tile (one MFMA column block)
+constexpr int kCoT = 128; // output channels per workgroup tile
+
+__device__ __forceinline__ float r16(float x) { return (float)(_Float16)x; }
+__device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// One input source of a convolution: chunks of a CK buffer.
+struct CkSrc {
+    const _Float16* p;  // chunk 0 of image 0
+    int nchunk;         // chunks taken from this source
+    long nstride;       // elements between images
+};
+
+enum Epi {
+    kEpiRelu = 0,   // out16 = round16(relu(conv + b))
+    kEpiGate = 1,   // out16 = round16(round16(sigmoid(round16(conv + b))) * net)
+    kEpiZR = 2,     // rows < 128: z; rows >= 128: r and out r*net (see below)
+    kEpiQ = 3,      // q and the state update
+    kEpiHeads = 4,  // rows < 256: out16 = round16(relu(conv + b)); rows >= 256: out32
+};
+
+struct ConvArgs {
+    CkSrc s0, s1;         // input chunks [0, s0.nchunk) from s0, the rest from s1
+    int nchunk;           // input chunks in total
+    const _Float16* wt;   // [taps][nchunk][co_tot][16]
+    const float* bias;    // [co_tot]
+    int co_tot, Co;       // padded / real output channels
+    int h, w, tiles_x;
+    // epilogue operands (CK buffers are [image][chunks][hw][16] with nstride)
+    _Float16* out16;      // kEpiRelu/kEpiGate/kEpiHeads: output chunks
+    long out16_nstride;
+    _Float16* zbuf;       // kEpiZR: z (8 chunks); kEpiQ: z input
+    _Float16* rnet;       // kEpiZR: r * net (8 chunks)
+    long zr_nstride;
+    _Float16* net16;      // 8 chunks of the state (read by Gate/ZR/Q; Q writes it)
+    long net_nstride;
+    const float* gterm;   // [image][384] rounded global terms (zg | rg | qg)
+    float* out32;         // kEpiQ: the new state; kEpiHeads: agg_conv1, NCHW fp32
+    long out32_nstride;
+};
+
+// One conv tile: kCoT output channels x (kTH x kTW) pixels of one image. Four
+// waves: wave (wm, wn) takes 64 channels (two 32-row MFMA blocks) of image
+// rows wn*4 .. wn*4+3 of the tile (four 32-pixel column blocks). Per input
+// chunk, the (kTH + KS - 1) x (kTW + KS - 1) patch of 16 channels is staged
+// in LDS (double-buffered: the next chunk's global loads are in flight during
+// the current chunk's MFMAs); the weight fragments of all taps of a chunk are
+// read from global memory (L2-resident) into registers ahead of the taps.
+template <int KS, int EPI>
+__global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
+    constexpr int P = KS / 2;
+    constexpr int PH = kTH + KS - 1, PW = kTW + KS - 1;
+    constexpr int UNITS = PH * PW * 2;  // 16-byte units of a chunk's patch
+    constexpr int UPT = (UNITS + 255) / 256;
+    constexpr int TAPS = KS * KS;
+    constexpr int AHEAD = KS <= 3 ? TAPS : 1;  // weight taps held in registers
+    __shared__ __attribute__((aligned(16))) _Float16 patch[2][PH * PW * 16];
+    const int HW = a.h * a.w;
+    const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
+    const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+
+    f16x8 reg[UPT];
+    auto load_chunk = [&](int c) {
+        const bool first = c < a.s0.nchunk;
+        const CkSrc& s = first ? a.s0 : a.s1;
+        const int cc = first ? c : c - a.s0.nchunk;
+        const _Float16* base = s.p + (long)n * s.nstride + (long)cc * HW * 16;
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u;
+            const int pix = unit >> 1, half = unit & 1;
+            const int py = pix / PW, px = pix - (pix / PW) * PW;
+            const int y = ty0 - P + py, x = tx0 - P + px;
+            const bool ok = unit < UNITS && y >= 0 && y < a.h && x >= 0 && x < a.w;
+            f16x8 v = {};
+            if (ok) v = *reinterpret_cast<const f16x8*>(base + ((long)y * a.w + x) * 16 + half * 8);
+            reg[u] = v;
+        }
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u;
+            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[u];
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+
+    const long tap_stride = (long)a.nchunk * a.co_tot * 16;
+    const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int c = 0; c < a.nchunk; c++) {
+        const int buf = c & 1;
+        const _Float16* wc = wbase + (long)c * a.co_tot * 16;
+        f16x8 A[AHEAD][2];
+        if constexpr (AHEAD == TAPS) {
+#pragma unroll
+            for (int t = 0; t < TAPS; t++) {
+                A[t][0] = *reinterpret_cast<const f16x8*>(wc + t * tap_stride);
+                A[t][1] = *reinterpret_cast<const f16x8*>(wc + t * tap_stride + 32 * 16);
+            }
+        }
+        if (c + 1 < a.nchunk) load_chunk(c + 1);
+        const _Float16* pb = &patch[buf][0];
+#pragma unroll
+        for (int t = 0; t < TAPS; t++) {
+            const int ky = t / KS, kx = t - (t / KS) * KS;
+            f16x8 a0, a1;
+            if constexpr (AHEAD == TAPS) {
+                a0 = A[t][0];
+                a1 = A[t][1];
+            } else {
+                a0 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride);
+                a1 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride + 32 * 16);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int prow = wn * 4 + r + ky;
+                const f16x8 b =
+                    *reinterpret_cast<const f16x8*>(pb + ((prow * PW + l32 + kx) * 16 + lhi * 8));
+                acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0][r], 0, 0, 0);
+                acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1][r], 0, 0, 0);
+            }
+        }
+        if (c + 1 < a.nchunk) store_chunk(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane (l32, lhi), register v of block (mb, r) holds output
+    // channel co = cot*128 + wm*64 + mb*32 + 8*(v/4) + 4*lhi + v%4 at pixel
+    // (ty0 + wn*4 + r, tx0 + l32); four consecutive channels per v/4 group
+    const int x = tx0 + l32;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int y = ty0 + wn * 4 + r;
+        if (y >= a.h || x >= a.w) continue;
+        const int p = y * a.w + x;
+#pragma unroll
+        for (int mb = 0; mb < 2; mb++) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int co = cot * kCoT + wm * 64 + mb * 32 + 8 * g + 4 * lhi;
+                if (co >= a.Co) continue;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = acc[mb][r][4 * g + i] + a.bias[co + i];
+                if constexpr (EPI == kEpiRelu) {
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
+                    *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+                } else if constexpr (EPI == kEpiGate) {
+                    const f16x4 nt = *reinterpret_cast<const f16x4*>(
+                        a.net16 + (long)n * a.net_nstride + ((long)(co >> 4) * HW + p) * 16 +
+                        (co & 15));
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        o[i] = (_Float16)(r16(sigm(r16(v[i]))) * (float)nt[i]);
+                    *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+                } else if constexpr (EPI == kEpiZR) {
+                    const float* gt = a.gterm + (long)n * 384 + co;
+                    f16x4 s;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s[i] = (_Float16)sigm(r16(v[i]) + gt[i]);
+                    if (co < 128) {
+                        *reinterpret_cast<f16x4*>(a.zbuf + (long)n * a.zr_nstride +
+                                                  ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = s;
+                    } else {
+                        const int cr = co - 128;
+                        const long off = ((long)(cr >> 4) * HW + p) * 16 + (cr & 15);
+                        const f16x4 nt =
+                            *reinterpret_cast<const f16x4*>(a.net16 + (long)n * a.net_nstride + off);
+                        f16x4 o;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) o[i] = (_Float16)((float)nt[i] * (float)s[i]);
+                        *reinterpret_cast<f16x4*>(a.rnet + (long)n * a.zr_nstride + off) = o;
+                    }
+                } else if constexpr (EPI == kEpiQ) {
+                    const float* gt = a.gterm + (long)n * 384 + 256 + co;
+                    const long off = ((long)(co >> 4) * HW + p) * 16 + (co & 15);
+                    const f16x4 z =
+                        *reinterpret_cast<const f16x4*>(a.zbuf + (long)n * a.zr_nstride + off);
+                    _Float16* np = a.net16 + (long)n * a.net_nstride + off;
+                    const f16x4 nt = *reinterpret_cast<const f16x4*>(np);
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float q = r16(tanhf(r16(v[i]) + gt[i]));
+                        const float zi = (float)z[i];
+                        const float nn = (1.0f - zi) * (float)nt[i] + zi * q;
+                        o[i] = (_Float16)nn;
+                        a.out32[(long)n * a.out32_nstride + (long)(co + i) * HW + p] = (float)o[i];
+                    }
+                    *reinterpret_cast<f16x4*>(np) = o;
+                } else {  // kEpiHeads
+                    if (co < 256) {
+                        f16x4 o;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
+                        *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                                  ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            a.out32[(long)n * a.out32_nstride + (long)(co - 256 + i) * HW + p] =
+                                r16(fmaxf(v[i], 0.0f));
+                    }
+                }
+            }
+        }
+    }
+}
+
+// NCHW fp32 [image][C][hw] -> CK fp16 chunks [c0 ..) of out; channels past C
+// up to the chunk boundary are zero. With writeback, the rounded values also
+// replace the fp32 source (round_to_fp16 in place, nn.cuh:563-569).
+__global__ void k_to_ck(const float* in, long in_nstride, int C, _Float16* out, long out_nstride,
+                        int c0, int hw, float* writeback) {
+    const int n = blockIdx.z, ch = blockIdx.y;  // chunk index within the source
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= hw) return;
+    alignas(16) _Float16 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int c = ch * 16 + i;
+        float x = 0.0f;
+        if (c < C) {
+            const long idx = (long)n * in_nstride + (long)c * hw + p;
+            x = in[idx];
+            if (writeback) writeback[idx] = (float)(_Float16)x;
+        }
+        v[i] = (_Float16)x;
+    }
+    _Float16* o = out + (long)n * out_nstride + ((long)(c0 + ch) * hw + p) * 16;
+    *reinterpret_cast<f16x8*>(o) = *reinterpret_cast<f16x8*>(&v[0]);
+    *reinterpret_cast<f16x8*>(o + 8) = *reinterpret_cast<f16x8*>(&v[8]);
+}
+
+// global_avg_pool_kernel (nn.cuh:414-431) of the gated state: glo[n][c] =
+// sum_p gate[n][c][p] / hw in fp32, one workgroup per (image, chunk), a
+// fixed-order tree over the threads.
+__global__ __launch_bounds__(256) void k_gate_pool(const _Float16* gate, long nstride, int hw,
+                                                   float* glo) {
+    __shared__ float red[256][17];
+    const int n = blockIdx.y, ch = blockIdx.x;
+    const _Float16* g = gate + (long)n * nstride + (long)ch * hw * 16;
+    float s[16] = {};
+    for (int p = threadIdx.x; p < hw; p += 256) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(g + (long)p * 16);
+        const f16x8 b = *reinterpret_cast<const f16x8*>(g + (long)p * 16 + 8);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s[i] += (float)a[i];
+            s[8 + i] += (float)b[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) red[threadIdx.x][i] = s[i];
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (threadIdx.x < st)
+#pragma unroll
+            for (int i = 0; i < 16; i++) red[threadIdx.x][i] += red[threadIdx.x + st][i];
+        __syncthreads();
+    }
+    if (threadIdx.x < 16) glo[(long)n * 128 + ch * 16 + threadIdx.x] = red[0][threadIdx.x] / (float)hw;
+}
+
+// The three 1x1 global convolutions of the pooled vector (convz_glo,
+// convr_glo, convq_glo, main.cu:492-523): gterm[n][j] = round16(W[j] .
+// round16(glo[n]) + b[j]) for j in 0..383, W and b stacked z | r | q.
+__global__ __launch_bounds__(384) void k_glo_fc(const float* glo, const float* W, const float* b,
+                                                float* gterm) {
+    __shared__ float gs[128];
+    const int n = blockIdx.x, j = threadIdx.x;
+    if (j < 128) gs[j] = r16(glo[(long)n * 128 + j]);
+    __syncthreads();
+    float s = 0.0f;
+    for (int c = 0; c < 128; c++) s += W[(long)j * 128 + c] * gs[c];
+    gterm[(long)n * 384 + j] = r16(s + b[j]);
+}
+
+// 3x3 convolutions to at most 3 output channels (delta_2, weight_2,
+// agg_eta_0): one thread per pixel, fp32 accumulation of fp16-rounded
+// operands (weights rounded on upload). mode 0: round16(conv + b)
+// (delta, main.cu:634-635); 1: round16(sigmoid(conv + b)) (weight,
+// :641-643); 2: 0.01 * softplus(round16(conv + b)) (eta, :663-665).
+__global__ __launch_bounds__(256) void k_conv_small(const _Float16* in, long in_nstride, int nch,
+                                                    const float* W, const float* b, int Co,
+                                                    int h, int w, int mode, float* out,
+                                                    long out_nstride) {
+    __shared__ float ws[3 * 128 * 9];
+    const int n = blockIdx.y;
+    for (int t = threadIdx.x; t < Co * nch * 16 * 9; t += 256) ws[t] = W[t];
+    __syncthreads();
+    const int hw = h * w;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= hw) return;
+    const int y = p / w, x = p - (p / w) * w;
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+    const _Float16* base = in + (long)n * in_nstride;
+    for (int ch = 0; ch < nch; ch++) {
+        for (int t = 0; t < 9; t++) {
+            const int yy = y + t / 3 - 1, xx = x + t % 3 - 1;
+            if (yy < 0 || yy >= h || xx < 0 || xx >= w) continue;
+            const _Float16* src = base + ((long)ch * hw + yy * w + xx) * 16;
+            const f16x8 u0 = *reinterpret_cast<const f16x8*>(src);
+            const f16x8 u1 = *reinterpret_cast<const f16x8*>(src + 8);
+#pragma unroll
+            for (int o = 0; o < 3; o++) {
+                if (o >= Co) break;
+                const float* wr = ws + ((long)o * nch * 16 + ch * 16) * 9 + t;
+                float s = acc[o];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s += wr[i * 9] * (float)u0[i];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s += wr[(8 + i) * 9] * (float)u1[i];
+                acc[o] = s;
+            }
+        }
+    }
+    for (int o = 0; o < Co; o++) {
+        const float v = acc[o] + b[o];
+        float r;
+        if (mode == 0) r = r16(v);
+        else if (mode == 1) r = r16(sigm(v));
+        else r = 0.01f * logf(1.0f + expf(r16(v)));
+        out[(long)n * out_nstride + (long)o * hw + p] = r;
+    }
+}
+
+// ---------------------------------------------------------------- host side
+constexpr int kNumLayers = 18;
+struct LayerShape {
+    const char* name;
+    int co, ci, k;
+};
+constexpr LayerShape kLayers[kNumLayers] = {
+    {"update_corr_encoder_0", 128, 196, 1}, {"update_corr_encoder_2", 128, 128, 3},
+    {"update_flow_encoder_0", 128, 4, 7},   {"update_flow_encoder_2", 64, 128, 3},
+    {"update_gru_convz", 128, 448, 3},      {"update_gru_convr", 128, 448, 3},
+    {"update_gru_convq", 128, 448, 3},      {"update_gru_convz_glo", 128, 128, 1},
+    {"update_gru_convr_glo", 128, 128, 1},  {"update_gru_convq_glo", 128, 128, 1},
+    {"update_gru_w", 128, 128, 1},          {"update_weight_0", 128, 128, 3},
+    {"update_weight_2", 3, 128, 3},         {"update_delta_0", 128, 128, 3},
+    {"update_delta_2", 3, 128, 3},          {"update_agg_conv1", 128, 128, 3},
+    {"update_agg_conv2", 128, 128, 3},      {"update_agg_eta_0", 1, 128, 3},
+};
+enum {
+    L_CE0, L_CE2, L_FE0, L_FE2, L_Z, L_R, L_Q, L_ZG, L_RG, L_QG, L_W, L_WT0, L_WT2, L_DL0,
+    L_DL2, L_AG1, L_AG2, L_ETA
+};
+
+// A packed GEMM operand: [taps][nchunk][co_tot][16] fp16 + bias [co_tot].
+struct PackedConv {
+    int k = 1, nchunk = 0, co_tot = 0, Co = 0;
+    DevBuf wt, bias;
+};
+
+float round_half_host(float x) {
+    // round to nearest even fp16 and back, on the host
+    _Float16 h = (_Float16)x;
+    return (float)h;
+}
+
+}  // namespace
+
+struct UpdateState {
+    int max_batch = 0, h = 0, w = 0;
+    std::vector<float> hw_[kNumLayers], hb_[kNumLayers];  // host copies, reference layout
+    bool have[kNumLayers] = {};
+    bool packed = false;
+    PackedConv ce0, ce2, fe0, fe2, gw, zr, q, heads, ag2;
+    DevBuf glo_w, glo_b, small_w[3], small_b[3];  // delta_2, weight_2, eta_0
+    // activations (CK fp16) and small vectors
+    DevBuf corr16, mot16, cat, tmp, zr_buf, glo, gterm, agg16, agg_t;
+    int tiles_x = 0, tiles_y = 0;
+};
+
+namespace {
+
+int pack(PackedConv& pc, const UpdateState* s, std::initializer_list<int> layers) {
+    // all listed layers share k and ci; their output rows are stacked
+    int co = 0, ci = 0, k = 0;
+    for (int L : layers) {
+        co += kLayers[L].co;
+        ci = kLayers[L].ci;
+        k = kLayers[L].k;
+    }
+    pc.k = k;
+    pc.Co = co;
+    pc.nchunk = (ci + 15) / 16;
+    pc.co_tot = (co + kCoT - 1) / kCoT * kCoT;
+    const int taps = k * k;
+    std::vector<_Float16> w((size_t)taps * pc.nchunk * pc.co_tot * 16, (_Float16)0.0f);
+    std::vector<float> b(pc.co_tot, 0.0f);
+    int row = 0;
+    for (int L : layers) {
+        const LayerShape& ls = kLayers[L];
+        const std::vector<float>& src = s->hw_[L];
+        for (int o = 0; o < ls.co; o++) {
+            b[row + o] = s->hb_[L][o];
+            for (int c = 0; c < ls.ci; c++)
+                for (int t = 0; t < taps; t++) {
+                    const float v = src[((size_t)o * ls.ci + c) * taps + t];
+                    w[(((size_t)t * pc.nchunk + c / 16) * pc.co_tot + row + o) * 16 + c % 16] =
+                        (_Float16)v;
+                }
+        }
+        row += ls.co;
+    }
+    SLK_TRY(pc.wt.ensure(w.size() * sizeof(_Float16)));
+    SLK_TRY(pc.bias.ensure(b.size() * sizeof(float)));
+    SLK_HIP(hipMemcpy(pc.wt.ptr, w.data(), w.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+    SLK_HIP(hipMemcpy(pc.bias.ptr, b.data(), b.size() * sizeof(float), hipMemcpyHostToDevice));
+    return SLK_OK;
+}
+
+int upload_rounded(DevBuf& d, const std::vector<float>& v) {
+    std::vector<float> r(v.size());
+    for (size_t i = 0; i < v.size(); i++) r[i] = round_half_host(v[i]);
+    SLK_TRY(d.ensure(std::max<size_t>(1, r.size()) * sizeof(float)));
+    SLK_HIP(hipMemcpy(d.ptr, r.data(), r.size() * sizeof(float), hipMemcpyHostToDevice));
+    return SLK_OK;
+}
+
+int upload(DevBuf& d, const std::vector<float>& v) {
+    SLK_TRY(d.ensure(std::max<size_t>(1, v.size()) * sizeof(float)));
+    SLK_HIP(hipMemcpy(d.ptr, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+    return SLK_OK;
+}
+
+// small 3x3 heads: weights [Co][128][9] fp16-rounded as float, in the
+// k_conv_small order (o, channel, tap)
+int pack_small(DevBuf& w, DevBuf& b, const UpdateState* s, int L) {
+    SLK_TRY(upload_rounded(w, s->hw_[L]));
+    SLK_TRY(upload(b, s->hb_[L]));
+    return SLK_OK;
+}
+
+int pack_all(UpdateState* s) {
+    for (int L = 0; L < kNumLayers; L++)
+        if (!s->have[L])
+            return fail(SLK_E_STATE, std::string("update: weights of ") + kLayers[L].name +
+                                         " not set");
+    SLK_TRY(pack(s->ce0, s, {L_CE0}));
+    SLK_TRY(pack(s->ce2, s, {L_CE2}));
+    SLK_TRY(pack(s->fe0, s, {L_FE0}));
+    SLK_TRY(pack(s->fe2, s, {L_FE2}));
+    SLK_TRY(pack(s->gw, s, {L_W}));
+    SLK_TRY(pack(s->zr, s, {L_Z, L_R}));
+    SLK_TRY(pack(s->q, s, {L_Q}));
+    SLK_TRY(pack(s->heads, s, {L_DL0, L_WT0, L_AG1}));
+    SLK_TRY(pack(s->ag2, s, {L_AG2}));
+    // global convs: [384][128] rounded, stacked z | r | q
+    std::vector<float> gw, gb;
+    for (int L : {L_ZG, L_RG, L_QG}) {
+        gw.insert(gw.end(), s->hw_[L].begin(), s->hw_[L].end());
+        gb.insert(gb.end(), s->hb_[L].begin(), s->hb_[L].end());
+    }
+    SLK_TRY(upload_rounded(s->glo_w, gw));
+    SLK_TRY(upload(s->glo_b, gb));
+    SLK_TRY(pack_small(s->small_w[0], s->small_b[0], s, L_DL2));
+    SLK_TRY(pack_small(s->small_w[1], s->small_b[1], s, L_WT2));
+    SLK_TRY(pack_small(s->small_w[2], s->small_b[2], s, L_ETA));
+    SLK_HIP(hipDeviceSynchronize());
+    s->packed = true;
+    return SLK_OK;
+}
+
+template <int KS, int EPI>
+int launch_conv(const UpdateState* s, const PackedConv& pc, ConvArgs a, int N,
+                hipStream_t stream) {
+    a.nchunk = pc.nchunk;
+    a.wt = pc.wt.as<_Float16>();
+    a.bias = pc.bias.as<float>();
+    a.co_tot = pc.co_tot;
+    a.Co = pc.Co;
+    a.h = s->h;
+    a.w = s->w;
+    a.tiles_x = s->tiles_x;
+    if (a.s0.nchunk > a.nchunk) a.s0.nchunk = a.nchunk;
+    hipLaunchKernelGGL((k_conv<KS, EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
+                       dim3(256), 0, stream, a);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+CkSrc src(const DevBuf& b, int chunk0, int nchunk, long nstride, int hw) {
+    CkSrc c;
+    c.p = b.as<_Float16>() + (long)chunk0 * hw * 16;
+    c.nchunk = nchunk;
+    c.nstride = nstride;
+    return c;
+}
+
+// chunks of the activation buffers (per image)
+constexpr int kCorrCh = 13;  // 196 channels -> 13 chunks (208, zero-padded)
+constexpr int kCatCh = 28;   // net 0..7 | inp 8..15 | corr features 16..23 | flow 24..27
+constexpr int kTmpCh = 8;    // c1 / f1 / gate
+constexpr int kZrCh = 16;    // z 0..7 | r*net 8..15; later the heads' 256 channels
+
+}  // namespace
+}  // namespace slk
+
+using namespace slk;
+
+struct slk_update {
+    UpdateState s;
+};
+
+extern "C" int slk_update_create(slk_update** out, int max_batch, int h, int w) {
+    if (!out) return fail(SLK_E_ARG, "update_create: null output");
+    *out = nullptr;
+    if (max_batch < 1 || h < 1 || w < 1 || (long)h * w > (1L << 22))
+        return fail(SLK_E_ARG, "update_create: need max_batch >= 1, 1 <= h*w <= 2^22");
+    slk_update* u = new slk_update();
+    UpdateState& s = u->s;
+    s.max_batch = max_batch;
+    s.h = h;
+    s.w = w;
+    s.tiles_x = (w + kTW - 1) / kTW;
+    s.tiles_y = (h + kTH - 1) / kTH;
+    const size_t hw = (size_t)h * w, chunk = hw * 16 * sizeof(_Float16);
+    const size_t N = (size_t)max_batch;
+    int st = SLK_OK;
+    if (st == SLK_OK) st = s.corr16.ensure(N * kCorrCh * chunk);
+    if (st == SLK_OK) st = s.mot16.ensure(N * chunk);
+    if (st == SLK_OK) st = s.cat.ensure(N * kCatCh * chunk);
+    if (st == SLK_OK) st = s.tmp.ensure(N * kTmpCh * chunk);
+    if (st == SLK_OK) st = s.zr_buf.ensure(N * kZrCh * chunk);
+    if (st == SLK_OK) st = s.glo.ensure(N * 128 * sizeof(float));
+    if (st == SLK_OK) st = s.gterm.ensure(N * 384 * sizeof(float));
+    if (st != SLK_OK) {
+        delete u;
+        return st;
+    }
+    *out = u;
+    return SLK_OK;
+}
+
+extern "C" int slk_update_destroy(slk_update* u) {
+    if (!u) return SLK_OK;
+    UpdateState& s = u->s;
+    for (PackedConv* pc : {&s.ce0, &s.ce2, &s.fe0, &s.fe2, &s.gw, &s.zr, &s.q, &s.heads, &s.ag2}) {
+        pc->wt.release();
+        pc->bias.release();
+    }
+    for (DevBuf* b : {&s.glo_w, &s.glo_b, &s.small_w[0], &s.small_w[1], &s.small_w[2],
+                      &s.small_b[0], &s.small_b[1], &s.small_b[2], &s.corr16, &s.mot16, &s.cat,
+                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t})
+        b->release();
+    delete u;
+    return SLK_OK;
+}
+
+extern "C" int slk_update_num_layers(void) { return kNumLayers; }
+
+extern "C" const char* slk_update_layer_name(int layer) {
+    return layer >= 0 && layer < kNumLayers ? kLayers[layer].name : nullptr;
+}
+
+extern "C" int slk_update_layer_shape(int layer, int* co, int* ci, int* k) {
+    if (layer < 0 || layer >= kNumLayers) return fail(SLK_E_ARG, "update_layer_shape: bad layer");
+    if (co) *co = kLayers[layer].co;
+    if (ci) *ci = kLayers[layer].ci;
+    if (k) *k = kLayers[layer].k;
+    return SLK_OK;
+}
+
+extern "C" int slk_update_set_conv(slk_update* u, int layer, const float* weight_host,
+                                   const float* bias_host) {
+    if (!u || layer < 0 || layer >= kNumLayers || !weight_host || !bias_host)
+        return fail(SLK_E_ARG, "update_set_conv: bad argument");
+    UpdateState& s = u->s;
+    const LayerShape& ls = kLayers[layer];
+    const size_t nw = (size_t)ls.co * ls.ci * ls.k * ls.k;
+    s.hw_[layer].assign(weight_host, weight_host + nw);
+    s.hb_[layer].assign(bias_host, bias_host + ls.co);
+    s.have[layer] = true;
+    s.packed = false;
+    return SLK_OK;
+}
+
+extern "C" int slk_update_load_dir(slk_update* u, const char* dir) {
+    if (!u || !dir) return fail(SLK_E_ARG, "update_load_dir: bad argument");
+    for (int L = 0; L < kNumLayers; L++) {
+        const LayerShape& ls = kLayers[L];
+        std::vector<float> wb[2];
+        for (int part = 0; part < 2; part++) {
+            const std::string path = std::string(dir) + "/" + ls.name +
+                                     (part ? "_bias.bin" : "_weight.bin");
+            FILE* f = std::fopen(path.c_str(), "rb");
+            if (!f) return fail(SLK_E_ARG, "update_load_dir: cannot open " + path);
+            int nd = 0;
+            bool ok = std::fread(&nd, sizeof(int), 1, f) == 1 && nd >= 1 && nd <= 4;
+            size_t total = 1;
+            int dims[4] = {0, 0, 0, 0};
+            for (int d = 0; ok && d < nd; d++) {
+                ok = std::fread(&dims[d], sizeof(int), 1, f) == 1 && dims[d] > 0;
+                total *= ok ? (size_t)dims[d] : 0;
+            }
+            const size_t want = part ? (size_t)ls.co : (size_t)ls.co * ls.ci * ls.k * ls.k;
+            ok = ok && total == want;
+            if (ok) {
+                wb[part].resize(total);
+                ok = std::fread(wb[part].data(), sizeof(float), total, f) == total;
+            }
+            std::fclose(f);
+            if (!ok) return fail(SLK_E_ARG, "update_load_dir: bad tensor file " + path);
+        }
+        SLK_TRY(slk_update_set_conv(u, L, wb[0].data(), wb[1].data()));
+    }
+    return SLK_OK;
+}
+
+extern "C" int slk_update_forward(slk_update* u, const float* corr, const float* motion,
+                                  float* net, const float* inp, float* delta_out,
+                                  float* weight_out, float* agg_conv1_out, int batch,
+                                  hipStream_t stream) {
+    if (!u) return fail(SLK_E_ARG, "update_forward: null module");
+    UpdateState& s = u->s;
+    if (batch < 0 || batch > s.max_batch)
+        return fail(SLK_E_ARG, "update_forward: batch outside [0, max_batch]");
+    if (batch == 0) return SLK_OK;
+    if (!corr || !motion || !net || !inp || !delta_out || !weight_out || !agg_conv1_out)
+        return fail(SLK_E_ARG, "update_forward: null argument");
+    if (!s.packed) SLK_TRY(pack_all(&s));
+    const int hw = s.h * s.w, N = batch;
+    const long ck = (long)hw * 16;  // elements of one chunk
+    // inputs to CK fp16: corr (196 ch), motion (4 ch), net and inp (128 ch)
+    auto to_ck = [&](const float* in, int C, DevBuf& out, int out_ch, int c0, float* wb) {
+        dim3 g((hw + 255) / 256, (C + 15) / 16, N);
+        hipLaunchKernelGGL(k_to_ck, g, dim3(256), 0, stream, in, (long)C * hw, C,
+                           out.as<_Float16>(), out_ch * ck, c0, hw, wb);
+    };
+    to_ck(corr, 196, s.corr16, kCorrCh, 0, nullptr);
+    to_ck(motion, 4, s.mot16, 1, 0, nullptr);
+    to_ck(net, 128, s.cat, kCatCh, 0, nullptr);
+    to_ck(inp, 128, s.cat, kCatCh, 8, nullptr);
+    SLK_HIP(hipGetLastError());
+    const long catS = kCatCh * ck, tmpS = kTmpCh * ck, zrS = kZrCh * ck;
+    // corr encoder: 1x1 196 -> 128, 3x3 128 -> 128 into cat chunks 16..23
+    {
+        ConvArgs a{};
+        a.s0 = src(s.corr16, 0, kCorrCh, kCorrCh * ck, hw);
+        a.out16 = s.tmp.as<_Float16>();
+        a.out16_nstride = tmpS;
+        SLK_TRY((launch_conv<1, kEpiRelu>(&s, s.ce0, a, N, stream)));
+        ConvArgs b{};
+        b.s0 = src(s.tmp, 0, 8, tmpS, hw);
+        b.out16 = s.cat.as<_Float16>() + 16 * ck;
+        b.out16_nstride = catS;
+        SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.ce2, b, N, stream)));
+    }
+    // flow encoder: 7x7 4 -> 128, 3x3 128 -> 64 into cat chunks 24..27
+    {
+        ConvArgs a{};
+        a.s0 = src(s.mot16, 0, 1, ck, hw);
+        a.out16 = s.tmp.as<_Float16>();
+        a.out16_nstride = tmpS;
+        SLK_TRY((launch_conv<7, kEpiRelu>(&s, s.fe0, a, N, stream)));
+        ConvArgs b{};
+        b.s0 = src(s.tmp, 0, 8, tmpS, hw);
+        b.out16 = s.cat.as<_Float16>() + 24 * ck;
+        b.out16_nstride = catS;
+        SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.fe2, b, N, stream)));
+    }
+    // GRU: gate = round16(sigmoid(w(net))) * net, pooled; global terms
+    {
+        ConvArgs a{};
+        a.s0 = src(s.cat, 0, 8, catS, hw);
+        a.out16 = s.tmp.as<_Float16>();
+        a.out16_nstride = tmpS;
+        a.net16 = s.cat.as<_Float16>();
+        a.net_nstride = catS;
+        SLK_TRY((launch_conv<1, kEpiGate>(&s, s.gw, a, N, stream)));
+        hipLaunchKernelGGL(k_gate_pool, dim3(8, N), dim3(256), 0, stream, s.tmp.as<_Float16>(),
+                           tmpS, hw, s.glo.as<float>());
+        hipLaunchKernelGGL(k_glo_fc, dim3(N), dim3(384), 0, stream, s.glo.as<float>(),
+                           s.glo_w.as<float>(), s.glo_b.as<float>(), s.gterm.as<float>());
+        SLK_HIP(hipGetLastError());
+    }
+    // z | r (one 256-row GEMM over the 448-channel concatenation), then q and
+    // the state update
+    {
+        ConvArgs a{};
+        a.s0 = src(s.cat, 0, kCatCh, catS, hw);
+        a.zbuf = s.zr_buf.as<_Float16>();
+        a.rnet = s.zr_buf.as<_Float16>() + 8 * ck;
+        a.zr_nstride = zrS;
+        a.net16 = s.cat.as<_Float16>();
+        a.net_nstride = catS;
+        a.gterm = s.gterm.as<float>();
+        SLK_TRY((launch_conv<3, kEpiZR>(&s, s.zr, a, N, stream)));
+        ConvArgs b{};
+        b.s0 = src(s.zr_buf, 8, 8, zrS, hw);   // r * net
+        b.s1 = src(s.cat, 8, 20, catS, hw);    // inp | corr features | flow
+        b.zbuf = s.zr_buf.as<_Float16>();
+        b.zr_nstride = zrS;
+        b.net16 = s.cat.as<_Float16>();
+        b.net_nstride = catS;
+        b.gterm = s.gterm.as<float>();
+        b.out32 = net;
+        b.out32_nstride = 128L * hw;
+        SLK_TRY((launch_conv<3, kEpiQ>(&s, s.q, b, N, stream)));
+    }
+    // heads of the new state: delta_0 | weight_0 | agg_conv1
+    {
+        ConvArgs a{};
+        a.s0 = src(s.cat, 0, 8, catS, hw);
+        a.out16 = s.zr_buf.as<_Float16>();  // 16 chunks: delta_0 | weight_0
+        a.out16_nstride = zrS;
+        a.out32 = agg_conv1_out;
+        a.out32_nstride = 128L * hw;
+        SLK_TRY((launch_conv<3, kEpiHeads>(&s, s.heads, a, N, stream)));
+        const dim3 g((hw + 255) / 256, N);
+        hipLaunchKernelGGL(k_conv_small, g, dim3(256), 0, stream, s.zr_buf.as<_Float16>(), zrS,
+                           8, s.small_w[0].as<float>(), s.small_b[0].as<float>(), 3, s.h, s.w, 0,
+                           delta_out, 3L * hw);
+        hipLaunchKernelGGL(k_conv_small, g, dim3(256), 0, stream,
+                           s.zr_buf.as<_Float16>() + 8 * ck, zrS, 8, s.small_w[1].as<float>(),
+                           s.small_b[1].as<float>(), 3, s.h, s.w, 1, weight_out, 3L * hw);
+        SLK_HIP(hipGetLastError());
+    }
+    return SLK_OK;
+}
+
+extern "C" int slk_update_compute_eta(slk_update* u, float* agg_features, float* eta_out,
+                                      int num_kf, hipStream_t stream) {
+    if (!u) return fail(SLK_E_ARG, "update_compute_eta: null module");
+    UpdateState& s = u->s;
+    if (num_kf < 0) return fail(SLK_E_ARG, "update_compute_eta: num_kf < 0");
+    if (num_kf == 0) return SLK_OK;
+    if (!agg_features || !eta_out) return fail(SLK_E_ARG, "update_compute_eta: null argument");
+    if (!s.packed) SLK_TRY(pack_all(&s));
+    const int hw = s.h * s.w, K = num_kf;
+    const long ck = (long)hw * 16;
+    const size_t chunk = (size_t)ck * sizeof(_Float16);
+    if (s.agg16.bytes < (size_t)K * 8 * chunk) {
+        SLK_HIP(hipStreamSynchronize(stream));  // earlier calls may still read them
+        SLK_TRY(s.agg16.ensure((size_t)K * 8 * chunk));
+        SLK_TRY(s.agg_t.ensure((size_t)K * 8 * chunk));
+    }
+    // round16 of the features in place (main.cu:659), to CK fp16
+    hipLaunchKernelGGL(k_to_ck, dim3((hw + 255) / 256, 8, K), dim3(256), 0, stream,
+                       agg_features, 128L * hw, 128, s.agg16.as<_Float16>(), 8 * ck, 0, hw,
+                       agg_features);
+    SLK_HIP(hipGetLastError());
+    ConvArgs a{};
+    a.s0 = src(s.agg16, 0, 8, 8 * ck, hw);
+    a.out16 = s.agg_t.as<_Float16>();
+    a.out16_nstride = 8 * ck;
+    SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.ag2, a, K, stream)));
+    hipLaunchKernelGGL(k_conv_small, dim3((hw + 255) / 256, K), dim3(256), 0, stream,
+                       s.agg_t.as<_Float16>(), 8 * ck, 8, s.small_w[2].as<float>(),
+                       s.small_b[2].as<float>(), 1, s.h, s.w, 2, eta_out, (long)hw);
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}

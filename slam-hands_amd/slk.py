@@ -40,6 +40,9 @@ EXPORTS = [
     "slk_scatter_rows", "slk_scatter_mean", "slk_ba_edge_set", "slk_proximity_factors",
     "slk_oldest_edges_mask", "slk_store_and_remove_edges", "slk_init_new_edges",
     "slk_rm_keyframe",
+    "slk_update_create", "slk_update_destroy", "slk_update_num_layers", "slk_update_layer_name",
+    "slk_update_layer_shape", "slk_update_set_conv", "slk_update_load_dir", "slk_update_forward",
+    "slk_update_compute_eta",
 ]
 
 
@@ -122,12 +125,24 @@ def lib():
             "slk_rm_keyframe": [P, I, I, P, P, P, I, P, P, L, P, P, P, I, ctypes.POINTER(I), P,
                                 P, I, ctypes.POINTER(I), P, P, P, P, P, P],
         }
+        sig.update({
+            "slk_update_create": [ctypes.POINTER(P), I, I, I],
+            "slk_update_destroy": [P],
+            "slk_update_num_layers": [],
+            "slk_update_layer_shape": [I, ctypes.POINTER(I), ctypes.POINTER(I), ctypes.POINTER(I)],
+            "slk_update_set_conv": [P, I, P, P],
+            "slk_update_load_dir": [P, ctypes.c_char_p],
+            "slk_update_forward": [P, P, P, P, P, P, P, P, I, P],
+            "slk_update_compute_eta": [P, P, P, I, P],
+        })
         for name, args in sig.items():
             fn = getattr(L_, name)
             fn.argtypes = args
             fn.restype = I
         L_.slk_oldest_edges_mask.argtypes = [P, I, I, P]
         L_.slk_oldest_edges_mask.restype = None
+        L_.slk_update_layer_name.argtypes = [I]
+        L_.slk_update_layer_name.restype = ctypes.c_char_p
         L_.slk_last_error.argtypes = []
         L_.slk_last_error.restype = ctypes.c_char_p
         _lib = L_
@@ -400,3 +415,55 @@ class Context:
         check(lib().slk_ba_last_system(self.ptr, S.ctypes.data, b.ctypes.data, dx.ctypes.data,
                                        ctypes.byref(n), stream))
         return S, b, dx
+
+
+class UpdateModule:
+    """slk_update_*: the update operator (UpdateModule / ConvGRU of
+    cuda_slam/main.cu:385-667) on device arrays."""
+
+    def __init__(self, max_batch, h, w):
+        self.h, self.w, self.max_batch = h, w, max_batch
+        p = P()
+        check(lib().slk_update_create(ctypes.byref(p), max_batch, h, w))
+        self.ptr = p
+
+    @staticmethod
+    def layers():
+        """[(name, co, ci, k)] in the ABI's layer order."""
+        L = lib()
+        out = []
+        for i in range(L.slk_update_num_layers()):
+            co, ci, k = I(), I(), I()
+            check(L.slk_update_layer_shape(i, ctypes.byref(co), ctypes.byref(ci), ctypes.byref(k)))
+            out.append((L.slk_update_layer_name(i).decode(), co.value, ci.value, k.value))
+        return out
+
+    def set_weights(self, weights):
+        """weights: {name: (w [co, ci, k, k], b [co]) float32 host arrays}."""
+        for i, (name, co, ci, k) in enumerate(self.layers()):
+            w, b = weights[name]
+            w = np.ascontiguousarray(w, np.float32)
+            b = np.ascontiguousarray(b, np.float32)
+            assert w.shape == (co, ci, k, k) and b.shape == (co,), name
+            check(lib().slk_update_set_conv(self.ptr, i, w.ctypes.data, b.ctypes.data))
+
+    def load_dir(self, path):
+        check(lib().slk_update_load_dir(self.ptr, os.fsencode(path)))
+
+    def forward(self, corr, motion, net, inp, delta, weight, agg, batch, stream=None):
+        check(lib().slk_update_forward(self.ptr, _p(corr), _p(motion), _p(net), _p(inp),
+                                       _p(delta), _p(weight), _p(agg), batch, stream))
+
+    def compute_eta(self, agg, eta, num_kf, stream=None):
+        check(lib().slk_update_compute_eta(self.ptr, _p(agg), _p(eta), num_kf, stream))
+
+    def close(self):
+        if self.ptr:
+            lib().slk_update_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
