@@ -431,6 +431,19 @@ int slk_update_forward(slk_update* um, const float* corr, const float* motion, f
 int slk_update_compute_eta(slk_update* um, float* agg_features, float* eta_out, int num_kf,
                            hipStream_t stream);
 
+/* CudaDroid::compute_motion_gru(last_kf_idx), main.cu:1934-1983: the
+ * frontend's motion filter. Builds the single-edge correlation of
+ * (f_last, f_cur) in ctx (as build_correlation(last_kf, temp_slot)), samples
+ * it at the identity grid, runs one update step (batch 1, zero motion) from
+ * copies of the keyframe's hidden state net_kf and context inp_kf (both
+ * [128][h*w], left unchanged), and writes the mean over pixels of the
+ * magnitude of delta's flow channels to *mean_flow (summed on the host in
+ * pixel order, like the reference). ctx and um must have the same h, w and
+ * ctx 4 levels. Synchronises `stream`. */
+int slk_motion_filter(slk_ctx* ctx, slk_update* um, const void* f_last, const void* f_cur,
+                      int dtype, const float* net_kf, const float* inp_kf, float* mean_flow,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,11 @@
 //   projmap, pose_retr, frame_distance, clamp_disps
 //                     the SE3 kernel launches with the reference's argument
 //                     lists (se3.cuh:118-277, main.cu:2392-2397).
+//   UpdateModule      init / forward / compute_eta of the update operator with
+//                     its ConvGRU (main.cu:535-667), weights from the
+//                     reference's exported tensor files.
+//   CorrEngine::compute_motion_gru
+//                     the frontend's motion filter (main.cu:1934-1983).
 //   UpdateGlue        the steps of run_update_pass around correlation and BA
 //                     (main.cu:2186-2390): motion and target kernels, the
 //                     hidden-state loads and saves, GraphAgg's scatter-mean
@@ -118,6 +123,20 @@ class CorrEngine {
         return p;
     }
 
+    // main.cu:1934 -- the motion filter between keyframe last_kf_idx and the
+    // frame in temp_slot of the fmaps, from that keyframe's hidden state and
+    // context (nets/inps [n][128][h*w]); returns the mean flow magnitude.
+    float compute_motion_gru(slk_update* update, int last_kf_idx, int temp_slot,
+                             const float* nets, const float* inps) {
+        float mean = 0.0f;
+        const long row = 128L * h_ * w_;
+        check(slk_motion_filter(ctx_, update, frame(last_kf_idx), frame(temp_slot), dtype_,
+                                nets + last_kf_idx * row, inps + last_kf_idx * row, &mean,
+                                nullptr),
+              "compute_motion_gru");
+        return mean;
+    }
+
     void destroy() {
         if (ctx_) slk_destroy(ctx_);
         ctx_ = nullptr;
@@ -201,6 +220,51 @@ class CorrBlock {
     }
     slk_ctx* ctx_ = nullptr;
     float scale_ = 1.0f / 16.0f;
+};
+
+// UpdateModule of cuda_slam/main.cu:535-667 with its member signatures. The
+// reference's init takes a cuDNN handle and a WeightStore reading
+// <dir>/<name>.bin tensor files; here the handle is an opaque pointer that is
+// ignored and the store is its directory. forward/compute_eta keep the
+// reference's argument lists; the temp buffers and workspace the reference
+// passes are not needed (the module owns its activations) and may be null.
+class UpdateModule {
+  public:
+    void init(void* /*cudnn*/, const char* weight_dir, int batch, int h, int w) {
+        h_ = h;
+        w_ = w;
+        check(slk_update_create(&um_, batch, h, w), "UpdateModule::init");
+        check(slk_update_load_dir(um_, weight_dir), "UpdateModule::init (weights)");
+    }
+
+    // main.cu:606
+    void forward(void* /*cudnn*/, float* corr_features, float* motion, float* net, float* inp,
+                 float* delta_out, float* weight_out, float* agg_conv1_out, float* /*temp1*/,
+                 float* /*temp2*/, float* /*workspace*/, int batch, int h, int w) {
+        if (h != h_ || w != w_) check(SLK_E_ARG, "UpdateModule::forward (map size)");
+        check(slk_update_forward(um_, corr_features, motion, net, inp, delta_out, weight_out,
+                                 agg_conv1_out, batch, nullptr),
+              "UpdateModule::forward");
+    }
+
+    // main.cu:654
+    void compute_eta(void* /*cudnn*/, float* agg_features, float* eta_out, float* /*temp1*/,
+                     float* /*temp2*/, float* /*workspace*/, int num_kf, int h, int w) {
+        if (h != h_ || w != w_) check(SLK_E_ARG, "UpdateModule::compute_eta (map size)");
+        check(slk_update_compute_eta(um_, agg_features, eta_out, num_kf, nullptr),
+              "UpdateModule::compute_eta");
+    }
+
+    void destroy() {
+        if (um_) slk_update_destroy(um_);
+        um_ = nullptr;
+    }
+
+    slk_update* module() const { return um_; }
+
+  private:
+    slk_update* um_ = nullptr;
+    int h_ = 0, w_ = 0;
 };
 
 // BundleAdjustment of cuda_slam/ba.cuh:397-819 (and, with motion_only, the

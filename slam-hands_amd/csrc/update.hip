@@ -82,6 +82,154 @@ struct ConvArgs {
     long out32_nstride;
 };
 
+// The epilogue of one pixel's two 32-row accumulator blocks: acc0/acc1
+// register v holds output channel co0 + mb*32 + 8*(v/4) + v%4 (co0 includes
+// the lane's 4*lhi), so each group of four registers is four consecutive
+// channels of the CK layout.
+template <int EPI>
+__device__ __forceinline__ void epi_block(const ConvArgs& a, const f32x16& acc0,
+                                          const f32x16& acc1, int n, int co0, int p, int HW) {
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++) {
+        const f32x16& acc = mb ? acc1 : acc0;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int co = co0 + mb * 32 + 8 * g;
+            if (co >= a.Co) continue;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = acc[4 * g + i] + a.bias[co + i];
+            if constexpr (EPI == kEpiRelu) {
+                f16x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
+                *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                          ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+            } else if constexpr (EPI == kEpiGate) {
+                const f16x4 nt = *reinterpret_cast<const f16x4*>(
+                    a.net16 + (long)n * a.net_nstride + ((long)(co >> 4) * HW + p) * 16 + (co & 15));
+                f16x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = (_Float16)(r16(sigm(r16(v[i]))) * (float)nt[i]);
+                *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                          ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+            } else if constexpr (EPI == kEpiZR) {
+                const float* gt = a.gterm + (long)n * 384 + co;
+                f16x4 sg;
+#pragma unroll
+                for (int i = 0; i < 4; i++) sg[i] = (_Float16)sigm(r16(v[i]) + gt[i]);
+                if (co < 128) {
+                    *reinterpret_cast<f16x4*>(a.zbuf + (long)n * a.zr_nstride +
+                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = sg;
+                } else {
+                    const int cr = co - 128;
+                    const long off = ((long)(cr >> 4) * HW + p) * 16 + (cr & 15);
+                    const f16x4 nt =
+                        *reinterpret_cast<const f16x4*>(a.net16 + (long)n * a.net_nstride + off);
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = (_Float16)((float)nt[i] * (float)sg[i]);
+                    *reinterpret_cast<f16x4*>(a.rnet + (long)n * a.zr_nstride + off) = o;
+                }
+            } else if constexpr (EPI == kEpiQ) {
+                const float* gt = a.gterm + (long)n * 384 + 256 + co;
+                const long off = ((long)(co >> 4) * HW + p) * 16 + (co & 15);
+                const f16x4 z = *reinterpret_cast<const f16x4*>(a.zbuf + (long)n * a.zr_nstride + off);
+                _Float16* np = a.net16 + (long)n * a.net_nstride + off;
+                const f16x4 nt = *reinterpret_cast<const f16x4*>(np);
+                f16x4 o;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float q = r16(tanhf(r16(v[i]) + gt[i]));
+                    const float zi = (float)z[i];
+                    const float nn = (1.0f - zi) * (float)nt[i] + zi * q;
+                    o[i] = (_Float16)nn;
+                    a.out32[(long)n * a.out32_nstride + (long)(co + i) * HW + p] = (float)o[i];
+                }
+                *reinterpret_cast<f16x4*>(np) = o;
+            } else {  // kEpiHeads
+                if (co < 256) {
+                    f16x4 o;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
+                    *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
+                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        a.out32[(long)n * a.out32_nstride + (long)(co - 256 + i) * HW + p] =
+                            r16(fmaxf(v[i], 0.0f));
+                }
+            }
+        }
+    }
+}
+
+// 1x1 convolutions as a plain GEMM with register-direct operands (no halo,
+// so nothing is staged in LDS): tile kCoT output channels x 256 consecutive
+// pixels, wave (wm, wn) = 64 channels x 128 pixels; every lane loads its
+// 16-byte A (weights) and B (8 channels of one pixel) fragments straight from
+// global memory, two chunks ahead of their MFMAs.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
+    const int HW = a.h * a.w;
+    const int cot = blockIdx.x, n = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+    const int p0 = blockIdx.y * 256 + wn * 128;
+    const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
+    f16x8 A[3][2], B[3][4];
+    auto load = [&](int c, int slot) {
+        const _Float16* wc = wbase + (long)c * a.co_tot * 16;
+        A[slot][0] = *reinterpret_cast<const f16x8*>(wc);
+        A[slot][1] = *reinterpret_cast<const f16x8*>(wc + 32 * 16);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int p = p0 + r * 32 + l32;
+            f16x8 v = {};
+            if (p < HW) {
+                const bool first = c < a.s0.nchunk;
+                const CkSrc& s = first ? a.s0 : a.s1;
+                const int cc = first ? c : c - a.s0.nchunk;
+                v = *reinterpret_cast<const f16x8*>(s.p + (long)n * s.nstride +
+                                                    ((long)cc * HW + p) * 16 + lhi * 8);
+            }
+            B[slot][r] = v;
+        }
+    };
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+    // three register slots, so every slot index below is a compile-time constant
+    auto step = [&](int c, int slot) {
+        if (c >= a.nchunk) return;
+        if (c + 2 < a.nchunk) load(c + 2, slot == 0 ? 2 : slot - 1);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][0], B[slot][r], acc[0][r],
+                                                               0, 0, 0);
+            acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][1], B[slot][r], acc[1][r],
+                                                               0, 0, 0);
+        }
+    };
+    load(0, 0);
+    if (a.nchunk > 1) load(1, 1);
+    for (int c = 0; c < a.nchunk; c += 3) {
+        step(c, 0);
+        step(c + 1, 1);
+        step(c + 2, 2);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int p = p0 + r * 32 + l32;
+        if (p < HW) epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, p, HW);
+    }
+}
+
 // One conv tile: kCoT output channels x (kTH x kTW) pixels of one image. Four
 // waves: wave (wm, wn) takes 64 channels (two 32-row MFMA blocks) of image
 // rows wn*4 .. wn*4+3 of the tile (four 32-pixel column blocks). Per input
@@ -146,6 +294,7 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
     for (int c = 0; c < a.nchunk; c++) {
         const int buf = c & 1;
         const _Float16* wc = wbase + (long)c * a.co_tot * 16;
+        // the weight fragments of every tap of the chunk, issued before the taps
         f16x8 A[AHEAD][2];
         if constexpr (AHEAD == TAPS) {
 #pragma unroll
@@ -181,90 +330,15 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
     }
 
     // epilogue: lane (l32, lhi), register v of block (mb, r) holds output
-    // channel co = cot*128 + wm*64 + mb*32 + 8*(v/4) + 4*lhi + v%4 at pixel
-    // (ty0 + wn*4 + r, tx0 + l32); four consecutive channels per v/4 group
+    // channel cot*128 + wm*64 + mb*32 + 8*(v/4) + 4*lhi + v%4 at pixel
+    // (ty0 + wn*4 + r, tx0 + l32)
     const int x = tx0 + l32;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int y = ty0 + wn * 4 + r;
         if (y >= a.h || x >= a.w) continue;
-        const int p = y * a.w + x;
-#pragma unroll
-        for (int mb = 0; mb < 2; mb++) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int co = cot * kCoT + wm * 64 + mb * 32 + 8 * g + 4 * lhi;
-                if (co >= a.Co) continue;
-                float v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = acc[mb][r][4 * g + i] + a.bias[co + i];
-                if constexpr (EPI == kEpiRelu) {
-                    f16x4 o;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
-                    *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
-                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
-                } else if constexpr (EPI == kEpiGate) {
-                    const f16x4 nt = *reinterpret_cast<const f16x4*>(
-                        a.net16 + (long)n * a.net_nstride + ((long)(co >> 4) * HW + p) * 16 +
-                        (co & 15));
-                    f16x4 o;
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        o[i] = (_Float16)(r16(sigm(r16(v[i]))) * (float)nt[i]);
-                    *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
-                                              ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
-                } else if constexpr (EPI == kEpiZR) {
-                    const float* gt = a.gterm + (long)n * 384 + co;
-                    f16x4 s;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) s[i] = (_Float16)sigm(r16(v[i]) + gt[i]);
-                    if (co < 128) {
-                        *reinterpret_cast<f16x4*>(a.zbuf + (long)n * a.zr_nstride +
-                                                  ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = s;
-                    } else {
-                        const int cr = co - 128;
-                        const long off = ((long)(cr >> 4) * HW + p) * 16 + (cr & 15);
-                        const f16x4 nt =
-                            *reinterpret_cast<const f16x4*>(a.net16 + (long)n * a.net_nstride + off);
-                        f16x4 o;
-#pragma unroll
-                        for (int i = 0; i < 4; i++) o[i] = (_Float16)((float)nt[i] * (float)s[i]);
-                        *reinterpret_cast<f16x4*>(a.rnet + (long)n * a.zr_nstride + off) = o;
-                    }
-                } else if constexpr (EPI == kEpiQ) {
-                    const float* gt = a.gterm + (long)n * 384 + 256 + co;
-                    const long off = ((long)(co >> 4) * HW + p) * 16 + (co & 15);
-                    const f16x4 z =
-                        *reinterpret_cast<const f16x4*>(a.zbuf + (long)n * a.zr_nstride + off);
-                    _Float16* np = a.net16 + (long)n * a.net_nstride + off;
-                    const f16x4 nt = *reinterpret_cast<const f16x4*>(np);
-                    f16x4 o;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float q = r16(tanhf(r16(v[i]) + gt[i]));
-                        const float zi = (float)z[i];
-                        const float nn = (1.0f - zi) * (float)nt[i] + zi * q;
-                        o[i] = (_Float16)nn;
-                        a.out32[(long)n * a.out32_nstride + (long)(co + i) * HW + p] = (float)o[i];
-                    }
-                    *reinterpret_cast<f16x4*>(np) = o;
-                } else {  // kEpiHeads
-                    if (co < 256) {
-                        f16x4 o;
-#pragma unroll
-                        for (int i = 0; i < 4; i++) o[i] = (_Float16)fmaxf(v[i], 0.0f);
-                        *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
-                                                  ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            a.out32[(long)n * a.out32_nstride + (long)(co - 256 + i) * HW + p] =
-                                r16(fmaxf(v[i], 0.0f));
-                    }
-                }
-            }
-        }
+        epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, y * a.w + x,
+                       HW);
     }
 }
 
@@ -338,51 +412,79 @@ __global__ __launch_bounds__(384) void k_glo_fc(const float* glo, const float* W
 }
 
 // 3x3 convolutions to at most 3 output channels (delta_2, weight_2,
-// agg_eta_0): one thread per pixel, fp32 accumulation of fp16-rounded
-// operands (weights rounded on upload). mode 0: round16(conv + b)
-// (delta, main.cu:634-635); 1: round16(sigmoid(conv + b)) (weight,
-// :641-643); 2: 0.01 * softplus(round16(conv + b)) (eta, :663-665).
-__global__ __launch_bounds__(256) void k_conv_small(const _Float16* in, long in_nstride, int nch,
-                                                    const float* W, const float* b, int Co,
-                                                    int h, int w, int mode, float* out,
-                                                    long out_nstride) {
-    __shared__ float ws[3 * 128 * 9];
-    const int n = blockIdx.y;
-    for (int t = threadIdx.x; t < Co * nch * 16 * 9; t += 256) ws[t] = W[t];
-    __syncthreads();
-    const int hw = h * w;
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= hw) return;
-    const int y = p / w, x = p - (p / w) * w;
+// agg_eta_0) on 8 input chunks: one thread per pixel of a kTH x kTW tile, the
+// tile's (kTH + 2) x (kTW + 2) patch of each chunk staged in LDS, fp32
+// accumulation of fp16-rounded operands (weights rounded on upload, laid out
+// [o][chunk][tap][16] so each tap's 16 weights are four broadcast reads).
+// mode 0: round16(conv + b) (delta, main.cu:634-635); 1: round16(sigmoid(
+// conv + b)) (weight, :641-643); 2: 0.01 * softplus(round16(conv + b)) (eta,
+// :663-665). blockIdx.y = image * nheads + head: head h reads chunks
+// [8h, 8h + 8) of `in`, weights W + h * wstride and writes out + h * ostride.
+struct SmallArgs {
+    const _Float16* in;
+    long in_nstride;
+    const float* W;
+    const float* b;
+    long wstride;  // floats between the heads' weight blocks (Co * 8 * 9 * 16)
+    int Co, h, w, tiles_x, nheads;
+    int mode[2];
+    float* out[2];
+    long out_nstride;
+};
+__global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
+    constexpr int PH = kTH + 2, PW = kTW + 2;
+    __shared__ __attribute__((aligned(16))) _Float16 patch[PH * PW * 16];
+    __shared__ __attribute__((aligned(16))) float ws[3 * 8 * 9 * 16];
+    const int n = blockIdx.z, head = blockIdx.y, tile = blockIdx.x;
+    const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
+    const int tid = threadIdx.x;
+    const int Co = a.Co, hw = a.h * a.w;
+    const float* W = a.W + head * a.wstride;
+    for (int t = tid; t < Co * 8 * 9 * 16; t += 256) ws[t] = W[t];
+    const int y = ty0 + (tid >> 5), x = tx0 + (tid & 31);
     float acc[3] = {0.0f, 0.0f, 0.0f};
-    const _Float16* base = in + (long)n * in_nstride;
-    for (int ch = 0; ch < nch; ch++) {
+    const _Float16* base = a.in + (long)n * a.in_nstride + (long)head * 8 * hw * 16;
+    for (int ch = 0; ch < 8; ch++) {
+        __syncthreads();  // the previous chunk's patch reads are done (and ws is loaded)
+        for (int u = tid; u < PH * PW * 2; u += 256) {
+            const int pix = u >> 1, half = u & 1;
+            const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
+            f16x8 v = {};
+            if (yy >= 0 && yy < a.h && xx >= 0 && xx < a.w)
+                v = *reinterpret_cast<const f16x8*>(base + ((long)ch * hw + yy * a.w + xx) * 16 +
+                                                    half * 8);
+            *reinterpret_cast<f16x8*>(&patch[u * 8]) = v;
+        }
+        __syncthreads();
+#pragma unroll
         for (int t = 0; t < 9; t++) {
-            const int yy = y + t / 3 - 1, xx = x + t % 3 - 1;
-            if (yy < 0 || yy >= h || xx < 0 || xx >= w) continue;
-            const _Float16* src = base + ((long)ch * hw + yy * w + xx) * 16;
-            const f16x8 u0 = *reinterpret_cast<const f16x8*>(src);
-            const f16x8 u1 = *reinterpret_cast<const f16x8*>(src + 8);
+            const int py = (tid >> 5) + t / 3, px = (tid & 31) + t % 3;
+            const f16x8 u0 = *reinterpret_cast<const f16x8*>(&patch[(py * PW + px) * 16]);
+            const f16x8 u1 = *reinterpret_cast<const f16x8*>(&patch[(py * PW + px) * 16 + 8]);
 #pragma unroll
             for (int o = 0; o < 3; o++) {
                 if (o >= Co) break;
-                const float* wr = ws + ((long)o * nch * 16 + ch * 16) * 9 + t;
+                const float* wr = ws + ((o * 8 + ch) * 9 + t) * 16;
                 float s = acc[o];
 #pragma unroll
-                for (int i = 0; i < 8; i++) s += wr[i * 9] * (float)u0[i];
+                for (int i = 0; i < 8; i++) s += wr[i] * (float)u0[i];
 #pragma unroll
-                for (int i = 0; i < 8; i++) s += wr[(8 + i) * 9] * (float)u1[i];
+                for (int i = 0; i < 8; i++) s += wr[8 + i] * (float)u1[i];
                 acc[o] = s;
             }
         }
     }
+    if (y >= a.h || x >= a.w) return;
+    const int p = y * a.w + x;
+    const int mode = a.mode[head];
+    float* out = a.out[head] + (long)n * a.out_nstride;
     for (int o = 0; o < Co; o++) {
-        const float v = acc[o] + b[o];
+        const float v = acc[o] + a.b[head * 3 + o];
         float r;
         if (mode == 0) r = r16(v);
         else if (mode == 1) r = r16(sigm(v));
         else r = 0.01f * logf(1.0f + expf(r16(v)));
-        out[(long)n * out_nstride + (long)o * hw + p] = r;
+        out[(long)o * hw + p] = r;
     }
 }
 
@@ -428,9 +530,12 @@ struct UpdateState {
     bool have[kNumLayers] = {};
     bool packed = false;
     PackedConv ce0, ce2, fe0, fe2, gw, zr, q, heads, ag2;
-    DevBuf glo_w, glo_b, small_w[3], small_b[3];  // delta_2, weight_2, eta_0
+    DevBuf glo_w, glo_b, small_w[3], small_b[3];  // [0]: delta_2 | weight_2, [2]: eta_0
     // activations (CK fp16) and small vectors
     DevBuf corr16, mot16, cat, tmp, zr_buf, glo, gterm, agg16, agg_t;
+    // motion filter (batch 1): grid coords, lookup, motion, state copies, heads
+    DevBuf mf_coords, mf_corr, mf_motion, mf_net, mf_inp, mf_delta, mf_weight, mf_agg;
+    std::vector<float> mf_host;
     int tiles_x = 0, tiles_y = 0;
 };
 
@@ -487,12 +592,16 @@ int upload(DevBuf& d, const std::vector<float>& v) {
     return SLK_OK;
 }
 
-// small 3x3 heads: weights [Co][128][9] fp16-rounded as float, in the
-// k_conv_small order (o, channel, tap)
-int pack_small(DevBuf& w, DevBuf& b, const UpdateState* s, int L) {
-    SLK_TRY(upload_rounded(w, s->hw_[L]));
-    SLK_TRY(upload(b, s->hb_[L]));
-    return SLK_OK;
+// small 3x3 heads: weights fp16-rounded as float in the k_conv_small order
+// [o][chunk][tap][16] (from the reference's [o][ci][3][3]); biases padded to 3
+void small_layout(const UpdateState* s, int L, std::vector<float>& w, std::vector<float>& b) {
+    const int co = kLayers[L].co;
+    for (int o = 0; o < co; o++)
+        for (int ch = 0; ch < 8; ch++)
+            for (int t = 0; t < 9; t++)
+                for (int i = 0; i < 16; i++)
+                    w.push_back(round_half_host(s->hw_[L][((size_t)o * 128 + ch * 16 + i) * 9 + t]));
+    for (int o = 0; o < 3; o++) b.push_back(o < co ? s->hb_[L][o] : 0.0f);
 }
 
 int pack_all(UpdateState* s) {
@@ -517,9 +626,17 @@ int pack_all(UpdateState* s) {
     }
     SLK_TRY(upload_rounded(s->glo_w, gw));
     SLK_TRY(upload(s->glo_b, gb));
-    SLK_TRY(pack_small(s->small_w[0], s->small_b[0], s, L_DL2));
-    SLK_TRY(pack_small(s->small_w[1], s->small_b[1], s, L_WT2));
-    SLK_TRY(pack_small(s->small_w[2], s->small_b[2], s, L_ETA));
+    {
+        std::vector<float> w, b;  // delta_2 then weight_2: one launch, two heads
+        small_layout(s, L_DL2, w, b);
+        small_layout(s, L_WT2, w, b);
+        SLK_TRY(upload(s->small_w[0], w));
+        SLK_TRY(upload(s->small_b[0], b));
+        std::vector<float> we, be;
+        small_layout(s, L_ETA, we, be);
+        SLK_TRY(upload(s->small_w[2], we));
+        SLK_TRY(upload(s->small_b[2], be));
+    }
     SLK_HIP(hipDeviceSynchronize());
     s->packed = true;
     return SLK_OK;
@@ -537,8 +654,14 @@ int launch_conv(const UpdateState* s, const PackedConv& pc, ConvArgs a, int N,
     a.w = s->w;
     a.tiles_x = s->tiles_x;
     if (a.s0.nchunk > a.nchunk) a.s0.nchunk = a.nchunk;
-    hipLaunchKernelGGL((k_conv<KS, EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
-                       dim3(256), 0, stream, a);
+    if constexpr (KS == 1) {
+        const int hw = s->h * s->w;
+        hipLaunchKernelGGL((k_conv1x1<EPI>), dim3(pc.co_tot / kCoT, (hw + 255) / 256, N),
+                           dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_conv<KS, EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
+                           dim3(256), 0, stream, a);
+    }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -605,7 +728,9 @@ extern "C" int slk_update_destroy(slk_update* u) {
     }
     for (DevBuf* b : {&s.glo_w, &s.glo_b, &s.small_w[0], &s.small_w[1], &s.small_w[2],
                       &s.small_b[0], &s.small_b[1], &s.small_b[2], &s.corr16, &s.mot16, &s.cat,
-                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t})
+                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t, &s.mf_coords,
+                      &s.mf_corr, &s.mf_motion, &s.mf_net, &s.mf_inp, &s.mf_delta, &s.mf_weight,
+                      &s.mf_agg})
         b->release();
     delete u;
     return SLK_OK;
@@ -771,13 +896,24 @@ extern "C" int slk_update_forward(slk_update* u, const float* corr, const float*
         a.out32 = agg_conv1_out;
         a.out32_nstride = 128L * hw;
         SLK_TRY((launch_conv<3, kEpiHeads>(&s, s.heads, a, N, stream)));
-        const dim3 g((hw + 255) / 256, N);
-        hipLaunchKernelGGL(k_conv_small, g, dim3(256), 0, stream, s.zr_buf.as<_Float16>(), zrS,
-                           8, s.small_w[0].as<float>(), s.small_b[0].as<float>(), 3, s.h, s.w, 0,
-                           delta_out, 3L * hw);
-        hipLaunchKernelGGL(k_conv_small, g, dim3(256), 0, stream,
-                           s.zr_buf.as<_Float16>() + 8 * ck, zrS, 8, s.small_w[1].as<float>(),
-                           s.small_b[1].as<float>(), 3, s.h, s.w, 1, weight_out, 3L * hw);
+        SmallArgs m{};
+        m.in = s.zr_buf.as<_Float16>();  // delta_0 chunks 0..7, weight_0 chunks 8..15
+        m.in_nstride = zrS;
+        m.W = s.small_w[0].as<float>();
+        m.b = s.small_b[0].as<float>();
+        m.wstride = 3L * 8 * 9 * 16;
+        m.Co = 3;
+        m.h = s.h;
+        m.w = s.w;
+        m.tiles_x = s.tiles_x;
+        m.nheads = 2;
+        m.mode[0] = 0;
+        m.mode[1] = 1;
+        m.out[0] = delta_out;
+        m.out[1] = weight_out;
+        m.out_nstride = 3L * hw;
+        hipLaunchKernelGGL(k_conv_small, dim3(s.tiles_x * s.tiles_y, 2, N), dim3(256), 0, stream,
+                           m);
         SLK_HIP(hipGetLastError());
     }
     return SLK_OK;
@@ -809,9 +945,68 @@ extern "C" int slk_update_compute_eta(slk_update* u, float* agg_features, float*
     a.out16 = s.agg_t.as<_Float16>();
     a.out16_nstride = 8 * ck;
     SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.ag2, a, K, stream)));
-    hipLaunchKernelGGL(k_conv_small, dim3((hw + 255) / 256, K), dim3(256), 0, stream,
-                       s.agg_t.as<_Float16>(), 8 * ck, 8, s.small_w[2].as<float>(),
-                       s.small_b[2].as<float>(), 1, s.h, s.w, 2, eta_out, (long)hw);
+    SmallArgs m{};
+    m.in = s.agg_t.as<_Float16>();
+    m.in_nstride = 8 * ck;
+    m.W = s.small_w[2].as<float>();
+    m.b = s.small_b[2].as<float>();
+    m.Co = 1;
+    m.h = s.h;
+    m.w = s.w;
+    m.tiles_x = s.tiles_x;
+    m.nheads = 1;
+    m.mode[0] = 2;
+    m.out[0] = eta_out;
+    m.out_nstride = hw;
+    hipLaunchKernelGGL(k_conv_small, dim3(s.tiles_x * s.tiles_y, 1, K), dim3(256), 0, stream, m);
     SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+extern "C" int slk_motion_filter(slk_ctx* ctx, slk_update* u, const void* f_last,
+                                 const void* f_cur, int dtype, const float* net_kf,
+                                 const float* inp_kf, float* mean_flow, hipStream_t stream) {
+    if (!ctx || !u || !f_last || !f_cur || !net_kf || !inp_kf || !mean_flow)
+        return fail(SLK_E_ARG, "motion_filter: null argument");
+    UpdateState& s = u->s;
+    if (ctx->h != s.h || ctx->w != s.w)
+        return fail(SLK_E_ARG, "motion_filter: context and update module map sizes differ");
+    if (ctx->levels != 4) return fail(SLK_E_ARG, "motion_filter: needs a 4-level context");
+    const int hw = s.h * s.w;
+    const size_t f4 = sizeof(float);
+    if (!s.mf_coords.ptr) {
+        SLK_TRY(s.mf_coords.ensure(2 * hw * f4));
+        SLK_TRY(s.mf_corr.ensure(196 * hw * f4));
+        SLK_TRY(s.mf_motion.ensure(4 * hw * f4));
+        SLK_TRY(s.mf_net.ensure(128 * hw * f4));
+        SLK_TRY(s.mf_inp.ensure(128 * hw * f4));
+        SLK_TRY(s.mf_delta.ensure(3 * hw * f4));
+        SLK_TRY(s.mf_weight.ensure(3 * hw * f4));
+        SLK_TRY(s.mf_agg.ensure(128 * hw * f4));
+        s.mf_host.resize(2 * (size_t)hw);
+    }
+    // build_correlation(last_kf, temp slot) and the lookup at the identity
+    // grid (main.cu:1939-1951)
+    SLK_TRY(slk_corr_build(ctx, f_last, f_cur, dtype, stream));
+    SLK_TRY(slk_fill_coords0(s.mf_coords.as<float>(), 1, s.h, s.w, stream));
+    SLK_TRY(slk_corr_sample(ctx, s.mf_coords.as<float>(), s.mf_corr.as<float>(), stream));
+    // the keyframe's hidden state and context, zero motion (main.cu:1954-1961)
+    SLK_HIP(hipMemcpyAsync(s.mf_net.ptr, net_kf, 128 * hw * f4, hipMemcpyDeviceToDevice, stream));
+    SLK_HIP(hipMemcpyAsync(s.mf_inp.ptr, inp_kf, 128 * hw * f4, hipMemcpyDeviceToDevice, stream));
+    SLK_HIP(hipMemsetAsync(s.mf_motion.ptr, 0, 4 * hw * f4, stream));
+    SLK_TRY(slk_update_forward(u, s.mf_corr.as<float>(), s.mf_motion.as<float>(),
+                               s.mf_net.as<float>(), s.mf_inp.as<float>(), s.mf_delta.as<float>(),
+                               s.mf_weight.as<float>(), s.mf_agg.as<float>(), 1, stream));
+    // mean flow magnitude of delta's first two channels, summed on the host in
+    // pixel order as the reference does (main.cu:1970-1981)
+    SLK_HIP(hipMemcpyAsync(s.mf_host.data(), s.mf_delta.ptr, 2 * hw * f4, hipMemcpyDeviceToHost,
+                           stream));
+    SLK_HIP(hipStreamSynchronize(stream));
+    float sum = 0.0f;
+    for (int k = 0; k < hw; k++) {
+        const float dx = s.mf_host[k], dy = s.mf_host[hw + k];
+        sum += std::sqrt(dx * dx + dy * dy);
+    }
+    *mean_flow = sum / (float)hw;
     return SLK_OK;
 }

@@ -42,7 +42,7 @@ EXPORTS = [
     "slk_rm_keyframe",
     "slk_update_create", "slk_update_destroy", "slk_update_num_layers", "slk_update_layer_name",
     "slk_update_layer_shape", "slk_update_set_conv", "slk_update_load_dir", "slk_update_forward",
-    "slk_update_compute_eta",
+    "slk_update_compute_eta", "slk_motion_filter",
 ]
 
 
@@ -134,6 +134,7 @@ def lib():
             "slk_update_load_dir": [P, ctypes.c_char_p],
             "slk_update_forward": [P, P, P, P, P, P, P, P, I, P],
             "slk_update_compute_eta": [P, P, P, I, P],
+            "slk_motion_filter": [P, P, P, P, I, P, P, ctypes.POINTER(F), P],
         })
         for name, args in sig.items():
             fn = getattr(L_, name)
@@ -456,6 +457,14 @@ class UpdateModule:
 
     def compute_eta(self, agg, eta, num_kf, stream=None):
         check(lib().slk_update_compute_eta(self.ptr, _p(agg), _p(eta), num_kf, stream))
+
+    def motion_filter(self, ctx, f_last, f_cur, net_kf, inp_kf, dtype=SLK_F32, stream=None):
+        """compute_motion_gru: mean flow magnitude of one update step between
+        the last keyframe and the current frame."""
+        out = F()
+        check(lib().slk_motion_filter(ctx.ptr, self.ptr, _p(f_last), _p(f_cur), dtype,
+                                      _p(net_kf), _p(inp_kf), ctypes.byref(out), stream))
+        return out.value
 
     def close(self):
         if self.ptr:

@@ -245,3 +245,48 @@ extern "C" int adapter_glue(int h, int w, int E, int bs, int B, int nkf, const i
         (void)hipFree(p);
     return bad;
 }
+
+// UpdateModule (main.cu:535-667) through the adapter: weights from the
+// reference's tensor files in `dir`, forward on host inputs corr
+// [B][196][hw], motion [B][4][hw], net [B][128][hw] (updated), inp, then
+// compute_eta on agg_kf [K][128][hw]; and the motion filter between frames 0
+// and 1 of fmaps [2][128][hw] fp32 from state 0 of net/inp (before the
+// update), written to *mean_flow.
+extern "C" int adapter_update(const char* dir, int B, int K, int h, int w, const float* corr,
+                              const float* motion, float* net, const float* inp, float* delta,
+                              float* weight, float* agg, const float* agg_kf, float* eta,
+                              const float* fmaps, float* mean_flow) {
+    const size_t hw = (size_t)h * w;
+    float* d_c = upload(corr, B * 196 * hw);
+    float* d_m = upload(motion, B * 4 * hw);
+    float* d_n = upload(net, B * 128 * hw);
+    float* d_i = upload(inp, B * 128 * hw);
+    float* d_k = upload(agg_kf, K * 128 * hw);
+    float* d_f = upload(fmaps, 2 * 128 * hw);
+    float *d_d = nullptr, *d_w = nullptr, *d_a = nullptr, *d_e = nullptr;
+    if (!d_c || !d_m || !d_n || !d_i || !d_k || !d_f ||
+        hipMalloc(&d_d, B * 3 * hw * 4) != hipSuccess ||
+        hipMalloc(&d_w, B * 3 * hw * 4) != hipSuccess ||
+        hipMalloc(&d_a, B * 128 * hw * 4) != hipSuccess ||
+        hipMalloc(&d_e, K * hw * 4) != hipSuccess)
+        return 1;
+    slk_droid::UpdateModule update;
+    update.init(nullptr, dir, B, h, w);
+    slk_droid::CorrEngine corr_engine;
+    const int ii[1] = {0}, jj[1] = {1};
+    corr_engine.init(h, w, d_f, SLK_F32, ii, jj, 1);
+    *mean_flow = corr_engine.compute_motion_gru(update.module(), 0, 1, d_n, d_i);
+    update.forward(nullptr, d_c, d_m, d_n, d_i, d_d, d_w, d_a, nullptr, nullptr, nullptr, B, h, w);
+    update.compute_eta(nullptr, d_k, d_e, nullptr, nullptr, nullptr, K, h, w);
+    int bad = download(net, d_n, B * 128 * hw);
+    bad |= download(delta, d_d, B * 3 * hw);
+    bad |= download(weight, d_w, B * 3 * hw);
+    bad |= download(agg, d_a, B * 128 * hw);
+    bad |= download(eta, d_e, K * hw);
+    corr_engine.destroy();
+    update.destroy();
+    for (void* p : {(void*)d_c, (void*)d_m, (void*)d_n, (void*)d_i, (void*)d_k, (void*)d_f,
+                    (void*)d_d, (void*)d_w, (void*)d_a, (void*)d_e})
+        (void)hipFree(p);
+    return bad;
+}

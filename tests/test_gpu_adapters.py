@@ -32,6 +32,7 @@ def harness():
     lib.adapter_corr.argtypes = [P, I, I, I, I, P, P, I, P, P, P]
     lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, P]
     lib.adapter_corrblock.argtypes = [P, P, I, I, I, I, P, P, P, P, I, I, P, P]
+    lib.adapter_update.argtypes = [ctypes.c_char_p, I, I, I, I] + [P] * 11
     lib.adapter_glue.argtypes = [I, I, I, I, I, I] + [P] * 12 + [I] + [P] * 4 + [P] * 14
     return lib
 
@@ -175,3 +176,42 @@ def test_update_glue_batch(harness):
     np.testing.assert_array_equal(out["bjj"][:m], es["jj"])
     np.testing.assert_array_equal(out["bt"][:m], es["target"])
     np.testing.assert_array_equal(out["bw"][:m], es["weight"])
+
+
+def test_update_module_and_motion_filter(harness, tmp_path):
+    """UpdateModule init/forward/compute_eta (main.cu:535-667) with weights
+    read from the reference's tensor files, and CorrEngine::compute_motion_gru
+    (main.cu:1934-1983), against the oracle at the update bars of
+    test_gpu_update.py."""
+    from oracle import update_oracle as uo
+    announce("adapters: UpdateModule + motion filter")
+    h, w, B, K = 16, 24, 3, 2
+    P = uo.seeded_weights(50)
+    for name, (wt, b) in P.items():
+        uo.save_bin(os.path.join(tmp_path, name + "_weight.bin"), wt)
+        uo.save_bin(os.path.join(tmp_path, name + "_bias.bin"), b)
+    corr, motion, net, inp = uo.seeded_inputs(B, h, w, seed=51)
+    agg_kf = np.random.default_rng(52).uniform(0, 2, (K, 128, h, w)).astype(np.float32)
+    f = wl.frames(2, C=128, h=h, w=w, seed=53)
+    net_io = net.copy()
+    delta = np.zeros((B, 3, h, w), np.float32)
+    weight = np.zeros((B, 3, h, w), np.float32)
+    agg = np.zeros((B, 128, h, w), np.float32)
+    eta = np.zeros((K, 1, h, w), np.float32)
+    mean = np.zeros(1, np.float32)
+    st = harness.adapter_update(os.fsencode(str(tmp_path)), B, K, h, w, _p(corr), _p(motion),
+                                _p(net_io), _p(inp), _p(delta), _p(weight), _p(agg), _p(agg_kf),
+                                _p(eta), _p(f), _p(mean))
+    assert st == 0
+    rn, rd, rw, ra = uo.update_forward(P, corr, motion, net, inp)
+    for got, ref, what in ((net_io, rn, "net"), (delta, rd, "delta"), (weight, rw, "weight"),
+                           (agg, ra, "agg"), (eta, uo.compute_eta(P, agg_kf), "eta")):
+        assert_close_rel(got, ref, tol=5e-3, what=what)
+        assert norm_rel(got, ref) < 2e-3, what
+    grid = wl.grid_coords(h, w)[None].astype(np.float32)
+    lk = orc.corr_batch(f, np.array([0], np.int32), np.array([1], np.int32), grid, 1.0 / 16.0)
+    _, d1, _, _ = uo.update_forward(P, lk.reshape(1, 196, h, w),
+                                    np.zeros((1, 4, h, w), np.float32), net[:1], inp[:1])
+    mag = np.sqrt(d1[0, 0] ** 2 + d1[0, 1] ** 2).astype(np.float32).reshape(-1)
+    ref = float(np.cumsum(mag, dtype=np.float32)[-1] / np.float32(h * w))
+    assert abs(float(mean[0]) - ref) <= 2e-3 * abs(ref)

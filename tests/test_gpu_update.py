@@ -126,3 +126,41 @@ def test_weights_from_reference_tensor_files(slk, tmp_path):
     with pytest.raises(slk.SlkError):  # no weights set
         fresh.forward(x, x, x, x, x, x, x, 1)
     fresh.close()
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_motion_filter(slk, f16):
+    """compute_motion_gru (main.cu:1934-1983): the single-edge correlation of
+    (last keyframe, current frame) sampled at the identity grid, one update
+    step from the keyframe's state with zero motion, then the mean flow
+    magnitude of delta; against the oracle lookup + update operator, and the
+    keyframe's state is left unchanged. fp16 fmaps are the reference's
+    storage (main.cu:677)."""
+    from oracle import oracle as orc
+    import workloads as wl
+    orc.build()
+    announce(f"motion filter 48x64 fp16={f16}")
+    h, w = 48, 64
+    P = uo.seeded_weights(40)
+    f = wl.frames(2, C=128, h=h, w=w, seed=41)
+    if f16:
+        f = f.astype(np.float16)
+    _, _, net, inp = uo.seeded_inputs(1, h, w, seed=42)
+    ctx = slk.Context(h, w, C=128, max_batch=1, corr_scale=wl.CORR_ALPHA_REF)
+    um = slk.UpdateModule(1, h, w)
+    um.set_weights(P)
+    D = slk.DeviceArray.from_host
+    d0, d1, dn, di = D(f[0]), D(f[1]), D(net[0]), D(inp[0])
+    dt = slk.SLK_F16 if f16 else slk.SLK_F32
+    got = um.motion_filter(ctx, d0, d1, dn, di, dtype=dt)
+    np.testing.assert_array_equal(dn.to_host(), net[0])
+    ctx.close()
+    um.close()
+    grid = wl.grid_coords(h, w)[None].astype(np.float32)
+    corr = orc.corr_batch(f.astype(np.float32), np.array([0], np.int32), np.array([1], np.int32),
+                          grid, wl.CORR_ALPHA_REF)
+    _, delta, _, _ = uo.update_forward(P, corr.reshape(1, 196, h, w),
+                                       np.zeros((1, 4, h, w), np.float32), net, inp)
+    mag = np.sqrt(delta[0, 0] ** 2 + delta[0, 1] ** 2).astype(np.float32).reshape(-1)
+    ref = float(np.cumsum(mag, dtype=np.float32)[-1] / np.float32(h * w))
+    assert abs(got - ref) <= 2e-3 * abs(ref), (got, ref)
