@@ -30,6 +30,10 @@ frames of 128x54x96 features, 64 edges in one launch, 3 BA iterations over
 ConvGRU on the 48-edge window, then compute_eta of the 12 keyframes,
 main.cu:385-667) and prints one JSON line for it.
 
+`--encode` times the front of the pipe for one 384x512 frame: the NV12
+1920x1080 -> 512x384 BGR conversion (main.cu:947-985) and encode_frame
+(fnet + cnet fp16 encoders, main.cu:1465-1497), and prints one JSON line.
+
 `--glue` times the update-pass glue around the path (motion/target kernels,
 hidden-state gathers and scatters, the keyframe scatter-mean, the BA edge
 set) for one 48-edge batch and prints one JSON line for it.
@@ -87,6 +91,8 @@ def parse():
     ap.add_argument("--update", action="store_true",
                     help="time the update operator (UpdateModule forward of the 48-edge "
                          "window + compute_eta of its 12 keyframes) instead")
+    ap.add_argument("--encode", action="store_true",
+                    help="time the decode conversion + encode_frame of one 384x512 frame instead")
     ap.add_argument("--glue", action="store_true",
                     help="time the update-pass glue of one 48-edge batch instead")
     ap.add_argument("--cpu-edges", type=int, default=48,
@@ -115,6 +121,8 @@ def main():
         return glue(args, slk, wl, H)
     if args.update:
         return update(args, slk, wl, H)
+    if args.encode:
+        return encode(args, slk, wl, H)
     if args.graph:
         return graph(args, slk, wl, H)
 
@@ -398,6 +406,110 @@ def update_flops(h, w, B, K):
     for n in eta:
         fwd.pop(n)
     return fwd, eta
+
+
+def encoder_flops(H_, W_, out_dim):
+    """Algorithmic flops of one HalfBasicEncoder forward on an H x W frame:
+    2 * Co * Ci * k^2 per output pixel of every convolution (main.cu:316-353
+    shapes)."""
+    from oracle import encoder_oracle as eo
+    total, h, w = 0.0, H_, W_
+    for suffix, co, ci, k, s in eo.LAYERS:
+        co = out_dim if co is None else co
+        if suffix in ("conv1", "layer2_0_conv1", "layer3_0_conv1"):
+            h, w = h // 2, w // 2
+        total += 2.0 * co * ci * k * k * h * w
+    return total
+
+
+def encode(args, slk, wl, H):
+    """The front of the pipe for one frame: NV12 1920x1080 -> BGR 512x384
+    (bilinear, BT.709) and encode_frame (fnet 128 with instance norm, cnet
+    256) on seeded weights of the reference's shapes. One JSON line: frames/s
+    of encode_frame, its achieved fp16 MFMA TFLOP/s against the 2.5 PFLOP/s
+    dense peak, and the decode conversion's time and HBM rate."""
+    sys.path.insert(0, ROOT)
+    from oracle import encoder_oracle as eo
+    Hf, Wf, sw, sh = 384, 512, 1920, 1080
+    Pf = eo.seeded_weights("fnet", 128, seed=0)
+    Pc = eo.seeded_weights("cnet", 256, seed=1)
+    fnet = slk.Encoder(Hf, Wf, 128, True)
+    cnet = slk.Encoder(Hf, Wf, 256, False)
+    fnet.set_weights(Pf, "fnet")
+    cnet.set_weights(Pc, "cnet")
+    bgr = eo.seeded_frame(Hf, Wf, seed=2)
+    rng = np.random.default_rng(3)
+    D = slk.DeviceArray.from_host
+    d_bgr = D(bgr)
+    d_y = D(rng.integers(0, 256, (sh, sw), dtype=np.uint8))
+    d_uv = D(rng.integers(0, 256, (sh // 2, sw), dtype=np.uint8))
+    d_out = slk.DeviceArray((Hf, Wf, 3))
+    fmap = slk.DeviceArray((128, Hf // 8, Wf // 8), np.float16)
+    net = slk.DeviceArray((128, Hf // 8, Wf // 8))
+    inp = slk.DeviceArray((128, Hf // 8, Wf // 8))
+    stream = H.stream()
+
+    def enc():
+        slk.encode_frame(fnet, cnet, d_bgr, fmap, net, inp, stream=stream)
+
+    def dec():
+        slk.nv12_to_bgr(d_y, d_uv, d_out, sw, sh, sw, sw, Wf, Hf, stream=stream)
+
+    def timed(fn, k):
+        H.sync()
+        e0, e1 = H.event(), H.event()
+        H.record(e0, stream)
+        for _ in range(k):
+            fn()
+        H.record(e1, stream)
+        ms = H.elapsed_ms(e0, e1)
+        H.sync()
+        return ms / k
+
+    for _ in range(max(3, args.warmup)):
+        dec()
+        enc()
+    H.sync()
+    k = max(5, min(args.steps, 50))
+    t0w = time.perf_counter()
+    e_ms = timed(enc, k)
+    wall = time.perf_counter() - t0w
+    d_ms = timed(dec, k)
+    fl = encoder_flops(Hf, Wf, 128) + encoder_flops(Hf, Wf, 256)
+    peak = PEAK_BF16_TFLOPS
+    # decode bytes: the 2x2 Y neighbourhoods and UV samples come through
+    # the caches; algorithmic = Y plane + UV plane read once, BGR written
+    dec_bytes = sw * sh * 1.5 + Hf * Wf * 12
+    tc = time.perf_counter()
+    eo.encode_frame(bgr, Pf, Pc)
+    cpu_s = time.perf_counter() - tc
+    out = {
+        "metric": "front of the pipe: encode_frame (fnet + cnet) of a 384x512 frame, 1 MI355X",
+        "value": round(1e3 / e_ms, 1),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": k,
+        "higher_is_better": True,
+        "dtype": "f16 activations and MFMA operands, f32 accumulation (the reference's fp16 "
+                 "cuDNN convolutions)",
+        "data": "synthetic (seeded weights of the reference's shapes, a structured BGR frame)",
+        "config": {"workload": "encode_frame", "H": Hf, "W": Wf},
+        "encode_frame_ms": round(e_ms, 4),
+        "roofline": {"kernel": "encode_frame (every convolution of fnet and cnet)",
+                     "bound": "mfma", "achieved": round(fl / (e_ms * 1e-3) / 1e12, 2),
+                     "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(fl / (e_ms * 1e-3) / 1e12 / peak, 4), "traffic": None,
+                     "algorithmic_flop": fl},
+        "nv12_to_bgr_ms": round(d_ms, 4),
+        "nv12_to_bgr_GBs": round(dec_bytes / (d_ms * 1e-3) / 1e9, 1),
+        "cpu_baseline": {"value": round(1.0 / cpu_s, 3), "unit": "frames/s", "cores": 1,
+                         "kind": "port",
+                         "sample": "one frame through the numpy oracle (float64 sums)"},
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(out), flush=True)
+    fnet.close()
+    cnet.close()
 
 
 def update(args, slk, wl, H):

@@ -23,6 +23,7 @@
 #define SLK_H
 
 #include <stddef.h>
+#include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
 #ifdef __cplusplus
@@ -443,6 +444,81 @@ int slk_update_compute_eta(slk_update* um, float* agg_features, float* eta_out, 
 int slk_motion_filter(slk_ctx* ctx, slk_update* um, const void* f_last, const void* f_cur,
                       int dtype, const float* net_kf, const float* inp_kf, float* mean_flow,
                       hipStream_t stream);
+
+/* ------------------------------------------------------------- encoders */
+/* HalfBasicEncoder (cuda_slam/main.cu:306-381) with its HalfResBlocks
+ * (:236-303): the fp16 feature (fnet: output_dim 128, instance norm) and
+ * context (cnet: 256, no norm) networks of DROID-SLAM. conv1 7x7 stride 2,
+ * three stages of two residual blocks (32, 64 stride 2, 128 stride 2), conv2
+ * 1x1: [3][H][W] -> [output_dim][H/8][W/8]. Every convolution is an fp16
+ * MFMA GEMM with fp32 accumulation; outputs are rounded to fp16 before and
+ * after the fp32 bias as the reference's cuDNN call + bias_add_half_kernel
+ * do (nn.cuh:657-791), and instance norm (nn.cuh:609-654) has eps 1e-5. */
+typedef struct slk_encoder slk_encoder;
+
+/* HalfBasicEncoder::init(cudnn, ws, prefix, batch, inH, inW, out_dim,
+ * use_norm), main.cu:316-353, without the weights (set separately).
+ * in_h, in_w multiples of 8; out_dim a multiple of 16, at most 256. */
+int slk_encoder_create(slk_encoder** enc, int in_h, int in_w, int out_dim, int use_norm,
+                       int max_batch);
+int slk_encoder_destroy(slk_encoder* enc);
+
+/* The 16 convolutions in a fixed order; layer i's weight files are
+ * <prefix>_<suffix>_weight.bin / _bias.bin (conv1, layer1_0_conv1, ...,
+ * layer2_0_downsample_0, ..., conv2; WeightStore::load_conv, main.cu:81-86). */
+int slk_encoder_num_layers(void);
+const char* slk_encoder_layer_suffix(int layer);
+int slk_encoder_layer_shape(const slk_encoder* enc, int layer, int* co, int* ci, int* k,
+                            int* stride);
+
+/* Weights of one layer as host fp32 arrays (weight [co][ci][k][k], bias
+ * [co]); rounded to fp16 and repacked before the next forward
+ * (HalfConvLayer::init converts them with float_to_half, nn.cuh:683-690). */
+int slk_encoder_set_conv(slk_encoder* enc, int layer, const float* weight_host,
+                         const float* bias_host);
+int slk_encoder_load_dir(slk_encoder* enc, const char* dir, const char* prefix);
+
+/* HalfBasicEncoder::forward(cudnn, input, output, ...), main.cu:357-380:
+ * input [B][3][H][W] fp32 (converted to fp16 like float_to_half) ->
+ * output [B][out_dim][H/8][W/8] fp16. 1 <= B <= max_batch. */
+int slk_encoder_forward(slk_encoder* enc, const float* input, void* output_f16, int batch,
+                        hipStream_t stream);
+
+/* CudaDroid::encode_frame(bgr_hwc), main.cu:1465-1497: preprocess the BGR
+ * frame [H][W][3] (0..255; preprocess_image_kernel, main.cu:1062-1075), run
+ * fnet -> fmap [128][H/8][W/8] fp16 and cnet -> net = tanh(cmap[0:128]),
+ * inp = relu(cmap[128:256]) as fp32 [128][H/8][W/8]. fnet must have out_dim
+ * 128, cnet 256, both max_batch >= 1 and the same image size. */
+int slk_encode_frame(slk_encoder* fnet, slk_encoder* cnet, const float* bgr_hwc, void* fmap_f16,
+                     float* net, float* inp, hipStream_t stream);
+
+/* ------------------------------------------------------ front of the pipe */
+/* nv12_to_bgr_resize_kernel, main.cu:947-985: an NV12 frame (Y plane and
+ * interleaved half-resolution UV plane, strides in bytes) -> float BGR
+ * [dst_h][dst_w][3] in 0..255, bilinear Y, nearest UV, BT.709. */
+int slk_nv12_to_bgr(const uint8_t* y_plane, const uint8_t* uv_plane, float* bgr_out, int src_w,
+                    int src_h, int y_stride, int uv_stride, int dst_w, int dst_h,
+                    hipStream_t stream);
+/* p010_to_bgr_resize_kernel, main.cu:988-1027: the same from P010 (10 bits
+ * in the top of each 16-bit sample, scaled to the 8-bit range); strides in
+ * bytes. */
+int slk_p010_to_bgr(const uint16_t* y_plane, const uint16_t* uv_plane, float* bgr_out, int src_w,
+                    int src_h, int y_stride_bytes, int uv_stride_bytes, int dst_w, int dst_h,
+                    hipStream_t stream);
+/* bgr8_to_bgrf_resize_kernel, main.cu:1030-1058: 8-bit BGR (row stride in
+ * bytes) -> float BGR with bilinear resize. */
+int slk_bgr8_to_bgrf(const uint8_t* bgr_in, float* bgr_out, int src_w, int src_h, int src_stride,
+                     int dst_w, int dst_h, hipStream_t stream);
+/* preprocess_image_kernel, main.cu:1062-1075: BGR HWC (0..255) -> RGB NCHW,
+ * (x/255 - mean) / std with the ImageNet mean and std. */
+int slk_preprocess_image(const float* bgr_hwc, float* rgb_nchw, int H, int W, hipStream_t stream);
+
+/* The pose file of main.cu:2924-2937 ([num_keyframes: i32]
+ * [timestamps: i32 x nk] [poses: f32 x nk x 7]); with cam_to_world the
+ * world->camera poses are inverted first in the reference's float
+ * arithmetic (main.cu:2896-2914). poses are host memory. */
+int slk_write_poses_bin(const char* path, int num_keyframes, const int* timestamps,
+                        const float* poses, int cam_to_world);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,11 @@ EXPORTS = [
     "slk_update_create", "slk_update_destroy", "slk_update_num_layers", "slk_update_layer_name",
     "slk_update_layer_shape", "slk_update_set_conv", "slk_update_load_dir", "slk_update_forward",
     "slk_update_compute_eta", "slk_motion_filter",
+    "slk_encoder_create", "slk_encoder_destroy", "slk_encoder_num_layers",
+    "slk_encoder_layer_suffix", "slk_encoder_layer_shape", "slk_encoder_set_conv",
+    "slk_encoder_load_dir", "slk_encoder_forward", "slk_encode_frame",
+    "slk_nv12_to_bgr", "slk_p010_to_bgr", "slk_bgr8_to_bgrf", "slk_preprocess_image",
+    "slk_write_poses_bin",
 ]
 
 
@@ -135,6 +140,20 @@ def lib():
             "slk_update_forward": [P, P, P, P, P, P, P, P, I, P],
             "slk_update_compute_eta": [P, P, P, I, P],
             "slk_motion_filter": [P, P, P, P, I, P, P, ctypes.POINTER(F), P],
+            "slk_encoder_create": [ctypes.POINTER(P), I, I, I, I, I],
+            "slk_encoder_destroy": [P],
+            "slk_encoder_num_layers": [],
+            "slk_encoder_layer_shape": [P, I, ctypes.POINTER(I), ctypes.POINTER(I),
+                                        ctypes.POINTER(I), ctypes.POINTER(I)],
+            "slk_encoder_set_conv": [P, I, P, P],
+            "slk_encoder_load_dir": [P, ctypes.c_char_p, ctypes.c_char_p],
+            "slk_encoder_forward": [P, P, P, I, P],
+            "slk_encode_frame": [P, P, P, P, P, P, P],
+            "slk_nv12_to_bgr": [P, P, P, I, I, I, I, I, I, P],
+            "slk_p010_to_bgr": [P, P, P, I, I, I, I, I, I, P],
+            "slk_bgr8_to_bgrf": [P, P, I, I, I, I, I, P],
+            "slk_preprocess_image": [P, P, I, I, P],
+            "slk_write_poses_bin": [ctypes.c_char_p, I, P, P, I],
         })
         for name, args in sig.items():
             fn = getattr(L_, name)
@@ -144,6 +163,8 @@ def lib():
         L_.slk_oldest_edges_mask.restype = None
         L_.slk_update_layer_name.argtypes = [I]
         L_.slk_update_layer_name.restype = ctypes.c_char_p
+        L_.slk_encoder_layer_suffix.argtypes = [I]
+        L_.slk_encoder_layer_suffix.restype = ctypes.c_char_p
         L_.slk_last_error.argtypes = []
         L_.slk_last_error.restype = ctypes.c_char_p
         _lib = L_
@@ -476,3 +497,88 @@ class UpdateModule:
             self.close()
         except Exception:
             pass
+
+
+class Encoder:
+    """slk_encoder_*: HalfBasicEncoder (cuda_slam/main.cu:306-381), the fp16
+    feature (fnet: out_dim 128, instance norm) or context (cnet: 256, no
+    norm) network, on device arrays."""
+
+    def __init__(self, in_h, in_w, out_dim, use_norm, max_batch=1):
+        self.in_h, self.in_w, self.out_dim = in_h, in_w, out_dim
+        p = P()
+        check(lib().slk_encoder_create(ctypes.byref(p), in_h, in_w, out_dim, int(use_norm),
+                                       max_batch))
+        self.ptr = p
+
+    def layers(self):
+        """[(suffix, co, ci, k, stride)] in the ABI's layer order."""
+        L_ = lib()
+        out = []
+        for i in range(L_.slk_encoder_num_layers()):
+            co, ci, k, s = I(), I(), I(), I()
+            check(L_.slk_encoder_layer_shape(self.ptr, i, ctypes.byref(co), ctypes.byref(ci),
+                                             ctypes.byref(k), ctypes.byref(s)))
+            out.append((L_.slk_encoder_layer_suffix(i).decode(), co.value, ci.value, k.value,
+                        s.value))
+        return out
+
+    def set_weights(self, weights, prefix):
+        """weights: {prefix_suffix: (w [co, ci, k, k], b [co]) float32}."""
+        for i, (suffix, co, ci, k, _) in enumerate(self.layers()):
+            w, b = weights[f"{prefix}_{suffix}"]
+            w = np.ascontiguousarray(w, np.float32)
+            b = np.ascontiguousarray(b, np.float32)
+            assert w.shape == (co, ci, k, k) and b.shape == (co,), suffix
+            check(lib().slk_encoder_set_conv(self.ptr, i, w.ctypes.data, b.ctypes.data))
+
+    def load_dir(self, path, prefix):
+        check(lib().slk_encoder_load_dir(self.ptr, os.fsencode(path), prefix.encode()))
+
+    def forward(self, image, out, batch=1, stream=None):
+        """image [B][3][H][W] fp32 -> out [B][out_dim][H/8][W/8] fp16."""
+        check(lib().slk_encoder_forward(self.ptr, _p(image), _p(out), batch, stream))
+
+    def close(self):
+        if self.ptr:
+            lib().slk_encoder_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def encode_frame(fnet, cnet, bgr, fmap, net, inp, stream=None):
+    """CudaDroid::encode_frame: BGR [H][W][3] -> fmap fp16, net / inp fp32."""
+    check(lib().slk_encode_frame(fnet.ptr, cnet.ptr, _p(bgr), _p(fmap), _p(net), _p(inp), stream))
+
+
+def nv12_to_bgr(y, uv, out, src_w, src_h, y_stride, uv_stride, dst_w, dst_h, stream=None):
+    check(lib().slk_nv12_to_bgr(_p(y), _p(uv), _p(out), src_w, src_h, y_stride, uv_stride,
+                                dst_w, dst_h, stream))
+
+
+def p010_to_bgr(y, uv, out, src_w, src_h, y_stride_bytes, uv_stride_bytes, dst_w, dst_h,
+                stream=None):
+    check(lib().slk_p010_to_bgr(_p(y), _p(uv), _p(out), src_w, src_h, y_stride_bytes,
+                                uv_stride_bytes, dst_w, dst_h, stream))
+
+
+def bgr8_to_bgrf(src, out, src_w, src_h, stride, dst_w, dst_h, stream=None):
+    check(lib().slk_bgr8_to_bgrf(_p(src), _p(out), src_w, src_h, stride, dst_w, dst_h, stream))
+
+
+def preprocess_image(bgr, rgb, H, W, stream=None):
+    check(lib().slk_preprocess_image(_p(bgr), _p(rgb), H, W, stream))
+
+
+def write_poses_bin(path, timestamps, poses, cam_to_world=False):
+    """The reference's pose file: [nk: i32][timestamps: i32 x nk][poses: f32 x nk x 7]."""
+    ts = np.ascontiguousarray(timestamps, np.int32)
+    ps = np.ascontiguousarray(poses, np.float32).reshape(-1, 7)
+    assert ts.shape[0] == ps.shape[0]
+    check(lib().slk_write_poses_bin(os.fsencode(path), ts.shape[0], ts.ctypes.data,
+                                    ps.ctypes.data, int(cam_to_world)))

@@ -85,3 +85,23 @@ def test_oldest_edges_mask_host_helper_matches_oracle():
         slk.lib().slk_oldest_edges_mask(age.ctypes.data_as(ctypes.c_void_p), n, k,
                                         got.ctypes.data_as(ctypes.c_void_p))
         np.testing.assert_array_equal(got, orc.oldest_mask(age, k))
+
+
+def test_write_poses_bin_matches_the_reference_file(tmp_path):
+    """slk_write_poses_bin (host-only) writes the file of main.cu:2924-2937,
+    bytewise equal to the oracle's, with and without the camera-to-world
+    inversion; a bad path is an error."""
+    import slk
+    from oracle import encoder_oracle as eo
+    rng = np.random.default_rng(3)
+    q = rng.normal(size=(6, 4))
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    poses = np.concatenate([rng.normal(0, 2, (6, 3)), q], 1).astype(np.float32)
+    ts = np.array([0, 4, 9, 15, 22, 30], np.int32)
+    for c2w in (False, True):
+        path = os.path.join(tmp_path, f"p{int(c2w)}.bin")
+        slk.write_poses_bin(path, ts, poses, c2w)
+        with open(path, "rb") as f:
+            assert f.read() == eo.poses_bin_bytes(ts, poses, c2w)
+    with pytest.raises(slk.SlkError):
+        slk.write_poses_bin(os.path.join(tmp_path, "no", "such", "dir.bin"), ts, poses)
