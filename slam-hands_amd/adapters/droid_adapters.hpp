@@ -267,6 +267,79 @@ class UpdateModule {
     int h_ = 0, w_ = 0;
 };
 
+// HalfBasicEncoder of cuda_slam/main.cu:306-381 with its member signatures.
+// init takes the reference's cuDNN handle (ignored) and a WeightStore; here
+// the store is its directory, and the prefix ("fnet" / "cnet") names the
+// weight files <dir>/<prefix>_<layer>_weight.bin as load_conv does. forward
+// keeps the reference's argument list; its three half buffers and the
+// workspace are not needed (the encoder owns its activations) and may be
+// null.
+class HalfBasicEncoder {
+  public:
+    void init(void* /*cudnn*/, const char* weight_dir, const char* prefix, int batch, int inH,
+              int inW, int out_dim, bool use_norm) {
+        check(slk_encoder_create(&enc_, inH, inW, out_dim, use_norm ? 1 : 0, batch),
+              "HalfBasicEncoder::init");
+        check(slk_encoder_load_dir(enc_, weight_dir, prefix), "HalfBasicEncoder::init (weights)");
+    }
+
+    // main.cu:357: FP32 input [batch][3][inH][inW] -> FP16 output
+    void forward(void* /*cudnn*/, float* input, void* output_half, void* /*buf_a*/,
+                 void* /*buf_b*/, void* /*buf_c*/, float* /*workspace*/, int batch, int /*inH*/,
+                 int /*inW*/) {
+        check(slk_encoder_forward(enc_, input, output_half, batch, nullptr),
+              "HalfBasicEncoder::forward");
+    }
+
+    void destroy() {
+        if (enc_) slk_encoder_destroy(enc_);
+        enc_ = nullptr;
+    }
+
+    slk_encoder* encoder() const { return enc_; }
+
+  private:
+    slk_encoder* enc_ = nullptr;
+};
+
+// CudaDroid::encode_frame (main.cu:1465-1497): the BGR frame [H][W][3] ->
+// fmap (fp16, the keyframe's slot of state.fmaps), net = tanh and inp = relu
+// of the context halves (fp32).
+inline void encode_frame(HalfBasicEncoder& fnet, HalfBasicEncoder& cnet, float* bgr_hwc,
+                         void* fmap_half, float* net, float* inp) {
+    check(slk_encode_frame(fnet.encoder(), cnet.encoder(), bgr_hwc, fmap_half, net, inp, nullptr),
+          "encode_frame");
+}
+
+// The decode-side conversions of main.cu:2729-2753 (launch shapes are the
+// library's own): NV12 / P010 planes from the hardware decoder, or a
+// CPU-decoded 8-bit BGR upload, to the float BGR frame of process_frame.
+inline void nv12_to_bgr_resize(const uint8_t* y, const uint8_t* uv, float* bgr, int src_w,
+                               int src_h, int y_stride, int uv_stride, int dst_w, int dst_h) {
+    check(slk_nv12_to_bgr(y, uv, bgr, src_w, src_h, y_stride, uv_stride, dst_w, dst_h, nullptr),
+          "nv12_to_bgr_resize");
+}
+inline void p010_to_bgr_resize(const uint16_t* y, const uint16_t* uv, float* bgr, int src_w,
+                               int src_h, int y_stride_bytes, int uv_stride_bytes, int dst_w,
+                               int dst_h) {
+    check(slk_p010_to_bgr(y, uv, bgr, src_w, src_h, y_stride_bytes, uv_stride_bytes, dst_w,
+                          dst_h, nullptr),
+          "p010_to_bgr_resize");
+}
+inline void bgr8_to_bgrf_resize(const uint8_t* bgr8, float* bgr, int src_w, int src_h,
+                                int src_stride, int dst_w, int dst_h) {
+    check(slk_bgr8_to_bgrf(bgr8, bgr, src_w, src_h, src_stride, dst_w, dst_h, nullptr),
+          "bgr8_to_bgrf_resize");
+}
+
+// The pose file written at the end of a run (main.cu:2893-2937): poses are
+// the host copy of state.poses, timestamps the keyframes' frame indices.
+inline void save_poses(const char* path, int num_keyframes, const int* timestamps,
+                       const float* poses_host, bool cam_to_world) {
+    check(slk_write_poses_bin(path, num_keyframes, timestamps, poses_host, cam_to_world ? 1 : 0),
+          "save_poses");
+}
+
 // BundleAdjustment of cuda_slam/ba.cuh:397-819 (and, with motion_only, the
 // pipeline variant cuda_pipeline/slam.cuh:1475-1592).
 class BundleAdjustment {

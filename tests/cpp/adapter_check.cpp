@@ -290,3 +290,33 @@ extern "C" int adapter_update(const char* dir, int B, int K, int h, int w, const
         (void)hipFree(p);
     return bad;
 }
+
+// The front of the pipe through the adapters, in the reference's order
+// (main.cu:2729-2753, 1465-1497, 2924-2937): an 8-bit BGR frame resized to
+// H x W, fnet/cnet HalfBasicEncoders from <dir>, encode_frame, and the pose
+// file. fmap [128][H/8][W/8] (fp16 bits), net / inp [128][H/8][W/8].
+extern "C" int adapter_frontend(const char* dir, const unsigned char* bgr8, int src_w, int src_h,
+                                int H, int W, unsigned short* fmap, float* net, float* inp,
+                                const char* pose_path, int nk, const int* ts, const float* poses) {
+    const size_t hw = (size_t)(H / 8) * (W / 8);
+    unsigned char* d_src = upload(bgr8, (size_t)src_w * src_h * 3);
+    float *d_bgr = nullptr, *d_n = nullptr, *d_i = nullptr;
+    unsigned short* d_f = nullptr;
+    if (!d_src || hipMalloc(&d_bgr, (size_t)H * W * 3 * 4) != hipSuccess ||
+        hipMalloc(&d_f, 128 * hw * 2) != hipSuccess || hipMalloc(&d_n, 128 * hw * 4) != hipSuccess ||
+        hipMalloc(&d_i, 128 * hw * 4) != hipSuccess)
+        return 1;
+    slk_droid::bgr8_to_bgrf_resize(d_src, d_bgr, src_w, src_h, src_w * 3, W, H);
+    slk_droid::HalfBasicEncoder fnet, cnet;
+    fnet.init(nullptr, dir, "fnet", 1, H, W, 128, true);
+    cnet.init(nullptr, dir, "cnet", 1, H, W, 256, false);
+    slk_droid::encode_frame(fnet, cnet, d_bgr, d_f, d_n, d_i);
+    int bad = download(fmap, d_f, 128 * hw);
+    bad |= download(net, d_n, 128 * hw);
+    bad |= download(inp, d_i, 128 * hw);
+    slk_droid::save_poses(pose_path, nk, ts, poses, true);
+    fnet.destroy();
+    cnet.destroy();
+    for (void* p : {(void*)d_src, (void*)d_bgr, (void*)d_f, (void*)d_n, (void*)d_i}) (void)hipFree(p);
+    return bad;
+}

@@ -34,6 +34,8 @@ def harness():
     lib.adapter_corrblock.argtypes = [P, P, I, I, I, I, P, P, P, P, I, I, P, P]
     lib.adapter_update.argtypes = [ctypes.c_char_p, I, I, I, I] + [P] * 11
     lib.adapter_glue.argtypes = [I, I, I, I, I, I] + [P] * 12 + [I] + [P] * 4 + [P] * 14
+    lib.adapter_frontend.argtypes = [ctypes.c_char_p, P, I, I, I, I, P, P, P, ctypes.c_char_p,
+                                     I, P, P]
     return lib
 
 
@@ -215,3 +217,41 @@ def test_update_module_and_motion_filter(harness, tmp_path):
     mag = np.sqrt(d1[0, 0] ** 2 + d1[0, 1] ** 2).astype(np.float32).reshape(-1)
     ref = float(np.cumsum(mag, dtype=np.float32)[-1] / np.float32(h * w))
     assert abs(float(mean[0]) - ref) <= 2e-3 * abs(ref)
+
+
+def test_frontend_encoders_and_pose_file(harness, tmp_path):
+    """The front of the pipe through the adapters in the reference's order:
+    bgr8_to_bgrf_resize of a 96 x 72 8-bit frame to 64 x 48, HalfBasicEncoder
+    fnet / cnet with weights from the reference's tensor files, encode_frame,
+    and the pose file with the camera-to-world inversion; against the oracle
+    at the encoder bars of test_gpu_encoder.py, the file bytewise."""
+    from oracle import encoder_oracle as eo
+    from oracle import update_oracle as uo
+    announce("adapters: encoders + pose file")
+    H, W, sw, sh = 48, 64, 96, 72
+    P = {**eo.seeded_weights("fnet", 128, seed=90), **eo.seeded_weights("cnet", 256, seed=91)}
+    for name, (wt, b) in P.items():
+        uo.save_bin(os.path.join(tmp_path, name + "_weight.bin"), wt)
+        uo.save_bin(os.path.join(tmp_path, name + "_bias.bin"), b)
+    src = np.random.default_rng(92).integers(0, 256, (sh, sw, 3), dtype=np.uint8)
+    hw = (H // 8) * (W // 8)
+    fmap = np.zeros(128 * hw, np.uint16)
+    net = np.zeros(128 * hw, np.float32)
+    inp = np.zeros(128 * hw, np.float32)
+    ts = np.array([0, 3, 7], np.int32)
+    q = np.random.default_rng(93).normal(size=(3, 4))
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    poses = np.concatenate([np.random.default_rng(94).normal(size=(3, 3)), q], 1).astype(np.float32)
+    path = os.path.join(tmp_path, "poses.bin")
+    st = harness.adapter_frontend(os.fsencode(str(tmp_path)), _p(src), sw, sh, H, W, _p(fmap),
+                                  _p(net), _p(inp), os.fsencode(path), 3, _p(ts), _p(poses))
+    assert st == 0
+    bgr = eo.bgr8_to_bgrf(src, sw, sh, W, H)
+    rf, rn, ri = eo.encode_frame(bgr, P, P)
+    got_f = fmap.view(np.float16).astype(np.float64).reshape(128, H // 8, W // 8)
+    for got, ref, what in ((got_f, rf, "fmap"), (net.reshape(rn.shape), rn, "net"),
+                           (inp.reshape(ri.shape), ri, "inp")):
+        assert_close_rel(got, ref, tol=2e-2, what=what)
+        assert norm_rel(got, ref) < 4e-3, what
+    with open(path, "rb") as f:
+        assert f.read() == eo.poses_bin_bytes(ts, poses, True)
