@@ -957,7 +957,10 @@ def graph(args, slk, wl, H):
 def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
     """(active, total) 128-source x 256-target tiles of the batched correlation:
     a tile is active when some source's 8x8 window at some level has a cell in
-    its targets (the test tile_mask_edge makes on the GPU, restated in numpy)."""
+    its targets (the test tile_mask_edge makes on the GPU, restated in numpy).
+    Source tiles are runs of 128 sources in the order sort_sources gives them:
+    stably sorted by the clamped first row of their level-0 window when the
+    map has at most 247 rows, else in pixel order."""
     B, HW = coords.shape[0], h * w
     hl = [h >> l for l in range(levels)]
     wl = [w >> l for l in range(levels)]
@@ -967,6 +970,10 @@ def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
     lim = float(1 << 20)
     f = np.clip(np.floor(np.nan_to_num(coords, nan=-lim)), -lim, lim).astype(np.int64)
     fx, fy = f[:, 0, :], f[:, 1, :]
+    if h + 9 <= 256:
+        order = np.argsort(np.clip(fy - 3, -8, h), axis=1, kind="stable")
+        fx = np.take_along_axis(fx, order, axis=1)
+        fy = np.take_along_axis(fy, order, axis=1)
     src = (np.arange(B)[:, None] * mtiles + np.arange(HW)[None, :] // src_tile)
     act = np.zeros(B * mtiles * ntiles, bool)
     for l in range(levels):

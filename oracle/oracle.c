@@ -97,7 +97,8 @@ void orc_avg_pool_2x2(const float* in, float* out, long N, int H, int W) {
     /* main.cu:1150-1170; cuDNN AVERAGE_COUNT_INCLUDE_PADDING 2x2/2 no padding
      * gives the same floor shapes (nn.cuh:389-410). */
     const int oH = H / 2, oW = W / 2;
-#pragma omp parallel for schedule(static)
+    /* small calls run on the calling thread: a thread team costs more */
+#pragma omp parallel for schedule(static) if (N * oH * oW >= 65536)
     for (long n = 0; n < N; n++) {
         const float* src = in + (size_t)n * H * W;
         float* dst = out + (size_t)n * oH * oW;
@@ -120,7 +121,7 @@ void orc_corr_lookup_level(const float* level, const float* coords, float* out,
     const int hw1 = H1 * W1;
     const size_t plane = (size_t)H2 * W2;
     double* acc = NULL;
-#pragma omp parallel private(acc)
+#pragma omp parallel private(acc) if (hw1 >= 1024)
     {
         acc = (double*)malloc(sizeof(double) * D * D);
 #pragma omp for schedule(static)

@@ -174,6 +174,7 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     ctx->prep_feat.release();
     ctx->tile_ctr.release();
     ctx->tile_list.release();
+    ctx->src_order.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();
     ctx->zero_idx.release();
     ctx->glue_stage.release();

@@ -108,10 +108,193 @@ struct MaskArgs {
     const float* coords;
     int* list;
     int* ctr;
+    int* order;  // [edge][3][HW]: pixel, x, y of each sorted source position
     int mtiles, ntiles, nedges;
 };
+
+// Target tiles holding a cell of the 8x8 windows (every level) of a source
+// whose coordinates floor to (fx, fy), as bits t of a 64-bit mask for target
+// tile t (ntiles <= 64).
+__device__ __forceinline__ unsigned long long window_tiles(const Geom& g, int fx, int fy) {
+    unsigned long long m = 0ull;
+    for (int l = 0; l < g.levels; l++) {
+        const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
+        const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
+        const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
+        if (xa > xb || ya > yb) continue;
+        const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
+        const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
+        m |= (hi == 63 ? 0ull : (2ull << hi)) - (1ull << lo);
+    }
+    return m;
+}
+
+// ORs mask m (bit t = tile row + t) into the bitmap; a word is touched only
+// when it receives a set bit, so only words of existing tiles are
+__device__ __forceinline__ void merge_tiles(unsigned* bits, int row, unsigned long long m) {
+    const int w0 = row >> 5, sh = row & 31;
+    const unsigned part[2] = {(unsigned)m, (unsigned)(m >> 32)};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const unsigned a = part[k] << sh, b = sh ? part[k] >> (32 - sh) : 0u;
+        if (a) atomicOr(&bits[w0 + k], a);
+        if (b) atomicOr(&bits[w0 + k + 1], b);
+    }
+}
+
+// Marks the target tiles of one source in row `row` of the bitmap (any ntiles)
+__device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int row, int ntiles,
+                                            unsigned* bits) {
+    if (ntiles <= 64) {
+        const unsigned long long m = window_tiles(g, fx, fy);
+        if (m) merge_tiles(bits, row, m);
+        return;
+    }
+    for (int l = 0; l < g.levels; l++) {
+        const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
+        const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
+        const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
+        if (xa > xb || ya > yb) continue;
+        const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
+        const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
+        for (int t = row + lo; t <= row + hi; t++) atomicOr(&bits[t >> 5], 1u << (t & 31));
+    }
+}
+
+// Source order of an edge: its pixels sorted by the first row of their
+// level-0 window (floor(y) - 3, clamped to [-8, h]: rows outside never meet
+// the image at level 0), stably (pixel order within a row). Source tiles are
+// runs of 128 sorted sources, so a tile's windows span few image rows and far
+// fewer target tiles hold any of their cells than for 128 sources in image
+// order (whose +-8 px flows spread them over ~26 rows). A window cell is the
+// same dot product whichever tile computes it, so the order changes which
+// products are skipped, not any output. Counting sort in the workgroup:
+// every wave takes a contiguous quarter of the pixels, 64 at a time; the
+// lanes of a chunk holding equal keys find each other by one ballot per key
+// bit, the lowest of them adds their count to the wave's histogram, then
+// bucket-major offsets, then the same pass again scatters each pixel to its
+// bucket's next slot plus its rank among the equal lanes below it, and
+// marks the target tiles of its windows in the row of its source tile.
+// Writes ord[0][q] = the pixel at sorted position q and ord[1][q], ord[2][q]
+// = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with more rows
+// than that is not sorted: returns false, and neither ord nor the bitmap is
+// written.
+constexpr int kSortBuckets = 256;
+
+// the lanes of the wave whose key equals this lane's, among `live`
+__device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
+                                                         unsigned long long live) {
+    unsigned long long m = live;
+    for (int b = 0; b < nbits; b++) {  // uniform
+        const bool bit = (key >> b) & 1;
+        const unsigned long long bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+    }
+    return m;
+}
+
+__device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
+                              unsigned* bits, int ntiles) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int HW = g.HW, nb = g.h[0] + 9;
+    if (nb > kSortBuckets) return false;
+    float* oxy = reinterpret_cast<float*>(ord + HW);
+    const int nbits = 32 - __builtin_clz(nb - 1);
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int* hist = lds;                    // [4 waves][kSortBuckets]
+    int* pos = lds + 4 * kSortBuckets;  // [4 waves][kSortBuckets]: next sorted slot
+    for (int i = tid; i < 4 * kSortBuckets; i += kMaskThreads) hist[i] = 0;
+    __syncthreads();  // also orders the caller's clearing of the bitmap
+    const int quarter = (HW + 3) / 4;
+    const int q0 = std::min(HW, wv * quarter), q1 = std::min(HW, q0 + quarter);
+    auto key_of = [&](float y) {
+        const int oy = floor_clamped(y) - 3;
+        return std::min(std::max(oy, -8), g.h[0]) + 8;
+    };
+    // the coordinates of kG chunks are loaded before the first is used; when
+    // the quarter is one such group they stay in registers for the scatter
+    constexpr int kG = 12;
+    float xv[kG], yv[kG];
+    auto load = [&](int pg) {
+#pragma unroll
+        for (int u = 0; u < kG; u++) {
+            const int p = std::min(pg + 64 * u + lane, q1 - 1);
+            xv[u] = cc[p];
+            yv[u] = cc[HW + p];
+        }
+    };
+    const bool one = q1 - q0 <= 64 * kG;
+    // a wave's histogram: the lowest lane of each key of a chunk adds the
+    // key's count (distinct keys, distinct words)
+    for (int pg = q0; pg < q1; pg += 64 * kG) {
+        load(pg);
+#pragma unroll
+        for (int u = 0; u < kG; u++) {
+            const int pb = pg + 64 * u;
+            if (pb >= q1) break;  // uniform
+            const bool act = pb + lane < q1;
+            const int key = act ? key_of(yv[u]) : 0;
+            const unsigned long long m = equal_keys(key, nbits, __ballot(act));
+            if (act && !(m & below)) hist[wv * kSortBuckets + key] += __builtin_popcountll(m);
+        }
+    }
+    __syncthreads();
+    {
+        // thread b: bucket b's total, its exclusive prefix over the buckets
+        // (a wave scan, then the totals of the waves below), and each wave's
+        // first slot in it
+        const int bkt = tid;
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) tot += hist[w * kSortBuckets + bkt];
+        int incl = tot;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        if (lane == 63) wsum[wv] = incl;
+        __syncthreads();
+        int start = incl - tot;
+        for (int w = 0; w < wv; w++) start += wsum[w];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            pos[w * kSortBuckets + bkt] = start;
+            start += hist[w * kSortBuckets + bkt];
+        }
+    }
+    __syncthreads();
+    // stable scatter, chunk by chunk in pixel order: every lane reads its
+    // bucket's next slot, adds its rank among the equal lanes below it, and
+    // the lowest of them advances the slot past all of them
+    for (int pg = q0; pg < q1; pg += 64 * kG) {
+        if (!one) load(pg);
+#pragma unroll
+        for (int u = 0; u < kG; u++) {
+            const int pb = pg + 64 * u;
+            if (pb >= q1) break;  // uniform
+            const int p = pb + lane;
+            const bool act = p < q1;
+            const int key = act ? key_of(yv[u]) : 0;
+            const unsigned long long m = equal_keys(key, nbits, __ballot(act));
+            const int base = pos[wv * kSortBuckets + key];
+            const int rank = __builtin_popcountll(m & below);
+            if (act) {
+                const int q = base + rank;
+                ord[q] = p;
+                oxy[q] = xv[u];
+                oxy[HW + q] = yv[u];
+                if (rank == 0) pos[wv * kSortBuckets + key] = base + __builtin_popcountll(m);
+                mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
+                            q / kSrcTile * ntiles, ntiles, bits);
+            }
+        }
+    }
+    return true;
+}
+
 __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* bits,
-                               int* wave_sum) {
+                               int* wave_sum, int* sort_lds) {
     const float* coords = a.coords;
     int* list = a.list;
     int* ctr = a.ctr;
@@ -121,59 +304,50 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     const int nw = (tpe + 31) / 32;
     for (int i = tid; i < nw; i += kMaskThreads) bits[i] = 0u;
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
-    __syncthreads();
-    // A wave's 64 sources lie in one source tile (kSrcTile is a multiple of
-    // 64). When an edge's target tiles fit a 64-bit mask, each lane builds the
-    // mask of the tiles its windows touch, the wave ORs them by shuffles and
-    // lane 0 merges the result into the bitmap; otherwise every lane marks
-    // its tiles in the bitmap itself.
     const float* cc = coords + (size_t)e * 2 * g.HW;
-    constexpr int kU = 4;  // sources per thread whose coordinates load together
-    for (int pb = 0; pb < g.HW; pb += kU * kMaskThreads) {
-        int fx[kU], fy[kU];
+    int* ord = a.order + (size_t)e * 3 * g.HW;
+    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles)) {  // uniform
+        // pixel order: the order is the identity, written beside the mask.
+        // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
+        // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
+        // each lane builds the mask of the tiles its windows touch, the wave
+        // ORs them by shuffles and lane 0 merges the result into the bitmap;
+        // otherwise every lane marks its tiles in the bitmap itself.
+        __syncthreads();  // the bitmap is clear
+        float* oxy = reinterpret_cast<float*>(ord + g.HW);
+        constexpr int kU = 4;  // sources per thread whose coordinates load together
+        for (int pb = 0; pb < g.HW; pb += kU * kMaskThreads) {
+            float xs[kU], ys[kU];
 #pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int p = std::min(pb + u * kMaskThreads + tid, g.HW - 1);
-            fx[u] = floor_clamped(cc[p]);
-            fy[u] = floor_clamped(cc[g.HW + p]);
-        }
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int pw = pb + u * kMaskThreads + (tid & ~63);  // the wave's first source
-            if (pw >= g.HW) break;                                // uniform
-            const bool in = pw + lane < g.HW;
-            const int row = pw / kSrcTile * ntiles;  // first tile id of the source tile
-            unsigned long long m = 0ull;
-            for (int l = 0; l < g.levels; l++) {
-                const int ox = (fx[u] >> l) - 3, oy = (fy[u] >> l) - 3;
-                const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
-                const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
-                if (!in || xa > xb || ya > yb) continue;
-                const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
-                const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
-                if (ntiles <= 64)
-                    m |= (hi == 63 ? 0ull : (2ull << hi)) - (1ull << lo);
-                else
-                    for (int t = row + lo; t <= row + hi; t++)
-                        atomicOr(&bits[t >> 5], 1u << (t & 31));
+            for (int u = 0; u < kU; u++) {
+                const int q = std::min(pb + u * kMaskThreads + tid, g.HW - 1);
+                xs[u] = cc[q];
+                ys[u] = cc[g.HW + q];
             }
-            if (ntiles > 64) continue;  // uniform
-            unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                m0 |= __shfl_xor(m0, off, 64);
-                m1 |= __shfl_xor(m1, off, 64);
-            }
-            if (lane == 0) {
-                // bit t of (m1:m0) is tile row + t; a word is touched only
-                // when it receives a set bit, so only words below nw are
-                const int w0 = row >> 5, sh = row & 31;
-                const unsigned part[2] = {m0, m1};
-                for (int k = 0; k < 2; k++) {
-                    const unsigned a = part[k] << sh, b = sh ? part[k] >> (32 - sh) : 0u;
-                    if (a) atomicOr(&bits[w0 + k], a);
-                    if (b) atomicOr(&bits[w0 + k + 1], b);
+            for (int u = 0; u < kU; u++) {
+                const int pw = pb + u * kMaskThreads + (tid & ~63);  // the wave's first source
+                if (pw >= g.HW) break;                                // uniform
+                const bool in = pw + lane < g.HW;
+                const int row = pw / kSrcTile * ntiles;  // first tile id of the source tile
+                const int fx = floor_clamped(xs[u]), fy = floor_clamped(ys[u]);
+                if (in) {
+                    ord[pw + lane] = pw + lane;
+                    oxy[pw + lane] = xs[u];
+                    oxy[g.HW + pw + lane] = ys[u];
                 }
+                if (ntiles > 64) {
+                    if (in) mark_source(g, fx, fy, row, ntiles, bits);
+                    continue;
+                }
+                const unsigned long long m = in ? window_tiles(g, fx, fy) : 0ull;
+                unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) {
+                    m0 |= __shfl_xor(m0, off, 64);
+                    m1 |= __shfl_xor(m1, off, 64);
+                }
+                if (lane == 0) merge_tiles(bits, row, ((unsigned long long)m1 << 32) | m0);
             }
         }
     }
@@ -230,7 +404,8 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
     __shared__ int wave_sum[kMaskThreads / 64];
     if ((int)blockIdx.x < nmask) {  // uniform
-        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum);
+        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum,
+                       reinterpret_cast<int*>(&l1[0][0][0]));
         return;
     }
     const int tid = threadIdx.x;
@@ -326,6 +501,7 @@ struct alignas(16) SplitSmem {
     } u;
     int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
+    int pix[kSrcTile];        // pixel of each source
 };
 
 // One direct-to-LDS load per lane (16 or 4 bytes): lane l reads p and writes
@@ -370,9 +546,12 @@ __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
 // so the edges an XCD works on stay in its L2, and no CU idles while tiles
 // remain. Waves form a 2x2 grid: wave (wm, wn) owns sources
 // wm*64..+63 and targets wn*128..+127 of a tile, eight 32x32 accumulator
-// blocks.
+// blocks. Source tile mt holds sorted positions mt*128..+127 of the edge's
+// order (tile_mask_edge): the A rows are gathered through the order's pixel
+// column, the coordinates come from its sorted copies, and each source's
+// windows are stored at its own pixel.
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
-    const unsigned short* __restrict__ feat, EdgeSlots es, const float* __restrict__ coords,
+    const unsigned short* __restrict__ feat, EdgeSlots es, const int* __restrict__ order,
     float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles,
     int nedges, const int* __restrict__ list, int* __restrict__ ctr) {
     __shared__ SplitSmem sm;
@@ -428,6 +607,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const size_t plane = (size_t)g.C * Ttot;
     const unsigned short* fa = feat + (size_t)es.si[e] * 2 * plane;
     const unsigned short* fb = feat + (size_t)es.sj[e] * 2 * plane;
+    const int* ord = order + (size_t)e * 3 * HW;
 
     // Staging by direct-to-LDS loads (global_load_lds_dwordx4): lane l of wave
     // w writes bytes 16*(64w + l) of a 4 KB region, i.e. row tid/2, physical
@@ -437,7 +617,11 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // column j of B, so such rows only reach accumulator cells never read.
     const int hr = tid >> 1;
     const int hh = ((tid & 1) ^ (((hr >> 2) ^ (hr >> 3)) & 1)) * 8;  // rows hr, 128 + hr alike
-    const unsigned short* ga = fa + (size_t)std::min(p0 + hr, HW - 1) * kChunk + hh;
+    // pixel of source row hr (clamped: the DMA below must stay in the frame
+    // whatever the order buffer holds)
+    const int pa = std::min((unsigned)ord[std::min(p0 + hr, HW - 1)], (unsigned)(HW - 1));
+    if (!(tid & 1)) sm.pix[hr] = pa;  // read after the chunk loop's barriers
+    const unsigned short* ga = fa + (size_t)pa * kChunk + hh;
     const unsigned short* gb0 = fb + (size_t)std::min(t0 + hr, Ttot - 1) * kChunk + hh;
     const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
     const size_t kstep = (size_t)Ttot * kChunk;
@@ -515,7 +699,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     {
         const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
         const int pc = std::min(p0 + half * 64 + lane, HW - 1);
-        dma_x1(coords + ((size_t)e * 2 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
+        dma_x1(ord + (size_t)(1 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
     }
     if (nk > 1) issue(1, 1);
     // While in its chunk loop a wave issues at raised priority, so that on a
@@ -597,7 +781,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             const bool pin = p0 + lsrc < HW;
             const float* Tcol = &sm.u.T[0][s];
             // byte offset of cell (cx, row 0) of level 0 in the slot
-            const int woff = (int)win_index(0, 0, cx, HW, std::min(p0 + lsrc, HW - 1)) * 4;
+            const int woff = (int)win_index(0, 0, cx, HW, sm.pix[lsrc]) * 4;
 #pragma unroll
             for (int l = 0; l < kMaxLevels; l++) {
                 if (lr0[l] > lr1[l]) continue;  // level not in this tile
@@ -689,7 +873,8 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
     if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
         return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
-    MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(), mtiles, ntiles, n};
+    MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
+                ctx->src_order.as<int>(), mtiles, ntiles, n};
     {
         // feature preparation and the tile mask, one launch
         ProfScope ps(ctx, "corr_feat_prep", stream);
@@ -698,7 +883,7 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     {
         ProfScope ps(ctx, "corr_window", stream);
         hipLaunchKernelGGL(k_corr_split_win, dim3(ctx->ws_grid), dim3(256), 0, stream, feat, es,
-                           coords, win, slot0, g, ctx->alpha, mtiles, ntiles, n,
+                           ctx->src_order.as<int>(), win, slot0, g, ctx->alpha, mtiles, ntiles, n,
                            ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>());
     }
     SLK_HIP(hipGetLastError());
@@ -738,7 +923,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     // sources only need level 0 (their own launch); targets need every level
     {
         ProfScope ps(ctx, "corr_feat_prep", stream);
-        const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
+        const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0};
         SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
     }
     return mask_and_windows(ctx, fm, fstride, sf, g, n, n, true, es, feat, n, coords, win, slot0,
@@ -750,12 +935,13 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
 bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
 
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
-                          size_t* ctr_bytes) {
+                          size_t* order_per_edge, size_t* ctr_bytes) {
     const Geom g = make_geom(ctx);
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     *slot_bytes = 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short);
     *tiles_per_edge = mtiles * ntiles * sizeof(int);
+    *order_per_edge = 3 * (size_t)g.HW * sizeof(int);
     *ctr_bytes = kCtrInts * sizeof(int);
 }
 
@@ -770,6 +956,8 @@ int corr_split_alloc(slk_ctx* ctx) {
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
     SLK_TRY(ctx->tile_list.ensure(tiles * sizeof(int)));
+    SLK_TRY(ctx->src_order.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * 3 *
+                                  g.HW * sizeof(int)));
     SLK_TRY(ctx->tile_ctr.ensure(kCtrInts * sizeof(int)));
     // the correlation workgroups: two per CU, a multiple of the 8 XCDs
     int cus = 0;
@@ -805,7 +993,7 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     SLK_TRY(ctx->prep_feat.ensure(bytes));
     SlotFrames sf{};
     sf.ident = 1;
-    const MaskArgs none{nullptr, nullptr, nullptr, 0, 0, 0};
+    const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0};
     ProfScope ps(ctx, "corr_prepare_frames", stream);
     if (dtype == SLK_F32)
         SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,

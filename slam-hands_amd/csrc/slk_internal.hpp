@@ -81,6 +81,7 @@ struct slk_ctx {
     int prep_nframes = 0;
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
+    slk::DevBuf src_order;  // per edge: sources sorted by window row (pixel, x, y columns)
     int ws_grid = 0;        // workgroups of the batched correlation kernel
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
@@ -144,9 +145,9 @@ int corr_alloc(slk_ctx* ctx);
 bool corr_split_supported(const slk_ctx* ctx);
 int corr_split_alloc(slk_ctx* ctx);
 // bytes of one feature slot (two per edge of a launch), of one edge's tile
-// list, and of the launch's tile counters
+// list and source order, and of the launch's tile counters
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
-                          size_t* ctr_bytes);
+                          size_t* order_per_edge, size_t* ctr_bytes);
 // workgroups of the batched correlation kernel on a part with `cus` CUs
 int corr_split_grid(int cus);
 int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,

@@ -161,14 +161,16 @@ def test_window_48_edges_matches_oracle(slk, prec):
         assert_close_rel(out[e][:, pix], ref_sub, what=f"edge {e} sampled")
 
 
-@pytest.mark.parametrize("h,w", [(96, 128), (100, 128)])
+@pytest.mark.parametrize("h,w", [(96, 128), (100, 128), (256, 24), (260, 80)])
 def test_window_large_frames_sampled(slk, h, w):
     """Large feature maps, 12 edges in one launch. 96x128: 64 target tiles
     per source tile, the widest the tile marking handles with a 64-bit mask
     per lane (and the top bit set); 100x128: 67, which takes the per-tile
     marking path, and 6700 tiles per edge, several rounds of the tile
-    compaction. Every edge is checked on 48 random pixels by direct fp64
-    evaluation of their windows."""
+    compaction. 256x24 and 260x80: more than 247 rows, so the sources keep
+    their pixel order (no sort by window row), with 32 target tiles (64-bit
+    masks) and 108 (per-tile marking). Every edge is checked on 48 random
+    pixels by direct fp64 evaluation of their windows."""
     announce(f"corr window {h}x{w}, 12 edges")
     f, ii, jj, coords, out = _window(slk, 6, h, w, 12, seed=50, max_batch=12)
     assert np.all(np.isfinite(out))
