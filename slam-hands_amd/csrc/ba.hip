@@ -44,7 +44,7 @@ namespace slk {
 namespace {
 
 constexpr int kLinWG = 256;
-constexpr int kLinPx = 256;  // pixels per k_ba_lin_kf workgroup (1 per thread)
+constexpr int kLinPx = 256;  // pixels per linearization workgroup (<= kLinWG, a multiple of 64)
 constexpr int kSchWG = 256;
 constexpr int kNH = 90;      // 78 upper-triangle Hessian entries + vi(6) + vj(6)
 // Per (edge, pixel chunk) the linearization reduces only Hjj = sum w Jj Jj^T
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_kf(
     const int kf = plan.kf_list[kc];
     const double fx = intr[0], fy = intr[1], cx = intr[2], cy = intr[3];
     const int k = chunk * kLinPx + threadIdx.x;
-    const bool vpx = k < HW;
+    const bool vpx = (int)threadIdx.x < kLinPx && k < HW;  // threads past the chunk idle
     const int r0 = plan.kf_rptr[kc], r1 = plan.kf_rptr[kc + 1];
     if (!motion_only && vpx) {
         for (int r = r0; r < r1; r++) {
@@ -408,7 +408,7 @@ __global__ __launch_bounds__(kLinWG) void k_ba_lin_wv(
     if (!motion_only) {
         // one pixel per thread: the per-wave slices in wave order
         const int px = threadIdx.x, k = chunk * kLinPx + px;
-        if (k < HW) {
+        if (px < kLinPx && k < HW) {
             double c = 0.0, w = 0.0;
 #pragma unroll
             for (int v = 0; v < kLinWaves; v++) {
