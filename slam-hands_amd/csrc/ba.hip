@@ -22,9 +22,10 @@
 //   k_ba_assemble one workgroup per 6x6 block of S and per 6 entries of b:
 //                 sums the totals listed for the block (lists built on the
 //                 host; fixed order, no atomics), then S_ii += ep + lm*S_ii.
-//   k_ba_solve_*  fp64 Cholesky, solve, dx rounded to fp32, retraction of the
-//                 poses [t0, t1): one wavefront with S in registers up to 10
-//                 free poses, one workgroup blocked in LDS up to 84x84, else
+//   k_ba_solve_*  fp64 factorization and solve, dx rounded to fp32,
+//                 retraction of the poses [t0, t1): Cholesky in one
+//                 wavefront with S in registers up to 10 free poses, LDL^T in
+//                 one workgroup with S in LDS up to 120x120, else Cholesky
 //                 blocked over many workgroups in global memory.
 //   k_ba_backsub  grid (pixel chunk, keyframe): dz = Q (w - E^T dx),
 //                 disps += dz.
@@ -56,7 +57,6 @@ constexpr int kNJ = 27;
 // per-edge totals: Hii (36), Hij (36), Hjj (36), vi (6), vj (6)
 constexpr int kNT = 120;
 constexpr int kTotHii = 0, kTotHij = 36, kTotHjj = 72, kTotVi = 108, kTotVj = 114;
-constexpr int kSmallN = 84;  // one-workgroup LDS solve up to 84x84 (85 x 84 fp64, 57 KB)
 constexpr double kMinDepth = 0.25;  // se3.cuh:6
 
 __host__ __device__ __forceinline__ int tri(int n, int m) { return n * (n + 1) / 2 + m; }
@@ -585,7 +585,11 @@ __device__ __forceinline__ double bcast(double v, int src) {
     return __hiloint2double(hi, lo);
 }
 
-__device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok) {
+// Outputs of a solve: the status flags, dx (fp64 and the fp32 step), and the
+// retraction of poses t0..t1-1, whose current values are read from
+// pose_src[(k - t0) * 7 ..] (A.poses + 7 * t0, or a copy taken earlier).
+__device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok,
+                                             const float* pose_src) {
     const int n = A.n;
     if (threadIdx.x == 0) {
         A.flags[0] = ok ? 0 : 1;
@@ -599,7 +603,7 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
     // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
     for (int k = A.t0 + threadIdx.x; k < A.t1; k += blockDim.x) {
         double t[3], q[4], xi[6], t1[3], q1[4];
-        load_pose(A.poses, k, t, q);
+        load_pose(pose_src, k - A.t0, t, q);
         for (int m = 0; m < 6; m++) xi[m] = (double)(float)x[(k - A.t0) * 6 + m];
         retr_se3(xi, t, q, t1, q1);
         for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
@@ -748,6 +752,248 @@ __global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
 template <int P>
 void launch_solve_wave(const SolveArgs& A, hipStream_t stream) {
     hipLaunchKernelGGL(k_ba_solve_wave<6 * P>, dim3(1), dim3(64), 0, stream, A);
+}
+
+// ---- one-workgroup panel solver (n <= kPanelN: the frontend's systems) ----
+// LDL^T of the bordered matrix [S b; b^T *] in LDS, right-looking in panels
+// of kPW columns. The system is padded to n8 = a multiple of kPW with
+// identity rows and columns (b padded with zeros), so every panel is full,
+// every row block of the backward solve lies on one side of row 64, and the
+// latency chains below carry no bounds branches (a taken branch costs about
+// as much as a dependent fp64 operation). The packed lower triangle (row i
+// at tri(i)) holds rows 0..n8-1 and b^T in row n8. Per panel, two barriers:
+// (1) every wave g < ng holds the panel's diagonal rows in lanes 0..kPW-1
+//     and up to kPanelRows rows below the diagonal block in the other lanes,
+//     their panel entries in registers, and eliminates the panel's columns
+//     one at a time: pivot d_j by readlane, 1/d_j (hardware estimate + two
+//     Newton steps), l_ij = u_ij / d_j, and u_ik -= l_ij u_kj for the later
+//     panel columns k, u_kj being read by readlane before 1/d_j is known.
+//     Every wave eliminates the diagonal block itself, with the same
+//     arithmetic, so no wave waits on another inside a panel; each writes
+//     back the l of its rows below the block.
+// (2) after the barrier, wave 0 writes the diagonal block's l (its pivots
+//     went out before the barrier), and all threads subtract the panel's products from the
+//     trailing lower triangle, A[i][k] -= sum_m l_im d_m l_km, in 2 x 2
+//     register blocks.
+// Row n8 ends as w = D^-1 L^-1 b, so the backward solve L^T x = w (unit
+// diagonal) is one readlane and one multiply-add per row, in wave 0 (lane i
+// holding rows i and i + 64), with each block's entries of L read into
+// registers while the previous block runs. S = L D L^T is the reference's
+// S = L L^T with L_chol = L D^1/2; the pivot test is the reference's (every
+// pivot > 0, ba.cuh:422), and a failed pivot ends the factorization with a
+// zero step.
+constexpr int kPW = 8;
+constexpr int kPanelRows = 64 - kPW;  // rows below the diagonal block per wave
+constexpr int kPanelN = 120;          // packed [S; b^T] of n8 = 120: 7381 doubles, 59 KB
+constexpr int kPanelPoses = kPanelN / 6;
+static_assert(kPanelN % kPW == 0, "the largest system is a whole number of panels");
+static_assert(kPanelN + 1 - kPW <= 3 * kPanelRows, "three waves cover the rows below a panel");
+static_assert(kPanelN <= 128 && 64 % kPW == 0, "the backward solve holds two rows per lane");
+
+__host__ __device__ __forceinline__ int tri(int i) { return i * (i + 1) / 2; }
+__host__ __device__ __forceinline__ int pad_panel(int n) { return (n + kPW - 1) / kPW * kPW; }
+
+size_t panel_solve_lds_bytes(int n) {
+    const int n8 = pad_panel(n);
+    return ((size_t)tri(n8 + 1) + 2 * (size_t)n8) * sizeof(double);
+}
+
+// 1/d in fp64: hardware estimate + two Newton steps (~1 ulp for normal d)
+__device__ __forceinline__ double rcp_f64(double d) {
+    double y = __builtin_amdgcn_rcp(d);
+    y = __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
+    y = __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
+    return y;
+}
+
+__global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
+    extern __shared__ double sm[];
+    __shared__ int ok_sh;
+    __shared__ float pose0[kPanelPoses * 7];  // poses t0..t1-1 before the step
+    const int n = A.n, n8 = pad_panel(n), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double* L = sm;                   // packed lower [S; b^T], padded
+    double* piv = sm + tri(n8 + 1);   // [n8] pivots d_j
+    double* xs = piv + n8;            // [n8] the solution
+    if (tid < (A.t1 - A.t0) * 7) pose0[tid] = A.poses[A.t0 * 7 + tid];
+    // rows of [S; b^T] with the padding (identity rows, zeros elsewhere):
+    // wave w takes rows w, w + 4, .., lanes the columns lane, lane + 64; the
+    // loads of kLdRows rows go out before the first is stored (S comes from
+    // the assembly on other CUs)
+    constexpr int kLdRows = 8;
+    for (int i0 = wave; i0 <= n8; i0 += 4 * kLdRows) {
+        double v[kLdRows][2];
+#pragma unroll
+        for (int r = 0; r < kLdRows; r++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int i = i0 + 4 * r, k = lane + 64 * h;
+                double x = k == i ? 1.0 : 0.0;
+                if (k < n && i < n && k <= i) x = A.S_dbg[(size_t)i * n + k];
+                if (k < n && i == n8) x = A.b_dbg[k];
+                v[r][h] = x;
+            }
+#pragma unroll
+        for (int r = 0; r < kLdRows; r++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int i = i0 + 4 * r, k = lane + 64 * h;
+                if (i <= n8 && k <= i && k < n8) L[tri(i) + k] = v[r][h];
+            }
+    }
+    if (tid == 0) ok_sh = 1;
+    __syncthreads();
+    for (int c0 = 0; c0 < n8; c0 += kPW) {
+        const int r0 = c0 + kPW;
+        const int ng = (n8 + 1 - r0 + kPanelRows - 1) / kPanelRows;  // >= 1
+        const bool dg = lane < kPW;
+        double p[kPW];
+        double dj = 0.0;  // diagonal lane j: pivot j
+        if (wave < ng) {  // uniform
+            const int row = dg ? c0 + lane : r0 + kPanelRows * wave + lane - kPW;
+            const bool live = dg || row <= n8;
+            const double* src = L + tri(live ? row : n8) + c0;
+#pragma unroll
+            for (int m = 0; m < kPW; m++) {
+                const double v = src[m];
+                p[m] = live && (!dg || m <= lane) ? v : 0.0;
+            }
+            bool ok = true;
+#pragma unroll
+            for (int j = 0; j < kPW; j++) {
+                double u[kPW];  // u_kj of the later diagonal rows k, before the pivot is known
+#pragma unroll
+                for (int k = j + 1; k < kPW; k++) u[k] = bcast(p[j], k);
+                const double d = bcast(p[j], j);
+                ok = ok && (d > 0.0);
+                const double l = p[j] * rcp_f64(d);
+                if (lane == j) dj = d;
+                p[j] = l;
+#pragma unroll
+                for (int k = j + 1; k < kPW; k++) p[k] -= l * u[k];
+            }
+            if (!dg && live) {
+                double* dst = L + tri(row) + c0;
+#pragma unroll
+                for (int m = 0; m < kPW; m++) dst[m] = p[m];
+            }
+            if (wave == 0 && dg) piv[c0 + lane] = dj;  // read by the trailing update
+            if (!ok && lane == 0) ok_sh = 0;
+        }
+        __syncthreads();
+        if (!ok_sh) break;  // uniform
+        if (wave == 0 && dg) {
+            // the diagonal block: no wave reads it again during this panel
+            double* dst = L + tri(c0 + lane) + c0;
+#pragma unroll
+            for (int m = 0; m < kPW; m++)
+                if (m < lane) dst[m] = p[m];
+        }
+        // trailing update, rows r0..n8 (b^T last), columns r0..n8-1, 2 x 2
+        // blocks; the last block row holds b^T alone
+        const int nbi = (n8 - r0) / 2 + 1;
+        const int cnt = nbi * (nbi + 1) / 2;
+        for (int t = tid; t < cnt; t += 256) {
+            const int bi = (int)((__builtin_sqrt(8.0 * t + 1.0) - 1.0) * 0.5);
+            const int bk = t - tri(bi);
+            const int i0 = r0 + 2 * bi, k0 = r0 + 2 * bk;
+            if (k0 >= n8) continue;  // b^T's block row has one block fewer
+            const bool two = i0 < n8;  // i0 + 1 exists (not b^T's row)
+            const double* a0 = L + tri(i0) + c0;
+            const double* a1 = L + tri(two ? i0 + 1 : i0) + c0;
+            const double* b0 = L + tri(k0) + c0;
+            const double* b1 = L + tri(k0 + 1) + c0;
+            const double* dp = piv + c0;
+            double x0[kPW], x1[kPW], y0[kPW], y1[kPW];
+#pragma unroll
+            for (int m = 0; m < kPW; m++) {
+                x0[m] = a0[m];
+                x1[m] = a1[m];
+                y0[m] = b0[m] * dp[m];
+                y1[m] = b1[m] * dp[m];
+            }
+            double s00 = 0.0, s01 = 0.0, s10 = 0.0, s11 = 0.0;
+#pragma unroll
+            for (int m = 0; m < kPW; m++) {
+                s00 += x0[m] * y0[m];
+                s01 += x0[m] * y1[m];
+                s10 += x1[m] * y0[m];
+                s11 += x1[m] * y1[m];
+            }
+            L[tri(i0) + k0] -= s00;  // k0 <= i0
+            if (k0 < i0) L[tri(i0) + k0 + 1] -= s01;
+            if (two) {
+                L[tri(i0 + 1) + k0] -= s10;
+                L[tri(i0 + 1) + k0 + 1] -= s11;
+            }
+        }
+        __syncthreads();
+    }
+    const bool ok = ok_sh != 0;
+    if (ok && wave == 0 && n8 <= 64) {
+        // L^T x = w, w = row n8, lane i holding row i: x_k = acc_k once the
+        // rows below k are in, then acc_i -= l_ki x_k for i < k (l_ki taken
+        // as zero for i >= k, so lane k keeps x_k). The whole column of L is
+        // read into registers first; the 64 steps are straight-line code
+        // (rows past n8 carry zeros).
+        double c[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) {
+            const int kk = min(k, n8 - 1);  // rows past n8 - 1 read row n8 - 1, discarded
+            const double v = L[tri(kk) + min(lane, kk)];
+            c[k] = lane < k && k < n8 ? v : 0.0;
+        }
+        double acc = L[tri(n8) + min(lane, n8 - 1)];
+        if (lane >= n8) acc = 0.0;
+#pragma unroll
+        for (int k = 63; k >= 0; k--) acc -= c[k] * bcast(acc, k);
+        if (lane < n8) xs[lane] = acc;
+    } else if (ok && wave == 0) {
+        // L^T x = w, w = row n8: x_k = acc_k once the rows below k are in;
+        // then acc_i -= l_ki x_k for i < k (the prefetched l_ki is zero for
+        // i >= k, so lane k keeps x_k). Blocks of kPW rows from the bottom.
+        const double* w = L + tri(n8);
+        double acc0 = lane < n8 ? w[lane] : 0.0;
+        double acc1 = lane + 64 < n8 ? w[lane + 64] : 0.0;
+        double l0[kPW], l1[kPW];
+        auto fetch = [&](int kb) {  // rows kb, kb - 1, .., kb - kPW + 1
+#pragma unroll
+            for (int q = 0; q < kPW; q++) {
+                const int k = kb - q;
+                const double* Lk = L + tri(k);
+                const double v0 = Lk[min(lane, k)], v1 = Lk[min(lane + 64, k)];
+                l0[q] = lane < k ? v0 : 0.0;
+                l1[q] = lane + 64 < k ? v1 : 0.0;
+            }
+        };
+        fetch(n8 - 1);
+        for (int kb = n8 - 1; kb >= 0; kb -= kPW) {  // uniform
+            double c0v[kPW], c1v[kPW];
+#pragma unroll
+            for (int q = 0; q < kPW; q++) {
+                c0v[q] = l0[q];
+                c1v[q] = l1[q];
+            }
+            if (kb >= kPW) fetch(kb - kPW);
+            if (kb >= 64) {  // uniform: the block's rows are all >= 64
+#pragma unroll
+                for (int q = 0; q < kPW; q++) {
+                    const double xk = bcast(acc1, kb - 64 - q);
+                    acc0 -= c0v[q] * xk;
+                    acc1 -= c1v[q] * xk;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kPW; q++) {
+                    const double xk = bcast(acc0, kb - q);
+                    acc0 -= c0v[q] * xk;
+                }
+            }
+        }
+        if (lane < n8) xs[lane] = acc0;
+        if (lane + 64 < n8) xs[lane + 64] = acc1;
+    }
+    __syncthreads();
+    finish_solve(A, xs, ok, pose0);
 }
 
 // 1..kWaveP free poses take the wavefront solver
@@ -952,107 +1198,6 @@ __device__ void back_solve_blocked(const double* __restrict__ S, double* y, int 
     }
 }
 
-// One workgroup, kWaveP < P and n <= kSmallN: the damped system is copied
-// into LDS as the bordered matrix [S; b^T] (rows 0..n-1, b in row n, leading
-// dimension n) and factored right-looking in kMB-column steps: (1) wave 0
-// factors the diagonal block with one row per lane in registers; (2) one
-// thread per row below it (b's row included) solves that row against it;
-// (3) the trailing lower triangle takes the panel's products in 4 x 4
-// register blocks, one block per thread. Row n ends as z = L^-1 b; the
-// backward solve is back_solve_blocked on the factor in LDS.
-constexpr int kMB = 16;
-__global__ __launch_bounds__(256) void k_ba_solve_lds(SolveArgs A) {
-    extern __shared__ double S[];
-    __shared__ double invd[kMB];
-    __shared__ int ok_sh;
-    const int n = A.n, tid = threadIdx.x;
-    for (int t = tid; t < n * n + n; t += blockDim.x)
-        S[t] = t < n * n ? A.S_dbg[t] : A.b_dbg[t - n * n];
-    if (tid == 0) ok_sh = 1;
-    for (int j0 = 0; j0 < n; j0 += kMB) {
-        const int nb = min(kMB, n - j0);
-        __syncthreads();
-        if (tid < 64) {  // (1) the diagonal block, padded with an identity block
-            const int lane = tid;
-            double r[kMB];
-#pragma unroll
-            for (int m = 0; m < kMB; m++)
-                r[m] = (lane < nb && m < nb) ? S[(size_t)(j0 + lane) * n + j0 + m]
-                                             : (m == lane ? 1.0 : 0.0);
-            bool ok = true;
-            double inv = 0.0;
-            wave_cholesky<kMB, kMB>(r, static_cast<double (*)[kMB]>(nullptr), ok, inv);
-            if (lane < nb) {
-#pragma unroll
-                for (int m = 0; m < kMB; m++)
-                    if (m <= lane) S[(size_t)(j0 + lane) * n + j0 + m] = r[m];
-                invd[lane] = inv;
-            }
-            if (lane == 0 && !ok) ok_sh = 0;
-        }
-        __syncthreads();
-        if (!ok_sh) break;
-        const int r0 = j0 + nb;
-        // (2) panel rows r0..n (b's row is row n): x L_D^T = S[i][j0..j0+nb)
-        for (int i = r0 + tid; i <= n; i += blockDim.x) {
-            double* row = S + (size_t)i * n + j0;
-            double x[kMB];
-#pragma unroll
-            for (int k = 0; k < kMB; k++) {
-                if (k < nb) {
-                    double v = row[k];
-#pragma unroll
-                    for (int m = 0; m < k; m++) v -= x[m] * S[(size_t)(j0 + k) * n + j0 + m];
-                    x[k] = v * invd[k];
-                } else {
-                    x[k] = 0.0;
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kMB; k++)
-                if (k < nb) row[k] = x[k];
-        }
-        __syncthreads();
-        // (3) S[i][k] -= L[i][J] . L[k][J] for r0 <= k <= i <= n, k < n
-        const int nbi = (n + 1 - r0 + 3) / 4;
-        const int cnt = nbi * (nbi + 1) / 2;
-        for (int t = tid; t < cnt; t += blockDim.x) {
-            int bi = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
-            while (bi * (bi + 1) / 2 > t) bi--;
-            while ((bi + 1) * (bi + 2) / 2 <= t) bi++;
-            const int bk = t - bi * (bi + 1) / 2;
-            const int i0 = r0 + 4 * bi, k0 = r0 + 4 * bk;
-            if (k0 >= n) continue;
-            double acc[4][4] = {};
-            for (int m = 0; m < nb; m++) {
-                double a[4], b[4];
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    a[u] = i0 + u <= n ? S[(size_t)(i0 + u) * n + j0 + m] : 0.0;
-                    b[u] = k0 + u < n ? S[(size_t)(k0 + u) * n + j0 + m] : 0.0;
-                }
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[u][v] += a[u] * b[v];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int i = i0 + u, k = k0 + v;
-                    if (i <= n && k < n && k <= i) S[(size_t)i * n + k] -= acc[u][v];
-                }
-        }
-    }
-    __syncthreads();
-    const bool ok = ok_sh != 0;
-    double* y = S + (size_t)n * n;  // z, then x
-    if (ok) back_solve_blocked(S, y, n);
-    __syncthreads();
-    finish_solve(A, y, ok);
-}
-
 constexpr int kFinishWG = 512;
 __global__ __launch_bounds__(kFinishWG) void k_chol_finish(SolveArgs A) {
     extern __shared__ double smem[];
@@ -1063,7 +1208,7 @@ __global__ __launch_bounds__(kFinishWG) void k_chol_finish(SolveArgs A) {
     __syncthreads();
     if (ok) back_solve_blocked(A.S, b, n);
     __syncthreads();
-    finish_solve(A, b, ok);
+    finish_solve(A, b, ok, A.poses + 7 * A.t0);
 }
 
 int solve_blocked(const SolveArgs& A, hipStream_t stream) {
@@ -1339,7 +1484,7 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         SLK_TRY(s->E.ensure(std::max<size_t>(1, (size_t)s->N_E * 6 * HW) * sizeof(double)));
         SLK_TRY(s->Q.ensure((size_t)s->N_kf * HW * sizeof(double)));
         SLK_TRY(s->Wv.ensure((size_t)s->N_kf * HW * sizeof(double)));
-        if (n > (size_t)kSmallN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
+        if (n > (size_t)kPanelN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
         SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
         SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
         SLK_TRY(s->dx_dbg.ensure(n * sizeof(double)));
@@ -1399,10 +1544,11 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     if (s->P <= kWaveP) {
         ProfScope ps(ctx, "ba_solve", stream);
         solve_wave(s->P, A, stream);
-    } else if (s->n <= kSmallN) {
+    } else if (s->n <= kPanelN) {
+        // t1 - t0 = P <= kPanelPoses
         ProfScope ps(ctx, "ba_solve", stream);
-        const size_t shm = ((size_t)s->n * s->n + s->n) * sizeof(double);  // [S; b^T]
-        hipLaunchKernelGGL(k_ba_solve_lds, dim3(1), dim3(256), shm, stream, A);
+        hipLaunchKernelGGL(k_ba_solve_panel, dim3(1), dim3(256), panel_solve_lds_bytes(s->n),
+                           stream, A);
     } else {
         ProfScope ps(ctx, "ba_solve", stream);
         SLK_TRY(solve_blocked(A, stream));

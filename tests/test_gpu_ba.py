@@ -134,12 +134,14 @@ def test_not_spd_leaves_state_untouched(slk):
     ctx.close()
 
 
-@pytest.mark.parametrize("P", [11, 14, 15])
+@pytest.mark.parametrize("P", [11, 14, 15, 20, 21])
 def test_lds_solver_sizes(slk, P):
-    """P = 11 and 14 free poses (n = 66 and 84): the edges of the one-workgroup
-    solve with the bordered system in LDS (59,640 B at n = 84); P = 15
-    (n = 90): the first size of the blocked solve over many workgroups. One
-    iteration against the oracle, then a second from the updated state."""
+    """P = 11 to 20 free poses (n = 66 to 120) take the one-workgroup LDL^T
+    solve with the bordered system in LDS: n = 66, 84 and 90 are padded to
+    72, 88 and 96 (identity rows), n = 120 is the largest (59 KB of LDS);
+    P = 21 (n = 126): the first size of the blocked solve over many
+    workgroups. One iteration against the oracle, then a second from the
+    updated state."""
     announce(f"ba lds solver P={P} (n={6 * P})")
     n = P + 2
     p = wl.ba_problem(n=n, h=12, w=16, seed=30 + P)
@@ -164,7 +166,7 @@ def test_lds_solver_sizes(slk, P):
 
 
 def test_lds_solver_not_spd_late_pivot(slk):
-    """P = 12 (n = 72, the LDS solve) with every edge that touches frames 12
+    """P = 12 (n = 72, the one-workgroup LDS solve) with every edge that touches frames 12
     and 13 at zero weight and no damping: the rows of those two poses are
     zero, so the factorization fails at pivot 60, in a later column block than
     the first. Reported as SLK_E_NOT_SPD, poses and inverse depths untouched."""

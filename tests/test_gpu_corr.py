@@ -249,6 +249,52 @@ def test_window_fp16_features(slk):
     assert_close_rel(got, ref, what="fp16 window")
 
 
+def _window_of(slk, f, coords, ii, jj, alpha=1.0 / 16.0):
+    n, C, h, w = f.shape
+    ctx = slk.Context(h, w, C=C, max_batch=len(ii), corr_scale=alpha)
+    fd = slk.DeviceArray.from_host(f)
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((len(ii), 196, h * w))
+    ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, out)
+    slk.hip().sync()
+    got = out.to_host()
+    ctx.close()
+    return got
+
+
+def _err_ratio(got, ref):
+    rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+    return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms)))
+
+
+def test_split_precision_wide_range_and_coherent_lo(slk):
+    """Margins of the bf16 hi/lo split (hi.hi + hi.lo + lo.hi, lo.lo dropped)
+    where they are smallest:
+    * wide dynamic range: every feature N(0,1) * 2^U(-8, 8), each channel
+      also scaled by 2^U(-4, 4), so the result is dominated by a few large
+      products and the small ones sit many binades below;
+    * coherent lo: every feature is +-(1 + 2^-8) * 2^k, the bf16 half-way
+      case (hi = 1, lo = 2^-8, the largest lo relative to hi), with signs
+      that agree along the channels, so the dropped lo.lo terms (2^-16 of
+      each product) add up instead of cancelling.
+    Both must stay within helpers.TOL of the fp64 oracle; the error ratios
+    are printed."""
+    h, w, n = 24, 32, 5
+    ii, jj = wl.cyclic_edges(n)
+    coords = wl.flow_coords(len(ii), h, w, seed=41)
+    rng = np.random.default_rng(40)
+    wide = (rng.standard_normal((n, 128, h, w)) * np.exp2(rng.uniform(-8, 8, (n, 128, h, w)))
+            * np.exp2(rng.uniform(-4, 4, (1, 128, 1, 1)))).astype(np.float32)
+    sign = np.where(rng.random((n, 1, h, w)) < 0.5, -1.0, 1.0)
+    coh = (sign * (1.0 + 2.0 ** -8) * np.exp2(rng.integers(-2, 3, (n, 1, h, w)))
+           * np.ones((1, 128, 1, 1))).astype(np.float32)
+    for name, f in (("wide range", wide), ("coherent lo", coh)):
+        got = _window_of(slk, f, coords, ii, jj)
+        ref = orc.corr_batch(f, ii, jj, coords, 1.0 / 16.0)
+        print(f"{name}: max |g - r| / max(|r|, rms) = {_err_ratio(got, ref):.3g}")
+        assert_close_rel(got, ref, what=name)
+
+
 def test_device_indices_and_chunking(slk):
     """Device-resident ii/jj, and B above max_batch (processed in chunks)."""
     h, w = 24, 32
