@@ -683,77 +683,6 @@ __device__ __forceinline__ void wave_cholesky(double (&r)[N], double (*Lp)[W], b
 
 constexpr int kPanelW = 8;
 
-// One wavefront, n = N < 64 (the frontend's 6P x 6P systems, P <= 10). Lane
-// i < N holds row i of S and lane N holds b^T: wave_cholesky on the bordered
-// matrix [S; b^T] leaves z = L^-1 b in lane N's row, so the forward solve
-// costs nothing. The backward solve L^T x = z broadcasts x_k by readlane;
-// lane i's column of L comes from an LDS copy of the rows, read into
-// registers before the sequential part. No barrier anywhere: a wave's LDS
-// accesses are performed in program order.
-template <int N>
-__global__ __launch_bounds__(64) void k_ba_solve_wave(SolveArgs A) {
-    static_assert(N < 64, "lane N carries b");
-    __shared__ __attribute__((aligned(16))) double col[64];
-    __shared__ __attribute__((aligned(16))) double Lp[64][kPanelW];
-    __shared__ double Lrow[N * (N + 1)];  // L rows, leading dimension N + 1
-    const int lane = threadIdx.x;
-    const double* src = lane < N ? A.S_dbg + (size_t)lane * N : A.b_dbg;  // lanes > N: b too
-    double r[N];
-#pragma unroll
-    for (int m = 0; m < N; m++) r[m] = src[m];
-    bool ok = true;
-    double invd = 0.0;  // 1 / L_ii of this lane's row
-    wave_cholesky<N, kPanelW>(r, Lp, ok, invd);
-    // z to LDS (lane N), the rows of L to LDS, then each lane's column of L
-    if (lane == N) {
-#pragma unroll
-        for (int m = 0; m < N; m++) col[m] = r[m];
-    }
-    if (lane < N) {
-#pragma unroll
-        for (int m = 0; m < N; m++) Lrow[lane * (N + 1) + m] = r[m];
-    }
-    const int lc = lane < N ? lane : 0;
-    double c[N];  // c[k] = L[k][lane], used for k > lane
-#pragma unroll
-    for (int k = 0; k < N; k++) c[k] = Lrow[k * (N + 1) + lc];
-    // backward: L^T x = z; lanes past their own step keep updating unused acc
-    double acc = col[lc];
-    double x = 0.0;
-#pragma unroll
-    for (int k = N - 1; k >= 0; k--) {
-        const double xk = bcast(acc * invd, k);
-        if (lane == k) x = xk;
-        acc -= c[k] * xk;
-    }
-    col[lane] = x;
-    __builtin_amdgcn_wave_barrier();
-    // finish_solve's outputs with the solution in col[]
-    if (lane == 0) {
-        A.flags[0] = ok ? 0 : 1;
-        if (!ok) A.flags[1] = 1;
-    }
-    if (lane < N) {
-        A.dx_dbg[lane] = ok ? x : 0.0;
-        A.dx[lane] = ok ? (float)x : 0.0f;
-    }
-    if (!ok) return;
-    // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
-    for (int k = A.t0 + lane; k < A.t1; k += 64) {
-        double t[3], q[4], xi[6], t1[3], q1[4];
-        load_pose(A.poses, k, t, q);
-        for (int m = 0; m < 6; m++) xi[m] = (double)(float)col[(k - A.t0) * 6 + m];
-        retr_se3(xi, t, q, t1, q1);
-        for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
-        for (int m = 0; m < 4; m++) A.poses[k * 7 + 3 + m] = (float)q1[m];
-    }
-}
-
-template <int P>
-void launch_solve_wave(const SolveArgs& A, hipStream_t stream) {
-    hipLaunchKernelGGL(k_ba_solve_wave<6 * P>, dim3(1), dim3(64), 0, stream, A);
-}
-
 // ---- one-workgroup panel solver (n <= kPanelN: the frontend's systems) ----
 // LDL^T of the bordered matrix [S b; b^T *] in LDS, right-looking in panels
 // of kPW columns. The system is padded to n8 = a multiple of kPW with
@@ -996,31 +925,180 @@ __global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
     finish_solve(A, xs, ok, pose0);
 }
 
-// 1..kWaveP free poses take the wavefront solver
-constexpr int kWaveP = 10;
-bool solve_wave(int P, const SolveArgs& A, hipStream_t stream) {
-    switch (P) {
-        case 1: launch_solve_wave<1>(A, stream); return true;
-        case 2: launch_solve_wave<2>(A, stream); return true;
-        case 3: launch_solve_wave<3>(A, stream); return true;
-        case 4: launch_solve_wave<4>(A, stream); return true;
-        case 5: launch_solve_wave<5>(A, stream); return true;
-        case 6: launch_solve_wave<6>(A, stream); return true;
-        case 7: launch_solve_wave<7>(A, stream); return true;
-        case 8: launch_solve_wave<8>(A, stream); return true;
-        case 9: launch_solve_wave<9>(A, stream); return true;
-        case 10: launch_solve_wave<10>(A, stream); return true;
-        default: return false;
+// ---- one-workgroup solver with the system in registers (n <= 64) ----
+// LDL^T of the bordered matrix [S b; b^T *] padded to n8 (a multiple of
+// kPW, <= 64) as in k_ba_solve_panel, but the working matrix never lives in
+// LDS: its lower triangle is cut into 2 x 2 blocks (block row n8 / 2 holds
+// b^T alone), each owned by one thread for the whole factorization
+// (kSmallSlots register blocks per thread), and loaded from the assembled
+// system once. Per panel of kPW columns, two barriers:
+// (1) the owners of the panel's blocks publish them (rows c0..n8) to LDS;
+// (2) every thread reads the panel's diagonal block and eliminates it
+//     itself (uniform values: pivots, 1/d by estimate + two Newton steps,
+//     multipliers), so every thread takes the same pivot test without a
+//     shared flag; thread t then finishes row r0 + t of the panel by forward
+//     substitution against the diagonal block and publishes its l and d*l;
+// (3) every thread subtracts the panel's products from its own blocks right
+//     of the panel, A[i][k] -= sum_m l_im (d_m l_km).
+// The l of every panel also go to a full copy of L (upper part and rows
+// past n8 zero), which wave 0's backward solve L^T x = w (w = D^-1 L^-1 b,
+// the bordered row) reads column by column with constant offsets, every
+// read unconditional (a conditional LDS read becomes a branch that waits
+// for it).
+constexpr int kSmallN = 64;
+constexpr int kSmallSlots = 3;  // ceil(560 / 256): 2 x 2 blocks of n8 = 64 per thread
+static_assert(kSmallN % kPW == 0 && kSmallN <= 64, "one row per lane in the backward solve");
+
+__global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
+    __shared__ double PU[kSmallN + 1][kPW];                              // panel as published
+    __shared__ __attribute__((aligned(16))) double PL[kSmallN + 1][kPW];  // l of rows >= r0
+    __shared__ __attribute__((aligned(16))) double PD[kSmallN + 1][kPW];  // d_m * l of rows >= r0
+    // L by rows, row n8 = w; zero elsewhere (sized to whole rounds of zeroing)
+    __shared__ __attribute__((aligned(16))) double Lf[(kSmallN + 1 + 7) / 8 * 8][64];
+    __shared__ double xs[kSmallN];
+    __shared__ float pose0[(kSmallN / 6) * 7];
+    const int n = A.n, n8 = pad_panel(n), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hb = n8 / 2;                    // block rows 0..hb (hb: b^T)
+    const int nblk = hb * (hb + 1) / 2 + hb;  // lower 2 x 2 blocks
+    if (tid < (A.t1 - A.t0) * 7) pose0[tid] = A.poses[A.t0 * 7 + tid];
+    {
+        constexpr int kZeroRounds = sizeof(Lf) / (256 * 16);
+        static_assert(sizeof(Lf) % (256 * 16) == 0, "whole rounds of 16-byte writes");
+#pragma unroll
+        for (int u = 0; u < kZeroRounds; u++)
+            reinterpret_cast<double2*>(&Lf[0][0])[tid + 256 * u] = make_double2(0.0, 0.0);
     }
+    // this thread's blocks: (i0, k0) of slot s, and their four entries
+    int bi0[kSmallSlots], bk0[kSmallSlots];
+    double a[kSmallSlots][4];
+#pragma unroll
+    for (int s = 0; s < kSmallSlots; s++) {
+        const int b = tid + 256 * s;
+        int bi = hb, bk = b - hb * (hb + 1) / 2;
+        if (b < hb * (hb + 1) / 2) {
+            bi = (int)((__builtin_sqrt(8.0 * b + 1.0) - 1.0) * 0.5);
+            bk = b - bi * (bi + 1) / 2;
+        }
+        const bool live = b < nblk;
+        bi0[s] = live ? 2 * bi : -2;  // -2: no block (never in a panel's rows)
+        bk0[s] = live ? 2 * bk : -2;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = 2 * bi + (e >> 1), k = 2 * bk + (e & 1);
+            double x = i == k ? 1.0 : 0.0;
+            if (live && k < n && i < n && k <= i) x = A.S_dbg[(size_t)i * n + k];
+            if (live && k < n && i == n8) x = A.b_dbg[k];
+            a[s][e] = x;
+        }
+    }
+    bool ok = true;
+    for (int c0 = 0; c0 < n8; c0 += kPW) {  // uniform
+        const int r0 = c0 + kPW;
+        // (1) publish the panel's columns, rows c0..n8
+#pragma unroll
+        for (int s = 0; s < kSmallSlots; s++) {
+            const int i0 = bi0[s], k0 = bk0[s];
+            if (i0 >= c0 && k0 >= c0 && k0 < r0) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int i = i0 + (e >> 1), k = k0 + (e & 1);
+                    if (i <= n8 && k <= i) PU[i][k - c0] = a[s][e];
+                }
+            }
+        }
+        __syncthreads();
+        // (2) the diagonal block, eliminated by every thread (uniform)
+        double D[kPW][kPW], Lb[kPW][kPW], rj[kPW], dj[kPW];
+#pragma unroll
+        for (int i = 0; i < kPW; i++)
+#pragma unroll
+            for (int k = 0; k <= i; k++) D[i][k] = PU[c0 + i][k];
+#pragma unroll
+        for (int j = 0; j < kPW; j++) {
+            dj[j] = D[j][j];
+            ok = ok && (dj[j] > 0.0);
+            rj[j] = rcp_f64(dj[j]);
+#pragma unroll
+            for (int i = j + 1; i < kPW; i++) Lb[i][j] = D[i][j] * rj[j];
+#pragma unroll
+            for (int i = j + 1; i < kPW; i++)
+#pragma unroll
+                for (int k = j + 1; k <= i; k++) D[i][k] -= Lb[i][j] * D[k][j];
+        }
+        if (!ok) break;  // uniform: every thread took the same pivots
+        if (tid <= n8 - r0) {
+            // rows r0..n8: forward substitution against the block, thread t
+            // on row r0 + t
+            const int row = r0 + tid;
+            double u[kPW], l[kPW];
+#pragma unroll
+            for (int j = 0; j < kPW; j++) u[j] = PU[row][j];
+#pragma unroll
+            for (int j = 0; j < kPW; j++) {
+                double v = u[j];
+#pragma unroll
+                for (int m = 0; m < j; m++) v -= l[m] * (Lb[j][m] * dj[m]);
+                l[j] = v * rj[j];
+            }
+#pragma unroll
+            for (int j = 0; j < kPW; j++) {
+                PL[row][j] = l[j];
+                PD[row][j] = l[j] * dj[j];
+                Lf[row][c0 + j] = l[j];
+            }
+        }
+        if (tid == 255) {  // the diagonal block's rows of L (constant indices into Lb)
+#pragma unroll
+            for (int q = 1; q < kPW; q++)
+#pragma unroll
+                for (int m = 0; m < q; m++) Lf[c0 + q][c0 + m] = Lb[q][m];
+        }
+        __syncthreads();
+        // (3) this thread's blocks right of the panel
+#pragma unroll
+        for (int s = 0; s < kSmallSlots; s++) {
+            const int i0 = bi0[s], k0 = bk0[s];
+            if (k0 >= r0) {  // then i0 >= k0 >= r0 (no-block slots have k0 = -2)
+                const int i1 = min(i0 + 1, n8);
+                double s00 = 0.0, s01 = 0.0, s10 = 0.0, s11 = 0.0;
+#pragma unroll
+                for (int m = 0; m < kPW; m++) {
+                    const double x0 = PL[i0][m], x1 = PL[i1][m];
+                    const double y0 = PD[k0][m], y1 = PD[k0 + 1][m];
+                    s00 += x0 * y0;
+                    s01 += x0 * y1;
+                    s10 += x1 * y0;
+                    s11 += x1 * y1;
+                }
+                a[s][0] -= s00;
+                a[s][1] -= s01;
+                a[s][2] -= s10;
+                a[s][3] -= s11;
+            }
+        }
+    }
+    // (every thread left the loop at the same panel; the last barrier of a
+    // completed factorization orders the writes of Lf before these reads)
+    if (ok && wave == 0) {
+        double c[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) c[k] = Lf[k][lane];  // zero unless lane < k < n8
+        double acc = Lf[n8][lane];
+#pragma unroll
+        for (int k = 63; k >= 0; k--) acc -= c[k] * bcast(acc, k);
+        if (lane < n8) xs[lane] = acc;
+    }
+    __syncthreads();
+    finish_solve(A, xs, ok, pose0);
 }
 
-// ---- blocked Cholesky over many workgroups (n > 90: the backend's systems) ----
+// ---- blocked Cholesky over many workgroups (n > kPanelN: the backend's systems) ----
 // Right-looking, lower, on the row-major working copy A.S, which holds the
 // system in rows 0..n-1 and b^T in row n (leading dimension n): factoring the
 // bordered matrix [S b; b^T *] leaves L^-1 b in row n, so the forward solve
 // costs one more panel row. In kCB-column steps: (1) k_chol_diag factors the
-// kCB x kCB diagonal block in one wavefront's registers (lane = row, as
-// k_ba_solve_wave); (2) k_chol_panel solves the rows below it (b's row
+// kCB x kCB diagonal block in one wavefront's registers (lane = row,
+// wave_cholesky); (2) k_chol_panel solves the rows below it (b's row
 // included) against it, one thread per row; (3) k_chol_syrk subtracts the
 // new panel's products from the trailing lower triangle in 64 x 64 tiles,
 // one workgroup per tile. k_chol_finish then runs the backward solve
@@ -1541,9 +1619,9 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
         hipLaunchKernelGGL(k_ba_assemble, dim3(s->P * s->P + s->P), dim3(256), 0, stream, A);
     }
     SLK_HIP(hipGetLastError());
-    if (s->P <= kWaveP) {
+    if (s->n <= kSmallN) {
         ProfScope ps(ctx, "ba_solve", stream);
-        solve_wave(s->P, A, stream);
+        hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(256), 0, stream, A);
     } else if (s->n <= kPanelN) {
         // t1 - t0 = P <= kPanelPoses
         ProfScope ps(ctx, "ba_solve", stream);
