@@ -217,6 +217,19 @@ int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const float* intrin
                    const int* jj_host, int num_edges, int t0, int t1, float lm,
                    float ep, int motion_only, hipStream_t stream);
 
+/* `iters` iterations of slk_ba_iterate on the same edge set: the loop of
+ * run_update_pass over BundleAdjustment::iterate (cuda_slam/main.cu:2371-2389,
+ * cuda_pipeline/slam.cuh:3178-3186). Same results as `iters` calls; a window
+ * whose keyframes each have at most 7 E rows (own pose + other free poses)
+ * runs each iteration as linearization with Schur partials, assembly and
+ * solve, with the back-substitution of one step folded into the next
+ * linearization. */
+int slk_ba_iterate_n(slk_ctx* ctx, float* poses, float* disps, const float* intrinsics,
+                     const float* target, const float* weight, const float* eta,
+                     const int* ii_gpu, const int* jj_gpu, const int* ii_host,
+                     const int* jj_host, int num_edges, int t0, int t1, float lm,
+                     float ep, int motion_only, int iters, hipStream_t stream);
+
 /* Synchronises `stream` and returns SLK_E_NOT_SPD if any iterate since the
  * last call met an indefinite system, else SLK_OK; clears the flag. */
 int slk_ba_status(slk_ctx* ctx, hipStream_t stream);

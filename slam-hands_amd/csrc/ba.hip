@@ -167,38 +167,47 @@ __device__ __forceinline__ void edge_rel(const float* poses, int ix, int jx, dou
     }
 }
 
+// p[0] + p[stride] + ... + p[(n - 1) stride], added in that order, with the
+// loads of sixteen terms in flight at a time (a plain loop waits for each).
+__device__ __forceinline__ double sum_strided(const double* __restrict__ p, size_t stride, int n) {
+    double t = 0.0;
+    for (int c = 0; c < n; c += 16) {
+        double v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = c + u < n ? p[(size_t)(c + u) * stride] : 0.0;
+#pragma unroll
+        for (int u = 0; u < 16; u++) t += v[u];
+    }
+    return t;
+}
+
 // Totals of edge e over the nch pixel chunks (summed in chunk order),
 // expanded to the four Hessian blocks and both gradients of ba.cuh:198-220
-// with the edge's Adj: etot[e] = Hii, Hij, Hjj, vi, vj. One wave; `sh` holds
-// 27 + 36 + 36 doubles.
+// with the edge's Adj: et[0..120) = Hii, Hij, Hjj, vi, vj. One wave; `sh`
+// holds 27 + 36 + 36 doubles.
 __device__ void edge_totals(int e, const float* __restrict__ poses, const int* __restrict__ ii,
                             const int* __restrict__ jj, const double* __restrict__ hpart,
-                            double* __restrict__ etot, int nch, double* sh) {
+                            double* __restrict__ et, int nch, double* sh) {
     const int lane = threadIdx.x & 63;
     double* tot = sh;
     double* adj = tot + kNJ;
     double* ah = adj + 36;
-    if (lane < kNJ) {
-        const double* hp = hpart + (size_t)e * nch * kNJ + lane;
-        double t = 0.0;
-        for (int c = 0; c < nch; c++) t += hp[(size_t)c * kNJ];
-        tot[lane] = t;
-    }
+    if (lane < kNJ) tot[lane] = sum_strided(hpart + (size_t)e * nch * kNJ + lane, kNJ, nch);
     double tij[3], qij[4];
     edge_rel(poses, ii[e], jj[e], tij, qij);
-    // Adj column by column: adj_se3 of the unit vectors (se3.cuh:28-41)
-#pragma unroll 1
-    for (int c = 0; c < 6; c++) {
+    // Adj column by column, lane c < 6 forming column c: adj_se3 of the unit
+    // vectors (se3.cuh:28-41)
+    {
         double u[6], y[6];
-        for (int m = 0; m < 6; m++) u[m] = m == c ? 1.0 : 0.0;
-        adj_se3(tij, qij, u, y);
 #pragma unroll
-        for (int r = 0; r < 6; r++)
-            if (lane == r) adj[r * 6 + c] = y[r];
+        for (int m = 0; m < 6; m++) u[m] = m == lane ? 1.0 : 0.0;
+        adj_se3(tij, qij, u, y);
+        if (lane < 6)
+#pragma unroll
+            for (int r = 0; r < 6; r++) adj[r * 6 + lane] = y[r];
     }
     __builtin_amdgcn_wave_barrier();
     const int r = lane / 6, c = lane - (lane / 6) * 6;
-    double* et = etot + (size_t)e * kNT;
     if (lane < 36) {
         double t = 0.0;  // (Adj Hjj)[r][c]
 #pragma unroll
@@ -453,7 +462,9 @@ __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double*
     __shared__ double red[36 * (kSchWG / 64)];
     const int item = blockIdx.x;
     if (item >= N_items) {
-        if (threadIdx.x < 64) edge_totals(item - N_items, poses, ii, jj, hpart, etot, nch, red);
+        if (threadIdx.x < 64)
+            edge_totals(item - N_items, poses, ii, jj, hpart,
+                        etot + (size_t)(item - N_items) * kNT, nch, red);
         return;
     }
     double acc[36];
@@ -505,6 +516,7 @@ struct SolveArgs {
     float* dx;      // [n] fp32 step used by retraction and back-substitution
     int* flags;     // [0] this iteration not SPD, [1] sticky
     float* poses;
+    float* poses_prev;  // [P][7] poses t0..t1-1 before the step (fused path), or null
 };
 
 // One edge-block or Schur-item contribution to entry (r, c) of a 6x6 block of
@@ -603,6 +615,8 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
     // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
     for (int k = A.t0 + threadIdx.x; k < A.t1; k += blockDim.x) {
         double t[3], q[4], xi[6], t1[3], q1[4];
+        if (A.poses_prev)  // the fused path's back-substitution relinearizes at these
+            for (int m = 0; m < 7; m++) A.poses_prev[(k - A.t0) * 7 + m] = pose_src[(k - A.t0) * 7 + m];
         load_pose(pose_src, k - A.t0, t, q);
         for (int m = 0; m < 6; m++) xi[m] = (double)(float)x[(k - A.t0) * 6 + m];
         retr_se3(xi, t, q, t1, q1);
@@ -1332,6 +1346,509 @@ __global__ __launch_bounds__(256) void k_ba_backsub(PlanDev plan, const double* 
     *d = (float)((double)*d + dz);
 }
 
+// ===================================================== fused iteration ====
+// Systems whose keyframes have at most kFzMaxSlots E rows each (the
+// frontend's windows) run an iteration in three launches, and the E rows
+// never reach HBM:
+//   k_ba_fz  grid (pixel chunk, keyframe). Optionally first the
+//            back-substitution of the previous step (EvT6x1 + depth_update,
+//            ba.cuh:762-783), by relinearizing every edge of the keyframe at
+//            the poses and depths that step was taken from: dw = sum_e g_e .
+//            (dx_j - Adj_e^T dx_i), g_e = w Jz Jj per pixel (the E rows of
+//            ba.cuh:139-140, 167-168 regrouped by edge). Then the
+//            linearization at the current state: the Hjj/vj partials of every
+//            edge as in k_ba_lin_wv, and the keyframe's E rows and w for the
+//            chunk's pixels in LDS as [pixel][row], from which the chunk's
+//            Schur products Z = [E; w] Q [E; w]^T (EEt6x6 / Ev6x1,
+//            ba.cuh:303-372) are formed on fp64 MFMA (v_mfma_f64_16x16x4),
+//            each wave over 64 pixels, the four partials added in wave order.
+//   k_ba_fz_assemble  one workgroup per block of S and per segment of b: the
+//            chunk sums (in chunk order) of the Z entries and edge partials
+//            the block needs, then the LM damping.
+//   a solve kernel, which also keeps the poses before the step.
+// A last k_ba_fz<bs only> applies the final step's back-substitution.
+// E rows ("slots") of a keyframe: its own pose when free (slot 0), then one
+// per non-stereo edge whose jj is free, in edge order (two edges to the same
+// pose keep separate slots; the assembly adds their products). Row 6 * nslot
+// holds w; the rows after it, up to 16 T, are zero.
+constexpr int kFzMaxSlots = 7;
+constexpr int kFzMaxT = 3;                             // 16-row tiles of [E; w]
+constexpr int kFzMaxNT = kFzMaxT * (kFzMaxT + 1) / 2;  // tiles (ti <= tj) kept
+constexpr int kFzLd = 16 * kFzMaxT + 9;  // doubles per pixel in LDS (odd: 2-way stores)
+constexpr int kFzMaxDst = 32;            // distinct edges feeding one block of S or b
+static_assert(6 * kFzMaxSlots + 1 <= 16 * kFzMaxT, "the slot rows and w fill at most T tiles");
+static_assert(kLinPx == kLinWG && kLinPx == 256, "one pixel per thread in the per-pixel steps");
+
+struct FzKf {
+    int kf, e0, e1, info;  // edges e0..e1 of the edge table; info = nslot | ri << 8 | T << 12
+};
+struct FzEdge {
+    int e, ix, jx, slot;  // slot of the edge's own E row, -1 for none
+};
+
+struct FzArgs {
+    const FzKf* kfs;
+    const FzEdge* eds;
+    const float* target;
+    const float* weight;
+    const float* poses;
+    const float* poses_prev;  // [P][7]: poses t0..t1-1 before the last step
+    const float* intr;
+    const float* eta;
+    const float* dx;   // [6P] the last step
+    const int* flags;  // [0]: the last step was rejected (not SPD)
+    float* disps;
+    double* hpart;  // [M][nch][27]
+    double* spart;  // [N_kf][nch][kFzMaxNT][256] Z tiles in MFMA lane order
+    int HW, W, nch, t0, t1;
+};
+
+// Relative pose of edge (ix, jx) at the current poses, or (prev) at the poses
+// of the last step's linearization: only t0..t1-1 moved.
+__device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int jx, double* tij,
+                                       double* qij) {
+    if (ix == jx) {
+        edge_rel(F.poses, ix, jx, tij, qij);  // stereo constants
+        return;
+    }
+    double ti[3], qi[4], tj[3], qj[4];
+    const bool pi = prev && ix >= F.t0 && ix < F.t1, pj = prev && jx >= F.t0 && jx < F.t1;
+    load_pose(pi ? F.poses_prev : F.poses, pi ? ix - F.t0 : ix, ti, qi);
+    load_pose(pj ? F.poses_prev : F.poses, pj ? jx - F.t0 : jx, tj, qj);
+    rel_se3(ti, qi, tj, qj, tij, qij);
+}
+
+typedef double fz_d4 __attribute__((ext_vector_type(4)));
+
+template <bool kBs, bool kLin>
+__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
+    __shared__ double xs[kLinPx * kFzLd];        // [pixel][row]; then the MFMA partials
+    __shared__ double cw[3][kLinWaves][kLinPx];  // per-wave sums (dw, C, w) / (C, w)
+    __shared__ double qs[kLinPx];
+    __shared__ float dnew[kLinPx];
+    const int chunk = blockIdx.x, kc = blockIdx.y;
+    const FzKf K = F.kfs[kc];
+    const int nslot = K.info & 0xff, ri = (K.info >> 8) & 1, T = K.info >> 12;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int HW = F.HW;
+    const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
+    int kpx[kLinPPL];
+    bool vpx[kLinPPL];
+    double dsp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        kpx[s] = chunk * kLinPx + s * 64 + lane;
+        vpx[s] = kpx[s] < HW;
+        dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
+    }
+    // the wave's first edge as the back-substitution pass saw it, reused by the
+    // linearization pass: its record, relative pose at the current poses, and
+    // targets / weights
+    bool cached = false;
+    FzEdge E0 = {0, 0, 0, -1};
+    double t0n[3] = {0.0, 0.0, 0.0}, q0n[4] = {0.0, 0.0, 0.0, 1.0};
+    float c_tgu[kLinPPL], c_tgv[kLinPPL], c_wtu[kLinPPL], c_wtv[kLinPPL];
+    if (kBs && F.flags[0] == 0) {  // uniform; a rejected step leaves the depths as they are
+        double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
+        for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
+            const FzEdge E = F.eds[ei];
+            const bool stereo = E.ix == E.jx;
+            double tij[3], qij[4];
+            fz_rel(F, true, E.ix, E.jx, tij, qij);
+            const bool first = kLin && ei == K.e0 + wave;
+            if (first) fz_rel(F, false, E.ix, E.jx, t0n, q0n);
+            // dl = dx_j (the edge's own row) - Adj^T dx_i (the keyframe's row)
+            double dl[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+            if (!stereo) {
+                if (E.slot >= 0)
+#pragma unroll
+                    for (int n = 0; n < 6; n++) dl[n] = (double)F.dx[(E.jx - F.t0) * 6 + n];
+                if (ri) {  // lane c < 6: (Adj^T dx_i)[c] = adj_se3(e_c) . dx_i
+                    double u[6], y[6], t = 0.0;
+#pragma unroll
+                    for (int m = 0; m < 6; m++) u[m] = m == lane ? 1.0 : 0.0;
+                    adj_se3(tij, qij, u, y);
+#pragma unroll
+                    for (int m = 0; m < 6; m++) t += y[m] * (double)F.dx[(E.ix - F.t0) * 6 + m];
+#pragma unroll
+                    for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
+                }
+            }
+            float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
+                tgu[s] = F.target[base];
+                tgv[s] = F.target[base + HW];
+                wtu[s] = F.weight[base];
+                wtv[s] = F.weight[base + HW];
+            }
+            if (first) {
+                cached = true;
+                E0 = E;
+#pragma unroll
+                for (int s = 0; s < kLinPPL; s++) {
+                    c_tgu[s] = tgu[s];
+                    c_tgv[s] = tgv[s];
+                    c_wtu[s] = wtu[s];
+                    c_wtv[s] = wtv[s];
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                if (!vpx[s]) continue;
+                Lin L;
+                lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
+                          (double)tgv[s], (double)wtu[s], (double)wtv[s], L);
+                cp[s] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
+                wp[s] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
+                if (!stereo) {
+                    const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
+                    double t = 0.0;
+#pragma unroll
+                    for (int n = 0; n < 6; n++) t += (a0 * L.Jj[0][n] + a1 * L.Jj[1][n]) * dl[n];
+                    dwp[s] += t;
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            const int px = s * 64 + lane;
+            cw[0][wave][px] = dwp[s];
+            cw[1][wave][px] = cp[s];
+            cw[2][wave][px] = wp[s];
+        }
+        __syncthreads();
+        {
+            const int k = chunk * kLinPx + tid;
+            if (k < HW) {
+                double dw = 0.0, c = 0.0, w = 0.0;
+#pragma unroll
+                for (int v = 0; v < kLinWaves; v++) {
+                    dw += cw[0][v][tid];
+                    c += cw[1][v][tid];
+                    w += cw[2][v][tid];
+                }
+                // damping_Q_kernel (ep = 1e-7) and depth_update_kernel
+                const double q = 1.0 / (c + 0.2 * (double)F.eta[(size_t)K.kf * HW + k] + 1e-7);
+                float* d = F.disps + (size_t)K.kf * HW + k;
+                const float dn = (float)((double)*d + q * (w - dw));
+                *d = dn;
+                dnew[tid] = dn;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++)
+            if (vpx[s]) dsp[s] = (double)dnew[s * 64 + lane];
+    }
+    if (!kLin) return;
+    {
+        // rows past the slots and w (and every row of a pixel past HW) are zero
+        const int k = chunk * kLinPx + tid;
+        double* xr = xs + tid * kFzLd;
+        for (int r = k < HW ? 6 * nslot + 1 : 0; r < 16 * T; r++) xr[r] = 0.0;
+    }
+    double er[kLinPPL][6];  // this lane's pixels: -sum Adj g over the wave's edges
+    double cp[kLinPPL], wp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        cp[s] = wp[s] = 0.0;
+#pragma unroll
+        for (int n = 0; n < 6; n++) er[s][n] = 0.0;
+    }
+    for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
+        const bool hit = cached && ei == K.e0 + wave;  // uniform
+        const FzEdge E = hit ? E0 : F.eds[ei];
+        const bool stereo = E.ix == E.jx;
+        double tij[3], qij[4];
+        float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+        if (hit) {
+#pragma unroll
+            for (int m = 0; m < 3; m++) tij[m] = t0n[m];
+#pragma unroll
+            for (int m = 0; m < 4; m++) qij[m] = q0n[m];
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                tgu[s] = c_tgu[s];
+                tgv[s] = c_tgv[s];
+                wtu[s] = c_wtu[s];
+                wtv[s] = c_wtv[s];
+            }
+        } else {
+            fz_rel(F, false, E.ix, E.jx, tij, qij);
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
+                tgu[s] = F.target[base];
+                tgv[s] = F.target[base + HW];
+                wtu[s] = F.weight[base];
+                wtv[s] = F.weight[base + HW];
+            }
+        }
+        double acc[kNJ];
+#pragma unroll
+        for (int n = 0; n < kNJ; n++) acc[n] = 0.0;
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            if (!vpx[s]) continue;
+            const int px = s * 64 + lane;
+            Lin L;
+            lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
+                      (double)tgv[s], (double)wtu[s], (double)wtv[s], L);
+            accum_hjj(L, stereo, acc);
+            cp[s] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
+            wp[s] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
+            if (!stereo) {  // a stereo edge adds nothing to E
+                const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
+                double g[6];
+#pragma unroll
+                for (int n = 0; n < 6; n++) g[n] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                if (E.slot >= 0) {
+                    double* xr = xs + px * kFzLd + 6 * E.slot;
+#pragma unroll
+                    for (int n = 0; n < 6; n++) xr[n] = g[n];
+                }
+                if (ri) {  // Ji-row contribution -Adj g (ba.cuh:139-140)
+                    double gi[6];
+                    adj_se3(tij, qij, g, gi);
+#pragma unroll
+                    for (int n = 0; n < 6; n++) er[s][n] -= gi[n];
+                }
+            }
+        }
+        int rbase, rvalid;
+        wave_reduce_scatter(acc, lane, rbase, rvalid);
+        double* hp = F.hpart + ((size_t)E.e * F.nch + chunk) * kNJ;
+#pragma unroll
+        for (int q = 0; q < RsCounts<kNJ>::c6; q++)
+            if (q < rvalid) hp[rbase + q] = acc[q];
+    }
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        const int px = s * 64 + lane;
+        cw[0][wave][px] = cp[s];
+        cw[1][wave][px] = wp[s];
+    }
+    if (ri) {  // uniform: the keyframe's own row (slot 0), the waves' parts added in order
+        for (int v = 0; v < kLinWaves; v++) {
+            __syncthreads();
+            if (wave == v) {
+#pragma unroll
+                for (int s = 0; s < kLinPPL; s++) {
+                    if (!vpx[s]) continue;
+                    double* xr = xs + (s * 64 + lane) * kFzLd;
+#pragma unroll
+                    for (int n = 0; n < 6; n++) xr[n] = (v == 0 ? 0.0 : xr[n]) + er[s][n];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    {
+        const int k = chunk * kLinPx + tid;
+        double q = 0.0;
+        if (k < HW) {
+            double c = 0.0, w = 0.0;
+#pragma unroll
+            for (int v = 0; v < kLinWaves; v++) {
+                c += cw[0][v][tid];
+                w += cw[1][v][tid];
+            }
+            // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
+            q = 1.0 / (c + 0.2 * (double)F.eta[(size_t)K.kf * HW + k] + 1e-7);
+            xs[tid * kFzLd + 6 * nslot] = w;
+        }
+        qs[tid] = q;
+    }
+    __syncthreads();
+    // Z over this wave's 64 pixels: A = rows 16 ti.. of 4 pixels, B = Q * rows 16 tj..
+    // (lane l holds row l % 16 of pixel l / 16 in both operands)
+    fz_d4 z[kFzMaxNT];
+#pragma unroll
+    for (int t = 0; t < kFzMaxNT; t++) z[t] = fz_d4{0.0, 0.0, 0.0, 0.0};
+    const int i16 = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+        const int kp = wave * 64 + ks * 4 + kg;
+        const double q = qs[kp];
+        const double* xr = xs + kp * kFzLd + i16;
+        double a[kFzMaxT], b[kFzMaxT];
+#pragma unroll
+        for (int t = 0; t < kFzMaxT; t++) {
+            a[t] = t < T ? xr[16 * t] : 0.0;
+            b[t] = a[t] * q;
+        }
+        int tt = 0;
+#pragma unroll
+        for (int tj = 0; tj < kFzMaxT; tj++)
+#pragma unroll
+            for (int ti = 0; ti <= tj; ti++, tt++)
+                if (tj < T) z[tt] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ti], b[tj], z[tt], 0, 0, 0);
+    }
+    __syncthreads();
+    double* red = xs;  // [wave][tile][256]: lane * 4 + r
+    const int nt = T * (T + 1) / 2;
+#pragma unroll
+    for (int t = 0; t < kFzMaxNT; t++)
+        if (t < nt)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(wave * kFzMaxNT + t) * 256 + lane * 4 + r] = z[t][r];
+    __syncthreads();
+    double* sp = F.spart + (size_t)(kc * F.nch + chunk) * kFzMaxNT * 256;
+    for (int idx = tid; idx < nt * 256; idx += kLinWG) {
+        double v = red[idx];
+#pragma unroll
+        for (int w = 1; w < kLinWaves; w++) v += red[w * kFzMaxNT * 256 + idx];
+        sp[idx] = v;
+    }
+}
+
+struct FzAsmArgs {
+    const int4* items;  // {kc, s1, s2 or -1 (the w column), w row}
+    const int* dptr;    // [P*P + P + 1] contribution codes of each block / segment
+    const int* dsrc;
+    const int* deptr;   // [P*P + P + 1] the distinct edges those codes refer to
+    const int* dedges;
+    const double* hpart;
+    const double* spart;
+    const float* poses;
+    const int* ii;
+    const int* jj;
+    int nch, P, n;
+    float lm, ep;
+    double* S;  // [n][n] assembled system (after damping)
+    double* b;  // [n]
+};
+
+// Entry (row, col) of a keyframe's Z, summed over the chunks: Z is symmetric
+// and only its upper tiles are kept, in the MFMA's lane order (result
+// register r of lane l holds entry (4 r + l / 16, l % 16) of a 16 x 16 tile;
+// the A operand of lane l is (l % 16, l / 16), the B operand (l / 16, l % 16)).
+__device__ __forceinline__ double fz_z(const FzAsmArgs& A, int kc, int row, int col) {
+    const int lo = min(row, col), hi = max(row, col);
+    const int th = hi >> 4, tl = lo >> 4;
+    const int i = lo & 15, j = hi & 15;
+    const size_t idx = (size_t)(th * (th + 1) / 2 + tl) * 256 + ((i & 3) * 16 + j) * 4 + (i >> 2);
+    return sum_strided(A.spart + (size_t)kc * A.nch * kFzMaxNT * 256 + idx, kFzMaxNT * 256, A.nch);
+}
+
+// One workgroup per 6x6 block (a, b) of S (P*P) and per 6-entry segment of b
+// (P more), as k_ba_assemble, with the chunk sums done here. The totals of
+// the block's edges (edge_totals' arithmetic) are formed by the whole
+// workgroup at once: the chunk sums of all Hjj/vj partials, the Adj columns
+// (one thread per edge and column), then the expansions. Thread (slice,
+// entry) adds the Z entries of its slice's Schur items, then the edges' block
+// entries; the seven slices are added in a fixed order (deterministic, no
+// atomics).
+__global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
+    __shared__ double tot[kFzMaxDst][kNJ];   // chunk sums: Hjj (upper), vj
+    __shared__ double adj[kFzMaxDst][36];    // Adj of each edge, [r][c]
+    __shared__ double ah[kFzMaxDst][36];     // Adj Hjj
+    __shared__ double et[kFzMaxDst][kNT];    // Hii, Hij, Hjj, vi, vj
+    __shared__ double red[kAsmSlices][36];
+    const int g = blockIdx.x, tid = threadIdx.x;
+    const int sl = tid / 36, ent = tid - sl * 36;
+    const int P = A.P, n = A.n;
+    const bool isS = g < P * P;
+    const bool act = sl < kAsmSlices && (isS || ent < 6);
+    const int r = ent / 6, c = ent - (ent / 6) * 6;
+    const int q0 = A.dptr[g], q1 = A.dptr[g + 1];
+    const int d0 = A.deptr[g], nd = A.deptr[g + 1] - d0;
+    // (1) chunk sums of the edges' partials, and the Adj columns
+    for (int t = tid; t < nd * kNJ; t += 256) {
+        const int le = t / kNJ, v = t - (t / kNJ) * kNJ;
+        tot[le][v] = sum_strided(A.hpart + (size_t)A.dedges[d0 + le] * A.nch * kNJ + v, kNJ, A.nch);
+    }
+    for (int t = tid; t < nd * 6; t += 256) {
+        const int le = t / 6, cc = t - (t / 6) * 6;
+        const int e = A.dedges[d0 + le];
+        double tij[3], qij[4], u[6], y[6];
+        edge_rel(A.poses, A.ii[e], A.jj[e], tij, qij);
+#pragma unroll
+        for (int m = 0; m < 6; m++) u[m] = m == cc ? 1.0 : 0.0;
+        adj_se3(tij, qij, u, y);  // column cc (se3.cuh:28-41)
+#pragma unroll
+        for (int m = 0; m < 6; m++) adj[le][m * 6 + cc] = y[m];
+    }
+    // the Schur items (thread-private; their loads overlap the above)
+    double s = 0.0;
+    if (act) {
+        for (int q = q0 + sl; q < q1; q += kAsmSlices) {
+            const int cd = A.dsrc[q];
+            if (code_type(cd) != 1) continue;
+            const int4 it = A.items[code_val(cd)];
+            s -= isS ? fz_z(A, it.x, 6 * it.y + r, 6 * it.z + c) : fz_z(A, it.x, 6 * it.y + ent, it.w);
+        }
+    }
+    __syncthreads();
+    // (2) Hij = -Adj Hjj, Hjj, vi = -Adj vj, vj (ba.cuh:198-220 via Ji = -Adj^T Jj)
+    for (int t = tid; t < nd * 36; t += 256) {
+        const int le = t / 36, rc = t - (t / 36) * 36;
+        const int rr = rc / 6, cc = rc - (rc / 6) * 6;
+        double a = 0.0;
+#pragma unroll
+        for (int k = 0; k < 6; k++) a += adj[le][rr * 6 + k] * tot[le][tri(max(k, cc), min(k, cc))];
+        ah[le][rc] = a;
+        et[le][kTotHij + rc] = -a;
+        et[le][kTotHjj + rc] = tot[le][tri(max(rr, cc), min(rr, cc))];
+        if (rc < 6) {
+            double v = 0.0;
+#pragma unroll
+            for (int k = 0; k < 6; k++) v += adj[le][rc * 6 + k] * tot[le][21 + k];
+            et[le][kTotVi + rc] = -v;
+            et[le][kTotVj + rc] = tot[le][21 + rc];
+        }
+    }
+    __syncthreads();
+    // (3) Hii = Adj Hjj Adj^T
+    for (int t = tid; t < nd * 36; t += 256) {
+        const int le = t / 36, rc = t - (t / 36) * 36;
+        const int rr = rc / 6, cc = rc - (rc / 6) * 6;
+        double h = 0.0;
+#pragma unroll
+        for (int k = 0; k < 6; k++) h += ah[le][rr * 6 + k] * adj[le][cc * 6 + k];
+        et[le][kTotHii + rc] = h;
+    }
+    __syncthreads();
+    if (act) {
+        for (int q = q0 + sl; q < q1; q += kAsmSlices) {
+            const int cd = A.dsrc[q];
+            if (code_type(cd) != 0) continue;
+            const int v = code_val(cd);
+            if (isS) {
+                const double* e = et[v >> 2];
+                const int w = v & 3;
+                s += w == 0 ? e[kTotHii + r * 6 + c]
+                   : w == 1 ? e[kTotHij + r * 6 + c]
+                   : w == 2 ? e[kTotHij + c * 6 + r]
+                            : e[kTotHjj + r * 6 + c];
+            } else {
+                s += et[v >> 1][((v & 1) ? kTotVj : kTotVi) + ent];
+            }
+        }
+    }
+    if (sl < kAsmSlices) red[sl][ent] = s;
+    __syncthreads();
+    if (isS && tid < 36) {
+        double t = red[0][tid];
+#pragma unroll
+        for (int k = 1; k < kAsmSlices; k++) t += red[k][tid];
+        const int a = g / P, bb = g - (g / P) * P;
+        const int row = a * 6 + tid / 6, col = bb * 6 + tid % 6;
+        if (row == col) t = t + (double)A.ep + (double)A.lm * t;  // ba.cuh:749-750
+        A.S[(size_t)row * n + col] = t;
+    } else if (!isS && tid < 6) {
+        double t = red[0][tid];
+#pragma unroll
+        for (int k = 1; k < kAsmSlices; k++) t += red[k][tid];
+        A.b[(g - P * P) * 6 + tid] = t;
+    }
+}
+
 }  // namespace
 
 // ----------------------------------------------------------- host side ---
@@ -1348,6 +1865,10 @@ struct BaState {
     HostStage stage;
     bool has_system = false;
     bool lin_by_wave = false;  // no keyframe has two edges to the same free pose
+    // fused path (every keyframe with at most kFzMaxSlots E rows)
+    bool fz = false;
+    size_t fz_off[7] = {0};  // kfs, eds, items, dptr, dsrc, deptr, dedges (ints into host)
+    DevBuf spart, poses_prev;
 };
 
 namespace {
@@ -1361,6 +1882,86 @@ PlanDev plan_ptrs(BaState* s) {
                                  &p.blkmap};
     for (int i = 0; i < kPlanParts; i++) *f[i] = base + s->off[i];
     return p;
+}
+
+// Tables of the fused path (k_ba_fz, k_ba_fz_assemble), appended to the
+// packed plan 16-byte aligned; s->fz stays false when a keyframe has more
+// than kFzMaxSlots E rows or a block of S more than kFzMaxDst edges (those
+// systems take the five-kernel iteration). Slots, items and the contribution
+// lists follow the E rows and the S/b scatter of ba.cuh:520-548, 577-663.
+void build_fz(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, int motion_only,
+              const std::vector<int>& kf_list, const std::vector<int>& kf_eptr,
+              const std::vector<int>& kf_eidx) {
+    s->fz = false;
+    if (motion_only) return;
+    const int P = t1 - t0, N_kf = (int)kf_list.size();
+    const int ND = P * P + P;  // destinations: blocks of S, then segments of b
+    auto free_pose = [&](int f) { return f >= t0 && f < t1; };
+    std::vector<int> kfs, eds, items;
+    std::vector<std::vector<int>> codes(ND), dedges(ND);
+    for (int kc = 0; kc < N_kf; kc++) {
+        const int kf = kf_list[kc];
+        const int ri = free_pose(kf) ? 1 : 0;
+        std::vector<int> spose;  // pose of each slot
+        if (ri) spose.push_back(kf - t0);
+        for (int ei = kf_eptr[kc]; ei < kf_eptr[kc + 1]; ei++) {
+            const int e = kf_eidx[ei];
+            int slot = -1;
+            if (ii[e] != jj[e] && free_pose(jj[e])) {
+                slot = (int)spose.size();
+                spose.push_back(jj[e] - t0);
+            }
+            eds.insert(eds.end(), {e, ii[e], jj[e], slot});
+        }
+        const int nslot = (int)spose.size();
+        if (nslot > kFzMaxSlots) return;
+        const int T = (6 * nslot + 1 + 15) / 16;
+        kfs.insert(kfs.end(), {kf, kf_eptr[kc], kf_eptr[kc + 1], nslot | ri << 8 | T << 12});
+        const int wrow = 6 * nslot;
+        for (int s1 = 0; s1 < nslot; s1++) {
+            for (int s2 = 0; s2 < nslot; s2++) {
+                codes[spose[s1] * P + spose[s2]].push_back(code(1, (int)items.size() / 4));
+                items.insert(items.end(), {kc, s1, s2, wrow});
+            }
+            codes[P * P + spose[s1]].push_back(code(1, (int)items.size() / 4));
+            items.insert(items.end(), {kc, s1, -1, wrow});
+        }
+    }
+    auto local = [&](int d, int e) {
+        std::vector<int>& v = dedges[d];
+        for (int k = 0; k < (int)v.size(); k++)
+            if (v[k] == e) return k;
+        v.push_back(e);
+        return (int)v.size() - 1;
+    };
+    for (int e = 0; e < M; e++) {
+        const int a = ii[e] - t0, b = jj[e] - t0;
+        const bool va = a >= 0 && a < P, vb = b >= 0 && b < P;
+        if (va) codes[a * P + a].push_back(code(0, local(a * P + a, e) * 4 + 0));
+        if (va && vb) {
+            codes[a * P + b].push_back(code(0, local(a * P + b, e) * 4 + 1));
+            codes[b * P + a].push_back(code(0, local(b * P + a, e) * 4 + 2));
+        }
+        if (vb) codes[b * P + b].push_back(code(0, local(b * P + b, e) * 4 + 3));
+        if (va) codes[P * P + a].push_back(code(0, local(P * P + a, e) * 2 + 0));
+        if (vb) codes[P * P + b].push_back(code(0, local(P * P + b, e) * 2 + 1));
+    }
+    std::vector<int> dptr(1, 0), dsrc, deptr(1, 0), dflat;
+    for (int d = 0; d < ND; d++) {
+        if ((int)dedges[d].size() > kFzMaxDst) return;
+        dsrc.insert(dsrc.end(), codes[d].begin(), codes[d].end());
+        dptr.push_back((int)dsrc.size());
+        dflat.insert(dflat.end(), dedges[d].begin(), dedges[d].end());
+        deptr.push_back((int)dflat.size());
+    }
+    const std::vector<int>* parts[7] = {&kfs, &eds, &items, &dptr, &dsrc, &deptr, &dflat};
+    for (int i = 0; i < 7; i++) {
+        while (s->host.size() % 4) s->host.push_back(0);
+        s->fz_off[i] = s->host.size();
+        s->host.insert(s->host.end(), parts[i]->begin(), parts[i]->end());
+        s->host.push_back(0);
+    }
+    s->fz = true;
 }
 
 // Builds the index structures of ba.cuh:520-663 once per edge set: keyframes
@@ -1494,6 +2095,7 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
         s->host.insert(s->host.end(), parts[i]->begin(), parts[i]->end());
         s->host.push_back(0);  // keeps every array non-empty
     }
+    build_fz(s, ii, jj, M, t0, t1, motion_only, kf_list, kf_eptr, kf_eidx);
     return SLK_OK;
 }
 
@@ -1522,79 +2124,80 @@ void ba_destroy(slk_ctx* ctx) {
 
 using namespace slk;
 
-extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const float* intrinsics,
-                              const float* target, const float* weight, const float* eta,
-                              const int* ii_gpu, const int* jj_gpu, const int* ii_host,
-                              const int* jj_host, int num_edges, int t0, int t1, float lm,
-                              float ep, int motion_only, hipStream_t stream) {
+namespace {
+
+struct IterArgs {
+    float* poses;
+    float* disps;
+    const float* intr;
+    const float* target;
+    const float* weight;
+    const float* eta;
+    const int* ii_gpu;
+    const int* jj_gpu;
+    int t0, t1;
+    float lm, ep;
+    int motion_only;
+};
+
+// Argument checks, and the plan and buffers of the edge set (rebuilt only
+// when the edge list, t0/t1 or the mode change).
+int ba_prepare(slk_ctx* ctx, const IterArgs& I, const int* ii_host, const int* jj_host, int M,
+               hipStream_t stream) {
     if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_iterate: null context");
-    const int M = num_edges;
-    if (M < 1 || t0 < 0 || t1 <= t0) return fail(SLK_E_ARG, "ba_iterate: need M >= 1, 0 <= t0 < t1");
-    if (!poses || !disps || !intrinsics || !target || !weight || !ii_gpu || !jj_gpu ||
-        !ii_host || !jj_host || (!motion_only && !eta))
+    if (M < 1 || I.t0 < 0 || I.t1 <= I.t0)
+        return fail(SLK_E_ARG, "ba_iterate: need M >= 1, 0 <= t0 < t1");
+    if (!I.poses || !I.disps || !I.intr || !I.target || !I.weight || !I.ii_gpu || !I.jj_gpu ||
+        !ii_host || !jj_host || (!I.motion_only && !I.eta))
         return fail(SLK_E_ARG, "ba_iterate: null argument");
     BaState* s = ctx->ba;
     const int HW = ctx->HW;
-    motion_only = motion_only ? 1 : 0;
+    const int t0 = I.t0, t1 = I.t1, motion_only = I.motion_only;
     const bool same = s->valid && s->key_t0 == t0 && s->key_t1 == t1 &&
                       s->key_motion == motion_only && s->key_HW == HW &&
                       (int)s->key_ii.size() == M &&
                       std::memcmp(s->key_ii.data(), ii_host, sizeof(int) * M) == 0 &&
                       std::memcmp(s->key_jj.data(), jj_host, sizeof(int) * M) == 0;
-    if (!same) {
-        s->valid = false;
-        SLK_TRY(build_plan(s, ii_host, jj_host, M, t0, t1, motion_only, HW));
-        if (s->n > 0x7fff) return fail(SLK_E_ARG, "ba_iterate: too many free poses");
-        const size_t pbytes = s->host.size() * sizeof(int);
-        SLK_TRY(s->stage.ensure(pbytes));
-        std::memcpy(s->stage.ptr, s->host.data(), pbytes);
-        SLK_TRY(s->plan_dev.ensure(pbytes));
-        SLK_HIP(hipMemcpyAsync(s->plan_dev.ptr, s->stage.ptr, pbytes, hipMemcpyHostToDevice,
-                               stream));
-        SLK_HIP(hipEventRecord(s->stage.done, stream));
-        s->stage.pending = true;
-        const size_t n = (size_t)s->n;
-        SLK_TRY(s->hpart.ensure((size_t)M * s->nch * kNJ * sizeof(double)));
+    if (same) return SLK_OK;
+    s->valid = false;
+    SLK_TRY(build_plan(s, ii_host, jj_host, M, t0, t1, motion_only, HW));
+    if (s->n > 0x7fff) return fail(SLK_E_ARG, "ba_iterate: too many free poses");
+    const size_t pbytes = s->host.size() * sizeof(int);
+    SLK_TRY(s->stage.ensure(pbytes));
+    std::memcpy(s->stage.ptr, s->host.data(), pbytes);
+    SLK_TRY(s->plan_dev.ensure(pbytes));
+    SLK_HIP(hipMemcpyAsync(s->plan_dev.ptr, s->stage.ptr, pbytes, hipMemcpyHostToDevice, stream));
+    SLK_HIP(hipEventRecord(s->stage.done, stream));
+    s->stage.pending = true;
+    const size_t n = (size_t)s->n;
+    SLK_TRY(s->hpart.ensure((size_t)M * s->nch * kNJ * sizeof(double)));
+    if (s->fz) {
+        SLK_TRY(s->spart.ensure((size_t)s->N_kf * s->nch * kFzMaxNT * 256 * sizeof(double)));
+        SLK_TRY(s->poses_prev.ensure((size_t)s->P * 7 * sizeof(float)));
+    } else {
         SLK_TRY(s->etot.ensure((size_t)M * kNT * sizeof(double)));
         SLK_TRY(s->stot.ensure(std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * 36) *
                                sizeof(double)));
-
         SLK_TRY(s->E.ensure(std::max<size_t>(1, (size_t)s->N_E * 6 * HW) * sizeof(double)));
         SLK_TRY(s->Q.ensure((size_t)s->N_kf * HW * sizeof(double)));
         SLK_TRY(s->Wv.ensure((size_t)s->N_kf * HW * sizeof(double)));
-        if (n > (size_t)kPanelN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
-        SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
-        SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
-        SLK_TRY(s->dx_dbg.ensure(n * sizeof(double)));
-        SLK_TRY(s->dx.ensure(n * sizeof(float)));
-        s->key_ii.assign(ii_host, ii_host + M);
-        s->key_jj.assign(jj_host, jj_host + M);
-        s->key_t0 = t0;
-        s->key_t1 = t1;
-        s->key_motion = motion_only;
-        s->key_HW = HW;
-        s->valid = true;
     }
-    const PlanDev plan = plan_ptrs(s);
-    {
-        ProfScope ps(ctx, "ba_lin_kf", stream);
-        hipLaunchKernelGGL(s->lin_by_wave ? k_ba_lin_wv : k_ba_lin_kf, dim3(s->nch, s->N_kf),
-                           dim3(kLinWG), 0, stream, plan, target, weight, poses, disps,
-                           intrinsics, ii_gpu, jj_gpu, eta, s->hpart.as<double>(),
-                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW,
-                           ctx->w, s->nch, motion_only);
-    }
-    SLK_HIP(hipGetLastError());
-    {
-        // the Schur items, then one workgroup per edge for its totals
-        const int items = motion_only ? 0 : s->N_pu + s->N_E;
-        ProfScope ps(ctx, "ba_schur", stream);
-        hipLaunchKernelGGL(k_ba_schur, dim3(items + M), dim3(kSchWG), 0, stream, plan,
-                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
-                           s->stot.as<double>(), HW, s->N_pu, items, poses, ii_gpu, jj_gpu,
-                           s->hpart.as<double>(), s->etot.as<double>(), s->nch);
-        SLK_HIP(hipGetLastError());
-    }
+    if (n > (size_t)kPanelN) SLK_TRY(s->S.ensure((n + 1) * n * sizeof(double)));
+    SLK_TRY(s->S_dbg.ensure(n * n * sizeof(double)));
+    SLK_TRY(s->b_dbg.ensure(n * sizeof(double)));
+    SLK_TRY(s->dx_dbg.ensure(n * sizeof(double)));
+    SLK_TRY(s->dx.ensure(n * sizeof(float)));
+    s->key_ii.assign(ii_host, ii_host + M);
+    s->key_jj.assign(jj_host, jj_host + M);
+    s->key_t0 = t0;
+    s->key_t1 = t1;
+    s->key_motion = motion_only;
+    s->key_HW = HW;
+    s->valid = true;
+    return SLK_OK;
+}
+
+SolveArgs solve_args(BaState* s, const PlanDev& plan, const IterArgs& I) {
     SolveArgs A;
     A.plan = plan;
     A.etot = s->etot.as<double>();
@@ -1603,44 +2206,182 @@ extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const fl
     A.P = s->P;
     A.n = s->n;
     A.n_blk = s->n_blk;
-    A.t0 = t0;
-    A.t1 = t1;
-    A.lm = lm;
-    A.ep = ep;
+    A.t0 = I.t0;
+    A.t1 = I.t1;
+    A.lm = I.lm;
+    A.ep = I.ep;
     A.S = s->S.as<double>();
     A.S_dbg = s->S_dbg.as<double>();
     A.b_dbg = s->b_dbg.as<double>();
     A.dx_dbg = s->dx_dbg.as<double>();
     A.dx = s->dx.as<float>();
     A.flags = s->flags.as<int>();
-    A.poses = poses;
+    A.poses = I.poses;
+    A.poses_prev = s->fz ? s->poses_prev.as<float>() : nullptr;
+    return A;
+}
+
+int launch_solve(slk_ctx* ctx, BaState* s, const SolveArgs& A, hipStream_t stream) {
+    ProfScope ps(ctx, "ba_solve", stream);
+    if (s->n <= kSmallN) {
+        hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(256), 0, stream, A);
+    } else if (s->n <= kPanelN) {
+        // t1 - t0 = P <= kPanelPoses
+        hipLaunchKernelGGL(k_ba_solve_panel, dim3(1), dim3(256), panel_solve_lds_bytes(s->n),
+                           stream, A);
+    } else {
+        SLK_TRY(solve_blocked(A, stream));
+    }
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+// The five-kernel iteration: linearization with the E rows in HBM, Schur
+// items and edge totals, assembly, solve, back-substitution.
+int iterate_classic(slk_ctx* ctx, BaState* s, const IterArgs& I, hipStream_t stream) {
+    const int HW = ctx->HW, M = s->M;
+    const PlanDev plan = plan_ptrs(s);
+    {
+        ProfScope ps(ctx, "ba_lin_kf", stream);
+        hipLaunchKernelGGL(s->lin_by_wave ? k_ba_lin_wv : k_ba_lin_kf, dim3(s->nch, s->N_kf),
+                           dim3(kLinWG), 0, stream, plan, I.target, I.weight, I.poses, I.disps,
+                           I.intr, I.ii_gpu, I.jj_gpu, I.eta, s->hpart.as<double>(),
+                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(), HW,
+                           ctx->w, s->nch, I.motion_only);
+    }
+    SLK_HIP(hipGetLastError());
+    {
+        // the Schur items, then one workgroup per edge for its totals
+        const int items = I.motion_only ? 0 : s->N_pu + s->N_E;
+        ProfScope ps(ctx, "ba_schur", stream);
+        hipLaunchKernelGGL(k_ba_schur, dim3(items + M), dim3(kSchWG), 0, stream, plan,
+                           s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
+                           s->stot.as<double>(), HW, s->N_pu, items, I.poses, I.ii_gpu,
+                           I.jj_gpu, s->hpart.as<double>(), s->etot.as<double>(), s->nch);
+        SLK_HIP(hipGetLastError());
+    }
+    const SolveArgs A = solve_args(s, plan, I);
     {
         ProfScope ps(ctx, "ba_assemble", stream);
         hipLaunchKernelGGL(k_ba_assemble, dim3(s->P * s->P + s->P), dim3(256), 0, stream, A);
     }
     SLK_HIP(hipGetLastError());
-    if (s->n <= kSmallN) {
-        ProfScope ps(ctx, "ba_solve", stream);
-        hipLaunchKernelGGL(k_ba_solve_small, dim3(1), dim3(256), 0, stream, A);
-    } else if (s->n <= kPanelN) {
-        // t1 - t0 = P <= kPanelPoses
-        ProfScope ps(ctx, "ba_solve", stream);
-        hipLaunchKernelGGL(k_ba_solve_panel, dim3(1), dim3(256), panel_solve_lds_bytes(s->n),
-                           stream, A);
-    } else {
-        ProfScope ps(ctx, "ba_solve", stream);
-        SLK_TRY(solve_blocked(A, stream));
-    }
-    SLK_HIP(hipGetLastError());
-    if (!motion_only && s->N_E > 0) {
+    SLK_TRY(launch_solve(ctx, s, A, stream));
+    if (!I.motion_only && s->N_E > 0) {
         ProfScope ps(ctx, "ba_backsub", stream);
         hipLaunchKernelGGL(k_ba_backsub, dim3((HW + 255) / 256, s->N_kf), dim3(256), 0, stream,
                            plan, s->E.as<double>(), s->Q.as<double>(), s->Wv.as<double>(),
-                           s->dx.as<float>(), s->flags.as<int>(), disps, HW);
+                           s->dx.as<float>(), s->flags.as<int>(), I.disps, HW);
         SLK_HIP(hipGetLastError());
+    }
+    return SLK_OK;
+}
+
+// `iters` fused iterations: k_ba_fz (the previous step's back-substitution
+// from the second iteration on, then the linearization and Schur partials),
+// k_ba_fz_assemble and the solve each; then the last back-substitution.
+int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStream_t stream) {
+    const PlanDev plan = plan_ptrs(s);
+    const int* base = s->plan_dev.as<int>();
+    FzArgs F;
+    F.kfs = reinterpret_cast<const FzKf*>(base + s->fz_off[0]);
+    F.eds = reinterpret_cast<const FzEdge*>(base + s->fz_off[1]);
+    F.target = I.target;
+    F.weight = I.weight;
+    F.poses = I.poses;
+    F.poses_prev = s->poses_prev.as<float>();
+    F.intr = I.intr;
+    F.eta = I.eta;
+    F.dx = s->dx.as<float>();
+    F.flags = s->flags.as<int>();
+    F.disps = I.disps;
+    F.hpart = s->hpart.as<double>();
+    F.spart = s->spart.as<double>();
+    F.HW = ctx->HW;
+    F.W = ctx->w;
+    F.nch = s->nch;
+    F.t0 = I.t0;
+    F.t1 = I.t1;
+    FzAsmArgs G;
+    G.items = reinterpret_cast<const int4*>(base + s->fz_off[2]);
+    G.dptr = base + s->fz_off[3];
+    G.dsrc = base + s->fz_off[4];
+    G.deptr = base + s->fz_off[5];
+    G.dedges = base + s->fz_off[6];
+    G.hpart = s->hpart.as<double>();
+    G.spart = s->spart.as<double>();
+    G.poses = I.poses;
+    G.ii = I.ii_gpu;
+    G.jj = I.jj_gpu;
+    G.nch = s->nch;
+    G.P = s->P;
+    G.n = s->n;
+    G.lm = I.lm;
+    G.ep = I.ep;
+    G.S = s->S_dbg.as<double>();
+    G.b = s->b_dbg.as<double>();
+    const SolveArgs A = solve_args(s, plan, I);
+    const dim3 grid(s->nch, s->N_kf);
+    for (int it = 0; it < iters; it++) {
+        {
+            ProfScope ps(ctx, "ba_fz_lin", stream);
+            if (it == 0)
+                hipLaunchKernelGGL((k_ba_fz<false, true>), grid, dim3(kLinWG), 0, stream, F);
+            else
+                hipLaunchKernelGGL((k_ba_fz<true, true>), grid, dim3(kLinWG), 0, stream, F);
+        }
+        SLK_HIP(hipGetLastError());
+        {
+            ProfScope ps(ctx, "ba_fz_asm", stream);
+            hipLaunchKernelGGL(k_ba_fz_assemble, dim3(s->P * s->P + s->P), dim3(256), 0, stream,
+                               G);
+        }
+        SLK_HIP(hipGetLastError());
+        SLK_TRY(launch_solve(ctx, s, A, stream));
+    }
+    {
+        ProfScope ps(ctx, "ba_fz_bs", stream);
+        hipLaunchKernelGGL((k_ba_fz<true, false>), grid, dim3(kLinWG), 0, stream, F);
+    }
+    SLK_HIP(hipGetLastError());
+    return SLK_OK;
+}
+
+int ba_run(slk_ctx* ctx, const IterArgs& I, const int* ii_host, const int* jj_host, int M,
+           int iters, hipStream_t stream) {
+    if (iters < 1) return fail(SLK_E_ARG, "ba_iterate_n: need iters >= 1");
+    SLK_TRY(ba_prepare(ctx, I, ii_host, jj_host, M, stream));
+    BaState* s = ctx->ba;
+    if (s->fz) {
+        SLK_TRY(iterate_fused(ctx, s, I, iters, stream));
+    } else {
+        for (int it = 0; it < iters; it++) SLK_TRY(iterate_classic(ctx, s, I, stream));
     }
     s->has_system = true;
     return SLK_OK;
+}
+
+}  // namespace
+
+extern "C" int slk_ba_iterate(slk_ctx* ctx, float* poses, float* disps, const float* intrinsics,
+                              const float* target, const float* weight, const float* eta,
+                              const int* ii_gpu, const int* jj_gpu, const int* ii_host,
+                              const int* jj_host, int num_edges, int t0, int t1, float lm,
+                              float ep, int motion_only, hipStream_t stream) {
+    const IterArgs I = {poses, disps, intrinsics, target, weight, eta, ii_gpu, jj_gpu,
+                        t0,    t1,    lm,         ep,     motion_only ? 1 : 0};
+    return ba_run(ctx, I, ii_host, jj_host, num_edges, 1, stream);
+}
+
+extern "C" int slk_ba_iterate_n(slk_ctx* ctx, float* poses, float* disps,
+                                const float* intrinsics, const float* target, const float* weight,
+                                const float* eta, const int* ii_gpu, const int* jj_gpu,
+                                const int* ii_host, const int* jj_host, int num_edges, int t0,
+                                int t1, float lm, float ep, int motion_only, int iters,
+                                hipStream_t stream) {
+    const IterArgs I = {poses, disps, intrinsics, target, weight, eta, ii_gpu, jj_gpu,
+                        t0,    t1,    lm,         ep,     motion_only ? 1 : 0};
+    return ba_run(ctx, I, ii_host, jj_host, num_edges, iters, stream);
 }
 
 extern "C" int slk_ba_status(slk_ctx* ctx, hipStream_t stream) {

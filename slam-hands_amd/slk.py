@@ -33,7 +33,7 @@ EXPORTS = [
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
     "slk_projmap", "slk_pose_retr", "slk_disp_retr", "slk_frame_distance", "slk_clamp_disps",
-    "slk_ba_iterate", "slk_ba_status", "slk_ba_last_system", "slk_ba_projective_transform",
+    "slk_ba_iterate", "slk_ba_iterate_n", "slk_ba_status", "slk_ba_last_system", "slk_ba_projective_transform",
     "slk_ba_accum", "slk_ba_damping_q", "slk_ba_eet6x6", "slk_ba_ev6x1", "slk_ba_evt6x1",
     "slk_ba_depth_update",
     "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
@@ -105,6 +105,7 @@ def lib():
             "slk_frame_distance": [P, P, P, P, P, P, I, I, I, F, P],
             "slk_clamp_disps": [P, I, F, P],
             "slk_ba_iterate": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, F, F, I, P],
+            "slk_ba_iterate_n": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, P],
             "slk_ba_status": [P, P],
             "slk_ba_last_system": [P, P, P, P, ctypes.POINTER(I), P],
             "slk_ba_projective_transform": [P] * 13 + [I, I, I, P],
@@ -407,6 +408,16 @@ class Context:
                                    _p(weight), _p(eta), _p(ii_dev), _p(jj_dev), ii_p, jj_p,
                                    len(ii_h), t0, t1, float(lm), float(ep), int(bool(motion_only)),
                                    stream))
+
+    def ba_iterate_n(self, poses, disps, intr, target, weight, eta, ii_dev, jj_dev, ii, jj, t0,
+                     t1, lm, ep, iters, motion_only=False, stream=None):
+        """`iters` BA iterations on one edge set (slk_ba_iterate_n)."""
+        ii_h, ii_p = _host_i32(ii)
+        jj_h, jj_p = _host_i32(jj)
+        check(lib().slk_ba_iterate_n(self.ptr, _p(poses), _p(disps), _p(intr), _p(target),
+                                     _p(weight), _p(eta), _p(ii_dev), _p(jj_dev), ii_p, jj_p,
+                                     len(ii_h), t0, t1, float(lm), float(ep),
+                                     int(bool(motion_only)), int(iters), stream))
 
     def profile_enable(self, on=True):
         check(lib().slk_profile_enable(self.ptr, int(bool(on))))

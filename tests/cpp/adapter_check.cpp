@@ -130,8 +130,9 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
         ba.iterate(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M, t0,
                    t1, lm, ep, motion_only != 0);
     if (launches) {
-        // launches of the linearization and of the solve over all iterates
-        launches[0] = ba.profiled_launches("ba_lin_kf");
+        // launches of the linearization (five-kernel or fused iteration) and
+        // of the solve over all iterates
+        launches[0] = ba.profiled_launches("ba_lin_kf") + ba.profiled_launches("ba_fz_lin");
         launches[1] = ba.profiled_launches("ba_solve");
         ba.print_profile();
     }

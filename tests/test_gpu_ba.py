@@ -97,6 +97,81 @@ def test_three_iterations_chained(slk):
     ctx.close()
 
 
+def _path_kernels(ctx):
+    return set(ctx.profile())
+
+
+def _dense_keyframe_problem():
+    """Keyframe 0 with edges to 9 free poses (10 E rows): more than the fused
+    path's 7 per keyframe, so the window takes the five-kernel iteration."""
+    n = 11
+    ii = [0] * 9 + [k for k in range(1, n - 1)]
+    jj = [k for k in range(2, n)] + [k + 1 for k in range(1, n - 1)]
+    ii, jj = np.asarray(ii, np.int32), np.asarray(jj, np.int32)
+    return wl.ba_problem(n=n, h=12, w=16, ii=ii, jj=jj, seed=17, fixed=2)
+
+
+@pytest.mark.parametrize("case", ["window", "dense_keyframe"])
+def test_iterate_n_matches_oracle_and_single_calls(slk, case):
+    """slk_ba_iterate_n(3) against three chained oracle iterations and against
+    three slk_ba_iterate calls: the cfg3 window runs the fused iteration (E
+    rows and Schur products kept on chip, back-substitution folded into the
+    next linearization), the dense keyframe the five-kernel one."""
+    announce(f"ba iterate_n(3) {case}")
+    p = wl.ba_problem() if case == "window" else _dense_keyframe_problem()
+    h, w = p["h"], p["w"]
+    ref_p, ref_d = p["poses"], p["disps"]
+    for _ in range(3):
+        ref = oracle_iter(p, ref_p, ref_d, 1e-4, 0.1)
+        assert ref["status"] == 0
+        ref_p, ref_d = ref["poses"], ref["disps"]
+    a, b = Dev(slk, p), Dev(slk, p)
+    ctx_a = slk.Context(h, w, max_batch=1)
+    ctx_b = slk.Context(h, w, max_batch=1)
+    ctx_a.profile_enable(True)
+    d = a.d
+    ctx_a.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                       d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 3)
+    assert ctx_a.ba_status() == slk.SLK_OK
+    kernels = _path_kernels(ctx_a)
+    if case == "window":
+        assert {"ba_fz_lin", "ba_fz_asm", "ba_fz_bs"} <= kernels, kernels
+    else:
+        assert {"ba_lin_kf", "ba_schur", "ba_backsub"} <= kernels, kernels
+    for _ in range(3):
+        b.iterate(ctx_b, 1e-4, 0.1)
+    assert ctx_b.ba_status() == slk.SLK_OK
+    assert norm_rel(a.poses(), ref_p) < TOL
+    assert norm_rel(a.disps(), ref_d) < TOL
+    assert_close_rel(a.poses(), ref_p, what="poses after iterate_n(3)")
+    assert_close_rel(a.disps(), ref_d, what="disps after iterate_n(3)")
+    assert norm_rel(a.poses() - p["poses"], ref_p - p["poses"]) < TOL
+    # the same steps either way, up to fp64 summation order
+    assert norm_rel(a.poses(), b.poses()) < 1e-6
+    assert norm_rel(a.disps(), b.disps()) < 1e-6
+    ctx_a.close()
+    ctx_b.close()
+
+
+def test_iterate_n_not_spd_leaves_state_untouched(slk):
+    """A rejected step in the fused iteration: no retraction, and the
+    back-substitution folded into the next launch is skipped as well."""
+    p = wl.ba_problem(n=4, h=6, w=8, seed=2)
+    p["weight"] = np.zeros_like(p["weight"])
+    dev = Dev(slk, p)
+    ctx = slk.Context(6, 8, C=128, max_batch=1, levels=2)
+    d = dev.d
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 0.0, 0.0, 2)
+    assert ctx.ba_status() == slk.SLK_E_NOT_SPD
+    np.testing.assert_array_equal(dev.poses(), p["poses"])
+    np.testing.assert_array_equal(dev.disps(), p["disps"])
+    with pytest.raises(slk.SlkError):
+        ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                         d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 0)
+    ctx.close()
+
+
 @pytest.mark.parametrize("duplicate", [True, False])
 def test_edge_cases_stereo_duplicates_absent_frame(slk, duplicate):
     # with the duplicate (2, 3) edge the linearization runs edge by edge per

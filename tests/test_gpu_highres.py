@@ -113,6 +113,17 @@ def test_highres_ba_three_iterations(slk):
     assert_close_rel(d["poses"].to_host(), poses, what="highres poses after 3")
     assert norm_rel(d["poses"].to_host() - p["poses"], poses - p["poses"]) < TOL
     ctx.close()
+    # the same three iterations as one slk_ba_iterate_n call (fused iteration)
+    d = {k: D(p[k]) for k in ("poses", "disps", "intr", "target", "weight", "eta", "ii", "jj")}
+    ctx = slk.Context(54, 96, max_batch=1)
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 3)
+    assert ctx.ba_status() == slk.SLK_OK
+    assert norm_rel(d["poses"].to_host(), poses) < TOL
+    assert norm_rel(d["disps"].to_host(), disps) < TOL
+    assert_close_rel(d["poses"].to_host(), poses, what="highres poses after iterate_n(3)")
+    assert_close_rel(d["disps"].to_host(), disps, what="highres disps after iterate_n(3)")
+    ctx.close()
 
 
 def test_backend_correlation_sampled(slk):
