@@ -1420,6 +1420,44 @@ __device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int j
 
 typedef double fz_d4 __attribute__((ext_vector_type(4)));
 
+// Z = [E; w] Q [E; w]^T over this wave's 64 pixels of xs ([pixel][row]),
+// for the T (T + 1) / 2 upper 16 x 16 tiles: operand A = rows 16 ti + (l %
+// 16) of pixel l / 16 of a 4-pixel step, B = Q times rows 16 tj + (l % 16);
+// then the wave's tiles go to xs as [wave][tile][256] (lane * 4 + r), which
+// overwrites the rows: a barrier separates every wave's reads from the first
+// write.
+template <int T>
+__device__ __forceinline__ void fz_schur_tiles(double* xs, const double* qs, int wave, int lane) {
+    constexpr int NT = T * (T + 1) / 2;
+    fz_d4 z[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) z[t] = fz_d4{0.0, 0.0, 0.0, 0.0};
+    const int i16 = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 16; ks++) {
+        const int kp = wave * 64 + ks * 4 + kg;
+        const double q = qs[kp];
+        const double* xr = xs + kp * kFzLd + i16;
+        double a[T], b[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            a[t] = xr[16 * t];
+            b[t] = a[t] * q;
+        }
+        int tt = 0;
+#pragma unroll
+        for (int tj = 0; tj < T; tj++)
+#pragma unroll
+            for (int ti = 0; ti <= tj; ti++, tt++)
+                z[tt] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ti], b[tj], z[tt], 0, 0, 0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) xs[(wave * kFzMaxNT + t) * 256 + lane * 4 + r] = z[t][r];
+}
+
 template <bool kBs, bool kLin>
 __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
     __shared__ double xs[kLinPx * kFzLd];        // [pixel][row]; then the MFMA partials
@@ -1633,7 +1671,20 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
         cw[0][wave][px] = cp[s];
         cw[1][wave][px] = wp[s];
     }
-    if (ri) {  // uniform: the keyframe's own row (slot 0), the waves' parts added in order
+    // the keyframe's own row (slot 0): the waves' parts added in wave order,
+    // from per-wave copies in the columns past the tiles when two tiles hold
+    // the rows, else one wave after another
+    constexpr int kErCol = 32;
+    static_assert(kErCol + 6 * kLinWaves <= kFzLd, "four 6-row copies fit past two tiles");
+    const bool er_cols = T <= 2;  // uniform
+    if (ri && er_cols) {
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            double* xr = xs + (s * 64 + lane) * kFzLd + kErCol + 6 * wave;
+#pragma unroll
+            for (int n = 0; n < 6; n++) xr[n] = er[s][n];
+        }
+    } else if (ri) {
         for (int v = 0; v < kLinWaves; v++) {
             __syncthreads();
             if (wave == v) {
@@ -1651,6 +1702,7 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
     {
         const int k = chunk * kLinPx + tid;
         double q = 0.0;
+        double* xr = xs + tid * kFzLd;
         if (k < HW) {
             double c = 0.0, w = 0.0;
 #pragma unroll
@@ -1660,44 +1712,29 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
             }
             // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
             q = 1.0 / (c + 0.2 * (double)F.eta[(size_t)K.kf * HW + k] + 1e-7);
-            xs[tid * kFzLd + 6 * nslot] = w;
+            xr[6 * nslot] = w;
+            if (ri && er_cols) {
+#pragma unroll
+                for (int n = 0; n < 6; n++) {
+                    double t = xr[kErCol + n];
+#pragma unroll
+                    for (int v = 1; v < kLinWaves; v++) t += xr[kErCol + 6 * v + n];
+                    xr[n] = t;
+                }
+            }
         }
         qs[tid] = q;
     }
     __syncthreads();
-    // Z over this wave's 64 pixels: A = rows 16 ti.. of 4 pixels, B = Q * rows 16 tj..
-    // (lane l holds row l % 16 of pixel l / 16 in both operands)
-    fz_d4 z[kFzMaxNT];
-#pragma unroll
-    for (int t = 0; t < kFzMaxNT; t++) z[t] = fz_d4{0.0, 0.0, 0.0, 0.0};
-    const int i16 = lane & 15, kg = lane >> 4;
-#pragma unroll
-    for (int ks = 0; ks < 16; ks++) {
-        const int kp = wave * 64 + ks * 4 + kg;
-        const double q = qs[kp];
-        const double* xr = xs + kp * kFzLd + i16;
-        double a[kFzMaxT], b[kFzMaxT];
-#pragma unroll
-        for (int t = 0; t < kFzMaxT; t++) {
-            a[t] = t < T ? xr[16 * t] : 0.0;
-            b[t] = a[t] * q;
-        }
-        int tt = 0;
-#pragma unroll
-        for (int tj = 0; tj < kFzMaxT; tj++)
-#pragma unroll
-            for (int ti = 0; ti <= tj; ti++, tt++)
-                if (tj < T) z[tt] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[ti], b[tj], z[tt], 0, 0, 0);
-    }
+    if (T == 1)
+        fz_schur_tiles<1>(xs, qs, wave, lane);
+    else if (T == 2)
+        fz_schur_tiles<2>(xs, qs, wave, lane);
+    else
+        fz_schur_tiles<3>(xs, qs, wave, lane);
     __syncthreads();
-    double* red = xs;  // [wave][tile][256]: lane * 4 + r
     const int nt = T * (T + 1) / 2;
-#pragma unroll
-    for (int t = 0; t < kFzMaxNT; t++)
-        if (t < nt)
-#pragma unroll
-            for (int r = 0; r < 4; r++) red[(wave * kFzMaxNT + t) * 256 + lane * 4 + r] = z[t][r];
-    __syncthreads();
+    const double* red = xs;
     double* sp = F.spart + (size_t)(kc * F.nch + chunk) * kFzMaxNT * 256;
     for (int idx = tid; idx < nt * 256; idx += kLinWG) {
         double v = red[idx];
