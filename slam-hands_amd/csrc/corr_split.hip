@@ -101,6 +101,10 @@ __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
 // same stream. These workgroups run in the launch of k_feat_prep, beside the
 // feature preparation they do not depend on.
 constexpr int kMaskThreads = 256;
+// the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
+// which a tile-mask workgroup uses for its bitmap and sorted pixel indices
+constexpr int kPrepRows = 8, kPrepCols = 64;
+constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
 constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
 constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
@@ -169,17 +173,24 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // order (whose +-8 px flows spread them over ~26 rows). A window cell is the
 // same dot product whichever tile computes it, so the order changes which
 // products are skipped, not any output. Counting sort in the workgroup:
-// every wave takes a contiguous quarter of the pixels, 64 at a time; the
-// lanes of a chunk holding equal keys find each other by one ballot per key
-// bit, the lowest of them adds their count to the wave's histogram, then
-// bucket-major offsets, then the same pass again scatters each pixel to its
-// bucket's next slot plus its rank among the equal lanes below it, and
-// marks the target tiles of its windows in the row of its source tile.
-// Writes ord[0][q] = the pixel at sorted position q and ord[1][q], ord[2][q]
-// = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with more rows
-// than that is not sorted: returns false, and neither ord nor the bitmap is
-// written.
+// every wave takes a contiguous quarter of the pixels, 64 at a time, and
+// counts their keys in its own LDS histogram (atomic adds: the counts do not
+// depend on their order); then bucket-major offsets; then the same chunks
+// again in pixel order, the lanes of a chunk holding equal keys finding each
+// other by one ballot per key bit: each lane takes its bucket's next slot
+// plus its rank among the equal lanes below it, and the lowest of them
+// advances the slot. When the edge's pixels fit in LDS beside the tile
+// bitmap (`stage`, HW ints), the scatter writes only the pixel index there;
+// a last pass over the sorted positions (64 consecutive ones per wave and
+// round, so within one source tile) then writes ord and the coordinates
+// coalesced and marks each wave's target tiles with one merge. Otherwise the
+// scatter writes ord and the coordinates directly and every lane marks its
+// own tiles. Writes ord[0][q] = the pixel at sorted position q and ord[1][q],
+// ord[2][q] = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with
+// more rows than that is not sorted: returns false, and neither ord nor the
+// bitmap is written.
 constexpr int kSortBuckets = 256;
+constexpr bool kStageSorted = false;
 
 // the lanes of the wave whose key equals this lane's, among `live`
 __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
@@ -193,8 +204,29 @@ __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
     return m;
 }
 
+// The target tiles of the windows of one wave's 64 sources, all in the
+// source tile whose first tile id is `row`, into the bitmap: ORed over the
+// wave by shuffles and merged by lane 0 when the tiles fit a 64-bit mask,
+// else marked by every lane.
+__device__ __forceinline__ void mark_wave(const Geom& g, bool in, int fx, int fy, int row,
+                                          int ntiles, unsigned* bits) {
+    const int lane = threadIdx.x & 63;
+    if (ntiles > 64) {
+        if (in) mark_source(g, fx, fy, row, ntiles, bits);
+        return;
+    }
+    const unsigned long long m = in ? window_tiles(g, fx, fy) : 0ull;
+    unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        m0 |= __shfl_xor(m0, off, 64);
+        m1 |= __shfl_xor(m1, off, 64);
+    }
+    if (lane == 0) merge_tiles(bits, row, ((unsigned long long)m1 << 32) | m0);
+}
+
 __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
-                              unsigned* bits, int ntiles) {
+                              unsigned* bits, int ntiles, int* stage) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int HW = g.HW, nb = g.h[0] + 9;
     if (nb > kSortBuckets) return false;
@@ -224,18 +256,17 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
         }
     };
     const bool one = q1 - q0 <= 64 * kG;
-    // a wave's histogram: the lowest lane of each key of a chunk adds the
-    // key's count (distinct keys, distinct words)
+    // with the quarter in registers and at most 64 target tiles, each
+    // source's tile mask is formed here, while the loads of the histogram
+    // pass are what the waves wait for, and only merged in the scatter
+    const bool pre = one && ntiles <= 64 && !stage;
+    unsigned long long mk[kG];
     for (int pg = q0; pg < q1; pg += 64 * kG) {
         load(pg);
 #pragma unroll
         for (int u = 0; u < kG; u++) {
-            const int pb = pg + 64 * u;
-            if (pb >= q1) break;  // uniform
-            const bool act = pb + lane < q1;
-            const int key = act ? key_of(yv[u]) : 0;
-            const unsigned long long m = equal_keys(key, nbits, __ballot(act));
-            if (act && !(m & below)) hist[wv * kSortBuckets + key] += __builtin_popcountll(m);
+            if (pg + 64 * u + lane < q1) atomicAdd(&hist[wv * kSortBuckets + key_of(yv[u])], 1);
+            mk[u] = pre ? window_tiles(g, floor_clamped(xv[u]), floor_clamped(yv[u])) : 0ull;
         }
     }
     __syncthreads();
@@ -281,12 +312,54 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
             const int rank = __builtin_popcountll(m & below);
             if (act) {
                 const int q = base + rank;
-                ord[q] = p;
-                oxy[q] = xv[u];
-                oxy[HW + q] = yv[u];
                 if (rank == 0) pos[wv * kSortBuckets + key] = base + __builtin_popcountll(m);
-                mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
-                            q / kSrcTile * ntiles, ntiles, bits);
+                if (stage) {
+                    stage[q] = p;
+                } else {
+                    ord[q] = p;
+                    oxy[q] = xv[u];
+                    oxy[HW + q] = yv[u];
+                    if (pre) {
+                        if (mk[u]) merge_tiles(bits, q / kSrcTile * ntiles, mk[u]);
+                    } else {
+                        mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
+                                    q / kSrcTile * ntiles, ntiles, bits);
+                    }
+                }
+            }
+        }
+    }
+    if (stage) {
+        __syncthreads();
+        // sorted positions q = 256 r + tid (a wave's 64 lie in one source
+        // tile), kR rounds at a time: their pixels, then their coordinates,
+        // are loaded together before any is used
+        constexpr int kR = 12;
+        for (int qg = 0; qg < HW; qg += kR * kMaskThreads) {
+            int pr[kR];
+            float xr[kR], yr[kR];
+#pragma unroll
+            for (int r = 0; r < kR; r++) {
+                const int q = qg + r * kMaskThreads + tid;
+                pr[r] = q < HW ? stage[q] : 0;
+            }
+#pragma unroll
+            for (int r = 0; r < kR; r++) {
+                xr[r] = cc[pr[r]];
+                yr[r] = cc[HW + pr[r]];
+            }
+#pragma unroll
+            for (int r = 0; r < kR; r++) {
+                const int q = qg + r * kMaskThreads + tid;
+                if (q - lane >= HW) break;  // uniform: the wave's first position is past HW
+                const bool in = q < HW;
+                if (in) {
+                    ord[q] = pr[r];
+                    oxy[q] = xr[r];
+                    oxy[HW + q] = yr[r];
+                }
+                mark_wave(g, in, floor_clamped(xr[r]), floor_clamped(yr[r]),
+                          (q - lane) / kSrcTile * ntiles, ntiles, bits);
             }
         }
     }
@@ -306,7 +379,9 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     const float* cc = coords + (size_t)e * 2 * g.HW;
     int* ord = a.order + (size_t)e * 3 * g.HW;
-    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles)) {  // uniform
+    // the sorted pixel indices go to LDS after the bitmap when they fit
+    int* stage = kStageSorted && nw + g.HW <= kPrepLdsWords ? reinterpret_cast<int*>(bits) + nw : nullptr;
+    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles, stage)) {  // uniform
         // pixel order: the order is the identity, written beside the mask.
         // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
         // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
@@ -389,8 +464,6 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
 // bitmap is the level-0 LDS array; they are the longer chains, so they are
 // dispatched first), then the blocks x C/16 x slots preparation workgroups
 // (block fastest).
-constexpr int kPrepRows = 8, kPrepCols = 64;
-constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;  // level 0 / tile bitmap
 static_assert(kMaskThreads == 256, "the tile-mask workgroups share k_feat_prep's size");
 template <typename Tin>
 __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
@@ -404,6 +477,9 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
     __shared__ int wave_sum[kMaskThreads / 64];
     if ((int)blockIdx.x < nmask) {  // uniform
+        // the tile-mask chains are the launch's long pole: their waves issue
+        // ahead of the preparation waves sharing their SIMDs
+        __builtin_amdgcn_s_setprio(2);
         tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum,
                        reinterpret_cast<int*>(&l1[0][0][0]));
         return;
