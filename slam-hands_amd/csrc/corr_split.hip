@@ -178,19 +178,14 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // depend on their order); then bucket-major offsets; then the same chunks
 // again in pixel order, the lanes of a chunk holding equal keys finding each
 // other by one ballot per key bit: each lane takes its bucket's next slot
-// plus its rank among the equal lanes below it, and the lowest of them
-// advances the slot. When the edge's pixels fit in LDS beside the tile
-// bitmap (`stage`, HW ints), the scatter writes only the pixel index there;
-// a last pass over the sorted positions (64 consecutive ones per wave and
-// round, so within one source tile) then writes ord and the coordinates
-// coalesced and marks each wave's target tiles with one merge. Otherwise the
-// scatter writes ord and the coordinates directly and every lane marks its
-// own tiles. Writes ord[0][q] = the pixel at sorted position q and ord[1][q],
-// ord[2][q] = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with
+// plus its rank among the equal lanes below it (the lowest of them advances
+// the slot), writes its pixel and coordinates there, and marks the target
+// tiles of its windows in the row of its source tile (masks formed in the
+// histogram pass when the quarter stays in registers). Writes ord[0][q] =
+// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with
 // more rows than that is not sorted: returns false, and neither ord nor the
 // bitmap is written.
 constexpr int kSortBuckets = 256;
-constexpr bool kStageSorted = false;
 
 // the lanes of the wave whose key equals this lane's, among `live`
 __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
@@ -204,29 +199,8 @@ __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
     return m;
 }
 
-// The target tiles of the windows of one wave's 64 sources, all in the
-// source tile whose first tile id is `row`, into the bitmap: ORed over the
-// wave by shuffles and merged by lane 0 when the tiles fit a 64-bit mask,
-// else marked by every lane.
-__device__ __forceinline__ void mark_wave(const Geom& g, bool in, int fx, int fy, int row,
-                                          int ntiles, unsigned* bits) {
-    const int lane = threadIdx.x & 63;
-    if (ntiles > 64) {
-        if (in) mark_source(g, fx, fy, row, ntiles, bits);
-        return;
-    }
-    const unsigned long long m = in ? window_tiles(g, fx, fy) : 0ull;
-    unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        m0 |= __shfl_xor(m0, off, 64);
-        m1 |= __shfl_xor(m1, off, 64);
-    }
-    if (lane == 0) merge_tiles(bits, row, ((unsigned long long)m1 << 32) | m0);
-}
-
 __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
-                              unsigned* bits, int ntiles, int* stage) {
+                              unsigned* bits, int ntiles) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int HW = g.HW, nb = g.h[0] + 9;
     if (nb > kSortBuckets) return false;
@@ -259,7 +233,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
     // with the quarter in registers and at most 64 target tiles, each
     // source's tile mask is formed here, while the loads of the histogram
     // pass are what the waves wait for, and only merged in the scatter
-    const bool pre = one && ntiles <= 64 && !stage;
+    const bool pre = one && ntiles <= 64;
     unsigned long long mk[kG];
     for (int pg = q0; pg < q1; pg += 64 * kG) {
         load(pg);
@@ -313,53 +287,15 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
             if (act) {
                 const int q = base + rank;
                 if (rank == 0) pos[wv * kSortBuckets + key] = base + __builtin_popcountll(m);
-                if (stage) {
-                    stage[q] = p;
+                ord[q] = p;
+                oxy[q] = xv[u];
+                oxy[HW + q] = yv[u];
+                if (pre) {
+                    if (mk[u]) merge_tiles(bits, q / kSrcTile * ntiles, mk[u]);
                 } else {
-                    ord[q] = p;
-                    oxy[q] = xv[u];
-                    oxy[HW + q] = yv[u];
-                    if (pre) {
-                        if (mk[u]) merge_tiles(bits, q / kSrcTile * ntiles, mk[u]);
-                    } else {
-                        mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
-                                    q / kSrcTile * ntiles, ntiles, bits);
-                    }
+                    mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
+                                q / kSrcTile * ntiles, ntiles, bits);
                 }
-            }
-        }
-    }
-    if (stage) {
-        __syncthreads();
-        // sorted positions q = 256 r + tid (a wave's 64 lie in one source
-        // tile), kR rounds at a time: their pixels, then their coordinates,
-        // are loaded together before any is used
-        constexpr int kR = 12;
-        for (int qg = 0; qg < HW; qg += kR * kMaskThreads) {
-            int pr[kR];
-            float xr[kR], yr[kR];
-#pragma unroll
-            for (int r = 0; r < kR; r++) {
-                const int q = qg + r * kMaskThreads + tid;
-                pr[r] = q < HW ? stage[q] : 0;
-            }
-#pragma unroll
-            for (int r = 0; r < kR; r++) {
-                xr[r] = cc[pr[r]];
-                yr[r] = cc[HW + pr[r]];
-            }
-#pragma unroll
-            for (int r = 0; r < kR; r++) {
-                const int q = qg + r * kMaskThreads + tid;
-                if (q - lane >= HW) break;  // uniform: the wave's first position is past HW
-                const bool in = q < HW;
-                if (in) {
-                    ord[q] = pr[r];
-                    oxy[q] = xr[r];
-                    oxy[HW + q] = yr[r];
-                }
-                mark_wave(g, in, floor_clamped(xr[r]), floor_clamped(yr[r]),
-                          (q - lane) / kSrcTile * ntiles, ntiles, bits);
             }
         }
     }
@@ -379,9 +315,7 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     const float* cc = coords + (size_t)e * 2 * g.HW;
     int* ord = a.order + (size_t)e * 3 * g.HW;
-    // the sorted pixel indices go to LDS after the bitmap when they fit
-    int* stage = kStageSorted && nw + g.HW <= kPrepLdsWords ? reinterpret_cast<int*>(bits) + nw : nullptr;
-    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles, stage)) {  // uniform
+    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles)) {  // uniform
         // pixel order: the order is the identity, written beside the mask.
         // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
         // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
