@@ -11,7 +11,9 @@
 //                     DroidState.
 //   CorrBlock         init / build / sample_single / destroy of the
 //                     standalone correlation block (corr.cuh:61-263).
-//   BundleAdjustment  init / iterate / print_profile / destroy (ba.cuh:397-819).
+//   BundleAdjustment  init / iterate / print_profile / destroy (ba.cuh:397-819),
+//                     and iterate_n for the caller's loop of iterates
+//                     (main.cu:2371-2389).
 //   projmap, pose_retr, frame_distance, clamp_disps
 //                     the SE3 kernel launches with the reference's argument
 //                     lists (se3.cuh:118-277, main.cu:2392-2397).
@@ -361,6 +363,27 @@ class BundleAdjustment {
                                  "poses and disps left unchanged\n");
         else
             check(st, "BundleAdjustment::iterate");
+    }
+
+    // The caller's loop of `iters` iterate() calls on one edge set
+    // (run_update_pass, main.cu:2371-2389) as one call: the steps run back to
+    // back on the stream, fused where the edge set allows, and the call
+    // returns with poses and disps final. A step whose system is not positive
+    // definite changes neither poses nor disps, as in iterate().
+    void iterate_n(float* poses, float* disps, float* intrinsics, float* target, float* weight,
+                   float* eta, int* ii_gpu, int* jj_gpu, int* ii_host, int* jj_host,
+                   int num_edges, int t0, int t1, float lm, float ep, bool motion_only,
+                   int iters) {
+        check(slk_ba_iterate_n(ctx_, poses, disps, intrinsics, target, weight, eta, ii_gpu,
+                               jj_gpu, ii_host, jj_host, num_edges, t0, t1, lm, ep,
+                               motion_only ? 1 : 0, iters, nullptr),
+              "BundleAdjustment::iterate_n");
+        const int st = slk_ba_status(ctx_, nullptr);
+        if (st == SLK_E_NOT_SPD)
+            std::fprintf(stderr, "BundleAdjustment::iterate_n: system not positive definite; "
+                                 "rejected steps left poses and disps unchanged\n");
+        else
+            check(st, "BundleAdjustment::iterate_n");
     }
 
     // Totals per kernel over the iterates since enable_profile(true)

@@ -104,14 +104,14 @@ extern "C" int adapter_corrblock(const float* fmap1, const float* fmap2, int bn,
 }
 
 // `iters` BundleAdjustment::iterate calls followed by clamp_disps(0.001), as
-// run_update_pass does (main.cu:2371-2397). poses [N][7] and disps [N][h*w]
-// are updated in place. With launches != NULL the iterates run profiled and
-// launches[0..1] receive the total launch counts of the linearization and
-// solve kernels.
+// run_update_pass does (main.cu:2371-2397), or with one_call != 0 the same
+// loop as one iterate_n call. poses [N][7] and disps [N][h*w] are updated in
+// place. With launches != NULL the iterates run profiled and launches[0..1]
+// receive the total launch counts of the linearization and solve kernels.
 extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const float* intr,
                           const float* target, const float* weight, const float* eta,
                           const int* ii, const int* jj, int M, int t0, int t1, float lm,
-                          float ep, int motion_only, int iters, int* launches) {
+                          float ep, int motion_only, int iters, int one_call, int* launches) {
     const size_t hw = (size_t)h * w;
     float* d_p = upload(poses, (size_t)N * 7);
     float* d_d = upload(disps, (size_t)N * hw);
@@ -126,9 +126,13 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
     slk_droid::BundleAdjustment ba;
     ba.init(h, w);
     if (launches) ba.enable_profile(true);
-    for (int k = 0; k < iters; k++)
-        ba.iterate(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M, t0,
-                   t1, lm, ep, motion_only != 0);
+    if (one_call)
+        ba.iterate_n(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M, t0,
+                     t1, lm, ep, motion_only != 0, iters);
+    else
+        for (int k = 0; k < iters; k++)
+            ba.iterate(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M,
+                       t0, t1, lm, ep, motion_only != 0);
     if (launches) {
         // launches of the linearization (five-kernel or fused iteration) and
         // of the solve over all iterates

@@ -30,7 +30,7 @@ def harness():
     P = ctypes.c_void_p
     I, F = ctypes.c_int, ctypes.c_float
     lib.adapter_corr.argtypes = [P, I, I, I, I, P, P, I, P, P, P]
-    lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, P]
+    lib.adapter_ba.argtypes = [I, I, I, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, I, P]
     lib.adapter_corrblock.argtypes = [P, P, I, I, I, I, P, P, P, P, I, I, P, P]
     lib.adapter_update.argtypes = [ctypes.c_char_p, I, I, I, I] + [P] * 11
     lib.adapter_glue.argtypes = [I, I, I, I, I, I] + [P] * 12 + [I] + [P] * 4 + [P] * 14
@@ -91,16 +91,20 @@ def test_corr_block(harness):
     assert_close_rel(out2, ref2, what="CorrBlock after resize")
 
 
+@pytest.mark.parametrize("one_call", [0, 1])
 @pytest.mark.parametrize("motion_only", [0, 1])
-def test_bundle_adjustment_iterate(harness, motion_only):
-    announce(f"adapters: BundleAdjustment motion_only={motion_only}")
+def test_bundle_adjustment_iterate(harness, motion_only, one_call):
+    """Two iterate() calls, or one iterate_n(2) (the fused iteration unless
+    motion_only), then clamp_disps."""
+    announce(f"adapters: BundleAdjustment motion_only={motion_only} one_call={one_call}")
     p = wl.ba_problem(n=6, h=12, w=16, seed=52)
     poses, disps = p["poses"].copy(), p["disps"].copy()
     ii, jj = p["ii"].astype(np.int32), p["jj"].astype(np.int32)
     launches = np.zeros(2, np.int32)
     st = harness.adapter_ba(len(poses), p["h"], p["w"], _p(poses), _p(disps), _p(p["intr"]),
                             _p(p["target"]), _p(p["weight"]), _p(p["eta"]), _p(ii), _p(jj),
-                            len(ii), p["t0"], p["t1"], 1e-4, 0.1, motion_only, 2, _p(launches))
+                            len(ii), p["t0"], p["t1"], 1e-4, 0.1, motion_only, 2, one_call,
+                            _p(launches))
     assert st == 0
     # print_profile's totals cover both iterates: one launch per kernel each
     np.testing.assert_array_equal(launches, [2, 2])
