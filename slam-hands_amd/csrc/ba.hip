@@ -517,6 +517,7 @@ struct SolveArgs {
     int* flags;     // [0] this iteration not SPD, [1] sticky
     float* poses;
     float* poses_prev;  // [P][7] poses t0..t1-1 before the step (fused path), or null
+    float* poses_next;  // [P][7] poses t0..t1-1 after the step (overlapped fused path), or null
 };
 
 // One edge-block or Schur-item contribution to entry (r, c) of a 6x6 block of
@@ -611,7 +612,12 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
         A.dx_dbg[t] = ok ? x[t] : 0.0;
         A.dx[t] = ok ? (float)x[t] : 0.0f;
     }
-    if (!ok) return;
+    if (!ok) {  // the poses stay; the overlapped path still needs their copy
+        if (A.poses_next)
+            for (int t = threadIdx.x; t < (A.t1 - A.t0) * 7; t += blockDim.x)
+                A.poses_next[t] = pose_src[t];
+        return;
+    }
     // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
     for (int k = A.t0 + threadIdx.x; k < A.t1; k += blockDim.x) {
         double t[3], q[4], xi[6], t1[3], q1[4];
@@ -620,8 +626,12 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
         load_pose(pose_src, k - A.t0, t, q);
         for (int m = 0; m < 6; m++) xi[m] = (double)(float)x[(k - A.t0) * 6 + m];
         retr_se3(xi, t, q, t1, q1);
-        for (int m = 0; m < 3; m++) A.poses[k * 7 + m] = (float)t1[m];
-        for (int m = 0; m < 4; m++) A.poses[k * 7 + 3 + m] = (float)q1[m];
+        float pn[7];
+        for (int m = 0; m < 3; m++) pn[m] = (float)t1[m];
+        for (int m = 0; m < 4; m++) pn[3 + m] = (float)q1[m];
+        for (int m = 0; m < 7; m++) A.poses[k * 7 + m] = pn[m];
+        if (A.poses_next)  // read by the next overlapped step's relinearization
+            for (int m = 0; m < 7; m++) A.poses_next[(k - A.t0) * 7 + m] = pn[m];
     }
 }
 
@@ -747,6 +757,14 @@ __device__ __forceinline__ double rcp_f64(double d) {
     y = __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
     y = __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
     return y;
+}
+
+// 1/d with one Newton step: the estimate's 2^-24.4 relative error squared,
+// ~2^-48.8 (4e-15), for the pivots of the small solve, where each pivot's
+// reciprocal is on the factorization's dependency chain.
+__device__ __forceinline__ double rcp_f64_1(double d) {
+    const double y = __builtin_amdgcn_rcp(d);
+    return __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
 }
 
 __global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
@@ -963,24 +981,41 @@ constexpr int kSmallN = 64;
 constexpr int kSmallSlots = 3;  // ceil(560 / 256): 2 x 2 blocks of n8 = 64 per thread
 static_assert(kSmallN % kPW == 0 && kSmallN <= 64, "one row per lane in the backward solve");
 
-__global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
-    __shared__ double PU[kSmallN + 1][kPW];                              // panel as published
-    __shared__ __attribute__((aligned(16))) double PL[kSmallN + 1][kPW];  // l of rows >= r0
-    __shared__ __attribute__((aligned(16))) double PD[kSmallN + 1][kPW];  // d_m * l of rows >= r0
-    // L by rows, row n8 = w; zero elsewhere (sized to whole rounds of zeroing)
-    __shared__ __attribute__((aligned(16))) double Lf[(kSmallN + 1 + 7) / 8 * 8][64];
-    __shared__ double xs[kSmallN];
-    __shared__ float pose0[(kSmallN / 6) * 7];
+// Rows of the panel buffers hold kPW + 1 doubles and rows of L 65: a lane
+// per row then lands on a different pair of LDS banks for every lane (at
+// kPW and 64 doubles, 16 and 64 lanes of a wave share a bank).
+constexpr int kSmallPLd = kPW + 1;
+constexpr int kSmallLfLd = 65;
+constexpr int kSmallLfRows = (kSmallN + 1 + 7) / 8 * 8;
+static_assert(kSmallLfRows * kSmallLfLd % 2 == 0, "L zeroed as 16-byte pairs");
+
+struct SmallLds {
+    double PU[kSmallN + 1][kSmallPLd];  // panel as published
+    double PL[kSmallN + 1][kSmallPLd];  // l of rows >= r0
+    double PD[kSmallN + 1][kSmallPLd];  // d_m * l of rows >= r0
+    // L by rows, row n8 = w; zero elsewhere
+    __attribute__((aligned(16))) double Lf[kSmallLfRows][kSmallLfLd];
+    double xs[kSmallN];
+    float pose0[(kSmallN / 6) * 7];
+};
+
+__device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& sm) {
+    auto& PU = sm.PU;
+    auto& PL = sm.PL;
+    auto& PD = sm.PD;
+    auto& Lf = sm.Lf;
+    auto& xs = sm.xs;
+    auto& pose0 = sm.pose0;
     const int n = A.n, n8 = pad_panel(n), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hb = n8 / 2;                    // block rows 0..hb (hb: b^T)
     const int nblk = hb * (hb + 1) / 2 + hb;  // lower 2 x 2 blocks
     if (tid < (A.t1 - A.t0) * 7) pose0[tid] = A.poses[A.t0 * 7 + tid];
     {
-        constexpr int kZeroRounds = sizeof(Lf) / (256 * 16);
-        static_assert(sizeof(Lf) % (256 * 16) == 0, "whole rounds of 16-byte writes");
+        constexpr int kPairs = kSmallLfRows * kSmallLfLd / 2;
 #pragma unroll
-        for (int u = 0; u < kZeroRounds; u++)
-            reinterpret_cast<double2*>(&Lf[0][0])[tid + 256 * u] = make_double2(0.0, 0.0);
+        for (int u = 0; u < (kPairs + 255) / 256; u++)
+            if (tid + 256 * u < kPairs)
+                reinterpret_cast<double2*>(&Lf[0][0])[tid + 256 * u] = make_double2(0.0, 0.0);
     }
     // this thread's blocks: (i0, k0) of slot s, and their four entries
     int bi0[kSmallSlots], bk0[kSmallSlots];
@@ -1031,7 +1066,7 @@ __global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
         for (int j = 0; j < kPW; j++) {
             dj[j] = D[j][j];
             ok = ok && (dj[j] > 0.0);
-            rj[j] = rcp_f64(dj[j]);
+            rj[j] = rcp_f64_1(dj[j]);
 #pragma unroll
             for (int i = j + 1; i < kPW; i++) Lb[i][j] = D[i][j] * rj[j];
 #pragma unroll
@@ -1104,6 +1139,11 @@ __global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
     }
     __syncthreads();
     finish_solve(A, xs, ok, pose0);
+}
+
+__global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
+    __shared__ SmallLds sm;
+    solve_small_body(A, sm);
 }
 
 // ---- blocked Cholesky over many workgroups (n > kPanelN: the backend's systems) ----
@@ -1392,29 +1432,49 @@ struct FzArgs {
     const float* target;
     const float* weight;
     const float* poses;
-    const float* poses_prev;  // [P][7]: poses t0..t1-1 before the last step
+    const float* poses_prev;  // [P][7]: poses t0..t1-1 of the last step's linearization
+    float* pose_copy;         // [P][7] or null: k_ba_fz<false, *> copies poses t0..t1-1 here
     const float* intr;
     const float* eta;
     const float* dx;   // [6P] the last step
-    const int* flags;  // [0]: the last step was rejected (not SPD)
+    int* flags;        // [0]: the last step was rejected (not SPD); [3] a wait gave up
     float* disps;
     double* hpart;  // [M][nch][27]
     double* spart;  // [N_kf][nch][kFzMaxNT][256] Z tiles in MFMA lane order
     int HW, W, nch, t0, t1;
 };
 
-// Relative pose of edge (ix, jx) at the current poses, or (prev) at the poses
-// of the last step's linearization: only t0..t1-1 moved.
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Pose k of `poses`, read with device-coherent loads: values another
+// workgroup of the same launch wrote, which this workgroup's caches may hold
+// stale copies of (the lines were read before those writes).
+__device__ __forceinline__ void load_pose_coherent(const float* poses, int k, double* t,
+                                                   double* q) {
+    for (int m = 0; m < 3; m++) t[m] = (double)ld_coherent(poses + k * 7 + m);
+    for (int m = 0; m < 4; m++) q[m] = (double)ld_coherent(poses + k * 7 + 3 + m);
+}
+
+// Relative pose of edge (ix, jx) at the current poses (coherent: read them
+// with device-coherent loads), or (prev) at the poses of the last step's
+// linearization: only t0..t1-1 moved.
 __device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int jx, double* tij,
-                                       double* qij) {
+                                       double* qij, bool coherent = false) {
     if (ix == jx) {
         edge_rel(F.poses, ix, jx, tij, qij);  // stereo constants
         return;
     }
     double ti[3], qi[4], tj[3], qj[4];
-    const bool pi = prev && ix >= F.t0 && ix < F.t1, pj = prev && jx >= F.t0 && jx < F.t1;
-    load_pose(pi ? F.poses_prev : F.poses, pi ? ix - F.t0 : ix, ti, qi);
-    load_pose(pj ? F.poses_prev : F.poses, pj ? jx - F.t0 : jx, tj, qj);
+    if (coherent) {
+        load_pose_coherent(F.poses, ix, ti, qi);
+        load_pose_coherent(F.poses, jx, tj, qj);
+    } else {
+        const bool pi = prev && ix >= F.t0 && ix < F.t1, pj = prev && jx >= F.t0 && jx < F.t1;
+        load_pose(pi ? F.poses_prev : F.poses, pi ? ix - F.t0 : ix, ti, qi);
+        load_pose(pj ? F.poses_prev : F.poses, pj ? jx - F.t0 : jx, tj, qj);
+    }
     rel_se3(ti, qi, tj, qj, tij, qij);
 }
 
@@ -1458,132 +1518,44 @@ __device__ __forceinline__ void fz_schur_tiles(double* xs, const double* qs, int
         for (int r = 0; r < 4; r++) xs[(wave * kFzMaxNT + t) * 256 + lane * 4 + r] = z[t][r];
 }
 
-template <bool kBs, bool kLin>
-__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
-    __shared__ double xs[kLinPx * kFzLd];        // [pixel][row]; then the MFMA partials
-    __shared__ double cw[3][kLinWaves][kLinPx];  // per-wave sums (dw, C, w) / (C, w)
-    __shared__ double qs[kLinPx];
-    __shared__ float dnew[kLinPx];
-    const int chunk = blockIdx.x, kc = blockIdx.y;
-    const FzKf K = F.kfs[kc];
+// LDS of a fused linearization workgroup.
+struct FzLds {
+    double xs[kLinPx * kFzLd];        // [pixel][row]; then the MFMA partials
+    double cw[2][kLinWaves][kLinPx];  // per-wave sums (C, w)
+    double qs[kLinPx];
+    double dxr[6 * kFzMaxSlots];  // the last step's dx, by slot row
+    int spose[kFzMaxSlots];       // the pose of each slot
+    int wait_state;
+};
+
+// What the first pass over a wave's first edge read, reused by the second:
+// its targets and weights, and (rel) its relative pose at the current poses.
+struct FzCache {
+    bool valid, rel;
+    int ix, jx;
+    float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+    double tn[3], qn[4];
+};
+
+// One pass over the keyframe's edges for the chunk's pixels, at the poses of
+// the last step (kPrev: the rows that step's back-substitution needs) or at
+// the current poses (the Hjj/vj partials of every edge to hpart as well).
+// Leaves L.xs with the keyframe's E rows and w ([pixel][row]: the slots'
+// rows, own row in slot 0 when the keyframe's pose is free, w at row
+// 6 nslot, zeros up to 16 T) and L.qs with Q (damping_Q_kernel with
+// ep = 1e-7, ba.cuh:266-281, 701-702; eta_px: eta of the thread's pixel).
+// Ends with a barrier.
+template <bool kPrev>
+__device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L, int chunk,
+                                        const int (&kpx)[kLinPPL], const bool (&vpx)[kLinPPL],
+                                        const double (&dsp)[kLinPPL], double eta_px,
+                                        FzCache& cache, bool coherent = false) {
     const int nslot = K.info & 0xff, ri = (K.info >> 8) & 1, T = K.info >> 12;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int HW = F.HW;
     const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
-    int kpx[kLinPPL];
-    bool vpx[kLinPPL];
-    double dsp[kLinPPL];
-#pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
-        kpx[s] = chunk * kLinPx + s * 64 + lane;
-        vpx[s] = kpx[s] < HW;
-        dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
-    }
-    // the wave's first edge as the back-substitution pass saw it, reused by the
-    // linearization pass: its record, relative pose at the current poses, and
-    // targets / weights
-    bool cached = false;
-    FzEdge E0 = {0, 0, 0, -1};
-    double t0n[3] = {0.0, 0.0, 0.0}, q0n[4] = {0.0, 0.0, 0.0, 1.0};
-    float c_tgu[kLinPPL], c_tgv[kLinPPL], c_wtu[kLinPPL], c_wtv[kLinPPL];
-    if (kBs && F.flags[0] == 0) {  // uniform; a rejected step leaves the depths as they are
-        double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
-#pragma unroll
-        for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
-        for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
-            const FzEdge E = F.eds[ei];
-            const bool stereo = E.ix == E.jx;
-            double tij[3], qij[4];
-            fz_rel(F, true, E.ix, E.jx, tij, qij);
-            const bool first = kLin && ei == K.e0 + wave;
-            if (first) fz_rel(F, false, E.ix, E.jx, t0n, q0n);
-            // dl = dx_j (the edge's own row) - Adj^T dx_i (the keyframe's row)
-            double dl[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-            if (!stereo) {
-                if (E.slot >= 0)
-#pragma unroll
-                    for (int n = 0; n < 6; n++) dl[n] = (double)F.dx[(E.jx - F.t0) * 6 + n];
-                if (ri) {  // lane c < 6: (Adj^T dx_i)[c] = adj_se3(e_c) . dx_i
-                    double u[6], y[6], t = 0.0;
-#pragma unroll
-                    for (int m = 0; m < 6; m++) u[m] = m == lane ? 1.0 : 0.0;
-                    adj_se3(tij, qij, u, y);
-#pragma unroll
-                    for (int m = 0; m < 6; m++) t += y[m] * (double)F.dx[(E.ix - F.t0) * 6 + m];
-#pragma unroll
-                    for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
-                }
-            }
-            float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
-#pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
-                const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
-                tgu[s] = F.target[base];
-                tgv[s] = F.target[base + HW];
-                wtu[s] = F.weight[base];
-                wtv[s] = F.weight[base + HW];
-            }
-            if (first) {
-                cached = true;
-                E0 = E;
-#pragma unroll
-                for (int s = 0; s < kLinPPL; s++) {
-                    c_tgu[s] = tgu[s];
-                    c_tgv[s] = tgv[s];
-                    c_wtu[s] = wtu[s];
-                    c_wtv[s] = wtv[s];
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
-                if (!vpx[s]) continue;
-                Lin L;
-                lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
-                          (double)tgv[s], (double)wtu[s], (double)wtv[s], L);
-                cp[s] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
-                wp[s] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
-                if (!stereo) {
-                    const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
-                    double t = 0.0;
-#pragma unroll
-                    for (int n = 0; n < 6; n++) t += (a0 * L.Jj[0][n] + a1 * L.Jj[1][n]) * dl[n];
-                    dwp[s] += t;
-                }
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
-            const int px = s * 64 + lane;
-            cw[0][wave][px] = dwp[s];
-            cw[1][wave][px] = cp[s];
-            cw[2][wave][px] = wp[s];
-        }
-        __syncthreads();
-        {
-            const int k = chunk * kLinPx + tid;
-            if (k < HW) {
-                double dw = 0.0, c = 0.0, w = 0.0;
-#pragma unroll
-                for (int v = 0; v < kLinWaves; v++) {
-                    dw += cw[0][v][tid];
-                    c += cw[1][v][tid];
-                    w += cw[2][v][tid];
-                }
-                // damping_Q_kernel (ep = 1e-7) and depth_update_kernel
-                const double q = 1.0 / (c + 0.2 * (double)F.eta[(size_t)K.kf * HW + k] + 1e-7);
-                float* d = F.disps + (size_t)K.kf * HW + k;
-                const float dn = (float)((double)*d + q * (w - dw));
-                *d = dn;
-                dnew[tid] = dn;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < kLinPPL; s++)
-            if (vpx[s]) dsp[s] = (double)dnew[s * 64 + lane];
-    }
-    if (!kLin) return;
+    double* xs = L.xs;
     {
         // rows past the slots and w (and every row of a pixel past HW) are zero
         const int k = chunk * kLinPx + tid;
@@ -1599,25 +1571,28 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
         for (int n = 0; n < 6; n++) er[s][n] = 0.0;
     }
     for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
-        const bool hit = cached && ei == K.e0 + wave;  // uniform
-        const FzEdge E = hit ? E0 : F.eds[ei];
+        const bool first = ei == K.e0 + wave;  // uniform
+        const FzEdge E = F.eds[ei];
         const bool stereo = E.ix == E.jx;
         double tij[3], qij[4];
+        if (!kPrev && first && cache.rel) {
+#pragma unroll
+            for (int m = 0; m < 3; m++) tij[m] = cache.tn[m];
+#pragma unroll
+            for (int m = 0; m < 4; m++) qij[m] = cache.qn[m];
+        } else {
+            fz_rel(F, kPrev, E.ix, E.jx, tij, qij, coherent);
+        }
         float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
-        if (hit) {
-#pragma unroll
-            for (int m = 0; m < 3; m++) tij[m] = t0n[m];
-#pragma unroll
-            for (int m = 0; m < 4; m++) qij[m] = q0n[m];
+        if (!kPrev && first && cache.valid) {
 #pragma unroll
             for (int s = 0; s < kLinPPL; s++) {
-                tgu[s] = c_tgu[s];
-                tgv[s] = c_tgv[s];
-                wtu[s] = c_wtu[s];
-                wtv[s] = c_wtv[s];
+                tgu[s] = cache.tgu[s];
+                tgv[s] = cache.tgv[s];
+                wtu[s] = cache.wtu[s];
+                wtv[s] = cache.wtv[s];
             }
         } else {
-            fz_rel(F, false, E.ix, E.jx, tij, qij);
 #pragma unroll
             for (int s = 0; s < kLinPPL; s++) {
                 const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
@@ -1625,6 +1600,18 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
                 tgv[s] = F.target[base + HW];
                 wtu[s] = F.weight[base];
                 wtv[s] = F.weight[base + HW];
+            }
+            if (kPrev && first) {
+                cache.valid = true;
+                cache.ix = E.ix;
+                cache.jx = E.jx;
+#pragma unroll
+                for (int s = 0; s < kLinPPL; s++) {
+                    cache.tgu[s] = tgu[s];
+                    cache.tgv[s] = tgv[s];
+                    cache.wtu[s] = wtu[s];
+                    cache.wtv[s] = wtv[s];
+                }
             }
         }
         double acc[kNJ];
@@ -1634,17 +1621,17 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
         for (int s = 0; s < kLinPPL; s++) {
             if (!vpx[s]) continue;
             const int px = s * 64 + lane;
-            Lin L;
+            Lin Ln;
             lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
-                      (double)tgv[s], (double)wtu[s], (double)wtv[s], L);
-            accum_hjj(L, stereo, acc);
-            cp[s] += L.w[0] * L.Jz[0] * L.Jz[0] + L.w[1] * L.Jz[1] * L.Jz[1];
-            wp[s] += L.w[0] * L.r[0] * L.Jz[0] + L.w[1] * L.r[1] * L.Jz[1];
+                      (double)tgv[s], (double)wtu[s], (double)wtv[s], Ln);
+            if (!kPrev) accum_hjj(Ln, stereo, acc);
+            cp[s] += Ln.w[0] * Ln.Jz[0] * Ln.Jz[0] + Ln.w[1] * Ln.Jz[1] * Ln.Jz[1];
+            wp[s] += Ln.w[0] * Ln.r[0] * Ln.Jz[0] + Ln.w[1] * Ln.r[1] * Ln.Jz[1];
             if (!stereo) {  // a stereo edge adds nothing to E
-                const double a0 = L.w[0] * L.Jz[0], a1 = L.w[1] * L.Jz[1];
+                const double a0 = Ln.w[0] * Ln.Jz[0], a1 = Ln.w[1] * Ln.Jz[1];
                 double g[6];
 #pragma unroll
-                for (int n = 0; n < 6; n++) g[n] = a0 * L.Jj[0][n] + a1 * L.Jj[1][n];
+                for (int n = 0; n < 6; n++) g[n] = a0 * Ln.Jj[0][n] + a1 * Ln.Jj[1][n];
                 if (E.slot >= 0) {
                     double* xr = xs + px * kFzLd + 6 * E.slot;
 #pragma unroll
@@ -1658,18 +1645,20 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
                 }
             }
         }
-        int rbase, rvalid;
-        wave_reduce_scatter(acc, lane, rbase, rvalid);
-        double* hp = F.hpart + ((size_t)E.e * F.nch + chunk) * kNJ;
+        if (!kPrev) {
+            int rbase, rvalid;
+            wave_reduce_scatter(acc, lane, rbase, rvalid);
+            double* hp = F.hpart + ((size_t)E.e * F.nch + chunk) * kNJ;
 #pragma unroll
-        for (int q = 0; q < RsCounts<kNJ>::c6; q++)
-            if (q < rvalid) hp[rbase + q] = acc[q];
+            for (int q = 0; q < RsCounts<kNJ>::c6; q++)
+                if (q < rvalid) hp[rbase + q] = acc[q];
+        }
     }
 #pragma unroll
     for (int s = 0; s < kLinPPL; s++) {
         const int px = s * 64 + lane;
-        cw[0][wave][px] = cp[s];
-        cw[1][wave][px] = wp[s];
+        L.cw[0][wave][px] = cp[s];
+        L.cw[1][wave][px] = wp[s];
     }
     // the keyframe's own row (slot 0): the waves' parts added in wave order,
     // from per-wave copies in the columns past the tiles when two tiles hold
@@ -1707,11 +1696,10 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
             double c = 0.0, w = 0.0;
 #pragma unroll
             for (int v = 0; v < kLinWaves; v++) {
-                c += cw[0][v][tid];
-                w += cw[1][v][tid];
+                c += L.cw[0][v][tid];
+                w += L.cw[1][v][tid];
             }
-            // damping_Q_kernel with ep = 1e-7 (ba.cuh:266-281, 701-702)
-            q = 1.0 / (c + 0.2 * (double)F.eta[(size_t)K.kf * HW + k] + 1e-7);
+            q = 1.0 / (c + 0.2 * eta_px + 1e-7);
             xr[6 * nslot] = w;
             if (ri && er_cols) {
 #pragma unroll
@@ -1723,18 +1711,150 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
                 }
             }
         }
-        qs[tid] = q;
+        L.qs[tid] = q;
     }
     __syncthreads();
+}
+
+// The overlapped step's handshake: the assembly launch before it clears
+// *ready, the step launch's solve workgroup stores 1 there once dx, the flags
+// and the poses are written, and a linearization workgroup waits for it
+// (thread 0 polls, bounded: after kFzSpinMax polls the workgroup gives up,
+// flags[3] reports it, and it writes nothing more).
+constexpr int kFzSpinMax = 1 << 18;
+
+struct FzWait {
+    int* ready;  // null: no wait (the step's dx is known at launch)
+};
+
+// k_ba_fz's work for one (pixel chunk, keyframe): with kBs first the depth
+// update of the last step, dz = Q (w - E^T dx) (EvT6x1 + depth_update,
+// ba.cuh:762-783) from that step's E rows, Q and w recomputed at its poses
+// and depths (with a wait for dx when `wait.ready` is set); with kLin then the
+// linearization at the current state and the Schur tiles of the chunk.
+template <bool kBs, bool kLin>
+__device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, int kc,
+                                        FzWait wait) {
+    const FzKf K = F.kfs[kc];
+    const int nslot = K.info & 0xff, ri = (K.info >> 8) & 1, T = K.info >> 12;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int HW = F.HW;
+    int kpx[kLinPPL];
+    bool vpx[kLinPPL];
+    double dsp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        kpx[s] = chunk * kLinPx + s * 64 + lane;
+        vpx[s] = kpx[s] < HW;
+        dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
+    }
+    FzCache cache;
+    cache.valid = cache.rel = false;
+    const int kown = chunk * kLinPx + tid;  // the pixel of the per-pixel steps
+    const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
+    // without a wait the step's status is known now: a rejected step leaves
+    // the depths as they are
+    if (kBs && (wait.ready || F.flags[0] == 0)) {  // uniform
+        // the pose of each slot: the keyframe's for slot 0 when free, else
+        // the jj of the edge that owns it (ordered by the pass's barriers)
+        for (int ei = K.e0 + tid; ei < K.e1; ei += kLinWG) {
+            const FzEdge E = F.eds[ei];
+            if (E.slot >= 0) L.spose[E.slot] = E.jx;
+        }
+        if (ri && tid == 0) L.spose[0] = K.kf;
+        fz_pass<true>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache);
+        if (wait.ready) {
+            if (tid == 0) {
+                int st = 1;
+                for (int n = 0; __hip_atomic_load(wait.ready, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) == 0;
+                     n++) {
+                    if (n == kFzSpinMax) {
+                        st = 0;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                L.wait_state = st;
+            }
+            __syncthreads();
+            if (!L.wait_state) {  // uniform
+                if (tid == 0) F.flags[3] = 1;
+                return;
+            }
+            // What the solve wrote (the status, dx, the poses) is read from
+            // here on with device-coherent loads, issued after the flag was
+            // seen, so no cache of this workgroup needs invalidating.
+        }
+        // one round of loads, all issued before any is used: the status, dx
+        // by slot row (slot poses are free poses), and the poses of the
+        // wave's first edge (pose 0 stands in when there is none)
+        const int r6 = nslot > 0 ? min(tid, 6 * nslot - 1) : 0;
+        const int dxi = nslot > 0 ? (L.spose[r6 / 6] - F.t0) * 6 + r6 % 6 : 0;
+        const int pix = cache.valid ? cache.ix : 0, pjx = cache.valid ? cache.jx : 0;
+        const int okv = __hip_atomic_load(F.flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float dxf = ld_coherent(F.dx + dxi);
+        float pi[7], pj[7];
+#pragma unroll
+        for (int m = 0; m < 7; m++) {
+            pi[m] = ld_coherent(F.poses + pix * 7 + m);
+            pj[m] = ld_coherent(F.poses + pjx * 7 + m);
+        }
+        const bool ok = okv == 0;
+        if (kLin && cache.valid) {  // fz_rel at the current poses, from the loaded values
+            if (pix == pjx) {
+                edge_rel(F.poses, pix, pjx, cache.tn, cache.qn);  // stereo constants
+            } else {
+                double ti[3], qi[4], tj[3], qj[4];
+#pragma unroll
+                for (int m = 0; m < 3; m++) {
+                    ti[m] = (double)pi[m];
+                    tj[m] = (double)pj[m];
+                }
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    qi[m] = (double)pi[3 + m];
+                    qj[m] = (double)pj[3 + m];
+                }
+                rel_se3(ti, qi, tj, qj, cache.tn, cache.qn);
+            }
+            cache.rel = true;
+        }
+        if (tid < 6 * nslot) L.dxr[tid] = (double)dxf;
+        __syncthreads();
+        if (ok) {  // uniform
+            double own = dsp[0];  // the depth of pixel kown (lane's pixel of s = wave)
+#pragma unroll
+            for (int s = 1; s < kLinPPL; s++)
+                if (s == wave) own = dsp[s];
+            if (kown < HW) {
+                const double* xr = L.xs + tid * kFzLd;
+                double dw = 0.0;
+                for (int sl = 0; sl < nslot; sl++)
+#pragma unroll
+                    for (int m = 0; m < 6; m++) dw += xr[6 * sl + m] * L.dxr[6 * sl + m];
+                const float dn = (float)(own + L.qs[tid] * (xr[6 * nslot] - dw));
+                F.disps[(size_t)K.kf * HW + kown] = dn;
+                L.cw[0][0][tid] = (double)dn;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++)
+                if (vpx[s]) dsp[s] = L.cw[0][0][s * 64 + lane];
+        }
+    }
+    if (!kLin) return;
+    fz_pass<false>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache, wait.ready != nullptr);
     if (T == 1)
-        fz_schur_tiles<1>(xs, qs, wave, lane);
+        fz_schur_tiles<1>(L.xs, L.qs, wave, lane);
     else if (T == 2)
-        fz_schur_tiles<2>(xs, qs, wave, lane);
+        fz_schur_tiles<2>(L.xs, L.qs, wave, lane);
     else
-        fz_schur_tiles<3>(xs, qs, wave, lane);
+        fz_schur_tiles<3>(L.xs, L.qs, wave, lane);
     __syncthreads();
     const int nt = T * (T + 1) / 2;
-    const double* red = xs;
+    const double* red = L.xs;
     double* sp = F.spart + (size_t)(kc * F.nch + chunk) * kFzMaxNT * 256;
     for (int idx = tid; idx < nt * 256; idx += kLinWG) {
         double v = red[idx];
@@ -1742,6 +1862,43 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
         for (int w = 1; w < kLinWaves; w++) v += red[w * kFzMaxNT * 256 + idx];
         sp[idx] = v;
     }
+}
+
+template <bool kBs, bool kLin>
+__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
+    __shared__ FzLds L;
+    if (!kBs && F.pose_copy && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int t = threadIdx.x; t < (F.t1 - F.t0) * 7; t += kLinWG)
+            F.pose_copy[t] = F.poses[F.t0 * 7 + t];
+    fz_body<kBs, kLin>(F, L, blockIdx.x, blockIdx.y, FzWait{nullptr});
+}
+
+// One launch per step k >= 2 of the overlapped fused iteration (n <= kSmallN):
+// workgroup 0 solves step k - 1 (the system the assembly just wrote), the
+// others run k_ba_fz's work for their (chunk, keyframe), recomputing step
+// k - 1's E rows at F.poses_prev (its poses, copied by the step before)
+// while the solve runs, and waiting for its dx only for the depth update.
+// Every waiter waits on workgroup 0 alone, which is dispatched first.
+union FzStepLds {
+    FzLds fz;
+    SmallLds sv;
+};
+
+template <bool kLin>
+__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz_step(FzArgs F, SolveArgs A, FzWait wait) {
+    __shared__ FzStepLds lds;
+    if (blockIdx.x == 0) {
+        solve_small_body(A, lds.sv);
+        // every wave's writes (dx, flags, poses) made visible device-wide
+        // before the flag
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(wait.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int b = blockIdx.x - 1;
+    fz_body<true, kLin>(F, lds.fz, b % F.nch, b / F.nch, wait);
 }
 
 struct FzAsmArgs {
@@ -1759,6 +1916,7 @@ struct FzAsmArgs {
     float lm, ep;
     double* S;  // [n][n] assembled system (after damping)
     double* b;  // [n]
+    int* ready;  // or null: the overlapped step's flag, cleared here for the launch after
 };
 
 // Entry (row, col) of a keyframe's Z, summed over the chunks: Z is symmetric
@@ -1790,6 +1948,7 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     const int g = blockIdx.x, tid = threadIdx.x;
     const int sl = tid / 36, ent = tid - sl * 36;
     const int P = A.P, n = A.n;
+    if (A.ready && g == 0 && tid == 0) *A.ready = 0;
     const bool isS = g < P * P;
     const bool act = sl < kAsmSlices && (isS || ent < 6);
     const int r = ent / 6, c = ent - (ent / 6) * 6;
@@ -1906,6 +2065,8 @@ struct BaState {
     bool fz = false;
     size_t fz_off[7] = {0};  // kfs, eds, items, dptr, dsrc, deptr, dedges (ints into host)
     DevBuf spart, poses_prev;
+    // overlapped steps (n <= kSmallN): the second pose copy and the step flag
+    DevBuf poses_alt, ready;
 };
 
 namespace {
@@ -2211,6 +2372,8 @@ int ba_prepare(slk_ctx* ctx, const IterArgs& I, const int* ii_host, const int* j
     if (s->fz) {
         SLK_TRY(s->spart.ensure((size_t)s->N_kf * s->nch * kFzMaxNT * 256 * sizeof(double)));
         SLK_TRY(s->poses_prev.ensure((size_t)s->P * 7 * sizeof(float)));
+        SLK_TRY(s->poses_alt.ensure((size_t)s->P * 7 * sizeof(float)));
+        SLK_TRY(s->ready.ensure(sizeof(int)));
     } else {
         SLK_TRY(s->etot.ensure((size_t)M * kNT * sizeof(double)));
         SLK_TRY(s->stot.ensure(std::max<size_t>(1, (size_t)(s->N_pu + s->N_E) * 36) *
@@ -2255,6 +2418,7 @@ SolveArgs solve_args(BaState* s, const PlanDev& plan, const IterArgs& I) {
     A.flags = s->flags.as<int>();
     A.poses = I.poses;
     A.poses_prev = s->fz ? s->poses_prev.as<float>() : nullptr;
+    A.poses_next = nullptr;
     return A;
 }
 
@@ -2327,6 +2491,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     F.weight = I.weight;
     F.poses = I.poses;
     F.poses_prev = s->poses_prev.as<float>();
+    F.pose_copy = nullptr;
     F.intr = I.intr;
     F.eta = I.eta;
     F.dx = s->dx.as<float>();
@@ -2357,8 +2522,51 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     G.ep = I.ep;
     G.S = s->S_dbg.as<double>();
     G.b = s->b_dbg.as<double>();
+    G.ready = nullptr;
     const SolveArgs A = solve_args(s, plan, I);
     const dim3 grid(s->nch, s->N_kf);
+    if (s->n <= kSmallN) {
+        // Overlapped steps: the first linearization (which keeps a copy of the
+        // poses it used), then per step the assembly and one launch of the
+        // solve beside the next linearization. The pose copies alternate:
+        // step k's launch relinearizes at pp[k & 1] while its solve writes
+        // the new poses to pp[(k + 1) & 1].
+        float* pp[2] = {s->poses_prev.as<float>(), s->poses_alt.as<float>()};
+        FzArgs F1 = F;
+        F1.pose_copy = pp[0];
+        {
+            ProfScope ps(ctx, "ba_fz_lin", stream);
+            hipLaunchKernelGGL((k_ba_fz<false, true>), grid, dim3(kLinWG), 0, stream, F1);
+        }
+        SLK_HIP(hipGetLastError());
+        G.ready = s->ready.as<int>();
+        const FzWait wait = {s->ready.as<int>()};
+        const dim3 sgrid(1 + s->nch * s->N_kf);
+        for (int it = 0; it < iters; it++) {
+            {
+                ProfScope ps(ctx, "ba_fz_asm", stream);
+                hipLaunchKernelGGL(k_ba_fz_assemble, dim3(s->P * s->P + s->P), dim3(256), 0,
+                                   stream, G);
+            }
+            SLK_HIP(hipGetLastError());
+            FzArgs Fk = F;
+            Fk.poses_prev = pp[it & 1];
+            SolveArgs Ak = A;
+            Ak.poses_prev = nullptr;
+            Ak.poses_next = pp[(it + 1) & 1];
+            if (it + 1 < iters) {
+                ProfScope ps(ctx, "ba_fz_step", stream);
+                hipLaunchKernelGGL(k_ba_fz_step<true>, sgrid, dim3(kLinWG), 0, stream, Fk, Ak,
+                                   wait);
+            } else {
+                ProfScope ps(ctx, "ba_fz_last", stream);
+                hipLaunchKernelGGL(k_ba_fz_step<false>, sgrid, dim3(kLinWG), 0, stream, Fk, Ak,
+                                   wait);
+            }
+            SLK_HIP(hipGetLastError());
+        }
+        return SLK_OK;
+    }
     for (int it = 0; it < iters; it++) {
         {
             ProfScope ps(ctx, "ba_fz_lin", stream);
@@ -2426,9 +2634,11 @@ extern "C" int slk_ba_status(slk_ctx* ctx, hipStream_t stream) {
     int f[4];
     SLK_HIP(hipMemcpyAsync(f, ctx->ba->flags.ptr, sizeof f, hipMemcpyDeviceToHost, stream));
     SLK_HIP(hipStreamSynchronize(stream));
-    const int bad = f[1];
+    const int bad = f[1], gave_up = f[3];
     SLK_HIP(hipMemsetAsync(ctx->ba->flags.ptr, 0, sizeof f, stream));
     SLK_HIP(hipStreamSynchronize(stream));
+    if (gave_up)
+        return fail(SLK_E_HIP, "ba_iterate: a fused step stopped waiting for its solve");
     return bad ? fail(SLK_E_NOT_SPD, "ba_iterate: system not positive definite") : SLK_OK;
 }
 

@@ -135,9 +135,12 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
                        t0, t1, lm, ep, motion_only != 0);
     if (launches) {
         // launches of the linearization (five-kernel or fused iteration) and
-        // of the solve over all iterates
-        launches[0] = ba.profiled_launches("ba_lin_kf") + ba.profiled_launches("ba_fz_lin");
-        launches[1] = ba.profiled_launches("ba_solve");
+        // of the solve over all iterates; an overlapped fused step launch
+        // holds a solve and the next linearization, the last one a solve
+        const int steps = ba.profiled_launches("ba_fz_step");
+        launches[0] =
+            ba.profiled_launches("ba_lin_kf") + ba.profiled_launches("ba_fz_lin") + steps;
+        launches[1] = ba.profiled_launches("ba_solve") + steps + ba.profiled_launches("ba_fz_last");
         ba.print_profile();
     }
     slk_droid::clamp_disps(d_d, (int)(N * hw), 0.001f);

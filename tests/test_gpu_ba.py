@@ -116,7 +116,8 @@ def test_iterate_n_matches_oracle_and_single_calls(slk, case):
     """slk_ba_iterate_n(3) against three chained oracle iterations and against
     three slk_ba_iterate calls: the cfg3 window runs the fused iteration (E
     rows and Schur products kept on chip, back-substitution folded into the
-    next linearization), the dense keyframe the five-kernel one."""
+    next linearization, each solve in one launch with the next
+    linearization), the dense keyframe the five-kernel one."""
     announce(f"ba iterate_n(3) {case}")
     p = wl.ba_problem() if case == "window" else _dense_keyframe_problem()
     h, w = p["h"], p["w"]
@@ -135,7 +136,7 @@ def test_iterate_n_matches_oracle_and_single_calls(slk, case):
     assert ctx_a.ba_status() == slk.SLK_OK
     kernels = _path_kernels(ctx_a)
     if case == "window":
-        assert {"ba_fz_lin", "ba_fz_asm", "ba_fz_bs"} <= kernels, kernels
+        assert {"ba_fz_lin", "ba_fz_asm", "ba_fz_step", "ba_fz_last"} <= kernels, kernels
     else:
         assert {"ba_lin_kf", "ba_schur", "ba_backsub"} <= kernels, kernels
     for _ in range(3):
