@@ -87,6 +87,15 @@ __device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
 
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
+// four consecutive elements (16 or 8 bytes, aligned to that size)
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ldf4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ float4 ldf4(const _Float16* p) {
+    const half4_t h = *reinterpret_cast<const half4_t*>(p);
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
 
 // Which (edge, source tile, target tile) pairs hold at least one window cell:
 // per source and level present, the window's clipped rows/columns span the
@@ -114,6 +123,7 @@ struct MaskArgs {
     int* ctr;
     int* order;  // [edge][3][HW]: pixel, x, y of each sorted source position
     int mtiles, ntiles, nedges;
+    const unsigned long long* tab;  // window_tiles by floored coordinates, or null
 };
 
 // Target tiles holding a cell of the 8x8 windows (every level) of a source
@@ -133,6 +143,31 @@ __device__ __forceinline__ unsigned long long window_tiles(const Geom& g, int fx
     return m;
 }
 
+// window_tiles of every floored source position that can reach the image,
+// (fx, fy) in [-kTabPad, w + kTabPad) x [-kTabPad, h + kTabPad), at entry
+// (fy + kTabPad) * (w + 2 kTabPad) + fx + kTabPad. Outside that range no
+// level has a window cell: level l's window columns (fx >> l) - 3 ..
+// (fx >> l) + 4 meet 0 .. w_l - 1 only for -4 * 2^l <= fx < (w_l + 3) * 2^l,
+// inside [-32, w + 24) for l <= 3, and likewise for the rows.
+constexpr int kTabPad = 32;
+
+__global__ __launch_bounds__(256) void k_mask_table(Geom g, unsigned long long* tab) {
+    const int tw = g.w[0] + 2 * kTabPad, th = g.h[0] + 2 * kTabPad;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= tw * th) return;
+    tab[i] = window_tiles(g, i % tw - kTabPad, i / tw - kTabPad);
+}
+
+// window_tiles(g, fx, fy), from the table when there is one
+__device__ __forceinline__ unsigned long long tile_mask_of(const Geom& g,
+                                                           const unsigned long long* tab,
+                                                           int fx, int fy) {
+    if (!tab) return window_tiles(g, fx, fy);
+    const int tw = g.w[0] + 2 * kTabPad, th = g.h[0] + 2 * kTabPad;
+    const int tx = fx + kTabPad, ty = fy + kTabPad;
+    return (unsigned)tx < (unsigned)tw && (unsigned)ty < (unsigned)th ? tab[ty * tw + tx] : 0ull;
+}
+
 // ORs mask m (bit t = tile row + t) into the bitmap; a word is touched only
 // when it receives a set bit, so only words of existing tiles are
 __device__ __forceinline__ void merge_tiles(unsigned* bits, int row, unsigned long long m) {
@@ -148,9 +183,9 @@ __device__ __forceinline__ void merge_tiles(unsigned* bits, int row, unsigned lo
 
 // Marks the target tiles of one source in row `row` of the bitmap (any ntiles)
 __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int row, int ntiles,
-                                            unsigned* bits) {
+                                            unsigned* bits, const unsigned long long* tab) {
     if (ntiles <= 64) {
-        const unsigned long long m = window_tiles(g, fx, fy);
+        const unsigned long long m = tile_mask_of(g, tab, fx, fy);
         if (m) merge_tiles(bits, row, m);
         return;
     }
@@ -200,7 +235,7 @@ __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
 }
 
 __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
-                              unsigned* bits, int ntiles) {
+                              unsigned* bits, int ntiles, const unsigned long long* tab) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int HW = g.HW, nb = g.h[0] + 9;
     if (nb > kSortBuckets) return false;
@@ -240,7 +275,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
 #pragma unroll
         for (int u = 0; u < kG; u++) {
             if (pg + 64 * u + lane < q1) atomicAdd(&hist[wv * kSortBuckets + key_of(yv[u])], 1);
-            mk[u] = pre ? window_tiles(g, floor_clamped(xv[u]), floor_clamped(yv[u])) : 0ull;
+            mk[u] = pre ? tile_mask_of(g, tab, floor_clamped(xv[u]), floor_clamped(yv[u])) : 0ull;
         }
     }
     __syncthreads();
@@ -294,7 +329,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
                     if (mk[u]) merge_tiles(bits, q / kSrcTile * ntiles, mk[u]);
                 } else {
                     mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
-                                q / kSrcTile * ntiles, ntiles, bits);
+                                q / kSrcTile * ntiles, ntiles, bits, tab);
                 }
             }
         }
@@ -315,7 +350,7 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     const float* cc = coords + (size_t)e * 2 * g.HW;
     int* ord = a.order + (size_t)e * 3 * g.HW;
-    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles)) {  // uniform
+    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles, a.tab)) {  // uniform
         // pixel order: the order is the identity, written beside the mask.
         // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
         // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
@@ -346,10 +381,10 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
                     oxy[g.HW + pw + lane] = ys[u];
                 }
                 if (ntiles > 64) {
-                    if (in) mark_source(g, fx, fy, row, ntiles, bits);
+                    if (in) mark_source(g, fx, fy, row, ntiles, bits, a.tab);
                     continue;
                 }
-                const unsigned long long m = in ? window_tiles(g, fx, fy) : 0ull;
+                const unsigned long long m = in ? tile_mask_of(g, a.tab, fx, fy) : 0ull;
                 unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
 #pragma unroll
                 for (int off = 32; off >= 1; off >>= 1) {
@@ -403,8 +438,8 @@ template <typename Tin>
 __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
                                                    SlotFrames sf, int slot_lo,
                                                    unsigned short* __restrict__ out, Geom g,
-                                                   int pooled, int nbx, int nblk, int nmask,
-                                                   MaskArgs mk) {
+                                                   int pooled, int vec, int nbx, int nblk,
+                                                   int nmask, MaskArgs mk) {
     __shared__ float l0[kChunk][kPrepRows][kPrepCols];
     __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
     __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
@@ -428,20 +463,44 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     // all of a thread's loads are issued before the first is used
     constexpr int kPer = kChunk * kPrepRows * kPrepCols / 256;
     float ld[kPer];
+    if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
+        // four consecutive pixels of a row a lane (all inside or all outside)
 #pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = tid + u * 256;
-        const int c = i / (kPrepRows * kPrepCols);
-        const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-        const bool in = yy < H && xx < W;
-        ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-        if (!in) ld[u] = 0.0f;
-    }
+        for (int u = 0; u < kPer / 4; u++) {
+            const int i = 4 * (tid + u * 256);
+            const int c = i / (kPrepRows * kPrepCols);
+            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+            const bool in = yy < H && xx < W;
+            const float4 v = ldf4(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+            ld[4 * u] = in ? v.x : 0.0f;
+            ld[4 * u + 1] = in ? v.y : 0.0f;
+            ld[4 * u + 2] = in ? v.z : 0.0f;
+            ld[4 * u + 3] = in ? v.w : 0.0f;
+        }
 #pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = tid + u * 256;
-        l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
+        for (int u = 0; u < kPer / 4; u++) {
+            const int i = 4 * (tid + u * 256);
+            *reinterpret_cast<float4*>(
+                &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
+                make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kPer; u++) {
+            const int i = tid + u * 256;
+            const int c = i / (kPrepRows * kPrepCols);
+            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+            const bool in = yy < H && xx < W;
+            ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+            if (!in) ld[u] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; u++) {
+            const int i = tid + u * 256;
+            l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
+        }
     }
     __syncthreads();
     const size_t plane = (size_t)g.C * g.Ttot;
@@ -856,9 +915,12 @@ int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& s
     const long nmask = mk.list ? mk.nedges : 0;
     if (nprep + nmask == 0) return SLK_OK;
     if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
+    // vector loads of 4 pixels when every row starts 4-element aligned
+    const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
     hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(256), 0, stream,
-                       fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, nbx, nblk, (int)nmask,
-                       mk);
+                       fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, vec ? 1 : 0, nbx, nblk,
+                       (int)nmask, mk);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -884,7 +946,8 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
         return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
     MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
-                ctx->src_order.as<int>(), mtiles, ntiles, n};
+                ctx->src_order.as<int>(), mtiles, ntiles, n,
+                ctx->mask_tab.as<unsigned long long>()};
     {
         // feature preparation and the tile mask, one launch
         ProfScope ps(ctx, "corr_feat_prep", stream);
@@ -933,7 +996,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     // sources only need level 0 (their own launch); targets need every level
     {
         ProfScope ps(ctx, "corr_feat_prep", stream);
-        const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0};
+        const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
         SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
     }
     return mask_and_windows(ctx, fm, fstride, sf, g, n, n, true, es, feat, n, coords, win, slot0,
@@ -969,6 +1032,13 @@ int corr_split_alloc(slk_ctx* ctx) {
     SLK_TRY(ctx->src_order.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * 3 *
                                   g.HW * sizeof(int)));
     SLK_TRY(ctx->tile_ctr.ensure(kCtrInts * sizeof(int)));
+    if (ntiles <= 64) {  // tile masks as 64-bit words: their table by position
+        const long entries = (long)(g.w[0] + 2 * kTabPad) * (g.h[0] + 2 * kTabPad);
+        SLK_TRY(ctx->mask_tab.ensure((size_t)entries * sizeof(unsigned long long)));
+        hipLaunchKernelGGL(k_mask_table, dim3((unsigned)((entries + 255) / 256)), dim3(256), 0, 0,
+                           g, ctx->mask_tab.as<unsigned long long>());
+        SLK_HIP(hipGetLastError());
+    }
     // the correlation workgroups: two per CU, a multiple of the 8 XCDs
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) !=
@@ -1003,7 +1073,7 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     SLK_TRY(ctx->prep_feat.ensure(bytes));
     SlotFrames sf{};
     sf.ident = 1;
-    const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0};
+    const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
     ProfScope ps(ctx, "corr_prepare_frames", stream);
     if (dtype == SLK_F32)
         SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,
