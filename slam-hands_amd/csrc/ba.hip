@@ -767,10 +767,17 @@ __device__ __forceinline__ double rcp_f64_1(double d) {
     return __builtin_fma(y, __builtin_fma(-d, y, 1.0), y);
 }
 
-__global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
-    extern __shared__ double sm[];
-    __shared__ int ok_sh;
-    __shared__ float pose0[kPanelPoses * 7];  // poses t0..t1-1 before the step
+// LDS of the panel solver at its largest size, for a launch whose LDS is
+// declared statically (sm: packed [S; b^T], pivots, solution)
+struct PanelLds {
+    double sm[(kPanelN + 1) * (kPanelN + 2) / 2 + 2 * kPanelN];
+    int ok;
+    float pose0[kPanelPoses * 7];
+};
+
+// sm: panel_solve_lds_bytes(A.n) bytes; pose0: the poses t0..t1-1 before the step
+__device__ __forceinline__ void solve_panel_body(const SolveArgs& A, double* sm, int& ok_sh,
+                                                 float* pose0) {
     const int n = A.n, n8 = pad_panel(n), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     double* L = sm;                   // packed lower [S; b^T], padded
     double* piv = sm + tri(n8 + 1);   // [n8] pivots d_j
@@ -955,6 +962,13 @@ __global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
     }
     __syncthreads();
     finish_solve(A, xs, ok, pose0);
+}
+
+__global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
+    extern __shared__ double sm[];
+    __shared__ int ok_sh;
+    __shared__ float pose0[kPanelPoses * 7];
+    solve_panel_body(A, sm, ok_sh, pose0);
 }
 
 // ---- one-workgroup solver with the system in registers (n <= 64) ----
@@ -1753,9 +1767,113 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
     cache.valid = cache.rel = false;
     const int kown = chunk * kLinPx + tid;  // the pixel of the per-pixel steps
     const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
-    // without a wait the step's status is known now: a rejected step leaves
-    // the depths as they are
-    if (kBs && (wait.ready || F.flags[0] == 0)) {  // uniform
+    if (kBs && !wait.ready && F.flags[0] == 0) {  // uniform
+        // dx is known at launch (a rejected step leaves the depths as they
+        // are): per edge the step's projection dl = dx_j - Adj^T dx_i (lane
+        // c < 6 forms component c), then per pixel dw = sum_e g_e . dl_e,
+        // g_e = w Jz Jj at the last step's poses and depths
+        double* cwd = L.xs;  // [kLinWaves][kLinPx] per-wave sums of dw
+        double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
+        const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
+        for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
+            const FzEdge E = F.eds[ei];
+            const bool stereo = E.ix == E.jx;
+            const bool first = ei == K.e0 + wave;  // uniform
+            double tij[3], qij[4];
+            fz_rel(F, true, E.ix, E.jx, tij, qij);
+            if (kLin && first) {  // the linearization's relative pose of this edge
+                fz_rel(F, false, E.ix, E.jx, cache.tn, cache.qn);
+                cache.rel = true;
+            }
+            double dl[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+            if (!stereo) {
+                if (E.slot >= 0)
+#pragma unroll
+                    for (int n = 0; n < 6; n++) dl[n] = (double)F.dx[(E.jx - F.t0) * 6 + n];
+                if (ri) {  // lane c < 6: (Adj^T dx_i)[c] = adj_se3(e_c) . dx_i
+                    double u[6], y[6], t = 0.0;
+#pragma unroll
+                    for (int m = 0; m < 6; m++) u[m] = m == lane ? 1.0 : 0.0;
+                    adj_se3(tij, qij, u, y);
+#pragma unroll
+                    for (int m = 0; m < 6; m++) t += y[m] * (double)F.dx[(E.ix - F.t0) * 6 + m];
+#pragma unroll
+                    for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
+                }
+            }
+            float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
+                tgu[s] = F.target[base];
+                tgv[s] = F.target[base + HW];
+                wtu[s] = F.weight[base];
+                wtv[s] = F.weight[base + HW];
+            }
+            if (first) {
+                cache.valid = true;
+                cache.ix = E.ix;
+                cache.jx = E.jx;
+#pragma unroll
+                for (int s = 0; s < kLinPPL; s++) {
+                    cache.tgu[s] = tgu[s];
+                    cache.tgv[s] = tgv[s];
+                    cache.wtu[s] = wtu[s];
+                    cache.wtv[s] = wtv[s];
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                if (!vpx[s]) continue;
+                Lin Ln;
+                lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
+                          (double)tgv[s], (double)wtu[s], (double)wtv[s], Ln);
+                cp[s] += Ln.w[0] * Ln.Jz[0] * Ln.Jz[0] + Ln.w[1] * Ln.Jz[1] * Ln.Jz[1];
+                wp[s] += Ln.w[0] * Ln.r[0] * Ln.Jz[0] + Ln.w[1] * Ln.r[1] * Ln.Jz[1];
+                if (!stereo) {
+                    const double a0 = Ln.w[0] * Ln.Jz[0], a1 = Ln.w[1] * Ln.Jz[1];
+                    double t = 0.0;
+#pragma unroll
+                    for (int n = 0; n < 6; n++)
+                        t += (a0 * Ln.Jj[0][n] + a1 * Ln.Jj[1][n]) * dl[n];
+                    dwp[s] += t;
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            const int px = s * 64 + lane;
+            cwd[wave * kLinPx + px] = dwp[s];
+            L.cw[0][wave][px] = cp[s];
+            L.cw[1][wave][px] = wp[s];
+        }
+        __syncthreads();
+        if (kown < HW) {
+            double dw = 0.0, c = 0.0, w = 0.0;
+#pragma unroll
+            for (int v = 0; v < kLinWaves; v++) {
+                dw += cwd[v * kLinPx + tid];
+                c += L.cw[0][v][tid];
+                w += L.cw[1][v][tid];
+            }
+            // damping_Q_kernel (ep = 1e-7) and depth_update_kernel
+            const double q = 1.0 / (c + 0.2 * eta_px + 1e-7);
+            double own = dsp[0];
+#pragma unroll
+            for (int s = 1; s < kLinPPL; s++)
+                if (s == wave) own = dsp[s];
+            const float dn = (float)(own + q * (w - dw));
+            F.disps[(size_t)K.kf * HW + kown] = dn;
+            L.qs[tid] = (double)dn;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++)
+            if (vpx[s]) dsp[s] = L.qs[s * 64 + lane];
+        __syncthreads();  // qs and xs are the linearization's next
+    } else if (kBs && wait.ready) {  // uniform
         // the pose of each slot: the keyframe's for slot 0 when free, else
         // the jj of the edge that owns it (ordered by the pass's barriers)
         for (int ei = K.e0 + tid; ei < K.e1; ei += kLinWG) {
@@ -1873,7 +1991,7 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
     fz_body<kBs, kLin>(F, L, blockIdx.x, blockIdx.y, FzWait{nullptr});
 }
 
-// One launch per step k >= 2 of the overlapped fused iteration (n <= kSmallN):
+// One launch per step k >= 2 of the overlapped fused iteration (n <= kPanelN):
 // workgroup 0 solves step k - 1 (the system the assembly just wrote), the
 // others run k_ba_fz's work for their (chunk, keyframe), recomputing step
 // k - 1's E rows at F.poses_prev (its poses, copied by the step before)
@@ -1882,13 +2000,19 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
 union FzStepLds {
     FzLds fz;
     SmallLds sv;
+    PanelLds pv;
 };
 
-template <bool kLin>
+// kPanel: the system is solved by the panel solver (n <= kPanelN), else by
+// the register solver (n <= kSmallN)
+template <bool kLin, bool kPanel>
 __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz_step(FzArgs F, SolveArgs A, FzWait wait) {
     __shared__ FzStepLds lds;
     if (blockIdx.x == 0) {
-        solve_small_body(A, lds.sv);
+        if (kPanel)
+            solve_panel_body(A, lds.pv.sm, lds.pv.ok, lds.pv.pose0);
+        else
+            solve_small_body(A, lds.sv);
         // every wave's writes (dx, flags, poses) made visible device-wide
         // before the flag
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -2065,8 +2189,9 @@ struct BaState {
     bool fz = false;
     size_t fz_off[7] = {0};  // kfs, eds, items, dptr, dsrc, deptr, dedges (ints into host)
     DevBuf spart, poses_prev;
-    // overlapped steps (n <= kSmallN): the second pose copy and the step flag
+    // overlapped steps: the second pose copy and the step flag
     DevBuf poses_alt, ready;
+    int cus = 0;  // compute units: the overlapped step's workgroups must all be resident
 };
 
 namespace {
@@ -2303,15 +2428,19 @@ int ba_create(slk_ctx* ctx) {
     ctx->ba = new BaState();
     SLK_TRY(ctx->ba->flags.ensure(4 * sizeof(int)));
     SLK_HIP(hipMemset(ctx->ba->flags.ptr, 0, 4 * sizeof(int)));
+    if (hipDeviceGetAttribute(&ctx->ba->cus, hipDeviceAttributeMultiprocessorCount,
+                              ctx->device) != hipSuccess)
+        return fail(SLK_E_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
     return SLK_OK;
 }
 
 void ba_destroy(slk_ctx* ctx) {
     BaState* s = ctx->ba;
     if (!s) return;
-    DevBuf* bufs[] = {&s->plan_dev, &s->hpart, &s->etot, &s->stot,   &s->E,  &s->Q,
-                      &s->Wv,       &s->S,     &s->S_dbg, &s->b_dbg, &s->dx_dbg, &s->dx,
-                      &s->flags};
+    DevBuf* bufs[] = {&s->plan_dev, &s->hpart,  &s->etot,      &s->stot,      &s->E,
+                      &s->Q,        &s->Wv,     &s->S,         &s->S_dbg,     &s->b_dbg,
+                      &s->dx_dbg,   &s->dx,     &s->flags,     &s->spart,     &s->poses_prev,
+                      &s->poses_alt, &s->ready};
     for (DevBuf* b : bufs) b->release();
     s->stage.release();
     delete s;
@@ -2525,7 +2654,9 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     G.ready = nullptr;
     const SolveArgs A = solve_args(s, plan, I);
     const dim3 grid(s->nch, s->N_kf);
-    if (s->n <= kSmallN) {
+    // one workgroup per CU (their LDS), all resident at once: the waiting
+    // ones then never hold CUs that later linearization workgroups need
+    if (s->n <= kPanelN && 1 + s->nch * s->N_kf <= s->cus) {
         // Overlapped steps: the first linearization (which keeps a copy of the
         // poses it used), then per step the assembly and one launch of the
         // solve beside the next linearization. The pose copies alternate:
@@ -2554,14 +2685,23 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
             SolveArgs Ak = A;
             Ak.poses_prev = nullptr;
             Ak.poses_next = pp[(it + 1) & 1];
+            const bool panel = s->n > kSmallN;
             if (it + 1 < iters) {
                 ProfScope ps(ctx, "ba_fz_step", stream);
-                hipLaunchKernelGGL(k_ba_fz_step<true>, sgrid, dim3(kLinWG), 0, stream, Fk, Ak,
-                                   wait);
+                if (panel)
+                    hipLaunchKernelGGL((k_ba_fz_step<true, true>), sgrid, dim3(kLinWG), 0, stream,
+                                       Fk, Ak, wait);
+                else
+                    hipLaunchKernelGGL((k_ba_fz_step<true, false>), sgrid, dim3(kLinWG), 0,
+                                       stream, Fk, Ak, wait);
             } else {
                 ProfScope ps(ctx, "ba_fz_last", stream);
-                hipLaunchKernelGGL(k_ba_fz_step<false>, sgrid, dim3(kLinWG), 0, stream, Fk, Ak,
-                                   wait);
+                if (panel)
+                    hipLaunchKernelGGL((k_ba_fz_step<false, true>), sgrid, dim3(kLinWG), 0,
+                                       stream, Fk, Ak, wait);
+                else
+                    hipLaunchKernelGGL((k_ba_fz_step<false, false>), sgrid, dim3(kLinWG), 0,
+                                       stream, Fk, Ak, wait);
             }
             SLK_HIP(hipGetLastError());
         }
