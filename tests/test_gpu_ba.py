@@ -239,6 +239,28 @@ def test_lds_solver_sizes(slk, P):
         assert_close_rel(dev.disps(), disps, what=f"disps it {it}")
     assert ctx.ba_status() == slk.SLK_OK
     ctx.close()
+    if P > 20:
+        return
+    # three chained steps as one slk_ba_iterate_n call: the overlapped fused
+    # steps, each solve (the panel solver from n = 66) in one launch with the
+    # next linearization; the oracle's third step after the two above
+    ref = orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"],
+                         p["ii"], p["jj"], 12, 16, p["t0"], p["t1"], 1e-4, 0.1)
+    assert ref["status"] == 0
+    poses, disps = ref["poses"], ref["disps"]
+    dev = Dev(slk, p)
+    ctx = slk.Context(12, 16, max_batch=1, levels=2)
+    ctx.profile_enable(True)
+    d = dev.d
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 3)
+    assert ctx.ba_status() == slk.SLK_OK
+    assert {"ba_fz_step", "ba_fz_last"} <= _path_kernels(ctx)
+    assert norm_rel(dev.poses(), poses) < TOL
+    assert norm_rel(dev.disps(), disps) < TOL
+    assert_close_rel(dev.poses(), poses, what="poses after iterate_n(3)")
+    assert_close_rel(dev.disps(), disps, what="disps after iterate_n(3)")
+    ctx.close()
 
 
 def test_lds_solver_not_spd_late_pivot(slk):
