@@ -1741,6 +1741,127 @@ struct FzWait {
     int* ready;  // null: no wait (the step's dx is known at launch)
 };
 
+// The depth update of the last step when its dx is known at launch (a
+// rejected step leaves the depths as they are): per edge the step's
+// projection dl = dx_j - Adj^T dx_i (lane c < 6 forms component c), then per
+// pixel dw = sum_e g_e . dl_e, g_e = w Jz Jj at the last step's poses and
+// depths (EvT6x1 + depth_update, ba.cuh:762-783); dsp receives the new
+// depths. The first edge of each wave goes to `cache` (with its relative
+// pose at the current poses when want_rel). LDS: cwd, cw0, cw1 [kLinWaves]
+// [kLinPx] and qs [kLinPx] doubles; ends with a barrier.
+__device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int chunk,
+                                             const int (&kpx)[kLinPPL],
+                                             const bool (&vpx)[kLinPPL],
+                                             double (&dsp)[kLinPPL], double eta_px,
+                                             FzCache& cache, bool want_rel, double* cwd,
+                                             double* cw0, double* cw1, double* qs) {
+    const int ri = (K.info >> 8) & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int HW = F.HW;
+    const int kown = chunk * kLinPx + tid;
+    double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
+    const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
+    for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
+        const FzEdge E = F.eds[ei];
+        const bool stereo = E.ix == E.jx;
+        const bool first = ei == K.e0 + wave;  // uniform
+        double tij[3], qij[4];
+        fz_rel(F, true, E.ix, E.jx, tij, qij);
+        if (want_rel && first) {  // the linearization's relative pose of this edge
+            fz_rel(F, false, E.ix, E.jx, cache.tn, cache.qn);
+            cache.rel = true;
+        }
+        double dl[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+        if (!stereo) {
+            if (E.slot >= 0)
+#pragma unroll
+                for (int n = 0; n < 6; n++) dl[n] = (double)F.dx[(E.jx - F.t0) * 6 + n];
+            if (ri) {  // lane c < 6: (Adj^T dx_i)[c] = adj_se3(e_c) . dx_i
+                double u[6], y[6], t = 0.0;
+#pragma unroll
+                for (int m = 0; m < 6; m++) u[m] = m == lane ? 1.0 : 0.0;
+                adj_se3(tij, qij, u, y);
+#pragma unroll
+                for (int m = 0; m < 6; m++) t += y[m] * (double)F.dx[(E.ix - F.t0) * 6 + m];
+#pragma unroll
+                for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
+            }
+        }
+        float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
+            tgu[s] = F.target[base];
+            tgv[s] = F.target[base + HW];
+            wtu[s] = F.weight[base];
+            wtv[s] = F.weight[base + HW];
+        }
+        if (first) {
+            cache.valid = true;
+            cache.ix = E.ix;
+            cache.jx = E.jx;
+#pragma unroll
+            for (int s = 0; s < kLinPPL; s++) {
+                cache.tgu[s] = tgu[s];
+                cache.tgv[s] = tgv[s];
+                cache.wtu[s] = wtu[s];
+                cache.wtv[s] = wtv[s];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kLinPPL; s++) {
+            if (!vpx[s]) continue;
+            Lin Ln;
+            lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
+                      (double)tgv[s], (double)wtu[s], (double)wtv[s], Ln);
+            cp[s] += Ln.w[0] * Ln.Jz[0] * Ln.Jz[0] + Ln.w[1] * Ln.Jz[1] * Ln.Jz[1];
+            wp[s] += Ln.w[0] * Ln.r[0] * Ln.Jz[0] + Ln.w[1] * Ln.r[1] * Ln.Jz[1];
+            if (!stereo) {
+                const double a0 = Ln.w[0] * Ln.Jz[0], a1 = Ln.w[1] * Ln.Jz[1];
+                double t = 0.0;
+#pragma unroll
+                for (int n = 0; n < 6; n++)
+                    t += (a0 * Ln.Jj[0][n] + a1 * Ln.Jj[1][n]) * dl[n];
+                dwp[s] += t;
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        const int px = s * 64 + lane;
+        cwd[wave * kLinPx + px] = dwp[s];
+        cw0[wave * kLinPx + px] = cp[s];
+        cw1[wave * kLinPx + px] = wp[s];
+    }
+    __syncthreads();
+    if (kown < HW) {
+        double dw = 0.0, c = 0.0, w = 0.0;
+#pragma unroll
+        for (int v = 0; v < kLinWaves; v++) {
+            dw += cwd[v * kLinPx + tid];
+            c += cw0[v * kLinPx + tid];
+            w += cw1[v * kLinPx + tid];
+        }
+        // damping_Q_kernel (ep = 1e-7) and depth_update_kernel
+        const double q = 1.0 / (c + 0.2 * eta_px + 1e-7);
+        double own = dsp[0];
+#pragma unroll
+        for (int s = 1; s < kLinPPL; s++)
+            if (s == wave) own = dsp[s];
+        const float dn = (float)(own + q * (w - dw));
+        F.disps[(size_t)K.kf * HW + kown] = dn;
+        qs[tid] = (double)dn;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++)
+        if (vpx[s]) dsp[s] = qs[s * 64 + lane];
+    __syncthreads();  // the caller's next use of this LDS
+}
+
 // k_ba_fz's work for one (pixel chunk, keyframe): with kBs first the depth
 // update of the last step, dz = Q (w - E^T dx) (EvT6x1 + depth_update,
 // ba.cuh:762-783) from that step's E rows, Q and w recomputed at its poses
@@ -1768,6 +1889,9 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
     const int kown = chunk * kLinPx + tid;  // the pixel of the per-pixel steps
     const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
     if (kBs && !wait.ready && F.flags[0] == 0) {  // uniform
+        // (fz_bs_direct's computation, written out here: called as a
+        // function, it changed this kernel's register allocation and cost
+        // 2-6 us per launch)
         // dx is known at launch (a rejected step leaves the depths as they
         // are): per edge the step's projection dl = dx_j - Adj^T dx_i (lane
         // c < 6 forms component c), then per pixel dw = sum_e g_e . dl_e,
@@ -1989,6 +2113,38 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
         for (int t = threadIdx.x; t < (F.t1 - F.t0) * 7; t += kLinWG)
             F.pose_copy[t] = F.poses[F.t0 * 7 + t];
     fz_body<kBs, kLin>(F, L, blockIdx.x, blockIdx.y, FzWait{nullptr});
+}
+
+// The last step's depth update alone (the launch after the final solve of a
+// fused iteration that did not overlap its steps): fz_bs_direct with 26 KB
+// of LDS, so several workgroups share a CU.
+struct FzBsLds {
+    double cwd[kLinWaves * kLinPx];
+    double cw0[kLinWaves * kLinPx];
+    double cw1[kLinWaves * kLinPx];
+    double qs[kLinPx];
+};
+
+__global__ __launch_bounds__(kLinWG) void k_ba_fz_bs(FzArgs F) {
+    __shared__ FzBsLds L;
+    if (F.flags[0] != 0) return;  // uniform: a rejected step leaves the depths
+    const int chunk = blockIdx.x;
+    const FzKf K = F.kfs[blockIdx.y];
+    const int lane = threadIdx.x & 63, HW = F.HW;
+    int kpx[kLinPPL];
+    bool vpx[kLinPPL];
+    double dsp[kLinPPL];
+#pragma unroll
+    for (int s = 0; s < kLinPPL; s++) {
+        kpx[s] = chunk * kLinPx + s * 64 + lane;
+        vpx[s] = kpx[s] < HW;
+        dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
+    }
+    const int kown = chunk * kLinPx + threadIdx.x;
+    const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
+    FzCache cache;
+    cache.valid = cache.rel = false;
+    fz_bs_direct(F, K, chunk, kpx, vpx, dsp, eta_px, cache, false, L.cwd, L.cw0, L.cw1, L.qs);
 }
 
 // One launch per step k >= 2 of the overlapped fused iteration (n <= kPanelN):
@@ -2726,7 +2882,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     }
     {
         ProfScope ps(ctx, "ba_fz_bs", stream);
-        hipLaunchKernelGGL((k_ba_fz<true, false>), grid, dim3(kLinWG), 0, stream, F);
+        hipLaunchKernelGGL(k_ba_fz_bs, grid, dim3(kLinWG), 0, stream, F);
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
