@@ -1430,6 +1430,13 @@ constexpr int kFzMaxT = 3;                             // 16-row tiles of [E; w]
 constexpr int kFzMaxNT = kFzMaxT * (kFzMaxT + 1) / 2;  // tiles (ti <= tj) kept
 constexpr int kFzLd = 16 * kFzMaxT + 9;  // doubles per pixel in LDS (odd: 2-way stores)
 constexpr int kFzMaxDst = 32;            // distinct edges feeding one block of S or b
+constexpr int kFzMaxCodes = 80;          // contributions to one block of S or b
+// A block's assembly record: [0] contributions, [1] distinct edges, then
+// (edge, ii, jj) of each edge at kFzRecEdges, then (code, Schur item) of
+// each contribution, 5 ints, at kFzRecCodes
+constexpr int kFzRecEdges = 2;
+constexpr int kFzRecCodes = kFzRecEdges + 3 * kFzMaxDst;
+constexpr int kFzRecInts = (kFzRecCodes + 5 * kFzMaxCodes + 63) / 64 * 64;
 static_assert(6 * kFzMaxSlots + 1 <= 16 * kFzMaxT, "the slot rows and w fill at most T tiles");
 static_assert(kLinPx == kLinWG && kLinPx == 256, "one pixel per thread in the per-pixel steps");
 
@@ -2182,16 +2189,13 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz_step(FzArgs F, SolveArgs A,
 }
 
 struct FzAsmArgs {
-    const int4* items;  // {kc, s1, s2 or -1 (the w column), w row}
-    const int* dptr;    // [P*P + P + 1] contribution codes of each block / segment
-    const int* dsrc;
-    const int* deptr;   // [P*P + P + 1] the distinct edges those codes refer to
-    const int* dedges;
+    // [P*P + P][kFzRecInts] assembly record of each block / segment: its
+    // contribution codes (with the Schur item {kc, s1, s2 or -1 (the w
+    // column), w row} of each code of type 1) and its distinct edges
+    const int* rec;
     const double* hpart;
     const double* spart;
     const float* poses;
-    const int* ii;
-    const int* jj;
     int nch, P, n;
     float lm, ep;
     double* S;  // [n][n] assembled system (after damping)
@@ -2225,6 +2229,7 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     __shared__ double ah[kFzMaxDst][36];     // Adj Hjj
     __shared__ double et[kFzMaxDst][kNT];    // Hii, Hij, Hjj, vi, vj
     __shared__ double red[kAsmSlices][36];
+    __shared__ int rec[kFzRecInts];
     const int g = blockIdx.x, tid = threadIdx.x;
     const int sl = tid / 36, ent = tid - sl * 36;
     const int P = A.P, n = A.n;
@@ -2232,18 +2237,21 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     const bool isS = g < P * P;
     const bool act = sl < kAsmSlices && (isS || ent < 6);
     const int r = ent / 6, c = ent - (ent / 6) * 6;
-    const int q0 = A.dptr[g], q1 = A.dptr[g + 1];
-    const int d0 = A.deptr[g], nd = A.deptr[g + 1] - d0;
+    // the block's record in one round of loads
+    for (int t = tid; t < kFzRecInts; t += 256) rec[t] = A.rec[(size_t)g * kFzRecInts + t];
+    __syncthreads();
+    const int nq = rec[0], nd = rec[1];
+    const int* redge = rec + kFzRecEdges;  // (edge, ii, jj)
+    const int* rcode = rec + kFzRecCodes;  // (code, Schur item)
     // (1) chunk sums of the edges' partials, and the Adj columns
     for (int t = tid; t < nd * kNJ; t += 256) {
         const int le = t / kNJ, v = t - (t / kNJ) * kNJ;
-        tot[le][v] = sum_strided(A.hpart + (size_t)A.dedges[d0 + le] * A.nch * kNJ + v, kNJ, A.nch);
+        tot[le][v] = sum_strided(A.hpart + (size_t)redge[3 * le] * A.nch * kNJ + v, kNJ, A.nch);
     }
     for (int t = tid; t < nd * 6; t += 256) {
         const int le = t / 6, cc = t - (t / 6) * 6;
-        const int e = A.dedges[d0 + le];
         double tij[3], qij[4], u[6], y[6];
-        edge_rel(A.poses, A.ii[e], A.jj[e], tij, qij);
+        edge_rel(A.poses, redge[3 * le + 1], redge[3 * le + 2], tij, qij);
 #pragma unroll
         for (int m = 0; m < 6; m++) u[m] = m == cc ? 1.0 : 0.0;
         adj_se3(tij, qij, u, y);  // column cc (se3.cuh:28-41)
@@ -2253,11 +2261,11 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     // the Schur items (thread-private; their loads overlap the above)
     double s = 0.0;
     if (act) {
-        for (int q = q0 + sl; q < q1; q += kAsmSlices) {
-            const int cd = A.dsrc[q];
-            if (code_type(cd) != 1) continue;
-            const int4 it = A.items[code_val(cd)];
-            s -= isS ? fz_z(A, it.x, 6 * it.y + r, 6 * it.z + c) : fz_z(A, it.x, 6 * it.y + ent, it.w);
+        for (int q = sl; q < nq; q += kAsmSlices) {
+            const int* rc = rcode + 5 * q;
+            if (code_type(rc[0]) != 1) continue;
+            s -= isS ? fz_z(A, rc[1], 6 * rc[2] + r, 6 * rc[3] + c)
+                     : fz_z(A, rc[1], 6 * rc[2] + ent, rc[4]);
         }
     }
     __syncthreads();
@@ -2291,8 +2299,8 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     }
     __syncthreads();
     if (act) {
-        for (int q = q0 + sl; q < q1; q += kAsmSlices) {
-            const int cd = A.dsrc[q];
+        for (int q = sl; q < nq; q += kAsmSlices) {
+            const int cd = rcode[5 * q];
             if (code_type(cd) != 0) continue;
             const int v = code_val(cd);
             if (isS) {
@@ -2343,7 +2351,7 @@ struct BaState {
     bool lin_by_wave = false;  // no keyframe has two edges to the same free pose
     // fused path (every keyframe with at most kFzMaxSlots E rows)
     bool fz = false;
-    size_t fz_off[7] = {0};  // kfs, eds, items, dptr, dsrc, deptr, dedges (ints into host)
+    size_t fz_off[3] = {0};  // kfs, eds, assembly records (ints into host)
     DevBuf spart, poses_prev;
     // overlapped steps: the second pose copy and the step flag
     DevBuf poses_alt, ready;
@@ -2425,16 +2433,33 @@ void build_fz(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, i
         if (va) codes[P * P + a].push_back(code(0, local(P * P + a, e) * 2 + 0));
         if (vb) codes[P * P + b].push_back(code(0, local(P * P + b, e) * 2 + 1));
     }
-    std::vector<int> dptr(1, 0), dsrc, deptr(1, 0), dflat;
+    // one record of kFzRecInts per block of S / segment of b; the records of
+    // every block, empty ones included, stay under 4 MB (P <= 42; frontend
+    // windows have P ~ 10-20, and larger graphs exceed kFzMaxSlots anyway)
+    if ((size_t)ND * kFzRecInts > ((size_t)1 << 20)) return;
+    std::vector<int> rec((size_t)ND * kFzRecInts, 0);
     for (int d = 0; d < ND; d++) {
-        if ((int)dedges[d].size() > kFzMaxDst) return;
-        dsrc.insert(dsrc.end(), codes[d].begin(), codes[d].end());
-        dptr.push_back((int)dsrc.size());
-        dflat.insert(dflat.end(), dedges[d].begin(), dedges[d].end());
-        deptr.push_back((int)dflat.size());
+        const int nd = (int)dedges[d].size(), nq = (int)codes[d].size();
+        if (nd > kFzMaxDst || nq > kFzMaxCodes) return;
+        int* r = rec.data() + (size_t)d * kFzRecInts;
+        r[0] = nq;
+        r[1] = nd;
+        for (int le = 0; le < nd; le++) {
+            const int e = dedges[d][le];
+            r[kFzRecEdges + 3 * le] = e;
+            r[kFzRecEdges + 3 * le + 1] = ii[e];
+            r[kFzRecEdges + 3 * le + 2] = jj[e];
+        }
+        for (int q = 0; q < nq; q++) {
+            const int cd = codes[d][q];
+            int* c = r + kFzRecCodes + 5 * q;
+            c[0] = cd;
+            if (code_type(cd) == 1)
+                for (int k = 0; k < 4; k++) c[1 + k] = items[(size_t)code_val(cd) * 4 + k];
+        }
     }
-    const std::vector<int>* parts[7] = {&kfs, &eds, &items, &dptr, &dsrc, &deptr, &dflat};
-    for (int i = 0; i < 7; i++) {
+    const std::vector<int>* parts[3] = {&kfs, &eds, &rec};
+    for (int i = 0; i < 3; i++) {
         while (s->host.size() % 4) s->host.push_back(0);
         s->fz_off[i] = s->host.size();
         s->host.insert(s->host.end(), parts[i]->begin(), parts[i]->end());
@@ -2790,16 +2815,10 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     F.t0 = I.t0;
     F.t1 = I.t1;
     FzAsmArgs G;
-    G.items = reinterpret_cast<const int4*>(base + s->fz_off[2]);
-    G.dptr = base + s->fz_off[3];
-    G.dsrc = base + s->fz_off[4];
-    G.deptr = base + s->fz_off[5];
-    G.dedges = base + s->fz_off[6];
+    G.rec = base + s->fz_off[2];
     G.hpart = s->hpart.as<double>();
     G.spart = s->spart.as<double>();
     G.poses = I.poses;
-    G.ii = I.ii_gpu;
-    G.jj = I.jj_gpu;
     G.nch = s->nch;
     G.P = s->P;
     G.n = s->n;
