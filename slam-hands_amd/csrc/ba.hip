@@ -169,14 +169,15 @@ __device__ __forceinline__ void edge_rel(const float* poses, int ix, int jx, dou
 
 // p[0] + p[stride] + ... + p[(n - 1) stride], added in that order, with the
 // loads of sixteen terms in flight at a time (a plain loop waits for each).
+template <int kB = 16>
 __device__ __forceinline__ double sum_strided(const double* __restrict__ p, size_t stride, int n) {
     double t = 0.0;
-    for (int c = 0; c < n; c += 16) {
-        double v[16];
+    for (int c = 0; c < n; c += kB) {
+        double v[kB];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = c + u < n ? p[(size_t)(c + u) * stride] : 0.0;
+        for (int u = 0; u < kB; u++) v[u] = c + u < n ? p[(size_t)(c + u) * stride] : 0.0;
 #pragma unroll
-        for (int u = 0; u < 16; u++) t += v[u];
+        for (int u = 0; u < kB; u++) t += v[u];
     }
     return t;
 }
@@ -1438,7 +1439,15 @@ constexpr int kFzRecEdges = 2;
 constexpr int kFzRecCodes = kFzRecEdges + 3 * kFzMaxDst;
 constexpr int kFzRecInts = (kFzRecCodes + 5 * kFzMaxCodes + 63) / 64 * 64;
 static_assert(6 * kFzMaxSlots + 1 <= 16 * kFzMaxT, "the slot rows and w fill at most T tiles");
-static_assert(kLinPx == kLinWG && kLinPx == 256, "one pixel per thread in the per-pixel steps");
+// pixels of a fused workgroup's chunk: half its threads take one pixel each
+// in the per-pixel steps, and each wave's lanes hold kFzPPL pixels
+constexpr int kFzPx = 192;
+constexpr int kFzPPL = kFzPx / 64;
+// fused workgroups resident per CU (their LDS takes more than half of a CU's
+// 160 KB)
+constexpr int kFzWgPerCu = 1;
+static_assert(kFzPx <= kLinWG && kFzPx % 64 == 0 && kFzPx % 16 == 0, "chunk shape");
+static_assert((3 * kFzMaxNT + kFzMaxNT) * 256 <= kFzPx * kFzLd, "the waves' MFMA tiles fit in xs");
 
 struct FzKf {
     int kf, e0, e1, info;  // edges e0..e1 of the edge table; info = nslot | ri << 8 | T << 12
@@ -1515,8 +1524,8 @@ __device__ __forceinline__ void fz_schur_tiles(double* xs, const double* qs, int
     for (int t = 0; t < NT; t++) z[t] = fz_d4{0.0, 0.0, 0.0, 0.0};
     const int i16 = lane & 15, kg = lane >> 4;
 #pragma unroll
-    for (int ks = 0; ks < 16; ks++) {
-        const int kp = wave * 64 + ks * 4 + kg;
+    for (int ks = 0; ks < kFzPx / 16; ks++) {
+        const int kp = wave * (kFzPx / 4) + ks * 4 + kg;
         const double q = qs[kp];
         const double* xr = xs + kp * kFzLd + i16;
         double a[T], b[T];
@@ -1541,9 +1550,9 @@ __device__ __forceinline__ void fz_schur_tiles(double* xs, const double* qs, int
 
 // LDS of a fused linearization workgroup.
 struct FzLds {
-    double xs[kLinPx * kFzLd];        // [pixel][row]; then the MFMA partials
-    double cw[2][kLinWaves][kLinPx];  // per-wave sums (C, w)
-    double qs[kLinPx];
+    double xs[kFzPx * kFzLd];        // [pixel][row]; then the MFMA partials
+    double cw[2][kLinWaves][kFzPx];  // per-wave sums (C, w)
+    double qs[kFzPx];
     double dxr[6 * kFzMaxSlots];  // the last step's dx, by slot row
     int spose[kFzMaxSlots];       // the pose of each slot
     int wait_state;
@@ -1554,7 +1563,7 @@ struct FzLds {
 struct FzCache {
     bool valid, rel;
     int ix, jx;
-    float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+    float tgu[kFzPPL], tgv[kFzPPL], wtu[kFzPPL], wtv[kFzPPL];
     double tn[3], qn[4];
 };
 
@@ -1568,8 +1577,8 @@ struct FzCache {
 // Ends with a barrier.
 template <bool kPrev>
 __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L, int chunk,
-                                        const int (&kpx)[kLinPPL], const bool (&vpx)[kLinPPL],
-                                        const double (&dsp)[kLinPPL], double eta_px,
+                                        const int (&kpx)[kFzPPL], const bool (&vpx)[kFzPPL],
+                                        const double (&dsp)[kFzPPL], double eta_px,
                                         FzCache& cache, bool coherent = false) {
     const int nslot = K.info & 0xff, ri = (K.info >> 8) & 1, T = K.info >> 12;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1577,16 +1586,16 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
     const int HW = F.HW;
     const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
     double* xs = L.xs;
-    {
+    if (tid < kFzPx) {
         // rows past the slots and w (and every row of a pixel past HW) are zero
-        const int k = chunk * kLinPx + tid;
+        const int k = chunk * kFzPx + tid;
         double* xr = xs + tid * kFzLd;
         for (int r = k < HW ? 6 * nslot + 1 : 0; r < 16 * T; r++) xr[r] = 0.0;
     }
-    double er[kLinPPL][6];  // this lane's pixels: -sum Adj g over the wave's edges
-    double cp[kLinPPL], wp[kLinPPL];
+    double er[kFzPPL][6];  // this lane's pixels: -sum Adj g over the wave's edges
+    double cp[kFzPPL], wp[kFzPPL];
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
+    for (int s = 0; s < kFzPPL; s++) {
         cp[s] = wp[s] = 0.0;
 #pragma unroll
         for (int n = 0; n < 6; n++) er[s][n] = 0.0;
@@ -1604,10 +1613,10 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
         } else {
             fz_rel(F, kPrev, E.ix, E.jx, tij, qij, coherent);
         }
-        float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+        float tgu[kFzPPL], tgv[kFzPPL], wtu[kFzPPL], wtv[kFzPPL];
         if (!kPrev && first && cache.valid) {
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
+            for (int s = 0; s < kFzPPL; s++) {
                 tgu[s] = cache.tgu[s];
                 tgv[s] = cache.tgv[s];
                 wtu[s] = cache.wtu[s];
@@ -1615,7 +1624,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
+            for (int s = 0; s < kFzPPL; s++) {
                 const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
                 tgu[s] = F.target[base];
                 tgv[s] = F.target[base + HW];
@@ -1627,7 +1636,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
                 cache.ix = E.ix;
                 cache.jx = E.jx;
 #pragma unroll
-                for (int s = 0; s < kLinPPL; s++) {
+                for (int s = 0; s < kFzPPL; s++) {
                     cache.tgu[s] = tgu[s];
                     cache.tgv[s] = tgv[s];
                     cache.wtu[s] = wtu[s];
@@ -1639,7 +1648,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
 #pragma unroll
         for (int n = 0; n < kNJ; n++) acc[n] = 0.0;
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
+        for (int s = 0; s < kFzPPL; s++) {
             if (!vpx[s]) continue;
             const int px = s * 64 + lane;
             Lin Ln;
@@ -1676,7 +1685,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
         }
     }
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
+    for (int s = 0; s < kFzPPL; s++) {
         const int px = s * 64 + lane;
         L.cw[0][wave][px] = cp[s];
         L.cw[1][wave][px] = wp[s];
@@ -1689,7 +1698,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
     const bool er_cols = T <= 2;  // uniform
     if (ri && er_cols) {
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
+        for (int s = 0; s < kFzPPL; s++) {
             double* xr = xs + (s * 64 + lane) * kFzLd + kErCol + 6 * wave;
 #pragma unroll
             for (int n = 0; n < 6; n++) xr[n] = er[s][n];
@@ -1699,7 +1708,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
             __syncthreads();
             if (wave == v) {
 #pragma unroll
-                for (int s = 0; s < kLinPPL; s++) {
+                for (int s = 0; s < kFzPPL; s++) {
                     if (!vpx[s]) continue;
                     double* xr = xs + (s * 64 + lane) * kFzLd;
 #pragma unroll
@@ -1709,8 +1718,8 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
         }
     }
     __syncthreads();
-    {
-        const int k = chunk * kLinPx + tid;
+    if (tid < kFzPx) {
+        const int k = chunk * kFzPx + tid;
         double q = 0.0;
         double* xr = xs + tid * kFzLd;
         if (k < HW) {
@@ -1755,21 +1764,22 @@ struct FzWait {
 // depths (EvT6x1 + depth_update, ba.cuh:762-783); dsp receives the new
 // depths. The first edge of each wave goes to `cache` (with its relative
 // pose at the current poses when want_rel). LDS: cwd, cw0, cw1 [kLinWaves]
-// [kLinPx] and qs [kLinPx] doubles; ends with a barrier.
+// [kFzPx] and qs [kFzPx] doubles; ends with a barrier.
 __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int chunk,
-                                             const int (&kpx)[kLinPPL],
-                                             const bool (&vpx)[kLinPPL],
-                                             double (&dsp)[kLinPPL], double eta_px,
+                                             const int (&kpx)[kFzPPL],
+                                             const bool (&vpx)[kFzPPL],
+                                             double (&dsp)[kFzPPL], double eta_px,
                                              FzCache& cache, bool want_rel, double* cwd,
                                              double* cw0, double* cw1, double* qs) {
     const int ri = (K.info >> 8) & 1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int HW = F.HW;
-    const int kown = chunk * kLinPx + tid;
-    double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
+    const int kown = chunk * kFzPx + tid;
+    const bool mine = tid < kFzPx && kown < HW;  // this thread's pixel, if any
+    double dwp[kFzPPL], cp[kFzPPL], wp[kFzPPL];
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
+    for (int s = 0; s < kFzPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
     const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
     for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
         const FzEdge E = F.eds[ei];
@@ -1797,9 +1807,9 @@ __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int
                 for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
             }
         }
-        float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+        float tgu[kFzPPL], tgv[kFzPPL], wtu[kFzPPL], wtv[kFzPPL];
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
+        for (int s = 0; s < kFzPPL; s++) {
             const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
             tgu[s] = F.target[base];
             tgv[s] = F.target[base + HW];
@@ -1811,7 +1821,7 @@ __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int
             cache.ix = E.ix;
             cache.jx = E.jx;
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
+            for (int s = 0; s < kFzPPL; s++) {
                 cache.tgu[s] = tgu[s];
                 cache.tgv[s] = tgv[s];
                 cache.wtu[s] = wtu[s];
@@ -1819,7 +1829,7 @@ __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int
             }
         }
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
+        for (int s = 0; s < kFzPPL; s++) {
             if (!vpx[s]) continue;
             Lin Ln;
             lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
@@ -1837,26 +1847,26 @@ __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int
         }
     }
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
+    for (int s = 0; s < kFzPPL; s++) {
         const int px = s * 64 + lane;
-        cwd[wave * kLinPx + px] = dwp[s];
-        cw0[wave * kLinPx + px] = cp[s];
-        cw1[wave * kLinPx + px] = wp[s];
+        cwd[wave * kFzPx + px] = dwp[s];
+        cw0[wave * kFzPx + px] = cp[s];
+        cw1[wave * kFzPx + px] = wp[s];
     }
     __syncthreads();
-    if (kown < HW) {
+    if (mine) {
         double dw = 0.0, c = 0.0, w = 0.0;
 #pragma unroll
         for (int v = 0; v < kLinWaves; v++) {
-            dw += cwd[v * kLinPx + tid];
-            c += cw0[v * kLinPx + tid];
-            w += cw1[v * kLinPx + tid];
+            dw += cwd[v * kFzPx + tid];
+            c += cw0[v * kFzPx + tid];
+            w += cw1[v * kFzPx + tid];
         }
         // damping_Q_kernel (ep = 1e-7) and depth_update_kernel
         const double q = 1.0 / (c + 0.2 * eta_px + 1e-7);
         double own = dsp[0];
 #pragma unroll
-        for (int s = 1; s < kLinPPL; s++)
+        for (int s = 1; s < kFzPPL; s++)
             if (s == wave) own = dsp[s];
         const float dn = (float)(own + q * (w - dw));
         F.disps[(size_t)K.kf * HW + kown] = dn;
@@ -1864,7 +1874,7 @@ __device__ __forceinline__ void fz_bs_direct(const FzArgs& F, const FzKf& K, int
     }
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++)
+    for (int s = 0; s < kFzPPL; s++)
         if (vpx[s]) dsp[s] = qs[s * 64 + lane];
     __syncthreads();  // the caller's next use of this LDS
 }
@@ -1882,19 +1892,20 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int HW = F.HW;
-    int kpx[kLinPPL];
-    bool vpx[kLinPPL];
-    double dsp[kLinPPL];
+    int kpx[kFzPPL];
+    bool vpx[kFzPPL];
+    double dsp[kFzPPL];
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
-        kpx[s] = chunk * kLinPx + s * 64 + lane;
+    for (int s = 0; s < kFzPPL; s++) {
+        kpx[s] = chunk * kFzPx + s * 64 + lane;
         vpx[s] = kpx[s] < HW;
         dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
     }
     FzCache cache;
     cache.valid = cache.rel = false;
-    const int kown = chunk * kLinPx + tid;  // the pixel of the per-pixel steps
-    const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
+    const int kown = chunk * kFzPx + tid;  // the pixel of the per-pixel steps
+    const bool mine = tid < kFzPx && kown < HW;
+    const double eta_px = mine ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
     if (kBs && !wait.ready && F.flags[0] == 0) {  // uniform
         // (fz_bs_direct's computation, written out here: called as a
         // function, it changed this kernel's register allocation and cost
@@ -1903,10 +1914,10 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
         // are): per edge the step's projection dl = dx_j - Adj^T dx_i (lane
         // c < 6 forms component c), then per pixel dw = sum_e g_e . dl_e,
         // g_e = w Jz Jj at the last step's poses and depths
-        double* cwd = L.xs;  // [kLinWaves][kLinPx] per-wave sums of dw
-        double dwp[kLinPPL], cp[kLinPPL], wp[kLinPPL];
+        double* cwd = L.xs;  // [kLinWaves][kFzPx] per-wave sums of dw
+        double dwp[kFzPPL], cp[kFzPPL], wp[kFzPPL];
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
+        for (int s = 0; s < kFzPPL; s++) dwp[s] = cp[s] = wp[s] = 0.0;
         const double fx = F.intr[0], fy = F.intr[1], cx = F.intr[2], cy = F.intr[3];
         for (int ei = K.e0 + wave; ei < K.e1; ei += kLinWaves) {
             const FzEdge E = F.eds[ei];
@@ -1934,9 +1945,9 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
                     for (int c = 0; c < 6; c++) dl[c] -= __shfl(t, c);
                 }
             }
-            float tgu[kLinPPL], tgv[kLinPPL], wtu[kLinPPL], wtv[kLinPPL];
+            float tgu[kFzPPL], tgv[kFzPPL], wtu[kFzPPL], wtv[kFzPPL];
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
+            for (int s = 0; s < kFzPPL; s++) {
                 const size_t base = (size_t)E.e * 2 * HW + (vpx[s] ? kpx[s] : 0);
                 tgu[s] = F.target[base];
                 tgv[s] = F.target[base + HW];
@@ -1948,7 +1959,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
                 cache.ix = E.ix;
                 cache.jx = E.jx;
 #pragma unroll
-                for (int s = 0; s < kLinPPL; s++) {
+                for (int s = 0; s < kFzPPL; s++) {
                     cache.tgu[s] = tgu[s];
                     cache.tgv[s] = tgv[s];
                     cache.wtu[s] = wtu[s];
@@ -1956,7 +1967,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
                 }
             }
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++) {
+            for (int s = 0; s < kFzPPL; s++) {
                 if (!vpx[s]) continue;
                 Lin Ln;
                 lin_pixel(tij, qij, fx, fy, cx, cy, kpx[s], F.W, dsp[s], (double)tgu[s],
@@ -1974,18 +1985,18 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             }
         }
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++) {
+        for (int s = 0; s < kFzPPL; s++) {
             const int px = s * 64 + lane;
-            cwd[wave * kLinPx + px] = dwp[s];
+            cwd[wave * kFzPx + px] = dwp[s];
             L.cw[0][wave][px] = cp[s];
             L.cw[1][wave][px] = wp[s];
         }
         __syncthreads();
-        if (kown < HW) {
+        if (mine) {
             double dw = 0.0, c = 0.0, w = 0.0;
 #pragma unroll
             for (int v = 0; v < kLinWaves; v++) {
-                dw += cwd[v * kLinPx + tid];
+                dw += cwd[v * kFzPx + tid];
                 c += L.cw[0][v][tid];
                 w += L.cw[1][v][tid];
             }
@@ -1993,7 +2004,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             const double q = 1.0 / (c + 0.2 * eta_px + 1e-7);
             double own = dsp[0];
 #pragma unroll
-            for (int s = 1; s < kLinPPL; s++)
+            for (int s = 1; s < kFzPPL; s++)
                 if (s == wave) own = dsp[s];
             const float dn = (float)(own + q * (w - dw));
             F.disps[(size_t)K.kf * HW + kown] = dn;
@@ -2001,7 +2012,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
         }
         __syncthreads();
 #pragma unroll
-        for (int s = 0; s < kLinPPL; s++)
+        for (int s = 0; s < kFzPPL; s++)
             if (vpx[s]) dsp[s] = L.qs[s * 64 + lane];
         __syncthreads();  // qs and xs are the linearization's next
     } else if (kBs && wait.ready) {  // uniform
@@ -2075,9 +2086,9 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
         if (ok) {  // uniform
             double own = dsp[0];  // the depth of pixel kown (lane's pixel of s = wave)
 #pragma unroll
-            for (int s = 1; s < kLinPPL; s++)
+            for (int s = 1; s < kFzPPL; s++)
                 if (s == wave) own = dsp[s];
-            if (kown < HW) {
+            if (mine) {
                 const double* xr = L.xs + tid * kFzLd;
                 double dw = 0.0;
                 for (int sl = 0; sl < nslot; sl++)
@@ -2089,7 +2100,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             }
             __syncthreads();
 #pragma unroll
-            for (int s = 0; s < kLinPPL; s++)
+            for (int s = 0; s < kFzPPL; s++)
                 if (vpx[s]) dsp[s] = L.cw[0][0][s * 64 + lane];
         }
     }
@@ -2114,7 +2125,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
 }
 
 template <bool kBs, bool kLin>
-__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
+__global__ __launch_bounds__(kLinWG, kFzWgPerCu) void k_ba_fz(FzArgs F) {
     __shared__ FzLds L;
     if (!kBs && F.pose_copy && blockIdx.x == 0 && blockIdx.y == 0)
         for (int t = threadIdx.x; t < (F.t1 - F.t0) * 7; t += kLinWG)
@@ -2126,10 +2137,10 @@ __global__ __launch_bounds__(kLinWG, 1) void k_ba_fz(FzArgs F) {
 // fused iteration that did not overlap its steps): fz_bs_direct with 26 KB
 // of LDS, so several workgroups share a CU.
 struct FzBsLds {
-    double cwd[kLinWaves * kLinPx];
-    double cw0[kLinWaves * kLinPx];
-    double cw1[kLinWaves * kLinPx];
-    double qs[kLinPx];
+    double cwd[kLinWaves * kFzPx];
+    double cw0[kLinWaves * kFzPx];
+    double cw1[kLinWaves * kFzPx];
+    double qs[kFzPx];
 };
 
 __global__ __launch_bounds__(kLinWG) void k_ba_fz_bs(FzArgs F) {
@@ -2138,17 +2149,18 @@ __global__ __launch_bounds__(kLinWG) void k_ba_fz_bs(FzArgs F) {
     const int chunk = blockIdx.x;
     const FzKf K = F.kfs[blockIdx.y];
     const int lane = threadIdx.x & 63, HW = F.HW;
-    int kpx[kLinPPL];
-    bool vpx[kLinPPL];
-    double dsp[kLinPPL];
+    int kpx[kFzPPL];
+    bool vpx[kFzPPL];
+    double dsp[kFzPPL];
 #pragma unroll
-    for (int s = 0; s < kLinPPL; s++) {
-        kpx[s] = chunk * kLinPx + s * 64 + lane;
+    for (int s = 0; s < kFzPPL; s++) {
+        kpx[s] = chunk * kFzPx + s * 64 + lane;
         vpx[s] = kpx[s] < HW;
         dsp[s] = vpx[s] ? (double)F.disps[(size_t)K.kf * HW + kpx[s]] : 1.0;
     }
-    const int kown = chunk * kLinPx + threadIdx.x;
-    const double eta_px = kown < HW ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
+    const int kown = chunk * kFzPx + threadIdx.x;
+    const bool mine = threadIdx.x < kFzPx && kown < HW;
+    const double eta_px = mine ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
     FzCache cache;
     cache.valid = cache.rel = false;
     fz_bs_direct(F, K, chunk, kpx, vpx, dsp, eta_px, cache, false, L.cwd, L.cw0, L.cw1, L.qs);
@@ -2165,13 +2177,17 @@ union FzStepLds {
     SmallLds sv;
     PanelLds pv;
 };
+static_assert(kFzWgPerCu * sizeof(FzStepLds) <= 160 * 1024, "kFzWgPerCu step workgroups per CU");
 
 // kPanel: the system is solved by the panel solver (n <= kPanelN), else by
 // the register solver (n <= kSmallN)
 template <bool kLin, bool kPanel>
-__global__ __launch_bounds__(kLinWG, 1) void k_ba_fz_step(FzArgs F, SolveArgs A, FzWait wait) {
+__global__ __launch_bounds__(kLinWG, kFzWgPerCu) void k_ba_fz_step(FzArgs F, SolveArgs A, FzWait wait) {
     __shared__ FzStepLds lds;
     if (blockIdx.x == 0) {
+        // the solve is the launch's spine; a linearization workgroup may share
+        // its CU, so its waves issue first
+        __builtin_amdgcn_s_setprio(3);
         if (kPanel)
             solve_panel_body(A, lds.pv.sm, lds.pv.ok, lds.pv.pose0);
         else
@@ -2212,7 +2228,7 @@ __device__ __forceinline__ double fz_z(const FzAsmArgs& A, int kc, int row, int 
     const int th = hi >> 4, tl = lo >> 4;
     const int i = lo & 15, j = hi & 15;
     const size_t idx = (size_t)(th * (th + 1) / 2 + tl) * 256 + ((i & 3) * 16 + j) * 4 + (i >> 2);
-    return sum_strided(A.spart + (size_t)kc * A.nch * kFzMaxNT * 256 + idx, kFzMaxNT * 256, A.nch);
+    return sum_strided<32>(A.spart + (size_t)kc * A.nch * kFzMaxNT * 256 + idx, kFzMaxNT * 256, A.nch);
 }
 
 // One workgroup per 6x6 block (a, b) of S (P*P) and per 6-entry segment of b
@@ -2246,7 +2262,7 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     // (1) chunk sums of the edges' partials, and the Adj columns
     for (int t = tid; t < nd * kNJ; t += 256) {
         const int le = t / kNJ, v = t - (t / kNJ) * kNJ;
-        tot[le][v] = sum_strided(A.hpart + (size_t)redge[3 * le] * A.nch * kNJ + v, kNJ, A.nch);
+        tot[le][v] = sum_strided<32>(A.hpart + (size_t)redge[3 * le] * A.nch * kNJ + v, kNJ, A.nch);
     }
     for (int t = tid; t < nd * 6; t += 256) {
         const int le = t / 6, cc = t - (t / 6) * 6;
@@ -2600,6 +2616,7 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
         s->host.push_back(0);  // keeps every array non-empty
     }
     build_fz(s, ii, jj, M, t0, t1, motion_only, kf_list, kf_eptr, kf_eidx);
+    if (s->fz) s->nch = (HW + kFzPx - 1) / kFzPx;  // the fused kernels' chunks
     return SLK_OK;
 }
 
@@ -2829,9 +2846,9 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     G.ready = nullptr;
     const SolveArgs A = solve_args(s, plan, I);
     const dim3 grid(s->nch, s->N_kf);
-    // one workgroup per CU (their LDS), all resident at once: the waiting
-    // ones then never hold CUs that later linearization workgroups need
-    if (s->n <= kPanelN && 1 + s->nch * s->N_kf <= s->cus) {
+    // all workgroups resident at once (kFzWgPerCu per CU): the waiting ones
+    // then never hold CUs that later linearization workgroups need
+    if (s->n <= kPanelN && 1 + s->nch * s->N_kf <= kFzWgPerCu * s->cus) {
         // Overlapped steps: the first linearization (which keeps a copy of the
         // poses it used), then per step the assembly and one launch of the
         // solve beside the next linearization. The pose copies alternate:
