@@ -109,7 +109,10 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // zeroes the tile counters of k_corr_split_win, which runs after this on the
 // same stream. These workgroups run in the launch of k_feat_prep, beside the
 // feature preparation they do not depend on.
-constexpr int kMaskThreads = 256;
+constexpr int kMaskThreads = 512;
+constexpr int kMaskWaves = kMaskThreads / 64;
+// threads of every workgroup of the k_feat_prep launch
+constexpr int kFeatThreads = kMaskThreads;
 // the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
 // which a tile-mask workgroup uses for its bitmap and sorted pixel indices
 constexpr int kPrepRows = 8, kPrepCols = 64;
@@ -217,7 +220,7 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // the slot), writes its pixel and coordinates there, and marks the target
 // tiles of its windows in the row of its source tile (masks formed in the
 // histogram pass when the quarter stays in registers). Writes ord[0][q] =
-// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * 4 * kSortBuckets ints. A map with
+// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * kMaskWaves * kSortBuckets ints (or is null: no room). A map with
 // more rows than that is not sorted: returns false, and neither ord nor the
 // bitmap is written.
 constexpr int kSortBuckets = 256;
@@ -238,22 +241,22 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
                               unsigned* bits, int ntiles, const unsigned long long* tab) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int HW = g.HW, nb = g.h[0] + 9;
-    if (nb > kSortBuckets) return false;
+    if (nb > kSortBuckets || !lds) return false;
     float* oxy = reinterpret_cast<float*>(ord + HW);
     const int nbits = 32 - __builtin_clz(nb - 1);
     const unsigned long long below = (1ull << lane) - 1ull;
-    int* hist = lds;                    // [4 waves][kSortBuckets]
-    int* pos = lds + 4 * kSortBuckets;  // [4 waves][kSortBuckets]: next sorted slot
-    for (int i = tid; i < 4 * kSortBuckets; i += kMaskThreads) hist[i] = 0;
+    int* hist = lds;                             // [kMaskWaves][kSortBuckets]
+    int* pos = lds + kMaskWaves * kSortBuckets;  // [kMaskWaves][kSortBuckets]: next slot
+    for (int i = tid; i < kMaskWaves * kSortBuckets; i += kMaskThreads) hist[i] = 0;
     __syncthreads();  // also orders the caller's clearing of the bitmap
-    const int quarter = (HW + 3) / 4;
-    const int q0 = std::min(HW, wv * quarter), q1 = std::min(HW, q0 + quarter);
+    const int part = (HW + kMaskWaves - 1) / kMaskWaves;  // pixels of each wave
+    const int q0 = std::min(HW, wv * part), q1 = std::min(HW, q0 + part);
     auto key_of = [&](float y) {
         const int oy = floor_clamped(y) - 3;
         return std::min(std::max(oy, -8), g.h[0]) + 8;
     };
     // the coordinates of kG chunks are loaded before the first is used; when
-    // the quarter is one such group they stay in registers for the scatter
+    // a wave's pixels are one such group they stay in registers for the scatter
     constexpr int kG = 12;
     float xv[kG], yv[kG];
     auto load = [&](int pg) {
@@ -280,27 +283,32 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
     }
     __syncthreads();
     {
-        // thread b: bucket b's total, its exclusive prefix over the buckets
-        // (a wave scan, then the totals of the waves below), and each wave's
-        // first slot in it
+        // thread b < kSortBuckets: bucket b's total, its exclusive prefix over
+        // the buckets (a wave scan, then the totals of the waves below), and
+        // each wave's first slot in it
         const int bkt = tid;
-        int tot = 0;
+        const bool bw = tid < kSortBuckets;  // uniform per wave
+        int tot = 0, incl = 0;
+        if (bw) {
 #pragma unroll
-        for (int w = 0; w < 4; w++) tot += hist[w * kSortBuckets + bkt];
-        int incl = tot;
+            for (int w = 0; w < kMaskWaves; w++) tot += hist[w * kSortBuckets + bkt];
+            incl = tot;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            if (lane == 63) wsum[wv] = incl;
         }
-        if (lane == 63) wsum[wv] = incl;
         __syncthreads();
-        int start = incl - tot;
-        for (int w = 0; w < wv; w++) start += wsum[w];
+        if (bw) {
+            int start = incl - tot;
+            for (int w = 0; w < wv; w++) start += wsum[w];
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            pos[w * kSortBuckets + bkt] = start;
-            start += hist[w * kSortBuckets + bkt];
+            for (int w = 0; w < kMaskWaves; w++) {
+                pos[w * kSortBuckets + bkt] = start;
+                start += hist[w * kSortBuckets + bkt];
+            }
         }
     }
     __syncthreads();
@@ -338,7 +346,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
 }
 
 __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* bits,
-                               int* wave_sum, int* sort_lds) {
+                               int* wave_sum) {
     const float* coords = a.coords;
     int* list = a.list;
     int* ctr = a.ctr;
@@ -350,6 +358,11 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     const float* cc = coords + (size_t)e * 2 * g.HW;
     int* ord = a.order + (size_t)e * 3 * g.HW;
+    // the sort's histograms take the upper half of the bitmap's LDS when the
+    // bitmap fits in the lower half
+    static_assert(2 * kMaskWaves * kSortBuckets <= kPrepLdsWords / 2, "sort LDS");
+    int* sort_lds = nw <= kPrepLdsWords / 2 ? reinterpret_cast<int*>(bits + kPrepLdsWords / 2)
+                                            : nullptr;
     if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles, a.tab)) {  // uniform
         // pixel order: the order is the identity, written beside the mask.
         // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
@@ -433,9 +446,9 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
 // bitmap is the level-0 LDS array; they are the longer chains, so they are
 // dispatched first), then the blocks x C/16 x slots preparation workgroups
 // (block fastest).
-static_assert(kMaskThreads == 256, "the tile-mask workgroups share k_feat_prep's size");
+static_assert(kMaskThreads == kFeatThreads, "the tile-mask workgroups share k_feat_prep's size");
 template <typename Tin>
-__global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
+__global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
                                                    SlotFrames sf, int slot_lo,
                                                    unsigned short* __restrict__ out, Geom g,
                                                    int pooled, int vec, int nbx, int nblk,
@@ -449,8 +462,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
         // the tile-mask chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum,
-                       reinterpret_cast<int*>(&l1[0][0][0]));
+        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum);
         return;
     }
     const int tid = threadIdx.x;
@@ -461,13 +473,13 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     const int W = g.w[0], H = g.h[0];
     const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
     // all of a thread's loads are issued before the first is used
-    constexpr int kPer = kChunk * kPrepRows * kPrepCols / 256;
+    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kFeatThreads;
     float ld[kPer];
     if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
         // four consecutive pixels of a row a lane (all inside or all outside)
 #pragma unroll
         for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * 256);
+            const int i = 4 * (tid + u * kFeatThreads);
             const int c = i / (kPrepRows * kPrepCols);
             const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
             const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
@@ -480,7 +492,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
         }
 #pragma unroll
         for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * 256);
+            const int i = 4 * (tid + u * kFeatThreads);
             *reinterpret_cast<float4*>(
                 &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
                 make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
@@ -488,7 +500,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     } else {
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * 256;
+            const int i = tid + u * kFeatThreads;
             const int c = i / (kPrepRows * kPrepCols);
             const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
             const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
@@ -498,7 +510,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
         }
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * 256;
+            const int i = tid + u * kFeatThreads;
             l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
         }
     }
@@ -520,7 +532,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
         *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
     };
     // level 0
-    for (int p = tid; p < kPrepRows * kPrepCols; p += 256) {
+    for (int p = tid; p < kPrepRows * kPrepCols; p += kFeatThreads) {
         const int r = p / kPrepCols, x = p % kPrepCols;
         const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
         if (yy >= H || xx >= W) continue;
@@ -532,7 +544,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
     if (!pooled) return;
     // pooled levels: level l from level l-1 in LDS, then its pixels out
     auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
-        for (int i = tid; i < kChunk * rows * cols; i += 256) {
+        for (int i = tid; i < kChunk * rows * cols; i += kFeatThreads) {
             const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
             float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
             sum = sum + src[c][2 * r + 1][2 * x];
@@ -540,7 +552,7 @@ __global__ __launch_bounds__(256) void k_feat_prep(const Tin* __restrict__ fm, l
             dst[c][r][x] = 0.25f * sum;
         }
         __syncthreads();
-        for (int p = tid; p < rows * cols; p += 256) {
+        for (int p = tid; p < rows * cols; p += kFeatThreads) {
             const int r = p / cols, x = p % cols;
             const int yy = by * rows + r, xx = bx * cols + x;
             if (yy >= g.h[l] || xx >= g.w[l]) continue;
@@ -918,9 +930,9 @@ int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& s
     // vector loads of 4 pixels when every row starts 4-element aligned
     const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
-    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(256), 0, stream,
-                       fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, vec ? 1 : 0, nbx, nblk,
-                       (int)nmask, mk);
+    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(kFeatThreads), 0,
+                       stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, vec ? 1 : 0,
+                       nbx, nblk, (int)nmask, mk);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
