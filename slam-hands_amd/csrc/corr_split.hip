@@ -102,17 +102,15 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // concatenated target indices [off + ya*w + xa, off + yb*w + xb], and every
 // target tile in that span is marked (a superset of the tiles holding a cell).
 // Tiles not marked are skipped by k_corr_split_win: they would store nothing.
-// One workgroup of kMaskThreads per edge: an LDS bitmap (`bits`, at least
+// One workgroup (kT threads, 512 or 1024) per edge: an LDS bitmap (`bits`, at least
 // ceil(mtiles * ntiles / 32) words) of the edge's tiles, then the marked ones
 // compacted in tile order into the edge's segment list[e * tpe ..] (ids
 // mt * ntiles + nt) and their number into ctr[kCtrCount + e]. Edge 0 also
 // zeroes the tile counters of k_corr_split_win, which runs after this on the
 // same stream. These workgroups run in the launch of k_feat_prep, beside the
 // feature preparation they do not depend on.
-constexpr int kMaskThreads = 512;
-constexpr int kMaskWaves = kMaskThreads / 64;
-// threads of every workgroup of the k_feat_prep launch
-constexpr int kFeatThreads = kMaskThreads;
+// (k_feat_prep launches with kT = 512 or 1024 threads a workgroup; the
+// tile-mask chain of an edge then sorts with kT / 64 waves.)
 // the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
 // which a tile-mask workgroup uses for its bitmap and sorted pixel indices
 constexpr int kPrepRows = 8, kPrepCols = 64;
@@ -220,7 +218,7 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // the slot), writes its pixel and coordinates there, and marks the target
 // tiles of its windows in the row of its source tile (masks formed in the
 // histogram pass when the quarter stays in registers). Writes ord[0][q] =
-// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * kMaskWaves * kSortBuckets ints (or is null: no room). A map with
+// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * (kT / 64) * kSortBuckets ints (or is null: no room). A map with
 // more rows than that is not sorted: returns false, and neither ord nor the
 // bitmap is written.
 constexpr int kSortBuckets = 256;
@@ -237,6 +235,7 @@ __device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
     return m;
 }
 
+template <int kT>
 __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
                               unsigned* bits, int ntiles, const unsigned long long* tab) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -245,11 +244,11 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
     float* oxy = reinterpret_cast<float*>(ord + HW);
     const int nbits = 32 - __builtin_clz(nb - 1);
     const unsigned long long below = (1ull << lane) - 1ull;
-    int* hist = lds;                             // [kMaskWaves][kSortBuckets]
-    int* pos = lds + kMaskWaves * kSortBuckets;  // [kMaskWaves][kSortBuckets]: next slot
-    for (int i = tid; i < kMaskWaves * kSortBuckets; i += kMaskThreads) hist[i] = 0;
+    int* hist = lds;                             // [(kT / 64)][kSortBuckets]
+    int* pos = lds + (kT / 64) * kSortBuckets;  // [(kT / 64)][kSortBuckets]: next slot
+    for (int i = tid; i < (kT / 64) * kSortBuckets; i += kT) hist[i] = 0;
     __syncthreads();  // also orders the caller's clearing of the bitmap
-    const int part = (HW + kMaskWaves - 1) / kMaskWaves;  // pixels of each wave
+    const int part = (HW + (kT / 64) - 1) / (kT / 64);  // pixels of each wave
     const int q0 = std::min(HW, wv * part), q1 = std::min(HW, q0 + part);
     auto key_of = [&](float y) {
         const int oy = floor_clamped(y) - 3;
@@ -291,7 +290,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
         int tot = 0, incl = 0;
         if (bw) {
 #pragma unroll
-            for (int w = 0; w < kMaskWaves; w++) tot += hist[w * kSortBuckets + bkt];
+            for (int w = 0; w < (kT / 64); w++) tot += hist[w * kSortBuckets + bkt];
             incl = tot;
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
@@ -305,7 +304,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
             int start = incl - tot;
             for (int w = 0; w < wv; w++) start += wsum[w];
 #pragma unroll
-            for (int w = 0; w < kMaskWaves; w++) {
+            for (int w = 0; w < (kT / 64); w++) {
                 pos[w * kSortBuckets + bkt] = start;
                 start += hist[w * kSortBuckets + bkt];
             }
@@ -345,8 +344,9 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
     return true;
 }
 
-__device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* bits,
-                               int* wave_sum) {
+template <int kT>
+__device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* big,
+                               unsigned* small, int small_words, int* wave_sum) {
     const float* coords = a.coords;
     int* list = a.list;
     int* ctr = a.ctr;
@@ -354,16 +354,17 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int tpe = mtiles * ntiles;
     const int nw = (tpe + 31) / 32;
-    for (int i = tid; i < nw; i += kMaskThreads) bits[i] = 0u;
+    // the bitmap in `small` when it fits, the sort's histograms then in
+    // `big` (kPrepLdsWords words); else the bitmap in `big` and no sort
+    const bool fits = nw <= small_words;
+    unsigned* bits = fits ? small : big;
+    for (int i = tid; i < nw; i += kT) bits[i] = 0u;
     if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
     const float* cc = coords + (size_t)e * 2 * g.HW;
     int* ord = a.order + (size_t)e * 3 * g.HW;
-    // the sort's histograms take the upper half of the bitmap's LDS when the
-    // bitmap fits in the lower half
-    static_assert(2 * kMaskWaves * kSortBuckets <= kPrepLdsWords / 2, "sort LDS");
-    int* sort_lds = nw <= kPrepLdsWords / 2 ? reinterpret_cast<int*>(bits + kPrepLdsWords / 2)
-                                            : nullptr;
-    if (!sort_and_mark(g, cc, ord, sort_lds, wave_sum, bits, ntiles, a.tab)) {  // uniform
+    static_assert(2 * (kT / 64) * kSortBuckets <= kPrepLdsWords, "sort LDS");
+    int* sort_lds = fits ? reinterpret_cast<int*>(big) : nullptr;
+    if (!sort_and_mark<kT>(g, cc, ord, sort_lds, wave_sum, bits, ntiles, a.tab)) {  // uniform
         // pixel order: the order is the identity, written beside the mask.
         // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
         // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
@@ -373,17 +374,17 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
         __syncthreads();  // the bitmap is clear
         float* oxy = reinterpret_cast<float*>(ord + g.HW);
         constexpr int kU = 4;  // sources per thread whose coordinates load together
-        for (int pb = 0; pb < g.HW; pb += kU * kMaskThreads) {
+        for (int pb = 0; pb < g.HW; pb += kU * kT) {
             float xs[kU], ys[kU];
 #pragma unroll
             for (int u = 0; u < kU; u++) {
-                const int q = std::min(pb + u * kMaskThreads + tid, g.HW - 1);
+                const int q = std::min(pb + u * kT + tid, g.HW - 1);
                 xs[u] = cc[q];
                 ys[u] = cc[g.HW + q];
             }
 #pragma unroll
             for (int u = 0; u < kU; u++) {
-                const int pw = pb + u * kMaskThreads + (tid & ~63);  // the wave's first source
+                const int pw = pb + u * kT + (tid & ~63);  // the wave's first source
                 if (pw >= g.HW) break;                                // uniform
                 const bool in = pw + lane < g.HW;
                 const int row = pw / kSrcTile * ntiles;  // first tile id of the source tile
@@ -409,11 +410,11 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
         }
     }
     __syncthreads();
-    // compaction, kMaskThreads tiles a round: ballot ranks within a wave,
+    // compaction, kT tiles a round: ballot ranks within a wave,
     // wave totals through LDS
     int* seg = list + (size_t)e * tpe;
     int base = 0;
-    for (int t0 = 0; t0 < tpe; t0 += kMaskThreads) {
+    for (int t0 = 0; t0 < tpe; t0 += kT) {
         const int t = t0 + tid;
         const bool m = t < tpe && ((bits[t >> 5] >> (t & 31)) & 1u);
         const unsigned long long bal = __ballot(m);
@@ -422,7 +423,7 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
         __syncthreads();
         int before = 0, all = 0;
 #pragma unroll
-        for (int q = 0; q < kMaskThreads / 64; q++) {
+        for (int q = 0; q < kT / 64; q++) {
             const int v = wave_sum[q];
             before += q < wv ? v : 0;
             all += v;
@@ -446,9 +447,8 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
 // bitmap is the level-0 LDS array; they are the longer chains, so they are
 // dispatched first), then the blocks x C/16 x slots preparation workgroups
 // (block fastest).
-static_assert(kMaskThreads == kFeatThreads, "the tile-mask workgroups share k_feat_prep's size");
-template <typename Tin>
-__global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
+template <typename Tin, int kT>
+__global__ __launch_bounds__(kT) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
                                                    SlotFrames sf, int slot_lo,
                                                    unsigned short* __restrict__ out, Geom g,
                                                    int pooled, int vec, int nbx, int nblk,
@@ -457,12 +457,13 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
     __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
     __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
     __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
-    __shared__ int wave_sum[kMaskThreads / 64];
+    __shared__ int wave_sum[kT / 64];
     if ((int)blockIdx.x < nmask) {  // uniform
         // the tile-mask chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        tile_mask_edge(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]), wave_sum);
+        tile_mask_edge<kT>(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]),
+                       reinterpret_cast<unsigned*>(&l1[0][0][0]), (int)(sizeof(l1) / 4), wave_sum);
         return;
     }
     const int tid = threadIdx.x;
@@ -473,13 +474,13 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
     const int W = g.w[0], H = g.h[0];
     const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
     // all of a thread's loads are issued before the first is used
-    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kFeatThreads;
+    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kT;
     float ld[kPer];
     if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
         // four consecutive pixels of a row a lane (all inside or all outside)
 #pragma unroll
         for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kFeatThreads);
+            const int i = 4 * (tid + u * kT);
             const int c = i / (kPrepRows * kPrepCols);
             const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
             const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
@@ -492,7 +493,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
         }
 #pragma unroll
         for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kFeatThreads);
+            const int i = 4 * (tid + u * kT);
             *reinterpret_cast<float4*>(
                 &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
                 make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
@@ -500,7 +501,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
     } else {
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kFeatThreads;
+            const int i = tid + u * kT;
             const int c = i / (kPrepRows * kPrepCols);
             const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
             const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
         }
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kFeatThreads;
+            const int i = tid + u * kT;
             l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
         }
     }
@@ -532,7 +533,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
         *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
     };
     // level 0
-    for (int p = tid; p < kPrepRows * kPrepCols; p += kFeatThreads) {
+    for (int p = tid; p < kPrepRows * kPrepCols; p += kT) {
         const int r = p / kPrepCols, x = p % kPrepCols;
         const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
         if (yy >= H || xx >= W) continue;
@@ -544,7 +545,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
     if (!pooled) return;
     // pooled levels: level l from level l-1 in LDS, then its pixels out
     auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
-        for (int i = tid; i < kChunk * rows * cols; i += kFeatThreads) {
+        for (int i = tid; i < kChunk * rows * cols; i += kT) {
             const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
             float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
             sum = sum + src[c][2 * r + 1][2 * x];
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(kFeatThreads) void k_feat_prep(const Tin* __restric
             dst[c][r][x] = 0.25f * sum;
         }
         __syncthreads();
-        for (int p = tid; p < rows * cols; p += kFeatThreads) {
+        for (int p = tid; p < rows * cols; p += kT) {
             const int r = p / cols, x = p % cols;
             const int yy = by * rows + r, xx = bx * cols + x;
             if (yy >= g.h[l] || xx >= g.w[l]) continue;
@@ -930,9 +931,17 @@ int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& s
     // vector loads of 4 pixels when every row starts 4-element aligned
     const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
-    hipLaunchKernelGGL(k_feat_prep<Tin>, dim3((unsigned)(nprep + nmask)), dim3(kFeatThreads), 0,
-                       stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0, vec ? 1 : 0,
-                       nbx, nblk, (int)nmask, mk);
+    // 1024-thread workgroups (16-wave mask chains) for maps up to 4096
+    // pixels, 512 above: measured, 20.3 against 21.8 us at 48x64 and 39.3
+    // against 32.6 us at 54x96, where the preparation's share is larger
+    if (g.HW <= 4096)
+        hipLaunchKernelGGL((k_feat_prep<Tin, 1024>), dim3((unsigned)(nprep + nmask)), dim3(1024),
+                           0, stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0,
+                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk);
+    else
+        hipLaunchKernelGGL((k_feat_prep<Tin, 512>), dim3((unsigned)(nprep + nmask)), dim3(512),
+                           0, stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0,
+                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
