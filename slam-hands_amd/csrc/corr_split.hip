@@ -103,7 +103,9 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // target tile in that span is marked (a superset of the tiles holding a cell).
 // Tiles not marked are skipped by k_corr_split_win: they would store nothing.
 // One workgroup (kT threads, 512 or 1024) per edge: an LDS bitmap (`bits`, at least
-// ceil(mtiles * ntiles / 32) words) of the edge's tiles, then the marked ones
+// ceil(mtiles * ntiles / 32) words; in the level-1 array when it fits there,
+// the sort's histograms then taking the level-0 array, else in the level-0
+// array with the sources left in pixel order) of the edge's tiles, then the marked ones
 // compacted in tile order into the edge's segment list[e * tpe ..] (ids
 // mt * ntiles + nt) and their number into ctr[kCtrCount + e]. Edge 0 also
 // zeroes the tile counters of k_corr_split_win, which runs after this on the
@@ -112,7 +114,7 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // (k_feat_prep launches with kT = 512 or 1024 threads a workgroup; the
 // tile-mask chain of an edge then sorts with kT / 64 waves.)
 // the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
-// which a tile-mask workgroup uses for its bitmap and sorted pixel indices
+// which a tile-mask workgroup uses for its sort's histograms or its bitmap
 constexpr int kPrepRows = 8, kPrepCols = 64;
 constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
@@ -209,7 +211,7 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // order (whose +-8 px flows spread them over ~26 rows). A window cell is the
 // same dot product whichever tile computes it, so the order changes which
 // products are skipped, not any output. Counting sort in the workgroup:
-// every wave takes a contiguous quarter of the pixels, 64 at a time, and
+// every wave takes a contiguous 64/kT of the pixels, 64 at a time, and
 // counts their keys in its own LDS histogram (atomic adds: the counts do not
 // depend on their order); then bucket-major offsets; then the same chunks
 // again in pixel order, the lanes of a chunk holding equal keys finding each
@@ -217,7 +219,7 @@ __device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int r
 // plus its rank among the equal lanes below it (the lowest of them advances
 // the slot), writes its pixel and coordinates there, and marks the target
 // tiles of its windows in the row of its source tile (masks formed in the
-// histogram pass when the quarter stays in registers). Writes ord[0][q] =
+// histogram pass when a wave's pixels stay in registers). Writes ord[0][q] =
 // the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * (kT / 64) * kSortBuckets ints (or is null: no room). A map with
 // more rows than that is not sorted: returns false, and neither ord nor the
 // bitmap is written.
@@ -267,7 +269,7 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
         }
     };
     const bool one = q1 - q0 <= 64 * kG;
-    // with the quarter in registers and at most 64 target tiles, each
+    // with the wave's pixels in registers and at most 64 target tiles, each
     // source's tile mask is formed here, while the loads of the histogram
     // pass are what the waves wait for, and only merged in the scatter
     const bool pre = one && ntiles <= 64;
@@ -443,8 +445,8 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
 // hi/lo split of every pixel of the levels present, 16 channels = 32 bytes
 // per pixel and plane, into out[slot][plane][C/16][Ttot][16]. `pooled` = 0
 // writes level 0 only (source slots). One-dimensional grid: first, when
-// mk.list is set, one tile-mask workgroup per edge (tile_mask_edge, whose
-// bitmap is the level-0 LDS array; they are the longer chains, so they are
+// mk.list is set, one tile-mask workgroup per edge (tile_mask_edge, with
+// the level-0 and level-1 LDS arrays; they are the longer chains, so they are
 // dispatched first), then the blocks x C/16 x slots preparation workgroups
 // (block fastest).
 template <typename Tin, int kT>
