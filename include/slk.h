@@ -231,8 +231,19 @@ int slk_ba_iterate_n(slk_ctx* ctx, float* poses, float* disps, const float* intr
                      float ep, int motion_only, int iters, hipStream_t stream);
 
 /* Synchronises `stream` and returns SLK_E_NOT_SPD if any iterate since the
- * last call met an indefinite system, else SLK_OK; clears the flag. */
+ * last call met an indefinite system, SLK_E_HIP if a workgroup of an
+ * overlapped fused step stopped waiting for its solve (see
+ * slk_ba_set_wait_limit), else SLK_OK; clears the flags. */
 int slk_ba_status(slk_ctx* ctx, hipStream_t stream);
+
+/* No counterpart in the reference: the bound of the wait inside an
+ * overlapped fused BA step launch (slk_ba_iterate_n), where the linearization
+ * workgroups wait for the solve of the same launch. After `polls` polls a
+ * waiting workgroup gives up, skips the rest of its step and the next
+ * slk_ba_status reports SLK_E_HIP; polls < 0 restores the default (2^18,
+ * far above the ~40 a step takes). A diagnostic, used by the tests to run
+ * the give-up path; production callers leave the default. */
+int slk_ba_set_wait_limit(slk_ctx* ctx, int polls);
 
 /* Debug copy of the last iterate's system (synchronising): S_host [(6P)^2]
  * after Schur + damping, b_host [6P], dx_host [6P]; any may be NULL. *n gets

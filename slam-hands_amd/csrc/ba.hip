@@ -1472,6 +1472,7 @@ struct FzArgs {
     double* hpart;  // [M][nch][27]
     double* spart;  // [N_kf][nch][kFzMaxNT][256] Z tiles in MFMA lane order
     int HW, W, nch, t0, t1;
+    int spin_max;  // polls before a waiting workgroup gives up
 };
 
 __device__ __forceinline__ float ld_coherent(const float* p) {
@@ -1749,8 +1750,9 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
 // The overlapped step's handshake: the assembly launch before it clears
 // *ready, the step launch's solve workgroup stores 1 there once dx, the flags
 // and the poses are written, and a linearization workgroup waits for it
-// (thread 0 polls, bounded: after kFzSpinMax polls the workgroup gives up,
-// flags[3] reports it, and it writes nothing more).
+// (thread 0 polls, bounded: after F.spin_max polls, kFzSpinMax unless
+// slk_ba_set_wait_limit set another, the workgroup gives up, flags[3]
+// reports it, and it writes nothing more).
 constexpr int kFzSpinMax = 1 << 18;
 
 struct FzWait {
@@ -2030,7 +2032,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
                 for (int n = 0; __hip_atomic_load(wait.ready, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT) == 0;
                      n++) {
-                    if (n == kFzSpinMax) {
+                    if (n >= F.spin_max) {
                         st = 0;
                         break;
                     }
@@ -2372,6 +2374,7 @@ struct BaState {
     // overlapped steps: the second pose copy and the step flag
     DevBuf poses_alt, ready;
     int cus = 0;  // compute units: the overlapped step's workgroups must all be resident
+    int spin_max = kFzSpinMax;  // the step launch's bounded wait
 };
 
 namespace {
@@ -2819,6 +2822,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     F.poses = I.poses;
     F.poses_prev = s->poses_prev.as<float>();
     F.pose_copy = nullptr;
+    F.spin_max = s->spin_max;
     F.intr = I.intr;
     F.eta = I.eta;
     F.dx = s->dx.as<float>();
@@ -2959,6 +2963,12 @@ extern "C" int slk_ba_iterate_n(slk_ctx* ctx, float* poses, float* disps,
     const IterArgs I = {poses, disps, intrinsics, target, weight, eta, ii_gpu, jj_gpu,
                         t0,    t1,    lm,         ep,     motion_only ? 1 : 0};
     return ba_run(ctx, I, ii_host, jj_host, num_edges, iters, stream);
+}
+
+extern "C" int slk_ba_set_wait_limit(slk_ctx* ctx, int polls) {
+    if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_set_wait_limit: null context");
+    ctx->ba->spin_max = polls < 0 ? kFzSpinMax : polls;
+    return SLK_OK;
 }
 
 extern "C" int slk_ba_status(slk_ctx* ctx, hipStream_t stream) {

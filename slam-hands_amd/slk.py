@@ -33,7 +33,7 @@ EXPORTS = [
     "slk_corr_build", "slk_corr_sample", "slk_corr_level", "slk_avg_pool_2x2",
     "slk_corr_sample_level", "slk_coords_hw2_to_2hw",
     "slk_projmap", "slk_pose_retr", "slk_disp_retr", "slk_frame_distance", "slk_clamp_disps",
-    "slk_ba_iterate", "slk_ba_iterate_n", "slk_ba_status", "slk_ba_last_system", "slk_ba_projective_transform",
+    "slk_ba_iterate", "slk_ba_iterate_n", "slk_ba_status", "slk_ba_set_wait_limit", "slk_ba_last_system", "slk_ba_projective_transform",
     "slk_ba_accum", "slk_ba_damping_q", "slk_ba_eet6x6", "slk_ba_ev6x1", "slk_ba_evt6x1",
     "slk_ba_depth_update",
     "slk_compute_motion", "slk_fill_coords0", "slk_compute_target", "slk_gather_rows",
@@ -107,6 +107,7 @@ def lib():
             "slk_ba_iterate": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, F, F, I, P],
             "slk_ba_iterate_n": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, F, F, I, I, P],
             "slk_ba_status": [P, P],
+            "slk_ba_set_wait_limit": [P, I],
             "slk_ba_last_system": [P, P, P, P, ctypes.POINTER(I), P],
             "slk_ba_projective_transform": [P] * 13 + [I, I, I, P],
             "slk_ba_accum": [P, P, P, P, I, I, I, P],
@@ -438,6 +439,11 @@ class Context:
 
     def ba_status(self, stream=None):
         return lib().slk_ba_status(self.ptr, stream)
+
+    def ba_set_wait_limit(self, polls):
+        """Polls before a workgroup of an overlapped BA step stops waiting for
+        its solve (negative: the default); see include/slk.h."""
+        check(lib().slk_ba_set_wait_limit(self.ptr, polls))
 
     def ba_last_system(self, stream=None):
         n = I()

@@ -173,6 +173,39 @@ def test_iterate_n_not_spd_leaves_state_untouched(slk):
     ctx.close()
 
 
+def test_iterate_n_wait_give_up_is_reported(slk):
+    """The bounded wait inside an overlapped step launch: with the limit set to
+    zero polls from the host, the linearization workgroups stop waiting for
+    their solve, skip the rest of their step and every launch still ends;
+    slk_ba_status reports it as SLK_E_HIP. With the default limit restored,
+    the next call on the same context runs normally and matches the oracle."""
+    announce("ba iterate_n wait give-up (limit 0)")
+    p = wl.ba_problem()
+    dev = Dev(slk, p)
+    ctx = slk.Context(p["h"], p["w"], max_batch=1)
+    d = dev.d
+    args = (d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"], d["ii"],
+            d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1)
+    ctx.ba_set_wait_limit(0)
+    ctx.ba_iterate_n(*args, 2)
+    assert ctx.ba_status() == slk.SLK_E_HIP
+    assert b"stopped waiting" in slk.lib().slk_last_error()
+    ctx.ba_set_wait_limit(-1)
+    dev2 = Dev(slk, p)
+    d2 = dev2.d
+    ctx.ba_iterate_n(d2["poses"], d2["disps"], d2["intr"], d2["target"], d2["weight"],
+                     d2["eta"], d2["ii"], d2["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4,
+                     0.1, 2)
+    assert ctx.ba_status() == slk.SLK_OK
+    ref_p, ref_d = p["poses"], p["disps"]
+    for _ in range(2):
+        ref = oracle_iter(p, ref_p, ref_d, 1e-4, 0.1)
+        ref_p, ref_d = ref["poses"], ref["disps"]
+    assert norm_rel(dev2.poses(), ref_p) < TOL
+    assert norm_rel(dev2.disps(), ref_d) < TOL
+    ctx.close()
+
+
 @pytest.mark.parametrize("duplicate", [True, False])
 def test_edge_cases_stereo_duplicates_absent_frame(slk, duplicate):
     # with the duplicate (2, 3) edge the linearization runs edge by edge per
