@@ -1416,12 +1416,16 @@ __global__ __launch_bounds__(256) void k_ba_backsub(PlanDev plan, const double* 
 //            chunk's pixels in LDS as [pixel][row], from which the chunk's
 //            Schur products Z = [E; w] Q [E; w]^T (EEt6x6 / Ev6x1,
 //            ba.cuh:303-372) are formed on fp64 MFMA (v_mfma_f64_16x16x4),
-//            each wave over 64 pixels, the four partials added in wave order.
+//            each wave over 48 pixels, the four partials added in wave order.
 //   k_ba_fz_assemble  one workgroup per block of S and per segment of b: the
 //            chunk sums (in chunk order) of the Z entries and edge partials
 //            the block needs, then the LM damping.
 //   a solve kernel, which also keeps the poses before the step.
-// A last k_ba_fz<bs only> applies the final step's back-substitution.
+// A last k_ba_fz_bs applies the final step's back-substitution. When every
+// linearization workgroup fits the CUs at once, the solve and the next
+// k_ba_fz share a launch instead (k_ba_fz_step): the linearization
+// workgroups rebuild the solved step's E rows while it runs and wait for its
+// dx on a flag, so an iteration is two launches (assembly, step).
 // E rows ("slots") of a keyframe: its own pose when free (slot 0), then one
 // per non-stereo edge whose jj is free, in edge order (two edges to the same
 // pose keep separate slots; the assembly adds their products). Row 6 * nslot
