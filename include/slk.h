@@ -233,16 +233,23 @@ int slk_ba_iterate_n(slk_ctx* ctx, float* poses, float* disps, const float* intr
 /* Synchronises `stream` and returns SLK_E_NOT_SPD if any iterate since the
  * last call met an indefinite system, SLK_E_HIP if a workgroup of an
  * overlapped fused step stopped waiting for its solve (see
- * slk_ba_set_wait_limit), else SLK_OK; clears the flags. */
+ * slk_ba_set_wait_limit), else SLK_OK; clears the flags.
+ * After SLK_E_HIP the state is not a whole number of steps: the poses hold
+ * every step solved up to and including the one whose wait gave up, the
+ * inverse depths of the pixel chunks that stopped waiting miss that step's
+ * update (the other chunks have it), and every later step of that call
+ * changed neither. Restore poses and disps from a copy before iterating on. */
 int slk_ba_status(slk_ctx* ctx, hipStream_t stream);
 
 /* No counterpart in the reference: the bound of the wait inside an
  * overlapped fused BA step launch (slk_ba_iterate_n), where the linearization
- * workgroups wait for the solve of the same launch. After `polls` polls a
- * waiting workgroup gives up, skips the rest of its step and the next
- * slk_ba_status reports SLK_E_HIP; polls < 0 restores the default (2^18,
- * far above the ~40 a step takes). A diagnostic, used by the tests to run
- * the give-up path; production callers leave the default. */
+ * workgroups wait for the solve of the same launch. After `polls` polls (at
+ * once for polls = 0) a waiting workgroup gives up: its pixel chunk skips
+ * that step's depth update and the next linearization, the call's later
+ * steps take no step at all, and the next slk_ba_status reports SLK_E_HIP
+ * (the state left behind is described there); polls < 0 restores the
+ * default (2^18, far above the ~40 a step takes). A diagnostic, used by the
+ * tests to run the give-up path; production callers leave the default. */
 int slk_ba_set_wait_limit(slk_ctx* ctx, int polls);
 
 /* Debug copy of the last iterate's system (synchronising): S_host [(6P)^2]

@@ -504,6 +504,12 @@ __global__ __launch_bounds__(kSchWG) void k_ba_schur(PlanDev plan, const double*
 }
 
 // ----------------------------------------------------------- solve ------
+// the BA status words (BaState::flags): [0] the last step was rejected, [1]
+// a step was rejected (sticky), [2] a failed pivot of the blocked solve, [3]
+// a wait of an overlapped step gave up (sticky), [4], [5] that give-up within
+// the current call (see the overlapped step's handshake)
+constexpr int kBaFlags = 8;
+
 struct SolveArgs {
     PlanDev plan;
     const double* etot;   // [M][120] per-edge Hii, Hij, Hjj, vi, vj
@@ -516,6 +522,7 @@ struct SolveArgs {
     double* dx_dbg; // [n]
     float* dx;      // [n] fp32 step used by retraction and back-substitution
     int* flags;     // [0] this iteration not SPD, [1] sticky
+    const int* halt;  // or null: when *halt is set the step is not taken (an earlier wait gave up)
     float* poses;
     float* poses_prev;  // [P][7] poses t0..t1-1 before the step (fused path), or null
     float* poses_next;  // [P][7] poses t0..t1-1 after the step (overlapped fused path), or null
@@ -605,10 +612,14 @@ __device__ __forceinline__ double bcast(double v, int src) {
 __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok,
                                              const float* pose_src) {
     const int n = A.n;
+    // a halted call takes no more steps: like a rejected step, but not
+    // reported as one
+    const bool halted = A.halt && *A.halt != 0;
     if (threadIdx.x == 0) {
-        A.flags[0] = ok ? 0 : 1;
-        if (!ok) A.flags[1] = 1;
+        A.flags[0] = ok && !halted ? 0 : 1;
+        if (!ok && !halted) A.flags[1] = 1;
     }
+    ok = ok && !halted;
     for (int t = threadIdx.x; t < n; t += blockDim.x) {
         A.dx_dbg[t] = ok ? x[t] : 0.0;
         A.dx[t] = ok ? (float)x[t] : 0.0f;
@@ -1471,7 +1482,10 @@ struct FzArgs {
     const float* intr;
     const float* eta;
     const float* dx;   // [6P] the last step
-    int* flags;        // [0]: the last step was rejected (not SPD); [3] a wait gave up
+    // [0]: the last step was rejected (not SPD); [3] a wait gave up (sticky,
+    // reported by slk_ba_status); [4] a wait of this call gave up (cleared by
+    // the call's first launch); [5] the copy of [4] the next solve reads
+    int* flags;
     float* disps;
     double* hpart;  // [M][nch][27]
     double* spart;  // [N_kf][nch][kFzMaxNT][256] Z tiles in MFMA lane order
@@ -1755,8 +1769,12 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
 // *ready, the step launch's solve workgroup stores 1 there once dx, the flags
 // and the poses are written, and a linearization workgroup waits for it
 // (thread 0 polls, bounded: after F.spin_max polls, kFzSpinMax unless
-// slk_ba_set_wait_limit set another, the workgroup gives up, flags[3]
-// reports it, and it writes nothing more).
+// slk_ba_set_wait_limit set another, or at once for a limit of 0, the
+// workgroup gives up: it sets flags[3] (reported by slk_ba_status) and
+// flags[4], and writes nothing more, so its chunk's depths miss that step's
+// update. The next assembly launch copies flags[4] to flags[5], and every
+// later solve of the call then takes no step (finish_solve), so the rest of
+// the call changes neither poses nor depths.)
 constexpr int kFzSpinMax = 1 << 18;
 
 struct FzWait {
@@ -2032,9 +2050,9 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
         fz_pass<true>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache);
         if (wait.ready) {
             if (tid == 0) {
-                int st = 1;
-                for (int n = 0; __hip_atomic_load(wait.ready, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT) == 0;
+                int st = F.spin_max > 0 ? 1 : 0;  // a limit of 0 gives up without a poll
+                for (int n = 0; st && __hip_atomic_load(wait.ready, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) == 0;
                      n++) {
                     if (n >= F.spin_max) {
                         st = 0;
@@ -2046,12 +2064,21 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             }
             __syncthreads();
             if (!L.wait_state) {  // uniform
-                if (tid == 0) F.flags[3] = 1;
+                if (tid == 0) {
+                    F.flags[3] = 1;
+                    F.flags[4] = 1;
+                }
                 return;
             }
             // What the solve wrote (the status, dx, the poses) is read from
-            // here on with device-coherent loads, issued after the flag was
-            // seen, so no cache of this workgroup needs invalidating.
+            // here on with device-coherent loads (agent scope, relaxed),
+            // issued after the flag was seen and a workgroup barrier: the
+            // solve's release fence wrote them back before its flag store,
+            // and these loads bypass the caches that could hold older
+            // copies, so no cache of this workgroup needs invalidating. (An
+            // agent-scope acquire fence here would invalidate this XCD's L2
+            // as well, and the next step's input loads measured ~4.5 us
+            // slower after it.)
         }
         // one round of loads, all issued before any is used: the status, dx
         // by slot row (slot poses are free poses), and the poses of the
@@ -2133,9 +2160,16 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
 template <bool kBs, bool kLin>
 __global__ __launch_bounds__(kLinWG, kFzWgPerCu) void k_ba_fz(FzArgs F) {
     __shared__ FzLds L;
-    if (!kBs && F.pose_copy && blockIdx.x == 0 && blockIdx.y == 0)
+    if (!kBs && F.pose_copy && blockIdx.x == 0 && blockIdx.y == 0) {
+        // the first launch of an overlapped call: the poses its first step
+        // starts from, and no wait of this call has given up yet
         for (int t = threadIdx.x; t < (F.t1 - F.t0) * 7; t += kLinWG)
             F.pose_copy[t] = F.poses[F.t0 * 7 + t];
+        if (threadIdx.x == 0) {
+            F.flags[4] = 0;
+            F.flags[5] = 0;
+        }
+    }
     fz_body<kBs, kLin>(F, L, blockIdx.x, blockIdx.y, FzWait{nullptr});
 }
 
@@ -2223,6 +2257,7 @@ struct FzAsmArgs {
     double* S;  // [n][n] assembled system (after damping)
     double* b;  // [n]
     int* ready;  // or null: the overlapped step's flag, cleared here for the launch after
+    int* flags;  // with ready: flags[5] = flags[4] for the solve of the launch after
 };
 
 // Entry (row, col) of a keyframe's Z, summed over the chunks: Z is symmetric
@@ -2255,7 +2290,10 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     const int g = blockIdx.x, tid = threadIdx.x;
     const int sl = tid / 36, ent = tid - sl * 36;
     const int P = A.P, n = A.n;
-    if (A.ready && g == 0 && tid == 0) *A.ready = 0;
+    if (A.ready && g == 0 && tid == 0) {
+        *A.ready = 0;
+        A.flags[5] = A.flags[4];  // a wait of the last launch gave up: no more steps
+    }
     const bool isS = g < P * P;
     const bool act = sl < kAsmSlices && (isS || ent < 6);
     const int r = ent / 6, c = ent - (ent / 6) * 6;
@@ -2631,8 +2669,8 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
 
 int ba_create(slk_ctx* ctx) {
     ctx->ba = new BaState();
-    SLK_TRY(ctx->ba->flags.ensure(4 * sizeof(int)));
-    SLK_HIP(hipMemset(ctx->ba->flags.ptr, 0, 4 * sizeof(int)));
+    SLK_TRY(ctx->ba->flags.ensure(kBaFlags * sizeof(int)));
+    SLK_HIP(hipMemset(ctx->ba->flags.ptr, 0, kBaFlags * sizeof(int)));
     if (hipDeviceGetAttribute(&ctx->ba->cus, hipDeviceAttributeMultiprocessorCount,
                               ctx->device) != hipSuccess)
         return fail(SLK_E_HIP, "hipDeviceGetAttribute(multiProcessorCount) failed");
@@ -2750,6 +2788,7 @@ SolveArgs solve_args(BaState* s, const PlanDev& plan, const IterArgs& I) {
     A.dx_dbg = s->dx_dbg.as<double>();
     A.dx = s->dx.as<float>();
     A.flags = s->flags.as<int>();
+    A.halt = nullptr;
     A.poses = I.poses;
     A.poses_prev = s->fz ? s->poses_prev.as<float>() : nullptr;
     A.poses_next = nullptr;
@@ -2777,7 +2816,9 @@ int iterate_classic(slk_ctx* ctx, BaState* s, const IterArgs& I, hipStream_t str
     const int HW = ctx->HW, M = s->M;
     const PlanDev plan = plan_ptrs(s);
     {
-        ProfScope ps(ctx, "ba_lin_kf", stream);
+        // one profile name per kernel: k_ba_lin_wv (one wave per edge) or
+        // k_ba_lin_kf (edge by edge, when a row has two edges)
+        ProfScope ps(ctx, s->lin_by_wave ? "ba_lin_wv" : "ba_lin_kf", stream);
         hipLaunchKernelGGL(s->lin_by_wave ? k_ba_lin_wv : k_ba_lin_kf, dim3(s->nch, s->N_kf),
                            dim3(kLinWG), 0, stream, plan, I.target, I.weight, I.poses, I.disps,
                            I.intr, I.ii_gpu, I.jj_gpu, I.eta, s->hpart.as<double>(),
@@ -2852,6 +2893,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     G.S = s->S_dbg.as<double>();
     G.b = s->b_dbg.as<double>();
     G.ready = nullptr;
+    G.flags = s->flags.as<int>();
     const SolveArgs A = solve_args(s, plan, I);
     const dim3 grid(s->nch, s->N_kf);
     // all workgroups resident at once (kFzWgPerCu per CU): the waiting ones
@@ -2885,6 +2927,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
             SolveArgs Ak = A;
             Ak.poses_prev = nullptr;
             Ak.poses_next = pp[(it + 1) & 1];
+            Ak.halt = s->flags.as<int>() + 5;
             const bool panel = s->n > kSmallN;
             if (it + 1 < iters) {
                 ProfScope ps(ctx, "ba_fz_step", stream);
@@ -2977,7 +3020,7 @@ extern "C" int slk_ba_set_wait_limit(slk_ctx* ctx, int polls) {
 
 extern "C" int slk_ba_status(slk_ctx* ctx, hipStream_t stream) {
     if (!ctx || !ctx->ba) return fail(SLK_E_ARG, "ba_status: null context");
-    int f[4];
+    int f[kBaFlags];
     SLK_HIP(hipMemcpyAsync(f, ctx->ba->flags.ptr, sizeof f, hipMemcpyDeviceToHost, stream));
     SLK_HIP(hipStreamSynchronize(stream));
     const int bad = f[1], gave_up = f[3];

@@ -96,11 +96,17 @@ def project(poses, disps, intr, ii, jj, h, w):
 
 
 def ba_problem(n=12, h=48, w=64, ii=None, jj=None, seed=3, fixed=2, noise_px=0.5,
-               rot_sigma=0.05, trans_sigma=0.1):
+               rot_sigma=0.05, trans_sigma=0.1, tz_step=0.0, disp_range=(0.2, 2.0)):
     """BA window: poses near identity, inverse depth U(0.2, 2.0), intrinsics
     fx=fy=60, cx=32, cy=24 scaled to (h, w) about the 48x64 base, targets =
-    exact reprojection + N(0, noise_px), weights U(0,1)^2, eta = 1e-6 (the
-    reference's initial damping, main.cu:745-748)."""
+    exact reprojection + N(0, noise_px) (clipped to +-1e6 px, which only
+    points near a camera plane reach), weights U(0,1)^2, eta = 1e-6 (the
+    reference's initial damping, main.cu:745-748). tz_step moves the free
+    frames forward: frame k's camera centre advances by tz_step * k along
+    the optical axis (translation z -= tz_step * k for k >= fixed), which puts
+    near points of forward edges behind MIN_DEPTH; disp_range replaces the
+    inverse-depth law's bounds. The defaults draw the same numbers as
+    always."""
     rng = np.random.default_rng(seed)
     if ii is None:
         ii, jj = cyclic_edges(n)
@@ -108,11 +114,22 @@ def ba_problem(n=12, h=48, w=64, ii=None, jj=None, seed=3, fixed=2, noise_px=0.5
     poses[:, 3:] = quat_from_rotvec(rng.normal(0.0, rot_sigma, size=(n, 3)))
     poses[:, :3] = rng.normal(0.0, trans_sigma, size=(n, 3))
     poses[:fixed] = [0, 0, 0, 0, 0, 0, 1]
+    if tz_step:
+        poses[fixed:, 2] -= tz_step * np.arange(fixed, n)
     poses = poses.astype(np.float32)
-    disps = rng.uniform(0.2, 2.0, size=(n, h, w)).astype(np.float32)
+    disps = rng.uniform(disp_range[0], disp_range[1], size=(n, h, w)).astype(np.float32)
     intr = np.array([60.0 * w / 64, 60.0 * h / 48, 32.0 * w / 64, 24.0 * h / 48], np.float32)
-    proj, _ = project(poses, disps, intr, ii, jj, h, w)
-    target = (proj + rng.normal(0.0, noise_px, size=proj.shape)).astype(np.float32)
+    proj, depth = project(poses, disps, intr, ii, jj, h, w)
+    target = np.clip(proj + rng.normal(0.0, noise_px, size=proj.shape), -1e6, 1e6)
+    if tz_step:
+        # a pixel behind MIN_DEPTH (homogeneous depth = depth * disp < 0.25,
+        # ba.cuh:117-122) keeps its weight but aims at its own grid position,
+        # so a step that brings it back in front has a residual of pixels,
+        # not of the exploding projection
+        zh = depth * disps[np.asarray(ii)].reshape(len(ii), -1)
+        grid = grid_coords(h, w)[None].astype(np.float64)
+        target = np.where((zh < 0.25)[:, None, :], grid + (target - proj), target)
+    target = target.astype(np.float32)
     weight = (rng.uniform(0.0, 1.0, size=proj.shape) ** 2).astype(np.float32)
     eta = np.full((n, h, w), 1e-6, np.float32)
     return dict(poses=poses, disps=disps, intr=intr, ii=np.asarray(ii, np.int32),

@@ -101,25 +101,31 @@ def _path_kernels(ctx):
     return set(ctx.profile())
 
 
-def _dense_keyframe_problem():
+def _dense_keyframe_problem(duplicate=False):
     """Keyframe 0 with edges to 9 free poses (10 E rows): more than the fused
-    path's 7 per keyframe, so the window takes the five-kernel iteration."""
+    path's 7 per keyframe, so the window takes the five-kernel iteration.
+    With `duplicate`, edge (0, 5) appears twice: E row (pose 5, keyframe 0)
+    then belongs to two edges, which the one-wave-per-edge linearization
+    cannot store, so the edge-serial k_ba_lin_kf runs."""
     n = 11
-    ii = [0] * 9 + [k for k in range(1, n - 1)]
-    jj = [k for k in range(2, n)] + [k + 1 for k in range(1, n - 1)]
+    ii = [0] * 9 + [k for k in range(1, n - 1)] + ([0] if duplicate else [])
+    jj = [k for k in range(2, n)] + [k + 1 for k in range(1, n - 1)] + ([5] if duplicate else [])
     ii, jj = np.asarray(ii, np.int32), np.asarray(jj, np.int32)
     return wl.ba_problem(n=n, h=12, w=16, ii=ii, jj=jj, seed=17, fixed=2)
 
 
-@pytest.mark.parametrize("case", ["window", "dense_keyframe"])
+@pytest.mark.parametrize("case", ["window", "dense_keyframe", "dense_keyframe_dup"])
 def test_iterate_n_matches_oracle_and_single_calls(slk, case):
     """slk_ba_iterate_n(3) against three chained oracle iterations and against
     three slk_ba_iterate calls: the cfg3 window runs the fused iteration (E
     rows and Schur products kept on chip, back-substitution folded into the
     next linearization, each solve in one launch with the next
-    linearization), the dense keyframe the five-kernel one."""
+    linearization), the dense keyframe the five-kernel one with one wave per
+    edge (k_ba_lin_wv), and the dense keyframe with a duplicated edge the
+    five-kernel one with the edge-serial linearization (k_ba_lin_kf)."""
     announce(f"ba iterate_n(3) {case}")
-    p = wl.ba_problem() if case == "window" else _dense_keyframe_problem()
+    p = (wl.ba_problem() if case == "window"
+         else _dense_keyframe_problem(duplicate=case == "dense_keyframe_dup"))
     h, w = p["h"], p["w"]
     ref_p, ref_d = p["poses"], p["disps"]
     for _ in range(3):
@@ -137,8 +143,12 @@ def test_iterate_n_matches_oracle_and_single_calls(slk, case):
     kernels = _path_kernels(ctx_a)
     if case == "window":
         assert {"ba_fz_lin", "ba_fz_asm", "ba_fz_step", "ba_fz_last"} <= kernels, kernels
+    elif case == "dense_keyframe":
+        assert {"ba_lin_wv", "ba_schur", "ba_backsub"} <= kernels, kernels
+        assert "ba_lin_kf" not in kernels, kernels
     else:
         assert {"ba_lin_kf", "ba_schur", "ba_backsub"} <= kernels, kernels
+        assert "ba_lin_wv" not in kernels, kernels
     for _ in range(3):
         b.iterate(ctx_b, 1e-4, 0.1)
     assert ctx_b.ba_status() == slk.SLK_OK
@@ -175,10 +185,14 @@ def test_iterate_n_not_spd_leaves_state_untouched(slk):
 
 def test_iterate_n_wait_give_up_is_reported(slk):
     """The bounded wait inside an overlapped step launch: with the limit set to
-    zero polls from the host, the linearization workgroups stop waiting for
-    their solve, skip the rest of their step and every launch still ends;
-    slk_ba_status reports it as SLK_E_HIP. With the default limit restored,
-    the next call on the same context runs normally and matches the oracle."""
+    zero from the host, every linearization workgroup gives up without a poll,
+    skipping its chunk's depth update and its next linearization, and every
+    launch still ends; slk_ba_status reports it as SLK_E_HIP. The state left
+    is the one slk.h states: the first step's solve ran (the poses take its
+    step), no chunk applied its depth update, and the call's later steps took
+    no step (the solve of the last launch saw the give-up). With the default
+    limit restored, the next call on the same context runs normally and
+    matches the oracle."""
     announce("ba iterate_n wait give-up (limit 0)")
     p = wl.ba_problem()
     dev = Dev(slk, p)
@@ -187,9 +201,16 @@ def test_iterate_n_wait_give_up_is_reported(slk):
     args = (d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"], d["ii"],
             d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1)
     ctx.ba_set_wait_limit(0)
-    ctx.ba_iterate_n(*args, 2)
-    assert ctx.ba_status() == slk.SLK_E_HIP
-    assert b"stopped waiting" in slk.lib().slk_last_error()
+    for iters in (2, 3):
+        dev.d["poses"].upload(p["poses"])
+        dev.d["disps"].upload(p["disps"])
+        ctx.ba_iterate_n(*args, iters)
+        assert ctx.ba_status() == slk.SLK_E_HIP
+        assert b"stopped waiting" in slk.lib().slk_last_error()
+        one = oracle_iter(p, p["poses"], p["disps"], 1e-4, 0.1)
+        assert norm_rel(dev.poses(), one["poses"]) < TOL, iters
+        assert norm_rel(dev.poses() - p["poses"], one["poses"] - p["poses"]) < TOL, iters
+        np.testing.assert_array_equal(dev.disps(), p["disps"])
     ctx.ba_set_wait_limit(-1)
     dev2 = Dev(slk, p)
     d2 = dev2.d
@@ -208,15 +229,21 @@ def test_iterate_n_wait_give_up_is_reported(slk):
 
 @pytest.mark.parametrize("duplicate", [True, False])
 def test_edge_cases_stereo_duplicates_absent_frame(slk, duplicate):
-    # with the duplicate (2, 3) edge the linearization runs edge by edge per
-    # keyframe (k_ba_lin_kf); without it, one wave per edge (k_ba_lin_wv)
+    # A stereo edge (1, 1), a frame (3) that is no keyframe and, optionally, a
+    # duplicated (2, 3) edge. Every keyframe here has at most 7 E-row slots,
+    # so a single iteration runs the fused path (k_ba_fz), whose E rows live
+    # in LDS; the duplicate's two edges then add into the same slot. The
+    # five-kernel path with a duplicated edge (k_ba_lin_kf) is the
+    # dense_keyframe_dup case of test_iterate_n_matches_oracle_and_single_calls.
     ii = np.array([0, 1, 2, 1, 2, 0, 1] + ([2] if duplicate else []), np.int32)
     jj = np.array([1, 2, 3, 0, 1, 2, 1] + ([3] if duplicate else []), np.int32)
     p = wl.ba_problem(n=4, h=6, w=8, ii=ii, jj=jj, seed=8, fixed=1)
     p["eta"] = np.random.default_rng(9).uniform(0, 1e-3, p["eta"].shape).astype(np.float32)
     dev = Dev(slk, p)
     ctx = slk.Context(6, 8, C=128, max_batch=1, levels=2)
+    ctx.profile_enable(True)
     dev.iterate(ctx, 1e-4, 0.1)
+    assert "ba_fz_lin" in _path_kernels(ctx)
     S, b, dx = ctx.ba_last_system()
     ref = oracle_iter(p, p["poses"], p["disps"], 1e-4, 0.1)
     assert norm_rel(S, ref["S"]) < 1e-7
@@ -383,6 +410,136 @@ def test_backend_geometry_1188(slk):
         assert norm_rel(dev.poses(), poses) < TOL, step
         assert norm_rel(dev.disps(), disps) < TOL, step
     ctx.close()
+
+
+def _homogeneous_depth(p):
+    """Homogeneous depth of every edge-pixel at the problem's poses: the
+    camera-j depth times the source pixel's inverse depth, the quantity
+    ba.cuh:117-122 compares with MIN_DEPTH = 0.25 (se3.cuh:6)."""
+    _, depth = wl.project(p["poses"], p["disps"], p["intr"], p["ii"], p["jj"], p["h"], p["w"])
+    return depth * p["disps"][p["ii"]].reshape(len(p["ii"]), -1)
+
+
+def test_iterate_n_masked_pixels_overlapped_steps(slk):
+    """The cfg3 window with the free frames moving forward (tz_step 0.1), so
+    5.5% of its edge-pixels, on five edges, lie behind MIN_DEPTH: their
+    weights and inverse depth are masked (ba.cuh:117-122) in every
+    linearization, including the overlapped step launches (k_ba_fz_step), whose
+    relinearization and depth update see them too. slk_ba_iterate_n(3)
+    against three chained oracle iterations, and S, b, dx of a single
+    iteration."""
+    announce("ba iterate_n(3) masked pixels (cfg3 window, tz_step 0.1)")
+    p = wl.ba_problem(seed=23, tz_step=0.1)
+    zh = _homogeneous_depth(p)
+    assert (zh < 0.25).mean() >= 0.05, (zh < 0.25).mean()
+    assert np.abs(zh - 0.25).min() > 1e-4  # no pixel the fp64 orders could classify apart
+    ref_p, ref_d = p["poses"], p["disps"]
+    refs = []
+    for _ in range(3):
+        ref = oracle_iter(p, ref_p, ref_d, 1e-4, 0.1)
+        assert ref["status"] == 0
+        refs.append(ref)
+        ref_p, ref_d = ref["poses"], ref["disps"]
+    one = Dev(slk, p)
+    ctx1 = slk.Context(p["h"], p["w"], max_batch=1)
+    one.iterate(ctx1, 1e-4, 0.1)
+    assert ctx1.ba_status() == slk.SLK_OK
+    S, b, dx = ctx1.ba_last_system()
+    assert norm_rel(S, refs[0]["S"]) < 1e-7
+    assert norm_rel(b, refs[0]["b"]) < 1e-7
+    assert norm_rel(dx, refs[0]["dx"]) < 1e-5
+    ctx1.close()
+    dev = Dev(slk, p)
+    ctx = slk.Context(p["h"], p["w"], max_batch=1)
+    ctx.profile_enable(True)
+    d = dev.d
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 3)
+    assert ctx.ba_status() == slk.SLK_OK
+    assert {"ba_fz_lin", "ba_fz_step", "ba_fz_last"} <= _path_kernels(ctx)
+    assert norm_rel(dev.poses(), ref_p) < TOL
+    assert norm_rel(dev.disps(), ref_d) < TOL
+    assert norm_rel(dev.poses() - p["poses"], ref_p - p["poses"]) < TOL
+    assert_close_rel(dev.poses(), ref_p, what="poses after iterate_n(3), masked")
+    assert_close_rel(dev.disps(), ref_d, what="disps after iterate_n(3), masked")
+    ctx.close()
+
+
+def test_iterate_n_all_pixels_masked(slk):
+    """Every edge-pixel behind MIN_DEPTH (SURVEY's forcible case): all
+    weights are masked, so H and the gradients vanish, S is the damping
+    ep * I, dx = 0 and every inverse depth stays as it was. Run through the
+    overlapped fused steps of slk_ba_iterate_n(3)."""
+    announce("ba iterate_n(3) every pixel masked")
+    ii = np.array([0, 1, 0, 1, 2], np.int32)
+    jj = np.array([2, 3, 3, 2, 3], np.int32)
+    p = wl.ba_problem(n=4, h=12, w=16, ii=ii, jj=jj, seed=6, fixed=1, tz_step=1.0,
+                      disp_range=(1.0, 2.0))
+    assert (_homogeneous_depth(p) < 0.25).all()
+    ref = oracle_iter(p, p["poses"], p["disps"], 1e-4, 0.1)
+    assert ref["status"] == 0
+    assert not ref["dx"].any() and not ref["b"].any()
+    np.testing.assert_array_equal(ref["disps"], p["disps"])
+    dev = Dev(slk, p)
+    ctx = slk.Context(12, 16, max_batch=1, levels=2)
+    ctx.profile_enable(True)
+    d = dev.d
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-4, 0.1, 3)
+    assert ctx.ba_status() == slk.SLK_OK
+    assert {"ba_fz_step", "ba_fz_last"} <= _path_kernels(ctx)
+    S, b, dx = ctx.ba_last_system()
+    assert not dx.any() and not b.any()
+    np.testing.assert_array_equal(S, np.diag(np.diag(S)))  # the damping alone
+    np.testing.assert_allclose(np.diag(S), np.float32(0.1), rtol=1e-12)
+    np.testing.assert_array_equal(S, ref["S"])
+    np.testing.assert_array_equal(dev.disps(), p["disps"])
+    assert_close_rel(dev.poses(), ref["poses"], what="poses, every pixel masked")
+    ctx.close()
+
+
+def test_backend_full_size_iterate_n5(slk):
+    """Config backend's BA leg at its real size: 200 keyframes of 48x64,
+    backend_edges(200, 2000), 198 free poses (a 1188 x 1188 Schur system),
+    the reference backend's lm = 1e-5, ep = 1e-2 (main.cu:2486-2489), five
+    iterations in one slk_ba_iterate_n call against five chained oracle
+    iterations; S and b (1e-7) and dx (1e-5) of a single iteration first."""
+    announce("ba backend full size: 200 x 48x64, 2000 edges, iterate_n(5)")
+    ii, jj = wl.backend_edges(200, 2000)
+    p = wl.ba_problem(n=200, h=48, w=64, ii=ii, jj=jj, seed=21)
+    one = Dev(slk, p)
+    ctx1 = slk.Context(48, 64, max_batch=1)
+    one.iterate(ctx1, 1e-5, 1e-2)
+    assert ctx1.ba_status() == slk.SLK_OK
+    S, b, dx = ctx1.ba_last_system()
+    ctx1.close()
+    dev = Dev(slk, p)
+    ctx = slk.Context(48, 64, max_batch=1)
+    d = dev.d
+    ctx.ba_iterate_n(d["poses"], d["disps"], d["intr"], d["target"], d["weight"], d["eta"],
+                     d["ii"], d["jj"], p["ii"], p["jj"], p["t0"], p["t1"], 1e-5, 1e-2, 5)
+    assert ctx.ba_status() == slk.SLK_OK
+    got_p, got_d = dev.poses(), dev.disps()
+    ctx.close()
+    poses, disps = p["poses"], p["disps"]
+    for it in range(5):
+        ref = orc.ba_iterate(poses, disps, p["intr"], p["target"], p["weight"], p["eta"],
+                             p["ii"], p["jj"], 48, 64, p["t0"], p["t1"], 1e-5, 1e-2)
+        announce(f"  oracle iteration {it + 1} of 5 done")
+        assert ref["status"] == 0
+        if it == 0:
+            assert S.shape == (1188, 1188)
+            assert norm_rel(S, ref["S"]) < 1e-7
+            assert norm_rel(b, ref["b"]) < 1e-7
+            assert norm_rel(dx, ref["dx"]) < 1e-5
+            assert_close_rel(one.poses(), ref["poses"], what="poses after one iteration")
+            assert_close_rel(one.disps(), ref["disps"], what="disps after one iteration")
+        poses, disps = ref["poses"], ref["disps"]
+    assert norm_rel(got_p, poses) < TOL
+    assert norm_rel(got_d, disps) < TOL
+    assert norm_rel(got_p - p["poses"], poses - p["poses"]) < TOL
+    assert_close_rel(got_p, poses, what="poses after iterate_n(5)")
+    assert_close_rel(got_d, disps, what="disps after iterate_n(5)")
 
 
 # ------------------------------------------------------------ stage kernels --
