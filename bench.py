@@ -60,7 +60,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "corr edges/sec + BA iters/sec (48-edge window, 1 MI355X); % roofline"
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (matrix and vector)
-PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 # HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
 # (profiles/corr_window48_pmc_traffic.md)
@@ -222,20 +222,23 @@ def window(args, slk, wl, H, name):
     # windows stored). `achieved` is the reference's algorithmic work, 2*HW^2*C
     # flops per edge (the volume GEMM of main.cu:1573-1581), over the average
     # launch duration, against the dense MFMA peak of the datapath the kernel
-    # runs on (bf16 for the default 3-pass hi/lo split, fp32 for SLK_PREC_FP32).
-    # The split issues 3 bf16 MFMA passes per product and the kernel skips
-    # target tiles that hold no window cell: `mfma_issued_*` is the bf16 MFMA
-    # work it actually issued (active 128x256 tiles x C x 2 x 3) in the same
-    # time, and `frac_ceiling_of_method` = algorithmic / issued flops is the
-    # highest `frac` this method reaches with the MFMA pipes always busy.
+    # runs on (fp16 for the default 3-pass scaled hi/lo split, bf16 for the
+    # bf16 split: both 2.5 PFLOP/s dense; fp32 for SLK_PREC_FP32). The split
+    # issues 3 MFMA passes per product of fp32 features and the kernel skips
+    # target tiles that hold no window cell: `mfma_issued_*` is the MFMA work
+    # it actually issued (active 128x256 tiles x C x 2 x 3) in the same time,
+    # and `frac_ceiling_of_method` = algorithmic / issued flops is the highest
+    # `frac` this method reaches with the MFMA pipes always busy.
     flop = 2.0 * HW * HW * C * B
     gemm_s = kern["corr_window"]["avg_us"] * 1e-6
     achieved = flop / gemm_s / 1e12
-    split = ctx.corr_precision == slk.SLK_PREC_BF16X3
-    peak = PEAK_BF16_TFLOPS if split else PEAK_FP32_TFLOPS
+    split = ctx.corr_precision in (slk.SLK_PREC_F16X3, slk.SLK_PREC_BF16X3)
+    f16 = ctx.corr_precision == slk.SLK_PREC_F16X3
+    peak = PEAK_F16_TFLOPS if split else PEAK_FP32_TFLOPS
     roof = {
-        "kernel": (f"corr_window (bf16x3-split MFMA: all-pairs volume at every pyramid level, "
-                   f"lookup windows stored; {B} edges)" if split else
+        "kernel": (f"corr_window ({'scaled fp16' if f16 else 'bf16'} hi/lo split, 3 MFMA "
+                   f"passes: all-pairs volume at every pyramid level, lookup windows stored; "
+                   f"{B} edges)" if split else
                    f"corr_window (fp32 MFMA all-pairs GEMM + pyramid epilogue, {B} edges)"),
         "bound": "mfma",
         "achieved": round(achieved, 2),
@@ -252,7 +255,7 @@ def window(args, slk, wl, H, name):
         roof.update({"active_tiles": int(active), "tiles": int(total),
                      "mfma_issued_flop_per_launch": exe,
                      "mfma_issued_TFLOPs": round(exe / gemm_s / 1e12, 2),
-                     "mfma_issued_frac": round(exe / gemm_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "mfma_issued_frac": round(exe / gemm_s / 1e12 / PEAK_F16_TFLOPS, 4),
                      "frac_ceiling_of_method": round(flop / exe, 4)})
     # lookup: coords + four 8x8 windows read, 196 channels written per pixel
     look_bytes = B * HW * (2 * 4 + 4 * 64 * 4 + 196 * 4)
@@ -270,8 +273,8 @@ def window(args, slk, wl, H, name):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("f32 (correlation: f32 features as a 3-pass bf16 hi/lo MFMA split, f32 "
-                  "accumulation) / f64 (BA arithmetic and storage)"),
+        "dtype": ("f32 (correlation: f32 features as a 3-pass scaled fp16 hi/lo MFMA split, "
+                  "22 significant bits, f32 accumulation) / f64 (BA arithmetic and storage)"),
         "data": "synthetic (seeded N(0,1) features, U(-8,8) flow, BA window of workloads.py)",
         "config": {"workload": cfg["workload"], "frames": n, "edges": B, "h": h,
                    "w": w, "C": C, "levels": 4, "radius": 3, "ba_iters_per_step": iters,
@@ -378,7 +381,7 @@ def backend(args, slk, wl, H):
         "n_gpus": 1,
         "steps": steps,
         "higher_is_better": True,
-        "dtype": "f32 correlation (bf16x3 MFMA) / f64 BA",
+        "dtype": "f32 correlation (scaled fp16 hi/lo split, 3 MFMA passes) / f64 BA",
         "data": "synthetic (workloads.py backend graph)",
         "config": {"workload": "backend corr + 5x ba", "frames": n, "edges": M, "h": h, "w": w,
                    "C": C, "free_poses": p["t1"] - p["t0"], "system": 6 * (p["t1"] - p["t0"]),
@@ -477,7 +480,7 @@ def encode(args, slk, wl, H):
     wall = time.perf_counter() - t0w
     d_ms = timed(dec, k)
     fl = encoder_flops(Hf, Wf, 128) + encoder_flops(Hf, Wf, 256)
-    peak = PEAK_BF16_TFLOPS
+    peak = PEAK_F16_TFLOPS
     # decode bytes: the 2x2 Y neighbourhoods and UV samples come through
     # the caches; algorithmic = Y plane + UV plane read once, BGR written
     dec_bytes = sw * sh * 1.5 + Hf * Wf * 12
@@ -561,7 +564,7 @@ def update(args, slk, wl, H):
     e_ms = timed(eta, k)
     ff, fe = update_flops(h, w, B, K)
     f_fl, e_fl = sum(ff.values()), sum(fe.values())
-    peak = PEAK_BF16_TFLOPS  # dense fp16 MFMA peak equals the bf16 one
+    peak = PEAK_F16_TFLOPS
     zr_fl = ff["update_gru_convz"] + ff["update_gru_convr"]
     tc = time.perf_counter()
     uo.update_forward(P, corr[:1], motion[:1], net[:1], inp[:1])

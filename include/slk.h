@@ -43,15 +43,31 @@ typedef enum {
 
 typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
 
-/* Contraction used for fp32 features:
- *  SLK_PREC_BF16X3 (default) -- hi/lo bf16 split, three bf16 MFMA passes,
- *                               ~3e-5 relative to the row scale;
- *  SLK_PREC_FP32             -- fp32 MFMA (v_mfma_f32_32x32x2f32).
- * fp16 features are exact in either form: the batched path splits them like
- * fp32 (hi + lo represents every fp16 value), the single-edge path uses fp16
- * MFMA products with fp32 accumulation (the arithmetic of the reference's
- * cublasGemmEx on its fp16 fmaps, main.cu:1508-1515). */
-typedef enum { SLK_PREC_BF16X3 = 0, SLK_PREC_FP32 = 1 } slk_corr_precision;
+/* Contraction used for the features:
+ *  SLK_PREC_F16X3 (default)  -- batched path: every pixel's features scaled by
+ *                               a power of two (its largest magnitude into
+ *                               [2^14, 2^15)) and split into fp16 hi + lo
+ *                               (22 significant bits), three fp16 MFMA passes
+ *                               hi.hi + hi.lo + lo.hi with fp32 accumulation,
+ *                               ~1e-6 relative to the row scale. fp16 features
+ *                               are their own hi (lo = 0): a level-0 target
+ *                               tile takes the one pass hi.hi, the exact fp16
+ *                               products of the reference's cublasGemmEx on
+ *                               its fp16 fmaps (main.cu:1508-1515,1573-1581),
+ *                               a pooled-level tile two.
+ *  SLK_PREC_BF16X3           -- hi/lo bf16 split without a scale, three bf16
+ *                               MFMA passes, ~5e-5 relative to the row scale.
+ *  SLK_PREC_FP32             -- fp32 MFMA (v_mfma_f32_32x32x2f32) for fp32
+ *                               features.
+ * The single-edge path (slk_corr_build) splits fp32 features into bf16 hi/lo
+ * under either split precision, and multiplies fp16 features as fp16 MFMA
+ * products with fp32 accumulation. The split precisions need C a multiple of
+ * 16 and at most 128 in the batched path; other C take fp32 MFMA. */
+typedef enum {
+    SLK_PREC_BF16X3 = 0,
+    SLK_PREC_FP32 = 1,
+    SLK_PREC_F16X3 = 2
+} slk_corr_precision;
 
 /* ---------------------------------------------------------------- context */
 
@@ -115,13 +131,14 @@ int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fmaps, int dty
  * reference's backend update (run_update_pass over batches of 48 edges,
  * main.cu:2197-2203) rebuilds each frame's operands in every batch that
  * touches it. slk_corr_prepare_frames splits frames [0, nframes) of fmaps
- * (all levels, bf16 hi/lo; 2*C*(h*w*85/64) bytes per frame, held by the
+ * (all levels, hi/lo; ~2*C*(h*w*85/64) bytes per frame, held by the
  * context until the next call or slk_destroy); the _prepared calls then
  * take ii_host/jj_host as frame indices into them and compute the batches
  * without that step. Call it again whenever fmaps change. Results are
  * bitwise those of slk_corr_batch_build_and_sample on the same fmaps. Needs
- * the split contraction (C a multiple of 16; fp16 fmaps, or fp32 with
- * SLK_PREC_BF16X3). */
+ * the split contraction (C a multiple of 16 up to 128; fp16 fmaps, or fp32
+ * with SLK_PREC_F16X3 or SLK_PREC_BF16X3), and the precision of the calls
+ * that follow is the one in force at slk_corr_prepare_frames. */
 int slk_corr_prepare_frames(slk_ctx* ctx, const void* fmaps, int dtype, long fmap_stride,
                             int nframes, hipStream_t stream);
 int slk_corr_batch_build_and_sample_prepared(slk_ctx* ctx, const int* ii_host,

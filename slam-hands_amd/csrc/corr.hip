@@ -811,7 +811,8 @@ int corr_alloc(slk_ctx* ctx) {
 using namespace slk;
 
 extern "C" int slk_set_corr_precision(slk_ctx* ctx, int precision) {
-    if (!ctx || (precision != SLK_PREC_BF16X3 && precision != SLK_PREC_FP32))
+    if (!ctx || (precision != SLK_PREC_BF16X3 && precision != SLK_PREC_FP32 &&
+                 precision != SLK_PREC_F16X3))
         return fail(SLK_E_ARG, "set_corr_precision: bad argument");
     ctx->corr_prec = precision;
     return SLK_OK;
@@ -1051,7 +1052,7 @@ extern "C" int slk_corr_batch_build_and_sample_dev_noalloc(
     c.levels = kMaxLevels;
     c.radius = 3;
     c.alpha = corr_scale;
-    c.corr_prec = SLK_PREC_BF16X3;
+    c.corr_prec = SLK_PREC_F16X3;
     for (int l = 0; l < kMaxLevels; l++) {
         c.lh[l] = h >> l;
         c.lw[l] = w >> l;

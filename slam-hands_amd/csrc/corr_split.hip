@@ -19,22 +19,35 @@
 // every intermediate is exact and the windows are bitwise equal.
 //
 // Stage 1 (k_feat_prep), once per frame a launch uses: the fp32 pooled
-// features of levels 1..3 (formed in LDS from level 0) and a bf16 hi/lo split
-// of all levels (hi = rne(x), lo = rne(x - hi)), stored chunk-major
-// [plane][C/16][rows][16] so a 16-channel chunk of consecutive rows is one
-// contiguous block.
+// features of levels 1..3 (formed in LDS from level 0) and a hi/lo split of
+// every pixel of all levels, stored chunk-major [plane][C/16][rows][16] so a
+// 16-channel chunk of consecutive rows is one contiguous block, followed by
+// one float per row: the inverse of the row's split scale.
+//   fp16 split (SLK_PREC_F16X3, the default): each pixel's features are
+//   scaled by a power of two 2^e chosen from the pixel's largest magnitude
+//   m over the channels (m * 2^e in [2^14, 2^15)), then hi = rne_f16(x 2^e),
+//   lo = rne_f16(x 2^e - hi): 22 significant bits, the dropped lo.lo term
+//   ~2^-22 relative. fp16 features are taken with e >= 0, which makes hi
+//   exact and lo zero at level 0.
+//   bf16 split (SLK_PREC_BF16X3): hi = rne_bf16(x), lo = rne_bf16(x - hi),
+//   no scale (16 significant bits, lo.lo ~2^-16).
 // Stage 2 (tile_mask_edge, workgroups of the same launch as stage 1): which
 // (edge, source tile, target tile) pairs hold any window cell; the others are
 // never computed.
 // Stage 3 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
-// hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_bf16 (exact products, fp32
-// accumulation; the dropped lo.lo term is ~2^-16 relative), staging 16-channel
-// chunks through LDS in a 3-stage ring filled by direct-to-LDS loads, so the
-// loads of chunk k+2 are in flight during the MFMAs of chunk k. The
-// accumulator tile is then transposed through LDS ([target][source]), and the
-// window cells that fall inside the tile are read back with one lane per
-// (source, window column), walking the 8 window rows: each masked store
-// covers one row of 8 sources' windows. Only ~2% of the level-0 products are
+// hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_f16 (or _bf16) (exact
+// products, fp32 accumulation), staging 16-channel chunks through LDS in a
+// 3-stage ring filled by direct-to-LDS loads, so the loads of chunk k+2 are in
+// flight during the MFMAs of chunk k. A pass whose operand plane is zero is
+// not issued: with fp16 features every level-0 lo is zero, so a level-0 tile
+// takes the one pass hi.hi (the reference's fp16 x fp16 -> fp32 products,
+// main.cu:1573-1581) and a pooled tile hi.hi + hi.lo. The accumulator tile
+// is then transposed through LDS ([target][source]), each target column
+// multiplied by its inverse scale on the way, and the window cells that fall
+// inside the tile are read back with one lane per (source, window column),
+// walking the 8 window rows: each masked store covers one row of 8 sources'
+// windows, multiplied by alpha times the source's inverse scale (powers of
+// two: the scaling adds no rounding). Only ~2% of the level-0 products are
 // window cells, and none of them costs more than its LDS round trip.
 #include <algorithm>
 #include <climits>
@@ -113,10 +126,14 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // feature preparation they do not depend on.
 // (k_feat_prep launches with kT = 512 or 1024 threads a workgroup; the
 // tile-mask chain of an edge then sorts with kT / 64 waves.)
-// the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
-// which a tile-mask workgroup uses for its sort's histograms or its bitmap
-constexpr int kPrepRows = 8, kPrepCols = 64;
-constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
+// the preparation's level-0 block (every channel, at most kPrepMaxC, of 8 x 8
+// pixels) in LDS, which a tile-mask workgroup uses for its sort's histograms
+// or its bitmap
+constexpr int kPrepB = 8;
+constexpr int kPrepMaxC = 128;
+constexpr int kPrepLdsWords = kPrepMaxC * kPrepB * kPrepB;
+// pixels of a block over the four levels: 8 x 8, 4 x 4, 2 x 2, 1
+constexpr int kPrepPix = 64 + 16 + 4 + 1;
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
 constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
 constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
@@ -257,8 +274,11 @@ __device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds
         return std::min(std::max(oy, -8), g.h[0]) + 8;
     };
     // the coordinates of kG chunks are loaded before the first is used; when
-    // a wave's pixels are one such group they stay in registers for the scatter
-    constexpr int kG = 12;
+    // a wave's pixels are one such group they stay in registers for the
+    // scatter. 1024-thread workgroups serve maps up to 4096 pixels, 256 a
+    // wave: 4 chunks, which keeps the launch within 64 VGPRs (two
+    // workgroups a CU)
+    constexpr int kG = kT >= 1024 ? 4 : 12;
     float xv[kG], yv[kG];
     auto load = [&](int pg) {
 #pragma unroll
@@ -437,137 +457,241 @@ __device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned
     if (tid == 0) ctr[kCtrCount + e] = base;
 }
 
-// Feature preparation of one frame slot, one launch: a workgroup takes a
-// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
-// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
-// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
-// a pooled pixel's parents always lie in the block), and writes the bf16
-// hi/lo split of every pixel of the levels present, 16 channels = 32 bytes
-// per pixel and plane, into out[slot][plane][C/16][Ttot][16]. `pooled` = 0
-// writes level 0 only (source slots). One-dimensional grid: first, when
-// mk.list is set, one tile-mask workgroup per edge (tile_mask_edge, with
-// the level-0 and level-1 LDS arrays; they are the longer chains, so they are
-// dispatched first), then the blocks x C/16 x slots preparation workgroups
-// (block fastest).
+// Split modes of the preparation and the window kernel
+enum { kSplitBF16 = 0, kSplitF16 = 1 };
+
+// hi = rne_f16(x), lo = rne_f16(x - hi), packed as lo << 16 | hi (|x| < 2^15:
+// x - hi is exact in fp32, hi never overflows)
+__device__ __forceinline__ unsigned split_f16(float x) {
+    const _Float16 h = (_Float16)x;
+    const _Float16 l = (_Float16)(x - (float)h);
+    return (unsigned)__builtin_bit_cast(unsigned short, h) |
+           ((unsigned)__builtin_bit_cast(unsigned short, l) << 16);
+}
+
+// The exponent e of a pixel's fp16 split scale 2^e from its largest magnitude
+// m over the channels: m * 2^e in [2^14, 2^15), so every scaled feature and
+// its hi stay below 2^15 (fp16 holds up to 65504), bounded to [-120, 120]
+// (2^+-e stays a normal float; a bound only lowers m * 2^e); 0 for m = 0 or
+// non-finite. `exact`: at least 0 (fp16 features at level 0: then x 2^e is
+// exact in fp16 and lo is zero).
+__device__ __forceinline__ int split_exponent(float m, bool exact) {
+    int e = 0;
+    if (m > 0.0f && m <= 3.402823466e38f) {
+        e = 15 - __builtin_amdgcn_frexp_expf(m);  // m = f 2^k, f in [0.5, 1)
+        e = std::min(std::max(e, -120), 120);
+        if (exact) e = std::max(e, 0);
+    }
+    return e;
+}
+
+// Feature preparation of one frame slot, one launch. A workgroup takes an
+// 8 x 8 block of level-0 pixels with every channel (C <= kPrepMaxC) into an LDS
+// image F[pixel][channel] (pixels 0..63 the block's level-0 pixels in row
+// order, 64..79 its 4 x 4 level-1 pixels, 80..83 the 2 x 2 of level 2, 84 the
+// level-3 pixel; channels fastest, the pixel stride padded to 132 floats so
+// that 16-byte reads of consecutive pixels spread over the banks). Threads
+// (channel, level-2 pixel) form a level-2 pixel's four level-1 pixels and
+// itself, then threads (channel) the level-3 pixel, each pooled value
+// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first.
+// Threads (pixel, 16-channel group) find each pixel's largest magnitude over
+// the channels (their group's, then a DPP maximum over the eight groups in
+// consecutive lanes), which gives its split scale; threads (pixel, chunk)
+// then scale and split 16 channels and write them, 32 bytes per pixel and
+// plane, to out[slot][plane][C/16][Ttot][16], and each pixel's inverse scale
+// to the slot's row-scale array. `pooled` = 0 writes level 0 only (source
+// slots). One-dimensional grid: first, when mk.list is set, one tile-mask
+// workgroup per edge (tile_mask_edge, in the LDS of the image; they are the
+// longer chains, so they are dispatched first), then the blocks x slots
+// preparation workgroups, remapped so that each XCD takes a contiguous run
+// of blocks: a block's rows are 32-byte pieces of 128-byte lines whose other
+// pieces belong to its neighbours in x.
+constexpr int kPrepLd = kPrepMaxC + 4;  // floats per pixel of the LDS image
+static_assert(kPrepPix * kPrepLd >= kPrepLdsWords + 2048, "mask LDS inside the image");
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                         0u, __builtin_bit_cast(unsigned, v), kCtrl, 0xF, 0xF,
+                                         false));
+}
+// the largest m over each group of 8 consecutive lanes, by DPP: lanes xor 1,
+// xor 2, then the mirrored lane within 8
+__device__ __forceinline__ float max8(float m) {
+    m = fmaxf(m, dpp_f<0xB1>(m));      // quad_perm [1, 0, 3, 2]
+    m = fmaxf(m, dpp_f<0x4E>(m));      // quad_perm [2, 3, 0, 1]
+    return fmaxf(m, dpp_f<0x141>(m));  // row_half_mirror
+}
+
 template <typename Tin, int kT>
-__global__ __launch_bounds__(kT) void k_feat_prep(const Tin* __restrict__ fm, long fstride,
-                                                   SlotFrames sf, int slot_lo,
-                                                   unsigned short* __restrict__ out, Geom g,
-                                                   int pooled, int vec, int nbx, int nblk,
-                                                   int nmask, MaskArgs mk) {
-    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
-    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
-    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
-    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
+__global__ __launch_bounds__(kT, kT >= 1024 ? 2 : 1) void k_feat_prep(
+    const Tin* __restrict__ fm, long fstride, SlotFrames sf, int slot_lo,
+    unsigned short* __restrict__ out, long slot_elems, Geom g, int pooled, int vec, int nbx,
+    int nblk, int nprep, int nmask, MaskArgs mk, int mode) {
+    __shared__ __attribute__((aligned(16))) float F[kPrepPix * kPrepLd];
+    __shared__ float pscale[kPrepPix];  // 2^e of each pixel of the block
+    __shared__ int trow[kPrepPix];      // target row of each pixel, or -1
     __shared__ int wave_sum[kT / 64];
     if ((int)blockIdx.x < nmask) {  // uniform
         // the tile-mask chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        tile_mask_edge<kT>(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]),
-                       reinterpret_cast<unsigned*>(&l1[0][0][0]), (int)(sizeof(l1) / 4), wave_sum);
+        unsigned* lds = reinterpret_cast<unsigned*>(F);
+        tile_mask_edge<kT>(mk, g, blockIdx.x, lds, lds + kPrepLdsWords, 2048, wave_sum);
         return;
     }
     const int tid = threadIdx.x;
-    const int b = blockIdx.x - nmask;
-    const int blk = b % nblk, rest = b / nblk;
+    const int j = xcd_remap((int)blockIdx.x - nmask, nprep);
+    const int blk = j % nblk, s = slot_lo + j / nblk;
     const int bx = blk % nbx, by = blk / nbx;
-    const int k = rest % (g.C / kChunk), s = slot_lo + rest / (g.C / kChunk);
-    const int W = g.w[0], H = g.h[0];
-    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
-    // all of a thread's loads are issued before the first is used
-    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kT;
-    float ld[kPer];
+    const int W = g.w[0], H = g.h[0], C = g.C;
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride;
+    const int y0 = by * kPrepB, x0 = bx * kPrepB;
+    // level 0: channel fastest across the lanes (consecutive LDS words); every
+    // load goes out before the first is stored
     if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
-        // four consecutive pixels of a row a lane (all inside or all outside)
+        constexpr int kPer = kPrepMaxC * kPrepB * 2 / kT;  // float4 of 4 pixels each
+        float4 v[kPer];
 #pragma unroll
-        for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kT);
-            const int c = i / (kPrepRows * kPrepCols);
-            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-            const bool in = yy < H && xx < W;
-            const float4 v = ldf4(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-            ld[4 * u] = in ? v.x : 0.0f;
-            ld[4 * u + 1] = in ? v.y : 0.0f;
-            ld[4 * u + 2] = in ? v.z : 0.0f;
-            ld[4 * u + 3] = in ? v.w : 0.0f;
+        for (int u = 0; u < kPer; u++) {
+            const int i = tid + u * kT;
+            const int c = i & (kPrepMaxC - 1), r = i >> 8, x = ((i >> 7) & 1) * 4;
+            const bool in = c < C && y0 + r < H && x0 + x < W;
+            v[u] = ldf4(src + (in ? (long)c * g.HW + (long)(y0 + r) * W + x0 + x : 0L));
+            if (!in) v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
-        for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kT);
-            *reinterpret_cast<float4*>(
-                &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
-                make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
+        for (int u = 0; u < kPer; u++) {
+            const int i = tid + u * kT;
+            const int c = i & (kPrepMaxC - 1), p = (i >> 8) * kPrepB + ((i >> 7) & 1) * 4;
+            F[p * kPrepLd + c] = v[u].x;
+            F[(p + 1) * kPrepLd + c] = v[u].y;
+            F[(p + 2) * kPrepLd + c] = v[u].z;
+            F[(p + 3) * kPrepLd + c] = v[u].w;
         }
     } else {
+        constexpr int kPer = kPrepMaxC * kPrepB * kPrepB / kT;
+        float v[kPer];
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
             const int i = tid + u * kT;
-            const int c = i / (kPrepRows * kPrepCols);
-            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-            const bool in = yy < H && xx < W;
-            ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-            if (!in) ld[u] = 0.0f;
+            const int c = i & (kPrepMaxC - 1), p = i >> 7, r = p >> 3, x = p & 7;
+            const bool in = c < C && y0 + r < H && x0 + x < W;
+            v[u] = ldf(src + (in ? (long)c * g.HW + (long)(y0 + r) * W + x0 + x : 0L));
+            if (!in) v[u] = 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
             const int i = tid + u * kT;
-            l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
+            F[(i >> 7) * kPrepLd + (i & (kPrepMaxC - 1))] = v[u];
         }
     }
+    // the target row of each pixel of the block, -1 outside its level's map
+    // (or above level 0 for a source slot)
+    for (int pp = tid; pp < kPrepPix; pp += kT) {
+        int l = 0, q = pp, side = kPrepB;
+        if (pp >= 84) {
+            l = 3, q = 0, side = 1;
+        } else if (pp >= 80) {
+            l = 2, q = pp - 80, side = 2;
+        } else if (pp >= 64) {
+            l = 1, q = pp - 64, side = 4;
+        }
+        const int yy = by * side + q / side, xx = bx * side + q % side;
+        const bool ok = (pooled || l == 0) && l < g.levels && yy < g.h[l] && xx < g.w[l];
+        trow[pp] = ok ? g.off[l] + yy * g.w[l] + xx : -1;
+    }
     __syncthreads();
-    const size_t plane = (size_t)g.C * g.Ttot;
-    unsigned short* const base = out + (size_t)s * 2 * plane + (size_t)k * g.Ttot * kChunk;
-    auto emit = [&](int t, const float (&v)[kChunk]) {
+    if (pooled) {
+        // thread (channel, level-2 pixel q): the four level-1 pixels of q
+        // from their 2x2 parents, then q from them
+        for (int i = tid; i < kPrepMaxC * 4; i += kT) {
+            const int c = i & (kPrepMaxC - 1), q = i >> 7, y2 = q >> 1, x2 = q & 1;
+            float l1[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int y1 = 2 * y2 + (k >> 1), x1 = 2 * x2 + (k & 1);
+                const float* a = F + ((2 * y1) * kPrepB + 2 * x1) * kPrepLd + c;
+                float sum = a[0] + a[kPrepLd];
+                sum = sum + a[kPrepB * kPrepLd];
+                sum = sum + a[(kPrepB + 1) * kPrepLd];
+                l1[k] = 0.25f * sum;
+                F[(64 + y1 * 4 + x1) * kPrepLd + c] = l1[k];
+            }
+            float sum = l1[0] + l1[1];
+            sum = sum + l1[2];
+            sum = sum + l1[3];
+            F[(80 + q) * kPrepLd + c] = 0.25f * sum;
+        }
+        __syncthreads();
+        for (int c = tid; c < kPrepMaxC; c += kT) {  // level 3 from the level-2 pixels
+            const float* a = F + 80 * kPrepLd + c;
+            float sum = a[0] + a[kPrepLd];
+            sum = sum + a[2 * kPrepLd];
+            sum = sum + a[3 * kPrepLd];
+            F[84 * kPrepLd + c] = 0.25f * sum;
+        }
+        __syncthreads();
+    }
+    const int npx = pooled ? kPrepPix : 64;
+    const int nck = C / kChunk;
+    if (mode == kSplitF16) {  // uniform
+        // thread (pixel, group of 16 channels), groups in consecutive lanes
+        constexpr bool kHalf = std::is_same<Tin, _Float16>::value;
+        for (int i = tid; i < npx * 8; i += kT) {  // whole groups of 8 lanes
+            const int pp = i >> 3, grp = i & 7;
+            float m = 0.0f;
+            if (grp < nck) {
+                const float4* a = reinterpret_cast<const float4*>(F + pp * kPrepLd + grp * kChunk);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 t = a[u];
+                    m = fmaxf(fmaxf(m, fabsf(t.x)), fabsf(t.y));
+                    m = fmaxf(fmaxf(m, fabsf(t.z)), fabsf(t.w));
+                }
+            }
+            m = max8(m);
+            if (grp == 0)
+                pscale[pp] = __builtin_amdgcn_ldexpf(1.0f, split_exponent(m, kHalf && pp < 64));
+        }
+    } else {
+        for (int pp = tid; pp < npx; pp += kT) pscale[pp] = 1.0f;
+    }
+    __syncthreads();
+    // thread (pixel, chunk), pixels fastest: a row of 8 level-0 pixels is
+    // 256 contiguous bytes of a chunk
+    const size_t plane = (size_t)C * g.Ttot;
+    unsigned short* const base = out + (size_t)s * slot_elems;
+    for (int i = tid; i < npx * nck; i += kT) {
+        const int pp = i % npx, k = i / npx;
+        const int t = trow[pp];
+        if (t < 0) continue;
+        const float sc = pscale[pp];
+        const float4* a = reinterpret_cast<const float4*>(F + pp * kPrepLd + k * kChunk);
         u16x8_t hi[2], lo[2];
 #pragma unroll
-        for (int u = 0; u < kChunk; u++) {
-            const unsigned pk = split_bf16(v[u]);
-            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
-            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+        for (int u = 0; u < 4; u++) {
+            const float4 t4 = a[u];
+            const float xs[4] = {t4.x, t4.y, t4.z, t4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int ch = 4 * u + e;
+                const unsigned pk =
+                    mode == kSplitF16 ? split_f16(xs[e] * sc) : split_bf16(xs[e]);
+                hi[ch >> 3][ch & 7] = (unsigned short)(pk & 0xffffu);
+                lo[ch >> 3][ch & 7] = (unsigned short)(pk >> 16);
+            }
         }
-        unsigned short* o = base + (size_t)t * kChunk;
+        unsigned short* o = base + (size_t)k * g.Ttot * kChunk + (size_t)t * kChunk;
         *reinterpret_cast<u16x8_t*>(o) = hi[0];
         *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
         *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
         *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
-    };
-    // level 0
-    for (int p = tid; p < kPrepRows * kPrepCols; p += kT) {
-        const int r = p / kPrepCols, x = p % kPrepCols;
-        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-        if (yy >= H || xx >= W) continue;
-        float v[kChunk];
-#pragma unroll
-        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
-        emit(yy * W + xx, v);
     }
-    if (!pooled) return;
-    // pooled levels: level l from level l-1 in LDS, then its pixels out
-    auto level = [&](auto& dst, const auto& src, int l, int rows, int cols) {
-        for (int i = tid; i < kChunk * rows * cols; i += kT) {
-            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
-            float sum = src[c][2 * r][2 * x] + src[c][2 * r][2 * x + 1];
-            sum = sum + src[c][2 * r + 1][2 * x];
-            sum = sum + src[c][2 * r + 1][2 * x + 1];
-            dst[c][r][x] = 0.25f * sum;
-        }
-        __syncthreads();
-        for (int p = tid; p < rows * cols; p += kT) {
-            const int r = p / cols, x = p % cols;
-            const int yy = by * rows + r, xx = bx * cols + x;
-            if (yy >= g.h[l] || xx >= g.w[l]) continue;
-            float v[kChunk];
-#pragma unroll
-            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
-            emit(g.off[l] + yy * g.w[l] + xx, v);
-        }
-    };
-    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
-    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
-    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
+    // the rows' inverse scales (exact powers of two)
+    float* const rs = reinterpret_cast<float*>(base + 2 * plane);
+    for (int pp = tid; pp < npx; pp += kT)
+        if (trow[pp] >= 0) rs[trow[pp]] = 1.0f / pscale[pp];
 }
 
 struct alignas(16) SplitSmem {
@@ -586,6 +710,8 @@ struct alignas(16) SplitSmem {
     int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
     int pix[kSrcTile];        // pixel of each source
+    float sfac[2 * kSrcTile]; // [2 r], [2 r + 1]: inverse split scale of source row r
+    float tfac[kTgtTile];     // inverse split scale of each target row of the tile
 };
 
 // One direct-to-LDS load per lane (16 or 4 bytes): lane l reads p and writes
@@ -603,8 +729,8 @@ __device__ __forceinline__ void dma_x1(const void* p, unsigned lds) {
 __device__ __forceinline__ unsigned lds_addr(const void* p) { return (unsigned)(size_t)p; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
-// lgkmcnt 11:8): vmcnt(6) lgkmcnt(0), vmcnt(0) lgkmcnt(0), and lgkmcnt(0) alone
-constexpr int kWaitVm6Lgkm0 = 0x0076;
+// lgkmcnt 11:8): vmcnt(n) lgkmcnt(0) is 0x0070 | n for n < 16; vmcnt(0)
+// lgkmcnt(0), and lgkmcnt(0) alone
 constexpr int kWaitVm0Lgkm0 = 0x0070;
 constexpr int kWaitLgkm0 = 0xC07F;
 
@@ -618,10 +744,20 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+// one 32x32x16 MFMA of the split mode's operand type
+template <bool kF16>
+__device__ __forceinline__ f32x16 mfma_split(u16x8_t a, u16x8_t b, f32x16 c) {
+    if constexpr (kF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0,
+                                                       0);
 }
+
+template <bool B>
+using bool_c = std::integral_constant<bool, B>;
 
 // Grid: a fixed number of workgroups of 256 threads, two per CU, each taking
 // marked tiles (tile_mask_edge) one at a time from its XCD's counter: tile
@@ -633,11 +769,16 @@ __device__ __forceinline__ f32x16 mfma_bf16(u16x8_t a, u16x8_t b, f32x16 c) {
 // blocks. Source tile mt holds sorted positions mt*128..+127 of the edge's
 // order (tile_mask_edge): the A rows are gathered through the order's pixel
 // column, the coordinates come from its sorted copies, and each source's
-// windows are stored at its own pixel.
+// windows are stored at its own pixel. kF16: fp16 operands (the scaled fp16
+// split), else bf16. alo = 0: every source lo is zero (fp16 features, fp16
+// split), and so is every level-0 target lo: a tile of level-0 targets then
+// takes the one pass hi.hi, a tile with pooled targets hi.hi + hi.lo.
+template <bool kF16>
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
-    const unsigned short* __restrict__ feat, EdgeSlots es, const int* __restrict__ order,
-    float* __restrict__ win, int slot0, Geom g, float alpha, int mtiles, int ntiles,
-    int nedges, const int* __restrict__ list, int* __restrict__ ctr) {
+    const unsigned short* __restrict__ feat, long slot_elems, EdgeSlots es,
+    const int* __restrict__ order, float* __restrict__ win, int slot0, Geom g, float alpha,
+    int mtiles, int ntiles, int nedges, const int* __restrict__ list, int* __restrict__ ctr,
+    int alo) {
     __shared__ SplitSmem sm;
     __shared__ int next_tile;
     const int tpe = mtiles * ntiles;
@@ -689,8 +830,10 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int HW = g.HW, Ttot = g.Ttot;
     const int p0 = mt * kSrcTile, t0 = nt * kTgtTile;
     const size_t plane = (size_t)g.C * Ttot;
-    const unsigned short* fa = feat + (size_t)es.si[e] * 2 * plane;
-    const unsigned short* fb = feat + (size_t)es.sj[e] * 2 * plane;
+    const unsigned short* fa = feat + (size_t)es.si[e] * slot_elems;
+    const unsigned short* fb = feat + (size_t)es.sj[e] * slot_elems;
+    const float* sca = reinterpret_cast<const float*>(fa + 2 * plane);  // row scales
+    const float* scb = reinterpret_cast<const float*>(fb + 2 * plane);
     const int* ord = order + (size_t)e * 3 * HW;
 
     // Staging by direct-to-LDS loads (global_load_lds_dwordx4): lane l of wave
@@ -710,15 +853,6 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
     const size_t kstep = (size_t)Ttot * kChunk;
     const int wdst = wave * 512;  // this wave's 1 KB of a 4 KB region, in u16
-    auto issue = [&](int k, int st) {
-        const size_t o = (size_t)k * kstep;
-        dma_x4(ga + o, lds_addr(&sm.u.st.A[st][0][wdst]));
-        dma_x4(ga + plane + o, lds_addr(&sm.u.st.A[st][1][wdst]));
-        dma_x4(gb0 + o, lds_addr(&sm.u.st.B[st][0][wdst]));
-        dma_x4(gb1 + o, lds_addr(&sm.u.st.B[st][0][2048 + wdst]));
-        dma_x4(gb0 + plane + o, lds_addr(&sm.u.st.B[st][1][wdst]));
-        dma_x4(gb1 + plane + o, lds_addr(&sm.u.st.B[st][1][2048 + wdst]));
-    };
 
     f32x16 acc[2][4];
 #pragma unroll
@@ -730,76 +864,115 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // lane's row is bit 2 xor bit 3 of l%32
     const int orow = lane & 31;
     const int ooff = orow * kChunk + ((((lane >> 5) ^ (((orow >> 2) ^ (orow >> 3)) & 1))) * 8);
-    auto compute = [&](int st) {
-        // every operand read of the step goes out first, in the order the
-        // MFMAs use them, so the matrix cores wait for the first reads only;
-        // each accumulator takes lo.hi, hi.lo, then hi.hi (the small cross
-        // terms before the large one)
-        u16x8_t ah[2], al[2], bh[4], bl[4];
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-            al[sb] = *reinterpret_cast<const u16x8_t*>(
-                &sm.u.st.A[st][1][(wm * 64 + sb * 32) * kChunk + ooff]);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-            bh[tb] = *reinterpret_cast<const u16x8_t*>(
-                &sm.u.st.B[st][0][(wn * 128 + tb * 32) * kChunk + ooff]);
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-            ah[sb] = *reinterpret_cast<const u16x8_t*>(
-                &sm.u.st.A[st][0][(wm * 64 + sb * 32) * kChunk + ooff]);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-            bl[tb] = *reinterpret_cast<const u16x8_t*>(
-                &sm.u.st.B[st][1][(wn * 128 + tb * 32) * kChunk + ooff]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int sb = 0; sb < 2; sb++)
-                acc[sb][tb] = mfma_bf16(al[sb], bh[tb], acc[sb][tb]);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int sb = 0; sb < 2; sb++)
-                acc[sb][tb] = mfma_bf16(ah[sb], bl[tb], acc[sb][tb]);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int sb = 0; sb < 2; sb++)
-                acc[sb][tb] = mfma_bf16(ah[sb], bh[tb], acc[sb][tb]);
-    };
-
-    // Pipeline: at step k the loads of chunks k and k+1 are in flight; wait
-    // for this thread's chunk k (6 loads) and for every wave at the barrier --
-    // after which chunk k is in LDS and stage (k+2)%3, last read at step k-1,
-    // is free for chunk k+2. The wait and barrier are explicit because a
-    // workgroup fence would also wait for chunk k+1.
     const int nk = g.C / kChunk;
-    issue(0, 0);
-    // coordinates of the tile's sources, in flight with the first chunk
-    // (also by a direct-to-LDS load: every load the pipeline waits on with
-    // vmcnt is of the same kind, and those complete in issue order)
-    {
-        const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
-        const int pc = std::min(p0 + half * 64 + lane, HW - 1);
-        dma_x1(ord + (size_t)(1 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
-    }
-    if (nk > 1) issue(1, 1);
-    // While in its chunk loop a wave issues at raised priority, so that on a
-    // SIMD shared with the other workgroup's extracting wave the MFMA issue
-    // goes first and the extraction takes the slots left over.
-    __builtin_amdgcn_s_setprio(1);
-    for (int k = 0; k < nk; k++) {
-        if (k + 1 < nk)
-            __builtin_amdgcn_s_waitcnt(kWaitVm6Lgkm0);
+    // The chunk loop of one tile, with (kA) or without the source lo plane
+    // and (kB) with or without the target lo plane: a plane that is zero is
+    // neither staged nor multiplied.
+    auto chunk_loop = [&](auto a_lo, auto b_lo) {
+        constexpr bool kA = decltype(a_lo)::value, kB = decltype(b_lo)::value;
+        constexpr int kLoads = 3 + (kA ? 1 : 0) + (kB ? 2 : 0);  // loads per chunk and thread
+        auto issue = [&](int k, int st) {
+            const size_t o = (size_t)k * kstep;
+            dma_x4(ga + o, lds_addr(&sm.u.st.A[st][0][wdst]));
+            if constexpr (kA) dma_x4(ga + plane + o, lds_addr(&sm.u.st.A[st][1][wdst]));
+            dma_x4(gb0 + o, lds_addr(&sm.u.st.B[st][0][wdst]));
+            dma_x4(gb1 + o, lds_addr(&sm.u.st.B[st][0][2048 + wdst]));
+            if constexpr (kB) {
+                dma_x4(gb0 + plane + o, lds_addr(&sm.u.st.B[st][1][wdst]));
+                dma_x4(gb1 + plane + o, lds_addr(&sm.u.st.B[st][1][2048 + wdst]));
+            }
+        };
+        auto compute = [&](int st) {
+            // every operand read of the step goes out first, in the order the
+            // MFMAs use them, so the matrix cores wait for the first reads
+            // only; each accumulator takes lo.hi, hi.lo, then hi.hi (the small
+            // cross terms before the large one)
+            u16x8_t ah[2], al[2], bh[4], bl[4];
+            if constexpr (kA)
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+                    al[sb] = *reinterpret_cast<const u16x8_t*>(
+                        &sm.u.st.A[st][1][(wm * 64 + sb * 32) * kChunk + ooff]);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++)
+                bh[tb] = *reinterpret_cast<const u16x8_t*>(
+                    &sm.u.st.B[st][0][(wn * 128 + tb * 32) * kChunk + ooff]);
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+                ah[sb] = *reinterpret_cast<const u16x8_t*>(
+                    &sm.u.st.A[st][0][(wm * 64 + sb * 32) * kChunk + ooff]);
+            if constexpr (kB)
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+                    bl[tb] = *reinterpret_cast<const u16x8_t*>(
+                        &sm.u.st.B[st][1][(wn * 128 + tb * 32) * kChunk + ooff]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kA)
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                    for (int sb = 0; sb < 2; sb++)
+                        acc[sb][tb] = mfma_split<kF16>(al[sb], bh[tb], acc[sb][tb]);
+            if constexpr (kB)
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                    for (int sb = 0; sb < 2; sb++)
+                        acc[sb][tb] = mfma_split<kF16>(ah[sb], bl[tb], acc[sb][tb]);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                for (int sb = 0; sb < 2; sb++)
+                    acc[sb][tb] = mfma_split<kF16>(ah[sb], bh[tb], acc[sb][tb]);
+        };
+
+        // Pipeline: at step k the loads of chunks k and k+1 are in flight;
+        // wait for this thread's chunk k (kLoads loads) and for every wave at
+        // the barrier -- after which chunk k is in LDS and stage (k+2)%3,
+        // last read at step k-1, is free for chunk k+2. The wait and barrier
+        // are explicit because a workgroup fence would also wait for chunk
+        // k+1.
+        issue(0, 0);
+        // coordinates and row scales of the tile's sources and the scales of
+        // its targets, in flight with the first chunk (also by direct-to-LDS
+        // loads: every load the pipeline waits on with vmcnt is of the same
+        // kind, and those complete in issue order)
+        {
+            const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
+            const int pc = std::min(p0 + half * 64 + lane, HW - 1);
+            dma_x1(ord + (size_t)(1 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
+            dma_x1(sca + pa, lds_addr(&sm.sfac[wave * 64]));  // sfac[tid]: row tid / 2
+            dma_x1(scb + std::min(t0 + tid, Ttot - 1), lds_addr(&sm.tfac[wave * 64]));
+        }
+        if (nk > 1) issue(1, 1);
+        // While in its chunk loop a wave issues at raised priority, so that on
+        // a SIMD shared with the other workgroup's extracting wave the MFMA
+        // issue goes first and the extraction takes the slots left over.
+        __builtin_amdgcn_s_setprio(1);
+        for (int k = 0; k < nk; k++) {
+            if (k + 1 < nk)
+                __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0 | kLoads);  // vmcnt(kLoads) lgkmcnt(0)
+            else
+                __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_barrier();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
+            compute(k % kStages);
+        }
+    };
+    if constexpr (kF16) {
+        // a target tile with a pooled row has lo planes (pooled fp16 values
+        // are fp32 sums)
+        const bool blo = alo || (g.levels > 1 && t0 + kTgtTile > g.off[1]);
+        if (alo)
+            chunk_loop(bool_c<true>{}, bool_c<true>{});
+        else if (blo)
+            chunk_loop(bool_c<false>{}, bool_c<true>{});
         else
-            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_barrier();
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
-        compute(k % kStages);
+            chunk_loop(bool_c<false>{}, bool_c<false>{});
+    } else {
+        chunk_loop(bool_c<true>{}, bool_c<true>{});
     }
     __builtin_amdgcn_s_setprio(0);
     if (tid == 0) next_tile = lo + taken;  // read after the end-of-tile barrier
@@ -847,21 +1020,24 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     for (int sb = 0; sb < 2; sb++) {
         if (sb) lds_barrier();  // the first half's cells have all been read
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++)
+        for (int tb = 0; tb < 4; tb++) {
+            const int t = wn * 128 + tb * 32 + orow;
+            const float tf = sm.tfac[t];  // the target's inverse split scale
 #pragma unroll
             for (int gq = 0; gq < 4; gq++) {
-                const int t = wn * 128 + tb * 32 + orow;
                 const int s = wm * 32 + gq * 8 + khalf * 4;
                 *reinterpret_cast<float4*>(&sm.u.T[t][s]) =
-                    make_float4(acc[sb][tb][4 * gq], acc[sb][tb][4 * gq + 1],
-                                acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
+                    make_float4(acc[sb][tb][4 * gq] * tf, acc[sb][tb][4 * gq + 1] * tf,
+                                acc[sb][tb][4 * gq + 2] * tf, acc[sb][tb][4 * gq + 3] * tf);
             }
+        }
         lds_barrier();
 #pragma unroll
         for (int grp = 0; grp < 2; grp++) {
             const int s = wave * 16 + grp * 8 + g8;                 // column of T
             const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
             const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
+            const float fs = alpha * sm.sfac[2 * lsrc];  // alpha / the source's scale
             const bool pin = p0 + lsrc < HW;
             const float* Tcol = &sm.u.T[0][s];
             // byte offset of cell (cx, row 0) of level 0 in the slot
@@ -891,7 +1067,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++)
                     __builtin_amdgcn_raw_buffer_store_b32(
-                        __builtin_bit_cast(unsigned, alpha * v[cy]), wrs,
+                        __builtin_bit_cast(unsigned, fs * v[cy]), wrs,
                         ok[cy] ? woff + (l * 8 + cy) * HW * 32 : kBufDiscard, 0, 0);
             }
         }
@@ -918,50 +1094,66 @@ Geom make_geom(const slk_ctx* ctx) {
     return g;
 }
 
+// u16 elements of one frame slot: the hi and lo planes [C/16][Ttot][16], then
+// the rows' inverse split scales (Ttot floats), padded to 256 bytes
+size_t slot_elems(const Geom& g) {
+    return (2 * (size_t)g.C * g.Ttot + 2 * (size_t)g.Ttot + 127) / 128 * 128;
+}
+
+// the split of fp32 (or fp16) features under the context's precision
+int split_mode(const slk_ctx* ctx) {
+    return ctx->corr_prec == SLK_PREC_BF16X3 ? kSplitBF16 : kSplitF16;
+}
+
 // the preparation of nslots frame slots and, when mk.list is set, the tile
 // mask of mk.nedges edges, in one launch
 template <typename Tin>
 int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
                   int slot_lo, int nslots, bool pooled, const MaskArgs& mk, unsigned short* out,
-                  hipStream_t stream) {
-    const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
-    const int nblk = nbx * ((g.h[0] + kPrepRows - 1) / kPrepRows);
-    const long nprep = (long)nblk * (g.C / kChunk) * std::max(nslots, 0);
+                  int mode, hipStream_t stream) {
+    const int nbx = (g.w[0] + kPrepB - 1) / kPrepB;
+    const int nblk = nbx * ((g.h[0] + kPrepB - 1) / kPrepB);
+    const long nprep = (long)nblk * std::max(nslots, 0);
     const long nmask = mk.list ? mk.nedges : 0;
     if (nprep + nmask == 0) return SLK_OK;
     if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
     // vector loads of 4 pixels when every row starts 4-element aligned
     const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
-    // 1024-thread workgroups (16-wave mask chains) for maps up to 4096
-    // pixels, 512 above: measured, 20.3 against 21.8 us at 48x64 and 39.3
-    // against 32.6 us at 54x96, where the preparation's share is larger
-    if (g.HW <= 4096)
+    const long se = (long)slot_elems(g);
+    // 512-thread workgroups (8-wave mask chains): three a CU, so the 576
+    // preparation workgroups and 48 mask chains of the 48-edge window at
+    // 48x64 all start at once (24.3 against 27.0 us with 1024-thread
+    // workgroups, two a CU, where the last 112 waited for a CU)
+    if (g.HW <= 0)
         hipLaunchKernelGGL((k_feat_prep<Tin, 1024>), dim3((unsigned)(nprep + nmask)), dim3(1024),
-                           0, stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk);
+                           0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
+                           vec ? 1 : 0, nbx, nblk, (int)nprep, (int)nmask, mk, mode);
     else
         hipLaunchKernelGGL((k_feat_prep<Tin, 512>), dim3((unsigned)(nprep + nmask)), dim3(512),
-                           0, stream, fm, fstride, sf, slot_lo, out, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk);
+                           0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
+                           vec ? 1 : 0, nbx, nblk, (int)nprep, (int)nmask, mk, mode);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
 
 template <typename Tin>
 int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
-               int slot_lo, int nslots, bool pooled, const MaskArgs& mk, hipStream_t stream) {
+               int slot_lo, int nslots, bool pooled, const MaskArgs& mk, int mode,
+               hipStream_t stream) {
     return prep_slots_to(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk,
-                         ctx->split_feat.as<unsigned short>(), stream);
+                         ctx->split_feat.as<unsigned short>(), mode, stream);
 }
 
 // The tile-mask workgroups (with the preparation of nslots slots when
 // nslots > 0) and the window kernel over `feat`, for edges whose slots are es.
+// mode: the split of `feat`; alo: whether its level-0 lo planes can be
+// nonzero (not for fp16 features under the fp16 split).
 template <typename Tin>
 int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf,
                      const Geom& g, int slot_lo, int nslots, bool pooled, const EdgeSlots& es,
                      const unsigned short* feat, int n, const float* coords, float* win,
-                     int slot0, hipStream_t stream) {
+                     int slot0, int mode, bool alo, hipStream_t stream) {
     const int mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const long total = (long)n * mtiles * ntiles;
@@ -974,13 +1166,21 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     {
         // feature preparation and the tile mask, one launch
         ProfScope ps(ctx, "corr_feat_prep", stream);
-        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, stream));
+        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
     }
     {
         ProfScope ps(ctx, "corr_window", stream);
-        hipLaunchKernelGGL(k_corr_split_win, dim3(ctx->ws_grid), dim3(256), 0, stream, feat, es,
-                           ctx->src_order.as<int>(), win, slot0, g, ctx->alpha, mtiles, ntiles, n,
-                           ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>());
+        const long se = (long)slot_elems(g);
+        if (mode == kSplitF16)
+            hipLaunchKernelGGL(k_corr_split_win<true>, dim3(ctx->ws_grid), dim3(256), 0, stream,
+                               feat, se, es, ctx->src_order.as<int>(), win, slot0, g, ctx->alpha,
+                               mtiles, ntiles, n, ctx->tile_list.as<int>(),
+                               ctx->tile_ctr.as<int>(), alo ? 1 : 0);
+        else
+            hipLaunchKernelGGL(k_corr_split_win<false>, dim3(ctx->ws_grid), dim3(256), 0, stream,
+                               feat, se, es, ctx->src_order.as<int>(), win, slot0, g, ctx->alpha,
+                               mtiles, ntiles, n, ctx->tile_list.as<int>(),
+                               ctx->tile_ctr.as<int>(), 1);
     }
     SLK_HIP(hipGetLastError());
     return SLK_OK;
@@ -994,6 +1194,8 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     SlotFrames sf{};
     EdgeSlots es{};
     const unsigned short* feat = ctx->split_feat.as<unsigned short>();
+    const int mode = split_mode(ctx);
+    const bool alo = !(mode == kSplitF16 && std::is_same<Tin, _Float16>::value);
     if (ii_host) {
         int ns = 0;
         auto slot_of = [&](int f) {
@@ -1007,7 +1209,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
             es.sj[e] = slot_of(jj_host[e]);
         }
         return mask_and_windows(ctx, fm, fstride, sf, g, 0, ns, true, es, feat, n, coords, win,
-                                slot0, stream);
+                                slot0, mode, alo, stream);
     }
     sf.da = ii_dev;
     sf.db = jj_dev;
@@ -1020,22 +1222,24 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     {
         ProfScope ps(ctx, "corr_feat_prep", stream);
         const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
-        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, stream));
+        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, mode, stream));
     }
     return mask_and_windows(ctx, fm, fstride, sf, g, n, n, true, es, feat, n, coords, win, slot0,
-                            stream);
+                            mode, alo, stream);
 }
 
 }  // namespace
 
-bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
+bool corr_split_supported(const slk_ctx* ctx) {
+    return ctx->C % kChunk == 0 && ctx->C <= kPrepMaxC;
+}
 
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
                           size_t* order_per_edge, size_t* ctr_bytes) {
     const Geom g = make_geom(ctx);
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
-    *slot_bytes = 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short);
+    *slot_bytes = slot_elems(g) * sizeof(unsigned short);
     *tiles_per_edge = mtiles * ntiles * sizeof(int);
     *order_per_edge = 3 * (size_t)g.HW * sizeof(int);
     *ctr_bytes = kCtrInts * sizeof(int);
@@ -1047,7 +1251,7 @@ int corr_split_alloc(slk_ctx* ctx) {
     if (!corr_split_supported(ctx)) return SLK_OK;
     const Geom g = make_geom(ctx);
     const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
-    SLK_TRY(ctx->split_feat.ensure(slots * 2 * (size_t)g.C * g.Ttot * sizeof(unsigned short)));
+    SLK_TRY(ctx->split_feat.ensure(slots * slot_elems(g) * sizeof(unsigned short)));
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
@@ -1090,7 +1294,7 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
                        hipStream_t stream) {
     if (nframes <= 0) return fail(SLK_E_ARG, "corr_prepare_frames: nframes <= 0");
     const Geom g = make_geom(ctx);
-    const size_t bytes = (size_t)nframes * 2 * g.C * g.Ttot * sizeof(unsigned short);
+    const size_t bytes = (size_t)nframes * slot_elems(g) * sizeof(unsigned short);
     if (bytes > ctx->prep_feat.bytes && ctx->prep_feat.ptr)
         SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old frames
     SLK_TRY(ctx->prep_feat.ensure(bytes));
@@ -1098,13 +1302,17 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     sf.ident = 1;
     const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
     ProfScope ps(ctx, "corr_prepare_frames", stream);
+    const int mode = split_mode(ctx);
     if (dtype == SLK_F32)
         SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,
-                              true, none, ctx->prep_feat.as<unsigned short>(), stream));
+                              true, none, ctx->prep_feat.as<unsigned short>(), mode, stream));
     else
         SLK_TRY(prep_slots_to(ctx, static_cast<const _Float16*>(fmaps), fstride, sf, g, 0,
-                              nframes, true, none, ctx->prep_feat.as<unsigned short>(), stream));
+                              nframes, true, none, ctx->prep_feat.as<unsigned short>(), mode,
+                              stream));
     ctx->prep_nframes = nframes;
+    ctx->prep_mode = mode;
+    ctx->prep_alo = !(mode == kSplitF16 && dtype == SLK_F16);
     return SLK_OK;
 }
 
@@ -1121,7 +1329,8 @@ int corr_split_windows_prepared(slk_ctx* ctx, const int* ii_host, const int* jj_
     }
     const SlotFrames none{};
     return mask_and_windows(ctx, static_cast<const float*>(nullptr), 0, none, g, 0, 0, true, es,
-                            ctx->prep_feat.as<unsigned short>(), n, coords, win, slot0, stream);
+                            ctx->prep_feat.as<unsigned short>(), n, coords, win, slot0,
+                            ctx->prep_mode, ctx->prep_alo, stream);
 }
 
 }  // namespace slk

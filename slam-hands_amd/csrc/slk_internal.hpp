@@ -69,16 +69,18 @@ struct slk_ctx {
     int device = 0;
     int h = 0, w = 0, HW = 0, C = 0, levels = 4, radius = 3, max_batch = 48;
     float alpha = 1.0f / 16.0f;
-    int corr_prec = SLK_PREC_BF16X3;  // contraction of fp32 features
+    int corr_prec = SLK_PREC_F16X3;  // contraction of fp32 features
     int lh[slk::kMaxLevels] = {0}, lw[slk::kMaxLevels] = {0};
     // batched-path scratch: 8x8 lookup windows [max_batch][4 levels][8 rows][HW][8]
     slk::DevBuf batch_win;
-    // batched-path operands: bf16 hi/lo split of every level's features per
-    // frame slot
+    // batched-path operands: hi/lo split of every level's features per
+    // frame slot, with each row's inverse split scale
     slk::DevBuf split_feat;
     // frames split once by slk_corr_prepare_frames (slot = frame index)
     slk::DevBuf prep_feat;
     int prep_nframes = 0;
+    int prep_mode = 0;      // their split (fp16 scaled or bf16)
+    bool prep_alo = true;   // whether their level-0 lo planes can be nonzero
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
     slk::DevBuf src_order;  // per edge: sources sorted by window row (pixel, x, y columns)

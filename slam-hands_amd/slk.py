@@ -22,7 +22,7 @@ HIP_LIB = "libamdhip64.so"
 
 SLK_OK, SLK_E_ARG, SLK_E_HIP, SLK_E_NOT_SPD, SLK_E_STATE = range(5)
 SLK_F32, SLK_F16 = 0, 1
-SLK_PREC_BF16X3, SLK_PREC_FP32 = 0, 1
+SLK_PREC_BF16X3, SLK_PREC_FP32, SLK_PREC_F16X3 = 0, 1, 2
 
 # every entry point declared in include/slk.h
 EXPORTS = [
@@ -336,7 +336,7 @@ class Context:
 
     def __init__(self, h, w, C=128, max_batch=48, levels=4, radius=3, corr_scale=1.0 / 16.0):
         self.h, self.w, self.C, self.levels = h, w, C, levels
-        self.corr_precision = SLK_PREC_BF16X3  # the library's default
+        self.corr_precision = SLK_PREC_F16X3  # the library's default
         self.ptr = P()
         check(lib().slk_create(ctypes.byref(self.ptr), h, w, C, max_batch, levels, radius,
                                float(corr_scale)))

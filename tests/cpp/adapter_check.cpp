@@ -134,12 +134,13 @@ extern "C" int adapter_ba(int N, int h, int w, float* poses, float* disps, const
             ba.iterate(d_p, d_d, d_i, d_t, d_w, d_e, d_ii, d_jj, ii_h.data(), jj_h.data(), M,
                        t0, t1, lm, ep, motion_only != 0);
     if (launches) {
-        // launches of the linearization (five-kernel or fused iteration) and
-        // of the solve over all iterates; an overlapped fused step launch
-        // holds a solve and the next linearization, the last one a solve
+        // launches of the linearization (five-kernel iteration: one wave per
+        // edge or edge by edge; fused iteration) and of the solve over all
+        // iterates; an overlapped fused step launch holds a solve and the
+        // next linearization, the last one a solve
         const int steps = ba.profiled_launches("ba_fz_step");
-        launches[0] =
-            ba.profiled_launches("ba_lin_kf") + ba.profiled_launches("ba_fz_lin") + steps;
+        launches[0] = ba.profiled_launches("ba_lin_wv") + ba.profiled_launches("ba_lin_kf") +
+                      ba.profiled_launches("ba_fz_lin") + steps;
         launches[1] = ba.profiled_launches("ba_solve") + steps + ba.profiled_launches("ba_fz_last");
         ba.print_profile();
     }

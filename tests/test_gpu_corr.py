@@ -4,7 +4,8 @@ against the CPU oracle on the same seeded inputs.
 Bars: indexing, shapes and the pyramid of a given level 0 are bitwise; with
 integer-coded features (exact fp32 products and sums, alpha = 1/16) the whole
 chain is bitwise; fp32 N(0,1) values are within helpers.TOL = 1e-4 of the
-oracle's fp64-accumulated result, relative to max(|r|, rms(r)).
+oracle's fp64-accumulated result, relative to max(|r|, rms(r)), and within
+F16X3_TOL = 1e-5 under the batched path's default scaled fp16 split.
 """
 import numpy as np
 import pytest
@@ -14,6 +15,10 @@ from oracle import oracle as orc
 import workloads as wl
 
 pytestmark = pytest.mark.gpu
+
+# the batched path's scaled fp16 split (22 significant bits): its bar, a tenth
+# of the north-star tolerance
+F16X3_TOL = 1e-5
 
 
 @pytest.fixture(scope="module")
@@ -112,14 +117,15 @@ def test_nonfinite_and_far_coords_give_zeros(slk):
     assert_close_rel(out, orc.lookup(pyr, coords), tol=1e-5)
 
 
-def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, prec=0):
+def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, prec=None):
     f = wl.frames(nframes, C=128, h=h, w=w, seed=seed)
     ii, jj = wl.cyclic_edges(nframes)
     ii, jj = ii[:B], jj[:B]
     coords = wl.flow_coords(B, h, w, seed=seed + 1)
     alpha = 1.0 / 16.0
     ctx = slk.Context(h, w, C=128, max_batch=max_batch, corr_scale=alpha)
-    ctx.set_corr_precision(prec)
+    if prec is not None:  # else the library's default, SLK_PREC_F16X3
+        ctx.set_corr_precision(prec)
     fd = slk.DeviceArray.from_host(f)
     cd = slk.DeviceArray.from_host(coords)
     out = slk.DeviceArray((B, 196, h * w))
@@ -135,18 +141,20 @@ def _window(slk, nframes, h, w, B, seed, max_batch=48, dev_idx=False, prec=0):
     return f, ii, jj, coords, res
 
 
-@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("prec", [2, 0, 1])
 def test_window_48_edges_matches_oracle(slk, prec):
     """Config corr_window: 12 frames, 48 edges; every edge checked on sampled
-    pixels plus 6 edges in full (prec 0: bf16x3, 1: fp32 MFMA)."""
+    pixels plus 6 edges in full (prec 2: the scaled fp16 split, held to
+    F16X3_TOL; 0: the bf16 split; 1: fp32 MFMA)."""
     announce(f"corr window 48 edges prec={prec}")
     h, w = 48, 64
+    tol = F16X3_TOL if prec == 2 else TOL
     f, ii, jj, coords, out = _window(slk, 12, h, w, 48, seed=20, prec=prec)
     assert np.all(np.isfinite(out))
     full = [0, 7, 18, 29, 40, 47]
     ref = orc.corr_batch(f, ii[full], jj[full], coords[full], 1.0 / 16.0)
     for k, e in enumerate(full):
-        assert_close_rel(out[e], ref[k], what=f"edge {e}")
+        assert_close_rel(out[e], ref[k], tol=tol, what=f"edge {e}")
     # all 48 edges on 64 random pixels: direct fp64 evaluation of the windows
     rng = np.random.default_rng(0)
     pix = rng.choice(h * w, 64, replace=False)
@@ -158,7 +166,7 @@ def test_window_48_edges_matches_oracle(slk, prec):
         for _ in range(3):
             pyr.append(orc.avg_pool_2x2(pyr[-1]))
         ref_sub = _lookup_rows(pyr, coords[e][:, pix])
-        assert_close_rel(out[e][:, pix], ref_sub, what=f"edge {e} sampled")
+        assert_close_rel(out[e][:, pix], ref_sub, tol=tol, what=f"edge {e} sampled")
 
 
 @pytest.mark.parametrize("h,w", [(96, 128), (100, 128), (256, 24), (260, 80)])
@@ -246,12 +254,46 @@ def test_window_fp16_features(slk):
     got = out.to_host()
     ctx.close()
     ref = orc.corr_batch(f.astype(np.float32), ii, jj, coords, 1.0 / 16.0)
-    assert_close_rel(got, ref, what="fp16 window")
+    assert_close_rel(got, ref, tol=F16X3_TOL, what="fp16 window")
 
 
-def _window_of(slk, f, coords, ii, jj, alpha=1.0 / 16.0):
+def test_window_fp16_features_config2(slk):
+    """Config corr_window with the reference's fp16 fmaps (main.cu:677): 12
+    frames of 128x48x64, 48 edges. Under the scaled fp16 split an fp16 fmap
+    is its own hi (lo = 0): level-0 target tiles take the one pass hi.hi,
+    whose products are the exact fp16 x fp16 products of the reference's
+    cublasGemmEx (main.cu:1508-1515,1573-1581), pooled tiles hi.hi + hi.lo.
+    Six edges in full against the fp64 oracle on the fp16 values: level 0
+    (channels 0..48) is fp32 accumulation of exact products, the pooled
+    levels carry the 22-bit split of their fp32 means; a dropped pooled lo
+    pass would be ~2^-12 off and fail the bar."""
+    announce("corr window 48 edges, fp16 fmaps")
+    h, w, n, B = 48, 64, 12, 48
+    f = wl.frames(n, C=128, h=h, w=w, seed=22).astype(np.float16)
+    ii, jj = wl.cyclic_edges(n)
+    coords = wl.flow_coords(B, h, w, seed=23)
+    ctx = slk.Context(h, w, C=128, max_batch=B, corr_scale=1.0 / 16.0)
+    fd = slk.DeviceArray.from_host(f)
+    cd = slk.DeviceArray.from_host(coords)
+    out = slk.DeviceArray((B, 196, h * w))
+    ctx.batch_build_and_sample_correlation(fd, ii, jj, cd, out, dtype=slk.SLK_F16)
+    slk.hip().sync()
+    got = out.to_host()
+    ctx.close()
+    full = [0, 9, 21, 30, 38, 47]
+    ref = orc.corr_batch(f.astype(np.float32), ii[full], jj[full], coords[full], 1.0 / 16.0)
+    for k, e in enumerate(full):
+        print(f"edge {e}: level 0 {_err_ratio(got[e][:49], ref[k][:49]):.3g}, "
+              f"levels 1-3 {_err_ratio(got[e][49:], ref[k][49:]):.3g}")
+        assert_close_rel(got[e][:49], ref[k][:49], tol=1e-6, what=f"edge {e} level 0")
+        assert_close_rel(got[e], ref[k], tol=F16X3_TOL, what=f"edge {e}")
+
+
+def _window_of(slk, f, coords, ii, jj, alpha=1.0 / 16.0, prec=None):
     n, C, h, w = f.shape
     ctx = slk.Context(h, w, C=C, max_batch=len(ii), corr_scale=alpha)
+    if prec is not None:
+        ctx.set_corr_precision(prec)
     fd = slk.DeviceArray.from_host(f)
     cd = slk.DeviceArray.from_host(coords)
     out = slk.DeviceArray((len(ii), 196, h * w))
@@ -267,32 +309,35 @@ def _err_ratio(got, ref):
     return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms)))
 
 
-def test_split_precision_wide_range_and_coherent_lo(slk):
-    """Margins of the bf16 hi/lo split (hi.hi + hi.lo + lo.hi, lo.lo dropped)
-    where they are smallest:
+@pytest.mark.parametrize("prec", [2, 0])
+def test_split_precision_wide_range_and_coherent_lo(slk, prec):
+    """Margins of the hi/lo splits (hi.hi + hi.lo + lo.hi, lo.lo dropped)
+    where they are smallest, for the scaled fp16 split (prec 2, the default,
+    held to F16X3_TOL) and the bf16 split (prec 0, held to helpers.TOL):
     * wide dynamic range: every feature N(0,1) * 2^U(-8, 8), each channel
       also scaled by 2^U(-4, 4), so the result is dominated by a few large
       products and the small ones sit many binades below;
-    * coherent lo: every feature is +-(1 + 2^-8) * 2^k, the bf16 half-way
-      case (hi = 1, lo = 2^-8, the largest lo relative to hi), with signs
-      that agree along the channels, so the dropped lo.lo terms (2^-16 of
-      each product) add up instead of cancelling.
-    Both must stay within helpers.TOL of the fp64 oracle; the error ratios
-    are printed."""
+    * coherent lo: every feature is +-(1 + 2^-p) * 2^k, the split's half-way
+      case (p = 11 for fp16, 8 for bf16: hi = 1, lo = 2^-p, the largest lo
+      relative to hi), with signs that agree along the channels, so the
+      dropped lo.lo terms (2^-2p of each product) add up instead of
+      cancelling.
+    The error ratios are printed."""
     h, w, n = 24, 32, 5
+    bar, p = (F16X3_TOL, 11) if prec == 2 else (TOL, 8)
     ii, jj = wl.cyclic_edges(n)
     coords = wl.flow_coords(len(ii), h, w, seed=41)
     rng = np.random.default_rng(40)
     wide = (rng.standard_normal((n, 128, h, w)) * np.exp2(rng.uniform(-8, 8, (n, 128, h, w)))
             * np.exp2(rng.uniform(-4, 4, (1, 128, 1, 1)))).astype(np.float32)
     sign = np.where(rng.random((n, 1, h, w)) < 0.5, -1.0, 1.0)
-    coh = (sign * (1.0 + 2.0 ** -8) * np.exp2(rng.integers(-2, 3, (n, 1, h, w)))
+    coh = (sign * (1.0 + 2.0 ** -p) * np.exp2(rng.integers(-2, 3, (n, 1, h, w)))
            * np.ones((1, 128, 1, 1))).astype(np.float32)
     for name, f in (("wide range", wide), ("coherent lo", coh)):
-        got = _window_of(slk, f, coords, ii, jj)
+        got = _window_of(slk, f, coords, ii, jj, prec=prec)
         ref = orc.corr_batch(f, ii, jj, coords, 1.0 / 16.0)
-        print(f"{name}: max |g - r| / max(|r|, rms) = {_err_ratio(got, ref):.3g}")
-        assert_close_rel(got, ref, what=name)
+        print(f"prec {prec} {name}: max |g - r| / max(|r|, rms) = {_err_ratio(got, ref):.3g}")
+        assert_close_rel(got, ref, tol=bar, what=name)
 
 
 def test_device_indices_and_chunking(slk):
