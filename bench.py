@@ -97,6 +97,11 @@ def parse():
                     help="time the update-pass glue of one 48-edge batch instead")
     ap.add_argument("--cpu-edges", type=int, default=48,
                     help="edges of the window the CPU baseline runs (bounded sample)")
+    ap.add_argument("--fp16-fmaps", action="store_true",
+                    help="the window with fp16 feature maps (the reference's fmap storage)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="the headline line without the extra keys of configs 4 and 5 and of "
+                         "the fp16-fmap window")
     return ap.parse_args()
 
 
@@ -126,7 +131,42 @@ def main():
     if args.graph:
         return graph(args, slk, wl, H)
 
-    return window(args, slk, wl, H, "highres" if args.highres else "corr_window")
+    if args.highres or args.fp16_fmaps:
+        out = window(args, slk, wl, H, "highres" if args.highres else "corr_window",
+                     fp16=args.fp16_fmaps)
+        print(json.dumps(out), flush=True)
+        return
+    out = window(args, slk, wl, H, "corr_window")
+    if not args.no_extras:
+        out["extra"] = extras(args, slk, wl, H)
+    print(json.dumps(out), flush=True)
+
+
+def extras(args, slk, wl, H):
+    """Summaries of the other configurations, measured in the same run: the
+    high-resolution window (config 5), the 200-keyframe backend (config 4),
+    and the headline window with the reference's fp16 fmaps."""
+    sub = argparse.Namespace(**vars(args))
+    sub.no_cpu_baseline = True
+    out = {}
+    hr = window(sub, slk, wl, H, "highres")
+    out["config5_highres"] = {
+        "workload": hr["config"]["workload"], "edges_per_s": hr["value"],
+        "ms_per_step": hr["ms_per_step"], "corr_edges_per_s": hr["corr_edges_per_s"],
+        "ba_iter_ms": hr["ba_iter_ms"], "corr_window_us": hr["kernels_us"]["corr_window"],
+        "corr_window_frac": hr["roofline"]["frac"], "kernels_us": hr["kernels_us"]}
+    f16 = window(sub, slk, wl, H, "corr_window", fp16=True)
+    out["config2_fp16_fmaps"] = {
+        "workload": f16["config"]["workload"] + " (fp16 fmaps)", "edges_per_s": f16["value"],
+        "ms_per_step": f16["ms_per_step"], "corr_edges_per_s": f16["corr_edges_per_s"],
+        "corr_window_us": f16["kernels_us"]["corr_window"],
+        "corr_window_frac": f16["roofline"]["frac"], "kernels_us": f16["kernels_us"]}
+    be = backend(sub, slk, wl, H, emit=False)
+    out["config4_backend"] = {k: be[k] for k in (
+        "value", "unit", "corr_ms_all_edges", "corr_edges_per_s", "ba_iter_ms",
+        "ba_iters_per_s")}
+    out["config4_backend"]["workload"] = be["config"]["workload"]
+    return out
 
 
 # the two window workloads: the headline (48 edges of a 12-frame 48x64 window)
@@ -140,7 +180,9 @@ WINDOWS = {
 }
 
 
-def window(args, slk, wl, H, name):
+def window(args, slk, wl, H, name, fp16=False):
+    """One window workload (fp16: the feature maps stored as fp16, the
+    reference's fmap storage); returns the JSON dict."""
     cfg = WINDOWS[name]
     h, w, n, B = cfg["h"], cfg["w"], cfg["n"], cfg["B"]
     C = 128
@@ -148,6 +190,9 @@ def window(args, slk, wl, H, name):
     iters = 3
     lm, ep = 1e-4, 0.1
     fm = wl.frames(n, C, h, w, seed=0)
+    if fp16:
+        fm = fm.astype(np.float16)
+    fdt = slk.SLK_F16 if fp16 else slk.SLK_F32
     ii, jj = wl.cyclic_edges(n)
     assert len(ii) == B
     coords = wl.flow_coords(B, h, w, seed=1)
@@ -161,7 +206,8 @@ def window(args, slk, wl, H, name):
     stream = H.stream()
 
     def corr():
-        ctx.batch_build_and_sample_correlation(d_f, ii, jj, d_c, d_out, stream=stream)
+        ctx.batch_build_and_sample_correlation(d_f, ii, jj, d_c, d_out, dtype=fdt,
+                                               stream=stream)
 
     def ba():
         # the step's BA iterations on the window's edge set, as the loop of
@@ -291,10 +337,11 @@ def window(args, slk, wl, H, name):
         "kernels_pass_ms_per_step": round(prof_ms_step, 4),
         "wall_s_timed": round(wall, 3),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not fp16:
         out["cpu_baseline"] = cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep,
                                            min(args.cpu_edges, B))
-    print(json.dumps(out), flush=True)
+    ctx.close()
+    return out
     if args.calibrate_copy > 0:
         nbytes = args.calibrate_copy << 20
         src, dst = H.malloc(nbytes), H.malloc(nbytes)
@@ -308,7 +355,7 @@ def window(args, slk, wl, H, name):
               flush=True)
 
 
-def backend(args, slk, wl, H):
+def backend(args, slk, wl, H, emit=True):
     """The backend configuration (200 keyframes, ~2000 edges): correlation + lookup
     of all 2000 edges of a 200-keyframe graph in 48-edge launches (every
     keyframe's operands split once per pass, slk_corr_prepare_frames; the
@@ -393,7 +440,10 @@ def backend(args, slk, wl, H):
         "ba_iters_per_s": round(1e3 / ba_ms, 1),
         "ba_kernels_us": {k: round(1e3 * v[0] / v[1], 1) for k, v in prof.items()},
     }
-    print(json.dumps(out), flush=True)
+    ctx.close()
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
 
 
 def update_flops(h, w, B, K):
