@@ -44,12 +44,13 @@ typedef enum {
 typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
 
 /* Contraction used for the features:
- *  SLK_PREC_F16X3 (default)  -- batched path: every pixel's features scaled by
- *                               a power of two (its largest magnitude into
- *                               [2^14, 2^15)) and split into fp16 hi + lo
- *                               (22 significant bits), three fp16 MFMA passes
- *                               hi.hi + hi.lo + lo.hi with fp32 accumulation,
- *                               ~1e-6 relative to the row scale. fp16 features
+ *  SLK_PREC_F16X3 (default)  -- batched path: every frame's features scaled
+ *                               by one power of two (the frame's largest
+ *                               magnitude into [2^14, 2^15)) and split into
+ *                               fp16 hi + lo (22 significant bits), three fp16
+ *                               MFMA passes hi.hi + hi.lo + lo.hi with fp32
+ *                               accumulation, ~1e-6 relative to the frame
+ *                               scale. fp16 features
  *                               are their own hi (lo = 0): a level-0 target
  *                               tile takes the one pass hi.hi, the exact fp16
  *                               products of the reference's cublasGemmEx on
@@ -136,7 +137,7 @@ int slk_corr_batch_build_and_sample_dev(slk_ctx* ctx, const void* fmaps, int dty
  * take ii_host/jj_host as frame indices into them and compute the batches
  * without that step. Call it again whenever fmaps change. Results are
  * bitwise those of slk_corr_batch_build_and_sample on the same fmaps. Needs
- * the split contraction (C a multiple of 16 up to 128; fp16 fmaps, or fp32
+ * the split contraction (C a multiple of 16; fp16 fmaps, or fp32
  * with SLK_PREC_F16X3 or SLK_PREC_BF16X3), and the precision of the calls
  * that follow is the one in force at slk_corr_prepare_frames. */
 int slk_corr_prepare_frames(slk_ctx* ctx, const void* fmaps, int dtype, long fmap_stride,

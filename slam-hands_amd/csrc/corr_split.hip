@@ -18,17 +18,19 @@
 // cells agree to fp32 rounding, ~1e-7 relative); with integer-coded features
 // every intermediate is exact and the windows are bitwise equal.
 //
+// Stage 0 (k_frame_max, fp16 split only): partial maxima of |x| over each
+// frame's level-0 features (a pooled value is an average, never larger).
 // Stage 1 (k_feat_prep), once per frame a launch uses: the fp32 pooled
 // features of levels 1..3 (formed in LDS from level 0) and a hi/lo split of
 // every pixel of all levels, stored chunk-major [plane][C/16][rows][16] so a
 // 16-channel chunk of consecutive rows is one contiguous block, followed by
-// one float per row: the inverse of the row's split scale.
-//   fp16 split (SLK_PREC_F16X3, the default): each pixel's features are
-//   scaled by a power of two 2^e chosen from the pixel's largest magnitude
-//   m over the channels (m * 2^e in [2^14, 2^15)), then hi = rne_f16(x 2^e),
-//   lo = rne_f16(x 2^e - hi): 22 significant bits, the dropped lo.lo term
-//   ~2^-22 relative. fp16 features are taken with e >= 0, which makes hi
-//   exact and lo zero at level 0.
+// one float per frame: the inverse of the frame's split scale.
+//   fp16 split (SLK_PREC_F16X3, the default): a frame's features are scaled
+//   by one power of two 2^e chosen from the frame's largest magnitude m
+//   (m * 2^e in [2^14, 2^15)), then hi = rne_f16(x 2^e),
+//   lo = rne_f16(x 2^e - hi): 22 significant bits relative to m, the
+//   dropped lo.lo term ~2^-22 m^2 per product. fp16 features are taken with
+//   e >= 0, which makes hi exact and lo zero at level 0.
 //   bf16 split (SLK_PREC_BF16X3): hi = rne_bf16(x), lo = rne_bf16(x - hi),
 //   no scale (16 significant bits, lo.lo ~2^-16).
 // Stage 2 (tile_mask_edge, workgroups of the same launch as stage 1): which
@@ -42,12 +44,11 @@
 // not issued: with fp16 features every level-0 lo is zero, so a level-0 tile
 // takes the one pass hi.hi (the reference's fp16 x fp16 -> fp32 products,
 // main.cu:1573-1581) and a pooled tile hi.hi + hi.lo. The accumulator tile
-// is then transposed through LDS ([target][source]), each target column
-// multiplied by its inverse scale on the way, and the window cells that fall
-// inside the tile are read back with one lane per (source, window column),
-// walking the 8 window rows: each masked store covers one row of 8 sources'
-// windows, multiplied by alpha times the source's inverse scale (powers of
-// two: the scaling adds no rounding). Only ~2% of the level-0 products are
+// is then transposed through LDS ([target][source]) and the window cells that
+// fall inside the tile are read back with one lane per (source, window
+// column), walking the 8 window rows: each masked store covers one row of 8
+// sources' windows, multiplied by alpha times both frames' inverse scales
+// (powers of two: the scaling adds no rounding). Only ~2% of the level-0 products are
 // window cells, and none of them costs more than its LDS round trip.
 #include <algorithm>
 #include <climits>
@@ -126,14 +127,10 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // feature preparation they do not depend on.
 // (k_feat_prep launches with kT = 512 or 1024 threads a workgroup; the
 // tile-mask chain of an edge then sorts with kT / 64 waves.)
-// the preparation's level-0 block (every channel, at most kPrepMaxC, of 8 x 8
-// pixels) in LDS, which a tile-mask workgroup uses for its sort's histograms
-// or its bitmap
-constexpr int kPrepB = 8;
-constexpr int kPrepMaxC = 128;
-constexpr int kPrepLdsWords = kPrepMaxC * kPrepB * kPrepB;
-// pixels of a block over the four levels: 8 x 8, 4 x 4, 2 x 2, 1
-constexpr int kPrepPix = 64 + 16 + 4 + 1;
+// the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
+// which a tile-mask workgroup uses for its sort's histograms or its bitmap
+constexpr int kPrepRows = 8, kPrepCols = 64;
+constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
 constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
 constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
@@ -469,12 +466,11 @@ __device__ __forceinline__ unsigned split_f16(float x) {
            ((unsigned)__builtin_bit_cast(unsigned short, l) << 16);
 }
 
-// The exponent e of a pixel's fp16 split scale 2^e from its largest magnitude
-// m over the channels: m * 2^e in [2^14, 2^15), so every scaled feature and
-// its hi stay below 2^15 (fp16 holds up to 65504), bounded to [-120, 120]
-// (2^+-e stays a normal float; a bound only lowers m * 2^e); 0 for m = 0 or
-// non-finite. `exact`: at least 0 (fp16 features at level 0: then x 2^e is
-// exact in fp16 and lo is zero).
+// The exponent e of a frame's fp16 split scale 2^e from its largest magnitude
+// m: m * 2^e in [2^14, 2^15), so every scaled feature and its hi stay below
+// 2^15 (fp16 holds up to 65504), bounded to [-120, 120] (2^+-e stays a normal
+// float; a bound only lowers m * 2^e); 0 for m = 0 or non-finite. `exact`: at
+// least 0 (fp16 features: then x 2^e is exact in fp16 and lo is zero).
 __device__ __forceinline__ int split_exponent(float m, bool exact) {
     int e = 0;
     if (m > 0.0f && m <= 3.402823466e38f) {
@@ -485,213 +481,205 @@ __device__ __forceinline__ int split_exponent(float m, bool exact) {
     return e;
 }
 
-// Feature preparation of one frame slot, one launch. A workgroup takes an
-// 8 x 8 block of level-0 pixels with every channel (C <= kPrepMaxC) into an LDS
-// image F[pixel][channel] (pixels 0..63 the block's level-0 pixels in row
-// order, 64..79 its 4 x 4 level-1 pixels, 80..83 the 2 x 2 of level 2, 84 the
-// level-3 pixel; channels fastest, the pixel stride padded to 132 floats so
-// that 16-byte reads of consecutive pixels spread over the banks). Threads
-// (channel, level-2 pixel) form a level-2 pixel's four level-1 pixels and
-// itself, then threads (channel) the level-3 pixel, each pooled value
-// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first.
-// Threads (pixel, 16-channel group) find each pixel's largest magnitude over
-// the channels (their group's, then a DPP maximum over the eight groups in
-// consecutive lanes), which gives its split scale; threads (pixel, chunk)
-// then scale and split 16 channels and write them, 32 bytes per pixel and
-// plane, to out[slot][plane][C/16][Ttot][16], and each pixel's inverse scale
-// to the slot's row-scale array. `pooled` = 0 writes level 0 only (source
-// slots). One-dimensional grid: first, when mk.list is set, one tile-mask
-// workgroup per edge (tile_mask_edge, in the LDS of the image; they are the
-// longer chains, so they are dispatched first), then the blocks x slots
-// preparation workgroups, remapped so that each XCD takes a contiguous run
-// of blocks: a block's rows are 32-byte pieces of 128-byte lines whose other
-// pieces belong to its neighbours in x.
-constexpr int kPrepLd = kPrepMaxC + 4;  // floats per pixel of the LDS image
-static_assert(kPrepPix * kPrepLd >= kPrepLdsWords + 2048, "mask LDS inside the image");
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                         0u, __builtin_bit_cast(unsigned, v), kCtrl, 0xF, 0xF,
-                                         false));
+// Partial maxima of |x| over the frames of slots slot_lo.., for the fp16
+// split's per-frame scale: workgroup (q, s) reduces chunks q, q + nparts, ..
+// of kMaxChunk elements of slot s's C x HW features into part[s][q] (no
+// atomics: the preparation reduces the parts of its slot). Each thread's four
+// 16-byte loads of a chunk are in flight together. The pooled levels' values
+// are means of level-0 values, so the frame's level-0 maximum bounds every
+// level.
+constexpr int kMaxParts = 256;              // partial maxima per slot, at most
+constexpr int kMaxChunk = 256 * 4 * 4;      // elements a workgroup reduces per round
+template <typename Tin>
+__global__ __launch_bounds__(256) void k_frame_max(const Tin* __restrict__ fm, long fstride,
+                                                   SlotFrames sf, int slot_lo, long n, int vec,
+                                                   int nparts, float* __restrict__ part) {
+    __shared__ float wm[4];
+    const int s = slot_lo + blockIdx.y, q = blockIdx.x, tid = threadIdx.x;
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride;
+    float m = 0.0f;
+    for (long c0 = (long)q * kMaxChunk; c0 < n; c0 += (long)nparts * kMaxChunk) {
+        if (vec) {  // uniform: n % 4 == 0, the frames 4-element aligned
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const long i = c0 + 4 * (tid + 256 * u);
+                v[u] = i < n ? ldf4(src + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                m = fmaxf(fmaxf(m, fabsf(v[u].x)), fabsf(v[u].y));
+                m = fmaxf(fmaxf(m, fabsf(v[u].z)), fabsf(v[u].w));
+            }
+        } else {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const long i = c0 + tid + 256 * u;
+                v[u] = i < n ? ldf(src + i) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) m = fmaxf(m, fabsf(v[u]));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) wm[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) part[(size_t)s * kMaxParts + q] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
 }
-// the largest m over each group of 8 consecutive lanes, by DPP: lanes xor 1,
-// xor 2, then the mirrored lane within 8
-__device__ __forceinline__ float max8(float m) {
-    m = fmaxf(m, dpp_f<0xB1>(m));      // quad_perm [1, 0, 3, 2]
-    m = fmaxf(m, dpp_f<0x4E>(m));      // quad_perm [2, 3, 0, 1]
-    return fmaxf(m, dpp_f<0x141>(m));  // row_half_mirror
-}
 
+// Feature preparation of one frame slot, one launch: a workgroup takes a
+// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
+// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
+// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
+// a pooled pixel's parents always lie in the block), and writes the hi/lo
+// split of every pixel of the levels present, 16 channels = 32 bytes per
+// pixel and plane, into out[slot][plane][C/16][Ttot][16]; under the fp16
+// split every value is first scaled by its frame's 2^e (from the partial
+// maxima of k_frame_max), and the first workgroup of a slot stores 2^-e
+// after the slot's planes. `pooled` = 0 writes level 0 only (source slots).
+// One-dimensional grid: first, when mk.list is set, one tile-mask workgroup
+// per edge (tile_mask_edge, with the level-0 and level-1 LDS arrays; they are
+// the longer chains, so they are dispatched first), then the blocks x C/16 x
+// slots preparation workgroups (block fastest).
+// (waves per SIMD: two 1024-thread or three 512-thread workgroups a CU)
 template <typename Tin, int kT>
-__global__ __launch_bounds__(kT, kT >= 1024 ? 2 : 1) void k_feat_prep(
+__global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
     const Tin* __restrict__ fm, long fstride, SlotFrames sf, int slot_lo,
     unsigned short* __restrict__ out, long slot_elems, Geom g, int pooled, int vec, int nbx,
-    int nblk, int nprep, int nmask, MaskArgs mk, int mode) {
-    __shared__ __attribute__((aligned(16))) float F[kPrepPix * kPrepLd];
-    __shared__ float pscale[kPrepPix];  // 2^e of each pixel of the block
-    __shared__ int trow[kPrepPix];      // target row of each pixel, or -1
+    int nblk, int nmask, MaskArgs mk, int mode, const float* __restrict__ part, int nparts) {
+    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
+    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
+    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
+    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
     __shared__ int wave_sum[kT / 64];
+    __shared__ float fscale;  // the frame's 2^e
     if ((int)blockIdx.x < nmask) {  // uniform
         // the tile-mask chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        unsigned* lds = reinterpret_cast<unsigned*>(F);
-        tile_mask_edge<kT>(mk, g, blockIdx.x, lds, lds + kPrepLdsWords, 2048, wave_sum);
+        tile_mask_edge<kT>(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]),
+                           reinterpret_cast<unsigned*>(&l1[0][0][0]), (int)(sizeof(l1) / 4),
+                           wave_sum);
         return;
     }
     const int tid = threadIdx.x;
-    const int j = xcd_remap((int)blockIdx.x - nmask, nprep);
-    const int blk = j % nblk, s = slot_lo + j / nblk;
+    const int b = blockIdx.x - nmask;
+    const int blk = b % nblk, rest = b / nblk;
     const int bx = blk % nbx, by = blk / nbx;
-    const int W = g.w[0], H = g.h[0], C = g.C;
-    const Tin* src = fm + (long)slot_frame(sf, s) * fstride;
-    const int y0 = by * kPrepB, x0 = bx * kPrepB;
-    // level 0: channel fastest across the lanes (consecutive LDS words); every
-    // load goes out before the first is stored
+    const int k = rest % (g.C / kChunk), s = slot_lo + rest / (g.C / kChunk);
+    const int W = g.w[0], H = g.h[0];
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
+    if (tid < 64) {  // the frame's scale, from the partial maxima of its slot
+        float m = 0.0f;
+        if (mode == kSplitF16)
+            for (int q = tid; q < nparts; q += 64) m = fmaxf(m, part[(size_t)s * kMaxParts + q]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if (tid == 0)
+            fscale = mode == kSplitF16
+                         ? __builtin_amdgcn_ldexpf(
+                               1.0f, split_exponent(m, std::is_same<Tin, _Float16>::value))
+                         : 1.0f;
+    }
+    // all of a thread's loads are issued before the first is used
+    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kT;
+    float ld[kPer];
     if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
-        constexpr int kPer = kPrepMaxC * kPrepB * 2 / kT;  // float4 of 4 pixels each
-        float4 v[kPer];
+        // four consecutive pixels of a row a lane (all inside or all outside)
 #pragma unroll
-        for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kT;
-            const int c = i & (kPrepMaxC - 1), r = i >> 8, x = ((i >> 7) & 1) * 4;
-            const bool in = c < C && y0 + r < H && x0 + x < W;
-            v[u] = ldf4(src + (in ? (long)c * g.HW + (long)(y0 + r) * W + x0 + x : 0L));
-            if (!in) v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int u = 0; u < kPer / 4; u++) {
+            const int i = 4 * (tid + u * kT);
+            const int c = i / (kPrepRows * kPrepCols);
+            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+            const bool in = yy < H && xx < W;
+            const float4 v = ldf4(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+            ld[4 * u] = in ? v.x : 0.0f;
+            ld[4 * u + 1] = in ? v.y : 0.0f;
+            ld[4 * u + 2] = in ? v.z : 0.0f;
+            ld[4 * u + 3] = in ? v.w : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kT;
-            const int c = i & (kPrepMaxC - 1), p = (i >> 8) * kPrepB + ((i >> 7) & 1) * 4;
-            F[p * kPrepLd + c] = v[u].x;
-            F[(p + 1) * kPrepLd + c] = v[u].y;
-            F[(p + 2) * kPrepLd + c] = v[u].z;
-            F[(p + 3) * kPrepLd + c] = v[u].w;
+        for (int u = 0; u < kPer / 4; u++) {
+            const int i = 4 * (tid + u * kT);
+            *reinterpret_cast<float4*>(
+                &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
+                make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
         }
     } else {
-        constexpr int kPer = kPrepMaxC * kPrepB * kPrepB / kT;
-        float v[kPer];
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
             const int i = tid + u * kT;
-            const int c = i & (kPrepMaxC - 1), p = i >> 7, r = p >> 3, x = p & 7;
-            const bool in = c < C && y0 + r < H && x0 + x < W;
-            v[u] = ldf(src + (in ? (long)c * g.HW + (long)(y0 + r) * W + x0 + x : 0L));
-            if (!in) v[u] = 0.0f;
+            const int c = i / (kPrepRows * kPrepCols);
+            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
+            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+            const bool in = yy < H && xx < W;
+            ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
+            if (!in) ld[u] = 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kPer; u++) {
             const int i = tid + u * kT;
-            F[(i >> 7) * kPrepLd + (i & (kPrepMaxC - 1))] = v[u];
+            l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
         }
-    }
-    // the target row of each pixel of the block, -1 outside its level's map
-    // (or above level 0 for a source slot)
-    for (int pp = tid; pp < kPrepPix; pp += kT) {
-        int l = 0, q = pp, side = kPrepB;
-        if (pp >= 84) {
-            l = 3, q = 0, side = 1;
-        } else if (pp >= 80) {
-            l = 2, q = pp - 80, side = 2;
-        } else if (pp >= 64) {
-            l = 1, q = pp - 64, side = 4;
-        }
-        const int yy = by * side + q / side, xx = bx * side + q % side;
-        const bool ok = (pooled || l == 0) && l < g.levels && yy < g.h[l] && xx < g.w[l];
-        trow[pp] = ok ? g.off[l] + yy * g.w[l] + xx : -1;
     }
     __syncthreads();
-    if (pooled) {
-        // thread (channel, level-2 pixel q): the four level-1 pixels of q
-        // from their 2x2 parents, then q from them
-        for (int i = tid; i < kPrepMaxC * 4; i += kT) {
-            const int c = i & (kPrepMaxC - 1), q = i >> 7, y2 = q >> 1, x2 = q & 1;
-            float l1[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int y1 = 2 * y2 + (k >> 1), x1 = 2 * x2 + (k & 1);
-                const float* a = F + ((2 * y1) * kPrepB + 2 * x1) * kPrepLd + c;
-                float sum = a[0] + a[kPrepLd];
-                sum = sum + a[kPrepB * kPrepLd];
-                sum = sum + a[(kPrepB + 1) * kPrepLd];
-                l1[k] = 0.25f * sum;
-                F[(64 + y1 * 4 + x1) * kPrepLd + c] = l1[k];
-            }
-            float sum = l1[0] + l1[1];
-            sum = sum + l1[2];
-            sum = sum + l1[3];
-            F[(80 + q) * kPrepLd + c] = 0.25f * sum;
-        }
-        __syncthreads();
-        for (int c = tid; c < kPrepMaxC; c += kT) {  // level 3 from the level-2 pixels
-            const float* a = F + 80 * kPrepLd + c;
-            float sum = a[0] + a[kPrepLd];
-            sum = sum + a[2 * kPrepLd];
-            sum = sum + a[3 * kPrepLd];
-            F[84 * kPrepLd + c] = 0.25f * sum;
-        }
-        __syncthreads();
-    }
-    const int npx = pooled ? kPrepPix : 64;
-    const int nck = C / kChunk;
-    if (mode == kSplitF16) {  // uniform
-        // thread (pixel, group of 16 channels), groups in consecutive lanes
-        constexpr bool kHalf = std::is_same<Tin, _Float16>::value;
-        for (int i = tid; i < npx * 8; i += kT) {  // whole groups of 8 lanes
-            const int pp = i >> 3, grp = i & 7;
-            float m = 0.0f;
-            if (grp < nck) {
-                const float4* a = reinterpret_cast<const float4*>(F + pp * kPrepLd + grp * kChunk);
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const float4 t = a[u];
-                    m = fmaxf(fmaxf(m, fabsf(t.x)), fabsf(t.y));
-                    m = fmaxf(fmaxf(m, fabsf(t.z)), fabsf(t.w));
-                }
-            }
-            m = max8(m);
-            if (grp == 0)
-                pscale[pp] = __builtin_amdgcn_ldexpf(1.0f, split_exponent(m, kHalf && pp < 64));
-        }
-    } else {
-        for (int pp = tid; pp < npx; pp += kT) pscale[pp] = 1.0f;
-    }
-    __syncthreads();
-    // thread (pixel, chunk), pixels fastest: a row of 8 level-0 pixels is
-    // 256 contiguous bytes of a chunk
-    const size_t plane = (size_t)C * g.Ttot;
-    unsigned short* const base = out + (size_t)s * slot_elems;
-    for (int i = tid; i < npx * nck; i += kT) {
-        const int pp = i % npx, k = i / npx;
-        const int t = trow[pp];
-        if (t < 0) continue;
-        const float sc = pscale[pp];
-        const float4* a = reinterpret_cast<const float4*>(F + pp * kPrepLd + k * kChunk);
+    const float sc = fscale;
+    const size_t plane = (size_t)g.C * g.Ttot;
+    unsigned short* const slot = out + (size_t)s * slot_elems;
+    if (blk == 0 && k == 0 && tid == 0)  // the slot's inverse scale (a power of two)
+        *reinterpret_cast<float*>(slot + 2 * plane) = 1.0f / sc;
+    unsigned short* const base = slot + (size_t)k * g.Ttot * kChunk;
+    auto emit = [&](int t, const float (&v)[kChunk]) {
         u16x8_t hi[2], lo[2];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float4 t4 = a[u];
-            const float xs[4] = {t4.x, t4.y, t4.z, t4.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int ch = 4 * u + e;
-                const unsigned pk =
-                    mode == kSplitF16 ? split_f16(xs[e] * sc) : split_bf16(xs[e]);
-                hi[ch >> 3][ch & 7] = (unsigned short)(pk & 0xffffu);
-                lo[ch >> 3][ch & 7] = (unsigned short)(pk >> 16);
-            }
+        for (int u = 0; u < kChunk; u++) {
+            const unsigned pk = mode == kSplitF16 ? split_f16(v[u] * sc) : split_bf16(v[u]);
+            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
+            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
         }
-        unsigned short* o = base + (size_t)k * g.Ttot * kChunk + (size_t)t * kChunk;
+        unsigned short* o = base + (size_t)t * kChunk;
         *reinterpret_cast<u16x8_t*>(o) = hi[0];
         *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
         *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
         *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+    };
+    // level 0
+    for (int p = tid; p < kPrepRows * kPrepCols; p += kT) {
+        const int r = p / kPrepCols, x = p % kPrepCols;
+        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
+        if (yy >= H || xx >= W) continue;
+        float v[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
+        emit(yy * W + xx, v);
     }
-    // the rows' inverse scales (exact powers of two)
-    float* const rs = reinterpret_cast<float*>(base + 2 * plane);
-    for (int pp = tid; pp < npx; pp += kT)
-        if (trow[pp] >= 0) rs[trow[pp]] = 1.0f / pscale[pp];
+    if (!pooled) return;
+    // pooled levels: level l from level l-1 in LDS, then its pixels out
+    auto level = [&](auto& dst, const auto& from, int l, int rows, int cols) {
+        for (int i = tid; i < kChunk * rows * cols; i += kT) {
+            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
+            float sum = from[c][2 * r][2 * x] + from[c][2 * r][2 * x + 1];
+            sum = sum + from[c][2 * r + 1][2 * x];
+            sum = sum + from[c][2 * r + 1][2 * x + 1];
+            dst[c][r][x] = 0.25f * sum;
+        }
+        __syncthreads();
+        for (int p = tid; p < rows * cols; p += kT) {
+            const int r = p / cols, x = p % cols;
+            const int yy = by * rows + r, xx = bx * cols + x;
+            if (yy >= g.h[l] || xx >= g.w[l]) continue;
+            float v[kChunk];
+#pragma unroll
+            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
+            emit(g.off[l] + yy * g.w[l] + xx, v);
+        }
+    };
+    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
+    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
+    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
 }
 
 struct alignas(16) SplitSmem {
@@ -710,8 +698,6 @@ struct alignas(16) SplitSmem {
     int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
     int pix[kSrcTile];        // pixel of each source
-    float sfac[2 * kSrcTile]; // [2 r], [2 r + 1]: inverse split scale of source row r
-    float tfac[kTgtTile];     // inverse split scale of each target row of the tile
 };
 
 // One direct-to-LDS load per lane (16 or 4 bytes): lane l reads p and writes
@@ -832,8 +818,9 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const size_t plane = (size_t)g.C * Ttot;
     const unsigned short* fa = feat + (size_t)es.si[e] * slot_elems;
     const unsigned short* fb = feat + (size_t)es.sj[e] * slot_elems;
-    const float* sca = reinterpret_cast<const float*>(fa + 2 * plane);  // row scales
-    const float* scb = reinterpret_cast<const float*>(fb + 2 * plane);
+    // alpha over both frames' split scales (powers of two: no rounding)
+    const float fs = alpha * *reinterpret_cast<const float*>(fa + 2 * plane) *
+                     *reinterpret_cast<const float*>(fb + 2 * plane);
     const int* ord = order + (size_t)e * 3 * HW;
 
     // Staging by direct-to-LDS loads (global_load_lds_dwordx4): lane l of wave
@@ -933,16 +920,13 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         // are explicit because a workgroup fence would also wait for chunk
         // k+1.
         issue(0, 0);
-        // coordinates and row scales of the tile's sources and the scales of
-        // its targets, in flight with the first chunk (also by direct-to-LDS
-        // loads: every load the pipeline waits on with vmcnt is of the same
-        // kind, and those complete in issue order)
+        // coordinates of the tile's sources, in flight with the first chunk
+        // (also by a direct-to-LDS load: every load the pipeline waits on with
+        // vmcnt is of the same kind, and those complete in issue order)
         {
             const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
             const int pc = std::min(p0 + half * 64 + lane, HW - 1);
             dma_x1(ord + (size_t)(1 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
-            dma_x1(sca + pa, lds_addr(&sm.sfac[wave * 64]));  // sfac[tid]: row tid / 2
-            dma_x1(scb + std::min(t0 + tid, Ttot - 1), lds_addr(&sm.tfac[wave * 64]));
         }
         if (nk > 1) issue(1, 1);
         // While in its chunk loop a wave issues at raised priority, so that on
@@ -1020,24 +1004,21 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     for (int sb = 0; sb < 2; sb++) {
         if (sb) lds_barrier();  // the first half's cells have all been read
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) {
-            const int t = wn * 128 + tb * 32 + orow;
-            const float tf = sm.tfac[t];  // the target's inverse split scale
+        for (int tb = 0; tb < 4; tb++)
 #pragma unroll
             for (int gq = 0; gq < 4; gq++) {
+                const int t = wn * 128 + tb * 32 + orow;
                 const int s = wm * 32 + gq * 8 + khalf * 4;
                 *reinterpret_cast<float4*>(&sm.u.T[t][s]) =
-                    make_float4(acc[sb][tb][4 * gq] * tf, acc[sb][tb][4 * gq + 1] * tf,
-                                acc[sb][tb][4 * gq + 2] * tf, acc[sb][tb][4 * gq + 3] * tf);
+                    make_float4(acc[sb][tb][4 * gq], acc[sb][tb][4 * gq + 1],
+                                acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
             }
-        }
         lds_barrier();
 #pragma unroll
         for (int grp = 0; grp < 2; grp++) {
             const int s = wave * 16 + grp * 8 + g8;                 // column of T
             const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
             const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
-            const float fs = alpha * sm.sfac[2 * lsrc];  // alpha / the source's scale
             const bool pin = p0 + lsrc < HW;
             const float* Tcol = &sm.u.T[0][s];
             // byte offset of cell (cx, row 0) of level 0 in the slot
@@ -1095,9 +1076,9 @@ Geom make_geom(const slk_ctx* ctx) {
 }
 
 // u16 elements of one frame slot: the hi and lo planes [C/16][Ttot][16], then
-// the rows' inverse split scales (Ttot floats), padded to 256 bytes
+// the frame's inverse split scale (one float), padded to 256 bytes
 size_t slot_elems(const Geom& g) {
-    return (2 * (size_t)g.C * g.Ttot + 2 * (size_t)g.Ttot + 127) / 128 * 128;
+    return (2 * (size_t)g.C * g.Ttot + 2 + 127) / 128 * 128;
 }
 
 // the split of fp32 (or fp16) features under the context's precision
@@ -1111,9 +1092,9 @@ template <typename Tin>
 int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
                   int slot_lo, int nslots, bool pooled, const MaskArgs& mk, unsigned short* out,
                   int mode, hipStream_t stream) {
-    const int nbx = (g.w[0] + kPrepB - 1) / kPrepB;
-    const int nblk = nbx * ((g.h[0] + kPrepB - 1) / kPrepB);
-    const long nprep = (long)nblk * std::max(nslots, 0);
+    const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
+    const int nblk = nbx * ((g.h[0] + kPrepRows - 1) / kPrepRows);
+    const long nprep = (long)nblk * (g.C / kChunk) * std::max(nslots, 0);
     const long nmask = mk.list ? mk.nedges : 0;
     if (nprep + nmask == 0) return SLK_OK;
     if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
@@ -1121,18 +1102,30 @@ int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& s
     const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
     const long se = (long)slot_elems(g);
-    // 512-thread workgroups (8-wave mask chains): three a CU, so the 576
-    // preparation workgroups and 48 mask chains of the 48-edge window at
-    // 48x64 all start at once (24.3 against 27.0 us with 1024-thread
-    // workgroups, two a CU, where the last 112 waited for a CU)
-    if (g.HW <= 0)
+    float* part = ctx->frame_max.as<float>();
+    const long n = (long)g.C * g.HW;
+    const int nparts = (int)std::min<long>(kMaxParts, (n + kMaxChunk - 1) / kMaxChunk);
+    if (mode == kSplitF16 && nslots > 0) {
+        // the frames' partial maxima for their split scales
+        if (ctx->frame_max.bytes < (size_t)(slot_lo + nslots) * kMaxParts * sizeof(float))
+            return fail(SLK_E_ARG, "feature preparation: frame-maximum buffer too small");
+        ProfScope ps(ctx, "corr_frame_max", stream);
+        hipLaunchKernelGGL((k_frame_max<Tin>), dim3(nparts, nslots), dim3(256), 0, stream, fm,
+                           fstride, sf, slot_lo, n, (vec && g.HW % 4 == 0) ? 1 : 0, nparts, part);
+        SLK_HIP(hipGetLastError());
+    }
+    ProfScope ps(ctx, "corr_feat_prep", stream);
+    // 1024-thread workgroups (16-wave mask chains) for maps up to 4096
+    // pixels, two a CU; 512 above, three a CU (the preparation's share of
+    // the launch is larger there)
+    if (g.HW <= 4096)
         hipLaunchKernelGGL((k_feat_prep<Tin, 1024>), dim3((unsigned)(nprep + nmask)), dim3(1024),
                            0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nprep, (int)nmask, mk, mode);
+                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk, mode, part, nparts);
     else
         hipLaunchKernelGGL((k_feat_prep<Tin, 512>), dim3((unsigned)(nprep + nmask)), dim3(512),
                            0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nprep, (int)nmask, mk, mode);
+                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk, mode, part, nparts);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -1163,11 +1156,9 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
                 ctx->src_order.as<int>(), mtiles, ntiles, n,
                 ctx->mask_tab.as<unsigned long long>()};
-    {
-        // feature preparation and the tile mask, one launch
-        ProfScope ps(ctx, "corr_feat_prep", stream);
-        SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
-    }
+    // feature preparation and the tile mask, one launch (after the frames'
+    // maxima under the fp16 split)
+    SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
     {
         ProfScope ps(ctx, "corr_window", stream);
         const long se = (long)slot_elems(g);
@@ -1220,7 +1211,6 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     }
     // sources only need level 0 (their own launch); targets need every level
     {
-        ProfScope ps(ctx, "corr_feat_prep", stream);
         const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
         SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, mode, stream));
     }
@@ -1230,12 +1220,11 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
 
 }  // namespace
 
-bool corr_split_supported(const slk_ctx* ctx) {
-    return ctx->C % kChunk == 0 && ctx->C <= kPrepMaxC;
-}
+bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
 
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
-                          size_t* order_per_edge, size_t* ctr_bytes) {
+                          size_t* order_per_edge, size_t* ctr_bytes, size_t* max_per_slot) {
+    *max_per_slot = kMaxParts * sizeof(float);
     const Geom g = make_geom(ctx);
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
@@ -1252,6 +1241,7 @@ int corr_split_alloc(slk_ctx* ctx) {
     const Geom g = make_geom(ctx);
     const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
     SLK_TRY(ctx->split_feat.ensure(slots * slot_elems(g) * sizeof(unsigned short)));
+    SLK_TRY(ctx->frame_max.ensure(slots * kMaxParts * sizeof(float)));
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
@@ -1298,10 +1288,12 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     if (bytes > ctx->prep_feat.bytes && ctx->prep_feat.ptr)
         SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old frames
     SLK_TRY(ctx->prep_feat.ensure(bytes));
+    if ((size_t)nframes * kMaxParts * sizeof(float) > ctx->frame_max.bytes && ctx->frame_max.ptr)
+        SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old maxima
+    SLK_TRY(ctx->frame_max.ensure((size_t)nframes * kMaxParts * sizeof(float)));
     SlotFrames sf{};
     sf.ident = 1;
     const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
-    ProfScope ps(ctx, "corr_prepare_frames", stream);
     const int mode = split_mode(ctx);
     if (dtype == SLK_F32)
         SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,
