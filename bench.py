@@ -270,9 +270,10 @@ def window(args, slk, wl, H, name, fp16=False):
     # launch duration, against the dense MFMA peak of the datapath the kernel
     # runs on (fp16 for the default 3-pass scaled hi/lo split, bf16 for the
     # bf16 split: both 2.5 PFLOP/s dense; fp32 for SLK_PREC_FP32). The split
-    # issues 3 MFMA passes per product of fp32 features and the kernel skips
-    # target tiles that hold no window cell: `mfma_issued_*` is the MFMA work
-    # it actually issued (active 128x256 tiles x C x 2 x 3) in the same time,
+    # issues 3 MFMA passes per product of fp32 features and each source tile
+    # multiplies only the targets of its windows' boxes: `mfma_issued_*` is the
+    # MFMA work it actually issued (listed 128x256 tiles x C x 2 x 3) in the
+    # same time,
     # and `frac_ceiling_of_method` = algorithmic / issued flops is the highest
     # `frac` this method reaches with the MFMA pipes always busy.
     flop = 2.0 * HW * HW * C * B
@@ -298,7 +299,7 @@ def window(args, slk, wl, H, name, fp16=False):
     if split:
         active, total = split_tiles_active(coords, h, w)
         exe = active * 128 * 256 * C * 2.0 * 3
-        roof.update({"active_tiles": int(active), "tiles": int(total),
+        roof.update({"listed_tiles": int(active), "all_pairs_tiles": int(total),
                      "mfma_issued_flop_per_launch": exe,
                      "mfma_issued_TFLOPs": round(exe / gemm_s / 1e12, 2),
                      "mfma_issued_frac": round(exe / gemm_s / 1e12 / PEAK_F16_TFLOPS, 4),
@@ -1008,41 +1009,57 @@ def graph(args, slk, wl, H):
     print(json.dumps(out), flush=True)
 
 
-def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256):
-    """(active, total) 128-source x 256-target tiles of the batched correlation:
-    a tile is active when some source's 8x8 window at some level has a cell in
-    its targets (the test tile_mask_edge makes on the GPU, restated in numpy).
-    Source tiles are runs of 128 sources in the order sort_sources gives them:
-    stably sorted by the clamped first row of their level-0 window when the
-    map has at most 247 rows, else in pixel order."""
+def split_tiles_active(coords, h, w, levels=4, src_tile=128, tgt_tile=256, band=16,
+                       max_keys=8192):
+    """(listed, all-pairs) 128-source x 256-target tiles of the batched
+    correlation, restating the order pass of the GPU (order_and_boxes) in
+    numpy: sources sorted by (band of 16 rows of the clamped floored y,
+    snaking column of the clamped floored x); a source tile is a run of 128
+    sorted sources, its level-l target box the windows' extent over the
+    tile's bucket range, clipped to the level; the boxes' cells concatenated
+    are cut into runs of 256 targets, each one listed tile. `all-pairs` is
+    the number of tiles of the full volume (every source tile x every
+    256-target run of the concatenated levels)."""
     B, HW = coords.shape[0], h * w
     hl = [h >> l for l in range(levels)]
     wl = [w >> l for l in range(levels)]
-    off = np.cumsum([0] + [a * b for a, b in zip(hl, wl)])
+    ttot = sum(a * b for a, b in zip(hl, wl))
     mtiles = -(-HW // src_tile)
-    ntiles = -(-int(off[-1]) // tgt_tile)
     lim = float(1 << 20)
     f = np.clip(np.floor(np.nan_to_num(coords, nan=-lim)), -lim, lim).astype(np.int64)
     fx, fy = f[:, 0, :], f[:, 1, :]
-    if h + 9 <= 256:
-        order = np.argsort(np.clip(fy - 3, -8, h), axis=1, kind="stable")
-        fx = np.take_along_axis(fx, order, axis=1)
-        fy = np.take_along_axis(fy, order, axis=1)
-    src = (np.arange(B)[:, None] * mtiles + np.arange(HW)[None, :] // src_tile)
-    act = np.zeros(B * mtiles * ntiles, bool)
+    kx, nb = w + 9, -(-(h + 9) // band)
+    sx, nxb = 0, kx
+    while nb * nxb > max_keys and sx < 20:
+        sx += 1
+        nxb = (kx + (1 << sx) - 1) >> sx
+    bnd = (np.clip(fy, -8, h) + 8) // band
+    xb = (np.clip(fx, -8, w) + 8) >> sx
+    key = np.sort(bnd * nxb + np.where(bnd & 1, nxb - 1 - xb, xb), axis=1)
+    first = np.arange(mtiles) * src_tile
+    last = np.minimum(first + src_tile, HW) - 1
+    b0, b1 = key[:, first], key[:, last]
+    band0, band1 = b0 // nxb, b1 // nxb
+
+    def col(b):
+        s_ = b % nxb
+        return np.where((b // nxb) & 1, nxb - 1 - s_, s_)
+
+    c0, c1 = col(b0), col(b1)
+    same, next_ = band0 == band1, band1 == band0 + 1
+    xlo = np.where(same, np.minimum(c0, c1),
+                   np.where(next_ & (band0 % 2 == 0), np.minimum(c0, c1), 0))
+    xhi = np.where(same, np.maximum(c0, c1),
+                   np.where(next_ & (band0 % 2 == 1), np.maximum(c0, c1), nxb - 1))
+    fx0, fx1 = (xlo << sx) - 8, ((xhi + 1) << sx) - 9
+    fy0, fy1 = band0 * band - 8, band1 * band + band - 9
+    total = np.zeros_like(b0)
     for l in range(levels):
-        ox, oy = (fx >> l) - 3, (fy >> l) - 3
-        xa, xb = np.maximum(ox, 0), np.minimum(ox + 7, wl[l] - 1)
-        ya, yb = np.maximum(oy, 0), np.minimum(oy + 7, hl[l] - 1)
-        ok = (xa <= xb) & (ya <= yb)
-        lo = (off[l] + ya * wl[l] + xa) // tgt_tile
-        hi = (off[l] + yb * wl[l] + xb) // tgt_tile
-        span = int((hi - lo)[ok].max()) if ok.any() else -1
-        for d in range(span + 1):
-            t = lo + d
-            m = ok & (t <= hi)
-            act[(src[m] * ntiles + t[m])] = True
-    return int(act.sum()), act.size
+        xa, xe = np.maximum((fx0 >> l) - 3, 0), np.minimum((fx1 >> l) + 4, wl[l] - 1)
+        ya, ye = np.maximum((fy0 >> l) - 3, 0), np.minimum((fy1 >> l) + 4, hl[l] - 1)
+        total += np.where((xa <= xe) & (ya <= ye), (xe - xa + 1) * (ye - ya + 1), 0)
+    listed = int((-(-total // tgt_tile)).sum())
+    return listed, B * mtiles * (-(-ttot // tgt_tile))
 
 
 def cpu_baseline(fm, ii, jj, coords, p, iters, lm, ep, nedges):

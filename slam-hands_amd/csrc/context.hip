@@ -175,7 +175,6 @@ extern "C" int slk_destroy(slk_ctx* ctx) {
     ctx->tile_ctr.release();
     ctx->tile_list.release();
     ctx->src_order.release();
-    ctx->mask_tab.release();
     for (int l = 0; l < slk::kMaxLevels; l++) ctx->single_lvl[l].release();
     ctx->zero_idx.release();
     ctx->glue_stage.release();

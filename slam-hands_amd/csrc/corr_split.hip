@@ -111,347 +111,245 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
     return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
 }
 
-// Which (edge, source tile, target tile) pairs hold at least one window cell:
-// per source and level present, the window's clipped rows/columns span the
-// concatenated target indices [off + ya*w + xa, off + yb*w + xb], and every
-// target tile in that span is marked (a superset of the tiles holding a cell).
-// Tiles not marked are skipped by k_corr_split_win: they would store nothing.
-// One workgroup (kT threads, 512 or 1024) per edge: an LDS bitmap (`bits`, at least
-// ceil(mtiles * ntiles / 32) words; in the level-1 array when it fits there,
-// the sort's histograms then taking the level-0 array, else in the level-0
-// array with the sources left in pixel order) of the edge's tiles, then the marked ones
-// compacted in tile order into the edge's segment list[e * tpe ..] (ids
-// mt * ntiles + nt) and their number into ctr[kCtrCount + e]. Edge 0 also
-// zeroes the tile counters of k_corr_split_win, which runs after this on the
-// same stream. These workgroups run in the launch of k_feat_prep, beside the
-// feature preparation they do not depend on.
-// (k_feat_prep launches with kT = 512 or 1024 threads a workgroup; the
-// tile-mask chain of an edge then sorts with kT / 64 waves.)
+// Source order and target boxes of an edge (one workgroup per edge, in the
+// launch of k_feat_prep beside the feature preparation it does not depend on).
+//
+// Sources are ordered by where their windows fall: the floored coordinates
+// (fx, fy), clamped to [-8, w] x [-8, h] (a window of a source outside that
+// range meets the level-0 image nowhere, and the clamp keeps it beside the
+// sources whose pooled-level windows it shares), fall in bands of kBand rows;
+// the bands are walked top to bottom and within a band the columns snake
+// (left to right in even bands, right to left in odd ones), so that a run of
+// 128 sorted sources -- a source tile -- covers about a 16 x 8 pixel patch of
+// the target frame, and a run crossing into the next band stays at the same
+// image side. Columns are taken in groups of 2^sx when the map is too wide for
+// kMaxKeys buckets.
+//
+// A source tile's target box at level l is the bounding box of its sources'
+// 8x8 windows there, clipped to the level: from the bucket range of its
+// first and last sorted source, every source of the tile lies in that range
+// of bands and column groups, and the box of the range's floored extremes
+// holds all of their in-grid window cells. The tile's target rows are the
+// boxes' cells concatenated (level 0 first, each box row-major), a "virtual"
+// target list cut into runs of kTgtTile: k_corr_split_win gathers its target
+// tile's operand rows through the box arithmetic, so a source tile computes
+// its own windows' neighbourhood only. Which tile computes a window cell
+// changes no result: a cell is the same dot product of the same operand rows.
+//
+// Per edge: a counting sort over the keys (LDS histogram by atomic adds, an
+// exclusive scan, a scatter by atomic slot claims: the order within a bucket
+// is not fixed, the bucket ranges are), ord[0][q] = pixel at sorted position
+// q and ord[1][q], ord[2][q] = its x, y; the boxes of each source tile as
+// kBoxInts ints (ya, xa, bh, bw per level) after them; the (source tile,
+// virtual tile) ids mt * ntiles + vt into the edge's segment list[e * tpe ..]
+// and their number into ctr[kCtrCount + e]. Edge 0 also zeroes the tile
+// counters of k_corr_split_win, which runs after this on the same stream.
 // the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
-// which a tile-mask workgroup uses for its sort's histograms or its bitmap
+// which an order workgroup uses for its bucket counts
 constexpr int kPrepRows = 8, kPrepCols = 64;
 constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
+// ... and its level-1 block, for the virtual tile counts of the source tiles
+constexpr int kPrepL1Words = kChunk * (kPrepRows / 2) * (kPrepCols / 2);
+constexpr int kBand = 16;                 // image rows per band of the source order
+constexpr int kMaxKeys = kPrepLdsWords;   // buckets of the sort
+constexpr int kBoxInts = 4 * kMaxLevels;  // per source tile: ya, xa, bh, bw of each level
 constexpr int kCtrXcd = 0;     // [0..7] next list index of each XCD's eighth
-constexpr int kCtrCount = 8;   // [8..8+edges) marked tiles of each edge
+constexpr int kCtrCount = 8;   // [8..8+edges) listed tiles of each edge
 constexpr int kCtrInts = kCtrCount + kMaxEdgesPerLaunch;
+
+// the bucket layout of the sort: nxb column groups of 2^sx columns, nkeys
+// buckets in all
+struct KeyGeom {
+    int nxb, sx, nkeys;
+};
+
+KeyGeom key_geom(const Geom& g) {
+    const int kx = g.w[0] + 9, nb = (g.h[0] + 9 + kBand - 1) / kBand;
+    KeyGeom k{kx, 0, nb * kx};
+    while (k.nkeys > kMaxKeys && k.sx < 20) {
+        k.sx++;
+        k.nxb = (kx + (1 << k.sx) - 1) >> k.sx;
+        k.nkeys = nb * k.nxb;
+    }
+    return k;
+}
+
 struct MaskArgs {
     const float* coords;
     int* list;
     int* ctr;
-    int* order;  // [edge][3][HW]: pixel, x, y of each sorted source position
+    int* order;   // [edge][ostride]: pixel, x, y of each sorted position, then the boxes
+    long ostride;
     int mtiles, ntiles, nedges;
-    const unsigned long long* tab;  // window_tiles by floored coordinates, or null
+    KeyGeom kg;
 };
 
-// Target tiles holding a cell of the 8x8 windows (every level) of a source
-// whose coordinates floor to (fx, fy), as bits t of a 64-bit mask for target
-// tile t (ntiles <= 64).
-__device__ __forceinline__ unsigned long long window_tiles(const Geom& g, int fx, int fy) {
-    unsigned long long m = 0ull;
-    for (int l = 0; l < g.levels; l++) {
-        const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
-        const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
-        const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
-        if (xa > xb || ya > yb) continue;
-        const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
-        const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
-        m |= (hi == 63 ? 0ull : (2ull << hi)) - (1ull << lo);
+// ints of an edge's order record: 3 columns of HW, then kBoxInts per source tile
+__host__ __device__ __forceinline__ long order_stride(int HW, int mtiles) {
+    return 3L * HW + (long)kBoxInts * mtiles;
+}
+
+__device__ __forceinline__ int sort_key(const KeyGeom& k, const Geom& g, int fx, int fy) {
+    const int band = (std::min(std::max(fy, -8), g.h[0]) + 8) / kBand;
+    const int xb = (std::min(std::max(fx, -8), g.w[0]) + 8) >> k.sx;
+    return band * k.nxb + ((band & 1) ? k.nxb - 1 - xb : xb);
+}
+
+// The boxes of a source tile whose sorted sources fall in buckets b0..b1
+// (b0 <= b1), as (ya, xa, bh, bw) of each level (an empty level has bh = bw = 0).
+__device__ __forceinline__ void tile_boxes(const KeyGeom& k, const Geom& g, int b0, int b1,
+                                           int* rec) {
+    const int n = k.nxb;
+    const int band0 = b0 / n, band1 = b1 / n;
+    auto col = [&](int b) {  // column group of bucket b
+        const int s = b % n;
+        return ((b / n) & 1) ? n - 1 - s : s;
+    };
+    const int c0 = col(b0), c1 = col(b1);
+    int xlo = 0, xhi = n - 1;  // bands b0 .. b1 two or more apart: every column
+    if (band0 == band1) {
+        xlo = std::min(c0, c1);
+        xhi = std::max(c0, c1);
+    } else if (band1 == band0 + 1) {  // both partial bands end at the same side
+        if (band0 & 1)
+            xhi = std::max(c0, c1);
+        else
+            xlo = std::min(c0, c1);
     }
-    return m;
-}
-
-// window_tiles of every floored source position that can reach the image,
-// (fx, fy) in [-kTabPad, w + kTabPad) x [-kTabPad, h + kTabPad), at entry
-// (fy + kTabPad) * (w + 2 kTabPad) + fx + kTabPad. Outside that range no
-// level has a window cell: level l's window columns (fx >> l) - 3 ..
-// (fx >> l) + 4 meet 0 .. w_l - 1 only for -4 * 2^l <= fx < (w_l + 3) * 2^l,
-// inside [-32, w + 24) for l <= 3, and likewise for the rows.
-constexpr int kTabPad = 32;
-
-__global__ __launch_bounds__(256) void k_mask_table(Geom g, unsigned long long* tab) {
-    const int tw = g.w[0] + 2 * kTabPad, th = g.h[0] + 2 * kTabPad;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= tw * th) return;
-    tab[i] = window_tiles(g, i % tw - kTabPad, i / tw - kTabPad);
-}
-
-// window_tiles(g, fx, fy), from the table when there is one
-__device__ __forceinline__ unsigned long long tile_mask_of(const Geom& g,
-                                                           const unsigned long long* tab,
-                                                           int fx, int fy) {
-    if (!tab) return window_tiles(g, fx, fy);
-    const int tw = g.w[0] + 2 * kTabPad, th = g.h[0] + 2 * kTabPad;
-    const int tx = fx + kTabPad, ty = fy + kTabPad;
-    return (unsigned)tx < (unsigned)tw && (unsigned)ty < (unsigned)th ? tab[ty * tw + tx] : 0ull;
-}
-
-// ORs mask m (bit t = tile row + t) into the bitmap; a word is touched only
-// when it receives a set bit, so only words of existing tiles are
-__device__ __forceinline__ void merge_tiles(unsigned* bits, int row, unsigned long long m) {
-    const int w0 = row >> 5, sh = row & 31;
-    const unsigned part[2] = {(unsigned)m, (unsigned)(m >> 32)};
+    // floored coordinate range (of the clamped coordinates: a source clamped
+    // at a side has its in-grid cells inside the box of the clamp value)
+    const int fx0 = (xlo << k.sx) - 8, fx1 = ((xhi + 1) << k.sx) - 9;
+    const int fy0 = band0 * kBand - 8, fy1 = band1 * kBand + kBand - 9;
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const unsigned a = part[k] << sh, b = sh ? part[k] >> (32 - sh) : 0u;
-        if (a) atomicOr(&bits[w0 + k], a);
-        if (b) atomicOr(&bits[w0 + k + 1], b);
+    for (int l = 0; l < kMaxLevels; l++) {
+        const int xa = std::max((fx0 >> l) - 3, 0), xb = std::min((fx1 >> l) + 4, g.w[l] - 1);
+        const int ya = std::max((fy0 >> l) - 3, 0), yb = std::min((fy1 >> l) + 4, g.h[l] - 1);
+        const bool in = l < g.levels && xa <= xb && ya <= yb;
+        rec[4 * l] = in ? ya : 0;
+        rec[4 * l + 1] = in ? xa : 0;
+        rec[4 * l + 2] = in ? yb - ya + 1 : 0;
+        rec[4 * l + 3] = in ? xb - xa + 1 : 0;
     }
 }
 
-// Marks the target tiles of one source in row `row` of the bitmap (any ntiles)
-__device__ __forceinline__ void mark_source(const Geom& g, int fx, int fy, int row, int ntiles,
-                                            unsigned* bits, const unsigned long long* tab) {
-    if (ntiles <= 64) {
-        const unsigned long long m = tile_mask_of(g, tab, fx, fy);
-        if (m) merge_tiles(bits, row, m);
-        return;
+// Exclusive prefix sums of a[0..n) in place (LDS), by all kT threads; returns
+// the total. Each thread takes a contiguous run, the runs' sums are scanned
+// in the waves and across them through wsum (kT / 64 ints).
+template <int kT>
+__device__ int scan_excl(int* a, int n, int* wsum) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int per = (n + kT - 1) / kT;
+    const int i0 = std::min(n, tid * per), i1 = std::min(n, i0 + per);
+    int s = 0;
+    for (int i = i0; i < i1; i++) s += a[i];
+    int incl = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
     }
-    for (int l = 0; l < g.levels; l++) {
-        const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
-        const int xa = std::max(ox, 0), xb = std::min(ox + 7, g.w[l] - 1);
-        const int ya = std::max(oy, 0), yb = std::min(oy + 7, g.h[l] - 1);
-        if (xa > xb || ya > yb) continue;
-        const int lo = (g.off[l] + ya * g.w[l] + xa) / kTgtTile;
-        const int hi = (g.off[l] + yb * g.w[l] + xb) / kTgtTile;
-        for (int t = row + lo; t <= row + hi; t++) atomicOr(&bits[t >> 5], 1u << (t & 31));
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    int before = incl - s, total = 0;
+#pragma unroll
+    for (int w = 0; w < kT / 64; w++) {
+        const int v = wsum[w];
+        before += w < wv ? v : 0;
+        total += v;
     }
-}
-
-// Source order of an edge: its pixels sorted by the first row of their
-// level-0 window (floor(y) - 3, clamped to [-8, h]: rows outside never meet
-// the image at level 0), stably (pixel order within a row). Source tiles are
-// runs of 128 sorted sources, so a tile's windows span few image rows and far
-// fewer target tiles hold any of their cells than for 128 sources in image
-// order (whose +-8 px flows spread them over ~26 rows). A window cell is the
-// same dot product whichever tile computes it, so the order changes which
-// products are skipped, not any output. Counting sort in the workgroup:
-// every wave takes a contiguous 64/kT of the pixels, 64 at a time, and
-// counts their keys in its own LDS histogram (atomic adds: the counts do not
-// depend on their order); then bucket-major offsets; then the same chunks
-// again in pixel order, the lanes of a chunk holding equal keys finding each
-// other by one ballot per key bit: each lane takes its bucket's next slot
-// plus its rank among the equal lanes below it (the lowest of them advances
-// the slot), writes its pixel and coordinates there, and marks the target
-// tiles of its windows in the row of its source tile (masks formed in the
-// histogram pass when a wave's pixels stay in registers). Writes ord[0][q] =
-// the pixel at sorted position q and ord[1][q], ord[2][q] = its x, y. `lds` holds 2 * (kT / 64) * kSortBuckets ints (or is null: no room). A map with
-// more rows than that is not sorted: returns false, and neither ord nor the
-// bitmap is written.
-constexpr int kSortBuckets = 256;
-
-// the lanes of the wave whose key equals this lane's, among `live`
-__device__ __forceinline__ unsigned long long equal_keys(int key, int nbits,
-                                                         unsigned long long live) {
-    unsigned long long m = live;
-    for (int b = 0; b < nbits; b++) {  // uniform
-        const bool bit = (key >> b) & 1;
-        const unsigned long long bal = __ballot(bit);
-        m &= bit ? bal : ~bal;
+    for (int i = i0; i < i1; i++) {
+        const int c = a[i];
+        a[i] = before;
+        before += c;
     }
-    return m;
+    __syncthreads();  // a is complete; wsum may be reused
+    return total;
 }
 
 template <int kT>
-__device__ bool sort_and_mark(const Geom& g, const float* cc, int* ord, int* lds, int* wsum,
-                              unsigned* bits, int ntiles, const unsigned long long* tab) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int HW = g.HW, nb = g.h[0] + 9;
-    if (nb > kSortBuckets || !lds) return false;
+__device__ void order_and_boxes(const MaskArgs& a, const Geom& g, int e, int* keys, int* ntv,
+                                int* wsum) {
+    const int tid = threadIdx.x;
+    const int HW = g.HW, mtiles = a.mtiles, ntiles = a.ntiles;
+    const KeyGeom kg = a.kg;
+    const float* cc = a.coords + (size_t)e * 2 * HW;
+    int* ord = a.order + (size_t)e * a.ostride;
     float* oxy = reinterpret_cast<float*>(ord + HW);
-    const int nbits = 32 - __builtin_clz(nb - 1);
-    const unsigned long long below = (1ull << lane) - 1ull;
-    int* hist = lds;                             // [(kT / 64)][kSortBuckets]
-    int* pos = lds + (kT / 64) * kSortBuckets;  // [(kT / 64)][kSortBuckets]: next slot
-    for (int i = tid; i < (kT / 64) * kSortBuckets; i += kT) hist[i] = 0;
-    __syncthreads();  // also orders the caller's clearing of the bitmap
-    const int part = (HW + (kT / 64) - 1) / (kT / 64);  // pixels of each wave
-    const int q0 = std::min(HW, wv * part), q1 = std::min(HW, q0 + part);
-    auto key_of = [&](float y) {
-        const int oy = floor_clamped(y) - 3;
-        return std::min(std::max(oy, -8), g.h[0]) + 8;
-    };
-    // the coordinates of kG chunks are loaded before the first is used; when
-    // a wave's pixels are one such group they stay in registers for the
-    // scatter. 1024-thread workgroups serve maps up to 4096 pixels, 256 a
-    // wave: 4 chunks, which keeps the launch within 64 VGPRs (two
-    // workgroups a CU)
-    constexpr int kG = kT >= 1024 ? 4 : 12;
-    float xv[kG], yv[kG];
-    auto load = [&](int pg) {
+    int* rec = ord + 3 * HW;
+    for (int i = tid; i < kg.nkeys; i += kT) keys[i] = 0;
+    if (e == 0 && tid < 8) a.ctr[kCtrXcd + tid] = 0;
+    __syncthreads();
+    // A thread's sources are p = tid + u * kT; up to kU of them stay in
+    // registers between the counting and the scatter (a map of more than
+    // kU * kT pixels loads its coordinates again for the scatter).
+    constexpr int kU = kT >= 1024 ? 4 : 12;
+    const bool keep = HW <= kU * kT;
+    int kv[kU];
+    float xv[kU], yv[kU];
+    auto load = [&](int p0) {
 #pragma unroll
-        for (int u = 0; u < kG; u++) {
-            const int p = std::min(pg + 64 * u + lane, q1 - 1);
+        for (int u = 0; u < kU; u++) {
+            const int p = std::min(p0 + u * kT + tid, HW - 1);
             xv[u] = cc[p];
             yv[u] = cc[HW + p];
         }
+#pragma unroll
+        for (int u = 0; u < kU; u++)
+            kv[u] = sort_key(kg, g, floor_clamped(xv[u]), floor_clamped(yv[u]));
     };
-    const bool one = q1 - q0 <= 64 * kG;
-    // with the wave's pixels in registers and at most 64 target tiles, each
-    // source's tile mask is formed here, while the loads of the histogram
-    // pass are what the waves wait for, and only merged in the scatter
-    const bool pre = one && ntiles <= 64;
-    unsigned long long mk[kG];
-    for (int pg = q0; pg < q1; pg += 64 * kG) {
-        load(pg);
+    for (int p0 = 0; p0 < HW; p0 += kU * kT) {
+        load(p0);
 #pragma unroll
-        for (int u = 0; u < kG; u++) {
-            if (pg + 64 * u + lane < q1) atomicAdd(&hist[wv * kSortBuckets + key_of(yv[u])], 1);
-            mk[u] = pre ? tile_mask_of(g, tab, floor_clamped(xv[u]), floor_clamped(yv[u])) : 0ull;
-        }
+        for (int u = 0; u < kU; u++)
+            if (p0 + u * kT + tid < HW) atomicAdd(&keys[kv[u]], 1);
     }
     __syncthreads();
-    {
-        // thread b < kSortBuckets: bucket b's total, its exclusive prefix over
-        // the buckets (a wave scan, then the totals of the waves below), and
-        // each wave's first slot in it
-        const int bkt = tid;
-        const bool bw = tid < kSortBuckets;  // uniform per wave
-        int tot = 0, incl = 0;
-        if (bw) {
+    scan_excl<kT>(keys, kg.nkeys, wsum);  // keys[b]: first sorted position of bucket b
+    for (int p0 = 0; p0 < HW; p0 += kU * kT) {
+        if (!keep) load(p0);
 #pragma unroll
-            for (int w = 0; w < (kT / 64); w++) tot += hist[w * kSortBuckets + bkt];
-            incl = tot;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int v = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += v;
-            }
-            if (lane == 63) wsum[wv] = incl;
-        }
-        __syncthreads();
-        if (bw) {
-            int start = incl - tot;
-            for (int w = 0; w < wv; w++) start += wsum[w];
-#pragma unroll
-            for (int w = 0; w < (kT / 64); w++) {
-                pos[w * kSortBuckets + bkt] = start;
-                start += hist[w * kSortBuckets + bkt];
-            }
-        }
-    }
-    __syncthreads();
-    // stable scatter, chunk by chunk in pixel order: every lane reads its
-    // bucket's next slot, adds its rank among the equal lanes below it, and
-    // the lowest of them advances the slot past all of them
-    for (int pg = q0; pg < q1; pg += 64 * kG) {
-        if (!one) load(pg);
-#pragma unroll
-        for (int u = 0; u < kG; u++) {
-            const int pb = pg + 64 * u;
-            if (pb >= q1) break;  // uniform
-            const int p = pb + lane;
-            const bool act = p < q1;
-            const int key = act ? key_of(yv[u]) : 0;
-            const unsigned long long m = equal_keys(key, nbits, __ballot(act));
-            const int base = pos[wv * kSortBuckets + key];
-            const int rank = __builtin_popcountll(m & below);
-            if (act) {
-                const int q = base + rank;
-                if (rank == 0) pos[wv * kSortBuckets + key] = base + __builtin_popcountll(m);
+        for (int u = 0; u < kU; u++) {
+            const int p = p0 + u * kT + tid;
+            if (p < HW) {
+                const int q = atomicAdd(&keys[kv[u]], 1);
                 ord[q] = p;
                 oxy[q] = xv[u];
                 oxy[HW + q] = yv[u];
-                if (pre) {
-                    if (mk[u]) merge_tiles(bits, q / kSrcTile * ntiles, mk[u]);
-                } else {
-                    mark_source(g, floor_clamped(xv[u]), floor_clamped(yv[u]),
-                                q / kSrcTile * ntiles, ntiles, bits, tab);
-                }
             }
         }
     }
-    return true;
-}
-
-template <int kT>
-__device__ void tile_mask_edge(const MaskArgs& a, const Geom& g, int e, unsigned* big,
-                               unsigned* small, int small_words, int* wave_sum) {
-    const float* coords = a.coords;
-    int* list = a.list;
-    int* ctr = a.ctr;
-    const int mtiles = a.mtiles, ntiles = a.ntiles;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int tpe = mtiles * ntiles;
-    const int nw = (tpe + 31) / 32;
-    // the bitmap in `small` when it fits, the sort's histograms then in
-    // `big` (kPrepLdsWords words); else the bitmap in `big` and no sort
-    const bool fits = nw <= small_words;
-    unsigned* bits = fits ? small : big;
-    for (int i = tid; i < nw; i += kT) bits[i] = 0u;
-    if (e == 0 && tid < 8) ctr[kCtrXcd + tid] = 0;
-    const float* cc = coords + (size_t)e * 2 * g.HW;
-    int* ord = a.order + (size_t)e * 3 * g.HW;
-    static_assert(2 * (kT / 64) * kSortBuckets <= kPrepLdsWords, "sort LDS");
-    int* sort_lds = fits ? reinterpret_cast<int*>(big) : nullptr;
-    if (!sort_and_mark<kT>(g, cc, ord, sort_lds, wave_sum, bits, ntiles, a.tab)) {  // uniform
-        // pixel order: the order is the identity, written beside the mask.
-        // A wave's 64 consecutive sources lie in one source tile (kSrcTile is
-        // a multiple of 64). When an edge's target tiles fit a 64-bit mask,
-        // each lane builds the mask of the tiles its windows touch, the wave
-        // ORs them by shuffles and lane 0 merges the result into the bitmap;
-        // otherwise every lane marks its tiles in the bitmap itself.
-        __syncthreads();  // the bitmap is clear
-        float* oxy = reinterpret_cast<float*>(ord + g.HW);
-        constexpr int kU = 4;  // sources per thread whose coordinates load together
-        for (int pb = 0; pb < g.HW; pb += kU * kT) {
-            float xs[kU], ys[kU];
-#pragma unroll
-            for (int u = 0; u < kU; u++) {
-                const int q = std::min(pb + u * kT + tid, g.HW - 1);
-                xs[u] = cc[q];
-                ys[u] = cc[g.HW + q];
-            }
-#pragma unroll
-            for (int u = 0; u < kU; u++) {
-                const int pw = pb + u * kT + (tid & ~63);  // the wave's first source
-                if (pw >= g.HW) break;                                // uniform
-                const bool in = pw + lane < g.HW;
-                const int row = pw / kSrcTile * ntiles;  // first tile id of the source tile
-                const int fx = floor_clamped(xs[u]), fy = floor_clamped(ys[u]);
-                if (in) {
-                    ord[pw + lane] = pw + lane;
-                    oxy[pw + lane] = xs[u];
-                    oxy[g.HW + pw + lane] = ys[u];
-                }
-                if (ntiles > 64) {
-                    if (in) mark_source(g, fx, fy, row, ntiles, bits, a.tab);
-                    continue;
-                }
-                const unsigned long long m = in ? tile_mask_of(g, a.tab, fx, fy) : 0ull;
-                unsigned m0 = (unsigned)m, m1 = (unsigned)(m >> 32);
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) {
-                    m0 |= __shfl_xor(m0, off, 64);
-                    m1 |= __shfl_xor(m1, off, 64);
-                }
-                if (lane == 0) merge_tiles(bits, row, ((unsigned long long)m1 << 32) | m0);
-            }
+    __syncthreads();  // keys[b]: one past the last sorted position of bucket b
+    // bucket of sorted position q: the first b whose end exceeds q
+    auto bucket_of = [&](int q) {
+        int lo = 0, hi = kg.nkeys - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (keys[mid] > q)
+                hi = mid;
+            else
+                lo = mid + 1;
         }
+        return lo;
+    };
+    for (int mt = tid; mt < mtiles; mt += kT) {
+        int r[kBoxInts];
+        tile_boxes(kg, g, bucket_of(mt * kSrcTile), bucket_of(std::min(mt * kSrcTile + kSrcTile, HW) - 1),
+                   r);
+        int total = 0;
+#pragma unroll
+        for (int i = 0; i < kBoxInts; i++) rec[(size_t)mt * kBoxInts + i] = r[i];
+#pragma unroll
+        for (int l = 0; l < kMaxLevels; l++) total += r[4 * l + 2] * r[4 * l + 3];
+        ntv[mt] = (total + kTgtTile - 1) / kTgtTile;
     }
     __syncthreads();
-    // compaction, kT tiles a round: ballot ranks within a wave,
-    // wave totals through LDS
-    int* seg = list + (size_t)e * tpe;
-    int base = 0;
-    for (int t0 = 0; t0 < tpe; t0 += kT) {
-        const int t = t0 + tid;
-        const bool m = t < tpe && ((bits[t >> 5] >> (t & 31)) & 1u);
-        const unsigned long long bal = __ballot(m);
-        const int rank = __builtin_popcountll(bal & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_sum[wv] = __builtin_popcountll(bal);
-        __syncthreads();
-        int before = 0, all = 0;
-#pragma unroll
-        for (int q = 0; q < kT / 64; q++) {
-            const int v = wave_sum[q];
-            before += q < wv ? v : 0;
-            all += v;
-        }
-        if (m) seg[base + before + rank] = t;
-        base += all;
-        __syncthreads();  // wave_sum is rewritten by the next round
+    const int count = scan_excl<kT>(ntv, mtiles, wsum);  // ntv[mt]: first list slot of mt
+    int* seg = a.list + (size_t)e * mtiles * ntiles;
+    for (int mt = tid; mt < mtiles; mt += kT) {
+        const int s0 = ntv[mt], s1 = mt + 1 < mtiles ? ntv[mt + 1] : count;
+        for (int s = s0; s < s1; s++) seg[s] = mt * ntiles + (s - s0);
     }
-    if (tid == 0) ctr[kCtrCount + e] = base;
+    if (tid == 0) a.ctr[kCtrCount + e] = count;
 }
 
 // Split modes of the preparation and the window kernel
@@ -559,9 +457,10 @@ __global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
         // the tile-mask chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        tile_mask_edge<kT>(mk, g, blockIdx.x, reinterpret_cast<unsigned*>(&l0[0][0][0]),
-                           reinterpret_cast<unsigned*>(&l1[0][0][0]), (int)(sizeof(l1) / 4),
-                           wave_sum);
+        static_assert(sizeof(l0) >= kMaxKeys * sizeof(int) &&
+                          sizeof(l1) >= kPrepL1Words * sizeof(int), "order LDS");
+        order_and_boxes<kT>(mk, g, blockIdx.x, reinterpret_cast<int*>(&l0[0][0][0]),
+                            reinterpret_cast<int*>(&l1[0][0][0]), wave_sum);
         return;
     }
     const int tid = threadIdx.x;
@@ -762,9 +661,9 @@ using bool_c = std::integral_constant<bool, B>;
 template <bool kF16>
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* __restrict__ feat, long slot_elems, EdgeSlots es,
-    const int* __restrict__ order, float* __restrict__ win, int slot0, Geom g, float alpha,
-    int mtiles, int ntiles, int nedges, const int* __restrict__ list, int* __restrict__ ctr,
-    int alo) {
+    const int* __restrict__ order, long ostride, float* __restrict__ win, int slot0, Geom g,
+    float alpha, int mtiles, int ntiles, int nedges, const int* __restrict__ list,
+    int* __restrict__ ctr, int alo) {
     __shared__ SplitSmem sm;
     __shared__ int next_tile;
     const int tpe = mtiles * ntiles;
@@ -809,19 +708,53 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const bool before_idx = (int)(threadIdx.x & 63) < nedges && pre <= idx;
     const int e = __builtin_popcountll(__ballot(before_idx)) - 1;
     const int r = list[(size_t)e * tpe + (idx - __builtin_amdgcn_readlane(pre, e))];
-    const int mt = r / ntiles, nt = r - mt * ntiles;
+    const int mt = r / ntiles, vt = r - mt * ntiles;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int HW = g.HW, Ttot = g.Ttot;
-    const int p0 = mt * kSrcTile, t0 = nt * kTgtTile;
+    const int p0 = mt * kSrcTile, v0 = vt * kTgtTile;
     const size_t plane = (size_t)g.C * Ttot;
     const unsigned short* fa = feat + (size_t)es.si[e] * slot_elems;
     const unsigned short* fb = feat + (size_t)es.sj[e] * slot_elems;
     // alpha over both frames' split scales (powers of two: no rounding)
     const float fs = alpha * *reinterpret_cast<const float*>(fa + 2 * plane) *
                      *reinterpret_cast<const float*>(fb + 2 * plane);
-    const int* ord = order + (size_t)e * 3 * HW;
+    const int* ord = order + (size_t)e * ostride;
+    // the source tile's target boxes: virtual rows cum[l] .. cum[l + 1] - 1 are
+    // level l's box (bh x bw cells from row ya, column xa), row-major
+    int bya[kMaxLevels], bxa[kMaxLevels], bwd[kMaxLevels], cum[kMaxLevels + 1];
+    {
+        const int* rec = ord + 3 * HW + mt * kBoxInts;
+        cum[0] = 0;
+#pragma unroll
+        for (int l = 0; l < kMaxLevels; l++) {
+            bya[l] = rec[4 * l];
+            bxa[l] = rec[4 * l + 1];
+            bwd[l] = rec[4 * l + 3];
+            cum[l + 1] = cum[l] + rec[4 * l + 2] * bwd[l];
+        }
+    }
+    const int total = cum[kMaxLevels];
+    // target row (concatenated levels) of virtual row v; rows past the boxes
+    // read row 0 (reaching accumulator cells never read), and every row is
+    // clamped into the slot
+    auto trow = [&](int v) {
+        int r = v, ya = bya[0], xa = bxa[0], bw = bwd[0], wl = g.w[0], ofs = g.off[0];
+#pragma unroll
+        for (int l = 1; l < kMaxLevels; l++)
+            if (v >= cum[l]) {  // the last level starting at or before v (a nonempty one)
+                r = v - cum[l];
+                ya = bya[l];
+                xa = bxa[l];
+                bw = bwd[l];
+                wl = g.w[l];
+                ofs = g.off[l];
+            }
+        const int q = bw > 0 ? r / bw : 0;
+        const int t = v < total ? ofs + (ya + q) * wl + xa + (r - q * bw) : 0;
+        return std::min(std::max(t, 0), Ttot - 1);
+    };
 
     // Staging by direct-to-LDS loads (global_load_lds_dwordx4): lane l of wave
     // w writes bytes 16*(64w + l) of a 4 KB region, i.e. row tid/2, physical
@@ -836,8 +769,8 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int pa = std::min((unsigned)ord[std::min(p0 + hr, HW - 1)], (unsigned)(HW - 1));
     if (!(tid & 1)) sm.pix[hr] = pa;  // read after the chunk loop's barriers
     const unsigned short* ga = fa + (size_t)pa * kChunk + hh;
-    const unsigned short* gb0 = fb + (size_t)std::min(t0 + hr, Ttot - 1) * kChunk + hh;
-    const unsigned short* gb1 = fb + (size_t)std::min(t0 + 128 + hr, Ttot - 1) * kChunk + hh;
+    const unsigned short* gb0 = fb + (size_t)trow(v0 + hr) * kChunk + hh;
+    const unsigned short* gb1 = fb + (size_t)trow(v0 + 128 + hr) * kChunk + hh;
     const size_t kstep = (size_t)Ttot * kChunk;
     const int wdst = wave * 512;  // this wave's 1 KB of a 4 KB region, in u16
 
@@ -948,7 +881,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     if constexpr (kF16) {
         // a target tile with a pooled row has lo planes (pooled fp16 values
         // are fp32 sums)
-        const bool blo = alo || (g.levels > 1 && t0 + kTgtTile > g.off[1]);
+        const bool blo = alo || (cum[1] < total && v0 + kTgtTile > cum[1]);
         if (alo)
             chunk_loop(bool_c<true>{}, bool_c<true>{});
         else if (blo)
@@ -968,21 +901,11 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     lds_barrier();  // every wave is done with the stages before T overwrites them
 
     // ---- window extraction ----
-    // rows of level l inside this tile: [lr0[l], lr1[l]] (empty: lr0 > lr1)
-    int lr0[kMaxLevels], lr1[kMaxLevels];
+    // whether this tile holds virtual rows of level l's box
+    bool lin[kMaxLevels];
 #pragma unroll
-    for (int l = 0; l < kMaxLevels; l++) {
-        lr0[l] = 1 << 30;
-        lr1[l] = -(1 << 30);
-        if (l < g.levels) {
-            const int a = std::max(t0, g.off[l]) - g.off[l];
-            const int b = std::min(t0 + kTgtTile, g.off[l] + g.h[l] * g.w[l]) - 1 - g.off[l];
-            if (a <= b) {
-                lr0[l] = a / g.w[l];
-                lr1[l] = b / g.w[l];
-            }
-        }
-    }
+    for (int l = 0; l < kMaxLevels; l++)
+        lin[l] = cum[l + 1] > cum[l] && cum[l] < v0 + kTgtTile && cum[l + 1] > v0;
     // accumulator layout of the 32x32 MFMA: lane l, register v holds
     // D[i][j] with j = l % 32 (target) and i = 8*(v/4) + 4*(l/32) + v%4 (source)
     const int khalf = lane >> 5;
@@ -1025,15 +948,17 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             const int woff = (int)win_index(0, 0, cx, HW, sm.pix[lsrc]) * 4;
 #pragma unroll
             for (int l = 0; l < kMaxLevels; l++) {
-                if (lr0[l] > lr1[l]) continue;  // level not in this tile
+                if (!lin[l]) continue;  // level not in this tile
                 const int wl = g.w[l], hl = g.h[l];
+                const unsigned bw = (unsigned)bwd[l];
                 const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
                 const int xs = ox + cx;
                 const bool colok = pin && (unsigned)xs < (unsigned)wl;
-                // tile row of cell (cx, 0); wraps harmlessly for far origins
-                // (then xs or the rows are out of range)
-                unsigned tl = (unsigned)(g.off[l] - t0) + (unsigned)oy * (unsigned)wl +
-                              (unsigned)xs;
+                // tile row of cell (cx, 0): every in-grid cell of the tile's
+                // windows lies in the box; the row wraps harmlessly for cells
+                // outside the grid (then xs or the row is out of range)
+                unsigned tl = (unsigned)(cum[l] - v0) + (unsigned)(oy - bya[l]) * bw +
+                              (unsigned)(xs - bxa[l]);
                 unsigned ta = tl * (unsigned)kTStride;  // offset of row tl in T
                 float v[8];
                 bool ok[8];  // this lane's cell of window row cy is in the tile and grid
@@ -1042,8 +967,8 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                     ok[cy] = colok && (unsigned)(oy + cy) < (unsigned)hl &&
                              tl < (unsigned)kTgtTile;
                     v[cy] = Tcol[ok[cy] ? ta : 0u];
-                    tl += (unsigned)wl;
-                    ta += (unsigned)wl * (unsigned)kTStride;
+                    tl += bw;
+                    ta += bw * (unsigned)kTStride;
                 }
 #pragma unroll
                 for (int cy = 0; cy < 8; cy++)
@@ -1151,11 +1076,13 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     const int ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const long total = (long)n * mtiles * ntiles;
     if (total > 0x7fffffffL) return fail(SLK_E_ARG, "correlation grid too large");
-    if ((long)mtiles * ntiles > 32L * kPrepLdsWords)
-        return fail(SLK_E_ARG, "correlation tiles per edge exceed the tile bitmap");
+    const KeyGeom kg = key_geom(g);
+    if (kg.nkeys > kMaxKeys) return fail(SLK_E_ARG, "correlation: map too tall for the source sort");
+    if (mtiles > kPrepL1Words)
+        return fail(SLK_E_ARG, "correlation: more source tiles per edge than the order pass holds");
+    const long ostride = order_stride(g.HW, mtiles);
     MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
-                ctx->src_order.as<int>(), mtiles, ntiles, n,
-                ctx->mask_tab.as<unsigned long long>()};
+                ctx->src_order.as<int>(), ostride, mtiles, ntiles, n, kg};
     // feature preparation and the tile mask, one launch (after the frames'
     // maxima under the fp16 split)
     SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
@@ -1164,13 +1091,13 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
         const long se = (long)slot_elems(g);
         if (mode == kSplitF16)
             hipLaunchKernelGGL(k_corr_split_win<true>, dim3(ctx->ws_grid), dim3(256), 0, stream,
-                               feat, se, es, ctx->src_order.as<int>(), win, slot0, g, ctx->alpha,
-                               mtiles, ntiles, n, ctx->tile_list.as<int>(),
+                               feat, se, es, ctx->src_order.as<int>(), ostride, win, slot0, g,
+                               ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
                                ctx->tile_ctr.as<int>(), alo ? 1 : 0);
         else
             hipLaunchKernelGGL(k_corr_split_win<false>, dim3(ctx->ws_grid), dim3(256), 0, stream,
-                               feat, se, es, ctx->src_order.as<int>(), win, slot0, g, ctx->alpha,
-                               mtiles, ntiles, n, ctx->tile_list.as<int>(),
+                               feat, se, es, ctx->src_order.as<int>(), ostride, win, slot0, g,
+                               ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
                                ctx->tile_ctr.as<int>(), 1);
     }
     SLK_HIP(hipGetLastError());
@@ -1211,7 +1138,7 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
     }
     // sources only need level 0 (their own launch); targets need every level
     {
-        const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
+        const MaskArgs none{};
         SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, 0, n, false, none, mode, stream));
     }
     return mask_and_windows(ctx, fm, fstride, sf, g, n, n, true, es, feat, n, coords, win, slot0,
@@ -1230,7 +1157,7 @@ void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     *slot_bytes = slot_elems(g) * sizeof(unsigned short);
     *tiles_per_edge = mtiles * ntiles * sizeof(int);
-    *order_per_edge = 3 * (size_t)g.HW * sizeof(int);
+    *order_per_edge = (size_t)order_stride(g.HW, (int)mtiles) * sizeof(int);
     *ctr_bytes = kCtrInts * sizeof(int);
 }
 
@@ -1246,16 +1173,9 @@ int corr_split_alloc(slk_ctx* ctx) {
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
     SLK_TRY(ctx->tile_list.ensure(tiles * sizeof(int)));
-    SLK_TRY(ctx->src_order.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * 3 *
-                                  g.HW * sizeof(int)));
+    SLK_TRY(ctx->src_order.ensure((size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) *
+                                  order_stride(g.HW, (int)mtiles) * sizeof(int)));
     SLK_TRY(ctx->tile_ctr.ensure(kCtrInts * sizeof(int)));
-    if (ntiles <= 64) {  // tile masks as 64-bit words: their table by position
-        const long entries = (long)(g.w[0] + 2 * kTabPad) * (g.h[0] + 2 * kTabPad);
-        SLK_TRY(ctx->mask_tab.ensure((size_t)entries * sizeof(unsigned long long)));
-        hipLaunchKernelGGL(k_mask_table, dim3((unsigned)((entries + 255) / 256)), dim3(256), 0, 0,
-                           g, ctx->mask_tab.as<unsigned long long>());
-        SLK_HIP(hipGetLastError());
-    }
     // the correlation workgroups: two per CU, a multiple of the 8 XCDs
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device) !=
@@ -1293,7 +1213,7 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     SLK_TRY(ctx->frame_max.ensure((size_t)nframes * kMaxParts * sizeof(float)));
     SlotFrames sf{};
     sf.ident = 1;
-    const MaskArgs none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, nullptr};
+    const MaskArgs none{};
     const int mode = split_mode(ctx);
     if (dtype == SLK_F32)
         SLK_TRY(prep_slots_to(ctx, static_cast<const float*>(fmaps), fstride, sf, g, 0, nframes,

@@ -84,8 +84,7 @@ struct slk_ctx {
     slk::DevBuf frame_max;  // partial maxima of |x| of each slot's frame (the fp16 split's scale)
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
-    slk::DevBuf src_order;  // per edge: sources sorted by window row (pixel, x, y columns)
-    slk::DevBuf mask_tab;   // target-tile mask of a source by its floored coordinates, or empty
+    slk::DevBuf src_order;  // per edge: sources sorted by window position (pixel, x, y), boxes
     int ws_grid = 0;        // workgroups of the batched correlation kernel
     // single-edge persistent volume + pyramid (build_correlation/sample_correlation)
     slk::DevBuf single_lvl[slk::kMaxLevels];
