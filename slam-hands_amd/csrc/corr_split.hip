@@ -738,21 +738,19 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int total = cum[kMaxLevels];
     // target row (concatenated levels) of virtual row v; rows past the boxes
     // read row 0 (reaching accumulator cells never read), and every row is
-    // clamped into the slot
+    // clamped into the slot. (Each level's candidate is formed and the one
+    // whose range holds v kept: a selection of the box fields by a computed
+    // level would index them from memory.)
     auto trow = [&](int v) {
-        int r = v, ya = bya[0], xa = bxa[0], bw = bwd[0], wl = g.w[0], ofs = g.off[0];
+        int t = 0;
 #pragma unroll
-        for (int l = 1; l < kMaxLevels; l++)
-            if (v >= cum[l]) {  // the last level starting at or before v (a nonempty one)
-                r = v - cum[l];
-                ya = bya[l];
-                xa = bxa[l];
-                bw = bwd[l];
-                wl = g.w[l];
-                ofs = g.off[l];
-            }
-        const int q = bw > 0 ? r / bw : 0;
-        const int t = v < total ? ofs + (ya + q) * wl + xa + (r - q * bw) : 0;
+        for (int l = 0; l < kMaxLevels; l++) {
+            const int r = v - cum[l];
+            const int bw = std::max(bwd[l], 1);
+            const int q = r / bw;
+            const int c = g.off[l] + (bya[l] + q) * g.w[l] + bxa[l] + (r - q * bw);
+            t = r >= 0 && v < cum[l + 1] ? c : t;
+        }
         return std::min(std::max(t, 0), Ttot - 1);
     };
 
@@ -909,19 +907,23 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // accumulator layout of the 32x32 MFMA: lane l, register v holds
     // D[i][j] with j = l % 32 (target) and i = 8*(v/4) + 4*(l/32) + v%4 (source)
     const int khalf = lane >> 5;
-    // extraction: lane = (source g8 of a group of 8, window column cx). A wave
-    // takes its 16 columns of T (sources) as two groups of 8 and walks the 8
-    // window rows, so every read and store instruction covers 8 sources x 8
-    // consecutive cells and all per-source set-up is plain per-lane arithmetic.
-    const int g8 = lane >> 3, cx = lane & 7;
+    // extraction: a wave takes its 16 columns of T (sources); lane = (source jj,
+    // quarter qq), and in each of 4 rounds a lane reads 4 consecutive cells of
+    // one window row (cells 4 * (f & 1) .. +3 of row f >> 1, f = 4 * round +
+    // qq) and stores them with one 16-byte store, so a store instruction covers
+    // 16 sources x 4 quarter-rows.
+    const int jj = lane >> 2, qq = lane & 3;
     // Window stores go through a buffer resource over this edge's window slot:
-    // a lane whose cell is not stored (outside the tile, the grid or the
-    // source range) gets an offset past the slot's size, and the hardware
-    // discards the store. Every store instruction is then issued without a
-    // branch around it.
+    // a lane with nothing to store gets an offset past the slot's size, and
+    // the hardware discards the store, so store instructions are issued
+    // without a branch around them. A 4-cell piece is stored whole by the one
+    // tile holding all of its in-grid cells (the cells outside the grid are
+    // never read: the lookup zeroes them); a piece whose in-grid cells a
+    // virtual-tile boundary splits is stored cell by cell by both tiles.
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         win + win_index(slot0 + e, 0, 0, HW, 0), 0, kMaxLevels * 64 * HW * (int)sizeof(float),
         kBufWord3);
+    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
@@ -937,44 +939,57 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                                 acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
             }
         lds_barrier();
+        const int s = wave * 16 + jj;                            // column of T
+        const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
+        const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
+        const bool pin = p0 + lsrc < HW;
+        const float* Tcol = &sm.u.T[0][s];
+        // byte offset of cell 0 of row 0 of level 0 of this source in the slot
+        const int woff = (int)win_index(0, 0, 0, HW, sm.pix[lsrc]) * 4;
 #pragma unroll
-        for (int grp = 0; grp < 2; grp++) {
-            const int s = wave * 16 + grp * 8 + g8;                 // column of T
-            const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
-            const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
-            const bool pin = p0 + lsrc < HW;
-            const float* Tcol = &sm.u.T[0][s];
-            // byte offset of cell (cx, row 0) of level 0 in the slot
-            const int woff = (int)win_index(0, 0, cx, HW, sm.pix[lsrc]) * 4;
+        for (int l = 0; l < kMaxLevels; l++) {
+            if (!lin[l]) continue;  // level not in this tile
+            const int wl = g.w[l], hl = g.h[l], bw = bwd[l];
+            const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
 #pragma unroll
-            for (int l = 0; l < kMaxLevels; l++) {
-                if (!lin[l]) continue;  // level not in this tile
-                const int wl = g.w[l], hl = g.h[l];
-                const unsigned bw = (unsigned)bwd[l];
-                const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
-                const int xs = ox + cx;
-                const bool colok = pin && (unsigned)xs < (unsigned)wl;
-                // tile row of cell (cx, 0): every in-grid cell of the tile's
-                // windows lies in the box; the row wraps harmlessly for cells
-                // outside the grid (then xs or the row is out of range)
-                unsigned tl = (unsigned)(cum[l] - v0) + (unsigned)(oy - bya[l]) * bw +
-                              (unsigned)(xs - bxa[l]);
-                unsigned ta = tl * (unsigned)kTStride;  // offset of row tl in T
-                float v[8];
-                bool ok[8];  // this lane's cell of window row cy is in the tile and grid
+            for (int rd = 0; rd < 4; rd++) {
+                const int f = 4 * rd + qq, cy = f >> 1, cx0 = (f & 1) * 4;
+                const int y = oy + cy, x0 = ox + cx0;
+                const bool rowok = pin && (unsigned)y < (unsigned)hl;
+                // tile row of the piece's first cell: every in-grid cell of the
+                // tile's windows lies in the box; the value is meaningless
+                // (and unused) for rows outside the grid
+                const unsigned tl0 = (unsigned)(cum[l] - v0) +
+                                     (unsigned)(y - bya[l]) * (unsigned)bw +
+                                     (unsigned)(x0 - bxa[l]);
+                float v[4];
+                bool val[4];
+                bool any = false, all = true;
 #pragma unroll
-                for (int cy = 0; cy < 8; cy++) {
-                    ok[cy] = colok && (unsigned)(oy + cy) < (unsigned)hl &&
-                             tl < (unsigned)kTgtTile;
-                    v[cy] = Tcol[ok[cy] ? ta : 0u];
-                    tl += bw;
-                    ta += bw * (unsigned)kTStride;
+                for (int i = 0; i < 4; i++) {
+                    const bool gin = (unsigned)(x0 + i) < (unsigned)wl;
+                    const unsigned tl = tl0 + (unsigned)i;
+                    const bool it = tl < (unsigned)kTgtTile;
+                    val[i] = rowok && gin && it;
+                    any = any || val[i];
+                    all = all && (!gin || it);
+                    v[i] = fs * Tcol[(it ? tl : 0u) * (unsigned)kTStride];
                 }
+                const int off = woff + ((l * 8 + cy) * HW * 8 + cx0) * 4;
+                const u32x4_t pk = {__builtin_bit_cast(unsigned, v[0]),
+                                    __builtin_bit_cast(unsigned, v[1]),
+                                    __builtin_bit_cast(unsigned, v[2]),
+                                    __builtin_bit_cast(unsigned, v[3])};
+                __builtin_amdgcn_raw_buffer_store_b128(pk, wrs, any && all ? off : kBufDiscard,
+                                                       0, 0);
+                const bool split = any && !all;
+                if (__ballot(split)) {  // uniform, rare: a piece cut by the tile's ends
 #pragma unroll
-                for (int cy = 0; cy < 8; cy++)
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        __builtin_bit_cast(unsigned, fs * v[cy]), wrs,
-                        ok[cy] ? woff + (l * 8 + cy) * HW * 32 : kBufDiscard, 0, 0);
+                    for (int i = 0; i < 4; i++)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __builtin_bit_cast(unsigned, v[i]), wrs,
+                            split && val[i] ? off + 4 * i : kBufDiscard, 0, 0);
+                }
             }
         }
     }
