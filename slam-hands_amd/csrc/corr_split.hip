@@ -956,39 +956,38 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                 const int f = 4 * rd + qq, cy = f >> 1, cx0 = (f & 1) * 4;
                 const int y = oy + cy, x0 = ox + cx0;
                 const bool rowok = pin && (unsigned)y < (unsigned)hl;
-                // tile row of the piece's first cell: every in-grid cell of the
-                // tile's windows lies in the box; the value is meaningless
-                // (and unused) for rows outside the grid
-                const unsigned tl0 = (unsigned)(cum[l] - v0) +
-                                     (unsigned)(y - bya[l]) * (unsigned)bw +
-                                     (unsigned)(x0 - bxa[l]);
+                // the piece's in-grid cells are ia..ib; tile row of its first
+                // cell (every in-grid cell of the tile's windows lies in the
+                // box; the value is meaningless, and unused, for rows outside
+                // the grid)
+                const int ia = std::max(0, -x0), ib = std::min(3, wl - 1 - x0);
+                const int tl0 = (int)((unsigned)(cum[l] - v0) +
+                                      (unsigned)(y - bya[l]) * (unsigned)bw +
+                                      (unsigned)(x0 - bxa[l]));
+                const int ta = tl0 + ia, tb = tl0 + ib;
+                // some in-grid cell in this tile; all of them
+                const bool has = rowok && ia <= ib && ta < kTgtTile && tb >= 0;
+                const bool full = has && ta >= 0 && tb < kTgtTile;
                 float v[4];
-                bool val[4];
-                bool any = false, all = true;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const bool gin = (unsigned)(x0 + i) < (unsigned)wl;
-                    const unsigned tl = tl0 + (unsigned)i;
-                    const bool it = tl < (unsigned)kTgtTile;
-                    val[i] = rowok && gin && it;
-                    any = any || val[i];
-                    all = all && (!gin || it);
-                    v[i] = fs * Tcol[(it ? tl : 0u) * (unsigned)kTStride];
-                }
+                for (int i = 0; i < 4; i++)
+                    v[i] = fs * Tcol[std::min(std::max(tl0 + i, 0), kTgtTile - 1) * kTStride];
                 const int off = woff + ((l * 8 + cy) * HW * 8 + cx0) * 4;
                 const u32x4_t pk = {__builtin_bit_cast(unsigned, v[0]),
                                     __builtin_bit_cast(unsigned, v[1]),
                                     __builtin_bit_cast(unsigned, v[2]),
                                     __builtin_bit_cast(unsigned, v[3])};
-                __builtin_amdgcn_raw_buffer_store_b128(pk, wrs, any && all ? off : kBufDiscard,
-                                                       0, 0);
-                const bool split = any && !all;
+                __builtin_amdgcn_raw_buffer_store_b128(pk, wrs, full ? off : kBufDiscard, 0, 0);
+                const bool split = has && !full;
                 if (__ballot(split)) {  // uniform, rare: a piece cut by the tile's ends
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        __builtin_amdgcn_raw_buffer_store_b32(
-                            __builtin_bit_cast(unsigned, v[i]), wrs,
-                            split && val[i] ? off + 4 * i : kBufDiscard, 0, 0);
+                    for (int i = 0; i < 4; i++) {
+                        const bool val = split && i >= ia && i <= ib &&
+                                         (unsigned)(tl0 + i) < (unsigned)kTgtTile;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[i]),
+                                                              wrs, val ? off + 4 * i : kBufDiscard,
+                                                              0, 0);
+                    }
                 }
             }
         }
