@@ -968,6 +968,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
                 // some in-grid cell in this tile; all of them
                 const bool has = rowok && ia <= ib && ta < kTgtTile && tb >= 0;
                 const bool full = has && ta >= 0 && tb < kTgtTile;
+                if (!__ballot(has)) continue;  // uniform: no piece of this round here
                 float v[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++)
