@@ -33,9 +33,10 @@
 //   e >= 0, which makes hi exact and lo zero at level 0.
 //   bf16 split (SLK_PREC_BF16X3): hi = rne_bf16(x), lo = rne_bf16(x - hi),
 //   no scale (16 significant bits, lo.lo ~2^-16).
-// Stage 2 (tile_mask_edge, workgroups of the same launch as stage 1): which
-// (edge, source tile, target tile) pairs hold any window cell; the others are
-// never computed.
+// Stage 2 (order_and_boxes, workgroups of the same launch as stage 1): each
+// edge's sources sorted by where their windows fall, runs of 128 of them
+// (source tiles) with the bounding box of their windows at every level; the
+// boxes' cells are a source tile's "virtual" targets, listed in tiles of 256.
 // Stage 3 (k_corr_split_win): a workgroup computes 128 sources x 256 targets as
 // hi.hi + hi.lo + lo.hi on v_mfma_f32_32x32x16_f16 (or _bf16) (exact
 // products, fp32 accumulation), staging 16-channel chunks through LDS in a
@@ -138,9 +139,10 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 //
 // Per edge: a counting sort over the keys (LDS histogram by atomic adds, an
 // exclusive scan, a scatter by atomic slot claims: the order within a bucket
-// is not fixed, the bucket ranges are), ord[0][q] = pixel at sorted position
-// q and ord[1][q], ord[2][q] = its x, y; the boxes of each source tile as
-// kBoxInts ints (ya, xa, bh, bw per level) after them; the (source tile,
+// is not fixed, the bucket ranges are), ord[q] = pixel at sorted position q
+// (claimed in LDS and written out in order when the keys leave room); the
+// boxes of each source tile as kBoxInts ints (ya, xa, bh, bw per level)
+// after them; the (source tile,
 // virtual tile) ids mt * ntiles + vt into the edge's segment list[e * tpe ..]
 // and their number into ctr[kCtrCount + e]. Edge 0 also zeroes the tile
 // counters of k_corr_split_win, which runs after this on the same stream.
@@ -178,15 +180,15 @@ struct MaskArgs {
     const float* coords;
     int* list;
     int* ctr;
-    int* order;   // [edge][ostride]: pixel, x, y of each sorted position, then the boxes
+    int* order;   // [edge][ostride]: pixel of each sorted position, then the boxes
     long ostride;
     int mtiles, ntiles, nedges;
     KeyGeom kg;
 };
 
-// ints of an edge's order record: 3 columns of HW, then kBoxInts per source tile
+// ints of an edge's order record: HW pixels, then kBoxInts per source tile
 __host__ __device__ __forceinline__ long order_stride(int HW, int mtiles) {
-    return 3L * HW + (long)kBoxInts * mtiles;
+    return (long)HW + (long)kBoxInts * mtiles;
 }
 
 __device__ __forceinline__ int sort_key(const KeyGeom& k, const Geom& g, int fx, int fy) {
@@ -266,6 +268,8 @@ __device__ int scan_excl(int* a, int n, int* wsum) {
     return total;
 }
 
+// keys: kPrepLdsWords ints of LDS (the bucket counts, then the sorted pixels
+// when they fit), ntv: mtiles ints of LDS
 template <int kT>
 __device__ void order_and_boxes(const MaskArgs& a, const Geom& g, int e, int* keys, int* ntv,
                                 int* wsum) {
@@ -274,8 +278,11 @@ __device__ void order_and_boxes(const MaskArgs& a, const Geom& g, int e, int* ke
     const KeyGeom kg = a.kg;
     const float* cc = a.coords + (size_t)e * 2 * HW;
     int* ord = a.order + (size_t)e * a.ostride;
-    float* oxy = reinterpret_cast<float*>(ord + HW);
-    int* rec = ord + 3 * HW;
+    int* rec = ord + HW;
+    // the sorted pixels are claimed in LDS and stored in order afterwards
+    // (scattered 4-byte stores from one workgroup are slow); a map too large
+    // for that scatters them to ord directly
+    int* spix = kg.nkeys + HW <= kPrepLdsWords ? keys + kg.nkeys : nullptr;
     for (int i = tid; i < kg.nkeys; i += kT) keys[i] = 0;
     if (e == 0 && tid < 8) a.ctr[kCtrXcd + tid] = 0;
     __syncthreads();
@@ -312,13 +319,16 @@ __device__ void order_and_boxes(const MaskArgs& a, const Geom& g, int e, int* ke
             const int p = p0 + u * kT + tid;
             if (p < HW) {
                 const int q = atomicAdd(&keys[kv[u]], 1);
-                ord[q] = p;
-                oxy[q] = xv[u];
-                oxy[HW + q] = yv[u];
+                if (spix)
+                    spix[q] = p;
+                else
+                    ord[q] = p;
             }
         }
     }
     __syncthreads();  // keys[b]: one past the last sorted position of bucket b
+    if (spix)
+        for (int i = tid; i < HW; i += kT) ord[i] = spix[i];
     // bucket of sorted position q: the first b whose end exceeds q
     auto bucket_of = [&](int q) {
         int lo = 0, hi = kg.nkeys - 1;
@@ -437,8 +447,8 @@ __global__ __launch_bounds__(256) void k_frame_max(const Tin* __restrict__ fm, l
 // split every value is first scaled by its frame's 2^e (from the partial
 // maxima of k_frame_max), and the first workgroup of a slot stores 2^-e
 // after the slot's planes. `pooled` = 0 writes level 0 only (source slots).
-// One-dimensional grid: first, when mk.list is set, one tile-mask workgroup
-// per edge (tile_mask_edge, with the level-0 and level-1 LDS arrays; they are
+// One-dimensional grid: first, when mk.list is set, one order workgroup per
+// edge (order_and_boxes, with the level-0 and level-1 LDS arrays; they are
 // the longer chains, so they are dispatched first), then the blocks x C/16 x
 // slots preparation workgroups (block fastest).
 // (waves per SIMD: two 1024-thread or three 512-thread workgroups a CU)
@@ -454,7 +464,7 @@ __global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
     __shared__ int wave_sum[kT / 64];
     __shared__ float fscale;  // the frame's 2^e
     if ((int)blockIdx.x < nmask) {  // uniform
-        // the tile-mask chains are the launch's long pole: their waves issue
+        // the order chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
         static_assert(sizeof(l0) >= kMaxKeys * sizeof(int) &&
@@ -645,23 +655,25 @@ template <bool B>
 using bool_c = std::integral_constant<bool, B>;
 
 // Grid: a fixed number of workgroups of 256 threads, two per CU, each taking
-// marked tiles (tile_mask_edge) one at a time from its XCD's counter: tile
+// listed tiles (order_and_boxes) one at a time from its XCD's counter: tile
 // index idx runs over the edges' segments concatenated, workgroup blockIdx % 8
 // runs on that XCD and serves the XCD's contiguous eighth of those indices,
 // so the edges an XCD works on stay in its L2, and no CU idles while tiles
 // remain. Waves form a 2x2 grid: wave (wm, wn) owns sources
 // wm*64..+63 and targets wn*128..+127 of a tile, eight 32x32 accumulator
 // blocks. Source tile mt holds sorted positions mt*128..+127 of the edge's
-// order (tile_mask_edge): the A rows are gathered through the order's pixel
-// column, the coordinates come from its sorted copies, and each source's
-// windows are stored at its own pixel. kF16: fp16 operands (the scaled fp16
+// order: the A rows and the coordinates are gathered through the order's
+// pixels, the B rows through the tile's target boxes (virtual tile vt holds
+// virtual rows vt*256..+255), and each source's windows are stored at its
+// own pixel. kF16: fp16 operands (the scaled fp16
 // split), else bf16. alo = 0: every source lo is zero (fp16 features, fp16
 // split), and so is every level-0 target lo: a tile of level-0 targets then
 // takes the one pass hi.hi, a tile with pooled targets hi.hi + hi.lo.
 template <bool kF16>
 __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const unsigned short* __restrict__ feat, long slot_elems, EdgeSlots es,
-    const int* __restrict__ order, long ostride, float* __restrict__ win, int slot0, Geom g,
+    const int* __restrict__ order, long ostride, const float* __restrict__ coords,
+    float* __restrict__ win, int slot0, Geom g,
     float alpha, int mtiles, int ntiles, int nedges, const int* __restrict__ list,
     int* __restrict__ ctr, int alo) {
     __shared__ SplitSmem sm;
@@ -725,7 +737,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // level l's box (bh x bw cells from row ya, column xa), row-major
     int bya[kMaxLevels], bxa[kMaxLevels], bwd[kMaxLevels], cum[kMaxLevels + 1];
     {
-        const int* rec = ord + 3 * HW + mt * kBoxInts;
+        const int* rec = ord + HW + mt * kBoxInts;
         cum[0] = 0;
 #pragma unroll
         for (int l = 0; l < kMaxLevels; l++) {
@@ -766,6 +778,11 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // whatever the order buffer holds)
     const int pa = std::min((unsigned)ord[std::min(p0 + hr, HW - 1)], (unsigned)(HW - 1));
     if (!(tid & 1)) sm.pix[hr] = pa;  // read after the chunk loop's barriers
+    // wave (half, comp) stages coordinate comp (x, y) of sources half * 64 ..
+    // + 63: gathered by their pixels (clamped like pa)
+    const float* cpt = coords + ((size_t)e * 2 + (wave >> 1)) * HW +
+                       std::min((unsigned)ord[std::min(p0 + (wave & 1) * 64 + lane, HW - 1)],
+                                (unsigned)(HW - 1));
     const unsigned short* ga = fa + (size_t)pa * kChunk + hh;
     const unsigned short* gb0 = fb + (size_t)trow(v0 + hr) * kChunk + hh;
     const unsigned short* gb1 = fb + (size_t)trow(v0 + 128 + hr) * kChunk + hh;
@@ -856,8 +873,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         // vmcnt is of the same kind, and those complete in issue order)
         {
             const int half = wave & 1, comp = wave >> 1;  // wave -> sources half*64.., x or y
-            const int pc = std::min(p0 + half * 64 + lane, HW - 1);
-            dma_x1(ord + (size_t)(1 + comp) * HW + pc, lds_addr(&sm.crd[comp][half * 64]));
+            dma_x1(cpt, lds_addr(&sm.crd[comp][half * 64]));
         }
         if (nk > 1) issue(1, 1);
         // While in its chunk loop a wave issues at raised priority, so that on
@@ -1078,7 +1094,7 @@ int prep_slots(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, 
                          ctx->split_feat.as<unsigned short>(), mode, stream);
 }
 
-// The tile-mask workgroups (with the preparation of nslots slots when
+// The order workgroups (with the preparation of nslots slots when
 // nslots > 0) and the window kernel over `feat`, for edges whose slots are es.
 // mode: the split of `feat`; alo: whether its level-0 lo planes can be
 // nonzero (not for fp16 features under the fp16 split).
@@ -1098,7 +1114,7 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     const long ostride = order_stride(g.HW, mtiles);
     MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
                 ctx->src_order.as<int>(), ostride, mtiles, ntiles, n, kg};
-    // feature preparation and the tile mask, one launch (after the frames'
+    // feature preparation and the source order, one launch (after the frames'
     // maxima under the fp16 split)
     SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
     {
@@ -1106,12 +1122,14 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
         const long se = (long)slot_elems(g);
         if (mode == kSplitF16)
             hipLaunchKernelGGL(k_corr_split_win<true>, dim3(ctx->ws_grid), dim3(256), 0, stream,
-                               feat, se, es, ctx->src_order.as<int>(), ostride, win, slot0, g,
+                               feat, se, es, ctx->src_order.as<int>(), ostride, coords, win,
+                               slot0, g,
                                ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
                                ctx->tile_ctr.as<int>(), alo ? 1 : 0);
         else
             hipLaunchKernelGGL(k_corr_split_win<false>, dim3(ctx->ws_grid), dim3(256), 0, stream,
-                               feat, se, es, ctx->src_order.as<int>(), ostride, win, slot0, g,
+                               feat, se, es, ctx->src_order.as<int>(), ostride, coords, win,
+                               slot0, g,
                                ctx->alpha, mtiles, ntiles, n, ctx->tile_list.as<int>(),
                                ctx->tile_ctr.as<int>(), 1);
     }
