@@ -566,8 +566,10 @@ __global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
         emit(yy * W + xx, v);
     }
     if (!pooled) return;
-    // pooled levels: level l from level l-1 in LDS, then its pixels out
-    auto level = [&](auto& dst, const auto& from, int l, int rows, int cols) {
+    // pooled levels: each level from the one before in LDS (level 1 while level
+    // 0 goes out: both only read level 0), then the three levels' pixels out
+    // together, one per thread
+    auto pool = [&](auto& dst, const auto& from, int rows, int cols) {
         for (int i = tid; i < kChunk * rows * cols; i += kT) {
             const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
             float sum = from[c][2 * r][2 * x] + from[c][2 * r][2 * x + 1];
@@ -575,20 +577,32 @@ __global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
             sum = sum + from[c][2 * r + 1][2 * x + 1];
             dst[c][r][x] = 0.25f * sum;
         }
-        __syncthreads();
-        for (int p = tid; p < rows * cols; p += kT) {
-            const int r = p / cols, x = p % cols;
-            const int yy = by * rows + r, xx = bx * cols + x;
-            if (yy >= g.h[l] || xx >= g.w[l]) continue;
-            float v[kChunk];
-#pragma unroll
-            for (int c = 0; c < kChunk; c++) v[c] = dst[c][r][x];
-            emit(g.off[l] + yy * g.w[l] + xx, v);
-        }
     };
-    if (g.levels > 1) level(l1, l0, 1, kPrepRows / 2, kPrepCols / 2);
-    if (g.levels > 2) level(l2, l1, 2, kPrepRows / 4, kPrepCols / 4);
-    if (g.levels > 3) level(l3, l2, 3, kPrepRows / 8, kPrepCols / 8);
+    if (g.levels > 1) pool(l1, l0, kPrepRows / 2, kPrepCols / 2);
+    __syncthreads();
+    if (g.levels > 2) pool(l2, l1, kPrepRows / 4, kPrepCols / 4);
+    __syncthreads();
+    if (g.levels > 3) pool(l3, l2, kPrepRows / 8, kPrepCols / 8);
+    __syncthreads();
+    auto out_level = [&](const auto& src, int l, int rows, int cols, int p) {
+        const int r = p / cols, x = p % cols;
+        const int yy = by * rows + r, xx = bx * cols + x;
+        if (yy >= g.h[l] || xx >= g.w[l]) return;
+        float v[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; c++) v[c] = src[c][r][x];
+        emit(g.off[l] + yy * g.w[l] + xx, v);
+    };
+    constexpr int n1 = (kPrepRows / 2) * (kPrepCols / 2), n2 = n1 / 4, n3 = n2 / 4;
+    for (int p = tid; p < n1 + n2 + n3; p += kT) {
+        if (p < n1) {
+            if (g.levels > 1) out_level(l1, 1, kPrepRows / 2, kPrepCols / 2, p);
+        } else if (p < n1 + n2) {
+            if (g.levels > 2) out_level(l2, 2, kPrepRows / 4, kPrepCols / 4, p - n1);
+        } else {
+            if (g.levels > 3) out_level(l3, 3, kPrepRows / 8, kPrepCols / 8, p - n1 - n2);
+        }
+    }
 }
 
 struct alignas(16) SplitSmem {
