@@ -1194,7 +1194,11 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
 
 }  // namespace
 
-bool corr_split_supported(const slk_ctx* ctx) { return ctx->C % kChunk == 0; }
+// the split path: whole 16-channel chunks, and an edge's source tiles within
+// the order pass's LDS (h*w <= 262144; larger maps take the fp32 MFMA kernels)
+bool corr_split_supported(const slk_ctx* ctx) {
+    return ctx->C % kChunk == 0 && (ctx->HW + kSrcTile - 1) / kSrcTile <= kPrepL1Words;
+}
 
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
                           size_t* order_per_edge, size_t* ctr_bytes, size_t* max_per_slot) {
