@@ -238,13 +238,12 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
 // the current chunk's MFMAs); the weight fragments of all taps of a chunk are
 // read from global memory (L2-resident) into registers ahead of the taps.
 template <int KS, int EPI>
-__global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
+__global__ __launch_bounds__(256, KS == 3 ? 2 : 1) void k_conv(ConvArgs a) {
     constexpr int P = KS / 2;
     constexpr int PH = kTH + KS - 1, PW = kTW + KS - 1;
     constexpr int UNITS = PH * PW * 2;  // 16-byte units of a chunk's patch
     constexpr int UPT = (UNITS + 255) / 256;
     constexpr int TAPS = KS * KS;
-    constexpr int AHEAD = KS <= 3 ? TAPS : 1;  // weight taps held in registers
     __shared__ __attribute__((aligned(16))) _Float16 patch[2][PH * PW * 16];
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
@@ -272,11 +271,17 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
             reg[u] = v;
         }
     };
+    // A patch pixel is 32 bytes (16 channels); its two 16-byte halves are
+    // swapped when bit 3 of the pixel index is set, so that the 16 lanes of
+    // one pass of a 128-bit operand read (16 consecutive pixels, one half
+    // each) touch 64 distinct banks: unswizzled, pixels p and p + 8 share
+    // their banks.
     auto store_chunk = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
-            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[u];
+            const int phys = unit ^ ((unit >> 4) & 1);  // (pixel, half ^ bit 3 of pixel)
+            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][phys * 8]) = reg[u];
         }
     };
 
@@ -288,30 +293,38 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
 
     const long tap_stride = (long)a.nchunk * a.co_tot * 16;
     const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
+    // The weight fragments of the 3x3 taps go through a ring of kRing taps
+    // in registers, loaded kRing taps ahead of their MFMAs across the chunk
+    // boundary (9 taps a chunk: a tap's ring slot is t % kRing at every
+    // chunk), which keeps the launch at two waves per SIMD; the 7x7 stem
+    // reads each tap's fragments just before its MFMAs.
+    constexpr int kRing = 3;
+    static_assert(KS != 3 || TAPS % kRing == 0, "ring slots fixed per tap");
+    f16x8 Ar[kRing][2];
+    auto wload = [&](int c, int t, int slot) {
+        const _Float16* wc = wbase + (long)c * a.co_tot * 16 + t * tap_stride;
+        Ar[slot][0] = *reinterpret_cast<const f16x8*>(wc);
+        Ar[slot][1] = *reinterpret_cast<const f16x8*>(wc + 32 * 16);
+    };
+    if constexpr (KS == 3) {
+#pragma unroll
+        for (int t = 0; t < kRing; t++) wload(0, t, t);
+    }
     load_chunk(0);
     store_chunk(0);
     __syncthreads();
     for (int c = 0; c < a.nchunk; c++) {
         const int buf = c & 1;
         const _Float16* wc = wbase + (long)c * a.co_tot * 16;
-        // the weight fragments of every tap of the chunk, issued before the taps
-        f16x8 A[AHEAD][2];
-        if constexpr (AHEAD == TAPS) {
-#pragma unroll
-            for (int t = 0; t < TAPS; t++) {
-                A[t][0] = *reinterpret_cast<const f16x8*>(wc + t * tap_stride);
-                A[t][1] = *reinterpret_cast<const f16x8*>(wc + t * tap_stride + 32 * 16);
-            }
-        }
         if (c + 1 < a.nchunk) load_chunk(c + 1);
         const _Float16* pb = &patch[buf][0];
 #pragma unroll
         for (int t = 0; t < TAPS; t++) {
             const int ky = t / KS, kx = t - (t / KS) * KS;
             f16x8 a0, a1;
-            if constexpr (AHEAD == TAPS) {
-                a0 = A[t][0];
-                a1 = A[t][1];
+            if constexpr (KS == 3) {
+                a0 = Ar[t % kRing][0];
+                a1 = Ar[t % kRing][1];
             } else {
                 a0 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride);
                 a1 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride + 32 * 16);
@@ -319,10 +332,18 @@ __global__ __launch_bounds__(256) void k_conv(ConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int prow = wn * 4 + r + ky;
-                const f16x8 b =
-                    *reinterpret_cast<const f16x8*>(pb + ((prow * PW + l32 + kx) * 16 + lhi * 8));
+                const int pix = prow * PW + l32 + kx;
+                const f16x8 b = *reinterpret_cast<const f16x8*>(
+                    pb + (pix * 16 + ((lhi ^ ((pix >> 3) & 1)) * 8)));
                 acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0][r], 0, 0, 0);
                 acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1][r], 0, 0, 0);
+            }
+            if constexpr (KS == 3) {  // tap t + kRing, of this chunk or the next
+                const int tn = t + kRing;
+                if (tn < TAPS)
+                    wload(c, tn, t % kRing);
+                else if (c + 1 < a.nchunk)
+                    wload(c + 1, tn - TAPS, t % kRing);
             }
         }
         if (c + 1 < a.nchunk) store_chunk(buf ^ 1);
