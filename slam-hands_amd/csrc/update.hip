@@ -31,6 +31,7 @@
 #include <string>
 #include <vector>
 
+#include "lds_dma.hpp"
 #include "slk_internal.hpp"
 
 namespace slk {
@@ -80,6 +81,7 @@ struct ConvArgs {
     const float* gterm;   // [image][384] rounded global terms (zg | rg | qg)
     float* out32;         // kEpiQ: the new state; kEpiHeads: agg_conv1, NCHW fp32
     long out32_nstride;
+    const _Float16* zero16;  // 16 zero bytes: the source of staged units outside the image
 };
 
 // The epilogue of one pixel's two 32-row accumulator blocks: acc0/acc1
@@ -363,6 +365,128 @@ __global__ __launch_bounds__(256, KS == 3 ? 2 : 1) void k_conv(ConvArgs a) {
     }
 }
 
+// The 3x3 convolutions: the tile of k_conv (kCoT output channels x kTH x kTW
+// pixels, four waves, wave (wm, wn) = 64 channels x image rows wn*4..+3), with
+// both operands staged in LDS by direct-to-LDS loads, so that the four waves
+// share one copy of the weights (k_conv reads them from L2 into every wave's
+// registers). Per input chunk c: the (kTH + 2) x (kTW + 2) patch (double
+// buffered), and the weights of taps 0-4 (WA) and 5-8 (WB) of the tile's
+// kCoT channels, one buffer each: WB(c) and the patch of chunk c + 1 are
+// loaded after the barrier that starts chunk c, WA(c + 1) after the barrier
+// between its taps 4 and 5, so each half has about half a chunk of MFMAs to
+// land. 60 KB of LDS: two workgroups a CU. Every staged 32-byte row (a pixel
+// of the patch, an output channel of the weights) has its two 16-byte halves
+// swapped when bit 3 of the row is set, so the 16 lanes of one pass of a
+// 128-bit operand read touch 64 distinct banks.
+constexpr int kPatchUnits = 768;  // 16-byte units of a patch buffer: (kTH + 2) x (kTW + 2) x 2 = 680, padded
+constexpr int kWaTaps = 5, kWbTaps = 4;
+static_assert(kPatchUnits >= (kTH + 2) * (kTW + 2) * 2 && kPatchUnits % 256 == 0, "patch units");
+static_assert(kCoT * 2 == 256, "one 256-unit round per weight tap");
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
+    constexpr int PW = kTW + 2;
+    __shared__ __attribute__((aligned(16))) _Float16 sp[2][kPatchUnits * 8];
+    __shared__ __attribute__((aligned(16))) _Float16 swa[kWaTaps * 256 * 8];
+    __shared__ __attribute__((aligned(16))) _Float16 swb[kWbTaps * 256 * 8];
+    const int HW = a.h * a.w;
+    const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
+    const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+    const int nch = a.nchunk;
+    const long tap_stride = (long)nch * a.co_tot * 16;
+    // weight unit tid of a tap: output channel co = tid / 2, physical half tid & 1
+    const int wco = tid >> 1;
+    const int whalf = (tid & 1) ^ ((wco >> 3) & 1);
+    const _Float16* wsrc = a.wt + ((long)cot * kCoT + wco) * 16 + whalf * 8;
+    auto issue_w = [&](int c, int t0, int ntaps, _Float16* dst) {
+        for (int t = 0; t < ntaps; t++)  // uniform
+            dma_x4(wsrc + (long)(t0 + t) * tap_stride + (long)c * a.co_tot * 16,
+                   lds_addr(dst + (t * 256 + wave * 64) * 8));
+    };
+    auto issue_patch = [&](int c, int buf) {
+        const bool first = c < a.s0.nchunk;
+        const CkSrc& s = first ? a.s0 : a.s1;
+        const int cc = first ? c : c - a.s0.nchunk;
+        const _Float16* base = s.p + (long)n * s.nstride + (long)cc * HW * 16;
+#pragma unroll
+        for (int r = 0; r < kPatchUnits / 256; r++) {
+            const int unit = r * 256 + tid;
+            const int pix = unit >> 1;
+            const int half = (unit & 1) ^ ((pix >> 3) & 1);
+            const int py = pix / PW, px = pix - (pix / PW) * PW;
+            const int y = ty0 - 1 + py, x = tx0 - 1 + px;
+            const bool ok = pix < (kTH + 2) * PW && y >= 0 && y < a.h && x >= 0 && x < a.w;
+            dma_x4(ok ? base + ((long)y * a.w + x) * 16 + half * 8 : a.zero16,
+                   lds_addr(&sp[buf][(r * 256 + wave * 64) * 8]));
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+    auto taps = [&](int t0, int nt, const _Float16* wb, const _Float16* pb) {
+#pragma unroll
+        for (int tt = 0; tt < nt; tt++) {  // the callers' counts are constants
+            const int t = t0 + tt, ky = t / 3, kx = t - (t / 3) * 3;
+            f16x8 av[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++) {
+                const int co = wm * 64 + mb * 32 + l32;
+                av[mb] = *reinterpret_cast<const f16x8*>(
+                    wb + ((tt * 256 + co * 2) * 8 + ((lhi ^ ((co >> 3) & 1)) * 8)));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int pix = (wn * 4 + r + ky) * PW + l32 + kx;
+                const f16x8 b = *reinterpret_cast<const f16x8*>(
+                    pb + (pix * 16 + ((lhi ^ ((pix >> 3) & 1)) * 8)));
+                acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[0], b, acc[0][r], 0, 0, 0);
+                acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[1], b, acc[1][r], 0, 0, 0);
+            }
+        }
+    };
+    // Issue order (every thread the same count of loads): P(0) WA(0) | WB(0)
+    // P(1) | WA(1) | WB(1) P(2) | WA(2) ...; a chunk starts once everything
+    // issued before it has landed (its patch and WA), its taps 5-8 once WB
+    // has (only the next patch, 3 loads, may still be in flight).
+    issue_patch(0, 0);
+    issue_w(0, 0, kWaTaps, swa);
+    for (int c = 0; c < nch; c++) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();  // P(c), WA(c) in; every wave done with chunk c - 1
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        issue_w(c, kWaTaps, kWbTaps, swb);
+        const bool more = c + 1 < nch;  // uniform
+        if (more) issue_patch(c + 1, (c + 1) & 1);
+        taps(0, kWaTaps, swa, &sp[c & 1][0]);
+        if (more)
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0 | (kPatchUnits / 256));
+        else
+            __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();  // WB(c) in; every wave done with WA(c)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (more) issue_w(c + 1, 0, kWaTaps, swa);
+        taps(kWaTaps, kWbTaps, swb, &sp[c & 1][0]);
+    }
+
+    const int x = tx0 + l32;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int y = ty0 + wn * 4 + r;
+        if (y >= a.h || x >= a.w) continue;
+        epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, y * a.w + x,
+                       HW);
+    }
+}
+
 // NCHW fp32 [image][C][hw] -> CK fp16 chunks [c0 ..) of out; channels past C
 // up to the chunk boundary are zero. With writeback, the rounded values also
 // replace the fp32 source (round_to_fp16 in place, nn.cuh:563-569).
@@ -554,6 +678,7 @@ struct UpdateState {
     DevBuf glo_w, glo_b, small_w[3], small_b[3];  // [0]: delta_2 | weight_2, [2]: eta_0
     // activations (CK fp16) and small vectors
     DevBuf corr16, mot16, cat, tmp, zr_buf, glo, gterm, agg16, agg_t;
+    DevBuf zero16;  // 256 zero bytes (staged units outside the image)
     // motion filter (batch 1): grid coords, lookup, motion, state copies, heads
     DevBuf mf_coords, mf_corr, mf_motion, mf_net, mf_inp, mf_delta, mf_weight, mf_agg;
     std::vector<float> mf_host;
@@ -679,6 +804,10 @@ int launch_conv(const UpdateState* s, const PackedConv& pc, ConvArgs a, int N,
         const int hw = s->h * s->w;
         hipLaunchKernelGGL((k_conv1x1<EPI>), dim3(pc.co_tot / kCoT, (hw + 255) / 256, N),
                            dim3(256), 0, stream, a);
+    } else if constexpr (KS == 3) {
+        a.zero16 = s->zero16.as<_Float16>();
+        hipLaunchKernelGGL((k_conv3<EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
+                           dim3(256), 0, stream, a);
     } else {
         hipLaunchKernelGGL((k_conv<KS, EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
                            dim3(256), 0, stream, a);
@@ -732,6 +861,9 @@ extern "C" int slk_update_create(slk_update** out, int max_batch, int h, int w) 
     if (st == SLK_OK) st = s.zr_buf.ensure(N * kZrCh * chunk);
     if (st == SLK_OK) st = s.glo.ensure(N * 128 * sizeof(float));
     if (st == SLK_OK) st = s.gterm.ensure(N * 384 * sizeof(float));
+    if (st == SLK_OK) st = s.zero16.ensure(256);
+    if (st == SLK_OK && hipMemset(s.zero16.ptr, 0, 256) != hipSuccess)
+        st = fail(SLK_E_HIP, "update_create: hipMemset failed");
     if (st != SLK_OK) {
         delete u;
         return st;
@@ -749,7 +881,7 @@ extern "C" int slk_update_destroy(slk_update* u) {
     }
     for (DevBuf* b : {&s.glo_w, &s.glo_b, &s.small_w[0], &s.small_w[1], &s.small_w[2],
                       &s.small_b[0], &s.small_b[1], &s.small_b[2], &s.corr16, &s.mot16, &s.cat,
-                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t, &s.mf_coords,
+                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t, &s.zero16, &s.mf_coords,
                       &s.mf_corr, &s.mf_motion, &s.mf_net, &s.mf_inp, &s.mf_delta, &s.mf_weight,
                       &s.mf_agg})
         b->release();
