@@ -526,6 +526,8 @@ struct SolveArgs {
     float* poses;
     float* poses_prev;  // [P][7] poses t0..t1-1 before the step (fused path), or null
     float* poses_next;  // [P][7] poses t0..t1-1 after the step (overlapped fused path), or null
+    int* publish;       // or null: set (agent-scope release) once the status and dx are out,
+                        // before the retraction (the overlapped step's ready flag)
 };
 
 // One edge-block or Schur-item contribution to entry (r, c) of a 6x6 block of
@@ -606,9 +608,28 @@ __device__ __forceinline__ double bcast(double v, int src) {
     return __hiloint2double(hi, lo);
 }
 
+// A pose after its step, as the solve stores it: the fp32 values of the fp64
+// retraction (pose_retr_kernel, ba.cuh:757-760) of pose p7 by the fp32 step
+// d6. The linearization workgroups of an overlapped step form the poses they
+// need with this too, from the same inputs, instead of waiting for the
+// solve's retraction.
+__device__ __forceinline__ void step_pose(const float* p7, const float (&d6)[6], float (&out)[7]) {
+    double t[3], q[4], xi[6], t1[3], q1[4];
+    load_pose(p7, 0, t, q);
+#pragma unroll
+    for (int m = 0; m < 6; m++) xi[m] = (double)d6[m];
+    retr_se3(xi, t, q, t1, q1);
+#pragma unroll
+    for (int m = 0; m < 3; m++) out[m] = (float)t1[m];
+#pragma unroll
+    for (int m = 0; m < 4; m++) out[3 + m] = (float)q1[m];
+}
+
 // Outputs of a solve: the status flags, dx (fp64 and the fp32 step), and the
 // retraction of poses t0..t1-1, whose current values are read from
 // pose_src[(k - t0) * 7 ..] (A.poses + 7 * t0, or a copy taken earlier).
+// With A.publish, the flag is set once the status and dx are out, before the
+// retraction (every thread of the workgroup calls this).
 __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok,
                                              const float* pose_src) {
     const int n = A.n;
@@ -624,6 +645,14 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
         A.dx_dbg[t] = ok ? x[t] : 0.0;
         A.dx[t] = ok ? (float)x[t] : 0.0f;
     }
+    if (A.publish) {
+        // every wave's writes (status, dx) made visible device-wide before
+        // the flag
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(A.publish, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (!ok) {  // the poses stay; the overlapped path still needs their copy
         if (A.poses_next)
             for (int t = threadIdx.x; t < (A.t1 - A.t0) * 7; t += blockDim.x)
@@ -632,15 +661,11 @@ __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x
     }
     // pose_retr_kernel on the fp32 step (ba.cuh:757-760), fp64 inside
     for (int k = A.t0 + threadIdx.x; k < A.t1; k += blockDim.x) {
-        double t[3], q[4], xi[6], t1[3], q1[4];
         if (A.poses_prev)  // the fused path's back-substitution relinearizes at these
             for (int m = 0; m < 7; m++) A.poses_prev[(k - A.t0) * 7 + m] = pose_src[(k - A.t0) * 7 + m];
-        load_pose(pose_src, k - A.t0, t, q);
-        for (int m = 0; m < 6; m++) xi[m] = (double)(float)x[(k - A.t0) * 6 + m];
-        retr_se3(xi, t, q, t1, q1);
-        float pn[7];
-        for (int m = 0; m < 3; m++) pn[m] = (float)t1[m];
-        for (int m = 0; m < 4; m++) pn[3 + m] = (float)q1[m];
+        float d6[6], pn[7];
+        for (int m = 0; m < 6; m++) d6[m] = (float)x[(k - A.t0) * 6 + m];
+        step_pose(pose_src + (k - A.t0) * 7, d6, pn);
         for (int m = 0; m < 7; m++) A.poses[k * 7 + m] = pn[m];
         if (A.poses_next)  // read by the next overlapped step's relinearization
             for (int m = 0; m < 7; m++) A.poses_next[(k - A.t0) * 7 + m] = pn[m];
@@ -1497,28 +1522,21 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Pose k of `poses`, read with device-coherent loads: values another
-// workgroup of the same launch wrote, which this workgroup's caches may hold
-// stale copies of (the lines were read before those writes).
-__device__ __forceinline__ void load_pose_coherent(const float* poses, int k, double* t,
-                                                   double* q) {
-    for (int m = 0; m < 3; m++) t[m] = (double)ld_coherent(poses + k * 7 + m);
-    for (int m = 0; m < 4; m++) q[m] = (double)ld_coherent(poses + k * 7 + 3 + m);
-}
-
-// Relative pose of edge (ix, jx) at the current poses (coherent: read them
-// with device-coherent loads), or (prev) at the poses of the last step's
+// Relative pose of edge (ix, jx) at the current poses, at the poses after
+// this launch's step (poses t0..t1-1 from pn, which the workgroup formed; the
+// others do not move), or (prev) at the poses of the last step's
 // linearization: only t0..t1-1 moved.
 __device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int jx, double* tij,
-                                       double* qij, bool coherent = false) {
+                                       double* qij, const float* pn = nullptr) {
     if (ix == jx) {
         edge_rel(F.poses, ix, jx, tij, qij);  // stereo constants
         return;
     }
     double ti[3], qi[4], tj[3], qj[4];
-    if (coherent) {
-        load_pose_coherent(F.poses, ix, ti, qi);
-        load_pose_coherent(F.poses, jx, tj, qj);
+    if (pn) {
+        const bool si = ix >= F.t0 && ix < F.t1, sj = jx >= F.t0 && jx < F.t1;
+        load_pose(si ? pn : F.poses, si ? ix - F.t0 : ix, ti, qi);
+        load_pose(sj ? pn : F.poses, sj ? jx - F.t0 : jx, tj, qj);
     } else {
         const bool pi = prev && ix >= F.t0 && ix < F.t1, pj = prev && jx >= F.t0 && jx < F.t1;
         load_pose(pi ? F.poses_prev : F.poses, pi ? ix - F.t0 : ix, ti, qi);
@@ -1574,6 +1592,7 @@ struct FzLds {
     double qs[kFzPx];
     double dxr[6 * kFzMaxSlots];  // the last step's dx, by slot row
     int spose[kFzMaxSlots];       // the pose of each slot
+    float pnew[kPanelPoses * 7];  // poses t0..t1-1 after the overlapped launch's step
     int wait_state;
 };
 
@@ -1598,7 +1617,7 @@ template <bool kPrev>
 __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L, int chunk,
                                         const int (&kpx)[kFzPPL], const bool (&vpx)[kFzPPL],
                                         const double (&dsp)[kFzPPL], double eta_px,
-                                        FzCache& cache, bool coherent = false) {
+                                        FzCache& cache, const float* pn = nullptr) {
     const int nslot = K.info & 0xff, ri = (K.info >> 8) & 1, T = K.info >> 12;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
@@ -1630,7 +1649,7 @@ __device__ __forceinline__ void fz_pass(const FzArgs& F, const FzKf& K, FzLds& L
 #pragma unroll
             for (int m = 0; m < 4; m++) qij[m] = cache.qn[m];
         } else {
-            fz_rel(F, kPrev, E.ix, E.jx, tij, qij, coherent);
+            fz_rel(F, kPrev, E.ix, E.jx, tij, qij, pn);
         }
         float tgu[kFzPPL], tgv[kFzPPL], wtu[kFzPPL], wtv[kFzPPL];
         if (!kPrev && first && cache.valid) {
@@ -1930,6 +1949,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
     const int kown = chunk * kFzPx + tid;  // the pixel of the per-pixel steps
     const bool mine = tid < kFzPx && kown < HW;
     const double eta_px = mine ? (double)F.eta[(size_t)K.kf * HW + kown] : 0.0;
+    const float* pn = nullptr;  // L.pnew once it holds the poses after this launch's step
     if (kBs && !wait.ready && F.flags[0] == 0) {  // uniform
         // (fz_bs_direct's computation, written out here: called as a
         // function, it changed this kernel's register allocation and cost
@@ -2070,7 +2090,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
                 }
                 return;
             }
-            // What the solve wrote (the status, dx, the poses) is read from
+            // What the solve wrote (the status, dx) is read from
             // here on with device-coherent loads (agent scope, relaxed),
             // issued after the flag was seen and a workgroup barrier: the
             // solve's release fence wrote them back before its flag store,
@@ -2080,42 +2100,38 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             // as well, and the next step's input loads measured ~4.5 us
             // slower after it.)
         }
-        // one round of loads, all issued before any is used: the status, dx
-        // by slot row (slot poses are free poses), and the poses of the
-        // wave's first edge (pose 0 stands in when there is none)
+        // the status and dx by slot row (slot poses are free poses)
         const int r6 = nslot > 0 ? min(tid, 6 * nslot - 1) : 0;
         const int dxi = nslot > 0 ? (L.spose[r6 / 6] - F.t0) * 6 + r6 % 6 : 0;
-        const int pix = cache.valid ? cache.ix : 0, pjx = cache.valid ? cache.jx : 0;
         const int okv = __hip_atomic_load(F.flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const float dxf = ld_coherent(F.dx + dxi);
-        float pi[7], pj[7];
-#pragma unroll
-        for (int m = 0; m < 7; m++) {
-            pi[m] = ld_coherent(F.poses + pix * 7 + m);
-            pj[m] = ld_coherent(F.poses + pjx * 7 + m);
-        }
         const bool ok = okv == 0;
-        if (kLin && cache.valid) {  // fz_rel at the current poses, from the loaded values
-            if (pix == pjx) {
-                edge_rel(F.poses, pix, pjx, cache.tn, cache.qn);  // stereo constants
-            } else {
-                double ti[3], qi[4], tj[3], qj[4];
+        if (kLin) {
+            // the free poses after the step, one thread each, formed as the
+            // solve forms them (step_pose, from the poses this step started
+            // at and its dx) rather than read after its retraction; a
+            // rejected or halted step leaves them as they were
+            for (int k = tid; k < F.t1 - F.t0; k += kLinWG) {
+                const float* p7 = F.poses_prev + k * 7;
+                float d6[6], out[7];
 #pragma unroll
-                for (int m = 0; m < 3; m++) {
-                    ti[m] = (double)pi[m];
-                    tj[m] = (double)pj[m];
-                }
+                for (int m = 0; m < 6; m++) d6[m] = ok ? ld_coherent(F.dx + k * 6 + m) : 0.0f;
+                if (ok)
+                    step_pose(p7, d6, out);
+                else
 #pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    qi[m] = (double)pi[3 + m];
-                    qj[m] = (double)pj[3 + m];
-                }
-                rel_se3(ti, qi, tj, qj, cache.tn, cache.qn);
+                    for (int m = 0; m < 7; m++) out[m] = p7[m];
+#pragma unroll
+                for (int m = 0; m < 7; m++) L.pnew[k * 7 + m] = out[m];
             }
-            cache.rel = true;
+            pn = L.pnew;
         }
         if (tid < 6 * nslot) L.dxr[tid] = (double)dxf;
         __syncthreads();
+        if (kLin && cache.valid) {  // the wave's first edge at the poses after the step
+            fz_rel(F, false, cache.ix, cache.jx, cache.tn, cache.qn, pn);
+            cache.rel = true;
+        }
         if (ok) {  // uniform
             double own = dsp[0];  // the depth of pixel kown (lane's pixel of s = wave)
 #pragma unroll
@@ -2138,7 +2154,7 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
         }
     }
     if (!kLin) return;
-    fz_pass<false>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache, wait.ready != nullptr);
+    fz_pass<false>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache, pn);
     if (T == 1)
         fz_schur_tiles<1>(L.xs, L.qs, wave, lane);
     else if (T == 2)
@@ -2228,16 +2244,12 @@ __global__ __launch_bounds__(kLinWG, kFzWgPerCu) void k_ba_fz_step(FzArgs F, Sol
         // the solve is the launch's spine; a linearization workgroup may share
         // its CU, so its waves issue first
         __builtin_amdgcn_s_setprio(3);
+        // the solve sets wait.ready (A.publish) once the status and dx are
+        // out, before it retracts the poses
         if (kPanel)
             solve_panel_body(A, lds.pv.sm, lds.pv.ok, lds.pv.pose0);
         else
             solve_small_body(A, lds.sv);
-        // every wave's writes (dx, flags, poses) made visible device-wide
-        // before the flag
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (threadIdx.x == 0)
-            __hip_atomic_store(wait.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     const int b = blockIdx.x - 1;
@@ -2789,6 +2801,7 @@ SolveArgs solve_args(BaState* s, const PlanDev& plan, const IterArgs& I) {
     A.dx = s->dx.as<float>();
     A.flags = s->flags.as<int>();
     A.halt = nullptr;
+    A.publish = nullptr;
     A.poses = I.poses;
     A.poses_prev = s->fz ? s->poses_prev.as<float>() : nullptr;
     A.poses_next = nullptr;
@@ -2928,6 +2941,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
             Ak.poses_prev = nullptr;
             Ak.poses_next = pp[(it + 1) & 1];
             Ak.halt = s->flags.as<int>() + 5;
+            Ak.publish = s->ready.as<int>();  // set by the solve before its retraction
             const bool panel = s->n > kSmallN;
             if (it + 1 < iters) {
                 ProfScope ps(ctx, "ba_fz_step", stream);
