@@ -44,13 +44,13 @@ typedef enum {
 typedef enum { SLK_F32 = 0, SLK_F16 = 1 } slk_dtype;
 
 /* Contraction used for the features:
- *  SLK_PREC_F16X3 (default)  -- batched path: every frame's features scaled
- *                               by one power of two (the frame's largest
- *                               magnitude into [2^14, 2^15)) and split into
- *                               fp16 hi + lo (22 significant bits), three fp16
- *                               MFMA passes hi.hi + hi.lo + lo.hi with fp32
- *                               accumulation, ~1e-6 relative to the frame
- *                               scale. fp16 features
+ *  SLK_PREC_F16X3 (default)  -- batched path: every pixel's features scaled
+ *                               by one power of two (its largest magnitude
+ *                               over the channels into [2^14, 2^15)) and split
+ *                               into fp16 hi + lo (22 significant bits), three
+ *                               fp16 MFMA passes hi.hi + hi.lo + lo.hi with
+ *                               fp32 accumulation, ~1e-6 relative to the two
+ *                               pixels' scales. fp16 features
  *                               are their own hi (lo = 0): a level-0 target
  *                               tile takes the one pass hi.hi, the exact fp16
  *                               products of the reference's cublasGemmEx on

@@ -1057,10 +1057,10 @@ extern "C" int slk_corr_batch_build_and_sample_dev_noalloc(
         c.lh[l] = h >> l;
         c.lw[l] = w >> l;
     }
-    size_t slot = 0, tiles = 0, order = 0, ctr = 0, maxp = 0;
-    corr_split_footprint(&c, &slot, &tiles, &order, &ctr, &maxp);
+    size_t slot = 0, tiles = 0, order = 0, ctr = 0;
+    corr_split_footprint(&c, &slot, &tiles, &order, &ctr);
     const size_t win = (size_t)c.HW * kMaxLevels * kWinCells * sizeof(float);
-    const size_t per_edge = 2 * align256(slot) + 2 * maxp + align256(tiles) + align256(order) +
+    const size_t per_edge = 2 * align256(slot) + align256(tiles) + align256(order) +
                             align256(win);
     const size_t fixed = align256(ctr);
     const size_t fit = per_edge + fixed <= kNoAllocBytes ? (kNoAllocBytes - fixed) / per_edge : 0;
@@ -1081,7 +1081,6 @@ extern "C" int slk_corr_batch_build_and_sample_dev_noalloc(
         at += align256(bytes);
     };
     carve(c.split_feat, 2 * (size_t)n * align256(slot));
-    carve(c.frame_max, 2 * (size_t)n * maxp);
     carve(c.tile_list, (size_t)n * tiles);
     carve(c.src_order, (size_t)n * order);
     carve(c.tile_ctr, ctr);

@@ -18,19 +18,18 @@
 // cells agree to fp32 rounding, ~1e-7 relative); with integer-coded features
 // every intermediate is exact and the windows are bitwise equal.
 //
-// Stage 0 (k_frame_max, fp16 split only): partial maxima of |x| over each
-// frame's level-0 features (a pooled value is an average, never larger).
 // Stage 1 (k_feat_prep), once per frame a launch uses: the fp32 pooled
 // features of levels 1..3 (formed in LDS from level 0) and a hi/lo split of
 // every pixel of all levels, stored chunk-major [plane][C/16][rows][16] so a
 // 16-channel chunk of consecutive rows is one contiguous block, followed by
-// one float per frame: the inverse of the frame's split scale.
-//   fp16 split (SLK_PREC_F16X3, the default): a frame's features are scaled
-//   by one power of two 2^e chosen from the frame's largest magnitude m
-//   (m * 2^e in [2^14, 2^15)), then hi = rne_f16(x 2^e),
+// one float per row: the inverse of the row's split scale.
+//   fp16 split (SLK_PREC_F16X3, the default): a pixel's features are scaled
+//   by one power of two 2^e chosen from their largest magnitude m over the
+//   channels (m * 2^e in [2^14, 2^15)), then hi = rne_f16(x 2^e),
 //   lo = rne_f16(x 2^e - hi): 22 significant bits relative to m, the
-//   dropped lo.lo term ~2^-22 m^2 per product. fp16 features are taken with
-//   e >= 0, which makes hi exact and lo zero at level 0.
+//   dropped lo.lo term ~2^-22 m_i m_j per product of pixels i and j. fp16
+//   features are taken with e >= 0, which makes hi exact and lo zero at
+//   level 0.
 //   bf16 split (SLK_PREC_BF16X3): hi = rne_bf16(x), lo = rne_bf16(x - hi),
 //   no scale (16 significant bits, lo.lo ~2^-16).
 // Stage 2 (order_and_boxes, workgroups of the same launch as stage 1): each
@@ -48,7 +47,7 @@
 // is then transposed through LDS ([target][source]) and the window cells that
 // fall inside the tile are read back with one lane per (source, window
 // column), walking the 8 window rows: each masked store covers one row of 8
-// sources' windows, multiplied by alpha times both frames' inverse scales
+// sources' windows, multiplied by alpha times both pixels' inverse scales
 // (powers of two: the scaling adds no rounding). Only ~2% of the level-0 products are
 // window cells, and none of them costs more than its LDS round trip.
 #include <algorithm>
@@ -103,15 +102,6 @@ __device__ __forceinline__ int slot_frame(const SlotFrames& m, int s) {
 
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const _Float16* p) { return (float)(*p); }
-// four consecutive elements (16 or 8 bytes, aligned to that size)
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 ldf4(const float* p) {
-    return *reinterpret_cast<const float4*>(p);
-}
-__device__ __forceinline__ float4 ldf4(const _Float16* p) {
-    const half4_t h = *reinterpret_cast<const half4_t*>(p);
-    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
-}
 
 // Source order and target boxes of an edge (one workgroup per edge, in the
 // launch of k_feat_prep beside the feature preparation it does not depend on).
@@ -147,12 +137,10 @@ __device__ __forceinline__ float4 ldf4(const _Float16* p) {
 // virtual tile) ids mt * ntiles + vt into the edge's segment list[e * tpe ..]
 // and their number into ctr[kCtrCount + e]. Edge 0 also zeroes the tile
 // counters of k_corr_split_win, which runs after this on the same stream.
-// the preparation's level-0 block (16 channels of 8 x 64 pixels) in LDS,
-// which an order workgroup uses for its bucket counts
-constexpr int kPrepRows = 8, kPrepCols = 64;
-constexpr int kPrepLdsWords = kChunk * kPrepRows * kPrepCols;
-// ... and its level-1 block, for the virtual tile counts of the source tiles
-constexpr int kPrepL1Words = kChunk * (kPrepRows / 2) * (kPrepCols / 2);
+// LDS of an order workgroup (arrays of the preparation's, reused): the
+// bucket counts of the sort, and the virtual tile counts of the source tiles
+constexpr int kPrepLdsWords = 8192;
+constexpr int kPrepL1Words = 2048;
 constexpr int kBand = 16;                 // image rows per band of the source order
 constexpr int kMaxKeys = kPrepLdsWords;   // buckets of the sort
 constexpr int kBoxInts = 4 * kMaxLevels;  // per source tile: ya, xa, bh, bw of each level
@@ -375,7 +363,7 @@ __device__ __forceinline__ unsigned split_f16(float x) {
            ((unsigned)__builtin_bit_cast(unsigned short, l) << 16);
 }
 
-// The exponent e of a frame's fp16 split scale 2^e from its largest magnitude
+// The exponent e of a pixel's fp16 split scale 2^e from its largest magnitude
 // m: m * 2^e in [2^14, 2^15), so every scaled feature and its hi stay below
 // 2^15 (fp16 holds up to 65504), bounded to [-120, 120] (2^+-e stays a normal
 // float; a bound only lowers m * 2^e); 0 for m = 0 or non-finite. `exact`: at
@@ -390,220 +378,214 @@ __device__ __forceinline__ int split_exponent(float m, bool exact) {
     return e;
 }
 
-// Partial maxima of |x| over the frames of slots slot_lo.., for the fp16
-// split's per-frame scale: workgroup (q, s) reduces chunks q, q + nparts, ..
-// of kMaxChunk elements of slot s's C x HW features into part[s][q] (no
-// atomics: the preparation reduces the parts of its slot). Each thread's four
-// 16-byte loads of a chunk are in flight together. The pooled levels' values
-// are means of level-0 values, so the frame's level-0 maximum bounds every
-// level.
-constexpr int kMaxParts = 256;              // partial maxima per slot, at most
-constexpr int kMaxChunk = 256 * 4 * 4;      // elements a workgroup reduces per round
-template <typename Tin>
-__global__ __launch_bounds__(256) void k_frame_max(const Tin* __restrict__ fm, long fstride,
-                                                   SlotFrames sf, int slot_lo, long n, int vec,
-                                                   int nparts, float* __restrict__ part) {
-    __shared__ float wm[4];
-    const int s = slot_lo + blockIdx.y, q = blockIdx.x, tid = threadIdx.x;
-    const Tin* src = fm + (long)slot_frame(sf, s) * fstride;
-    float m = 0.0f;
-    for (long c0 = (long)q * kMaxChunk; c0 < n; c0 += (long)nparts * kMaxChunk) {
-        if (vec) {  // uniform: n % 4 == 0, the frames 4-element aligned
-            float4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const long i = c0 + 4 * (tid + 256 * u);
-                v[u] = i < n ? ldf4(src + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                m = fmaxf(fmaxf(m, fabsf(v[u].x)), fabsf(v[u].y));
-                m = fmaxf(fmaxf(m, fabsf(v[u].z)), fabsf(v[u].w));
-            }
-        } else {
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const long i = c0 + tid + 256 * u;
-                v[u] = i < n ? ldf(src + i) : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 16; u++) m = fmaxf(m, fabsf(v[u]));
-        }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if ((tid & 63) == 0) wm[tid >> 6] = m;
-    __syncthreads();
-    if (tid == 0) part[(size_t)s * kMaxParts + q] = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+// Feature preparation of frame slots, one launch of 1024-thread workgroups.
+// A workgroup takes an 8 x 32 block of level-0 pixels, each thread one pixel
+// and one of four groups of 32 channels (waves 4q..4q+3: group q, two block
+// rows a wave, so each load instruction reads two 128-byte row pieces) in
+// registers. A pixel's split scale comes from the largest magnitude among
+// its channels (the four groups' maxima through LDS); the thread writes the
+// hi/lo split of its two chunks, 16 channels = 32 bytes per pixel and
+// plane, into out[slot][plane][C/16][Ttot][16], and group 0 the pixel's
+// inverse scale into the slot's float array [Ttot] after the planes. The
+// pooled levels of the block (4 x 16, 2 x 8, 1 x 4 pixels; each pooled value
+// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first; a
+// pooled pixel's parents always lie in the block) are formed in LDS one
+// chunk of every group at a time, level 2 from level 0 through the same
+// level-1 sums, and collected by one owner thread per pooled pixel and
+// group, which then splits them the same way. Under the fp16 split a pixel's
+// features are scaled by 2^e (split_exponent of its largest magnitude),
+// under the bf16 split by 1. `pooled` = 0 writes level 0 only (source slots).
+// One-dimensional grid: first, when mk.list is set, one order workgroup per
+// edge (order_and_boxes, on the exchange arrays; they are the longer chains,
+// so they are dispatched first), then the blocks x slots preparation
+// workgroups, renumbered so that each XCD (workgroups are dealt to the 8 XCDs
+// in turn) takes a contiguous run of blocks.
+constexpr int kPrepC = 128;          // channels of the split path, at most
+constexpr int kPW = 32, kPH = 8;     // block columns and rows
+constexpr int kPGrp = 4;             // channel groups
+constexpr int kPGc = kPrepC / kPGrp; // channels of a group (two chunks)
+constexpr int kPN1 = (kPH / 2) * (kPW / 2), kPN2 = (kPH / 4) * (kPW / 4), kPN3 = kPW / 8;
+static_assert(kPGrp * kPH * kPW == 1024 && kPGc == 2 * kChunk, "prep workgroup shape");
+
+__device__ __forceinline__ float pool4(float a, float b, float c, float d) {
+    return 0.25f * (((a + b) + c) + d);
 }
 
-// Feature preparation of one frame slot, one launch: a workgroup takes a
-// 16-channel chunk of an 8 x 64 block of level-0 pixels into LDS, forms its
-// 4 x 32, 2 x 16 and 1 x 8 pooled blocks in turn (each pooled value
-// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first;
-// a pooled pixel's parents always lie in the block), and writes the hi/lo
-// split of every pixel of the levels present, 16 channels = 32 bytes per
-// pixel and plane, into out[slot][plane][C/16][Ttot][16]; under the fp16
-// split every value is first scaled by its frame's 2^e (from the partial
-// maxima of k_frame_max), and the first workgroup of a slot stores 2^-e
-// after the slot's planes. `pooled` = 0 writes level 0 only (source slots).
-// One-dimensional grid: first, when mk.list is set, one order workgroup per
-// edge (order_and_boxes, with the level-0 and level-1 LDS arrays; they are
-// the longer chains, so they are dispatched first), then the blocks x C/16 x
-// slots preparation workgroups (block fastest).
-// (waves per SIMD: two 1024-thread or three 512-thread workgroups a CU)
-template <typename Tin, int kT>
-__global__ __launch_bounds__(kT, kT >= 1024 ? 8 : 6) void k_feat_prep(
+// the hi/lo split of one pixel's chunk k (16 channels) at row t
+__device__ __forceinline__ void emit_chunk(unsigned short* slot, size_t plane, int Ttot, int k,
+                                           int t, const float* v, float sc, int mode) {
+    u16x8_t hi[2], lo[2];
+#pragma unroll
+    for (int u = 0; u < kChunk; u++) {
+        const unsigned pk = mode == kSplitF16 ? split_f16(v[u] * sc) : split_bf16(v[u]);
+        hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
+        lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
+    }
+    unsigned short* o = slot + ((size_t)k * Ttot + t) * kChunk;
+    *reinterpret_cast<u16x8_t*>(o) = hi[0];
+    *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
+    *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
+    *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
+}
+
+template <typename Tin>
+__global__ __launch_bounds__(1024) void k_feat_prep(
     const Tin* __restrict__ fm, long fstride, SlotFrames sf, int slot_lo,
-    unsigned short* __restrict__ out, long slot_elems, Geom g, int pooled, int vec, int nbx,
-    int nblk, int nmask, MaskArgs mk, int mode, const float* __restrict__ part, int nparts) {
-    __shared__ float l0[kChunk][kPrepRows][kPrepCols];
-    __shared__ float l1[kChunk][kPrepRows / 2][kPrepCols / 2];
-    __shared__ float l2[kChunk][kPrepRows / 4][kPrepCols / 4];
-    __shared__ float l3[kChunk][kPrepRows / 8][kPrepCols / 8];
-    __shared__ int wave_sum[kT / 64];
-    __shared__ float fscale;  // the frame's 2^e
+    unsigned short* __restrict__ out, long slot_elems, Geom g, int pooled, int nbx, int nblk,
+    int nmask, MaskArgs mk, int mode) {
+    constexpr int kPNp = kPN1 + kPN2 + kPN3;
+    // a chunk of every group: level 0, and the pooled values (level 1 at
+    // [0, kPN1), 2 at [kPN1, kPN1 + kPN2), 3 after them, each row-major)
+    __shared__ __attribute__((aligned(16))) float xch[kPGrp][kChunk][kPH][kPW];
+    __shared__ float pl[kPGrp][kChunk][kPNp];
+    __shared__ float pmax[kPGrp][kPH * kPW];  // per group: max |x| of a pixel
+    __shared__ float pmaxp[kPGrp][kPNp];      // ... of a pooled pixel
+    __shared__ int wave_sum[16];
     if ((int)blockIdx.x < nmask) {  // uniform
         // the order chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        static_assert(sizeof(l0) >= kMaxKeys * sizeof(int) &&
-                          sizeof(l1) >= kPrepL1Words * sizeof(int), "order LDS");
-        order_and_boxes<kT>(mk, g, blockIdx.x, reinterpret_cast<int*>(&l0[0][0][0]),
-                            reinterpret_cast<int*>(&l1[0][0][0]), wave_sum);
+        static_assert(sizeof(xch) >= kMaxKeys * sizeof(int) &&
+                          sizeof(pl) >= kPrepL1Words * sizeof(int), "order LDS");
+        order_and_boxes<1024>(mk, g, blockIdx.x, reinterpret_cast<int*>(&xch[0][0][0][0]),
+                              reinterpret_cast<int*>(&pl[0][0][0]), wave_sum);
         return;
     }
-    const int tid = threadIdx.x;
-    const int b = blockIdx.x - nmask;
-    const int blk = b % nblk, rest = b / nblk;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q = wave >> 2, gi = tid & 255;  // channel group, thread in the group
+    const int r = 2 * (wave & 3) + (lane >> 5), x = lane & 31;  // gi = r * kPW + x
+    const int nprep = (int)gridDim.x - nmask;
+    int b = blockIdx.x - nmask;
+    {
+        const int qq = nprep / 8;  // XCD b % 8 takes blocks (b % 8) qq .. + qq - 1
+        if (b < 8 * qq) b = (b & 7) * qq + (b >> 3);
+    }
+    const int blk = b % nblk, s = slot_lo + b / nblk;
     const int bx = blk % nbx, by = blk / nbx;
-    const int k = rest % (g.C / kChunk), s = slot_lo + rest / (g.C / kChunk);
-    const int W = g.w[0], H = g.h[0];
-    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (long)(k * kChunk) * g.HW;
-    if (tid < 64) {  // the frame's scale, from the partial maxima of its slot
-        float m = 0.0f;
-        if (mode == kSplitF16)
-            for (int q = tid; q < nparts; q += 64) m = fmaxf(m, part[(size_t)s * kMaxParts + q]);
+    const int W = g.w[0], H = g.h[0], C = g.C, nk = C / kChunk;
+    const int yy = by * kPH + r, xx = bx * kPW + x;
+    const bool inmap = yy < H && xx < W;
+    const Tin* src = fm + (long)slot_frame(sf, s) * fstride + (inmap ? (long)yy * W + xx : 0L);
+    // the pixel's channels of group q (zero past C and outside the map): every
+    // load unconditional (from a clamped, in-range address) and issued before
+    // the first is used
+    float v[kPGc];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        if (tid == 0)
-            fscale = mode == kSplitF16
-                         ? __builtin_amdgcn_ldexpf(
-                               1.0f, split_exponent(m, std::is_same<Tin, _Float16>::value))
-                         : 1.0f;
-    }
-    // all of a thread's loads are issued before the first is used
-    constexpr int kPer = kChunk * kPrepRows * kPrepCols / kT;
-    float ld[kPer];
-    if (vec) {  // uniform: W % 4 == 0 and the frames 4-element aligned
-        // four consecutive pixels of a row a lane (all inside or all outside)
+    for (int i = 0; i < kPGc; i++) v[i] = ldf(src + (long)std::min(q * kPGc + i, C - 1) * g.HW);
+    __builtin_amdgcn_sched_barrier(0);  // every load out before the first use
+    // zero chunk j's values past C and outside the map (chunk by chunk, so
+    // the first chunk's work waits for its own loads only)
+    auto mask_chunk = [&](int j) {
 #pragma unroll
-        for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kT);
-            const int c = i / (kPrepRows * kPrepCols);
-            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-            const bool in = yy < H && xx < W;
-            const float4 v = ldf4(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-            ld[4 * u] = in ? v.x : 0.0f;
-            ld[4 * u + 1] = in ? v.y : 0.0f;
-            ld[4 * u + 2] = in ? v.z : 0.0f;
-            ld[4 * u + 3] = in ? v.w : 0.0f;
+        for (int c = 0; c < kChunk; c++)
+            v[kChunk * j + c] = inmap && q * kPGc + kChunk * j + c < C ? v[kChunk * j + c] : 0.0f;
+    };
+    // the pooled pixel thread gi of each group owns: level 1 (gi < kPN1),
+    // 2 or 3, or none; its channels of group q
+    const int ol = gi < kPN1 ? 1 : gi < kPN1 + kPN2 ? 2 : gi < kPNp ? 3 : 0;
+    const bool pool = pooled && g.levels > 1;  // uniform
+    float p[kPGc];
+    if (pool) {
+        // (the first chunk's round runs while the second chunk's loads are
+        // still in flight)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            // chunk 2q + j of every group (LDS hand-offs only: no wait for
+            // global memory at these barriers)
+            __builtin_amdgcn_sched_barrier(0);
+            mask_chunk(j);
+#pragma unroll
+            for (int c = 0; c < kChunk; c++) xch[q][c][r][x] = v[kChunk * j + c];
+            lds_barrier();
+            // level 1: (group, channel, row, column) items, 4 a thread
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = tid + 1024 * u;
+                const int gq = i >> 10, c = (i >> 6) & 15, y1 = (i >> 4) & 3, x1 = i & 15;
+                const float2 a = *reinterpret_cast<const float2*>(&xch[gq][c][2 * y1][2 * x1]);
+                const float2 d = *reinterpret_cast<const float2*>(&xch[gq][c][2 * y1 + 1][2 * x1]);
+                pl[gq][c][y1 * (kPW / 2) + x1] = pool4(a.x, a.y, d.x, d.y);
+            }
+            // level 2, one item a thread, through its four level-1 parents;
+            // the four level-2 parents of a level-3 pixel are the lanes of a
+            // quad (y2 = bit 1, x2 = 2 x3 + bit 0), whose first lane pools
+            // them (quad moves, no LDS round)
+            {
+                const int gq = tid >> 8, c = (tid >> 4) & 15, x3 = (tid >> 2) & 3;
+                const int y2 = (tid >> 1) & 1, x2 = 2 * x3 + (tid & 1);
+                float4 f[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    f[k] = *reinterpret_cast<const float4*>(&xch[gq][c][4 * y2 + k][4 * x2]);
+                const float a = pool4(f[0].x, f[0].y, f[1].x, f[1].y);
+                const float bb = pool4(f[0].z, f[0].w, f[1].z, f[1].w);
+                const float cc = pool4(f[2].x, f[2].y, f[3].x, f[3].y);
+                const float dd = pool4(f[2].z, f[2].w, f[3].z, f[3].w);
+                const float l2v = pool4(a, bb, cc, dd);
+                pl[gq][c][kPN1 + y2 * (kPW / 4) + x2] = l2v;
+                const int iv = __builtin_bit_cast(int, l2v);
+                // quad_perm broadcasts of lanes 1, 2, 3 of the quad
+                const float l2b = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x55, 0xf, 0xf, false));
+                const float l2c = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xaa, 0xf, 0xf, false));
+                const float l2d = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xff, 0xf, 0xf, false));
+                if ((tid & 3) == 0) pl[gq][c][kPN1 + kPN2 + x3] = pool4(l2v, l2b, l2c, l2d);
+            }
+            lds_barrier();
+            // owners collect their pixel's chunk (before the next chunk's
+            // first barrier, after which pl is written again)
+#pragma unroll
+            for (int c = 0; c < kChunk; c++) p[kChunk * j + c] = pl[q][c][std::min(gi, kPNp - 1)];
         }
+        float mp = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kPer / 4; u++) {
-            const int i = 4 * (tid + u * kT);
-            *reinterpret_cast<float4*>(
-                &l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols]) =
-                make_float4(ld[4 * u], ld[4 * u + 1], ld[4 * u + 2], ld[4 * u + 3]);
-        }
+        for (int i = 0; i < kPGc; i++) mp = fmaxf(mp, fabsf(p[i]));
+        if (ol) pmaxp[q][gi] = mp;
     } else {
-#pragma unroll
-        for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kT;
-            const int c = i / (kPrepRows * kPrepCols);
-            const int r = (i / kPrepCols) % kPrepRows, x = i % kPrepCols;
-            const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-            const bool in = yy < H && xx < W;
-            ld[u] = ldf(src + (in ? (long)c * g.HW + (long)yy * W + xx : 0L));
-            if (!in) ld[u] = 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kPer; u++) {
-            const int i = tid + u * kT;
-            l0[i / (kPrepRows * kPrepCols)][(i / kPrepCols) % kPrepRows][i % kPrepCols] = ld[u];
-        }
+        mask_chunk(0);
+        mask_chunk(1);
     }
-    __syncthreads();
-    const float sc = fscale;
-    const size_t plane = (size_t)g.C * g.Ttot;
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPGc; i++) m = fmaxf(m, fabsf(v[i]));
+    pmax[q][gi] = m;
+    lds_barrier();
+    auto scale_of = [&](float pm) {
+        return mode == kSplitF16 ? __builtin_amdgcn_ldexpf(
+                                       1.0f, split_exponent(pm, std::is_same<Tin, _Float16>::value))
+                                 : 1.0f;
+    };
+    const size_t plane = (size_t)C * g.Ttot;
     unsigned short* const slot = out + (size_t)s * slot_elems;
-    if (blk == 0 && k == 0 && tid == 0)  // the slot's inverse scale (a power of two)
-        *reinterpret_cast<float*>(slot + 2 * plane) = 1.0f / sc;
-    unsigned short* const base = slot + (size_t)k * g.Ttot * kChunk;
-    auto emit = [&](int t, const float (&v)[kChunk]) {
-        u16x8_t hi[2], lo[2];
+    float* const inv = reinterpret_cast<float*>(slot + 2 * plane);
+    // every store after the LDS work: level 0, then the pooled pixel
+    {
+        float pm = 0.0f;
 #pragma unroll
-        for (int u = 0; u < kChunk; u++) {
-            const unsigned pk = mode == kSplitF16 ? split_f16(v[u] * sc) : split_bf16(v[u]);
-            hi[u >> 3][u & 7] = (unsigned short)(pk & 0xffffu);
-            lo[u >> 3][u & 7] = (unsigned short)(pk >> 16);
-        }
-        unsigned short* o = base + (size_t)t * kChunk;
-        *reinterpret_cast<u16x8_t*>(o) = hi[0];
-        *reinterpret_cast<u16x8_t*>(o + 8) = hi[1];
-        *reinterpret_cast<u16x8_t*>(o + plane) = lo[0];
-        *reinterpret_cast<u16x8_t*>(o + plane + 8) = lo[1];
-    };
-    // level 0
-    for (int p = tid; p < kPrepRows * kPrepCols; p += kT) {
-        const int r = p / kPrepCols, x = p % kPrepCols;
-        const int yy = by * kPrepRows + r, xx = bx * kPrepCols + x;
-        if (yy >= H || xx >= W) continue;
-        float v[kChunk];
+        for (int gq = 0; gq < kPGrp; gq++) pm = fmaxf(pm, pmax[gq][gi]);
+        const float sc = scale_of(pm);
+        if (inmap) {
+            const int t = yy * W + xx;
 #pragma unroll
-        for (int c = 0; c < kChunk; c++) v[c] = l0[c][r][x];
-        emit(yy * W + xx, v);
-    }
-    if (!pooled) return;
-    // pooled levels: each level from the one before in LDS (level 1 while level
-    // 0 goes out: both only read level 0), then the three levels' pixels out
-    // together, one per thread
-    auto pool = [&](auto& dst, const auto& from, int rows, int cols) {
-        for (int i = tid; i < kChunk * rows * cols; i += kT) {
-            const int c = i / (rows * cols), r = (i / cols) % rows, x = i % cols;
-            float sum = from[c][2 * r][2 * x] + from[c][2 * r][2 * x + 1];
-            sum = sum + from[c][2 * r + 1][2 * x];
-            sum = sum + from[c][2 * r + 1][2 * x + 1];
-            dst[c][r][x] = 0.25f * sum;
-        }
-    };
-    if (g.levels > 1) pool(l1, l0, kPrepRows / 2, kPrepCols / 2);
-    __syncthreads();
-    if (g.levels > 2) pool(l2, l1, kPrepRows / 4, kPrepCols / 4);
-    __syncthreads();
-    if (g.levels > 3) pool(l3, l2, kPrepRows / 8, kPrepCols / 8);
-    __syncthreads();
-    auto out_level = [&](const auto& src, int l, int rows, int cols, int p) {
-        const int r = p / cols, x = p % cols;
-        const int yy = by * rows + r, xx = bx * cols + x;
-        if (yy >= g.h[l] || xx >= g.w[l]) return;
-        float v[kChunk];
-#pragma unroll
-        for (int c = 0; c < kChunk; c++) v[c] = src[c][r][x];
-        emit(g.off[l] + yy * g.w[l] + xx, v);
-    };
-    constexpr int n1 = (kPrepRows / 2) * (kPrepCols / 2), n2 = n1 / 4, n3 = n2 / 4;
-    for (int p = tid; p < n1 + n2 + n3; p += kT) {
-        if (p < n1) {
-            if (g.levels > 1) out_level(l1, 1, kPrepRows / 2, kPrepCols / 2, p);
-        } else if (p < n1 + n2) {
-            if (g.levels > 2) out_level(l2, 2, kPrepRows / 4, kPrepCols / 4, p - n1);
-        } else {
-            if (g.levels > 3) out_level(l3, 3, kPrepRows / 8, kPrepCols / 8, p - n1 - n2);
+            for (int j = 0; j < 2; j++)
+                if (2 * q + j < nk)
+                    emit_chunk(slot, plane, g.Ttot, 2 * q + j, t, &v[kChunk * j], sc, mode);
+            if (q == 0) inv[t] = 1.0f / sc;  // a power of two: exact
         }
     }
+    if (!pool || !ol || ol >= g.levels) return;
+    const int oy = ol == 1 ? gi / (kPW / 2) : ol == 2 ? (gi - kPN1) / (kPW / 4) : 0;
+    const int ox = ol == 1 ? gi % (kPW / 2) : ol == 2 ? (gi - kPN1) % (kPW / 4) : gi - kPN1 - kPN2;
+    const int ly = by * (kPH >> ol) + oy, lx = bx * (kPW >> ol) + ox;
+    if (ly >= g.h[ol] || lx >= g.w[ol]) return;
+    float pm = 0.0f;
+#pragma unroll
+    for (int gq = 0; gq < kPGrp; gq++) pm = fmaxf(pm, pmaxp[gq][gi]);
+    const float sc = scale_of(pm);
+    const int t = g.off[ol] + ly * g.w[ol] + lx;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        if (2 * q + j < nk) emit_chunk(slot, plane, g.Ttot, 2 * q + j, t, &p[kChunk * j], sc, mode);
+    if (q == 0) inv[t] = 1.0f / sc;
 }
 
 struct alignas(16) SplitSmem {
@@ -622,6 +604,8 @@ struct alignas(16) SplitSmem {
     int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
     int pix[kSrcTile];        // pixel of each source
+    float ssc[kSrcTile];      // alpha times each source's inverse split scale
+    float tsc[kTgtTile];      // each target's inverse split scale
 };
 
 // one 32x32x16 MFMA of the split mode's operand type
@@ -714,9 +698,9 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const size_t plane = (size_t)g.C * Ttot;
     const unsigned short* fa = feat + (size_t)es.si[e] * slot_elems;
     const unsigned short* fb = feat + (size_t)es.sj[e] * slot_elems;
-    // alpha over both frames' split scales (powers of two: no rounding)
-    const float fs = alpha * *reinterpret_cast<const float*>(fa + 2 * plane) *
-                     *reinterpret_cast<const float*>(fb + 2 * plane);
+    // the rows' inverse split scales (powers of two), after the planes
+    const float* isa = reinterpret_cast<const float*>(fa + 2 * plane);
+    const float* isb = reinterpret_cast<const float*>(fb + 2 * plane);
     const int* ord = order + (size_t)e * ostride;
     // the source tile's target boxes: virtual rows cum[l] .. cum[l + 1] - 1 are
     // level l's box (bh x bw cells from row ya, column xa), row-major
@@ -768,9 +752,14 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const float* cpt = coords + ((size_t)e * 2 + (wave >> 1)) * HW +
                        std::min((unsigned)ord[std::min(p0 + (wave & 1) * 64 + lane, HW - 1)],
                                 (unsigned)(HW - 1));
+    const int tr0 = trow(v0 + hr), tr1 = trow(v0 + 128 + hr);
+    // the inverse scales of source row hr and target rows hr, 128 + hr: loaded
+    // ahead of the chunk loop's staging (whose waits count loads in issue
+    // order) and put in LDS after it
+    const float sc_a = isa[pa], sc_b0 = isb[tr0], sc_b1 = isb[tr1];
     const unsigned short* ga = fa + (size_t)pa * kChunk + hh;
-    const unsigned short* gb0 = fb + (size_t)trow(v0 + hr) * kChunk + hh;
-    const unsigned short* gb1 = fb + (size_t)trow(v0 + 128 + hr) * kChunk + hh;
+    const unsigned short* gb0 = fb + (size_t)tr0 * kChunk + hh;
+    const unsigned short* gb1 = fb + (size_t)tr1 * kChunk + hh;
     const size_t kstep = (size_t)Ttot * kChunk;
     const int wdst = wave * 512;  // this wave's 1 KB of a 4 KB region, in u16
 
@@ -900,6 +889,11 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         sm.org[tid][0] = in ? floor_clamped(sm.crd[0][tid]) : -(1 << 20);  // matches no cell
         sm.org[tid][1] = in ? floor_clamped(sm.crd[1][tid]) : -(1 << 20);
     }
+    if (!(tid & 1)) {
+        sm.ssc[hr] = alpha * sc_a;  // powers of two: no rounding
+        sm.tsc[hr] = sc_b0;
+        sm.tsc[128 + hr] = sc_b1;
+    }
     lds_barrier();  // every wave is done with the stages before T overwrites them
 
     // ---- window extraction ----
@@ -929,6 +923,12 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         kBufWord3);
     typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
+    // T holds the accumulators times their targets' inverse scales (powers of
+    // two: no rounding); the extraction multiplies by alpha times the
+    // source's, so each cell is rounded once, as alpha times its fp32 sum
+    float tsv[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; tb++) tsv[tb] = sm.tsc[wn * 128 + tb * 32 + orow];
 #pragma unroll
     for (int sb = 0; sb < 2; sb++) {
         if (sb) lds_barrier();  // the first half's cells have all been read
@@ -938,14 +938,15 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             for (int gq = 0; gq < 4; gq++) {
                 const int t = wn * 128 + tb * 32 + orow;
                 const int s = wm * 32 + gq * 8 + khalf * 4;
-                *reinterpret_cast<float4*>(&sm.u.T[t][s]) =
-                    make_float4(acc[sb][tb][4 * gq], acc[sb][tb][4 * gq + 1],
-                                acc[sb][tb][4 * gq + 2], acc[sb][tb][4 * gq + 3]);
+                *reinterpret_cast<float4*>(&sm.u.T[t][s]) = make_float4(
+                    acc[sb][tb][4 * gq] * tsv[tb], acc[sb][tb][4 * gq + 1] * tsv[tb],
+                    acc[sb][tb][4 * gq + 2] * tsv[tb], acc[sb][tb][4 * gq + 3] * tsv[tb]);
             }
         lds_barrier();
         const int s = wave * 16 + jj;                            // column of T
         const int lsrc = (s >> 5) * 64 + sb * 32 + (s & 31);   // source in the tile
         const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
+        const float fs = sm.ssc[lsrc];
         const bool pin = p0 + lsrc < HW;
         const float* Tcol = &sm.u.T[0][s];
         // byte offset of cell 0 of row 0 of level 0 of this source in the slot
@@ -1020,9 +1021,9 @@ Geom make_geom(const slk_ctx* ctx) {
 }
 
 // u16 elements of one frame slot: the hi and lo planes [C/16][Ttot][16], then
-// the frame's inverse split scale (one float), padded to 256 bytes
+// each row's inverse split scale (Ttot floats), padded to 256 bytes
 size_t slot_elems(const Geom& g) {
-    return (2 * (size_t)g.C * g.Ttot + 2 + 127) / 128 * 128;
+    return (2 * (size_t)g.C * g.Ttot + 2 * (size_t)g.Ttot + 127) / 128 * 128;
 }
 
 // the split of fp32 (or fp16) features under the context's precision
@@ -1036,40 +1037,18 @@ template <typename Tin>
 int prep_slots_to(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames& sf, const Geom& g,
                   int slot_lo, int nslots, bool pooled, const MaskArgs& mk, unsigned short* out,
                   int mode, hipStream_t stream) {
-    const int nbx = (g.w[0] + kPrepCols - 1) / kPrepCols;
-    const int nblk = nbx * ((g.h[0] + kPrepRows - 1) / kPrepRows);
-    const long nprep = (long)nblk * (g.C / kChunk) * std::max(nslots, 0);
+    const int nbx = (g.w[0] + kPW - 1) / kPW;
+    const int nblk = nbx * ((g.h[0] + kPH - 1) / kPH);
+    const long nprep = (long)nblk * std::max(nslots, 0);
     const long nmask = mk.list ? mk.nedges : 0;
     if (nprep + nmask == 0) return SLK_OK;
     if (nprep + nmask > INT_MAX) return fail(SLK_E_ARG, "feature preparation grid too large");
-    // vector loads of 4 pixels when every row starts 4-element aligned
-    const bool vec = g.w[0] % 4 == 0 && fstride % 4 == 0 &&
-                     reinterpret_cast<uintptr_t>(fm) % (4 * sizeof(Tin)) == 0;
+    if (g.C > kPrepC) return fail(SLK_E_ARG, "feature preparation: more than 128 channels");
     const long se = (long)slot_elems(g);
-    float* part = ctx->frame_max.as<float>();
-    const long n = (long)g.C * g.HW;
-    const int nparts = (int)std::min<long>(kMaxParts, (n + kMaxChunk - 1) / kMaxChunk);
-    if (mode == kSplitF16 && nslots > 0) {
-        // the frames' partial maxima for their split scales
-        if (ctx->frame_max.bytes < (size_t)(slot_lo + nslots) * kMaxParts * sizeof(float))
-            return fail(SLK_E_ARG, "feature preparation: frame-maximum buffer too small");
-        ProfScope ps(ctx, "corr_frame_max", stream);
-        hipLaunchKernelGGL((k_frame_max<Tin>), dim3(nparts, nslots), dim3(256), 0, stream, fm,
-                           fstride, sf, slot_lo, n, (vec && g.HW % 4 == 0) ? 1 : 0, nparts, part);
-        SLK_HIP(hipGetLastError());
-    }
     ProfScope ps(ctx, "corr_feat_prep", stream);
-    // 1024-thread workgroups (16-wave mask chains) for maps up to 4096
-    // pixels, two a CU; 512 above, three a CU (the preparation's share of
-    // the launch is larger there)
-    if (g.HW <= 4096)
-        hipLaunchKernelGGL((k_feat_prep<Tin, 1024>), dim3((unsigned)(nprep + nmask)), dim3(1024),
-                           0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk, mode, part, nparts);
-    else
-        hipLaunchKernelGGL((k_feat_prep<Tin, 512>), dim3((unsigned)(nprep + nmask)), dim3(512),
-                           0, stream, fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0,
-                           vec ? 1 : 0, nbx, nblk, (int)nmask, mk, mode, part, nparts);
+    hipLaunchKernelGGL((k_feat_prep<Tin>), dim3((unsigned)(nprep + nmask)), dim3(1024), 0, stream,
+                       fm, fstride, sf, slot_lo, out, se, g, pooled ? 1 : 0, nbx, nblk,
+                       (int)nmask, mk, mode);
     SLK_HIP(hipGetLastError());
     return SLK_OK;
 }
@@ -1102,8 +1081,7 @@ int mask_and_windows(slk_ctx* ctx, const Tin* fm, long fstride, const SlotFrames
     const long ostride = order_stride(g.HW, mtiles);
     MaskArgs mk{coords, ctx->tile_list.as<int>(), ctx->tile_ctr.as<int>(),
                 ctx->src_order.as<int>(), ostride, mtiles, ntiles, n, kg};
-    // feature preparation and the source order, one launch (after the frames'
-    // maxima under the fp16 split)
+    // feature preparation and the source order, one launch
     SLK_TRY(prep_slots(ctx, fm, fstride, sf, g, slot_lo, nslots, pooled, mk, mode, stream));
     {
         ProfScope ps(ctx, "corr_window", stream);
@@ -1168,15 +1146,16 @@ int split_windows(slk_ctx* ctx, const Tin* fm, long fstride, const int* ii_host,
 
 }  // namespace
 
-// the split path: whole 16-channel chunks, and an edge's source tiles within
-// the order pass's LDS (h*w <= 262144; larger maps take the fp32 MFMA kernels)
+// the split path: whole 16-channel chunks, at most kPrepC channels (a
+// preparation block holds all of a pixel's), and an edge's source tiles within
+// the order pass's LDS (h*w <= 262144); other maps take the fp32 MFMA kernels
 bool corr_split_supported(const slk_ctx* ctx) {
-    return ctx->C % kChunk == 0 && (ctx->HW + kSrcTile - 1) / kSrcTile <= kPrepL1Words;
+    return ctx->C % kChunk == 0 && ctx->C <= kPrepC &&
+           (ctx->HW + kSrcTile - 1) / kSrcTile <= kPrepL1Words;
 }
 
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
-                          size_t* order_per_edge, size_t* ctr_bytes, size_t* max_per_slot) {
-    *max_per_slot = kMaxParts * sizeof(float);
+                          size_t* order_per_edge, size_t* ctr_bytes) {
     const Geom g = make_geom(ctx);
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
@@ -1193,7 +1172,6 @@ int corr_split_alloc(slk_ctx* ctx) {
     const Geom g = make_geom(ctx);
     const size_t slots = 2 * (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch);
     SLK_TRY(ctx->split_feat.ensure(slots * slot_elems(g) * sizeof(unsigned short)));
-    SLK_TRY(ctx->frame_max.ensure(slots * kMaxParts * sizeof(float)));
     const size_t mtiles = (g.HW + kSrcTile - 1) / kSrcTile;
     const size_t ntiles = (g.Ttot + kTgtTile - 1) / kTgtTile;
     const size_t tiles = (size_t)std::min(ctx->max_batch, kMaxEdgesPerLaunch) * mtiles * ntiles;
@@ -1233,9 +1211,6 @@ int corr_split_prepare(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,
     if (bytes > ctx->prep_feat.bytes && ctx->prep_feat.ptr)
         SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old frames
     SLK_TRY(ctx->prep_feat.ensure(bytes));
-    if ((size_t)nframes * kMaxParts * sizeof(float) > ctx->frame_max.bytes && ctx->frame_max.ptr)
-        SLK_HIP(hipDeviceSynchronize());  // earlier launches may still read the old maxima
-    SLK_TRY(ctx->frame_max.ensure((size_t)nframes * kMaxParts * sizeof(float)));
     SlotFrames sf{};
     sf.ident = 1;
     const MaskArgs none{};

@@ -81,7 +81,6 @@ struct slk_ctx {
     int prep_nframes = 0;
     int prep_mode = 0;      // their split (fp16 scaled or bf16)
     bool prep_alo = true;   // whether their level-0 lo planes can be nonzero
-    slk::DevBuf frame_max;  // partial maxima of |x| of each slot's frame (the fp16 split's scale)
     slk::DevBuf tile_list;  // the (edge, source tile, target tile) ids holding a window cell
     slk::DevBuf tile_ctr;   // listed-tile count and the correlation kernel's tile counters
     slk::DevBuf src_order;  // per edge: sources sorted by window position (pixel, x, y), boxes
@@ -150,7 +149,7 @@ int corr_split_alloc(slk_ctx* ctx);
 // bytes of one feature slot (two per edge of a launch), of one edge's tile
 // list and source order, and of the launch's tile counters
 void corr_split_footprint(const slk_ctx* ctx, size_t* slot_bytes, size_t* tiles_per_edge,
-                          size_t* order_per_edge, size_t* ctr_bytes, size_t* max_per_slot);
+                          size_t* order_per_edge, size_t* ctr_bytes);
 // workgroups of the batched correlation kernel on a part with `cus` CUs
 int corr_split_grid(int cus);
 int corr_split_windows(slk_ctx* ctx, const void* fmaps, int dtype, long fstride,

@@ -340,6 +340,33 @@ def test_split_precision_wide_range_and_coherent_lo(slk, prec):
         assert_close_rel(got, ref, tol=bar, what=name)
 
 
+def test_split_scale_per_pixel(slk):
+    """Pixels many binades below their frame's largest: source frames 0, 1
+    hold N(0,1) features times one factor 2^U(-24, 24) per pixel, target
+    frames 2, 3 plain N(0,1). Under the scaled fp16 split every pixel takes
+    its own scale, so each output is held to F16X3_TOL relative to the bound
+    alpha |f_i| max_q |f_j(q)| of its own source pixel i (Cauchy-Schwarz over
+    the channels; a pooled target's norm and a bilinear sample of cells never
+    exceed the largest level-0 norm). One scale per frame would flush the
+    small pixels' fp16 operands to zero (errors of order 1 against that
+    bound). The worst ratio is printed."""
+    h, w = 24, 32
+    ii = np.array([0, 1, 0, 1], np.int32)
+    jj = np.array([2, 3, 3, 2], np.int32)
+    rng = np.random.default_rng(50)
+    f = rng.standard_normal((4, 128, h, w))
+    f[:2] *= np.exp2(rng.uniform(-24, 24, (2, 1, h, w)))
+    f = f.astype(np.float32)
+    coords = wl.flow_coords(len(ii), h, w, seed=51)
+    got = _window_of(slk, f, coords, ii, jj, prec=2)
+    ref = orc.corr_batch(f, ii, jj, coords, 1.0 / 16.0)
+    norms = np.sqrt((f.astype(np.float64) ** 2).sum(axis=1)).reshape(4, h * w)
+    bound = (1.0 / 16.0) * norms[ii][:, None, :] * norms[jj].max(axis=1)[:, None, None]
+    ratio = float(np.max(np.abs(got.astype(np.float64) - ref) / bound))
+    print(f"per-pixel scale: max |g - r| / (alpha |f_i| max|f_j|) = {ratio:.3g}")
+    assert ratio <= F16X3_TOL
+
+
 def test_device_indices_and_chunking(slk):
     """Device-resident ii/jj, and B above max_batch (processed in chunks)."""
     h, w = 24, 32
