@@ -379,22 +379,25 @@ __device__ __forceinline__ int split_exponent(float m, bool exact) {
 }
 
 // Feature preparation of frame slots, one launch of 1024-thread workgroups.
-// A workgroup takes an 8 x 32 block of level-0 pixels, each thread one pixel
-// and one of four groups of 32 channels (waves 4q..4q+3: group q, two block
-// rows a wave, so each load instruction reads two 128-byte row pieces) in
-// registers. A pixel's split scale comes from the largest magnitude among
-// its channels (the four groups' maxima through LDS); the thread writes the
-// hi/lo split of its two chunks, 16 channels = 32 bytes per pixel and
-// plane, into out[slot][plane][C/16][Ttot][16], and group 0 the pixel's
-// inverse scale into the slot's float array [Ttot] after the planes. The
-// pooled levels of the block (4 x 16, 2 x 8, 1 x 4 pixels; each pooled value
-// 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents' row first; a
-// pooled pixel's parents always lie in the block) are formed in LDS one
-// chunk of every group at a time, level 2 from level 0 through the same
-// level-1 sums, and collected by one owner thread per pooled pixel and
-// group, which then splits them the same way. Under the fp16 split a pixel's
-// features are scaled by 2^e (split_exponent of its largest magnitude),
-// under the bf16 split by 1. `pooled` = 0 writes level 0 only (source slots).
+// A workgroup takes an 8 x 32 block of level-0 pixels; wave w holds block
+// rows 2 (w % 4) (lanes 0-31) and 2 (w % 4) + 1 (lanes 32-63) of channel
+// group w / 4 (32 channels of a pixel in a thread's registers), so each load
+// instruction reads two 128-byte row pieces. A pixel's split scale comes
+// from the largest magnitude among its channels (the four groups' maxima
+// through LDS); its thread writes the hi/lo split of its two chunks, 16
+// channels = 32 bytes per pixel and plane, into
+// out[slot][plane][C/16][Ttot][16], and group 0 the pixel's inverse scale
+// into the slot's float array [Ttot] after the planes. Pooled levels (each
+// pooled value 0.25 * (((a + b) + c) + d) of its 2x2 parents, the parents'
+// row first; a pooled pixel's parents always lie in the block): level 1 in
+// registers (the 2x2 parents of level-1 pixel (w % 4, x) are lanes 2x,
+// 2x + 1, 2x + 32, 2x + 33 of the wave: quad moves and a cross-half
+// permute), kept by lane 2x; level 2 from level 1 through LDS, level 3
+// from level 2 by quad moves; a level-2 or level-3 pixel's channels of a
+// group are collected by one owner thread (lanes 32.. of the group's waves).
+// Under the fp16 split a pixel's features are scaled by 2^e (split_exponent
+// of its largest magnitude), under the bf16 split by 1. `pooled` = 0 writes
+// level 0 only (source slots).
 // One-dimensional grid: first, when mk.list is set, one order workgroup per
 // edge (order_and_boxes, on the exchange arrays; they are the longer chains,
 // so they are dispatched first), then the blocks x slots preparation
@@ -410,6 +413,15 @@ static_assert(kPGrp * kPH * kPW == 1024 && kPGc == 2 * kChunk, "prep workgroup s
 __device__ __forceinline__ float pool4(float a, float b, float c, float d) {
     return 0.25f * (((a + b) + c) + d);
 }
+
+// v of another lane of the caller's quad (DPP quad_perm kCtrl)
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl,
+                                                              0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;                                       // quad_perm(1, 0, 3, 2)
+constexpr int kDppQ1 = 0x55, kDppQ2 = 0xAA, kDppQ3 = 0xFF;           // quad_perm(k, k, k, k)
 
 // the hi/lo split of one pixel's chunk k (16 channels) at row t
 __device__ __forceinline__ void emit_chunk(unsigned short* slot, size_t plane, int Ttot, int k,
@@ -433,27 +445,26 @@ __global__ __launch_bounds__(1024) void k_feat_prep(
     const Tin* __restrict__ fm, long fstride, SlotFrames sf, int slot_lo,
     unsigned short* __restrict__ out, long slot_elems, Geom g, int pooled, int nbx, int nblk,
     int nmask, MaskArgs mk, int mode) {
-    constexpr int kPNp = kPN1 + kPN2 + kPN3;
-    // a chunk of every group: level 0, and the pooled values (level 1 at
-    // [0, kPN1), 2 at [kPN1, kPN1 + kPN2), 3 after them, each row-major)
-    __shared__ __attribute__((aligned(16))) float xch[kPGrp][kChunk][kPH][kPW];
-    __shared__ float pl[kPGrp][kChunk][kPNp];
-    __shared__ float pmax[kPGrp][kPH * kPW];  // per group: max |x| of a pixel
-    __shared__ float pmaxp[kPGrp][kPNp];      // ... of a pooled pixel
+    constexpr int kPN23 = kPN2 + kPN3;
+    __shared__ float pl1[kPGrp][kPGc][kPH / 2][kPW / 2];  // level 1 of every group
+    __shared__ float pl2[kPGrp][kPGc][kPN23];             // levels 2 and 3, row-major
+    __shared__ float pmax[kPGrp][kPH * kPW];              // per group: max |x| of a pixel
+    __shared__ float pmax1[kPGrp][kPN1];                  // ... of a level-1 pixel
+    __shared__ float pmax23[kPGrp][kPN23];                // ... of a level-2 or 3 pixel
     __shared__ int wave_sum[16];
     if ((int)blockIdx.x < nmask) {  // uniform
         // the order chains are the launch's long pole: their waves issue
         // ahead of the preparation waves sharing their SIMDs
         __builtin_amdgcn_s_setprio(2);
-        static_assert(sizeof(xch) >= kMaxKeys * sizeof(int) &&
-                          sizeof(pl) >= kPrepL1Words * sizeof(int), "order LDS");
-        order_and_boxes<1024>(mk, g, blockIdx.x, reinterpret_cast<int*>(&xch[0][0][0][0]),
-                              reinterpret_cast<int*>(&pl[0][0][0]), wave_sum);
+        static_assert(sizeof(pl1) >= kMaxKeys * sizeof(int) &&
+                          sizeof(pl2) >= kPrepL1Words * sizeof(int), "order LDS");
+        order_and_boxes<1024>(mk, g, blockIdx.x, reinterpret_cast<int*>(&pl1[0][0][0][0]),
+                              reinterpret_cast<int*>(&pl2[0][0][0]), wave_sum);
         return;
     }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int q = wave >> 2, gi = tid & 255;  // channel group, thread in the group
-    const int r = 2 * (wave & 3) + (lane >> 5), x = lane & 31;  // gi = r * kPW + x
+    const int q = wave >> 2, wr = wave & 3, gi = tid & 255;  // group, row pair, thread in group
+    const int hf = lane >> 5, x = lane & 31, r = 2 * wr + hf;  // gi = r * kPW + x
     const int nprep = (int)gridDim.x - nmask;
     int b = blockIdx.x - nmask;
     {
@@ -473,81 +484,64 @@ __global__ __launch_bounds__(1024) void k_feat_prep(
 #pragma unroll
     for (int i = 0; i < kPGc; i++) v[i] = ldf(src + (long)std::min(q * kPGc + i, C - 1) * g.HW);
     __builtin_amdgcn_sched_barrier(0);  // every load out before the first use
-    // zero chunk j's values past C and outside the map (chunk by chunk, so
-    // the first chunk's work waits for its own loads only)
-    auto mask_chunk = [&](int j) {
 #pragma unroll
-        for (int c = 0; c < kChunk; c++)
-            v[kChunk * j + c] = inmap && q * kPGc + kChunk * j + c < C ? v[kChunk * j + c] : 0.0f;
-    };
-    // the pooled pixel thread gi of each group owns: level 1 (gi < kPN1),
-    // 2 or 3, or none; its channels of group q
-    const int ol = gi < kPN1 ? 1 : gi < kPN1 + kPN2 ? 2 : gi < kPNp ? 3 : 0;
-    const bool pool = pooled && g.levels > 1;  // uniform
-    float p[kPGc];
-    if (pool) {
-        // (the first chunk's round runs while the second chunk's loads are
-        // still in flight)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            // chunk 2q + j of every group (LDS hand-offs only: no wait for
-            // global memory at these barriers)
-            __builtin_amdgcn_sched_barrier(0);
-            mask_chunk(j);
-#pragma unroll
-            for (int c = 0; c < kChunk; c++) xch[q][c][r][x] = v[kChunk * j + c];
-            lds_barrier();
-            // level 1: (group, channel, row, column) items, 4 a thread
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int i = tid + 1024 * u;
-                const int gq = i >> 10, c = (i >> 6) & 15, y1 = (i >> 4) & 3, x1 = i & 15;
-                const float2 a = *reinterpret_cast<const float2*>(&xch[gq][c][2 * y1][2 * x1]);
-                const float2 d = *reinterpret_cast<const float2*>(&xch[gq][c][2 * y1 + 1][2 * x1]);
-                pl[gq][c][y1 * (kPW / 2) + x1] = pool4(a.x, a.y, d.x, d.y);
-            }
-            // level 2, one item a thread, through its four level-1 parents;
-            // the four level-2 parents of a level-3 pixel are the lanes of a
-            // quad (y2 = bit 1, x2 = 2 x3 + bit 0), whose first lane pools
-            // them (quad moves, no LDS round)
-            {
-                const int gq = tid >> 8, c = (tid >> 4) & 15, x3 = (tid >> 2) & 3;
-                const int y2 = (tid >> 1) & 1, x2 = 2 * x3 + (tid & 1);
-                float4 f[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    f[k] = *reinterpret_cast<const float4*>(&xch[gq][c][4 * y2 + k][4 * x2]);
-                const float a = pool4(f[0].x, f[0].y, f[1].x, f[1].y);
-                const float bb = pool4(f[0].z, f[0].w, f[1].z, f[1].w);
-                const float cc = pool4(f[2].x, f[2].y, f[3].x, f[3].y);
-                const float dd = pool4(f[2].z, f[2].w, f[3].z, f[3].w);
-                const float l2v = pool4(a, bb, cc, dd);
-                pl[gq][c][kPN1 + y2 * (kPW / 4) + x2] = l2v;
-                const int iv = __builtin_bit_cast(int, l2v);
-                // quad_perm broadcasts of lanes 1, 2, 3 of the quad
-                const float l2b = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x55, 0xf, 0xf, false));
-                const float l2c = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xaa, 0xf, 0xf, false));
-                const float l2d = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xff, 0xf, 0xf, false));
-                if ((tid & 3) == 0) pl[gq][c][kPN1 + kPN2 + x3] = pool4(l2v, l2b, l2c, l2d);
-            }
-            lds_barrier();
-            // owners collect their pixel's chunk (before the next chunk's
-            // first barrier, after which pl is written again)
-#pragma unroll
-            for (int c = 0; c < kChunk; c++) p[kChunk * j + c] = pl[q][c][std::min(gi, kPNp - 1)];
-        }
-        float mp = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kPGc; i++) mp = fmaxf(mp, fabsf(p[i]));
-        if (ol) pmaxp[q][gi] = mp;
-    } else {
-        mask_chunk(0);
-        mask_chunk(1);
-    }
+    for (int i = 0; i < kPGc; i++) v[i] = inmap && q * kPGc + i < C ? v[i] : 0.0f;
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < kPGc; i++) m = fmaxf(m, fabsf(v[i]));
     pmax[q][gi] = m;
+    const bool pool = pooled && g.levels > 1;  // uniform
+    // level-1 owners: lane 2 x1 of the lower half (pixel (wr, x1)); level-2
+    // and level-3 owners: lanes 32.. of the group's waves, o23 = wr * 32 + x
+    const bool own1 = hf == 0 && !(x & 1);
+    const int o23 = wr * 32 + x;
+    const bool own23 = hf == 1 && o23 < kPN23;
+    float p[kPGc];
+    if (pool) {
+#pragma unroll
+        for (int i = 0; i < kPGc; i++) {
+            const float bq = dpp_f<kDppXor1>(v[i]);
+            // lane xor 32 (ds_bpermute; this compiler's permlane32_swap
+            // builtin returned the operand's own half here)
+            const float cq = __builtin_bit_cast(
+                float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, v[i])));
+            const float dq = dpp_f<kDppXor1>(cq);
+            p[i] = pool4(v[i], bq, cq, dq);
+        }
+        float m1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPGc; i++) m1 = fmaxf(m1, fabsf(p[i]));
+        if (own1) {
+#pragma unroll
+            for (int i = 0; i < kPGc; i++) pl1[q][i][wr][x >> 1] = p[i];
+            pmax1[q][wr * (kPW / 2) + (x >> 1)] = m1;
+        }
+        lds_barrier();
+        // level 2: (group, channel, x3, y2, x2 & 1) items, 2 a thread; the four
+        // level-2 parents of a level-3 pixel are the lanes of a quad, whose
+        // first lane pools them
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int i = tid + 1024 * u;
+            const int gq = i >> 9, c = (i >> 4) & 31, x3 = (i >> 2) & 3;
+            const int y2 = (i >> 1) & 1, x2 = 2 * x3 + (i & 1);
+            const float l2 = pool4(pl1[gq][c][2 * y2][2 * x2], pl1[gq][c][2 * y2][2 * x2 + 1],
+                                   pl1[gq][c][2 * y2 + 1][2 * x2], pl1[gq][c][2 * y2 + 1][2 * x2 + 1]);
+            pl2[gq][c][y2 * (kPW / 4) + x2] = l2;
+            const float l3 = pool4(l2, dpp_f<kDppQ1>(l2), dpp_f<kDppQ2>(l2), dpp_f<kDppQ3>(l2));
+            if ((i & 3) == 0) pl2[gq][c][kPN2 + x3] = l3;
+        }
+        lds_barrier();
+        if (own23) {
+            float m23 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kPGc; i++) {
+                p[i] = pl2[q][i][o23];
+                m23 = fmaxf(m23, fabsf(p[i]));
+            }
+            pmax23[q][o23] = m23;
+        }
+    }
     lds_barrier();
     auto scale_of = [&](float pm) {
         return mode == kSplitF16 ? __builtin_amdgcn_ldexpf(
@@ -557,7 +551,7 @@ __global__ __launch_bounds__(1024) void k_feat_prep(
     const size_t plane = (size_t)C * g.Ttot;
     unsigned short* const slot = out + (size_t)s * slot_elems;
     float* const inv = reinterpret_cast<float*>(slot + 2 * plane);
-    // every store after the LDS work: level 0, then the pooled pixel
+    // every store after the LDS work: level 0, then the owned pooled pixel
     {
         float pm = 0.0f;
 #pragma unroll
@@ -572,14 +566,17 @@ __global__ __launch_bounds__(1024) void k_feat_prep(
             if (q == 0) inv[t] = 1.0f / sc;  // a power of two: exact
         }
     }
-    if (!pool || !ol || ol >= g.levels) return;
-    const int oy = ol == 1 ? gi / (kPW / 2) : ol == 2 ? (gi - kPN1) / (kPW / 4) : 0;
-    const int ox = ol == 1 ? gi % (kPW / 2) : ol == 2 ? (gi - kPN1) % (kPW / 4) : gi - kPN1 - kPN2;
+    if (!pool || !(own1 || own23)) return;
+    const int ol = own1 ? 1 : o23 < kPN2 ? 2 : 3;
+    if (ol >= g.levels) return;
+    const int oy = ol == 1 ? wr : ol == 2 ? o23 / (kPW / 4) : 0;
+    const int ox = ol == 1 ? x >> 1 : ol == 2 ? o23 % (kPW / 4) : o23 - kPN2;
     const int ly = by * (kPH >> ol) + oy, lx = bx * (kPW >> ol) + ox;
     if (ly >= g.h[ol] || lx >= g.w[ol]) return;
     float pm = 0.0f;
 #pragma unroll
-    for (int gq = 0; gq < kPGrp; gq++) pm = fmaxf(pm, pmaxp[gq][gi]);
+    for (int gq = 0; gq < kPGrp; gq++)
+        pm = fmaxf(pm, ol == 1 ? pmax1[gq][wr * (kPW / 2) + ox] : pmax23[gq][o23]);
     const float sc = scale_of(pm);
     const int t = g.off[ol] + ly * g.w[ol] + lx;
 #pragma unroll
