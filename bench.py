@@ -64,7 +64,7 @@ PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 # HBM bytes per corr_window launch (48 edges): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes of this script, scaled by a 256 MiB device copy
 # (profiles/corr_window48_pmc_traffic.md)
-TRAFFIC_BYTES = 379996167
+TRAFFIC_BYTES = 381435721
 # HBM bytes of the glue's 48-row copy (gather of 48 distinct 128x3072-float
 # rows): the same passes over bench.py --glue (profiles/glue48_kernel_stats.md)
 GLUE_ROWS_TRAFFIC_BYTES = 151029965
