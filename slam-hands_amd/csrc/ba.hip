@@ -1107,17 +1107,28 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
             }
         }
         __syncthreads();
-        // (2) the diagonal block, eliminated by every thread (uniform)
-        double D[kPW][kPW], Lb[kPW][kPW], rj[kPW], dj[kPW];
+        // (2) the diagonal block, eliminated by every thread (uniform), and
+        // with it, pivot by pivot, thread t's row r0 + t of rows r0..n8
+        // (right-looking: l_j = u_j / d_j, then u_k -= l_j D_kj for the later
+        // columns k, D_kj being the block's column j before its scaling), so
+        // the rows' chains run beside the pivots' instead of after them
+        const bool has_row = tid <= n8 - r0;
+        const int row = has_row ? r0 + tid : n8;
+        double D[kPW][kPW], Lb[kPW][kPW], rj[kPW], dj[kPW], u[kPW], l[kPW];
 #pragma unroll
         for (int i = 0; i < kPW; i++)
 #pragma unroll
             for (int k = 0; k <= i; k++) D[i][k] = PU[c0 + i][k];
 #pragma unroll
+        for (int j = 0; j < kPW; j++) u[j] = PU[row][j];
+#pragma unroll
         for (int j = 0; j < kPW; j++) {
             dj[j] = D[j][j];
             ok = ok && (dj[j] > 0.0);
             rj[j] = rcp_f64_1(dj[j]);
+            l[j] = u[j] * rj[j];
+#pragma unroll
+            for (int k = j + 1; k < kPW; k++) u[k] -= l[j] * D[k][j];
 #pragma unroll
             for (int i = j + 1; i < kPW; i++) Lb[i][j] = D[i][j] * rj[j];
 #pragma unroll
@@ -1126,20 +1137,7 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
                 for (int k = j + 1; k <= i; k++) D[i][k] -= Lb[i][j] * D[k][j];
         }
         if (!ok) break;  // uniform: every thread took the same pivots
-        if (tid <= n8 - r0) {
-            // rows r0..n8: forward substitution against the block, thread t
-            // on row r0 + t
-            const int row = r0 + tid;
-            double u[kPW], l[kPW];
-#pragma unroll
-            for (int j = 0; j < kPW; j++) u[j] = PU[row][j];
-#pragma unroll
-            for (int j = 0; j < kPW; j++) {
-                double v = u[j];
-#pragma unroll
-                for (int m = 0; m < j; m++) v -= l[m] * (Lb[j][m] * dj[m]);
-                l[j] = v * rj[j];
-            }
+        if (has_row) {
 #pragma unroll
             for (int j = 0; j < kPW; j++) {
                 PL[row][j] = l[j];
