@@ -625,17 +625,31 @@ __device__ __forceinline__ void step_pose(const float* p7, const float (&d6)[6],
     for (int m = 0; m < 4; m++) out[3 + m] = (float)q1[m];
 }
 
+// A halted call takes no more steps: like a rejected step, but not reported
+// as one. The flag is written by an earlier launch, so a solve reads it with
+// its system's loads rather than after the factorization: an unconditional
+// vector load (a zero word stands in for a missing flag) whose word is only
+// tested in finish_solve. Its address carries a per-lane zero offset the
+// compiler cannot fold, so the load is not turned into a scalar load that is
+// waited for at once; it stays in flight beside the system's loads.
+__device__ int g_no_halt = 0;
+__device__ __forceinline__ int solve_halt_word(const SolveArgs& A) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return __hip_atomic_load((A.halt ? A.halt : &g_no_halt) + z, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Outputs of a solve: the status flags, dx (fp64 and the fp32 step), and the
 // retraction of poses t0..t1-1, whose current values are read from
 // pose_src[(k - t0) * 7 ..] (A.poses + 7 * t0, or a copy taken earlier).
 // With A.publish, the flag is set once the status and dx are out, before the
-// retraction (every thread of the workgroup calls this).
+// retraction (every thread of the workgroup calls this). halt_word:
+// solve_halt_word, read when the solve starts.
 __device__ __forceinline__ void finish_solve(const SolveArgs& A, const double* x, bool ok,
-                                             const float* pose_src) {
+                                             int halt_word, const float* pose_src) {
     const int n = A.n;
-    // a halted call takes no more steps: like a rejected step, but not
-    // reported as one
-    const bool halted = A.halt && *A.halt != 0;
+    const bool halted = halt_word != 0;
     if (threadIdx.x == 0) {
         A.flags[0] = ok && !halted ? 0 : 1;
         if (!ok && !halted) A.flags[1] = 1;
@@ -819,6 +833,7 @@ __device__ __forceinline__ void solve_panel_body(const SolveArgs& A, double* sm,
     double* L = sm;                   // packed lower [S; b^T], padded
     double* piv = sm + tri(n8 + 1);   // [n8] pivots d_j
     double* xs = piv + n8;            // [n8] the solution
+    const int halt_word = solve_halt_word(A);
     if (tid < (A.t1 - A.t0) * 7) pose0[tid] = A.poses[A.t0 * 7 + tid];
     // rows of [S; b^T] with the padding (identity rows, zeros elsewhere):
     // wave w takes rows w, w + 4, .., lanes the columns lane, lane + 64; the
@@ -998,7 +1013,7 @@ __device__ __forceinline__ void solve_panel_body(const SolveArgs& A, double* sm,
         if (lane + 64 < n8) xs[lane + 64] = acc1;
     }
     __syncthreads();
-    finish_solve(A, xs, ok, pose0);
+    finish_solve(A, xs, ok, halt_word, pose0);
 }
 
 __global__ __launch_bounds__(256) void k_ba_solve_panel(SolveArgs A) {
@@ -1060,7 +1075,6 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
     const int n = A.n, n8 = pad_panel(n), tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hb = n8 / 2;                    // block rows 0..hb (hb: b^T)
     const int nblk = hb * (hb + 1) / 2 + hb;  // lower 2 x 2 blocks
-    if (tid < (A.t1 - A.t0) * 7) pose0[tid] = A.poses[A.t0 * 7 + tid];
     {
         constexpr int kPairs = kSmallLfRows * kSmallLfLd / 2;
 #pragma unroll
@@ -1069,8 +1083,9 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
                 reinterpret_cast<double2*>(&Lf[0][0])[tid + 256 * u] = make_double2(0.0, 0.0);
     }
     // this thread's blocks: (i0, k0) of slot s, and their four entries
+    // (every slot's indices first, then the loads: the index arithmetic
+    // carries waits of its own that would otherwise fall between the loads)
     int bi0[kSmallSlots], bk0[kSmallSlots];
-    double a[kSmallSlots][4];
 #pragma unroll
     for (int s = 0; s < kSmallSlots; s++) {
         const int b = tid + 256 * s;
@@ -1082,15 +1097,26 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
         const bool live = b < nblk;
         bi0[s] = live ? 2 * bi : -2;  // -2: no block (never in a panel's rows)
         bk0[s] = live ? 2 * bk : -2;
+    }
+    const int halt_word = solve_halt_word(A);
+    // this thread's word of the poses t0..t1-1 (clamped, unconditional: the
+    // load goes out with the system's and is waited for only at its store)
+    const int np7 = (A.t1 - A.t0) * 7;
+    const float pose_word = A.poses[np7 > 0 ? A.t0 * 7 + min(tid, np7 - 1) : 0];
+    double a[kSmallSlots][4];
+#pragma unroll
+    for (int s = 0; s < kSmallSlots; s++) {
+        const bool live = bi0[s] >= 0;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int i = 2 * bi + (e >> 1), k = 2 * bk + (e & 1);
+            const int i = bi0[s] + (e >> 1), k = bk0[s] + (e & 1);
             double x = i == k ? 1.0 : 0.0;
             if (live && k < n && i < n && k <= i) x = A.S_dbg[(size_t)i * n + k];
             if (live && k < n && i == n8) x = A.b_dbg[k];
             a[s][e] = x;
         }
     }
+    if (tid < np7) pose0[tid] = pose_word;
     bool ok = true;
     for (int c0 = 0; c0 < n8; c0 += kPW) {  // uniform
         const int r0 = c0 + kPW;
@@ -1187,7 +1213,7 @@ __device__ __forceinline__ void solve_small_body(const SolveArgs& A, SmallLds& s
         if (lane < n8) xs[lane] = acc;
     }
     __syncthreads();
-    finish_solve(A, xs, ok, pose0);
+    finish_solve(A, xs, ok, halt_word, pose0);
 }
 
 __global__ __launch_bounds__(256) void k_ba_solve_small(SolveArgs A) {
@@ -1385,11 +1411,12 @@ __global__ __launch_bounds__(kFinishWG) void k_chol_finish(SolveArgs A) {
     const int n = A.n;
     double* b = smem;
     const bool ok = A.flags[2] == 0;
+    const int halt_word = solve_halt_word(A);
     for (int t = threadIdx.x; t < n; t += blockDim.x) b[t] = A.S[(size_t)n * n + t];  // z
     __syncthreads();
     if (ok) back_solve_blocked(A.S, b, n);
     __syncthreads();
-    finish_solve(A, b, ok, A.poses + 7 * A.t0);
+    finish_solve(A, b, ok, halt_word, A.poses + 7 * A.t0);
 }
 
 int solve_blocked(const SolveArgs& A, hipStream_t stream) {
