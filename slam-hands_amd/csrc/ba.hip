@@ -2297,16 +2297,17 @@ struct FzAsmArgs {
     int* flags;  // with ready: flags[5] = flags[4] for the solve of the launch after
 };
 
-// Entry (row, col) of a keyframe's Z, summed over the chunks: Z is symmetric
-// and only its upper tiles are kept, in the MFMA's lane order (result
-// register r of lane l holds entry (4 r + l / 16, l % 16) of a 16 x 16 tile;
-// the A operand of lane l is (l % 16, l / 16), the B operand (l / 16, l % 16)).
-__device__ __forceinline__ double fz_z(const FzAsmArgs& A, int kc, int row, int col) {
+// Chunk 0's partial of entry (row, col) of a keyframe's Z (the other chunks'
+// follow at stride kFzMaxNT * 256): Z is symmetric and only its upper tiles
+// are kept, in the MFMA's lane order (result register r of lane l holds entry
+// (4 r + l / 16, l % 16) of a 16 x 16 tile; the A operand of lane l is
+// (l % 16, l / 16), the B operand (l / 16, l % 16)).
+__device__ __forceinline__ const double* fz_z(const FzAsmArgs& A, int kc, int row, int col) {
     const int lo = min(row, col), hi = max(row, col);
     const int th = hi >> 4, tl = lo >> 4;
     const int i = lo & 15, j = hi & 15;
     const size_t idx = (size_t)(th * (th + 1) / 2 + tl) * 256 + ((i & 3) * 16 + j) * 4 + (i >> 2);
-    return sum_strided<32>(A.spart + (size_t)kc * A.nch * kFzMaxNT * 256 + idx, kFzMaxNT * 256, A.nch);
+    return A.spart + (size_t)kc * A.nch * kFzMaxNT * 256 + idx;
 }
 
 // One workgroup per 6x6 block (a, b) of S (P*P) and per 6-entry segment of b
@@ -2323,19 +2324,18 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
     __shared__ double ah[kFzMaxDst][36];     // Adj Hjj
     __shared__ double et[kFzMaxDst][kNT];    // Hii, Hij, Hjj, vi, vj
     __shared__ double red[kAsmSlices][36];
-    __shared__ int rec[kFzRecInts];
+    __shared__ __attribute__((aligned(16))) int rec[kFzRecInts];
     const int g = blockIdx.x, tid = threadIdx.x;
     const int sl = tid / 36, ent = tid - sl * 36;
     const int P = A.P, n = A.n;
-    if (A.ready && g == 0 && tid == 0) {
-        *A.ready = 0;
-        A.flags[5] = A.flags[4];  // a wait of the last launch gave up: no more steps
-    }
     const bool isS = g < P * P;
     const bool act = sl < kAsmSlices && (isS || ent < 6);
     const int r = ent / 6, c = ent - (ent / 6) * 6;
-    // the block's record in one round of loads
-    for (int t = tid; t < kFzRecInts; t += 256) rec[t] = A.rec[(size_t)g * kFzRecInts + t];
+    // the block's record in one round of 16-byte loads
+    static_assert(kFzRecInts % 4 == 0 && kFzRecInts / 4 <= 256, "one int4 of the record a thread");
+    if (tid < kFzRecInts / 4)
+        reinterpret_cast<int4*>(rec)[tid] =
+            reinterpret_cast<const int4*>(A.rec + (size_t)g * kFzRecInts)[tid];
     __syncthreads();
     const int nq = rec[0], nd = rec[1];
     const int* redge = rec + kFzRecEdges;  // (edge, ii, jj)
@@ -2355,14 +2355,15 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
 #pragma unroll
         for (int m = 0; m < 6; m++) adj[le][m * 6 + cc] = y[m];
     }
-    // the Schur items (thread-private; their loads overlap the above)
+    // the Schur items (thread-private)
     double s = 0.0;
     if (act) {
         for (int q = sl; q < nq; q += kAsmSlices) {
             const int* rc = rcode + 5 * q;
             if (code_type(rc[0]) != 1) continue;
-            s -= isS ? fz_z(A, rc[1], 6 * rc[2] + r, 6 * rc[3] + c)
-                     : fz_z(A, rc[1], 6 * rc[2] + ent, rc[4]);
+            s -= sum_strided<32>(isS ? fz_z(A, rc[1], 6 * rc[2] + r, 6 * rc[3] + c)
+                                     : fz_z(A, rc[1], 6 * rc[2] + ent, rc[4]),
+                                 kFzMaxNT * 256, A.nch);
         }
     }
     __syncthreads();
@@ -2427,6 +2428,10 @@ __global__ __launch_bounds__(256) void k_ba_fz_assemble(FzAsmArgs A) {
 #pragma unroll
         for (int k = 1; k < kAsmSlices; k++) t += red[k][tid];
         A.b[(g - P * P) * 6 + tid] = t;
+    }
+    if (A.ready && g == 0 && tid == 0) {  // (last: its load is waited for at once)
+        *A.ready = 0;
+        A.flags[5] = A.flags[4];  // a wait of the last launch gave up: no more steps
     }
 }
 
