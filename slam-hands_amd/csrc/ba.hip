@@ -1540,17 +1540,25 @@ struct FzArgs {
     double* hpart;  // [M][nch][27]
     double* spart;  // [N_kf][nch][kFzMaxNT][256] Z tiles in MFMA lane order
     int HW, W, nch, t0, t1;
+    int npose;     // poses the call's edges and free range refer to (0..npose-1)
     int spin_max;  // polls before a waiting workgroup gives up
 };
+
+// Calls of at most this many poses keep all of them in LDS for the
+// linearization at the poses after an overlapped step (fixed poses staged
+// before the wait, the free ones formed after it), so that no pose is read
+// from memory after the flag.
+constexpr int kFzLdsPoses = 64;
+static_assert(kFzLdsPoses >= kPanelPoses, "the free poses fit the LDS pose array");
 
 __device__ __forceinline__ float ld_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Relative pose of edge (ix, jx) at the current poses, at the poses after
-// this launch's step (poses t0..t1-1 from pn, which the workgroup formed; the
-// others do not move), or (prev) at the poses of the last step's
-// linearization: only t0..t1-1 moved.
+// this launch's step (pn, which the workgroup formed: every pose when npose
+// <= kFzLdsPoses, else poses t0..t1-1, the others not moving), or (prev) at
+// the poses of the last step's linearization: only t0..t1-1 moved.
 __device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int jx, double* tij,
                                        double* qij, const float* pn = nullptr) {
     if (ix == jx) {
@@ -1558,7 +1566,10 @@ __device__ __forceinline__ void fz_rel(const FzArgs& F, bool prev, int ix, int j
         return;
     }
     double ti[3], qi[4], tj[3], qj[4];
-    if (pn) {
+    if (pn && F.npose <= kFzLdsPoses) {
+        load_pose(pn, ix, ti, qi);
+        load_pose(pn, jx, tj, qj);
+    } else if (pn) {
         const bool si = ix >= F.t0 && ix < F.t1, sj = jx >= F.t0 && jx < F.t1;
         load_pose(si ? pn : F.poses, si ? ix - F.t0 : ix, ti, qi);
         load_pose(sj ? pn : F.poses, sj ? jx - F.t0 : jx, tj, qj);
@@ -1617,7 +1628,9 @@ struct FzLds {
     double qs[kFzPx];
     double dxr[6 * kFzMaxSlots];  // the last step's dx, by slot row
     int spose[kFzMaxSlots];       // the pose of each slot
-    float pnew[kPanelPoses * 7];  // poses t0..t1-1 after the overlapped launch's step
+    // the poses after the overlapped launch's step: all of them when npose <=
+    // kFzLdsPoses, else poses t0..t1-1 (from index 0)
+    float pnew[kFzLdsPoses * 7];
     int wait_state;
 };
 
@@ -2092,6 +2105,12 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             if (E.slot >= 0) L.spose[E.slot] = E.jx;
         }
         if (ri && tid == 0) L.spose[0] = K.kf;
+        // the poses that do not move, for the linearization after the wait
+        // (the free ones' entries are replaced then; the pass's barriers
+        // order these writes)
+        const bool lds_all = kLin && F.npose <= kFzLdsPoses;  // uniform
+        if (lds_all)
+            for (int i = tid; i < F.npose * 7; i += kLinWG) L.pnew[i] = F.poses[i];
         fz_pass<true>(F, K, L, chunk, kpx, vpx, dsp, eta_px, cache);
         if (wait.ready) {
             if (tid == 0) {
@@ -2139,15 +2158,20 @@ __device__ __forceinline__ void fz_body(const FzArgs& F, FzLds& L, int chunk, in
             for (int k = tid; k < F.t1 - F.t0; k += kLinWG) {
                 const float* p7 = F.poses_prev + k * 7;
                 float d6[6], out[7];
+                // (loaded unconditionally, beside the status: a load under
+                // `ok` would wait for the status load first)
 #pragma unroll
-                for (int m = 0; m < 6; m++) d6[m] = ok ? ld_coherent(F.dx + k * 6 + m) : 0.0f;
+                for (int m = 0; m < 6; m++) d6[m] = ld_coherent(F.dx + k * 6 + m);
+#pragma unroll
+                for (int m = 0; m < 6; m++) d6[m] = ok ? d6[m] : 0.0f;
                 if (ok)
                     step_pose(p7, d6, out);
                 else
 #pragma unroll
                     for (int m = 0; m < 7; m++) out[m] = p7[m];
+                float* dst = L.pnew + (lds_all ? (F.t0 + k) * 7 : k * 7);
 #pragma unroll
-                for (int m = 0; m < 7; m++) L.pnew[k * 7 + m] = out[m];
+                for (int m = 0; m < 7; m++) dst[m] = out[m];
             }
             pn = L.pnew;
         }
@@ -2445,6 +2469,7 @@ struct BaState {
     int key_t0 = 0, key_t1 = 0, key_motion = 0, key_HW = 0;
     // plan sizes
     int M = 0, P = 0, n = 0, N_kf = 0, N_E = 0, N_pu = 0, n_blk = 0, nch = 1;
+    int npose = 0;  // max(the edges' largest frame index + 1, t1)
     std::vector<int> host;  // packed plan
     size_t off[kPlanParts] = {0};
     DevBuf plan_dev, hpart, etot, stot, E, Q, Wv, S, S_dbg, b_dbg, dx_dbg, dx, flags;
@@ -2586,6 +2611,7 @@ int build_plan(BaState* s, const int* ii, const int* jj, int M, int t0, int t1, 
         if (ii[e] < 0 || jj[e] < 0) return fail(SLK_E_ARG, "ba_iterate: negative frame index");
         maxf = std::max(maxf, std::max(ii[e], jj[e]));
     }
+    s->npose = std::max(maxf + 1, t1);
     std::vector<int> kf_compact(maxf + 1, -1), kf_list;
     for (int e = 0; e < M; e++) kf_compact[ii[e]] = 0;
     for (int k = 0; k <= maxf; k++)
@@ -2923,6 +2949,7 @@ int iterate_fused(slk_ctx* ctx, BaState* s, const IterArgs& I, int iters, hipStr
     F.nch = s->nch;
     F.t0 = I.t0;
     F.t1 = I.t1;
+    F.npose = s->npose;
     FzAsmArgs G;
     G.rec = base + s->fz_off[2];
     G.hpart = s->hpart.as<double>();
