@@ -71,6 +71,7 @@ constexpr int kBufWord3 = 0x00020000;
 // discarded by the range check
 constexpr int kBufDiscard = 0x7FFFFFF0;
 constexpr int kTStride = 68;   // floats per transposed-tile row (64 sources + 4 pad)
+constexpr int kTPad = 3;       // rows of the transposed tile before and after its targets
 constexpr int kMaxSlots = 2 * kMaxEdgesPerLaunch;
 
 struct Geom {
@@ -596,13 +597,22 @@ struct alignas(16) SplitSmem {
             unsigned short A[kStages][2][kSrcTile * kChunk];
             unsigned short B[kStages][2][kTgtTile * kChunk];
         } st;
-        float T[kTgtTile][kTStride];  // [target][source] of one 64-source half
+        // [kTPad + target][source] of one 64-source half; the kTPad rows on
+        // either side are never written and only read for cells outside the
+        // grid, which the lookup never reads
+        float T[kTgtTile + 2 * kTPad][kTStride];
     } u;
     int org[kSrcTile][2];     // floor_clamped(x), floor_clamped(y) of each source
     float crd[2][kSrcTile];   // x, y coordinates of the tile's sources
     int pix[kSrcTile];        // pixel of each source
     float ssc[kSrcTile];      // alpha times each source's inverse split scale
     float tsc[kTgtTile];      // each target's inverse split scale
+    // the next tile's list entry, box record and order pixels (pf_pix[i] =
+    // ord[min(p0 + i, HW - 1)]), put here by direct-to-LDS loads while the
+    // current tile's chunks stream
+    int pf_r;
+    int pf_rec[kBoxInts];
+    int pf_pix[kSrcTile];
 };
 
 // one 32x32x16 MFMA of the split mode's operand type
@@ -673,19 +683,59 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int xcd = blockIdx.x & 7;
     const int lo = (int)((long long)cnt * xcd / 8), hi = (int)((long long)cnt * (xcd + 1) / 8);
     // The next tile's index is taken at the start of a tile and published in
-    // LDS after the chunk loop (whose last wait covers the atomic's return).
+    // LDS after the chunk loop's first wait (which covers the atomic's return).
     int* const counter = ctr + kCtrXcd + xcd;
+    // the edge of tile idx: the last lane whose prefix is <= idx (edges
+    // with no marked tile share their successor's prefix)
+    auto edge_of = [&](int idx) {
+        const bool before_idx = (int)(threadIdx.x & 63) < nedges && pre <= idx;
+        return (int)__builtin_popcountll(__ballot(before_idx)) - 1;
+    };
+    // A tile's metadata into sm.pf_*, in two dependent steps: its list entry
+    // (thread 0), then its box record (lanes 0..15 of wave 0) and the order
+    // pixels of its sources (waves 0 and 1). Each step's data is in LDS after
+    // a vmcnt wait of the issuing waves and a barrier.
+    auto pf_list = [&](int idx) {
+        const int e = edge_of(idx);
+        if (threadIdx.x == 0)
+            dma_x1(list + (size_t)e * tpe + (idx - __builtin_amdgcn_readlane(pre, e)),
+                   lds_addr(&sm.pf_r));
+    };
+    auto pf_rest = [&](int idx) {
+        const int e = edge_of(idx);
+        const int mt = __builtin_amdgcn_readfirstlane(sm.pf_r) / ntiles;
+        const int* ord = order + (size_t)e * ostride;
+        const int t = threadIdx.x;
+        if (t < kBoxInts) dma_x1(ord + g.HW + mt * kBoxInts + t, lds_addr(&sm.pf_rec[0]));
+        if (t < kSrcTile)
+            dma_x1(ord + std::min(mt * kSrcTile + t, g.HW - 1), lds_addr(&sm.pf_pix[t & ~63]));
+    };
+    auto pf_sync = [&](int idx) {  // both steps, waiting for each
+        pf_list(idx);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        lds_barrier();
+        pf_rest(idx);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        lds_barrier();
+    };
     if (threadIdx.x == 0) next_tile = lo + atomicAdd(counter, 1);
     lds_barrier();
+    {
+        const int idx0 = __builtin_amdgcn_readfirstlane(next_tile);
+        if (idx0 < hi) pf_sync(idx0);  // uniform
+    }
+    // With four chunks or more, the next tile's metadata is fetched during
+    // the chunk loop (its list entry after the barrier of step 1, the rest
+    // after that of step 2, each waited for by the next step's vmcnt wait);
+    // otherwise after the tile's extraction.
+    const bool pf_loop = g.C / kChunk >= 4;
     for (int idx = __builtin_amdgcn_readfirstlane(next_tile); idx < hi;
          idx = __builtin_amdgcn_readfirstlane(next_tile)) {  // uniform
     int taken;  // thread 0 only
     if (threadIdx.x == 0) taken = atomicAdd(counter, 1);
-    // the edge of tile idx: the last lane whose prefix is <= idx (edges
-    // with no marked tile share their successor's prefix)
-    const bool before_idx = (int)(threadIdx.x & 63) < nedges && pre <= idx;
-    const int e = __builtin_popcountll(__ballot(before_idx)) - 1;
-    const int r = list[(size_t)e * tpe + (idx - __builtin_amdgcn_readlane(pre, e))];
+    int nidx = hi;  // the next tile, once read (uniform)
+    const int e = edge_of(idx);
+    const int r = __builtin_amdgcn_readfirstlane(sm.pf_r);
     const int mt = r / ntiles, vt = r - mt * ntiles;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -698,12 +748,11 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     // the rows' inverse split scales (powers of two), after the planes
     const float* isa = reinterpret_cast<const float*>(fa + 2 * plane);
     const float* isb = reinterpret_cast<const float*>(fb + 2 * plane);
-    const int* ord = order + (size_t)e * ostride;
     // the source tile's target boxes: virtual rows cum[l] .. cum[l + 1] - 1 are
     // level l's box (bh x bw cells from row ya, column xa), row-major
     int bya[kMaxLevels], bxa[kMaxLevels], bwd[kMaxLevels], cum[kMaxLevels + 1];
     {
-        const int* rec = ord + HW + mt * kBoxInts;
+        const int* rec = sm.pf_rec;
         cum[0] = 0;
 #pragma unroll
         for (int l = 0; l < kMaxLevels; l++) {
@@ -742,13 +791,12 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
     const int hh = ((tid & 1) ^ (((hr >> 2) ^ (hr >> 3)) & 1)) * 8;  // rows hr, 128 + hr alike
     // pixel of source row hr (clamped: the DMA below must stay in the frame
     // whatever the order buffer holds)
-    const int pa = std::min((unsigned)ord[std::min(p0 + hr, HW - 1)], (unsigned)(HW - 1));
+    const int pa = std::min((unsigned)sm.pf_pix[hr], (unsigned)(HW - 1));
     if (!(tid & 1)) sm.pix[hr] = pa;  // read after the chunk loop's barriers
     // wave (half, comp) stages coordinate comp (x, y) of sources half * 64 ..
     // + 63: gathered by their pixels (clamped like pa)
     const float* cpt = coords + ((size_t)e * 2 + (wave >> 1)) * HW +
-                       std::min((unsigned)ord[std::min(p0 + (wave & 1) * 64 + lane, HW - 1)],
-                                (unsigned)(HW - 1));
+                       std::min((unsigned)sm.pf_pix[(wave & 1) * 64 + lane], (unsigned)(HW - 1));
     const int tr0 = trow(v0 + hr), tr1 = trow(v0 + 128 + hr);
     // the inverse scales of source row hr and target rows hr, 128 + hr: loaded
     // ahead of the chunk loop's staging (whose waits count loads in issue
@@ -862,6 +910,15 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_barrier();
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            // the next tile: its index after every wave has read this one's
+            // (step 0), its metadata loads older than the chunk loads they
+            // are waited on with (steps 1 and 2)
+            if (k == 0 && tid == 0) next_tile = lo + taken;
+            if (pf_loop && k == 1) {  // uniform
+                nidx = __builtin_amdgcn_readfirstlane(next_tile);
+                if (nidx < hi) pf_list(nidx);
+            }
+            if (pf_loop && k == 2 && nidx < hi) pf_rest(nidx);
             if (k + 2 < nk) issue(k + 2, (k + 2) % kStages);
             compute(k % kStages);
         }
@@ -880,7 +937,6 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         chunk_loop(bool_c<true>{}, bool_c<true>{});
     }
     __builtin_amdgcn_s_setprio(2);
-    if (tid == 0) next_tile = lo + taken;  // read after the end-of-tile barrier
     if (tid < kSrcTile) {
         const bool in = p0 + tid < HW;
         sm.org[tid][0] = in ? floor_clamped(sm.crd[0][tid]) : -(1 << 20);  // matches no cell
@@ -935,7 +991,7 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
             for (int gq = 0; gq < 4; gq++) {
                 const int t = wn * 128 + tb * 32 + orow;
                 const int s = wm * 32 + gq * 8 + khalf * 4;
-                *reinterpret_cast<float4*>(&sm.u.T[t][s]) = make_float4(
+                *reinterpret_cast<float4*>(&sm.u.T[kTPad + t][s]) = make_float4(
                     acc[sb][tb][4 * gq] * tsv[tb], acc[sb][tb][4 * gq + 1] * tsv[tb],
                     acc[sb][tb][4 * gq + 2] * tsv[tb], acc[sb][tb][4 * gq + 3] * tsv[tb]);
             }
@@ -945,57 +1001,71 @@ __global__ __launch_bounds__(256, 2) void k_corr_split_win(
         const int fx = sm.org[lsrc][0], fy = sm.org[lsrc][1];
         const float fs = sm.ssc[lsrc];
         const bool pin = p0 + lsrc < HW;
-        const float* Tcol = &sm.u.T[0][s];
+        // column s of T at target row 0 (rows -kTPad .. kTgtTile + kTPad - 1 exist)
+        const float* Tcol = &sm.u.T[kTPad][s];
         // byte offset of cell 0 of row 0 of level 0 of this source in the slot
         const int woff = (int)win_index(0, 0, 0, HW, sm.pix[lsrc]) * 4;
+        // the lane's pieces: window rows 2 rd + cyq (rounds rd = 0..3), cells
+        // cx0 .. cx0 + 3 of each
+        const int cyq = qq >> 1, cx0 = (qq & 1) * 4;
 #pragma unroll
         for (int l = 0; l < kMaxLevels; l++) {
             if (!lin[l]) continue;  // level not in this tile
-            const int wl = g.w[l], hl = g.h[l], bw = bwd[l];
-            const int ox = (fx >> l) - 3, oy = (fy >> l) - 3;
+            const int hl = g.h[l], bw = bwd[l];
+            const int x0 = (fx >> l) - 3 + cx0, y0 = (fy >> l) - 3 + cyq;
+            // the piece's in-grid cells are ia..ib (the same in every round);
+            // tile row of its first cell in round 0, 2 bw further each round
+            // (every in-grid cell of the tile's windows lies in the box; the
+            // value is meaningless, and unused, for rows outside the grid)
+            const int ia = std::max(0, -x0), ib = std::min(3, g.w[l] - 1 - x0);
+            const bool xok = pin && ia <= ib;
+            const unsigned t00 = (unsigned)(cum[l] - v0) + (unsigned)(y0 - bya[l]) * (unsigned)bw +
+                                 (unsigned)(x0 - bxa[l]);
+            int tl[4];
+            bool has[4], full[4];
+            float v[4][4];
+            // every round's reads go out before the first store: a piece with
+            // an in-grid cell in the tile has tl in [-kTPad, kTgtTile - 1], so
+            // its four rows lie in T; another reads row 0
 #pragma unroll
             for (int rd = 0; rd < 4; rd++) {
-                const int f = 4 * rd + qq, cy = f >> 1, cx0 = (f & 1) * 4;
-                const int y = oy + cy, x0 = ox + cx0;
-                const bool rowok = pin && (unsigned)y < (unsigned)hl;
-                // the piece's in-grid cells are ia..ib; tile row of its first
-                // cell (every in-grid cell of the tile's windows lies in the
-                // box; the value is meaningless, and unused, for rows outside
-                // the grid)
-                const int ia = std::max(0, -x0), ib = std::min(3, wl - 1 - x0);
-                const int tl0 = (int)((unsigned)(cum[l] - v0) +
-                                      (unsigned)(y - bya[l]) * (unsigned)bw +
-                                      (unsigned)(x0 - bxa[l]));
-                const int ta = tl0 + ia, tb = tl0 + ib;
+                tl[rd] = (int)(t00 + (unsigned)(2 * rd * bw));
+                const int ta = tl[rd] + ia, tb = tl[rd] + ib;
                 // some in-grid cell in this tile; all of them
-                const bool has = rowok && ia <= ib && ta < kTgtTile && tb >= 0;
-                const bool full = has && ta >= 0 && tb < kTgtTile;
-                if (!__ballot(has)) continue;  // uniform: no piece of this round here
-                float v[4];
+                has[rd] = xok && (unsigned)(y0 + 2 * rd) < (unsigned)hl && ta < kTgtTile && tb >= 0;
+                full[rd] = has[rd] && ta >= 0 && tb < kTgtTile;
+                const float* tp = Tcol + (has[rd] ? tl[rd] : 0) * kTStride;
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    v[i] = fs * Tcol[std::min(std::max(tl0 + i, 0), kTgtTile - 1) * kTStride];
-                const int off = woff + ((l * 8 + cy) * HW * 8 + cx0) * 4;
-                const u32x4_t pk = {__builtin_bit_cast(unsigned, v[0]),
-                                    __builtin_bit_cast(unsigned, v[1]),
-                                    __builtin_bit_cast(unsigned, v[2]),
-                                    __builtin_bit_cast(unsigned, v[3])};
-                __builtin_amdgcn_raw_buffer_store_b128(pk, wrs, full ? off : kBufDiscard, 0, 0);
-                const bool split = has && !full;
+                for (int i = 0; i < 4; i++) v[rd][i] = tp[i * kTStride];
+            }
+#pragma unroll
+            for (int rd = 0; rd < 4; rd++) {
+                const int off = woff + ((l * 8 + cyq + 2 * rd) * HW * 8 + cx0) * 4;
+                const u32x4_t pk = {__builtin_bit_cast(unsigned, fs * v[rd][0]),
+                                    __builtin_bit_cast(unsigned, fs * v[rd][1]),
+                                    __builtin_bit_cast(unsigned, fs * v[rd][2]),
+                                    __builtin_bit_cast(unsigned, fs * v[rd][3])};
+                __builtin_amdgcn_raw_buffer_store_b128(pk, wrs, full[rd] ? off : kBufDiscard, 0,
+                                                       0);
+                const bool split = has[rd] && !full[rd];
                 if (__ballot(split)) {  // uniform, rare: a piece cut by the tile's ends
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const bool val = split && i >= ia && i <= ib &&
-                                         (unsigned)(tl0 + i) < (unsigned)kTgtTile;
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[i]),
-                                                              wrs, val ? off + 4 * i : kBufDiscard,
-                                                              0, 0);
+                                         (unsigned)(tl[rd] + i) < (unsigned)kTgtTile;
+                        __builtin_amdgcn_raw_buffer_store_b32(pk[i], wrs,
+                                                              val ? off + 4 * i : kBufDiscard, 0,
+                                                              0);
                     }
                 }
             }
         }
     }
     lds_barrier();  // T is free again, next_tile is visible
+    if (!pf_loop) {
+        const int n = __builtin_amdgcn_readfirstlane(next_tile);
+        if (n < hi) pf_sync(n);  // uniform
+    }
     }
 }
 
