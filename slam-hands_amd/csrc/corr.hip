@@ -665,12 +665,26 @@ __global__ __launch_bounds__(256) void k_corr_lookup_win(LevelIn lv, const float
         return;
     }
     const int ix = win_origin(cx, l), iy = win_origin(cy, l);
+    // The window rows through a buffer resource over this edge and level: a
+    // half row (4 cells, 16 bytes) with no cell in the grid, which the
+    // correlation kernel never writes, is read at an offset past the range
+    // and comes back as zeros without a memory access (22% of the pieces at
+    // a +-8 pixel flow on 48 x 64 maps).
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(wb + win_index(e, l, 0, HW1, 0)), 0, kWinCells * HW1 * (int)sizeof(float),
+        kBufWord3);
+    const bool hx0 = ix + 3 >= 0 && ix < W2, hx1 = ix + 7 >= 0 && ix + 4 < W2;
     float win[8][8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const bool vy = (unsigned)(iy + j) < (unsigned)H2;
-        const float4* src = reinterpret_cast<const float4*>(wb + win_index(e, l, j * 8, HW1, p));
-        const float4 lo4 = src[0], hi4 = src[1];
+        const int off = (int)win_index(0, 0, j * 8, HW1, p) * (int)sizeof(float);
+        // (whole-vector bit casts: this compiler's __builtin_bit_cast of a
+        // subscripted vector element reads element 0 whatever the index)
+        const float4 lo4 = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(rs, vy && hx0 ? off : kBufDiscard, 0, 0));
+        const float4 hi4 = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(rs, vy && hx1 ? off + 16 : kBufDiscard, 0, 0));
         const float cell[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {

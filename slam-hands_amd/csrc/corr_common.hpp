@@ -13,6 +13,13 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kMaxEdgesPerLaunch = 64;
+
+// word 3 of a raw buffer resource on gfx9-family parts (32-bit data format,
+// no swizzle; range checking against num_records)
+constexpr int kBufWord3 = 0x00020000;
+// an offset past any buffer the correlation kernels build a resource for: a
+// store there is discarded and a load returns zeros, without a memory access
+constexpr int kBufDiscard = 0x7FFFFFF0;
 constexpr int kWinCells = 64;  // 8x8 window cells per level
 
 // Lookup windows of a launch are stored row-major per window row,

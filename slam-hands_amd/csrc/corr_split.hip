@@ -64,12 +64,6 @@ constexpr int kSrcTile = 128;  // sources per workgroup
 constexpr int kTgtTile = 256;  // targets per workgroup
 constexpr int kChunk = 16;     // channels per LDS stage
 constexpr int kStages = 3;     // LDS stages: chunk k+2 streams in while chunk k is used
-// word 3 of a raw buffer resource on gfx9-family parts (32-bit data format,
-// no swizzle; range checking against num_records)
-constexpr int kBufWord3 = 0x00020000;
-// an offset past any buffer this file builds a resource for: such a store is
-// discarded by the range check
-constexpr int kBufDiscard = 0x7FFFFFF0;
 constexpr int kTStride = 68;   // floats per transposed-tile row (64 sources + 4 pad)
 constexpr int kTPad = 3;       // rows of the transposed tile before and after its targets
 constexpr int kMaxSlots = 2 * kMaxEdgesPerLaunch;
