@@ -40,6 +40,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTH = 8;    // output rows per workgroup tile
 constexpr int kTW = 32;   // output columns per workgroup tile (one MFMA column block)
@@ -232,21 +233,24 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
     }
 }
 
-// One conv tile: kCoT output channels x (kTH x kTW) pixels of one image. Four
-// waves: wave (wm, wn) takes 64 channels (two 32-row MFMA blocks) of image
-// rows wn*4 .. wn*4+3 of the tile (four 32-pixel column blocks). Per input
-// chunk, the (kTH + KS - 1) x (kTW + KS - 1) patch of 16 channels is staged
-// in LDS (double-buffered: the next chunk's global loads are in flight during
-// the current chunk's MFMAs); the weight fragments of all taps of a chunk are
-// read from global memory (L2-resident) into registers ahead of the taps.
-template <int KS, int EPI>
-__global__ __launch_bounds__(256, KS == 3 ? 2 : 1) void k_conv(ConvArgs a) {
-    constexpr int P = KS / 2;
+// The flow encoder's 7x7 stem (4 input channels) with its taps packed into
+// K: K step ks covers taps 4 ks .. 4 ks + 3 with their 4 channels (k =
+// 4 (t - 4 ks) + c), 13 steps for the 49 taps (taps 49..51 have zero
+// weights), where a chunked K would take 49 steps of 16 channels, 12 of them
+// zero. One conv tile: kCoT output channels x (kTH x kTW) pixels of one image,
+// four waves, wave (wm, wn) taking 64 channels (two 32-row MFMA blocks) of
+// image rows wn*4 .. wn*4+3 (four 32-pixel column blocks); the patch holds
+// each pixel's 4 channels (8 bytes), and lane (l32, lhi) reads two patch
+// pixels per K step, those of
+// taps 4 ks + 2 lhi and 4 ks + 2 lhi + 1. Weights [13][co_tot][16], read
+// from global memory (L2-resident) one K step at a time.
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
+    constexpr int KS = 7, P = 3, KSTEPS = 13;
     constexpr int PH = kTH + KS - 1, PW = kTW + KS - 1;
-    constexpr int UNITS = PH * PW * 2;  // 16-byte units of a chunk's patch
+    constexpr int UNITS = PH * PW;  // 8-byte pixels of the patch
     constexpr int UPT = (UNITS + 255) / 256;
-    constexpr int TAPS = KS * KS;
-    __shared__ __attribute__((aligned(16))) _Float16 patch[2][PH * PW * 16];
+    __shared__ __attribute__((aligned(16))) _Float16 patch[UNITS * 4];
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
     const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
@@ -254,107 +258,48 @@ __global__ __launch_bounds__(256, KS == 3 ? 2 : 1) void k_conv(ConvArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, lhi = lane >> 5;
-
-    f16x8 reg[UPT];
-    auto load_chunk = [&](int c) {
-        const bool first = c < a.s0.nchunk;
-        const CkSrc& s = first ? a.s0 : a.s1;
-        const int cc = first ? c : c - a.s0.nchunk;
-        const _Float16* base = s.p + (long)n * s.nstride + (long)cc * HW * 16;
+    // channels 0..3 of chunk 0 of the input
+    const _Float16* img = a.s0.p + (long)n * a.s0.nstride;
+    f16x4 reg[UPT];
 #pragma unroll
-        for (int u = 0; u < UPT; u++) {
-            const int unit = tid + 256 * u;
-            const int pix = unit >> 1, half = unit & 1;
-            const int py = pix / PW, px = pix - (pix / PW) * PW;
-            const int y = ty0 - P + py, x = tx0 - P + px;
-            const bool ok = unit < UNITS && y >= 0 && y < a.h && x >= 0 && x < a.w;
-            f16x8 v = {};
-            if (ok) v = *reinterpret_cast<const f16x8*>(base + ((long)y * a.w + x) * 16 + half * 8);
-            reg[u] = v;
-        }
-    };
-    // A patch pixel is 32 bytes (16 channels); its two 16-byte halves are
-    // swapped when bit 3 of the pixel index is set, so that the 16 lanes of
-    // one pass of a 128-bit operand read (16 consecutive pixels, one half
-    // each) touch 64 distinct banks: unswizzled, pixels p and p + 8 share
-    // their banks.
-    auto store_chunk = [&](int buf) {
+    for (int u = 0; u < UPT; u++) {
+        const int pix = tid + 256 * u;
+        const int py = pix / PW, px = pix - (pix / PW) * PW;
+        const int y = ty0 - P + py, x = tx0 - P + px;
+        f16x4 v = {};
+        if (pix < UNITS && y >= 0 && y < a.h && x >= 0 && x < a.w)
+            v = *reinterpret_cast<const f16x4*>(img + ((long)y * a.w + x) * 16);
+        reg[u] = v;
+    }
 #pragma unroll
-        for (int u = 0; u < UPT; u++) {
-            const int unit = tid + 256 * u;
-            const int phys = unit ^ ((unit >> 4) & 1);  // (pixel, half ^ bit 3 of pixel)
-            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][phys * 8]) = reg[u];
-        }
-    };
-
+    for (int u = 0; u < UPT; u++) {
+        const int pix = tid + 256 * u;
+        if (pix < UNITS) *reinterpret_cast<f16x4*>(&patch[pix * 4]) = reg[u];
+    }
+    __syncthreads();
     f32x16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
-
-    const long tap_stride = (long)a.nchunk * a.co_tot * 16;
     const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
-    // The weight fragments of the 3x3 taps go through a ring of kRing taps
-    // in registers, loaded kRing taps ahead of their MFMAs across the chunk
-    // boundary (9 taps a chunk: a tap's ring slot is t % kRing at every
-    // chunk), which keeps the launch at two waves per SIMD; the 7x7 stem
-    // reads each tap's fragments just before its MFMAs.
-    constexpr int kRing = 3;
-    static_assert(KS != 3 || TAPS % kRing == 0, "ring slots fixed per tap");
-    f16x8 Ar[kRing][2];
-    auto wload = [&](int c, int t, int slot) {
-        const _Float16* wc = wbase + (long)c * a.co_tot * 16 + t * tap_stride;
-        Ar[slot][0] = *reinterpret_cast<const f16x8*>(wc);
-        Ar[slot][1] = *reinterpret_cast<const f16x8*>(wc + 32 * 16);
-    };
-    if constexpr (KS == 3) {
 #pragma unroll
-        for (int t = 0; t < kRing; t++) wload(0, t, t);
-    }
-    load_chunk(0);
-    store_chunk(0);
-    __syncthreads();
-    for (int c = 0; c < a.nchunk; c++) {
-        const int buf = c & 1;
-        const _Float16* wc = wbase + (long)c * a.co_tot * 16;
-        if (c + 1 < a.nchunk) load_chunk(c + 1);
-        const _Float16* pb = &patch[buf][0];
+    for (int ks = 0; ks < KSTEPS; ks++) {
+        const f16x8 a0 = *reinterpret_cast<const f16x8*>(wbase + (long)ks * a.co_tot * 16);
+        const f16x8 a1 = *reinterpret_cast<const f16x8*>(wbase + (long)ks * a.co_tot * 16 + 32 * 16);
+        // (taps past 48 have zero weights; their reads stay in the patch)
+        const int t0 = min(4 * ks + 2 * lhi, 48), t1 = min(4 * ks + 2 * lhi + 1, 48);
+        const int ky0 = t0 / KS, kx0 = t0 - ky0 * KS, ky1 = t1 / KS, kx1 = t1 - ky1 * KS;
 #pragma unroll
-        for (int t = 0; t < TAPS; t++) {
-            const int ky = t / KS, kx = t - (t / KS) * KS;
-            f16x8 a0, a1;
-            if constexpr (KS == 3) {
-                a0 = Ar[t % kRing][0];
-                a1 = Ar[t % kRing][1];
-            } else {
-                a0 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride);
-                a1 = *reinterpret_cast<const f16x8*>(wc + t * tap_stride + 32 * 16);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int prow = wn * 4 + r + ky;
-                const int pix = prow * PW + l32 + kx;
-                const f16x8 b = *reinterpret_cast<const f16x8*>(
-                    pb + (pix * 16 + ((lhi ^ ((pix >> 3) & 1)) * 8)));
-                acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0][r], 0, 0, 0);
-                acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1][r], 0, 0, 0);
-            }
-            if constexpr (KS == 3) {  // tap t + kRing, of this chunk or the next
-                const int tn = t + kRing;
-                if (tn < TAPS)
-                    wload(c, tn, t % kRing);
-                else if (c + 1 < a.nchunk)
-                    wload(c + 1, tn - TAPS, t % kRing);
-            }
+        for (int r = 0; r < 4; r++) {
+            const int prow = wn * 4 + r;
+            const f16x4 b0 = *reinterpret_cast<const f16x4*>(&patch[((prow + ky0) * PW + l32 + kx0) * 4]);
+            const f16x4 b1 = *reinterpret_cast<const f16x4*>(&patch[((prow + ky1) * PW + l32 + kx1) * 4]);
+            const f16x8 b = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0][r], 0, 0, 0);
+            acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1][r], 0, 0, 0);
         }
-        if (c + 1 < a.nchunk) store_chunk(buf ^ 1);
-        __syncthreads();
     }
-
-    // epilogue: lane (l32, lhi), register v of block (mb, r) holds output
-    // channel cot*128 + wm*64 + mb*32 + 8*(v/4) + 4*lhi + v%4 at pixel
-    // (ty0 + wn*4 + r, tx0 + l32)
     const int x = tx0 + l32;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -365,11 +310,10 @@ __global__ __launch_bounds__(256, KS == 3 ? 2 : 1) void k_conv(ConvArgs a) {
     }
 }
 
-// The 3x3 convolutions: the tile of k_conv (kCoT output channels x kTH x kTW
+// The 3x3 convolutions: the tile of k_conv7p (kCoT output channels x kTH x kTW
 // pixels, four waves, wave (wm, wn) = 64 channels x image rows wn*4..+3), with
 // both operands staged in LDS by direct-to-LDS loads, so that the four waves
-// share one copy of the weights (k_conv reads them from L2 into every wave's
-// registers). Per input chunk c: the (kTH + 2) x (kTW + 2) patch (double
+// share one copy of the weights. Per input chunk c: the (kTH + 2) x (kTW + 2) patch (double
 // buffered), and the weights of taps 0-4 (WA) and 5-8 (WB) of the tile's
 // kCoT channels, one buffer each: WB(c) and the patch of chunk c + 1 are
 // loaded after the barrier that starts chunk c, WA(c + 1) after the barrier
@@ -557,10 +501,11 @@ __global__ __launch_bounds__(384) void k_glo_fc(const float* glo, const float* W
 }
 
 // 3x3 convolutions to at most 3 output channels (delta_2, weight_2,
-// agg_eta_0) on 8 input chunks: one thread per pixel of a kTH x kTW tile, the
-// tile's (kTH + 2) x (kTW + 2) patch of each chunk staged in LDS, fp32
-// accumulation of fp16-rounded operands (weights rounded on upload, laid out
-// [o][chunk][tap][16] so each tap's 16 weights are four broadcast reads).
+// agg_eta_0) on 8 input chunks, a kTH x kTW pixel tile per workgroup: the
+// tile's (kTH + 2) x (kTW + 2) patch of each chunk staged in LDS (double
+// buffered through registers), the products on 16x16 fp16 MFMA tiles whose
+// rows past the output channels are zero, fp32 accumulation (weights rounded
+// to fp16 on upload, laid out [o][chunk][tap][16] and held in LDS).
 // mode 0: round16(conv + b) (delta, main.cu:634-635); 1: round16(sigmoid(
 // conv + b)) (weight, :641-643); 2: 0.01 * softplus(round16(conv + b)) (eta,
 // :663-665). blockIdx.y = image * nheads + head: head h reads chunks
@@ -578,58 +523,94 @@ struct SmallArgs {
 };
 __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     constexpr int PH = kTH + 2, PW = kTW + 2;
-    __shared__ __attribute__((aligned(16))) _Float16 patch[PH * PW * 16];
+    constexpr int UNITS = PH * PW * 2;  // 16-byte units of a chunk's patch
+    constexpr int UPT = (UNITS + 255) / 256;
+    __shared__ __attribute__((aligned(16))) _Float16 patch[2][PH * PW * 16];
     __shared__ __attribute__((aligned(16))) float ws[3 * 8 * 9 * 16];
     const int n = blockIdx.z, head = blockIdx.y, tile = blockIdx.x;
     const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Co = a.Co, hw = a.h * a.w;
     const float* W = a.W + head * a.wstride;
     for (int t = tid; t < Co * 8 * 9 * 16; t += 256) ws[t] = W[t];
-    const int y = ty0 + (tid >> 5), x = tx0 + (tid & 31);
-    float acc[3] = {0.0f, 0.0f, 0.0f};
     const _Float16* base = a.in + (long)n * a.in_nstride + (long)head * 8 * hw * 16;
-    for (int ch = 0; ch < 8; ch++) {
-        __syncthreads();  // the previous chunk's patch reads are done (and ws is loaded)
-        for (int u = tid; u < PH * PW * 2; u += 256) {
-            const int pix = u >> 1, half = u & 1;
+    f16x8 reg[UPT];
+    auto load_chunk = [&](int ch) {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u;
+            const int pix = unit >> 1, half = unit & 1;
             const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
             f16x8 v = {};
-            if (yy >= 0 && yy < a.h && xx >= 0 && xx < a.w)
+            if (unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w)
                 v = *reinterpret_cast<const f16x8*>(base + ((long)ch * hw + yy * a.w + xx) * 16 +
                                                     half * 8);
-            *reinterpret_cast<f16x8*>(&patch[u * 8]) = v;
+            reg[u] = v;
         }
-        __syncthreads();
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < UPT; u++) {
+            const int unit = tid + 256 * u;
+            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[u];
+        }
+    };
+    // v_mfma_f32_16x16x16_f16 with M = output channel (rows past Co zero), N =
+    // 16 consecutive pixels, K = a chunk's 16 channels: lane (c16, kg) holds
+    // A row c16, B column c16 and k = 4 kg .. 4 kg + 3 of both; accumulator
+    // register v holds channel 4 kg + v of pixel c16. Wave w takes tile rows
+    // 2w and 2w + 1, as four 16-pixel groups g (row 2w + g / 2, columns
+    // 16 (g % 2) ..).
+    const int c16 = lane & 15, kg = lane >> 4;
+    f32x4 acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) acc[g] = f32x4{};
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();  // the first patch and ws
+    for (int ch = 0; ch < 8; ch++) {
+        const int buf = ch & 1;
+        if (ch + 1 < 8) load_chunk(ch + 1);
+        f16x4 A[9];
 #pragma unroll
         for (int t = 0; t < 9; t++) {
-            const int py = (tid >> 5) + t / 3, px = (tid & 31) + t % 3;
-            const f16x8 u0 = *reinterpret_cast<const f16x8*>(&patch[(py * PW + px) * 16]);
-            const f16x8 u1 = *reinterpret_cast<const f16x8*>(&patch[(py * PW + px) * 16 + 8]);
-#pragma unroll
-            for (int o = 0; o < 3; o++) {
-                if (o >= Co) break;
-                const float* wr = ws + ((o * 8 + ch) * 9 + t) * 16;
-                float s = acc[o];
-#pragma unroll
-                for (int i = 0; i < 8; i++) s += wr[i] * (float)u0[i];
-#pragma unroll
-                for (int i = 0; i < 8; i++) s += wr[8 + i] * (float)u1[i];
-                acc[o] = s;
+            A[t] = f16x4{};
+            if (c16 < Co) {
+                const float4 w4 = *reinterpret_cast<const float4*>(&ws[((c16 * 8 + ch) * 9 + t) * 16 + 4 * kg]);
+                A[t] = f16x4{(_Float16)w4.x, (_Float16)w4.y, (_Float16)w4.z, (_Float16)w4.w};
             }
         }
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            const int ky = t / 3, kx = t - (t / 3) * 3;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int py = 2 * wave + (g >> 1) + ky, px = 16 * (g & 1) + c16 + kx;
+                const f16x4 bv = *reinterpret_cast<const f16x4*>(&patch[buf][(py * PW + px) * 16 + 4 * kg]);
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[t], bv, acc[g], 0, 0, 0);
+            }
+        }
+        if (ch + 1 < 8) store_chunk(buf ^ 1);
+        __syncthreads();
     }
-    if (y >= a.h || x >= a.w) return;
-    const int p = y * a.w + x;
+    if (kg != 0) return;  // lanes 0..15 hold channels 0..3
     const int mode = a.mode[head];
     float* out = a.out[head] + (long)n * a.out_nstride;
-    for (int o = 0; o < Co; o++) {
-        const float v = acc[o] + a.b[head * 3 + o];
-        float r;
-        if (mode == 0) r = r16(v);
-        else if (mode == 1) r = r16(sigm(v));
-        else r = 0.01f * logf(1.0f + expf(r16(v)));
-        out[(long)o * hw + p] = r;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int y = ty0 + 2 * wave + (g >> 1), x = tx0 + 16 * (g & 1) + c16;
+        if (y >= a.h || x >= a.w) continue;
+        const int p = y * a.w + x;
+#pragma unroll
+        for (int o = 0; o < 3; o++) {
+            if (o >= Co) break;
+            const float v = acc[g][o] + a.b[head * 3 + o];
+            float r;
+            if (mode == 0) r = r16(v);
+            else if (mode == 1) r = r16(sigm(v));
+            else r = 0.01f * logf(1.0f + expf(r16(v)));
+            out[(long)o * hw + p] = r;
+        }
     }
 }
 
@@ -724,6 +705,33 @@ int pack(PackedConv& pc, const UpdateState* s, std::initializer_list<int> layers
     return SLK_OK;
 }
 
+// The 7x7 stem of 4 input channels with its taps packed into K (k_conv7p):
+// [13][co_tot][16] fp16, k = 4 (t - 4 ks) + c; taps 49..51 zero.
+int pack_taps4(PackedConv& pc, const UpdateState* s, int L) {
+    const LayerShape& ls = kLayers[L];
+    constexpr int kSteps = 13;
+    if (ls.k != 7 || ls.ci != 4) return fail(SLK_E_STATE, "update: tap-packed layer shape");
+    pc.k = 7;
+    pc.Co = ls.co;
+    pc.nchunk = kSteps;
+    pc.co_tot = (ls.co + kCoT - 1) / kCoT * kCoT;
+    std::vector<_Float16> w((size_t)kSteps * pc.co_tot * 16, (_Float16)0.0f);
+    std::vector<float> b(pc.co_tot, 0.0f);
+    const std::vector<float>& src = s->hw_[L];
+    for (int o = 0; o < ls.co; o++) {
+        b[o] = s->hb_[L][o];
+        for (int c = 0; c < 4; c++)
+            for (int t = 0; t < 49; t++)
+                w[((size_t)(t / 4) * pc.co_tot + o) * 16 + 4 * (t % 4) + c] =
+                    (_Float16)src[((size_t)o * 4 + c) * 49 + t];
+    }
+    SLK_TRY(pc.wt.ensure(w.size() * sizeof(_Float16)));
+    SLK_TRY(pc.bias.ensure(b.size() * sizeof(float)));
+    SLK_HIP(hipMemcpy(pc.wt.ptr, w.data(), w.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+    SLK_HIP(hipMemcpy(pc.bias.ptr, b.data(), b.size() * sizeof(float), hipMemcpyHostToDevice));
+    return SLK_OK;
+}
+
 int upload_rounded(DevBuf& d, const std::vector<float>& v) {
     std::vector<float> r(v.size());
     for (size_t i = 0; i < v.size(); i++) r[i] = round_half_host(v[i]);
@@ -757,7 +765,7 @@ int pack_all(UpdateState* s) {
                                          " not set");
     SLK_TRY(pack(s->ce0, s, {L_CE0}));
     SLK_TRY(pack(s->ce2, s, {L_CE2}));
-    SLK_TRY(pack(s->fe0, s, {L_FE0}));
+    SLK_TRY(pack_taps4(s->fe0, s, L_FE0));
     SLK_TRY(pack(s->fe2, s, {L_FE2}));
     SLK_TRY(pack(s->gw, s, {L_W}));
     SLK_TRY(pack(s->zr, s, {L_Z, L_R}));
@@ -809,7 +817,8 @@ int launch_conv(const UpdateState* s, const PackedConv& pc, ConvArgs a, int N,
         hipLaunchKernelGGL((k_conv3<EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
                            dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((k_conv<KS, EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
+        static_assert(KS == 7, "the 7x7 stem is the only other convolution");
+        hipLaunchKernelGGL((k_conv7p<EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
                            dim3(256), 0, stream, a);
     }
     SLK_HIP(hipGetLastError());
