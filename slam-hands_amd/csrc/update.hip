@@ -242,8 +242,10 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
 // image rows wn*4 .. wn*4+3 (four 32-pixel column blocks); the patch holds
 // each pixel's 4 channels (8 bytes), and lane (l32, lhi) reads two patch
 // pixels per K step, those of
-// taps 4 ks + 2 lhi and 4 ks + 2 lhi + 1. Weights [13][co_tot][16], read
-// from global memory (L2-resident) one K step at a time.
+// taps 4 ks + 2 lhi and 4 ks + 2 lhi + 1. The tile's weights of all 13 K
+// steps ([13][co_tot][16] in memory, 52 KB) are staged in LDS by
+// direct-to-LDS loads beside the patch's loads, every 32-byte row's halves
+// swapped when bit 3 of its channel is set (as in k_conv3).
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
     constexpr int KS = 7, P = 3, KSTEPS = 13;
@@ -251,6 +253,7 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
     constexpr int UNITS = PH * PW;  // 8-byte pixels of the patch
     constexpr int UPT = (UNITS + 255) / 256;
     __shared__ __attribute__((aligned(16))) _Float16 patch[UNITS * 4];
+    __shared__ __attribute__((aligned(16))) _Float16 wsh[KSTEPS * kCoT * 16];
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
     const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
@@ -258,6 +261,16 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, lhi = lane >> 5;
+    // the weights: 16-byte unit u = 256 r + tid is physical half u & 1 of row
+    // u / 2 = (ks, co); the thread loads the logical half that lands there
+#pragma unroll
+    for (int r = 0; r < KSTEPS; r++) {
+        const int unit = r * 256 + tid, row = unit >> 1;
+        const int ks = row / kCoT, co = row - (row / kCoT) * kCoT;
+        const int half = (unit & 1) ^ ((co >> 3) & 1);
+        dma_x4(a.wt + ((long)ks * a.co_tot + cot * kCoT + co) * 16 + half * 8,
+               lds_addr(&wsh[(r * 256 + wave * 64) * 8]));
+    }
     // channels 0..3 of chunk 0 of the input
     const _Float16* img = a.s0.p + (long)n * a.s0.nstride;
     f16x4 reg[UPT];
@@ -276,17 +289,19 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
         const int pix = tid + 256 * u;
         if (pix < UNITS) *reinterpret_cast<f16x4*>(&patch[pix * 4]) = reg[u];
     }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);  // the weights' direct-to-LDS loads
     __syncthreads();
     f32x16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
-    const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
+    // A rows co = wm*64 + mb*32 + l32 (bit 3 of co is bit 3 of l32)
+    const int aoff = ((wm * 64 + l32) * 2 + (lhi ^ ((l32 >> 3) & 1))) * 8;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ks++) {
-        const f16x8 a0 = *reinterpret_cast<const f16x8*>(wbase + (long)ks * a.co_tot * 16);
-        const f16x8 a1 = *reinterpret_cast<const f16x8*>(wbase + (long)ks * a.co_tot * 16 + 32 * 16);
+        const f16x8 a0 = *reinterpret_cast<const f16x8*>(&wsh[ks * kCoT * 16 + aoff]);
+        const f16x8 a1 = *reinterpret_cast<const f16x8*>(&wsh[ks * kCoT * 16 + aoff + 32 * 16]);
         // (taps past 48 have zero weights; their reads stay in the patch)
         const int t0 = min(4 * ks + 2 * lhi, 48), t1 = min(4 * ks + 2 * lhi + 1, 48);
         const int ky0 = t0 / KS, kx0 = t0 - ky0 * KS, ky1 = t1 / KS, kx1 = t1 - ky1 * KS;
@@ -432,24 +447,28 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
 }
 
 // NCHW fp32 [image][C][hw] -> CK fp16 chunks [c0 ..) of out; channels past C
-// up to the chunk boundary are zero. With writeback, the rounded values also
-// replace the fp32 source (round_to_fp16 in place, nn.cuh:563-569).
-__global__ void k_to_ck(const float* in, long in_nstride, int C, _Float16* out, long out_nstride,
-                        int c0, int hw, float* writeback) {
+// up to the chunk boundary are zero. kWB: the rounded values also replace
+// the fp32 source (round_to_fp16 in place, nn.cuh:563-569). The 16 loads of
+// a thread are unconditional (channels past C read channel C - 1 and are
+// zeroed after), so they are all in flight together.
+template <bool kWB>
+__global__ __launch_bounds__(256) void k_to_ck(const float* in, long in_nstride, int C,
+                                               _Float16* out, long out_nstride, int c0, int hw,
+                                               float* writeback) {
     const int n = blockIdx.z, ch = blockIdx.y;  // chunk index within the source
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= hw) return;
+    const long base = (long)n * in_nstride + p;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) x[i] = in[base + (long)min(ch * 16 + i, C - 1) * hw];
     alignas(16) _Float16 v[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int c = ch * 16 + i;
-        float x = 0.0f;
-        if (c < C) {
-            const long idx = (long)n * in_nstride + (long)c * hw + p;
-            x = in[idx];
-            if (writeback) writeback[idx] = (float)(_Float16)x;
-        }
-        v[i] = (_Float16)x;
+    for (int i = 0; i < 16; i++) v[i] = (_Float16)(ch * 16 + i < C ? x[i] : 0.0f);
+    if constexpr (kWB) {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (ch * 16 + i < C) writeback[base + (long)(ch * 16 + i) * hw] = (float)v[i];
     }
     _Float16* o = out + (long)n * out_nstride + ((long)(c0 + ch) * hw + p) * 16;
     *reinterpret_cast<f16x8*>(o) = *reinterpret_cast<f16x8*>(&v[0]);
@@ -975,7 +994,7 @@ extern "C" int slk_update_forward(slk_update* u, const float* corr, const float*
     // inputs to CK fp16: corr (196 ch), motion (4 ch), net and inp (128 ch)
     auto to_ck = [&](const float* in, int C, DevBuf& out, int out_ch, int c0, float* wb) {
         dim3 g((hw + 255) / 256, (C + 15) / 16, N);
-        hipLaunchKernelGGL(k_to_ck, g, dim3(256), 0, stream, in, (long)C * hw, C,
+        hipLaunchKernelGGL(k_to_ck<false>, g, dim3(256), 0, stream, in, (long)C * hw, C,
                            out.as<_Float16>(), out_ch * ck, c0, hw, wb);
     };
     to_ck(corr, 196, s.corr16, kCorrCh, 0, nullptr);
@@ -1098,7 +1117,7 @@ extern "C" int slk_update_compute_eta(slk_update* u, float* agg_features, float*
         SLK_TRY(s.agg_t.ensure((size_t)K * 8 * chunk));
     }
     // round16 of the features in place (main.cu:659), to CK fp16
-    hipLaunchKernelGGL(k_to_ck, dim3((hw + 255) / 256, 8, K), dim3(256), 0, stream,
+    hipLaunchKernelGGL(k_to_ck<true>, dim3((hw + 255) / 256, 8, K), dim3(256), 0, stream,
                        agg_features, 128L * hw, 128, s.agg16.as<_Float16>(), 8 * ck, 0, hw,
                        agg_features);
     SLK_HIP(hipGetLastError());
