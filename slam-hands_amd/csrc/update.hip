@@ -184,22 +184,23 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
     const int p0 = blockIdx.y * 256 + wn * 128;
     const _Float16* wbase = a.wt + ((long)cot * kCoT + wm * 64 + l32) * 16 + lhi * 8;
     f16x8 A[3][2], B[3][4];
+    // every load unconditional, from a clamped chunk and pixel (a chunk past
+    // the last goes to a slot no step multiplies; a pixel past the map only
+    // reaches accumulator columns never stored), so the waits count loads
+    // along one straight path and the next two chunks stay in flight
     auto load = [&](int c, int slot) {
+        c = min(c, a.nchunk - 1);
         const _Float16* wc = wbase + (long)c * a.co_tot * 16;
         A[slot][0] = *reinterpret_cast<const f16x8*>(wc);
         A[slot][1] = *reinterpret_cast<const f16x8*>(wc + 32 * 16);
+        const bool first = c < a.s0.nchunk;  // uniform
+        const _Float16* sp = first ? a.s0.p + (long)n * a.s0.nstride + (long)c * HW * 16
+                                   : a.s1.p + (long)n * a.s1.nstride +
+                                         (long)(c - a.s0.nchunk) * HW * 16;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int p = p0 + r * 32 + l32;
-            f16x8 v = {};
-            if (p < HW) {
-                const bool first = c < a.s0.nchunk;
-                const CkSrc& s = first ? a.s0 : a.s1;
-                const int cc = first ? c : c - a.s0.nchunk;
-                v = *reinterpret_cast<const f16x8*>(s.p + (long)n * s.nstride +
-                                                    ((long)cc * HW + p) * 16 + lhi * 8);
-            }
-            B[slot][r] = v;
+            const int p = min(p0 + r * 32 + l32, HW - 1);
+            B[slot][r] = *reinterpret_cast<const f16x8*>(sp + (long)p * 16 + lhi * 8);
         }
     };
     f32x16 acc[2][4];
@@ -209,18 +210,19 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
         for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
     // three register slots, so every slot index below is a compile-time constant
     auto step = [&](int c, int slot) {
-        if (c >= a.nchunk) return;
-        if (c + 2 < a.nchunk) load(c + 2, slot == 0 ? 2 : slot - 1);
+        load(c + 2, slot == 0 ? 2 : slot - 1);
+        if (c < a.nchunk) {  // uniform
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][0], B[slot][r], acc[0][r],
-                                                               0, 0, 0);
-            acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][1], B[slot][r], acc[1][r],
-                                                               0, 0, 0);
+            for (int r = 0; r < 4; r++) {
+                acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][0], B[slot][r],
+                                                                   acc[0][r], 0, 0, 0);
+                acc[1][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[slot][1], B[slot][r],
+                                                                   acc[1][r], 0, 0, 0);
+            }
         }
     };
     load(0, 0);
-    if (a.nchunk > 1) load(1, 1);
+    load(1, 1);
     for (int c = 0; c < a.nchunk; c += 3) {
         step(c, 0);
         step(c + 1, 1);
