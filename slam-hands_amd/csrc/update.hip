@@ -339,20 +339,23 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
 // of the patch, an output channel of the weights) has its two 16-byte halves
 // swapped when bit 3 of the row is set, so the 16 lanes of one pass of a
 // 128-bit operand read touch 64 distinct banks.
+constexpr int kTH3 = 6;            // output rows of a k_conv3 tile
 constexpr int kPatchUnits = 768;  // 16-byte units of a patch buffer: (kTH + 2) x (kTW + 2) x 2 = 680, padded
 constexpr int kWaTaps = 5, kWbTaps = 4;
 static_assert(kPatchUnits >= (kTH + 2) * (kTW + 2) * 2 && kPatchUnits % 256 == 0, "patch units");
 static_assert(kCoT * 2 == 256, "one 256-unit round per weight tap");
 
-template <int EPI>
+template <int EPI, int TH>
 __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
     constexpr int PW = kTW + 2;
+    constexpr int RW = TH / 2;  // output rows of a wave
+    static_assert(TH % 2 == 0 && (TH + 2) * PW * 2 <= kPatchUnits, "conv3 tile height");
     __shared__ __attribute__((aligned(16))) _Float16 sp[2][kPatchUnits * 8];
     __shared__ __attribute__((aligned(16))) _Float16 swa[kWaTaps * 256 * 8];
     __shared__ __attribute__((aligned(16))) _Float16 swb[kWbTaps * 256 * 8];
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
-    const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
+    const int ty0 = (tile / a.tiles_x) * TH, tx0 = (tile % a.tiles_x) * kTW;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
@@ -380,17 +383,17 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
             const int half = (unit & 1) ^ ((pix >> 3) & 1);
             const int py = pix / PW, px = pix - (pix / PW) * PW;
             const int y = ty0 - 1 + py, x = tx0 - 1 + px;
-            const bool ok = pix < (kTH + 2) * PW && y >= 0 && y < a.h && x >= 0 && x < a.w;
+            const bool ok = pix < (TH + 2) * PW && y >= 0 && y < a.h && x >= 0 && x < a.w;
             dma_x4(ok ? base + ((long)y * a.w + x) * 16 + half * 8 : a.zero16,
                    lds_addr(&sp[buf][(r * 256 + wave * 64) * 8]));
         }
     };
 
-    f32x16 acc[2][4];
+    f32x16 acc[2][RW];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x16{};
+        for (int j = 0; j < RW; j++) acc[i][j] = f32x16{};
     auto taps = [&](int t0, int nt, const _Float16* wb, const _Float16* pb) {
 #pragma unroll
         for (int tt = 0; tt < nt; tt++) {  // the callers' counts are constants
@@ -403,8 +406,8 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
                     wb + ((tt * 256 + co * 2) * 8 + ((lhi ^ ((co >> 3) & 1)) * 8)));
             }
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int pix = (wn * 4 + r + ky) * PW + l32 + kx;
+            for (int r = 0; r < RW; r++) {
+                const int pix = (wn * RW + r + ky) * PW + l32 + kx;
                 const f16x8 b = *reinterpret_cast<const f16x8*>(
                     pb + (pix * 16 + ((lhi ^ ((pix >> 3) & 1)) * 8)));
                 acc[0][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[0], b, acc[0][r], 0, 0, 0);
@@ -440,8 +443,8 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
 
     const int x = tx0 + l32;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int y = ty0 + wn * 4 + r;
+    for (int r = 0; r < RW; r++) {
+        const int y = ty0 + wn * RW + r;
         if (y >= a.h || x >= a.w) continue;
         epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, y * a.w + x,
                        HW);
@@ -835,7 +838,8 @@ int launch_conv(const UpdateState* s, const PackedConv& pc, ConvArgs a, int N,
                            dim3(256), 0, stream, a);
     } else if constexpr (KS == 3) {
         a.zero16 = s->zero16.as<_Float16>();
-        hipLaunchKernelGGL((k_conv3<EPI>), dim3(pc.co_tot / kCoT, s->tiles_x * s->tiles_y, N),
+        const int ty = (s->h + kTH3 - 1) / kTH3;
+        hipLaunchKernelGGL((k_conv3<EPI, kTH3>), dim3(pc.co_tot / kCoT, s->tiles_x * ty, N),
                            dim3(256), 0, stream, a);
     } else {
         static_assert(KS == 7, "the 7x7 stem is the only other convolution");
