@@ -88,10 +88,37 @@ struct ConvArgs {
 // The epilogue of one pixel's two 32-row accumulator blocks: acc0/acc1
 // register v holds output channel co0 + mb*32 + 8*(v/4) + v%4 (co0 includes
 // the lane's 4*lhi), so each group of four registers is four consecutive
-// channels of the CK layout.
+// channels of the CK layout. bias[co] is the channel's bias and, for kEpiZR
+// and kEpiQ, gts[co] its global term of image n (the 3x3 kernels stage
+// their tile's in LDS). Every memory read of the epilogue is
+// issued before its first store, from a clamped channel where the group is
+// past Co: vector memory counts loads and stores together, in order, so a
+// load issued after a store would wait for that store.
 template <int EPI>
 __device__ __forceinline__ void epi_block(const ConvArgs& a, const f32x16& acc0,
-                                          const f32x16& acc1, int n, int co0, int p, int HW) {
+                                          const f32x16& acc1, int n, int co0, int p, int HW,
+                                          const float* bias, const float* gts) {
+    // the state operands of each group: s0 (net, or for kEpiQ z), s1 (kEpiQ: net)
+    f16x4 s0[2][4], s1[2][4];
+#pragma unroll
+    for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int co = co0 + mb * 32 + 8 * g;
+            const int cc = co < a.Co ? co : 0;
+            if constexpr (EPI == kEpiGate) {
+                s0[mb][g] = *reinterpret_cast<const f16x4*>(
+                    a.net16 + (long)n * a.net_nstride + ((long)(cc >> 4) * HW + p) * 16 + (cc & 15));
+            } else if constexpr (EPI == kEpiZR) {
+                const int cr = cc >= 128 ? cc - 128 : 0;
+                s0[mb][g] = *reinterpret_cast<const f16x4*>(
+                    a.net16 + (long)n * a.net_nstride + ((long)(cr >> 4) * HW + p) * 16 + (cr & 15));
+            } else if constexpr (EPI == kEpiQ) {
+                const long off = ((long)(cc >> 4) * HW + p) * 16 + (cc & 15);
+                s0[mb][g] = *reinterpret_cast<const f16x4*>(a.zbuf + (long)n * a.zr_nstride + off);
+                s1[mb][g] = *reinterpret_cast<const f16x4*>(a.net16 + (long)n * a.net_nstride + off);
+            }
+        }
 #pragma unroll
     for (int mb = 0; mb < 2; mb++) {
         const f32x16& acc = mb ? acc1 : acc0;
@@ -101,7 +128,7 @@ __device__ __forceinline__ void epi_block(const ConvArgs& a, const f32x16& acc0,
             if (co >= a.Co) continue;
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = acc[4 * g + i] + a.bias[co + i];
+            for (int i = 0; i < 4; i++) v[i] = acc[4 * g + i] + bias[co + i];
             if constexpr (EPI == kEpiRelu) {
                 f16x4 o;
 #pragma unroll
@@ -109,47 +136,41 @@ __device__ __forceinline__ void epi_block(const ConvArgs& a, const f32x16& acc0,
                 *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
                                           ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
             } else if constexpr (EPI == kEpiGate) {
-                const f16x4 nt = *reinterpret_cast<const f16x4*>(
-                    a.net16 + (long)n * a.net_nstride + ((long)(co >> 4) * HW + p) * 16 + (co & 15));
+                const f16x4 nt = s0[mb][g];
                 f16x4 o;
 #pragma unroll
                 for (int i = 0; i < 4; i++) o[i] = (_Float16)(r16(sigm(r16(v[i]))) * (float)nt[i]);
                 *reinterpret_cast<f16x4*>(a.out16 + (long)n * a.out16_nstride +
                                           ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = o;
             } else if constexpr (EPI == kEpiZR) {
-                const float* gt = a.gterm + (long)n * 384 + co;
                 f16x4 sg;
 #pragma unroll
-                for (int i = 0; i < 4; i++) sg[i] = (_Float16)sigm(r16(v[i]) + gt[i]);
+                for (int i = 0; i < 4; i++) sg[i] = (_Float16)sigm(r16(v[i]) + gts[co + i]);
                 if (co < 128) {
                     *reinterpret_cast<f16x4*>(a.zbuf + (long)n * a.zr_nstride +
                                               ((long)(co >> 4) * HW + p) * 16 + (co & 15)) = sg;
                 } else {
                     const int cr = co - 128;
                     const long off = ((long)(cr >> 4) * HW + p) * 16 + (cr & 15);
-                    const f16x4 nt =
-                        *reinterpret_cast<const f16x4*>(a.net16 + (long)n * a.net_nstride + off);
+                    const f16x4 nt = s0[mb][g];
                     f16x4 o;
 #pragma unroll
                     for (int i = 0; i < 4; i++) o[i] = (_Float16)((float)nt[i] * (float)sg[i]);
                     *reinterpret_cast<f16x4*>(a.rnet + (long)n * a.zr_nstride + off) = o;
                 }
             } else if constexpr (EPI == kEpiQ) {
-                const float* gt = a.gterm + (long)n * 384 + 256 + co;
                 const long off = ((long)(co >> 4) * HW + p) * 16 + (co & 15);
-                const f16x4 z = *reinterpret_cast<const f16x4*>(a.zbuf + (long)n * a.zr_nstride + off);
-                _Float16* np = a.net16 + (long)n * a.net_nstride + off;
-                const f16x4 nt = *reinterpret_cast<const f16x4*>(np);
+                const f16x4 z = s0[mb][g], nt = s1[mb][g];
                 f16x4 o;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float q = r16(tanhf(r16(v[i]) + gt[i]));
+                    const float q = r16(tanhf(r16(v[i]) + gts[co + i]));
                     const float zi = (float)z[i];
                     const float nn = (1.0f - zi) * (float)nt[i] + zi * q;
                     o[i] = (_Float16)nn;
                     a.out32[(long)n * a.out32_nstride + (long)(co + i) * HW + p] = (float)o[i];
                 }
-                *reinterpret_cast<f16x4*>(np) = o;
+                *reinterpret_cast<f16x4*>(a.net16 + (long)n * a.net_nstride + off) = o;
             } else {  // kEpiHeads
                 if (co < 256) {
                     f16x4 o;
@@ -231,7 +252,9 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int p = p0 + r * 32 + l32;
-        if (p < HW) epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, p, HW);
+        if (p < HW)
+            epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, p, HW,
+                           a.bias, nullptr);
     }
 }
 
@@ -256,6 +279,7 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
     constexpr int UPT = (UNITS + 255) / 256;
     __shared__ __attribute__((aligned(16))) _Float16 patch[UNITS * 4];
     __shared__ __attribute__((aligned(16))) _Float16 wsh[KSTEPS * kCoT * 16];
+    __shared__ float bsh[kCoT];  // the tile's biases
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
     const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
@@ -273,6 +297,7 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
         dma_x4(a.wt + ((long)ks * a.co_tot + cot * kCoT + co) * 16 + half * 8,
                lds_addr(&wsh[(r * 256 + wave * 64) * 8]));
     }
+    if (tid < kCoT) bsh[tid] = a.bias[cot * kCoT + tid];
     // channels 0..3 of chunk 0 of the input
     const _Float16* img = a.s0.p + (long)n * a.s0.nstride;
     f16x4 reg[UPT];
@@ -323,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void k_conv7p(ConvArgs a) {
         const int y = ty0 + wn * 4 + r;
         if (y >= a.h || x >= a.w) continue;
         epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, y * a.w + x,
-                       HW);
+                       HW, bsh - cot * kCoT, nullptr);
     }
 }
 
@@ -353,6 +378,9 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sp[2][kPatchUnits * 8];
     __shared__ __attribute__((aligned(16))) _Float16 swa[kWaTaps * 256 * 8];
     __shared__ __attribute__((aligned(16))) _Float16 swb[kWbTaps * 256 * 8];
+    // the tile's biases and (kEpiZR, kEpiQ) global terms, in LDS by the first
+    // chunk's barrier
+    __shared__ float bsh[kCoT], gsh[kCoT];
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, tile = blockIdx.y, n = blockIdx.z;
     const int ty0 = (tile / a.tiles_x) * TH, tx0 = (tile % a.tiles_x) * kTW;
@@ -419,6 +447,9 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
     // P(1) | WA(1) | WB(1) P(2) | WA(2) ...; a chunk starts once everything
     // issued before it has landed (its patch and WA), its taps 5-8 once WB
     // has (only the next patch, 3 loads, may still be in flight).
+    if (tid < kCoT) bsh[tid] = a.bias[cot * kCoT + tid];
+    if constexpr (EPI == kEpiZR || EPI == kEpiQ)
+        if (tid < kCoT) gsh[tid] = a.gterm[(long)n * 384 + (EPI == kEpiQ ? 256 : 0) + cot * kCoT + tid];
     issue_patch(0, 0);
     issue_w(0, 0, kWaTaps, swa);
     for (int c = 0; c < nch; c++) {
@@ -447,7 +478,7 @@ __global__ __launch_bounds__(256, 2) void k_conv3(ConvArgs a) {
         const int y = ty0 + wn * RW + r;
         if (y >= a.h || x >= a.w) continue;
         epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, y * a.w + x,
-                       HW);
+                       HW, bsh - cot * kCoT, gsh - cot * kCoT);
     }
 }
 
