@@ -196,9 +196,11 @@ __device__ __forceinline__ void epi_block(const ConvArgs& a, const f32x16& acc0,
 // global memory, two chunks ahead of their MFMAs.
 template <int EPI>
 __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
+    __shared__ float bsh[kCoT];  // the tile's biases
     const int HW = a.h * a.w;
     const int cot = blockIdx.x, n = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < kCoT) bsh[tid] = a.bias[cot * kCoT + tid];
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int l32 = lane & 31, lhi = lane >> 5;
@@ -249,12 +251,13 @@ __global__ __launch_bounds__(256) void k_conv1x1(ConvArgs a) {
         step(c + 1, 1);
         step(c + 2, 2);
     }
+    __syncthreads();  // bsh
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int p = p0 + r * 32 + l32;
         if (p < HW)
             epi_block<EPI>(a, acc[0][r], acc[1][r], n, cot * kCoT + wm * 64 + 4 * lhi, p, HW,
-                           a.bias, nullptr);
+                           bsh - cot * kCoT, nullptr);
     }
 }
 
@@ -589,8 +592,9 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     const float* W = a.W + head * a.wstride;
     for (int t = tid; t < Co * 8 * 9 * 16; t += 256) ws[t] = W[t];
     const _Float16* base = a.in + (long)n * a.in_nstride + (long)head * 8 * hw * 16;
-    f16x8 reg[UPT];
-    auto load_chunk = [&](int ch) {
+    // chunk ch's patch units in register slot ch % 3, loaded two chunks ahead
+    f16x8 reg[3][UPT];
+    auto load_chunk = [&](int ch, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
@@ -600,14 +604,14 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
             if (unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w)
                 v = *reinterpret_cast<const f16x8*>(base + ((long)ch * hw + yy * a.w + xx) * 16 +
                                                     half * 8);
-            reg[u] = v;
+            reg[slot][u] = v;
         }
     };
-    auto store_chunk = [&](int buf) {
+    auto store_chunk = [&](int buf, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
-            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[u];
+            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[slot][u];
         }
     };
     // v_mfma_f32_16x16x16_f16 with M = output channel (rows past Co zero), N =
@@ -620,12 +624,16 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     f32x4 acc[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) acc[g] = f32x4{};
-    load_chunk(0);
-    store_chunk(0);
+    load_chunk(0, 0);
+    load_chunk(1, 1);
+    store_chunk(0, 0);
     __syncthreads();  // the first patch and ws
-    for (int ch = 0; ch < 8; ch++) {
+    // step ch: chunk ch + 2's loads out, chunk ch's products from LDS, chunk
+    // ch + 1 (loaded a step earlier) into the other LDS buffer
+    auto step = [&](int ch, int slot) {
+        if (ch >= 8) return;  // uniform
+        if (ch + 2 < 8) load_chunk(ch + 2, slot == 0 ? 2 : slot - 1);
         const int buf = ch & 1;
-        if (ch + 1 < 8) load_chunk(ch + 1);
         f16x4 A[9];
 #pragma unroll
         for (int t = 0; t < 9; t++) {
@@ -645,8 +653,13 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
                 acc[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[t], bv, acc[g], 0, 0, 0);
             }
         }
-        if (ch + 1 < 8) store_chunk(buf ^ 1);
+        if (ch + 1 < 8) store_chunk(buf ^ 1, slot == 2 ? 0 : slot + 1);
         __syncthreads();
+    };
+    for (int ch = 0; ch < 8; ch += 3) {
+        step(ch, 0);
+        step(ch + 1, 1);
+        step(ch + 2, 2);
     }
     if (kg != 0) return;  // lanes 0..15 hold channels 0..3
     const int mode = a.mode[head];
