@@ -594,24 +594,33 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     const _Float16* base = a.in + (long)n * a.in_nstride + (long)head * 8 * hw * 16;
     // chunk ch's patch units in register slot ch % 3, loaded two chunks ahead
     f16x8 reg[3][UPT];
+    // (every load unconditional, from a pixel clamped into the image, and
+    // units outside it zeroed after: a load under a branch makes the waits
+    // count conservatively, and the next chunks would no longer be in flight)
     auto load_chunk = [&](int ch, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
             const int pix = unit >> 1, half = unit & 1;
             const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
-            f16x8 v = {};
-            if (unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w)
-                v = *reinterpret_cast<const f16x8*>(base + ((long)ch * hw + yy * a.w + xx) * 16 +
-                                                    half * 8);
-            reg[slot][u] = v;
+            const int yc = min(max(yy, 0), a.h - 1), xc = min(max(xx, 0), a.w - 1);
+            reg[slot][u] = *reinterpret_cast<const f16x8*>(
+                base + ((long)ch * hw + yc * a.w + xc) * 16 + half * 8);
         }
+    };
+    auto unit_in = [&](int u) {
+        const int unit = tid + 256 * u;
+        const int pix = unit >> 1;
+        const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
+        return unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w;
     };
     auto store_chunk = [&](int buf, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
-            if (unit < UNITS) *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) = reg[slot][u];
+            if (unit < UNITS)
+                *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) =
+                    unit_in(u) ? reg[slot][u] : f16x8{};
         }
     };
     // v_mfma_f32_16x16x16_f16 with M = output channel (rows past Co zero), N =
@@ -631,17 +640,17 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     // step ch: chunk ch + 2's loads out, chunk ch's products from LDS, chunk
     // ch + 1 (loaded a step earlier) into the other LDS buffer
     auto step = [&](int ch, int slot) {
-        if (ch >= 8) return;  // uniform
-        if (ch + 2 < 8) load_chunk(ch + 2, slot == 0 ? 2 : slot - 1);
+        // (chunk 7 again past the end: every step issues the same loads, so the
+        // waits count them exactly)
+        load_chunk(min(ch + 2, 7), slot == 0 ? 2 : slot - 1);
         const int buf = ch & 1;
         f16x4 A[9];
+        const int oc = min(c16, Co - 1);  // rows past Co read row Co - 1, zeroed after
 #pragma unroll
         for (int t = 0; t < 9; t++) {
-            A[t] = f16x4{};
-            if (c16 < Co) {
-                const float4 w4 = *reinterpret_cast<const float4*>(&ws[((c16 * 8 + ch) * 9 + t) * 16 + 4 * kg]);
-                A[t] = f16x4{(_Float16)w4.x, (_Float16)w4.y, (_Float16)w4.z, (_Float16)w4.w};
-            }
+            const float4 w4 = *reinterpret_cast<const float4*>(&ws[((oc * 8 + ch) * 9 + t) * 16 + 4 * kg]);
+            A[t] = c16 < Co ? f16x4{(_Float16)w4.x, (_Float16)w4.y, (_Float16)w4.z, (_Float16)w4.w}
+                            : f16x4{};
         }
 #pragma unroll
         for (int t = 0; t < 9; t++) {
@@ -656,11 +665,8 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
         if (ch + 1 < 8) store_chunk(buf ^ 1, slot == 2 ? 0 : slot + 1);
         __syncthreads();
     };
-    for (int ch = 0; ch < 8; ch += 3) {
-        step(ch, 0);
-        step(ch + 1, 1);
-        step(ch + 2, 2);
-    }
+#pragma unroll
+    for (int ch = 0; ch < 8; ch++) step(ch, ch % 3);
     if (kg != 0) return;  // lanes 0..15 hold channels 0..3
     const int mode = a.mode[head];
     float* out = a.out[head] + (long)n * a.out_nstride;
