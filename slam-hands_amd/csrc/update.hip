@@ -561,9 +561,12 @@ __global__ __launch_bounds__(384) void k_glo_fc(const float* glo, const float* W
 // 3x3 convolutions to at most 3 output channels (delta_2, weight_2,
 // agg_eta_0) on 8 input chunks, a kTH x kTW pixel tile per workgroup: the
 // tile's (kTH + 2) x (kTW + 2) patch of each chunk staged in LDS (double
-// buffered through registers), the products on 16x16 fp16 MFMA tiles whose
-// rows past the output channels are zero, fp32 accumulation (weights rounded
-// to fp16 on upload, laid out [o][chunk][tap][16] and held in LDS).
+// buffered through registers). The taps go into M: for 32 patch pixels a
+// v_mfma_f32_32x32x16_f16 forms D[t * 3 + o][q] = W[o][.][t] . x[.][q] for
+// all 27 (tap, output) rows at once, summed over the chunks in fp32; D goes
+// through LDS and each output pixel adds its 9 taps' rows at the shifted
+// patch pixels (weights rounded to fp16 on upload, laid out
+// [o][chunk][tap][16]).
 // mode 0: round16(conv + b) (delta, main.cu:634-635); 1: round16(sigmoid(
 // conv + b)) (weight, :641-643); 2: 0.01 * softplus(round16(conv + b)) (eta,
 // :663-665). blockIdx.y = image * nheads + head: head h reads chunks
@@ -581,85 +584,97 @@ struct SmallArgs {
 };
 __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     constexpr int PH = kTH + 2, PW = kTW + 2;
-    constexpr int UNITS = PH * PW * 2;  // 16-byte units of a chunk's patch
+    constexpr int NPIX = PH * PW;                 // 340 patch pixels
+    constexpr int NB = (NPIX + 31) / 32;          // 11 blocks of 32 patch pixels
+    constexpr int UNITS = NPIX * 2;               // 16-byte units of a chunk's patch
     constexpr int UPT = (UNITS + 255) / 256;
-    __shared__ __attribute__((aligned(16))) _Float16 patch[2][PH * PW * 16];
-    __shared__ __attribute__((aligned(16))) float ws[3 * 8 * 9 * 16];
+    constexpr int NM = 27;                        // rows of D: tap * 3 + output channel
+    constexpr int PBUF = NB * 32 * 16;            // halves of one patch buffer (352 pixels)
+    // the patch (double-buffered) and A, then D over both
+    struct Stage {
+        _Float16 patch[2][PBUF];
+        _Float16 A[8][32 * 16];  // [chunk][row m][k], rows past the taps' outputs zero
+    };
+    constexpr int kSmem = sizeof(Stage) > NM * NB * 32 * 4 ? sizeof(Stage) : NM * NB * 32 * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
+    Stage& st = *reinterpret_cast<Stage*>(smem);
+    float* D = reinterpret_cast<float*>(smem);  // [NM][NB * 32], after the chunk loop
     const int n = blockIdx.z, head = blockIdx.y, tile = blockIdx.x;
     const int ty0 = (tile / a.tiles_x) * kTH, tx0 = (tile % a.tiles_x) * kTW;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Co = a.Co, hw = a.h * a.w;
-    const float* W = a.W + head * a.wstride;
-    for (int t = tid; t < Co * 8 * 9 * 16; t += 256) ws[t] = W[t];
+    // A of every chunk: row m = t * 3 + o holds W[o][chunk][t][0..15] (fp16),
+    // zero for o >= Co and m >= 27; 16 values a thread, loads unconditional
+    {
+        const float* W = a.W + head * a.wstride;
+        float wv[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int i = tid + 256 * u;  // (chunk, m, k)
+            const int ch = i >> 9, m = (i >> 4) & 31, k = i & 15;
+            const int t = min(m / 3, 8), o = min(m % 3, Co - 1);
+            wv[u] = W[((o * 8 + ch) * 9 + t) * 16 + k];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int i = tid + 256 * u;
+            const int m = (i >> 4) & 31;
+            const bool live = m < NM && m % 3 < Co;
+            (&st.A[0][0])[i] = (_Float16)(live ? wv[u] : 0.0f);
+        }
+    }
     const _Float16* base = a.in + (long)n * a.in_nstride + (long)head * 8 * hw * 16;
-    // chunk ch's patch units in register slot ch % 3, loaded two chunks ahead
+    // chunk ch's patch units in register slot ch % 3, loaded two chunks ahead,
+    // every load unconditional (a pixel clamped into the image; units
+    // outside it zeroed when stored)
     f16x8 reg[3][UPT];
-    // (every load unconditional, from a pixel clamped into the image, and
-    // units outside it zeroed after: a load under a branch makes the waits
-    // count conservatively, and the next chunks would no longer be in flight)
     auto load_chunk = [&](int ch, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
-            const int pix = unit >> 1, half = unit & 1;
+            const int pix = min(unit >> 1, NPIX - 1), half = unit & 1;
             const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
             const int yc = min(max(yy, 0), a.h - 1), xc = min(max(xx, 0), a.w - 1);
             reg[slot][u] = *reinterpret_cast<const f16x8*>(
                 base + ((long)ch * hw + yc * a.w + xc) * 16 + half * 8);
         }
     };
-    auto unit_in = [&](int u) {
-        const int unit = tid + 256 * u;
-        const int pix = unit >> 1;
-        const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
-        return unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w;
-    };
     auto store_chunk = [&](int buf, int slot) {
 #pragma unroll
         for (int u = 0; u < UPT; u++) {
             const int unit = tid + 256 * u;
-            if (unit < UNITS)
-                *reinterpret_cast<f16x8*>(&patch[buf][unit * 8]) =
-                    unit_in(u) ? reg[slot][u] : f16x8{};
+            const int pix = unit >> 1;
+            const int yy = ty0 - 1 + pix / PW, xx = tx0 - 1 + pix % PW;
+            const bool in = unit < UNITS && yy >= 0 && yy < a.h && xx >= 0 && xx < a.w;
+            // units up to the 11th block's end are written (zeros past the patch)
+            if (unit < NB * 32 * 2)
+                *reinterpret_cast<f16x8*>(&st.patch[buf][unit * 8]) = in ? reg[slot][u] : f16x8{};
         }
     };
-    // v_mfma_f32_16x16x16_f16 with M = output channel (rows past Co zero), N =
-    // 16 consecutive pixels, K = a chunk's 16 channels: lane (c16, kg) holds
-    // A row c16, B column c16 and k = 4 kg .. 4 kg + 3 of both; accumulator
-    // register v holds channel 4 kg + v of pixel c16. Wave w takes tile rows
-    // 2w and 2w + 1, as four 16-pixel groups g (row 2w + g / 2, columns
-    // 16 (g % 2) ..).
-    const int c16 = lane & 15, kg = lane >> 4;
-    f32x4 acc[4];
+    static_assert(UPT * 256 >= NB * 32 * 2, "the zero units past the patch are stored");
+    // D[m][q] = sum over channels of A[m] . patch[q] on v_mfma_f32_32x32x16_f16:
+    // wave w takes blocks w, w + 4, w + 8 of 32 patch pixels; lane l holds A
+    // row l % 32 and B column (pixel) l % 32, k = 8 (l / 32) .. + 7
+    constexpr int kBpw = (NB + 3) / 4;
+    f32x16 acc[kBpw];
 #pragma unroll
-    for (int g = 0; g < 4; g++) acc[g] = f32x4{};
+    for (int i = 0; i < kBpw; i++) acc[i] = f32x16{};
+    const int l32 = lane & 31, khalf = lane >> 5;
     load_chunk(0, 0);
     load_chunk(1, 1);
     store_chunk(0, 0);
-    __syncthreads();  // the first patch and ws
-    // step ch: chunk ch + 2's loads out, chunk ch's products from LDS, chunk
-    // ch + 1 (loaded a step earlier) into the other LDS buffer
+    __syncthreads();  // A and the first patch
     auto step = [&](int ch, int slot) {
-        // (chunk 7 again past the end: every step issues the same loads, so the
-        // waits count them exactly)
         load_chunk(min(ch + 2, 7), slot == 0 ? 2 : slot - 1);
         const int buf = ch & 1;
-        f16x4 A[9];
-        const int oc = min(c16, Co - 1);  // rows past Co read row Co - 1, zeroed after
+        const f16x8 av = *reinterpret_cast<const f16x8*>(&st.A[ch][l32 * 16 + khalf * 8]);
 #pragma unroll
-        for (int t = 0; t < 9; t++) {
-            const float4 w4 = *reinterpret_cast<const float4*>(&ws[((oc * 8 + ch) * 9 + t) * 16 + 4 * kg]);
-            A[t] = c16 < Co ? f16x4{(_Float16)w4.x, (_Float16)w4.y, (_Float16)w4.z, (_Float16)w4.w}
-                            : f16x4{};
-        }
-#pragma unroll
-        for (int t = 0; t < 9; t++) {
-            const int ky = t / 3, kx = t - (t / 3) * 3;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int py = 2 * wave + (g >> 1) + ky, px = 16 * (g & 1) + c16 + kx;
-                const f16x4 bv = *reinterpret_cast<const f16x4*>(&patch[buf][(py * PW + px) * 16 + 4 * kg]);
-                acc[g] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[t], bv, acc[g], 0, 0, 0);
+        for (int i = 0; i < kBpw; i++) {
+            const int blk = wave + 4 * i;
+            if (blk < NB) {  // uniform
+                const f16x8 bv = *reinterpret_cast<const f16x8*>(
+                    &st.patch[buf][(blk * 32 + l32) * 16 + khalf * 8]);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
             }
         }
         if (ch + 1 < 8) store_chunk(buf ^ 1, slot == 2 ? 0 : slot + 1);
@@ -667,24 +682,42 @@ __global__ __launch_bounds__(256) void k_conv_small(SmallArgs a) {
     };
 #pragma unroll
     for (int ch = 0; ch < 8; ch++) step(ch, ch % 3);
-    if (kg != 0) return;  // lanes 0..15 hold channels 0..3
+    // D to LDS (over the patch buffers, every wave past the last barrier):
+    // register v of a block holds row 8 (v / 4) + 4 khalf + v % 4, column l32
+#pragma unroll
+    for (int i = 0; i < kBpw; i++) {
+        const int blk = wave + 4 * i;
+        if (blk >= NB) continue;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = 8 * (v >> 2) + 4 * khalf + (v & 3);
+            if (m < NM) D[m * (NB * 32) + blk * 32 + l32] = acc[i][v];
+        }
+    }
+    __syncthreads();
+    // one thread per output pixel: out[o] = sum over taps of D[t * 3 + o] at
+    // the tap's patch pixel
+    const int r = tid >> 5, c = tid & 31;
+    const int y = ty0 + r, x = tx0 + c;
+    if (y >= a.h || x >= a.w) return;
+    const int p = y * a.w + x;
     const int mode = a.mode[head];
     float* out = a.out[head] + (long)n * a.out_nstride;
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const int y = ty0 + 2 * wave + (g >> 1), x = tx0 + 16 * (g & 1) + c16;
-        if (y >= a.h || x >= a.w) continue;
-        const int p = y * a.w + x;
+    for (int o = 0; o < 3; o++) {
+        if (o >= Co) break;
+        float sum = 0.0f;
 #pragma unroll
-        for (int o = 0; o < 3; o++) {
-            if (o >= Co) break;
-            const float v = acc[g][o] + a.b[head * 3 + o];
-            float r;
-            if (mode == 0) r = r16(v);
-            else if (mode == 1) r = r16(sigm(v));
-            else r = 0.01f * logf(1.0f + expf(r16(v)));
-            out[(long)o * hw + p] = r;
+        for (int t = 0; t < 9; t++) {
+            const int q = (r + t / 3) * PW + c + t % 3;
+            sum += D[(t * 3 + o) * (NB * 32) + q];
         }
+        const float v = sum + a.b[head * 3 + o];
+        float res;
+        if (mode == 0) res = r16(v);
+        else if (mode == 1) res = r16(sigm(v));
+        else res = 0.01f * logf(1.0f + expf(r16(v)));
+        out[(long)o * hw + p] = res;
     }
 }
 
