@@ -537,7 +537,11 @@ int slk_encoder_forward(slk_encoder* enc, const float* input, void* output_f16, 
  * frame [H][W][3] (0..255; preprocess_image_kernel, main.cu:1062-1075), run
  * fnet -> fmap [128][H/8][W/8] fp16 and cnet -> net = tanh(cmap[0:128]),
  * inp = relu(cmap[128:256]) as fp32 [128][H/8][W/8]. fnet must have out_dim
- * 128, cnet 256, both max_batch >= 1 and the same image size. */
+ * 128, cnet 256, both max_batch >= 1 and the same image size. cnet runs on a
+ * stream of the cnet object (created on the first call) forked from `stream`
+ * and joined back to it by events, so the outputs are ordered on `stream`
+ * as if both encoders had run there; calls that share a cnet object must not
+ * overlap. */
 int slk_encode_frame(slk_encoder* fnet, slk_encoder* cnet, const float* bgr_hwc, void* fmap_f16,
                      float* net, float* inp, hipStream_t stream);
 

@@ -450,6 +450,11 @@ struct slk_encoder_state {
     bool packed = false;
     EncPacked pk[kEncLayers];
     DevBuf img, A, B, T, D, part1, part2;
+    // encode_frame runs the context encoder on this stream (non-blocking,
+    // default priority) beside the feature encoder on the caller's, forked
+    // and joined by the two events; created on the first such call
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -698,6 +703,13 @@ extern "C" int slk_encoder_destroy(slk_encoder* enc) {
         pc.bias.release();
     }
     for (DevBuf* b : {&e.img, &e.A, &e.B, &e.T, &e.D, &e.part1, &e.part2}) b->release();
+    if (e.side) {
+        // the side stream's work is finished before its resources go
+        (void)hipStreamSynchronize(e.side);
+        (void)hipStreamDestroy(e.side);
+    }
+    if (e.ev_fork) (void)hipEventDestroy(e.ev_fork);
+    if (e.ev_join) (void)hipEventDestroy(e.ev_join);
     delete enc;
     return SLK_OK;
 }
@@ -796,10 +808,20 @@ extern "C" int slk_encode_frame(slk_encoder* fnet, slk_encoder* cnet, const floa
     if (f.in_h != c.in_h || f.in_w != c.in_w || f.out_dim != 128 || c.out_dim != 256)
         return fail(SLK_E_ARG, "encode_frame: need fnet (out 128) and cnet (out 256) of one size");
     const int hw = f.in_h * f.in_w;
+    if (!c.side) {
+        SLK_HIP(hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking));
+        SLK_HIP(hipEventCreateWithFlags(&c.ev_fork, hipEventDisableTiming));
+        SLK_HIP(hipEventCreateWithFlags(&c.ev_join, hipEventDisableTiming));
+    }
     hipLaunchKernelGGL(k_image_to_px4, dim3((hw + 255) / 256, 1), dim3(256), 0, stream, bgr_hwc, 1,
                        3L * hw, hw, f.img.as<_Float16>(), 4L * hw);
     SLK_HIP(hipGetLastError());
-    // both encoders read the one preprocessed image
+    // both encoders read the one preprocessed image: the context encoder on
+    // the side stream once the image is written, the feature encoder on the
+    // caller's stream, which then waits for the side stream (the two
+    // encoders' launches are latency-bound at one frame and overlap)
+    SLK_HIP(hipEventRecord(c.ev_fork, stream));
+    SLK_HIP(hipStreamWaitEvent(c.side, c.ev_fork, 0));
     SLK_TRY(encoder_run(f, f.img.as<_Float16>(), 1, stream, [&](const Act& x) {
         const EncPacked& pc = f.pk[kEncLayers - 1];
         EncArgs a{};
@@ -811,7 +833,8 @@ extern "C" int slk_encode_frame(slk_encoder* fnet, slk_encoder* cnet, const floa
         a.out_nstride = 128L * x.h * x.w;
         return launch_layer<kEpNchw>(pc, a, 1, stream);
     }));
-    return encoder_run(c, f.img.as<_Float16>(), 1, stream, [&](const Act& x) {
+    hipStream_t side = c.side;
+    SLK_TRY(encoder_run(c, f.img.as<_Float16>(), 1, side, [&](const Act& x) {
         const EncPacked& pc = c.pk[kEncLayers - 1];
         EncArgs a{};
         a.in = x.p;
@@ -821,6 +844,9 @@ extern "C" int slk_encode_frame(slk_encoder* fnet, slk_encoder* cnet, const floa
         a.net = net;
         a.inp = inp;
         a.ni_nstride = 128L * x.h * x.w;
-        return launch_layer<kEpNetInp>(pc, a, 1, stream);
-    });
+        return launch_layer<kEpNetInp>(pc, a, 1, side);
+    }));
+    SLK_HIP(hipEventRecord(c.ev_join, side));
+    SLK_HIP(hipStreamWaitEvent(stream, c.ev_join, 0));
+    return SLK_OK;
 }
