@@ -470,7 +470,11 @@ int slk_update_load_dir(slk_update* um, const char* dir);
  * weight_out, agg_conv1_out, ..., batch, h, w), main.cu:606-650: corr
  * [B][196][hw], motion [B][4][hw], net [B][128][hw] (updated in place: the
  * GRU state, fp16-valued), inp [B][128][hw] -> delta_out [B][3][hw],
- * weight_out [B][3][hw], agg_conv1_out [B][128][hw]. B <= max_batch. */
+ * weight_out [B][3][hw], agg_conv1_out [B][128][hw]. B <= max_batch.
+ * The flow encoder and the gate run on two streams of the module, forked
+ * from `stream` and joined back to it within the call; the outputs are
+ * ordered on `stream` as usual. Calls on one module must not overlap on
+ * different caller streams (they share the module's buffers). */
 int slk_update_forward(slk_update* um, const float* corr, const float* motion, float* net,
                        const float* inp, float* delta_out, float* weight_out,
                        float* agg_conv1_out, int batch, hipStream_t stream);

@@ -766,7 +766,13 @@ struct UpdateState {
     DevBuf glo_w, glo_b, small_w[3], small_b[3];  // [0]: delta_2 | weight_2, [2]: eta_0
     // activations (CK fp16) and small vectors
     DevBuf corr16, mot16, cat, tmp, zr_buf, glo, gterm, agg16, agg_t;
+    DevBuf tmp_f, tmp_g;  // the flow encoder's and the gate's first-layer outputs
     DevBuf zero16;  // 256 zero bytes (staged units outside the image)
+    // forward runs the flow encoder on side[0] and the gate on side[1]
+    // (non-blocking, default priority) beside the correlation encoder on the
+    // caller's stream: forked by ev_fork, joined by ev_join before convz|convr
+    hipStream_t side[2] = {nullptr, nullptr};
+    hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
     // motion filter (batch 1): grid coords, lookup, motion, state copies, heads
     DevBuf mf_coords, mf_corr, mf_motion, mf_net, mf_inp, mf_delta, mf_weight, mf_agg;
     std::vector<float> mf_host;
@@ -975,14 +981,22 @@ extern "C" int slk_update_create(slk_update** out, int max_batch, int h, int w) 
     if (st == SLK_OK) st = s.mot16.ensure(N * chunk);
     if (st == SLK_OK) st = s.cat.ensure(N * kCatCh * chunk);
     if (st == SLK_OK) st = s.tmp.ensure(N * kTmpCh * chunk);
+    if (st == SLK_OK) st = s.tmp_f.ensure(N * kTmpCh * chunk);
+    if (st == SLK_OK) st = s.tmp_g.ensure(N * kTmpCh * chunk);
     if (st == SLK_OK) st = s.zr_buf.ensure(N * kZrCh * chunk);
     if (st == SLK_OK) st = s.glo.ensure(N * 128 * sizeof(float));
     if (st == SLK_OK) st = s.gterm.ensure(N * 384 * sizeof(float));
     if (st == SLK_OK) st = s.zero16.ensure(256);
     if (st == SLK_OK && hipMemset(s.zero16.ptr, 0, 256) != hipSuccess)
         st = fail(SLK_E_HIP, "update_create: hipMemset failed");
+    for (int i = 0; i < 2 && st == SLK_OK; i++)
+        if (hipStreamCreateWithFlags(&s.side[i], hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&s.ev_join[i], hipEventDisableTiming) != hipSuccess)
+            st = fail(SLK_E_HIP, "update_create: stream or event creation failed");
+    if (st == SLK_OK && hipEventCreateWithFlags(&s.ev_fork, hipEventDisableTiming) != hipSuccess)
+        st = fail(SLK_E_HIP, "update_create: event creation failed");
     if (st != SLK_OK) {
-        delete u;
+        slk_update_destroy(u);
         return st;
     }
     *out = u;
@@ -992,13 +1006,23 @@ extern "C" int slk_update_create(slk_update** out, int max_batch, int h, int w) 
 extern "C" int slk_update_destroy(slk_update* u) {
     if (!u) return SLK_OK;
     UpdateState& s = u->s;
+    for (int i = 0; i < 2; i++) {
+        if (s.side[i]) {
+            // the side streams' work is finished before its buffers go
+            (void)hipStreamSynchronize(s.side[i]);
+            (void)hipStreamDestroy(s.side[i]);
+        }
+        if (s.ev_join[i]) (void)hipEventDestroy(s.ev_join[i]);
+    }
+    if (s.ev_fork) (void)hipEventDestroy(s.ev_fork);
     for (PackedConv* pc : {&s.ce0, &s.ce2, &s.fe0, &s.fe2, &s.gw, &s.zr, &s.q, &s.heads, &s.ag2}) {
         pc->wt.release();
         pc->bias.release();
     }
     for (DevBuf* b : {&s.glo_w, &s.glo_b, &s.small_w[0], &s.small_w[1], &s.small_w[2],
                       &s.small_b[0], &s.small_b[1], &s.small_b[2], &s.corr16, &s.mot16, &s.cat,
-                      &s.tmp, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t, &s.zero16, &s.mf_coords,
+                      &s.tmp, &s.tmp_f, &s.tmp_g, &s.zr_buf, &s.glo, &s.gterm, &s.agg16, &s.agg_t,
+                      &s.zero16, &s.mf_coords,
                       &s.mf_corr, &s.mf_motion, &s.mf_net, &s.mf_inp, &s.mf_delta, &s.mf_weight,
                       &s.mf_agg})
         b->release();
@@ -1081,19 +1105,26 @@ extern "C" int slk_update_forward(slk_update* u, const float* corr, const float*
     const int hw = s.h * s.w, N = batch;
     const long ck = (long)hw * 16;  // elements of one chunk
     // inputs to CK fp16: corr (196 ch), motion (4 ch), net and inp (128 ch)
-    auto to_ck = [&](const float* in, int C, DevBuf& out, int out_ch, int c0, float* wb) {
+    auto to_ck = [&](const float* in, int C, DevBuf& out, int out_ch, int c0, float* wb,
+                     hipStream_t on) {
         dim3 g((hw + 255) / 256, (C + 15) / 16, N);
-        hipLaunchKernelGGL(k_to_ck<false>, g, dim3(256), 0, stream, in, (long)C * hw, C,
+        hipLaunchKernelGGL(k_to_ck<false>, g, dim3(256), 0, on, in, (long)C * hw, C,
                            out.as<_Float16>(), out_ch * ck, c0, hw, wb);
     };
-    to_ck(corr, 196, s.corr16, kCorrCh, 0, nullptr);
-    to_ck(motion, 4, s.mot16, 1, 0, nullptr);
-    to_ck(net, 128, s.cat, kCatCh, 0, nullptr);
-    to_ck(inp, 128, s.cat, kCatCh, 8, nullptr);
-    SLK_HIP(hipGetLastError());
     const long catS = kCatCh * ck, tmpS = kTmpCh * ck, zrS = kZrCh * ck;
+    // The three encoders of convz|convr's input are independent: the flow
+    // encoder runs on side[0], the gate on side[1], the correlation encoder on
+    // the caller's stream; each writes its own chunks of cat through its own
+    // scratch, and the caller's stream waits for both sides before convz|convr.
+    // The fork follows everything the caller queued before this call (the
+    // inputs, and the previous call's readers of cat and the scratch).
+    hipStream_t sf = s.side[0], sg = s.side[1];
+    SLK_HIP(hipEventRecord(s.ev_fork, stream));
+    SLK_HIP(hipStreamWaitEvent(sf, s.ev_fork, 0));
+    SLK_HIP(hipStreamWaitEvent(sg, s.ev_fork, 0));
     // corr encoder: 1x1 196 -> 128, 3x3 128 -> 128 into cat chunks 16..23
     {
+        to_ck(corr, 196, s.corr16, kCorrCh, 0, nullptr, stream);
         ConvArgs a{};
         a.s0 = src(s.corr16, 0, kCorrCh, kCorrCh * ck, hw);
         a.out16 = s.tmp.as<_Float16>();
@@ -1107,32 +1138,40 @@ extern "C" int slk_update_forward(slk_update* u, const float* corr, const float*
     }
     // flow encoder: 7x7 4 -> 128, 3x3 128 -> 64 into cat chunks 24..27
     {
+        to_ck(motion, 4, s.mot16, 1, 0, nullptr, sf);
         ConvArgs a{};
         a.s0 = src(s.mot16, 0, 1, ck, hw);
-        a.out16 = s.tmp.as<_Float16>();
+        a.out16 = s.tmp_f.as<_Float16>();
         a.out16_nstride = tmpS;
-        SLK_TRY((launch_conv<7, kEpiRelu>(&s, s.fe0, a, N, stream)));
+        SLK_TRY((launch_conv<7, kEpiRelu>(&s, s.fe0, a, N, sf)));
         ConvArgs b{};
-        b.s0 = src(s.tmp, 0, 8, tmpS, hw);
+        b.s0 = src(s.tmp_f, 0, 8, tmpS, hw);
         b.out16 = s.cat.as<_Float16>() + 24 * ck;
         b.out16_nstride = catS;
-        SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.fe2, b, N, stream)));
+        SLK_TRY((launch_conv<3, kEpiRelu>(&s, s.fe2, b, N, sf)));
+        SLK_HIP(hipEventRecord(s.ev_join[0], sf));
     }
-    // GRU: gate = round16(sigmoid(w(net))) * net, pooled; global terms
+    // net and inp into cat chunks 0..15; GRU gate = round16(sigmoid(w(net)))
+    // * net, pooled; global terms
     {
+        to_ck(net, 128, s.cat, kCatCh, 0, nullptr, sg);
+        to_ck(inp, 128, s.cat, kCatCh, 8, nullptr, sg);
         ConvArgs a{};
         a.s0 = src(s.cat, 0, 8, catS, hw);
-        a.out16 = s.tmp.as<_Float16>();
+        a.out16 = s.tmp_g.as<_Float16>();
         a.out16_nstride = tmpS;
         a.net16 = s.cat.as<_Float16>();
         a.net_nstride = catS;
-        SLK_TRY((launch_conv<1, kEpiGate>(&s, s.gw, a, N, stream)));
-        hipLaunchKernelGGL(k_gate_pool, dim3(8, N), dim3(256), 0, stream, s.tmp.as<_Float16>(),
+        SLK_TRY((launch_conv<1, kEpiGate>(&s, s.gw, a, N, sg)));
+        hipLaunchKernelGGL(k_gate_pool, dim3(8, N), dim3(256), 0, sg, s.tmp_g.as<_Float16>(),
                            tmpS, hw, s.glo.as<float>());
-        hipLaunchKernelGGL(k_glo_fc, dim3(N), dim3(384), 0, stream, s.glo.as<float>(),
+        hipLaunchKernelGGL(k_glo_fc, dim3(N), dim3(384), 0, sg, s.glo.as<float>(),
                            s.glo_w.as<float>(), s.glo_b.as<float>(), s.gterm.as<float>());
         SLK_HIP(hipGetLastError());
+        SLK_HIP(hipEventRecord(s.ev_join[1], sg));
     }
+    SLK_HIP(hipStreamWaitEvent(stream, s.ev_join[0], 0));
+    SLK_HIP(hipStreamWaitEvent(stream, s.ev_join[1], 0));
     // z | r (one 256-row GEMM over the 448-channel concatenation), then q and
     // the state update
     {
